@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of race_fused_fwd on one MI355X; prints ONE JSON line.
+
+Default workload (the config its metric is quoted
+on): causal forward, N = 8 streams, L = 4, R = 16 (S = 64), d = 64,
+T = 65536, fp32, synthetic inputs from the BASELINE distribution generated
+on the GPU (resident in HBM before the timed region).  A "step" is one
+race_fused_fwd pass over that batch: every kernel of the op, through the C
+ABI (include/race_mi355x.h), with caller-owned output and workspace.
+
+Timing: W untimed warmup steps, then K steps bracketed by
+torch.cuda.synchronize() on both sides.  Each timed step runs through
+race_fwd_profiled, which records a HIP event on the launch stream before the
+first kernel and after every kernel, so the per-kernel durations behind
+`roofline` come from the same timed region.  `value` = N*T / (mean step time)
+in M tokens/s.
+
+roofline: the dominant kernel's algorithmic HBM bytes per launch (inputs read
+once, output written once: bytes_per_stream_token * N * T, plus its workspace
+records) / its mean duration, against MI355X's 8 TB/s.  traffic: HBM bytes
+per launch measured with rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, read from
+profiles/traffic.json when a measurement for this workload exists, else null.
+
+cpu_baseline: the reference's CPU path -- the fp32 torch cumsum + bmm
+composition of src/race_baseline.py:45-51, as restated in oracle/ -- timed on
+this host at BASELINE config 1 (N = 8, T = 4096): 1 warmup, median of 3.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
+                       [--T T] [--kernel auto|valu|mfma] [--tile N] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+import __graft_entry__ as entry  # noqa: E402
+
+METRIC = "causal fwd M tokens/s at N=8,S=64,d_k=64,T=64K on 1 GPU; max T that fits"
+UNIT = "M tokens/s"
+PEAK_HBM_GBPS = 8000.0
+# the reference's PyTorch path, T = 65536, A100-SXM4-40GB.
+REFERENCE_MTOKS_T65536 = 5.25
+
+WORKLOADS = {
+    # name: (config key, default T)
+    "cfg2": ("cfg2_causal_fp32", 65536),
+    "cfg3": ("cfg3_causal_bf16", 1 << 20),
+    "cfg4": ("cfg4_noncausal_fp32", 1024),
+    "cfg5": ("cfg5_causal_bf16_S256", 16384),
+}
+
+# Kernel names of each launch sequence, by (causal, kernel family).
+PHASES = {
+    (True, "valu"): ["tile_sums", "tile_scan", "output_pass_valu"],
+    (False, "valu"): ["tile_sums", "tile_reduce", "token_map"],
+}
+
+
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime torch already loaded."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so.7")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.created = []
+
+    def array(self, n):
+        arr = (ctypes.c_void_p * n)()
+        for i in range(n):
+            h = ctypes.c_void_p()
+            if self.lib.hipEventCreate(ctypes.byref(h)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            arr[i] = h
+            self.created.append(h)
+        return arr
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = ctypes.c_float()
+        if self.lib.hipEventSynchronize(b) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+        if self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self):
+        for h in self.created:
+            self.lib.hipEventDestroy(h)
+        self.created = []
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
+    ap.add_argument("--T", type=int, default=0)
+    ap.add_argument("--kernel", choices=["auto", "valu", "mfma"], default="auto")
+    ap.add_argument("--tile", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
+    """Algorithmic HBM bytes of one launch of kernel `name` (each operand once)."""
+    NT = cfg.N * T
+    S, d = cfg.S, cfg.d
+    state = 4.0 * cfg.N * tiles * rec
+    return {
+        "tile_sums": es * (S + d) * NT + state,
+        "tile_scan": 2 * state,
+        "tile_reduce": state,
+        "output_pass_valu": es * (2 * S + 2 * d) * NT + state,
+        "output_pass_mfma": es * (2 * S + 2 * d) * NT + state,
+        "fused_mfma": es * (2 * S + 2 * d) * NT,
+        "token_map": es * (S + d) * NT,
+    }.get(name, es * (2 * S + 2 * d) * NT)
+
+
+def traffic_for(workload_key: str, kernel_name: str):
+    path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        table = json.loads(path.read_text())
+    except ValueError:
+        return None
+    entry_ = table.get(f"{workload_key}:{kernel_name}")
+    return None if entry_ is None else entry_.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline():
+    """The reference CPU path (torch fp32 cumsum + bmm) at BASELINE config 1."""
+    import torch
+
+    race = entry.load_package()
+    oracle = entry.load_oracle()
+    N, T, L, R, d = 8, 4096, 4, 16, 64
+    q, k, v = race.make_inputs(N, T, L, R, d, seed=1)
+    q, k = q.flatten(2), k.flatten(2)
+    threads = torch.get_num_threads()
+    with torch.no_grad():
+        oracle.torch_reference_path(q, k, v)  # warmup
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.torch_reference_path(q, k, v)
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(N * T / med / 1e6, 4),
+        "unit": UNIT,
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"BASELINE config 1: causal N={N} T={T} L={L} R={R} d={d} fp32, the torch-CPU "
+                   f"cumsum+bmm composition of src/race_baseline.py:45-51 (oracle/oracle.py "
+                   f"torch_reference_path), {threads} threads, median of 3 after 1 warmup: "
+                   f"{med * 1e3:.1f} ms per call"),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding of the op is a design in DESIGN.md, not a measured path.",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    race = entry.load_package()
+    from race_attention_kernel_amd import abi
+
+    cfg_key, default_T = WORKLOADS[args.workload]
+    cfg = race.CONFIGS[cfg_key]
+    T = args.T or default_T
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    q, k, v = race.config_inputs(cfg, T, seed=0, device=dev, gen_device="cuda")
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    sh = abi.shape(cfg.N, T, cfg.L, cfg.R, cfg.d, abi.RACE_BF16 if es == 2 else abi.RACE_F32)
+    kernel_id = race.ops.KERNELS[args.kernel]
+    opts = abi.options(args.tile, kernel_id)
+    st, ws_bytes, tiles, rec = abi.fwd_workspace_bytes(sh, cfg.causal, opts)
+    if st != 0:
+        raise RuntimeError(abi.status_string(st))
+    tile = race.select_tile_tokens(cfg.N, T, cfg.L, cfg.R, cfg.d, bf16=(es == 2), causal=cfg.causal,
+                                   tile_tokens=args.tile, kernel=kernel_id)
+    family = "valu"
+    if cfg.causal and (kernel_id == 2 or (kernel_id == 0 and race.ops._lib.ext().shape_supported(
+            cfg.L, cfg.R, cfg.d)[1])):
+        family = "mfma"
+    ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)
+    out = torch.empty_like(v)
+    stream = torch.cuda.current_stream().cuda_stream
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+
+    events = HipEvents()
+    max_launches = 8
+    per_step = [events.array(max_launches + 1) for _ in range(args.steps)]
+    warm = events.array(max_launches + 1)
+
+    for _ in range(args.warmup):
+        st, _ = abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream, warm)
+        if st != 0:
+            raise RuntimeError(abi.status_string(st))
+    torch.cuda.synchronize()
+
+    n_events = 0
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        st, n_events = abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
+                                        stream, per_step[i])
+        if st != 0:
+            raise RuntimeError(abi.status_string(st))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    gpu_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1])
+    # Steps are back to back on one stream: first event of step 0 to last of step K-1.
+    ms_per_step = gpu_ms / args.steps
+    n_launch = n_events - 1
+    phase_ms = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step)
+                for j in range(n_launch)]
+    names = PHASES.get((cfg.causal, family), [f"kernel{j}" for j in range(n_launch)])
+    if len(names) != n_launch:
+        names = [f"kernel{j}" for j in range(n_launch)]
+    dom = max(range(n_launch), key=lambda j: phase_ms[j])
+    dom_bytes = phase_bytes(names[dom], cfg, T, es, tiles, rec)
+    achieved = dom_bytes / (phase_ms[dom] * 1e-3) / 1e9
+    peak_bytes = torch.cuda.max_memory_allocated(dev)
+    events.destroy()
+
+    NT = cfg.N * T
+    value = NT / (ms_per_step * 1e-3) / 1e6
+    total_mem = torch.cuda.get_device_properties(dev).total_memory
+    bytes_per_token = peak_bytes / T
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": UNIT,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": (round(value / REFERENCE_MTOKS_T65536, 2)
+                        if (args.workload == "cfg2" and T == 65536) else None),
+        "dtype": "bf16" if es == 2 else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: {'causal' if cfg.causal else 'non-causal'} fwd N={cfg.N} "
+                        f"L={cfg.L} R={cfg.R} d={cfg.d} T={T} {'bf16' if es == 2 else 'fp32'}",
+            "N": cfg.N, "T": T, "L": cfg.L, "R": cfg.R, "d": cfg.d, "causal": cfg.causal,
+            "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch,
+            "kernel_ms": {names[j]: round(phase_ms[j], 5) for j in range(n_launch)},
+            "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+            "peak_hbm_bytes_per_token": round(bytes_per_token, 1),
+            "workspace_bytes_per_token": round(ws_bytes / T, 2),
+            "max_T_fits_est": int(0.95 * total_mem / bytes_per_token),
+            "alg_bytes_per_stream_token": es * (2 * cfg.S + 2 * cfg.d),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": names[dom],
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic_for(args.workload, names[dom]),
+            "alg_bytes_per_launch": int(dom_bytes),
+            "whole_op_frac": round(es * (2 * cfg.S + 2 * cfg.d) * NT / (ms_per_step * 1e-3) / 1e9
+                                   / PEAK_HBM_GBPS, 4),
+        },
+        "cpu_baseline": None,
+    }
+    del q, k, v, out, ws
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    os.environ.setdefault("PYTHONUNBUFFERED", "1")
+    sys.exit(main())

@@ -1,0 +1,169 @@
+/*
+ * race_mi355x.h -- C ABI of the MI355X (gfx950) per-bucket RACE attention op.
+ *
+ * The op is race_fused_fwd(probsQ, probsK, V, causal): the hot span of the
+ * reference's BatchedACE.forward (src/race_baseline.py:45-51), which takes the
+ * bucket probabilities the hashing produced (src/race_baseline.py:43-44) and
+ * returns, per stream n and token t,
+ *
+ *     causal:      out[t] = sum_s probsQ[t,s] * B_t[s,:] / (A_t[s] + 1e-6)
+ *                  A_t = sum_{j<=t} probsK[j],  B_t = sum_{j<=t} probsK[j] (x) V[j]
+ *     non-causal:  the same with A, B summed over all T tokens
+ *                  (analysis/hot-path.md:157-162).
+ *
+ * plus the non-causal backward w.r.t. probsQ, probsK and V.  The name is the
+ * one of the upstream host wrapper the reference describes as taking
+ * "probsK/probsQ precomputed in fp32 ([N,T,S])" (src/race_fused_fwd.cu:9-13).
+ *
+ * Layouts (row-major, contiguous, 16-byte aligned base pointers):
+ *   probsQ, probsK, dQ, dK : [N][T][S], S = L*R, table-major (s = l*R + r),
+ *                            i.e. the reference's [N,T,L,R] viewed as [N,T,S]
+ *   V, out, dOut, dV       : [N][T][d]
+ *   state                  : [N][S*d + S] fp32: B[s][c] at s*d + c, then A[s]
+ *                            at S*d + s (the per-bucket sums over all T tokens)
+ * All token tensors of one call share one dtype (RACE_F32 or RACE_BF16);
+ * accumulation is fp32.
+ *
+ * Contract, mirroring the reference's torch-free launcher API
+ * (src/causal_v2/kernels/race_causal_fwd.h:40-49, :99-130):
+ *   - the caller allocates outputs and the workspace; nothing here allocates
+ *     device memory or synchronizes the host;
+ *   - every launch goes on the caller's stream, in order;
+ *   - a function returns the first error it hits: RACE_ERROR_INVALID_VALUE
+ *     (numerically hipErrorInvalidValue) for unsupported shapes, bad pointers,
+ *     a too-small workspace or an invalid tile length, else the hipError_t of
+ *     the failed HIP call;
+ *   - results are bitwise reproducible for a fixed shape, kernel and tile
+ *     length: no atomics, every sum has a fixed order;
+ *   - N == 0 or T == 0 is a successful no-op (the state, if given, is zeroed).
+ * Limits: 1 <= S <= 256, 1 <= d <= 128, N*T*max(S,d) < 2^62.
+ */
+#ifndef RACE_MI355X_H
+#define RACE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RACE_ABI_VERSION 1
+
+typedef int32_t race_status;
+#define RACE_SUCCESS 0
+#define RACE_ERROR_INVALID_VALUE 1 /* equals hipErrorInvalidValue */
+
+typedef enum race_dtype {
+    RACE_F32 = 0,
+    RACE_BF16 = 1
+} race_dtype;
+
+/* Which kernels run.  AUTO picks the MFMA kernels where a specialization
+ * exists for (S, d) and the VALU kernels otherwise.  VALU forces the fp32
+ * vector-ALU kernels (the reference-shaped path, any supported shape); MFMA
+ * forces the matrix-core kernels and fails with RACE_ERROR_INVALID_VALUE if
+ * the shape has none.  Mirrors the reference binding's tensor_cores flag
+ * (src/causal_v2/kernels/torch_binding.cpp:252-254). */
+typedef enum race_kernel {
+    RACE_KERNEL_AUTO = 0,
+    RACE_KERNEL_VALU = 1,
+    RACE_KERNEL_MFMA = 2
+} race_kernel;
+
+/* Shape of one call.  Mirrors CausalShape
+ * (src/causal_v2/kernels/race_causal_fwd.h:60-66) with the hashing
+ * parameters replaced by the bucket layout the op consumes. */
+typedef struct race_shape {
+    int64_t num_streams; /* N = batch * heads */
+    int64_t seq_len;     /* T */
+    int32_t num_tables;  /* L */
+    int32_t num_buckets; /* R, buckets per table */
+    int32_t head_dim;    /* d */
+    int32_t dtype;       /* race_dtype of every token tensor */
+} race_shape;
+
+/* Optional knobs; pass NULL for the defaults.  tile_tokens: 0 picks the tile
+ * length (tokens per workgroup of the causal output pass) automatically; a
+ * positive value must be a multiple of RACE_SUB_CHUNK_TOKENS.  Mirrors the
+ * reference's tile_tokens override (torch_binding.cpp:109-122). */
+typedef struct race_options {
+    int32_t tile_tokens;
+    int32_t kernel; /* race_kernel */
+} race_options;
+
+/* Tile lengths are multiples of this many tokens. */
+#define RACE_SUB_CHUNK_TOKENS 64
+
+/* ABI version of the loaded library (RACE_ABI_VERSION it was built with). */
+int32_t race_abi_version(void);
+
+/* Static description of a status code. */
+const char* race_status_string(race_status status);
+
+/* Whether the shape is supported at all (limits above), and whether an MFMA
+ * specialization exists for it.  Pure host logic, no device calls. */
+race_status race_shape_supported(const race_shape* shape, int32_t* supported, int32_t* has_mfma);
+
+/* The tile length a call with these arguments uses.  Automatic selection
+ * reads the current device's compute-unit count. */
+race_status race_select_tile_tokens(const race_shape* shape, int32_t causal,
+                                    const race_options* opts, int32_t* tile_tokens);
+
+/* Workspace of race_fwd in bytes for these arguments.  The causal workspace
+ * starts with the tile records [N][tiles][rec] fp32, rec = S*d + S rounded
+ * up to a multiple of 64 floats, B then A as in `state`; after race_fwd
+ * returns (and the stream reaches it) record (n, t) holds the exclusive
+ * prefix state at the first token of tile t of stream n.  *tiles and
+ * *record_floats (nullable) receive the layout. */
+race_status race_fwd_workspace_bytes(const race_shape* shape, int32_t causal,
+                                     const race_options* opts, size_t* bytes, int64_t* tiles,
+                                     int64_t* record_floats);
+
+/* race_fused_fwd(probsQ, probsK, V, causal) -> out.
+ * Replaces the reference's src/race_baseline.py:45-51 (causal) and the
+ * non-causal formula of analysis/hot-path.md:157-162.  state (nullable): the
+ * per-bucket totals over all T tokens (causal: the final scan state, the
+ * decode hand-off; non-causal: what race_noncausal_bwd needs). */
+race_status race_fwd(const void* probsQ, const void* probsK, const void* V, void* out,
+                     float* state, const race_shape* shape, int32_t causal,
+                     const race_options* opts, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
+
+/* race_fwd with a hipEventRecord on `stream` before the first launch and
+ * after every launch: events[0] .. events[*n_events - 1], at most max_events
+ * (an error if the call makes more launches than max_events - 1).  A
+ * profiling aid for per-kernel timing on the caller's stream; it has no
+ * counterpart in the reference. */
+race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void* V, void* out,
+                              float* state, const race_shape* shape, int32_t causal,
+                              const race_options* opts, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream, hipEvent_t* events, int32_t max_events,
+                              int32_t* n_events);
+
+/* Workspace of race_noncausal_bwd in bytes. */
+race_status race_noncausal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                               size_t* bytes);
+
+/* Gradients of the non-causal forward w.r.t. probsQ, probsK and V for the
+ * upstream gradient dOut, given the forward's state (B, A).  There is no
+ * reference kernel for this (the reference's backward differentiates a
+ * different, globally normalized function through the hash chain,
+ * src/noncausal/kernels/race_bwd.h:1-30); the math is the VJP of
+ * analysis/hot-path.md:157-162:
+ *   dQ = dOut E^T, dE = Q^T dOut, dB = dE / (A + eps),
+ *   dA[s] = -sum_c dE[s,c] E[s,c] / (A[s] + eps), dK = V dB^T + 1 dA^T,
+ *   dV = K dB, with E = B / (A + eps).
+ * Any of dQ, dK, dV may be NULL to skip it. */
+race_status race_noncausal_bwd(const void* probsQ, const void* probsK, const void* V,
+                               const void* dOut, const float* state, void* dQ, void* dK, void* dV,
+                               const race_shape* shape, const race_options* opts, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RACE_MI355X_H */

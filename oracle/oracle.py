@@ -1,0 +1,214 @@
+"""CPU oracle for per-bucket RACE attention -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module.  The product path (the HIP library and its Python op)
+never calls it and has no CPU fallback.
+
+What is here, and which reference lines each piece restates
+(paths relative to the reference repository):
+
+* ``causal_recurrence`` / ``causal_chunked`` / ``causal_tiled`` /
+  ``noncausal_fwd`` / ``noncausal_bwd`` -- ctypes wrappers over
+  ``race_oracle.c`` (fp64 accumulation).  The recurrence follows
+  src/race_fused_fwd.cu:131-146 and src/test_kernel_math.py:32-39; the
+  chunked form src/race_chunked.py:41-63; the tiled form the three-launch
+  decomposition of src/causal_v2/kernels/race_causal_fwd.h:23-27 with the
+  per-bucket function of src/causal_v2/reference.py:144-159.
+* ``cumsum_bmm`` -- numpy transcription of the unchunked composition of
+  src/race_baseline.py:45-51 (cumsum, broadcast product, cumsum, divide,
+  bmm), in a chosen dtype.  Memory O(N*T*S*d): small T only.
+* ``dense_causal`` -- the same function as a T x T masked matrix,
+  out = M v with M[i, j] = [j <= i] * sum_s q[i,s] k[j,s] / (A[i,s] + eps).
+  A different evaluation order from every other form; small T only.
+* ``torch_reference_path`` -- the reference's CPU path as torch ops in fp32
+  (src/race_baseline.py:45-51 verbatim in semantics).  It is the timed CPU
+  baseline of bench.py and the fp32 comparison point of the tests.
+* ``torch_noncausal_autograd`` -- torch.autograd on the non-causal formula
+  (analysis/hot-path.md:157-162), the oracle BASELINE config 4 names for the
+  gradients.
+
+Layouts: probsQ/probsK [N, T, S] (S = L*R, table-major), V/out [N, T, d].
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+EPS = 1e-6  # src/race_baseline.py:47
+
+_HERE = pathlib.Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+_lib = None
+
+
+def build(force: bool = False) -> pathlib.Path:
+    """Compile liboracle.so with the Makefile beside this file."""
+    if force or not _LIB_PATH.exists() or (
+        _LIB_PATH.stat().st_mtime < (_HERE / "race_oracle.c").stat().st_mtime
+    ):
+        subprocess.run(["make", "-s", "-C", str(_HERE), "-B" if force else "all"], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(_LIB_PATH))
+        f32p = ctypes.POINTER(ctypes.c_float)
+        f64p = ctypes.POINTER(ctypes.c_double)
+        i64 = ctypes.c_int64
+        d = ctypes.c_double
+        i = ctypes.c_int
+        lib.race_oracle_causal_recurrence.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i]
+        lib.race_oracle_causal_chunked.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i64, i]
+        lib.race_oracle_causal_tiled.argtypes = [f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i64, i64, i]
+        lib.race_oracle_noncausal_fwd.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i]
+        lib.race_oracle_noncausal_bwd.argtypes = [f32p, f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i]
+        for name in ("race_oracle_causal_recurrence", "race_oracle_causal_chunked", "race_oracle_causal_tiled",
+                     "race_oracle_noncausal_fwd", "race_oracle_noncausal_bwd"):
+            getattr(lib, name).restype = None
+        _lib = lib
+    return _lib
+
+
+def _f32(x) -> np.ndarray:
+    a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    return a
+
+
+def _ptr(a: np.ndarray, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _shape(q, v):
+    N, T, S = q.shape
+    d = v.shape[2]
+    assert v.shape[:2] == (N, T)
+    return N, T, S, d
+
+
+def causal_recurrence(q, k, v, eps: float = EPS, nthreads: int = 0, want_state: bool = False):
+    """Per-token scan, fp64.  Returns out [N,T,d] (and the final state [N, S*d+S])."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    N, T, S, d = _shape(q, v)
+    out = np.empty((N, T, d), np.float64)
+    st = np.empty((N, S * d + S), np.float64) if want_state else None
+    _load().race_oracle_causal_recurrence(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(out, ctypes.c_double),
+        _ptr(st, ctypes.c_double) if st is not None else None, N, T, S, d, eps, nthreads)
+    return (out, st) if want_state else out
+
+
+def causal_chunked(q, k, v, chunk: int, eps: float = EPS, nthreads: int = 0):
+    """Carried-state chunked form (chunk identity), fp64."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    N, T, S, d = _shape(q, v)
+    out = np.empty((N, T, d), np.float64)
+    _load().race_oracle_causal_chunked(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(out, ctypes.c_double),
+        None, N, T, S, d, eps, chunk, nthreads)
+    return out
+
+
+def causal_tiled(q, k, v, tile: int, chunk: int, eps: float = EPS, nthreads: int = 0):
+    """The GPU decomposition in fp64.  Returns (out, prefix_states [N,tiles,S*d+S], final [N,S*d+S])."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    N, T, S, d = _shape(q, v)
+    tiles = -(-T // tile)
+    out = np.empty((N, T, d), np.float64)
+    pref = np.empty((N, tiles, S * d + S), np.float64)
+    fin = np.empty((N, S * d + S), np.float64)
+    _load().race_oracle_causal_tiled(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(out, ctypes.c_double),
+        _ptr(pref, ctypes.c_double), _ptr(fin, ctypes.c_double), N, T, S, d, eps, tile, chunk, nthreads)
+    return out, pref, fin
+
+
+def noncausal_fwd(q, k, v, eps: float = EPS, nthreads: int = 0):
+    """Non-causal forward, fp64.  Returns (out [N,T,d], state [N, S*d+S] = (B, A))."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    N, T, S, d = _shape(q, v)
+    out = np.empty((N, T, d), np.float64)
+    st = np.empty((N, S * d + S), np.float64)
+    _load().race_oracle_noncausal_fwd(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(out, ctypes.c_double),
+        _ptr(st, ctypes.c_double), N, T, S, d, eps, nthreads)
+    return out, st
+
+
+def noncausal_bwd(q, k, v, g, eps: float = EPS, nthreads: int = 0):
+    """Closed-form VJP of the non-causal forward, fp64.  Returns (dq, dk, dv)."""
+    q, k, v, g = _f32(q), _f32(k), _f32(v), _f32(g)
+    N, T, S, d = _shape(q, v)
+    dq = np.empty((N, T, S), np.float64)
+    dk = np.empty((N, T, S), np.float64)
+    dv = np.empty((N, T, d), np.float64)
+    _load().race_oracle_noncausal_bwd(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(g, ctypes.c_float),
+        _ptr(dq, ctypes.c_double), _ptr(dk, ctypes.c_double), _ptr(dv, ctypes.c_double), N, T, S, d, eps, nthreads)
+    return dq, dk, dv
+
+
+def cumsum_bmm(q, k, v, eps: float = EPS, dtype=np.float64):
+    """src/race_baseline.py:45-51 transcribed to numpy, in ``dtype``.
+
+    A_pref = cumsum(k); B_pref = cumsum(k[..., None] * v[:, :, None]);
+    E_pref = B_pref / (A_pref[..., None] + eps); out = q . E_pref.
+    """
+    q, k, v = (np.asarray(x, dtype=dtype) for x in (q, k, v))
+    a_pref = np.cumsum(k, axis=1)
+    b_pref = np.cumsum(k[..., :, None] * v[..., None, :], axis=1)
+    e_pref = b_pref / (a_pref[..., None] + dtype(eps))
+    return np.einsum("nts,ntsc->ntc", q, e_pref)
+
+
+def dense_causal(q, k, v, eps: float = EPS):
+    """T x T masked-matrix form in fp64 (small T): out = M v."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    N, T, S = q.shape
+    a_pref = np.cumsum(k, axis=1)                    # [N,T,S]
+    w = q / (a_pref + eps)                           # [N,T,S]
+    m = np.einsum("nis,njs->nij", w, k)              # [N,T,T]
+    m = m * np.tril(np.ones((T, T)))[None]
+    return m @ v
+
+
+def torch_reference_path(q, k, v, eps: float = EPS):
+    """The reference's CPU path (src/race_baseline.py:45-51) as fp32 torch ops.
+
+    q, k: [N, T, S] float32 CPU tensors; v: [N, T, d].  Returns [N, T, d] fp32.
+    """
+    import torch
+
+    N, T, S = q.shape
+    d = v.shape[2]
+    a_pref = k.cumsum(dim=1)
+    b_pref = (k.unsqueeze(-1) * v.unsqueeze(2)).cumsum(dim=1)
+    e_pref = b_pref.div(a_pref.unsqueeze(-1).add(eps))
+    return torch.bmm(q.reshape(N * T, 1, S), e_pref.contiguous().view(N * T, S, d)).view(N, T, d)
+
+
+def torch_noncausal_reference(q, k, v, eps: float = EPS):
+    """analysis/hot-path.md:157-162 as torch ops (differentiable)."""
+    import torch
+
+    b_sum = k.transpose(1, 2).bmm(v)                 # [N,S,d]
+    a = k.sum(1)                                     # [N,S]
+    e = b_sum / (a.unsqueeze(-1) + eps)
+    return q.bmm(e)
+
+
+def torch_noncausal_autograd(q, k, v, g, eps: float = EPS):
+    """Gradients of the non-causal formula by torch.autograd in fp64."""
+    import torch
+
+    qt, kt, vt = (torch.as_tensor(np.asarray(x, np.float64)).requires_grad_(True) for x in (q, k, v))
+    gt = torch.as_tensor(np.asarray(g, np.float64))
+    out = torch_noncausal_reference(qt, kt, vt, eps)
+    dq, dk, dv = torch.autograd.grad(out, (qt, kt, vt), gt)
+    return out.detach().numpy(), dq.numpy(), dk.numpy(), dv.numpy()

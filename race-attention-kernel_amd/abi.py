@@ -1,0 +1,139 @@
+"""ctypes view of the C ABI in include/race_mi355x.h.
+
+This is the binding a maintainer of the reference would add to call the
+library without the PyTorch extension: plain pointers, sizes and a stream
+handle.  The declarations mirror the header one to one.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+
+RACE_SUCCESS = 0
+RACE_ERROR_INVALID_VALUE = 1
+RACE_F32 = 0
+RACE_BF16 = 1
+RACE_KERNEL_AUTO = 0
+RACE_KERNEL_VALU = 1
+RACE_KERNEL_MFMA = 2
+RACE_SUB_CHUNK_TOKENS = 64
+
+EXPORTED_SYMBOLS = (
+    "race_abi_version",
+    "race_status_string",
+    "race_shape_supported",
+    "race_select_tile_tokens",
+    "race_fwd_workspace_bytes",
+    "race_fwd",
+    "race_fwd_profiled",
+    "race_noncausal_bwd_workspace_bytes",
+    "race_noncausal_bwd",
+)
+
+
+class RaceShape(ctypes.Structure):
+    _fields_ = [
+        ("num_streams", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("num_tables", ctypes.c_int32),
+        ("num_buckets", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
+class RaceOptions(ctypes.Structure):
+    _fields_ = [("tile_tokens", ctypes.c_int32), ("kernel", ctypes.c_int32)]
+
+
+_configured = False
+
+
+def lib() -> ctypes.CDLL:
+    global _configured
+    L = _lib.cdll()
+    if not _configured:
+        vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+        shp, opp = ctypes.POINTER(RaceShape), ctypes.POINTER(RaceOptions)
+        L.race_abi_version.argtypes = []
+        L.race_abi_version.restype = i32
+        L.race_status_string.argtypes = [i32]
+        L.race_status_string.restype = ctypes.c_char_p
+        L.race_shape_supported.argtypes = [shp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+        L.race_select_tile_tokens.argtypes = [shp, i32, opp, ctypes.POINTER(i32)]
+        L.race_fwd_workspace_bytes.argtypes = [shp, i32, opp, ctypes.POINTER(sz),
+                                               ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        L.race_fwd.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp]
+        L.race_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp,
+                                        ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
+        L.race_noncausal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
+        L.race_noncausal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
+        for name in EXPORTED_SYMBOLS[2:]:
+            getattr(L, name).restype = i32
+        _configured = True
+    return L
+
+
+def shape(N: int, T: int, L: int, R: int, d: int, dtype: int = RACE_F32) -> RaceShape:
+    return RaceShape(N, T, L, R, d, dtype)
+
+
+def options(tile_tokens: int = 0, kernel: int = RACE_KERNEL_AUTO) -> RaceOptions:
+    return RaceOptions(tile_tokens, kernel)
+
+
+def status_string(status: int) -> str:
+    return lib().race_status_string(status).decode()
+
+
+def shape_supported(sh: RaceShape) -> tuple[bool, bool]:
+    ok, mf = ctypes.c_int32(0), ctypes.c_int32(0)
+    st = lib().race_shape_supported(ctypes.byref(sh), ctypes.byref(ok), ctypes.byref(mf))
+    if st != RACE_SUCCESS:
+        raise RuntimeError(status_string(st))
+    return bool(ok.value), bool(mf.value)
+
+
+def fwd_workspace_bytes(sh: RaceShape, causal: bool, opts: RaceOptions | None = None):
+    """(status, bytes, tiles, record_floats)."""
+    b, t, r = ctypes.c_size_t(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    st = lib().race_fwd_workspace_bytes(ctypes.byref(sh), int(causal),
+                                        ctypes.byref(opts) if opts is not None else None,
+                                        ctypes.byref(b), ctypes.byref(t), ctypes.byref(r))
+    return st, b.value, t.value, r.value
+
+
+def noncausal_bwd_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):
+    b = ctypes.c_size_t(0)
+    st = lib().race_noncausal_bwd_workspace_bytes(ctypes.byref(sh),
+                                                  ctypes.byref(opts) if opts is not None else None,
+                                                  ctypes.byref(b))
+    return st, b.value
+
+
+def fwd(q: int, k: int, v: int, out: int, state: int | None, sh: RaceShape, causal: bool,
+        opts: RaceOptions | None, workspace: int | None, workspace_bytes: int, stream: int) -> int:
+    """race_fwd on raw device addresses; returns the status."""
+    return lib().race_fwd(q, k, v, out, state, ctypes.byref(sh), int(causal),
+                          ctypes.byref(opts) if opts is not None else None,
+                          workspace, workspace_bytes, stream)
+
+
+def fwd_profiled(q: int, k: int, v: int, out: int, state: int | None, sh: RaceShape, causal: bool,
+                 opts: RaceOptions | None, workspace: int | None, workspace_bytes: int, stream: int,
+                 events) -> tuple[int, int]:
+    """race_fwd_profiled; ``events`` is a ctypes array of hipEvent_t.  Returns (status, n_events)."""
+    n = ctypes.c_int32(0)
+    st = lib().race_fwd_profiled(q, k, v, out, state, ctypes.byref(sh), int(causal),
+                                 ctypes.byref(opts) if opts is not None else None, workspace,
+                                 workspace_bytes, stream, events, len(events), ctypes.byref(n))
+    return st, n.value
+
+
+def noncausal_bwd(q: int, k: int, v: int, g: int, state: int, dq: int | None, dk: int | None,
+                  dv: int | None, sh: RaceShape, opts: RaceOptions | None, workspace: int | None,
+                  workspace_bytes: int, stream: int) -> int:
+    return lib().race_noncausal_bwd(q, k, v, g, state, dq, dk, dv, ctypes.byref(sh),
+                                    ctypes.byref(opts) if opts is not None else None,
+                                    workspace, workspace_bytes, stream)

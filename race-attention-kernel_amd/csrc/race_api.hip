@@ -1,0 +1,353 @@
+// race_api.hip -- the extern "C" entry points of include/race_mi355x.h:
+// argument validation, tile selection, workspace carving and launch order.
+//
+// Mirrors the reference's torch-free launcher contract
+// (src/causal_v2/kernels/race_causal_fwd.h:40-49): caller-owned outputs and
+// workspace, one stream, no allocation, no host synchronization, first error
+// returned, hipErrorInvalidValue for anything the kernels do not support.
+#include <climits>
+
+#include "race_internal.h"
+
+namespace race {
+namespace {
+
+constexpr int64_t kMaxStreams = 65535;  // grid.y
+constexpr int kMaxAutoTile = 4096;
+
+int64_t round64(int64_t floats) { return ((floats + 63) / 64) * 64; }
+
+bool shape_ok(const race_shape* sh) {
+    if (!sh) return false;
+    if (sh->num_streams < 0 || sh->num_streams > kMaxStreams) return false;
+    if (sh->seq_len < 0 || sh->seq_len > int64_t(INT_MAX) - kMaxAutoTile) return false;
+    if (sh->num_tables < 1 || sh->num_buckets < 1) return false;
+    const int64_t S = int64_t(sh->num_tables) * sh->num_buckets;
+    if (S > 256) return false;
+    if (sh->head_dim < 1 || sh->head_dim > 128) return false;
+    if (sh->dtype != RACE_F32 && sh->dtype != RACE_BF16) return false;
+    const int64_t w = S > sh->head_dim ? S : sh->head_dim;
+    if (sh->num_streams > 0 && sh->seq_len > 0 &&
+        sh->num_streams * sh->seq_len > (int64_t(1) << 62) / w)
+        return false;
+    return true;
+}
+
+int sub(const race_shape* sh) { return sh->num_tables * sh->num_buckets; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int kernel_choice(const race_options* o) { return o ? o->kernel : RACE_KERNEL_AUTO; }
+
+// Resolves which kernel family runs; INVALID_VALUE if the request cannot be met.
+race_status resolve_kernel(const race_shape* sh, int causal, const race_options* o, bool* mfma) {
+    const int k = kernel_choice(o);
+    if (k != RACE_KERNEL_AUTO && k != RACE_KERNEL_VALU && k != RACE_KERNEL_MFMA)
+        return RACE_ERROR_INVALID_VALUE;
+    const bool has = causal && mfma_causal_supported(sub(sh), sh->head_dim);
+    if (k == RACE_KERNEL_MFMA && !has) return RACE_ERROR_INVALID_VALUE;
+    *mfma = (k == RACE_KERNEL_MFMA) || (k == RACE_KERNEL_AUTO && has);
+    return RACE_SUCCESS;
+}
+
+int pow2_floor(int64_t x) {
+    int p = 1;
+    while (int64_t(p) * 2 <= x && p < (1 << 30)) p *= 2;
+    return p;
+}
+
+race_status resolve_tile(const race_shape* sh, int causal, const race_options* o, bool mfma,
+                         int* tile) {
+    if (o && o->tile_tokens != 0) {
+        if (o->tile_tokens < 0 || o->tile_tokens % RACE_SUB_CHUNK_TOKENS != 0)
+            return RACE_ERROR_INVALID_VALUE;
+        *tile = o->tile_tokens;
+        return RACE_SUCCESS;
+    }
+    const int64_t work = sh->num_streams * sh->seq_len;
+    if (work == 0) {
+        *tile = RACE_SUB_CHUNK_TOKENS;
+        return RACE_SUCCESS;
+    }
+    int dev = 0, cus = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return err;
+    if (cus < 1) cus = 1;
+    // Aim for a few resident workgroups per compute unit so the output pass
+    // streams HBM from every CU; longer tiles amortize the tile record
+    // (4*(S*d+S) bytes read and written per tile) over more tokens.
+    const int64_t per_cu = (causal && mfma) ? 2 : 2;
+    int t = pow2_floor(work / (per_cu * cus));
+    if (t < RACE_SUB_CHUNK_TOKENS) t = RACE_SUB_CHUNK_TOKENS;
+    if (t > kMaxAutoTile) t = kMaxAutoTile;
+    *tile = t;
+    return RACE_SUCCESS;
+}
+
+race_status make_problem(const race_shape* sh, int causal, const race_options* o, bool* mfma,
+                         Problem* p) {
+    if (!shape_ok(sh)) return RACE_ERROR_INVALID_VALUE;
+    race_status st = resolve_kernel(sh, causal, o, mfma);
+    if (st != RACE_SUCCESS) return st;
+    int tile = 0;
+    st = resolve_tile(sh, causal, o, *mfma, &tile);
+    if (st != RACE_SUCCESS) return st;
+    p->N = sh->num_streams;
+    p->T = sh->seq_len;
+    p->S = sub(sh);
+    p->d = sh->head_dim;
+    p->dtype = sh->dtype;
+    p->tile = tile;
+    p->tiles = sh->seq_len == 0 ? 0 : (sh->seq_len + tile - 1) / tile;
+    p->rec = record_floats(p->S, p->d);
+    return RACE_SUCCESS;
+}
+
+// Workspace regions, in floats, each a multiple of 64 floats.
+struct FwdLayout {
+    int64_t records = 0;  // [N][tiles][rec]
+    int64_t totals = 0;   // non-causal: [N][rec]
+    int64_t E = 0;        // non-causal: [N][S*d]
+    int64_t total() const { return records + totals + E; }
+};
+
+FwdLayout fwd_layout(const Problem& p, int causal) {
+    FwdLayout l;
+    l.records = p.N * p.tiles * p.rec;
+    if (!causal) {
+        l.totals = p.N * p.rec;
+        l.E = round64(p.N * p.S * p.d);
+    }
+    return l;
+}
+
+struct BwdLayout {
+    int64_t records = 0, totals = 0, E = 0, dB = 0, dA = 0;
+    int64_t total() const { return records + totals + E + dB + dA; }
+};
+
+BwdLayout bwd_layout(const Problem& p) {
+    BwdLayout l;
+    l.records = p.N * p.tiles * p.rec;
+    l.totals = p.N * p.rec;
+    l.E = round64(p.N * p.S * p.d);
+    l.dB = round64(p.N * p.S * p.d);
+    l.dA = round64(p.N * p.S);
+    return l;
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
+hipError_t zero_fill(float* p, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    fill_zero_kernel<<<unsigned((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(p, n);
+    return hipGetLastError();
+}
+
+hipError_t max_lds(int* bytes) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+}
+
+#define RACE_TRY(expr)                                   \
+    do {                                                 \
+        const hipError_t race_err_ = (expr);             \
+        if (race_err_ != hipSuccess) return race_err_;   \
+    } while (0)
+
+}  // namespace
+}  // namespace race
+
+using namespace race;
+
+extern "C" {
+
+int32_t race_abi_version(void) { return RACE_ABI_VERSION; }
+
+const char* race_status_string(race_status status) {
+    if (status == RACE_SUCCESS) return "success";
+    if (status == RACE_ERROR_INVALID_VALUE)
+        return "invalid value: unsupported shape or kernel, null or misaligned pointer, "
+               "workspace too small, or tile length not a positive multiple of "
+               "RACE_SUB_CHUNK_TOKENS";
+    return hipGetErrorString(static_cast<hipError_t>(status));
+}
+
+race_status race_shape_supported(const race_shape* shape, int32_t* supported, int32_t* has_mfma) {
+    if (!shape || !supported) return RACE_ERROR_INVALID_VALUE;
+    *supported = shape_ok(shape) ? 1 : 0;
+    if (has_mfma)
+        *has_mfma = (*supported && mfma_causal_supported(sub(shape), shape->head_dim)) ? 1 : 0;
+    return RACE_SUCCESS;
+}
+
+race_status race_select_tile_tokens(const race_shape* shape, int32_t causal,
+                                    const race_options* opts, int32_t* tile_tokens) {
+    if (!tile_tokens) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    const race_status st = make_problem(shape, causal, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    *tile_tokens = p.tile;
+    return RACE_SUCCESS;
+}
+
+race_status race_fwd_workspace_bytes(const race_shape* shape, int32_t causal,
+                                     const race_options* opts, size_t* bytes, int64_t* tiles,
+                                     int64_t* record_floats_out) {
+    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    const race_status st = make_problem(shape, causal, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(fwd_layout(p, causal).total()) * sizeof(float);
+    if (tiles) *tiles = p.tiles;
+    if (record_floats_out) *record_floats_out = p.rec;
+    return RACE_SUCCESS;
+}
+
+}  // extern "C"
+
+namespace race {
+namespace {
+
+race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void* out, float* state,
+                     const race_shape* shape, int32_t causal, const race_options* opts,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream, Marks* marks) {
+    Problem p;
+    bool mfma = false;
+    race_status st = make_problem(shape, causal, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (state && !aligned16(state)) return RACE_ERROR_INVALID_VALUE;
+    if (p.N == 0 || p.T == 0) {
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(zero_fill(state, p.N * state_floats(p.S, p.d), stream));
+        return marks->mark(stream);
+    }
+    if (!probsQ || !probsK || !V || !out) return RACE_ERROR_INVALID_VALUE;
+    if (!aligned16(probsQ) || !aligned16(probsK) || !aligned16(V) || !aligned16(out))
+        return RACE_ERROR_INVALID_VALUE;
+    const FwdLayout l = fwd_layout(p, causal);
+    if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
+        return RACE_ERROR_INVALID_VALUE;
+    float* ws = static_cast<float*>(workspace);
+    float* records = ws;
+
+    if (causal) {
+        if (mfma) {
+            RACE_TRY(marks->mark(stream));
+            return launch_causal_mfma(probsQ, probsK, V, out, records, state, p, stream, marks);
+        }
+        int lds_limit = 0;
+        RACE_TRY(max_lds(&lds_limit));
+        if (causal_output_valu_lds_bytes(p.S) > size_t(lds_limit)) return RACE_ERROR_INVALID_VALUE;
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(launch_tile_outer_sums(probsK, V, records, p, p.S, p.d, stream));
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(launch_tile_scan(records, state, p, stream));
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(launch_causal_output_valu(probsQ, probsK, V, out, records, p, stream));
+        return marks->mark(stream);
+    }
+
+    float* totals = records + l.records;
+    float* E = totals + l.totals;
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_tile_outer_sums(probsK, V, records, p, p.S, p.d, stream));
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_tile_reduce(records, totals, state, E, p, stream));
+    RACE_TRY(marks->mark(stream));
+    // out = q . E: M[a][c] = E[a*d + c].
+    RACE_TRY(launch_token_map(probsQ, out, E, int64_t(p.S) * p.d, p.d, 1, nullptr, 0, p, p.S, p.d,
+                              stream));
+    return marks->mark(stream);
+}
+
+}  // namespace
+}  // namespace race
+
+extern "C" {
+
+race_status race_fwd(const void* probsQ, const void* probsK, const void* V, void* out,
+                     float* state, const race_shape* shape, int32_t causal,
+                     const race_options* opts, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+    Marks none;
+    return fwd_impl(probsQ, probsK, V, out, state, shape, causal, opts, workspace, workspace_bytes,
+                    stream, &none);
+}
+
+race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void* V, void* out,
+                              float* state, const race_shape* shape, int32_t causal,
+                              const race_options* opts, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream, hipEvent_t* events, int32_t max_events,
+                              int32_t* n_events) {
+    if (!events || max_events < 2 || !n_events) return RACE_ERROR_INVALID_VALUE;
+    Marks marks;
+    marks.events = events;
+    marks.max = max_events;
+    const race_status st = fwd_impl(probsQ, probsK, V, out, state, shape, causal, opts, workspace,
+                                    workspace_bytes, stream, &marks);
+    *n_events = marks.n;
+    return st;
+}
+
+race_status race_noncausal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                               size_t* bytes) {
+    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    const race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(bwd_layout(p).total()) * sizeof(float);
+    return RACE_SUCCESS;
+}
+
+race_status race_noncausal_bwd(const void* probsQ, const void* probsK, const void* V,
+                               const void* dOut, const float* state, void* dQ, void* dK, void* dV,
+                               const race_shape* shape, const race_options* opts, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
+    Problem p;
+    bool mfma = false;
+    race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (p.N == 0 || p.T == 0) return RACE_SUCCESS;
+    if (!state || !dOut || !aligned16(state) || !aligned16(dOut)) return RACE_ERROR_INVALID_VALUE;
+    if (dQ && !aligned16(dQ)) return RACE_ERROR_INVALID_VALUE;
+    if ((dQ || dK || dV) && (!probsQ || !aligned16(probsQ))) return RACE_ERROR_INVALID_VALUE;
+    if (dK && (!V || !aligned16(V) || !aligned16(dK))) return RACE_ERROR_INVALID_VALUE;
+    if (dV && (!probsK || !aligned16(probsK) || !aligned16(dV))) return RACE_ERROR_INVALID_VALUE;
+    if (!dQ && !dK && !dV) return RACE_SUCCESS;
+    const BwdLayout l = bwd_layout(p);
+    if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
+        return RACE_ERROR_INVALID_VALUE;
+    float* records = static_cast<float*>(workspace);
+    float* totals = records + l.records;
+    float* E = totals + l.totals;
+    float* dB = E + l.E;
+    float* dA = dB + l.dB;
+    const int64_t Sd = int64_t(p.S) * p.d;
+
+    RACE_TRY(launch_state_to_E(state, E, p, stream));
+    // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c].
+    if (dQ) RACE_TRY(launch_token_map(dOut, dQ, E, Sd, 1, p.d, nullptr, 0, p, p.d, p.S, stream));
+    if (!dK && !dV) return RACE_SUCCESS;
+    // dE = Q^T dOut, as per-tile partials then a fixed-order reduce.
+    RACE_TRY(launch_tile_outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
+    RACE_TRY(launch_tile_reduce(records, totals, nullptr, nullptr, p, stream));
+    RACE_TRY(launch_bwd_finalize(totals, state, E, dB, dA, p, stream));
+    // dK = V dB^T + dA: M[a = c][b = s] = dB[s*d + c].
+    if (dK) RACE_TRY(launch_token_map(V, dK, dB, Sd, 1, p.d, dA, p.S, p, p.d, p.S, stream));
+    // dV = K dB: M[a = s][b = c] = dB[s*d + c].
+    if (dV) RACE_TRY(launch_token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
+    return RACE_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// race_internal.h -- shared device helpers and launcher declarations of the
+// MI355X RACE attention library.  Not part of the ABI (include/race_mi355x.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "race_mi355x.h"
+
+namespace race {
+
+// Denominator offset of the per-bucket normalization (src/race_baseline.py:47).
+constexpr float kEps = 1e-6f;
+constexpr int kThreads = 256;   // every kernel runs 4 wave64s per workgroup
+constexpr int kSliceCols = 64;  // V/out columns per workgroup in the VALU kernels
+
+// bf16 is carried as its bit pattern.
+using bf16_t = uint16_t;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (IEEE rounding of the top 16 bits);
+// NaN stays NaN (quiet bit set).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return bf16_t(u >> 16);
+}
+
+__device__ __forceinline__ void store_val(float* p, float x) { *p = x; }
+__device__ __forceinline__ void store_val(bf16_t* p, float x) { *p = f32_to_bf16(x); }
+
+// Floats in one tile record: B [S][d] then A [S], padded to 64 floats so every
+// record starts 256-byte aligned.
+inline int64_t record_floats(int64_t S, int64_t d) { return ((S * d + S + 63) / 64) * 64; }
+inline int64_t state_floats(int64_t S, int64_t d) { return S * d + S; }
+
+// Problem description handed from the API layer to the launchers (all sizes
+// validated by the API layer before any launch).
+struct Problem {
+    int64_t N, T;
+    int S, d;
+    int dtype;       // race_dtype
+    int tile;        // tokens per tile (multiple of RACE_SUB_CHUNK_TOKENS)
+    int64_t tiles;   // ceil(T / tile)
+    int64_t rec;     // record_floats(S, d)
+};
+
+// Optional hipEventRecord after each launch (race_fwd_profiled).
+struct Marks {
+    hipEvent_t* events = nullptr;
+    int max = 0;
+    int n = 0;
+    hipError_t mark(hipStream_t stream) {
+        if (!events) return hipSuccess;
+        if (n >= max) return hipErrorInvalidValue;
+        return hipEventRecord(events[n++], stream);
+    }
+};
+
+// ---- VALU kernels (valu_kernels.hip): any supported shape, fp32 math ----
+
+// Per (stream, tile) sums: rec[a*Wb + c] = sum_t x[t][a] * y[t][c] and
+// rec[Wa*Wb + a] = sum_t x[t][a], over the tokens of the tile.
+hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, const Problem& p,
+                                  int Wa, int Wb, hipStream_t stream);
+// In-place exclusive scan of the records over tiles (fixed tile order); the
+// inclusive total goes to state ([N][S*d+S]) when it is not null.
+hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream);
+// Totals over tiles into `totals` ([N][rec]) and, when not null, into
+// `state` ([N][S*d+S]); E = B / (A + eps) into `E` ([N][S][d]) when not null.
+hipError_t launch_tile_reduce(const float* records, float* totals, float* state, float* E,
+                              const Problem& p, hipStream_t stream);
+// Causal output pass from the scanned records.
+hipError_t launch_causal_output_valu(const void* q, const void* k, const void* v, void* out,
+                                     const float* records, const Problem& p, hipStream_t stream);
+// out[n][t][c] = sum_a x[n][t][a] * M[n][a*ms_row + c*ms_col] (+ bias[n][c]).
+hipError_t launch_token_map(const void* x, void* out, const float* M, int64_t m_stream_stride,
+                            int64_t ms_row, int64_t ms_col, const float* bias,
+                            int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
+                            hipStream_t stream);
+// E = B / (A + eps) from state records ([N][S*d+S]) into E ([N][S][d]).
+hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hipStream_t stream);
+// Dynamic LDS of the VALU output pass and map kernels.
+size_t causal_output_valu_lds_bytes(int S);
+size_t token_map_lds_bytes(int Wa);
+// Backward finalize: from dE totals ([N][rec]), the forward state (B, A) and
+// E: dB = dE / (A + eps) into dB ([N][S][d]), dA into dA ([N][S]).
+hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
+                               float* dB, float* dA, const Problem& p, hipStream_t stream);
+
+// ---- MFMA kernels (mfma_causal.hip) ----
+
+// Whether the MFMA causal path has a specialization for (S, d).
+bool mfma_causal_supported(int S, int d);
+hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void* out,
+                              float* records, float* state, const Problem& p, hipStream_t stream,
+                              Marks* marks);
+
+}  // namespace race

@@ -1,0 +1,452 @@
+// valu_kernels.hip -- fp32 vector-ALU kernels of the RACE attention op, for
+// every supported shape (1 <= S <= 256, 1 <= d <= 128).
+//
+// These are the reference-shaped kernels: the causal forward is the
+// three-launch decomposition of the reference's v2a
+// (src/causal_v2/kernels/race_causal_fwd.h:23-27) -- per-tile totals, an
+// exclusive scan over tiles, an output pass walking sub-chunks -- computing
+// the per-bucket function of src/race_baseline.py:45-51 from the chunk
+// identity (docs/causal_v2_design.md:70-77):
+//     Abar_i = A0 + sum_{j<=i} k_j,  W_i = q_i / (Abar_i + eps),
+//     O_i    = W_i . B0 + sum_{j<=i} (W_i . k_j) v_j.
+// The non-causal forward and backward are bucket reductions over T
+// (tile partials, fixed-order reduce) followed by token-parallel maps.
+//
+// Work split: V/out columns are cut into slices of 64 (grid.z) so the state
+// slice B0 [S][64] fits in LDS for S = 256.  No atomics; every sum has a fixed
+// order, so results are bitwise reproducible for a given tile length.
+#include "race_internal.h"
+
+namespace race {
+namespace {
+
+constexpr int kStageTokens = 32;  // tokens staged per step in the reduction kernels
+constexpr int kValuChunk = 32;    // sub-chunk of the causal output pass
+constexpr int kMapTokens = 32;    // tokens per workgroup of the map kernel
+
+template <typename TIn>
+__device__ __forceinline__ float ld(const TIn* __restrict__ p, int64_t i) {
+    return to_f32(p[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Per (tile, stream, column slice): rec[a*Wb + c] = sum_t x[t][a] * y[t][c],
+// rec[Wa*Wb + a] = sum_t x[t][a] (slice 0 only).  Thread (tr, tc) =
+// (tid / 16, tid % 16) owns rows a = tr + 16 i, i < MI, and slice columns
+// tc + 16 j, j < 4, accumulating in registers over the tile's tokens in order.
+template <typename TIn, int MI>
+__global__ __launch_bounds__(kThreads) void tile_outer_sums_kernel(
+    const TIn* __restrict__ x, const TIn* __restrict__ y, float* __restrict__ records, int64_t T,
+    int tile, int64_t tiles, int64_t rec, int Wa, int Wb) {
+    extern __shared__ float smem[];
+    constexpr int kWaPad = MI * 16;
+    float* xs = smem;                          // [kStageTokens][kWaPad]
+    float* ys = xs + kStageTokens * kWaPad;    // [kStageTokens][kSliceCols]
+    const int tid = threadIdx.x;
+    const int tr = tid >> 4, tc = tid & 15;
+    const int64_t n = blockIdx.y;
+    const int64_t ti = blockIdx.x;
+    const int c0 = blockIdx.z * kSliceCols;
+    const int ncols = min(kSliceCols, Wb - c0);
+    const int64_t t_begin = ti * tile;
+    const int64_t t_end = min(T, t_begin + tile);
+    const TIn* xn = x + n * T * Wa;
+    const TIn* yn = y + n * T * Wb;
+
+    float acc[MI][4];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    float asum = 0.f;
+
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kStageTokens) {
+        const int cnt = int(min<int64_t>(kStageTokens, t_end - t0));
+        __syncthreads();
+        for (int e = tid; e < kStageTokens * kWaPad; e += kThreads) {
+            const int i = e / kWaPad, a = e - i * kWaPad;
+            xs[e] = (i < cnt && a < Wa) ? ld(xn, (t0 + i) * Wa + a) : 0.f;
+        }
+        for (int e = tid; e < kStageTokens * kSliceCols; e += kThreads) {
+            const int i = e / kSliceCols, c = e - i * kSliceCols;
+            ys[e] = (i < cnt && c < ncols) ? ld(yn, (t0 + i) * Wb + c0 + c) : 0.f;
+        }
+        __syncthreads();
+        for (int i = 0; i < cnt; ++i) {
+            float yv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) yv[j] = ys[i * kSliceCols + tc + 16 * j];
+#pragma unroll
+            for (int ii = 0; ii < MI; ++ii) {
+                const float xv = xs[i * kWaPad + tr + 16 * ii];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[ii][j] = fmaf(xv, yv[j], acc[ii][j]);
+            }
+        }
+        if (blockIdx.z == 0 && tid < Wa)
+            for (int i = 0; i < cnt; ++i) asum += xs[i * kWaPad + tid];
+    }
+
+    float* r = records + (n * tiles + ti) * rec;
+#pragma unroll
+    for (int ii = 0; ii < MI; ++ii) {
+        const int a = tr + 16 * ii;
+        if (a >= Wa) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = tc + 16 * j;
+            if (c < ncols) r[int64_t(a) * Wb + c0 + c] = acc[ii][j];
+        }
+    }
+    if (blockIdx.z == 0 && tid < Wa) r[int64_t(Wa) * Wb + tid] = asum;
+}
+
+// ---------------------------------------------------------------------------
+// Exclusive scan over tiles, one thread per record element (the element-
+// parallel scan of docs/causal_v2_design.md:242-261), tiles walked in order
+// with 8 loads in flight.
+__global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__ records,
+                                                             float* __restrict__ state,
+                                                             int64_t tiles, int64_t rec, int used) {
+    const int e = blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n = blockIdx.y;
+    if (e >= used) return;
+    float* r = records + n * tiles * rec + e;
+    float run = 0.f;
+    int64_t t = 0;
+    for (; t + 8 <= tiles; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = r[(t + u) * rec];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            r[(t + u) * rec] = run;
+            run += v[u];
+        }
+    }
+    for (; t < tiles; ++t) {
+        const float v = r[t * rec];
+        r[t * rec] = run;
+        run += v;
+    }
+    if (state) state[n * used + e] = run;
+}
+
+__device__ __forceinline__ float sum_over_tiles(const float* __restrict__ r, int64_t tiles,
+                                                int64_t rec) {
+    float sum = 0.f;
+    int64_t t = 0;
+    for (; t + 8 <= tiles; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = r[(t + u) * rec];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += v[u];
+    }
+    for (; t < tiles; ++t) sum += r[t * rec];
+    return sum;
+}
+
+// Totals over tiles (fixed order).  The thread of B element (s, c) also sums
+// A[s] in the same order as the thread of A element s, so E uses exactly the
+// A that is stored.
+__global__ __launch_bounds__(kThreads) void tile_reduce_kernel(
+    const float* __restrict__ records, float* __restrict__ totals, float* __restrict__ state,
+    float* __restrict__ E, int64_t tiles, int64_t rec, int S, int d) {
+    const int e = blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const int used = S * d + S;
+    if (e >= used) return;
+    const float* r = records + n * tiles * rec;
+    const float sum = sum_over_tiles(r + e, tiles, rec);
+    totals[n * rec + e] = sum;
+    if (state) state[n * used + e] = sum;
+    if (E && e < S * d) {
+        const int s = e / d;
+        const float a = sum_over_tiles(r + S * d + s, tiles, rec);
+        E[n * S * d + e] = sum / (a + kEps);
+    }
+}
+
+// E = B / (A + eps) from a state record [S*d + S].
+__global__ __launch_bounds__(kThreads) void state_to_E_kernel(const float* __restrict__ state,
+                                                              float* __restrict__ E, int S, int d) {
+    const int e = blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n = blockIdx.y;
+    if (e >= S * d) return;
+    const float* st = state + n * (S * d + S);
+    E[n * S * d + e] = st[e] / (st[S * d + e / d] + kEps);
+}
+
+// dB = dE / (A + eps); dA[s] = -sum_c dE[s][c] E[s][c] / (A[s] + eps)
+// (the sum over c in order, one thread per s).
+__global__ __launch_bounds__(kThreads) void bwd_finalize_kernel(
+    const float* __restrict__ dE_totals, const float* __restrict__ state,
+    const float* __restrict__ E, float* __restrict__ dB, float* __restrict__ dA, int64_t rec,
+    int S, int d) {
+    const int e = blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const float* dE = dE_totals + n * rec;
+    const float* A = state + n * (S * d + S) + S * d;
+    if (e < S * d) {
+        dB[n * S * d + e] = dE[e] / (A[e / d] + kEps);
+    } else if (e < S * d + S) {
+        const int s = e - S * d;
+        const float den = A[s] + kEps;
+        const float* En = E + n * S * d + int64_t(s) * d;
+        float acc = 0.f;
+        for (int c = 0; c < d; ++c) acc = fmaf(dE[s * d + c], En[c], acc);
+        dA[n * S + s] = -acc / den;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Causal output pass, one workgroup per (tile, stream, 64-column slice).
+// Walks the tile in sub-chunks of kValuChunk tokens with the state slice
+// (A0 [S], B0 [S][64]) in LDS, starting from the tile's exclusive prefix.
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void causal_output_valu_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
+    TIn* __restrict__ out, const float* __restrict__ records, int64_t T, int S, int d, int tile,
+    int64_t tiles, int64_t rec) {
+    extern __shared__ float smem[];
+    constexpr int C = kValuChunk;
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const int64_t ti = blockIdx.x;
+    const int c0 = blockIdx.z * kSliceCols;
+    const int ncols = min(kSliceCols, d - c0);
+    float* B0 = smem;                  // [S][64]
+    float* A0 = B0 + S * kSliceCols;   // [S]
+    float* W = A0 + S;                 // [C][S]: q, then w = q / (Abar + eps)
+    float* Ks = W + C * S;             // [C][S]
+    float* Vs = Ks + C * S;            // [C][64]
+    float* P = Vs + C * kSliceCols;    // [C][C]: tril(W K^T)
+
+    const float* r = records + (n * tiles + ti) * rec;
+    for (int e = tid; e < S * kSliceCols; e += kThreads) {
+        const int s = e / kSliceCols, c = e - s * kSliceCols;
+        B0[e] = c < ncols ? r[int64_t(s) * d + c0 + c] : 0.f;
+    }
+    for (int s = tid; s < S; s += kThreads) A0[s] = r[int64_t(S) * d + s];
+
+    const int64_t t_begin = ti * tile;
+    const int64_t t_end = min(T, t_begin + tile);
+    const TIn* qn = q + n * T * S;
+    const TIn* kn = k + n * T * S;
+    const TIn* vn = v + n * T * d;
+    TIn* on = out + n * T * d;
+
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += C) {
+        const int cnt = int(min<int64_t>(C, t_end - t0));
+        __syncthreads();
+        for (int e = tid; e < cnt * S; e += kThreads) {
+            W[e] = ld(qn, t0 * S + e);
+            Ks[e] = ld(kn, t0 * S + e);
+        }
+        for (int e = tid; e < cnt * kSliceCols; e += kThreads) {
+            const int i = e / kSliceCols, c = e - i * kSliceCols;
+            Vs[e] = c < ncols ? ld(vn, (t0 + i) * d + c0 + c) : 0.f;
+        }
+        __syncthreads();
+        // Inclusive running mass per bucket and the rescaled queries.
+        for (int s = tid; s < S; s += kThreads) {
+            float run = A0[s];
+            for (int i = 0; i < cnt; ++i) {
+                run += Ks[i * S + s];
+                W[i * S + s] = W[i * S + s] / (run + kEps);
+            }
+            A0[s] = run;
+        }
+        __syncthreads();
+        // P = tril(W K^T), diagonal included.
+        for (int e = tid; e < cnt * cnt; e += kThreads) {
+            const int i = e / cnt, j = e - i * cnt;
+            float acc = 0.f;
+            if (j <= i)
+                for (int s = 0; s < S; ++s) acc = fmaf(W[i * S + s], Ks[j * S + s], acc);
+            P[i * C + j] = acc;
+        }
+        __syncthreads();
+        // O = W B0 + P V.
+        for (int e = tid; e < cnt * kSliceCols; e += kThreads) {
+            const int i = e / kSliceCols, c = e - i * kSliceCols;
+            if (c >= ncols) continue;
+            float acc = 0.f;
+            for (int s = 0; s < S; ++s) acc = fmaf(W[i * S + s], B0[s * kSliceCols + c], acc);
+            for (int j = 0; j <= i; ++j) acc = fmaf(P[i * C + j], Vs[j * kSliceCols + c], acc);
+            store_val(on + (t0 + i) * d + c0 + c, acc);
+        }
+        __syncthreads();
+        // B0 += K^T V.
+        for (int e = tid; e < S * kSliceCols; e += kThreads) {
+            const int s = e / kSliceCols, c = e - s * kSliceCols;
+            float acc = 0.f;
+            for (int i = 0; i < cnt; ++i) acc = fmaf(Ks[i * S + s], Vs[i * kSliceCols + c], acc);
+            B0[e] += acc;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// out[t][c] = sum_a x[t][a] * M[a*ms_row + c*ms_col] (+ bias[c]), one
+// workgroup per (kMapTokens tokens, stream, 64-column slice).  Thread
+// (i, tc) = (tid / 8, tid % 8) computes token i, slice columns tc + 8 j.
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void token_map_kernel(
+    const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
+    int64_t m_stream_stride, int64_t ms_row, int64_t ms_col, const float* __restrict__ bias,
+    int64_t bias_stream_stride, int64_t T, int Wa, int Wb) {
+    extern __shared__ float smem[];
+    float* Ms = smem;                    // [Wa][64]
+    float* xs = Ms + Wa * kSliceCols;    // [kMapTokens][Wa]
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const int c0 = blockIdx.z * kSliceCols;
+    const int ncols = min(kSliceCols, Wb - c0);
+    const int64_t t0 = int64_t(blockIdx.x) * kMapTokens;
+    const int cnt = int(min<int64_t>(kMapTokens, T - t0));
+    const float* Mn = M + n * m_stream_stride;
+    for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
+        const int a = e / kSliceCols, c = e - a * kSliceCols;
+        Ms[e] = c < ncols ? Mn[a * ms_row + (c0 + c) * ms_col] : 0.f;
+    }
+    const TIn* xn = x + n * T * Wa;
+    for (int e = tid; e < cnt * Wa; e += kThreads) xs[e] = ld(xn, t0 * Wa + e);
+    __syncthreads();
+    const int i = tid >> 3, tc = tid & 7;
+    if (i >= cnt) return;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int a = 0; a < Wa; ++a) {
+        const float xv = xs[i * Wa + a];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(xv, Ms[a * kSliceCols + tc + 8 * j], acc[j]);
+    }
+    TIn* on = out + (n * T + t0 + i) * Wb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = tc + 8 * j;
+        if (c < ncols) {
+            float val = acc[j];
+            if (bias) val += bias[n * bias_stream_stride + c0 + c];
+            store_val(on + c0 + c, val);
+        }
+    }
+}
+
+int rows_per_thread(int Wa) {
+    const int need = (Wa + 15) / 16;
+    int mi = 1;
+    while (mi < need) mi *= 2;
+    return mi;
+}
+
+}  // namespace
+
+hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, const Problem& p,
+                                  int Wa, int Wb, hipStream_t stream) {
+    const int mi = rows_per_thread(Wa);
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N), unsigned((Wb + kSliceCols - 1) / kSliceCols));
+    const size_t lds = size_t(kStageTokens) * (mi * 16 + kSliceCols) * sizeof(float);
+#define RACE_OUTER(TIN, MI)                                                                      \
+    tile_outer_sums_kernel<TIN, MI><<<grid, kThreads, lds, stream>>>(                            \
+        static_cast<const TIN*>(x), static_cast<const TIN*>(y), records, p.T, p.tile, p.tiles, \
+        p.rec, Wa, Wb)
+#define RACE_OUTER_MI(TIN)                     \
+    switch (mi) {                              \
+        case 1: RACE_OUTER(TIN, 1); break;     \
+        case 2: RACE_OUTER(TIN, 2); break;     \
+        case 4: RACE_OUTER(TIN, 4); break;     \
+        case 8: RACE_OUTER(TIN, 8); break;     \
+        default: RACE_OUTER(TIN, 16); break;   \
+    }
+    if (p.dtype == RACE_BF16) {
+        RACE_OUTER_MI(bf16_t)
+    } else {
+        RACE_OUTER_MI(float)
+    }
+#undef RACE_OUTER_MI
+#undef RACE_OUTER
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream) {
+    const int used = p.S * p.d + p.S;
+    const dim3 grid(unsigned((used + kThreads - 1) / kThreads), unsigned(p.N));
+    tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.tiles, p.rec, used);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_reduce(const float* records, float* totals, float* state, float* E,
+                              const Problem& p, hipStream_t stream) {
+    const int used = p.S * p.d + p.S;
+    const dim3 grid(unsigned((used + kThreads - 1) / kThreads), unsigned(p.N));
+    tile_reduce_kernel<<<grid, kThreads, 0, stream>>>(records, totals, state, E, p.tiles, p.rec,
+                                                      p.S, p.d);
+    return hipGetLastError();
+}
+
+hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hipStream_t stream) {
+    const dim3 grid(unsigned((p.S * p.d + kThreads - 1) / kThreads), unsigned(p.N));
+    state_to_E_kernel<<<grid, kThreads, 0, stream>>>(state, E, p.S, p.d);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
+                               float* dB, float* dA, const Problem& p, hipStream_t stream) {
+    const int used = p.S * p.d + p.S;
+    const dim3 grid(unsigned((used + kThreads - 1) / kThreads), unsigned(p.N));
+    bwd_finalize_kernel<<<grid, kThreads, 0, stream>>>(dE_totals, state, E, dB, dA, p.rec, p.S,
+                                                       p.d);
+    return hipGetLastError();
+}
+
+size_t causal_output_valu_lds_bytes(int S) {
+    const int C = kValuChunk;
+    return size_t(S * kSliceCols + S + 2 * C * S + C * kSliceCols + C * C) * sizeof(float);
+}
+
+hipError_t launch_causal_output_valu(const void* q, const void* k, const void* v, void* out,
+                                     const float* records, const Problem& p, hipStream_t stream) {
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N), unsigned((p.d + kSliceCols - 1) / kSliceCols));
+    const size_t lds = causal_output_valu_lds_bytes(p.S);
+    if (p.dtype == RACE_BF16) {
+        causal_output_valu_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+            static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+            static_cast<const bf16_t*>(v), static_cast<bf16_t*>(out), records, p.T, p.S, p.d,
+            p.tile, p.tiles, p.rec);
+    } else {
+        causal_output_valu_kernel<float><<<grid, kThreads, lds, stream>>>(
+            static_cast<const float*>(q), static_cast<const float*>(k),
+            static_cast<const float*>(v), static_cast<float*>(out), records, p.T, p.S, p.d, p.tile,
+            p.tiles, p.rec);
+    }
+    return hipGetLastError();
+}
+
+size_t token_map_lds_bytes(int Wa) {
+    return size_t(Wa * kSliceCols + kMapTokens * Wa) * sizeof(float);
+}
+
+hipError_t launch_token_map(const void* x, void* out, const float* M, int64_t m_stream_stride,
+                            int64_t ms_row, int64_t ms_col, const float* bias,
+                            int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
+                            hipStream_t stream) {
+    const dim3 grid(unsigned((p.T + kMapTokens - 1) / kMapTokens), unsigned(p.N),
+                    unsigned((Wb + kSliceCols - 1) / kSliceCols));
+    const size_t lds = token_map_lds_bytes(Wa);
+    if (p.dtype == RACE_BF16) {
+        token_map_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+            static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), M, m_stream_stride, ms_row,
+            ms_col, bias, bias_stream_stride, p.T, Wa, Wb);
+    } else {
+        token_map_kernel<float><<<grid, kThreads, lds, stream>>>(
+            static_cast<const float*>(x), static_cast<float*>(out), M, m_stream_stride, ms_row,
+            ms_col, bias, bias_stream_stride, p.T, Wa, Wb);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace race

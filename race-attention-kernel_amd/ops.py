@@ -1,0 +1,116 @@
+"""The drop-in op: race_fused_fwd(probsQ, probsK, V, causal).
+
+Replaces the hot span of the reference's BatchedACE.forward
+(src/race_baseline.py:45-51): given the bucket probabilities the hashing
+produced (src/race_baseline.py:43-44), returns
+
+    out[n, t] = sum_s probsQ[n, t, s] * B[n, t, s, :] / (A[n, t, s] + 1e-6)
+
+with A, B the inclusive running sums of probsK and probsK (x) V over tokens
+(causal) or their totals over the whole sequence (non-causal,
+analysis/hot-path.md:157-162).  The 5-D prefix tensors of the reference never
+exist: the HIP kernels carry the per-bucket state on chip.
+
+The autograd wrapper follows the reference's non-causal op
+(src/noncausal/ops.py:20-63): it saves the inputs plus the small per-bucket
+state, is once_differentiable, makes the incoming gradient dense and returns
+only the gradients autograd asks for.  The causal backward does not exist in
+the reference either and raises.
+"""
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _lib
+
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2}
+
+
+def _kernel_id(kernel: str | int) -> int:
+    if isinstance(kernel, int):
+        return kernel
+    try:
+        return KERNELS[kernel]
+    except KeyError:
+        raise ValueError(f"kernel must be one of {sorted(KERNELS)}, got {kernel!r}") from None
+
+
+def _dense(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+class RaceFusedFunction(torch.autograd.Function):
+    """out = race_fused_fwd(probsQ, probsK, V, causal) on the HIP kernels."""
+
+    @staticmethod
+    def forward(ctx, probsQ, probsK, V, causal, tile_tokens, kernel):
+        needs = any(ctx.needs_input_grad[:3])
+        want_state = needs and not causal
+        out, state = _lib.ext().forward(probsQ, probsK, V, bool(causal), int(tile_tokens),
+                                        int(kernel), want_state)
+        ctx.causal = bool(causal)
+        ctx.tile_tokens = int(tile_tokens)
+        if want_state:
+            ctx.save_for_backward(probsQ, probsK, V, state)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_out):
+        if ctx.causal:
+            raise RuntimeError(
+                "race_fused_fwd: the causal backward is not implemented (the reference has none "
+                "either); only causal=False is differentiable")
+        need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        if not (need_q or need_k or need_v):
+            return None, None, None, None, None, None
+        q, k, v, state = ctx.saved_tensors
+        grad_out = _dense(grad_out.to(v.dtype))
+        dq, dk, dv = _lib.ext().noncausal_backward(q, k, v, grad_out, state, need_q, need_k,
+                                                  need_v, ctx.tile_tokens)
+        return dq, dk, dv, None, None, None
+
+
+def race_fused_fwd(probsQ: torch.Tensor, probsK: torch.Tensor, V: torch.Tensor, causal: bool = True,
+                   *, tile_tokens: int = 0, kernel: str | int = "auto") -> torch.Tensor:
+    """Per-bucket RACE attention on MI355X.
+
+    Args:
+        probsQ, probsK: [N, T, L, R] (or [N, T, S]) bucket probabilities,
+            float32 or bfloat16, on a ROCm device, contiguous.
+        V: [N, T, d] values of the same dtype and device.
+        causal: inclusive running sums (True) or full-sequence sums (False).
+        tile_tokens: 0 for automatic, else a positive multiple of 64 (the
+            tokens each workgroup of the causal output pass owns).
+        kernel: "auto", "valu" (fp32 vector kernels) or "mfma" (matrix cores).
+
+    Returns:
+        out: [N, T, d] in V's dtype.
+    """
+    return RaceFusedFunction.apply(probsQ, probsK, V, causal, tile_tokens, _kernel_id(kernel))
+
+
+def race_fused_fwd_with_state(probsQ, probsK, V, causal: bool = True, *, tile_tokens: int = 0,
+                              kernel: str | int = "auto"):
+    """(out, state): state [N, S*d + S] fp32 holds B [S, d] then A [S], the
+    per-bucket sums over all T tokens (for causal=True the decode hand-off of
+    src/causal_v2/kernels/race_causal_fwd.h:20-21).  No autograd."""
+    return _lib.ext().forward(probsQ, probsK, V, bool(causal), int(tile_tokens),
+                              _kernel_id(kernel), True)
+
+
+def race_noncausal_backward(probsQ, probsK, V, dOut, state, *, need=(True, True, True),
+                            tile_tokens: int = 0):
+    """(dQ, dK, dV) of the non-causal forward for upstream gradient dOut."""
+    return _lib.ext().noncausal_backward(probsQ, probsK, V, _dense(dOut), state, *need,
+                                         tile_tokens)
+
+
+def select_tile_tokens(N: int, T: int, L: int, R: int, d: int, *, bf16: bool = False,
+                       causal: bool = True, tile_tokens: int = 0, kernel: str | int = "auto") -> int:
+    return _lib.ext().select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens,
+                                         _kernel_id(kernel))

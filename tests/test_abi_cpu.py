@@ -1,0 +1,166 @@
+"""CPU tests of the boundary: the C-ABI library loads and exports what the header
+declares, pure host logic (shape limits, workspace sizes, argument checks)
+answers without touching a device, and the PyTorch binding validates its
+inputs.  No kernel is launched here."""
+from __future__ import annotations
+
+import pathlib
+import re
+
+import pytest
+
+REPO = pathlib.Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "race_mi355x.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(race_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(race):
+    from race_attention_kernel_amd import _lib, abi
+
+    lib = _lib.cdll()
+    names = declared_functions()
+    assert names, "no declarations found in the header"
+    for name in names:
+        assert hasattr(lib, name), f"librace_mi355x.so does not export {name}"
+    assert sorted(abi.EXPORTED_SYMBOLS) == names
+
+
+def test_abi_version_and_status_strings(race):
+    from race_attention_kernel_amd import abi
+
+    assert abi.lib().race_abi_version() == 1
+    assert abi.status_string(0) == "success"
+    assert "invalid value" in abi.status_string(1)
+
+
+@pytest.mark.parametrize("L, R, d, ok", [(4, 16, 64, True), (8, 32, 128, True), (1, 1, 1, True),
+                                         (16, 16, 64, True), (16, 17, 64, False), (4, 16, 129, False),
+                                         (0, 16, 64, False), (4, 16, 0, False)])
+def test_shape_limits(race, L, R, d, ok):
+    from race_attention_kernel_amd import abi
+
+    supported, _ = abi.shape_supported(abi.shape(8, 1024, L, R, d))
+    assert supported == ok
+
+
+def test_stream_and_length_limits(race):
+    from race_attention_kernel_amd import abi
+
+    assert abi.shape_supported(abi.shape(65535, 1, 4, 16, 64))[0]
+    assert not abi.shape_supported(abi.shape(65536, 1, 4, 16, 64))[0]
+    assert not abi.shape_supported(abi.shape(-1, 1, 4, 16, 64))[0]
+    assert not abi.shape_supported(abi.shape(8, 1, 4, 16, 64, dtype=7))[0]
+
+
+def test_workspace_bytes_for_explicit_tiles(race):
+    # Pure host arithmetic when the tile length is given (no device query).
+    from race_attention_kernel_amd import abi
+
+    sh = abi.shape(8, 65536, 4, 16, 64)
+    st, nbytes, tiles, rec = abi.fwd_workspace_bytes(sh, True, abi.options(1024, abi.RACE_KERNEL_VALU))
+    assert st == 0
+    assert tiles == 64 and rec == 4160 and rec % 64 == 0
+    assert nbytes == 8 * 64 * 4160 * 4
+    # Ragged T: ceil division.
+    st, _, tiles, _ = abi.fwd_workspace_bytes(abi.shape(2, 1025, 4, 16, 64), True, abi.options(512, 1))
+    assert st == 0 and tiles == 3
+    # Non-causal adds the totals and E regions.
+    st, nc_bytes, _, _ = abi.fwd_workspace_bytes(sh, False, abi.options(1024, abi.RACE_KERNEL_VALU))
+    assert st == 0 and nc_bytes == (8 * 64 * 4160 + 8 * 4160 + 8 * 64 * 64) * 4
+    st, bwd_bytes = abi.noncausal_bwd_workspace_bytes(sh, abi.options(1024, 0))
+    assert st == 0 and bwd_bytes > nc_bytes
+
+
+def test_scratch_per_token_is_constant(race):
+    # The causal workspace is O(T / tile): per token it stays at 4 * rec / tile bytes.
+    from race_attention_kernel_amd import abi
+
+    per_token = []
+    for T in (1 << 17, 1 << 18, 1 << 20):
+        st, nbytes, _, _ = abi.fwd_workspace_bytes(abi.shape(8, T, 4, 16, 64, abi.RACE_BF16), True,
+                                                   abi.options(4096, 1))
+        assert st == 0
+        per_token.append(nbytes / T)
+    assert max(per_token) == min(per_token) and per_token[0] <= 8 * 4160 * 4 / 4096 + 1e-9
+
+
+@pytest.mark.parametrize("tile", [-64, 32, 100])
+def test_invalid_tile_lengths_are_rejected(race, tile):
+    from race_attention_kernel_amd import abi
+
+    st, *_ = abi.fwd_workspace_bytes(abi.shape(8, 4096, 4, 16, 64), True, abi.options(tile, 1))
+    assert st == abi.RACE_ERROR_INVALID_VALUE
+
+
+def test_invalid_arguments_are_rejected_before_any_launch(race):
+    from race_attention_kernel_amd import abi
+
+    opts = abi.options(64, abi.RACE_KERNEL_VALU)
+    bad = abi.shape(8, 1024, 4, 16, 300)
+    assert abi.fwd(0, 0, 0, 0, None, bad, True, opts, None, 0, 0) == abi.RACE_ERROR_INVALID_VALUE
+    good = abi.shape(8, 1024, 4, 16, 64)
+    # Null inputs, misaligned pointers, missing workspace.
+    assert abi.fwd(0, 0, 0, 0, None, good, True, opts, None, 0, 0) == abi.RACE_ERROR_INVALID_VALUE
+    assert abi.fwd(16, 16, 16, 18, None, good, True, opts, 64, 1 << 30, 0) == abi.RACE_ERROR_INVALID_VALUE
+    assert abi.fwd(16, 16, 16, 16, None, good, True, opts, None, 0, 0) == abi.RACE_ERROR_INVALID_VALUE
+    assert abi.fwd(16, 16, 16, 16, None, good, True, opts, 64, 16, 0) == abi.RACE_ERROR_INVALID_VALUE
+    # Bad kernel id.
+    assert abi.fwd(16, 16, 16, 16, None, good, True, abi.options(64, 9), 64, 1 << 30, 0) == \
+        abi.RACE_ERROR_INVALID_VALUE
+    # The non-causal path has no MFMA kernel.
+    assert abi.fwd(16, 16, 16, 16, None, good, False, abi.options(64, abi.RACE_KERNEL_MFMA), 64, 1 << 30,
+                   0) == abi.RACE_ERROR_INVALID_VALUE
+    # Backward needs the state and dOut.
+    assert abi.noncausal_bwd(16, 16, 16, 0, 0, 16, 16, 16, good, opts, 64, 1 << 30, 0) == \
+        abi.RACE_ERROR_INVALID_VALUE
+
+
+def test_torch_binding_validates_inputs_on_the_host(race, ext):
+    import torch
+
+    q, k, v = race.make_inputs(1, 64, 4, 16, 64)
+    with pytest.raises(RuntimeError, match="must be a GPU tensor"):
+        ext.forward(q, k, v, True)
+    with pytest.raises(ValueError):
+        race.race_fused_fwd(q, k, v, True, kernel="tensor")
+    assert ext.shape_supported(4, 16, 64)[0]
+    assert not ext.shape_supported(4, 16, 256)[0]
+    assert ext.abi_version() == 1
+    with pytest.raises(RuntimeError):
+        ext.select_tile_tokens(8, 1024, 4, 16, 64, False, True, 48, 0)
+    del torch
+
+
+def test_inputs_are_seeded_softmax_probabilities(race):
+    import torch
+
+    a = race.make_inputs(2, 33, 4, 16, 8, seed=3, grad_out=True)
+    b = race.make_inputs(2, 33, 4, 16, 8, seed=3, grad_out=True)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    q, k, v, g = a
+    assert q.shape == (2, 33, 4, 16) and v.shape == (2, 33, 8) and g.shape == v.shape
+    torch.testing.assert_close(q.sum(-1), torch.ones(2, 33, 4))
+    assert (q > 0).all() and (k > 0).all()
+    bq, _, _ = race.make_inputs(2, 33, 4, 16, 8, seed=3, dtype=torch.bfloat16)
+    assert bq.dtype == torch.bfloat16 and torch.equal(bq, q.to(torch.bfloat16))
+
+
+def test_configs_match_baseline(race):
+    c = race.CONFIGS
+    assert (c["cfg2_causal_fp32"].N, c["cfg2_causal_fp32"].S, c["cfg2_causal_fp32"].d) == (8, 64, 64)
+    assert c["cfg4_noncausal_fp32"].N == 384 and not c["cfg4_noncausal_fp32"].causal
+    assert (c["cfg5_causal_bf16_S256"].S, c["cfg5_causal_bf16_S256"].d) == (256, 128)
+
+
+def test_product_path_never_imports_the_oracle():
+    pkg = REPO / "race-attention-kernel_amd"
+    for path in list(pkg.glob("*.py")) + list((pkg / "csrc").glob("*")):
+        text = path.read_text(errors="ignore")
+        hit = re.search(r"liboracle|race_oracle|oracle\.py|load_oracle|from oracle|import oracle", text)
+        assert hit is None, f"{path.name} reaches the oracle: {hit.group(0)}"
