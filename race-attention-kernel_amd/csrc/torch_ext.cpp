@@ -17,8 +17,8 @@
 // TORCH_CHECK failures surface as RuntimeError.
 #include <torch/extension.h>
 
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <c10/core/DeviceGuard.h>
 
 #include <cstdint>
 #include <tuple>
@@ -93,7 +93,7 @@ FwdResult run_forward(const at::Tensor& q, const at::Tensor& k, const at::Tensor
                       int64_t tile_tokens, int64_t kernel, bool want_state) {
     const race_shape sh = validate(q, k, v);
     const race_options opts = make_options(tile_tokens, kernel);
-    const c10::hip::HIPGuard guard(q.device());
+    const c10::DeviceGuard guard(q.device());
     FwdResult r;
     r.out = at::empty_like(v);
     const int64_t S = int64_t(sh.num_tables) * sh.num_buckets;
@@ -104,7 +104,7 @@ FwdResult run_forward(const at::Tensor& q, const at::Tensor& k, const at::Tensor
                  "race_fwd_workspace_bytes");
     check_status(race_select_tile_tokens(&sh, causal, &opts, &r.tile), "race_select_tile_tokens");
     r.workspace = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
-    const hipStream_t stream = c10::hip::getCurrentHIPStream().stream();
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
     check_status(race_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), r.out.data_ptr(),
                           want_state ? r.state.data_ptr<float>() : nullptr, &sh, causal, &opts,
                           r.workspace.data_ptr(), bytes, stream),
@@ -151,7 +151,7 @@ noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
                     state.device() == q.device(),
                 "state must be the forward's fp32 [N, S*d + S] state on the same device");
     const race_options opts = make_options(tile_tokens, RACE_KERNEL_AUTO);
-    const c10::hip::HIPGuard guard(q.device());
+    const c10::DeviceGuard guard(q.device());
     at::Tensor dq, dk, dv;
     if (need_q) dq = at::empty_like(q);
     if (need_k) dk = at::empty_like(k);
@@ -160,7 +160,7 @@ noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
     check_status(race_noncausal_bwd_workspace_bytes(&sh, &opts, &bytes),
                  "race_noncausal_bwd_workspace_bytes");
     at::Tensor ws = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
-    const hipStream_t stream = c10::hip::getCurrentHIPStream().stream();
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
     check_status(race_noncausal_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
                                     state.data_ptr<float>(), need_q ? dq.data_ptr() : nullptr,
                                     need_k ? dk.data_ptr() : nullptr,

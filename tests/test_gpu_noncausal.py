@@ -52,6 +52,21 @@ def test_cfg4_gradients_match_torch_autograd(race, oracle, cuda):
         assert per_stream_rel_err(to_np(got[pick]), want) <= FP32_TOL
 
 
+def dk_term_scale(q, k, v, g, eps=1e-6):
+    """Per-stream max over (t, s) of sum_c |v[t,c] dB[s,c]| + |dA[s]|: the size of
+    the terms whose sum is dK.  When they cancel (S = 1 makes dK = q g v eps /
+    (k + eps)^2, ~1e-6 of each term), fp32 can only be accurate relative to
+    this, so dK's error is bounded by tol * this scale."""
+    q, k, v, g = (np.asarray(x, np.float64) for x in (q, k, v, g))
+    A = k.sum(1)                                            # [N,S]
+    E = np.einsum("nts,ntc->nsc", k, v) / (A[..., None] + eps)
+    dE = np.einsum("nts,ntc->nsc", q, g)
+    dB = dE / (A[..., None] + eps)
+    dA = -(dE * E).sum(-1) / (A + eps)
+    terms = np.einsum("ntc,nsc->nts", np.abs(v), np.abs(dB)) + np.abs(dA)[:, None, :]
+    return terms.reshape(terms.shape[0], -1).max(1)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("L, R, d", [(1, 1, 1), (2, 8, 32), (4, 16, 64), (3, 5, 7), (8, 32, 128)])
 @pytest.mark.parametrize("T", [1, 63, 65, 1000])
@@ -65,7 +80,9 @@ def test_shapes(race, oracle, cuda, dtype, L, R, d, T):
     tol = tol_for(dtype)
     assert per_stream_rel_err(to_np(out), ref_out) <= tol
     assert per_stream_rel_err(to_np(dq), rq) <= tol
-    assert per_stream_rel_err(to_np(dk), rk) <= tol
+    scale = dk_term_scale(to_np(q), to_np(k), to_np(v), to_np(g))
+    dk_err = np.abs(to_np(dk).astype(np.float64) - rk).reshape(3, -1).max(1)
+    assert (dk_err <= tol * scale).all()
     assert per_stream_rel_err(to_np(dv), rv) <= tol
 
 
