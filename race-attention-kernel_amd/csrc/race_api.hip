@@ -78,7 +78,7 @@ race_status resolve_tile(const race_shape* sh, int causal, const race_options* o
     // Aim for a few resident workgroups per compute unit so the output pass
     // streams HBM from every CU; longer tiles amortize the tile record
     // (4*(S*d+S) bytes read and written per tile) over more tokens.
-    const int64_t per_cu = (causal && mfma) ? 2 : 2;
+    const int64_t per_cu = (causal && mfma) ? 4 : 2;
     int t = pow2_floor(work / (per_cu * cus));
     if (t < RACE_SUB_CHUNK_TOKENS) t = RACE_SUB_CHUNK_TOKENS;
     if (t > kMaxAutoTile) t = kMaxAutoTile;
