@@ -62,6 +62,7 @@ WORKLOADS = {
 PHASES = {
     (True, "valu"): ["tile_sums", "tile_scan", "output_pass_valu"],
     (False, "valu"): ["tile_sums", "tile_reduce", "token_map"],
+    (True, "mfma"): ["tile_sums_mfma", "tile_scan", "output_pass_mfma"],
 }
 
 
@@ -108,7 +109,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
     ap.add_argument("--T", type=int, default=0)
-    ap.add_argument("--kernel", choices=["auto", "valu", "mfma"], default="auto")
+    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
@@ -121,6 +122,7 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
     state = 4.0 * cfg.N * tiles * rec
     return {
         "tile_sums": es * (S + d) * NT + state,
+        "tile_sums_mfma": es * (S + d) * NT + state,
         "tile_scan": 2 * state,
         "tile_reduce": state,
         "output_pass_valu": es * (2 * S + 2 * d) * NT + state,
@@ -202,7 +204,7 @@ def main() -> int:
     tile = race.select_tile_tokens(cfg.N, T, cfg.L, cfg.R, cfg.d, bf16=(es == 2), causal=cfg.causal,
                                    tile_tokens=args.tile, kernel=kernel_id)
     family = "valu"
-    if cfg.causal and (kernel_id == 2 or (kernel_id == 0 and race.ops._lib.ext().shape_supported(
+    if cfg.causal and (kernel_id in (2, 3) or (kernel_id == 0 and race.ops._lib.ext().shape_supported(
             cfg.L, cfg.R, cfg.d)[1])):
         family = "mfma"
     ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)

@@ -65,12 +65,15 @@ typedef enum race_dtype {
  * exists for (S, d) and the VALU kernels otherwise.  VALU forces the fp32
  * vector-ALU kernels (the reference-shaped path, any supported shape); MFMA
  * forces the matrix-core kernels and fails with RACE_ERROR_INVALID_VALUE if
- * the shape has none.  Mirrors the reference binding's tensor_cores flag
- * (src/causal_v2/kernels/torch_binding.cpp:252-254). */
+ * the shape has none.  The MFMA path runs one wave per tile where a tile's
+ * working set fits (S = d = 64) and workgroup-cooperative tiles otherwise;
+ * MFMA_WG forces the workgroup-cooperative kernels.  Mirrors the reference
+ * binding's tensor_cores flag (src/causal_v2/kernels/torch_binding.cpp:252-254). */
 typedef enum race_kernel {
     RACE_KERNEL_AUTO = 0,
     RACE_KERNEL_VALU = 1,
-    RACE_KERNEL_MFMA = 2
+    RACE_KERNEL_MFMA = 2,
+    RACE_KERNEL_MFMA_WG = 3
 } race_kernel;
 
 /* Shape of one call.  Mirrors CausalShape

@@ -17,6 +17,7 @@ RACE_BF16 = 1
 RACE_KERNEL_AUTO = 0
 RACE_KERNEL_VALU = 1
 RACE_KERNEL_MFMA = 2
+RACE_KERNEL_MFMA_WG = 3
 RACE_SUB_CHUNK_TOKENS = 64
 
 EXPORTED_SYMBOLS = (

@@ -15,8 +15,8 @@
 //
 // Launch sequence (the decomposition of the reference's v2,
 // src/causal_v2/kernels/race_causal_fwd.h:23-27, for the per-bucket function):
-//   1. tile_sums_mfma_kernel   per (tile, stream): B_tile = K^T V, A_tile = 1^T K
-//   2. tile_scan_kernel        exclusive scan of the tile records (VALU file)
+//   1. tile_sums_mfma_kernel     per (tile, stream): B_tile = K^T V, A_tile = 1^T K
+//   2. tile_scan_kernel          exclusive scan of the tile records (VALU file)
 //   3. causal_output_mfma_kernel per (tile, stream): walks the tile's
 //      sub-chunks from its exclusive prefix state.
 //
@@ -29,170 +29,112 @@
 //     k = 32 kk + 4 g + (e % 4) + 16 (e / 4),
 // which is exactly the set of rows an accumulator of two stacked 16-row blocks
 // gives a lane; so the carried state B0, held in accumulators, feeds the next
-// product without a trip through LDS.  Every LDS operand tile is stored in
-// "slots" of 4 consecutive elements of one row -- 16 bytes (4 bf16 hi, then
-// 4 bf16 lo) with hi/lo, 8 bytes without -- so one fragment is two slot reads.
-#include <type_traits>
-
-#include "race_internal.h"
+// product without a trip through LDS.
+//
+// LDS operand tiles are stored in that "fragment order": a row of K elements
+// holds the bf16 high parts of all its elements in fragment order, then (with
+// hi/lo) the low parts, so element k sits at position
+//     fpos(k) = 32 (k / 32) + 8 ((k / 4) % 4) + 4 ((k / 16) % 2) + k % 4
+// of each plane and one fragment is a single 16-byte read per plane (the
+// chunk swizzle of Plane keeps those reads and the staging stores spread over
+// the banks).
+#include "mfma_common.h"
 
 namespace race {
 namespace {
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using namespace mfma;
 
-__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 
-// acc += A B with optional hi/lo operands: lo*hi and hi*lo first, then hi*hi.
-template <bool kSplit>
-__device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
-                                       const bf16x8& bl, f32x4 acc) {
-    if constexpr (kSplit) {
-        acc = mfma16(al, bh, acc);
-        acc = mfma16(ah, bl, acc);
+// Plane tile geometry for rows of K elements.  A plane row is K / 8 chunks of
+// 16 bytes (8 elements).  Chunk u of row r is stored at chunk u ^ sw(r),
+//     sw(r) = ((r / 8) % 8 ^ (r / 4) % 2) & (K / 8 - 1),
+// and rows are 32 bytes longer than the planes.  With that layout the 16-byte
+// fragment reads (16 consecutive rows, one chunk) touch every bank once, and
+// the transposed staging stores (rows 4 apart, one 8-byte half chunk) are
+// spread over all banks instead of piling into two.
+template <bool kSplit, int K>
+struct Plane {
+    static constexpr int kLoOff = 2 * K;                       // bytes to the lo plane
+    static constexpr int kPitch = (kSplit ? 4 : 2) * K + 32;   // row pitch in bytes
+    static constexpr int kMask = (K / 8 < 8 ? K / 8 : 8) - 1;
+    __device__ __forceinline__ static int sw(int row) { return ((row >> 3) ^ ((row >> 2) & 1)) & kMask; }
+    // Store 4 consecutive elements k0..k0+3 (k0 % 4 == 0) of row `row`.
+    __device__ __forceinline__ static void put4(unsigned char* t, int row, int k0, const uint2& hi,
+                                                const uint2& lo) {
+        const int pos = fpos(k0);
+        unsigned char* p = t + row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 8 * ((pos >> 2) & 1);
+        *reinterpret_cast<uint2*>(p) = hi;
+        if constexpr (kSplit) *reinterpret_cast<uint2*>(p + kLoOff) = lo;
     }
-    return mfma16(ah, bh, acc);
-}
-
-__device__ __forceinline__ bf16x8 cat(const bf16x4& a, const bf16x4& b) {
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// Four consecutive elements of one row of an LDS operand tile.
-template <bool kSplit>
-struct alignas(kSplit ? 16 : 8) Slot {
-    bf16x4 hi;
-    bf16x4 lo;
-};
-template <>
-struct alignas(8) Slot<false> {
-    bf16x4 hi;
-};
-
-template <bool kSplit>
-__device__ __forceinline__ Slot<kSplit> make_slot(const f32x4& x) {
-    Slot<kSplit> s;
-    s.hi = __builtin_convertvector(x, bf16x4);  // round to nearest even
-    if constexpr (kSplit) s.lo = __builtin_convertvector(x - __builtin_convertvector(s.hi, f32x4), bf16x4);
-    return s;
-}
-
-// Fragment of row `row` of a slot tile for contraction step kk (permuted k).
-template <bool kSplit>
-__device__ __forceinline__ void read_frag(const unsigned char* tile, int pitch, int row, int kk,
-                                          int g, bf16x8& hi, bf16x8& lo) {
-    constexpr int kSlot = sizeof(Slot<kSplit>);
-    const unsigned char* p = tile + row * pitch + (8 * kk + g) * kSlot;
-    const Slot<kSplit> s0 = *reinterpret_cast<const Slot<kSplit>*>(p);
-    const Slot<kSplit> s1 = *reinterpret_cast<const Slot<kSplit>*>(p + 4 * kSlot);
-    hi = cat(s0.hi, s1.hi);
-    if constexpr (kSplit) lo = cat(s0.lo, s1.lo);
-}
-
-// ---------------------------------------------------------------------------
-// Global <-> register traffic.  Token rows of one stream are contiguous, so a
-// sub-chunk of C tokens is one contiguous block of C*W elements.
-
-template <typename TIn>
-struct Elem;
-template <>
-struct Elem<float> {
-    static constexpr int kPerVec = 4;  // elements per 16-byte vector
-    __device__ static float get(const uint4& v, int i) {
-        return __uint_as_float(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+    // Fragment of row `row` for contraction step kk.
+    __device__ __forceinline__ static void frag(const unsigned char* t, int row, int kk, int g,
+                                                bf16x8& hi, bf16x8& lo) {
+        const unsigned char* p = t + row * kPitch + 16 * ((4 * kk + g) ^ sw(row));
+        hi = *reinterpret_cast<const bf16x8*>(p);
+        if constexpr (kSplit) lo = *reinterpret_cast<const bf16x8*>(p + kLoOff);
     }
 };
-template <>
-struct Elem<bf16_t> {
-    static constexpr int kPerVec = 8;
-    __device__ static float get(const uint4& v, int i) {
-        const uint32_t w = (i >> 1) == 0 ? v.x : (i >> 1) == 1 ? v.y : (i >> 1) == 2 ? v.z : v.w;
-        return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
-    }
-};
-
-__device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
 // Geometry of one (S, D, C, dtype) specialization.
 template <typename TIn, int S, int D, int C>
 struct Geo {
     static constexpr bool kSplit = std::is_same<TIn, float>::value;
-    static constexpr int kSlot = sizeof(Slot<kSplit>);
     static constexpr int E = Elem<TIn>::kPerVec;
-    // Row pitches in bytes: the slots of a row plus one 16-byte pad.
-    static constexpr int kPitchS = (S / 4) * kSlot + 16;
-    static constexpr int kPitchC = (C / 4) * kSlot + 16;
-    static constexpr int kQBytes = C * kPitchS;  // Q, then W in place
-    static constexpr int kKBytes = C * (kPitchS > kPitchC ? kPitchS : kPitchC);  // K, then P
-    static constexpr int kKTBytes = S * kPitchC;
-    static constexpr int kVTBytes = D * kPitchC;
-    static constexpr int kOutputLds = kQBytes + kKBytes + kKTBytes + kVTBytes;
+    using PS = Plane<kSplit, S>;  // rows over buckets: W, K
+    using PC = Plane<kSplit, C>;  // rows over tokens: K^T, V^T, P
+    static constexpr int kWBytes = C * PS::kPitch;
+    static constexpr int kKBytes = C * (PS::kPitch > PC::kPitch ? PS::kPitch : PC::kPitch);
+    static constexpr int kKTBytes = S * PC::kPitch;
+    static constexpr int kVTBytes = D * PC::kPitch;
+    static constexpr int kOutputLds = kWBytes + kKBytes + kKTBytes + kVTBytes;
     static constexpr int kSumsLds = kKTBytes + kVTBytes + 16 * S * 4;
-    // Register staging of one sub-chunk.
-    static constexpr int kQVec = C * S / E;          // 16-byte vectors of Q
-    static constexpr int kQPer = (kQVec + kThreads - 1) / kThreads;
-    static constexpr int kKBlk = (C / 4) * (S / E);  // 4-row x E-column blocks of K
+    // Register staging of K and V: blocks of 4 rows x E columns.
+    static constexpr int kKBlk = (C / 4) * (S / E);
     static constexpr int kKPer = (kKBlk + kThreads - 1) / kThreads;
     static constexpr int kVBlk = (C / 4) * (D / E);
     static constexpr int kVPer = (kVBlk + kThreads - 1) / kThreads;
-    static_assert(S % 64 == 0 && D % 64 == 0 && C % 32 == 0 && C <= 64, "unsupported tile");
+    static_assert(S % 64 == 0 && D % 64 == 0 && (C == 32 || C == 64), "unsupported tile");
     static_assert(S >= C, "P overlays the K tile");
 };
 
-// Raw registers of one sub-chunk (rows >= cnt read as zero).
+// Raw K and V registers of one sub-chunk.
 template <typename TIn, int S, int D, int C>
-struct Stage {
+struct KVStage {
     using G = Geo<TIn, S, D, C>;
-    uint4 q[G::kQPer];
     uint4 k[G::kKPer][4];
     uint4 v[G::kVPer][4];
 
-    __device__ __forceinline__ void load(const TIn* qn, const TIn* kn, const TIn* vn, int64_t t0,
-                                         int cnt, bool want_q) {
+    // Rows r0 .. r0 + C - 1 of the tile buffers (row r0 is the sub-chunk's
+    // first token relative to the tile; rows past the tile read as zero).
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int r0) {
         const int tid = threadIdx.x;
-        const uint4 zero = make_uint4(0, 0, 0, 0);
-        if (want_q) {
-#pragma unroll
-            for (int p = 0; p < G::kQPer; ++p) {
-                const int idx = tid + p * kThreads;
-                const int row = idx / (S / G::E);
-                q[p] = (idx < G::kQVec && row < cnt) ? load16(qn + t0 * S + int64_t(idx) * G::E) : zero;
-            }
-        }
 #pragma unroll
         for (int p = 0; p < G::kKPer; ++p) {
             const int blk = tid + p * kThreads;
             const int a = blk / (S / G::E), b = blk % (S / G::E);
+            if (G::kKBlk % kThreads == 0 || blk < G::kKBlk) {
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = 4 * a + rr;
-                k[p][rr] = (blk < G::kKBlk && row < cnt)
-                               ? load16(kn + (t0 + row) * S + b * G::E)
-                               : zero;
+                for (int rr = 0; rr < 4; ++rr)
+                    k[p][rr] = buf_load16(kr, ((r0 + 4 * a + rr) * S + b * G::E) * int(sizeof(TIn)));
             }
         }
 #pragma unroll
         for (int p = 0; p < G::kVPer; ++p) {
             const int blk = tid + p * kThreads;
             const int a = blk / (D / G::E), b = blk % (D / G::E);
+            if (G::kVBlk % kThreads == 0 || blk < G::kVBlk) {
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = 4 * a + rr;
-                v[p][rr] = (blk < G::kVBlk && row < cnt)
-                               ? load16(vn + (t0 + row) * D + b * G::E)
-                               : zero;
+                for (int rr = 0; rr < 4; ++rr)
+                    v[p][rr] = buf_load16(vr, ((r0 + 4 * a + rr) * D + b * G::E) * int(sizeof(TIn)));
             }
         }
     }
 
-    // K^T [S][C] and V^T [D][C] slot tiles; K [C][S] too when Ks is given;
-    // column sums of K into asum when given.
-    __device__ __forceinline__ void store_kv(unsigned char* Ks, unsigned char* KTs,
-                                             unsigned char* VTs, float* asum) const {
+    // K^T [S][C] and V^T [D][C] plane tiles, K [C][S] too when Ks is given,
+    // column sums of K into asum when given.  Each element is split once.
+    __device__ __forceinline__ void store(unsigned char* Ks, unsigned char* KTs, unsigned char* VTs,
+                                          float* asum) const {
         constexpr bool kSplit = G::kSplit;
         constexpr int E = G::E;
         const int tid = threadIdx.x;
@@ -201,27 +143,37 @@ struct Stage {
             const int blk = tid + p * kThreads;
             if (blk >= G::kKBlk) continue;
             const int a = blk / (S / E), b = blk % (S / E);
-            float x[4][E];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-                for (int c = 0; c < E; ++c) x[rr][c] = Elem<TIn>::get(k[p][rr], c);
-            if (Ks) {
+            for (int h = 0; h < E / 4; ++h) {
+                float x[4][4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-                    for (int h = 0; h < E / 4; ++h) {
-                        const f32x4 f = {x[rr][4 * h], x[rr][4 * h + 1], x[rr][4 * h + 2], x[rr][4 * h + 3]};
-                        *reinterpret_cast<Slot<kSplit>*>(Ks + (4 * a + rr) * G::kPitchS +
-                                                         (b * E / 4 + h) * G::kSlot) = make_slot<kSplit>(f);
-                    }
-            }
+                    for (int c = 0; c < 4; ++c) x[rr][c] = Elem<TIn>::get(k[p][rr], 4 * h + c);
+                const int s0 = b * E + 4 * h;
+                // Column slots (4 tokens of one bucket) for K^T.
+                uint2 chi[4], clo[4];
 #pragma unroll
-            for (int c = 0; c < E; ++c) {
-                const f32x4 f = {x[0][c], x[1][c], x[2][c], x[3][c]};
-                *reinterpret_cast<Slot<kSplit>*>(KTs + (b * E + c) * G::kPitchC + a * G::kSlot) =
-                    make_slot<kSplit>(f);
-                if (asum) asum[p * E + c] += ((x[0][c] + x[1][c]) + x[2][c]) + x[3][c];
+                for (int c = 0; c < 4; ++c) {
+                    split4<kSplit>(x[0][c], x[1][c], x[2][c], x[3][c], chi[c], clo[c]);
+                    G::PC::put4(KTs, s0 + c, 4 * a, chi[c], clo[c]);
+                    if (asum) asum[p * E + 4 * h + c] += ((x[0][c] + x[1][c]) + x[2][c]) + x[3][c];
+                }
+                if (Ks) {
+                    // Row slots (4 buckets of one token) for K, from the same split:
+                    // element (rr, c) is half rr % 2 of word rr / 2 of chi[c].
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        uint2 rhi, rlo;
+                        rhi.x = half16(word(chi[0], rr >> 1), rr & 1) | (half16(word(chi[1], rr >> 1), rr & 1) << 16);
+                        rhi.y = half16(word(chi[2], rr >> 1), rr & 1) | (half16(word(chi[3], rr >> 1), rr & 1) << 16);
+                        if constexpr (kSplit) {
+                            rlo.x = half16(word(clo[0], rr >> 1), rr & 1) | (half16(word(clo[1], rr >> 1), rr & 1) << 16);
+                            rlo.y = half16(word(clo[2], rr >> 1), rr & 1) | (half16(word(clo[3], rr >> 1), rr & 1) << 16);
+                        }
+                        G::PS::put4(Ks, 4 * a + rr, s0, rhi, rlo);
+                    }
+                }
             }
         }
 #pragma unroll
@@ -231,44 +183,14 @@ struct Stage {
             const int a = blk / (D / E), b = blk % (D / E);
 #pragma unroll
             for (int c = 0; c < E; ++c) {
-                const f32x4 f = {Elem<TIn>::get(v[p][0], c), Elem<TIn>::get(v[p][1], c),
-                                 Elem<TIn>::get(v[p][2], c), Elem<TIn>::get(v[p][3], c)};
-                *reinterpret_cast<Slot<kSplit>*>(VTs + (b * E + c) * G::kPitchC + a * G::kSlot) =
-                    make_slot<kSplit>(f);
+                uint2 hi, lo;
+                split4<kSplit>(Elem<TIn>::get(v[p][0], c), Elem<TIn>::get(v[p][1], c),
+                               Elem<TIn>::get(v[p][2], c), Elem<TIn>::get(v[p][3], c), hi, lo);
+                G::PC::put4(VTs, b * E + c, 4 * a, hi, lo);
             }
         }
     }
-
-    // Raw Q into the Q tile: fp32 values (16-byte slots) or bf16 (8-byte slots).
-    __device__ __forceinline__ void store_q(unsigned char* Qs) const {
-        const int tid = threadIdx.x;
-#pragma unroll
-        for (int p = 0; p < G::kQPer; ++p) {
-            const int idx = tid + p * kThreads;
-            if (idx >= G::kQVec) continue;
-            const int row = idx / (S / G::E), col = (idx % (S / G::E)) * G::E;
-            *reinterpret_cast<uint4*>(Qs + row * G::kPitchS + (col / 4) * G::kSlot) = q[p];
-        }
-    }
 };
-
-// Four consecutive Q values of row i (fp32 or bf16 slot) as floats.
-template <bool kSplit>
-__device__ __forceinline__ f32x4 read_q4(const unsigned char* p) {
-    if constexpr (kSplit) {
-        return *reinterpret_cast<const f32x4*>(p);
-    } else {
-        const uint2 u = *reinterpret_cast<const uint2*>(p);
-        return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
-    }
-}
-
-__device__ __forceinline__ void store4(float* p, const f32x4& x) { *reinterpret_cast<f32x4*>(p) = x; }
-__device__ __forceinline__ void store4(bf16_t* p, const f32x4& x) {
-    const bf16x4 b = __builtin_convertvector(x, bf16x4);
-    *reinterpret_cast<bf16x4*>(p) = b;
-}
 
 // ---------------------------------------------------------------------------
 // K1: per (tile, stream) totals B_tile = K^T V and A_tile = colsum(K) into the
@@ -279,6 +201,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
     const TIn* __restrict__ k, const TIn* __restrict__ v, float* __restrict__ records, int64_t T,
     int tile, int64_t tiles, int64_t rec) {
     using G = Geo<TIn, S, D, C>;
+    using PC = typename G::PC;
     constexpr bool kSplit = G::kSplit;
     constexpr int NSB = S / 16, NKC = C / 32, CBW = D / 64;
     extern __shared__ __align__(16) unsigned char lds[];
@@ -290,8 +213,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
     const int64_t n = blockIdx.y, ti = blockIdx.x;
     const int64_t t_begin = ti * tile;
     const int64_t t_end = min(T, t_begin + tile);
-    const TIn* kn = k + n * T * S;
-    const TIn* vn = v + n * T * D;
+    const int rows = int(t_end - t_begin);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + (n * T + t_begin) * S, int64_t(rows) * S * sizeof(TIn));
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + (n * T + t_begin) * D, int64_t(rows) * D * sizeof(TIn));
 
     f32x4 acc[NSB][CBW];
 #pragma unroll
@@ -302,26 +226,24 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < G::kKPer * G::E; ++i) asum[i] = 0.f;
 
-    Stage<TIn, S, D, C> st;
-    st.load(nullptr, kn, vn, t_begin, int(min<int64_t>(C, t_end - t_begin)), false);
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += C) {
+    KVStage<TIn, S, D, C> st;
+    st.load(kr, vr, 0);
+    for (int r0 = 0; r0 < rows; r0 += C) {
         __syncthreads();
-        st.store_kv(nullptr, KTs, VTs, asum);
-        const int64_t t1 = t0 + C;
-        if (t1 < t_end) st.load(nullptr, kn, vn, t1, int(min<int64_t>(C, t_end - t1)), false);
+        st.store(nullptr, KTs, VTs, asum);
+        if (r0 + C < rows) st.load(kr, vr, r0 + C);
         __syncthreads();
         bf16x8 vh[CBW][NKC], vl[CBW][NKC];
 #pragma unroll
         for (int cbw = 0; cbw < CBW; ++cbw)
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk)
-                read_frag<kSplit>(VTs, G::kPitchC, 16 * (w + 4 * cbw) + lr, kk, g, vh[cbw][kk], vl[cbw][kk]);
+            for (int kk = 0; kk < NKC; ++kk) PC::frag(VTs, 16 * (w + 4 * cbw) + lr, kk, g, vh[cbw][kk], vl[cbw][kk]);
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
             for (int kk = 0; kk < NKC; ++kk) {
                 bf16x8 kh, kl;
-                read_frag<kSplit>(KTs, G::kPitchC, 16 * sb + lr, kk, g, kh, kl);
+                PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
 #pragma unroll
                 for (int cbw = 0; cbw < CBW; ++cbw)
                     acc[sb][cbw] = mfma3<kSplit>(kh, kl, vh[cbw][kk], vl[cbw][kk], acc[sb][cbw]);
@@ -363,9 +285,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 //
 // Per sub-chunk:
 //   1. Abar^T [S][C] = A0 + K^T tril(1)       wave w: s-blocks w, w+4, ..
-//   2. W [C][S] = Q / (Abar + eps), in place over Q
-//   3. P^T blocks (j-block <= i-block) = K W^T, masked j > i; written as
-//      P [C][C] over the dead K tile (upper blocks as zeros)
+//   2. W [C][S] = Q / (Abar + eps)             Q read from global memory in
+//      the accumulator layout, W written as a plane tile
+//   3. P^T blocks (j-block <= i-block) = K W^T, masked j > i, written as the
+//      plane tile P [C][C] over the dead K tile
 //   4. O^T [D][C] = B0^T W^T + V^T P^T         wave w: c-blocks w, w+4, ..
 //   5. B0 += K^T V                             same c-blocks, all s-blocks
 template <typename TIn, int S, int D, int C, int kMinBlocks>
@@ -374,14 +297,16 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     TIn* __restrict__ out, const float* __restrict__ records, int64_t T, int tile, int64_t tiles,
     int64_t rec) {
     using G = Geo<TIn, S, D, C>;
+    using PS = typename G::PS;
+    using PC = typename G::PC;
     constexpr bool kSplit = G::kSplit;
     constexpr int NSB = S / 16, NBI = C / 16, NKS = S / 32, NKC = C / 32;
     constexpr int SBW = S / 64, CBW = D / 64;
-    constexpr int NPB = NBI * NBI;                  // P blocks, lower triangle first
-    constexpr int PBW = (NPB + 3) / 4;              // P blocks per wave
+    constexpr int NLB = NBI * (NBI + 1) / 2;       // lower-triangular P blocks
+    constexpr int PBW = (NLB + 3) / 4;             // P blocks per wave
     extern __shared__ __align__(16) unsigned char lds[];
-    unsigned char* Qs = lds;
-    unsigned char* Ks = Qs + G::kQBytes;
+    unsigned char* Ws = lds;
+    unsigned char* Ks = Ws + G::kWBytes;
     unsigned char* Ps = Ks;
     unsigned char* KTs = Ks + G::kKBytes;
     unsigned char* VTs = KTs + G::kKTBytes;
@@ -390,10 +315,11 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     const int64_t n = blockIdx.y, ti = blockIdx.x;
     const int64_t t_begin = ti * tile;
     const int64_t t_end = min(T, t_begin + tile);
-    const TIn* qn = q + n * T * S;
-    const TIn* kn = k + n * T * S;
-    const TIn* vn = v + n * T * D;
-    TIn* on = out + n * T * D;
+    const int rows = int(t_end - t_begin);
+    const __amdgpu_buffer_rsrc_t qr_ = make_rsrc(q + (n * T + t_begin) * S, int64_t(rows) * S * sizeof(TIn));
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + (n * T + t_begin) * S, int64_t(rows) * S * sizeof(TIn));
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + (n * T + t_begin) * D, int64_t(rows) * D * sizeof(TIn));
+    const __amdgpu_buffer_rsrc_t or_ = make_rsrc(out + (n * T + t_begin) * D, int64_t(rows) * D * sizeof(TIn));
 
     // Carried state from the tile's exclusive prefix record.
     const float* rec_p = records + (n * tiles + ti) * rec;
@@ -411,27 +337,39 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) a0[sbw][rr] = rec_p[S * D + 16 * (w + 4 * sbw) + 4 * g + rr];
 
-    // Lower-triangular ones as a B operand: L^T[j][i] = (j <= i) for j in the
-    // permuted k set of step kk and i = 16 bi + lr.
-    auto tril_frag = [&](int kk, int bi) {
-        bf16x8 f;
+    // The two partial triangles of the running-mass operand (i - j offset 0 or 16).
+    const bf16x8 tri0 = tril_frag(0, g, lr), tri1 = tril_frag(16, g, lr);
+    bf16x8 ones;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int j = 32 * kk + 4 * g + (e & 3) + 16 * (e >> 2);
-            f[e] = (j <= 16 * bi + lr) ? __bf16(1.0f) : __bf16(0.0f);
-        }
-        return f;
+    for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
+
+    // Q of a sub-chunk in the layout of step 2: lane (g, lr) holds
+    // Q[16 bi + lr][16 (w + 4 sbw) + 4 g .. + 3].
+    f32x4 qr[SBW][NBI];
+    auto load_q = [&](int r0) {
+#pragma unroll
+        for (int sbw = 0; sbw < SBW; ++sbw)
+#pragma unroll
+            for (int bi = 0; bi < NBI; ++bi)
+                qr[sbw][bi] = load_q4<TIn>(
+                    qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + 4 * sbw) + 4 * g) * int(sizeof(TIn)));
     };
 
-    Stage<TIn, S, D, C> st;
-    st.load(qn, kn, vn, t_begin, int(min<int64_t>(C, t_end - t_begin)), true);
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += C) {
-        const int cnt = int(min<int64_t>(C, t_end - t0));
+    KVStage<TIn, S, D, C> st;
+    st.load(kr, vr, 0);
+    load_q(0);
+    for (int r0 = 0; r0 < rows; r0 += C) {
         __syncthreads();
-        st.store_q(Qs);
-        st.store_kv(Ks, KTs, VTs, nullptr);
-        const int64_t t1 = t0 + C;
-        if (t1 < t_end) st.load(qn, kn, vn, t1, int(min<int64_t>(C, t_end - t1)), true);
+        st.store(Ks, KTs, VTs, nullptr);
+        f32x4 qc[SBW][NBI];
+#pragma unroll
+        for (int sbw = 0; sbw < SBW; ++sbw)
+#pragma unroll
+            for (int bi = 0; bi < NBI; ++bi) qc[sbw][bi] = qr[sbw][bi];
+        if (r0 + C < rows) {
+            st.load(kr, vr, r0 + C);
+            load_q(r0 + C);
+        }
         __syncthreads();
 
         // 1 + 2: running mass and W.
@@ -440,55 +378,54 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
             const int sb = w + 4 * sbw;
             bf16x8 kh[NKC], kl[NKC];
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) read_frag<kSplit>(KTs, G::kPitchC, 16 * sb + lr, kk, g, kh[kk], kl[kk]);
+            for (int kk = 0; kk < NKC; ++kk) PC::frag(KTs, 16 * sb + lr, kk, g, kh[kk], kl[kk]);
             f32x4 last;
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) {
                 f32x4 acc = {a0[sbw][0], a0[sbw][1], a0[sbw][2], a0[sbw][3]};
 #pragma unroll
                 for (int kk = 0; kk < NKC; ++kk) {
-                    if (32 * kk > 16 * bi + 15) continue;
-                    const bf16x8 lf = tril_frag(kk, bi);
+                    const int off = 16 * bi - 32 * kk;
+                    if (off < 0) continue;
+                    const bf16x8& lf = off == 0 ? tri0 : off == 16 ? tri1 : ones;
                     if constexpr (kSplit) acc = mfma16(kl[kk], lf, acc);
                     acc = mfma16(kh[kk], lf, acc);
                 }
-                unsigned char* qp = Qs + (16 * bi + lr) * G::kPitchS + (4 * sb + g) * G::kSlot;
-                const f32x4 qv = read_q4<kSplit>(qp);
-                f32x4 wv;
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) wv[rr] = qv[rr] * __builtin_amdgcn_rcpf(acc[rr] + kEps);
-                *reinterpret_cast<Slot<kSplit>*>(qp) = make_slot<kSplit>(wv);
+                const f32x4 qv = qc[sbw][bi];
+                uint2 hi, lo;
+                split4<kSplit>(qv[0] * __builtin_amdgcn_rcpf(acc[0] + kEps),
+                               qv[1] * __builtin_amdgcn_rcpf(acc[1] + kEps),
+                               qv[2] * __builtin_amdgcn_rcpf(acc[2] + kEps),
+                               qv[3] * __builtin_amdgcn_rcpf(acc[3] + kEps), hi, lo);
+                PS::put4(Ws, 16 * bi + lr, 16 * sb + 4 * g, hi, lo);
                 last = acc;
             }
-            // Inclusive mass at the chunk's last row (zero rows past cnt add nothing).
+            // Inclusive mass at the chunk's last row (zero rows past the tile add nothing).
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) a0[sbw][rr] = __shfl(last[rr], 16 * g + 15);
         }
         __syncthreads();
 
-        // 3: P^T blocks.
+        // 3: P^T blocks of the lower triangle, round robin over the waves.
         f32x4 pacc[PBW];
+        int pbi[PBW], pbj[PBW];
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
             const int idx = w + 4 * pb;
+            int bi = 0, rem = idx;
+            while (rem > bi) { rem -= bi + 1; ++bi; }
+            pbi[pb] = bi;
+            pbj[pb] = rem;
             pacc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (idx >= NPB) continue;
-            int bi = 0, bj = 0;
-            if (idx < NBI * (NBI + 1) / 2) {
-                int rem = idx;
-                while (rem > bi) { rem -= bi + 1; ++bi; }
-                bj = rem;
-            } else {
-                continue;  // upper blocks stay zero
-            }
+            if (idx >= NLB) continue;
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
                 bf16x8 ah, al, bh, bl;
-                read_frag<kSplit>(Ks, G::kPitchS, 16 * bj + lr, kk, g, ah, al);
-                read_frag<kSplit>(Qs, G::kPitchS, 16 * bi + lr, kk, g, bh, bl);
+                PS::frag(Ks, 16 * rem + lr, kk, g, ah, al);
+                PS::frag(Ws, 16 * bi + lr, kk, g, bh, bl);
                 pacc[pb] = mfma3<kSplit>(ah, al, bh, bl, pacc[pb]);
             }
-            if (bj == bi) {
+            if (rem == bi) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
                     if (4 * g + rr > lr) pacc[pb][rr] = 0.f;
@@ -497,21 +434,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         __syncthreads();
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
-            const int idx = w + 4 * pb;
-            if (idx >= NPB) continue;
-            int bi = 0, bj = 0;
-            if (idx < NBI * (NBI + 1) / 2) {
-                int rem = idx;
-                while (rem > bi) { rem -= bi + 1; ++bi; }
-                bj = rem;
-            } else {
-                int rem = idx - NBI * (NBI + 1) / 2;  // upper blocks (bj > bi), row by row
-                bi = 0;
-                while (rem >= NBI - 1 - bi) { rem -= NBI - 1 - bi; ++bi; }
-                bj = bi + 1 + rem;
-            }
-            *reinterpret_cast<Slot<kSplit>*>(Ps + (16 * bi + lr) * G::kPitchC + (4 * bj + g) * G::kSlot) =
-                make_slot<kSplit>(pacc[pb]);
+            if (w + 4 * pb >= NLB) continue;
+            uint2 hi, lo;
+            split4<kSplit>(pacc[pb][0], pacc[pb][1], pacc[pb][2], pacc[pb][3], hi, lo);
+            PC::put4(Ps, 16 * pbi[pb] + lr, 16 * pbj[pb] + 4 * g, hi, lo);
         }
         __syncthreads();
 
@@ -521,20 +447,23 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
             const int cb = w + 4 * cbw;
             bf16x8 vh[NKC], vl[NKC];
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) read_frag<kSplit>(VTs, G::kPitchC, 16 * cb + lr, kk, g, vh[kk], vl[kk]);
+            for (int kk = 0; kk < NKC; ++kk) PC::frag(VTs, 16 * cb + lr, kk, g, vh[kk], vl[kk]);
             f32x4 o[NBI];
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) o[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
                 const f32x4 x0 = b0[2 * kk][cbw], x1 = b0[2 * kk + 1][cbw];
-                const Slot<kSplit> s0 = make_slot<kSplit>(x0), s1 = make_slot<kSplit>(x1);
-                bf16x8 bh = cat(s0.hi, s1.hi), bl;
-                if constexpr (kSplit) bl = cat(s0.lo, s1.lo);
+                uint2 h0, l0, h1, l1;
+                split4<kSplit>(x0[0], x0[1], x0[2], x0[3], h0, l0);
+                split4<kSplit>(x1[0], x1[1], x1[2], x1[3], h1, l1);
+                const bf16x8 bh = __builtin_bit_cast(bf16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                bf16x8 bl;
+                if constexpr (kSplit) bl = __builtin_bit_cast(bf16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
 #pragma unroll
                 for (int bi = 0; bi < NBI; ++bi) {
                     bf16x8 wh, wl;
-                    read_frag<kSplit>(Qs, G::kPitchS, 16 * bi + lr, kk, g, wh, wl);
+                    PS::frag(Ws, 16 * bi + lr, kk, g, wh, wl);
                     o[bi] = mfma3<kSplit>(bh, bl, wh, wl, o[bi]);
                 }
             }
@@ -542,20 +471,28 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
             for (int bi = 0; bi < NBI; ++bi) {
 #pragma unroll
                 for (int kk = 0; kk < NKC; ++kk) {
-                    if (32 * kk > 16 * bi + 15) continue;
+                    if (32 * kk > 16 * bi) continue;
                     bf16x8 ph, pl;
-                    read_frag<kSplit>(Ps, G::kPitchC, 16 * bi + lr, kk, g, ph, pl);
+                    PC::frag(Ps, 16 * bi + lr, kk, g, ph, pl);
+                    if (32 * kk == 16 * bi) {
+                        // The upper half of this step is the block above the
+                        // diagonal: zero, and never written to the P tile.
+#pragma unroll
+                        for (int e = 4; e < 8; ++e) {
+                            ph[e] = __bf16(0.0f);
+                            if constexpr (kSplit) pl[e] = __bf16(0.0f);
+                        }
+                    }
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
-                const int i = 16 * bi + lr;
-                if (i < cnt) store4(on + (t0 + i) * D + 16 * cb + 4 * g, o[bi]);
+                store4<TIn>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * int(sizeof(TIn)), o[bi]);
             }
 #pragma unroll
             for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
                 for (int kk = 0; kk < NKC; ++kk) {
                     bf16x8 kh, kl;
-                    read_frag<kSplit>(KTs, G::kPitchC, 16 * sb + lr, kk, g, kh, kl);
+                    PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
                     b0[sb][cbw] = mfma3<kSplit>(kh, kl, vh[kk], vl[kk], b0[sb][cbw]);
                 }
         }
@@ -566,11 +503,20 @@ template <typename TIn, int S, int D, int C, int kMinBlocks>
 hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void* out, float* records,
                               float* state, const Problem& p, hipStream_t stream, Marks* marks) {
     using G = Geo<TIn, S, D, C>;
+    // Tiles are whole sub-chunks, and a tile's bytes fit a 32-bit buffer range.
     if (p.tile % C != 0) return hipErrorInvalidValue;
+    if (int64_t(p.tile) * (S > D ? S : D) * int64_t(sizeof(TIn)) >= (int64_t(1) << 31))
+        return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
-    tile_sums_mfma_kernel<TIn, S, D, C, kMinBlocks><<<grid, kThreads, G::kSumsLds, stream>>>(
-        static_cast<const TIn*>(k), static_cast<const TIn*>(v), records, p.T, p.tile, p.tiles, p.rec);
-    hipError_t err = hipGetLastError();
+    hipError_t err;
+    if (direct_sums_supported(S, D)) {
+        err = launch_tile_sums_direct(k, v, records, p, stream);
+    } else {
+        tile_sums_mfma_kernel<TIn, S, D, C, kMinBlocks><<<grid, kThreads, G::kSumsLds, stream>>>(
+            static_cast<const TIn*>(k), static_cast<const TIn*>(v), records, p.T, p.tile, p.tiles,
+            p.rec);
+        err = hipGetLastError();
+    }
     if (err != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
     if ((err = launch_tile_scan(records, state, p, stream)) != hipSuccess) return err;
@@ -604,6 +550,12 @@ hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out,
 
 }  // namespace
 
+int mfma_tiles_per_cu(int S, int d, int dtype, int kernel) {
+    if (kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(S, d, dtype))
+        return direct_output_tiles_per_cu();
+    return 4;  // two resident workgroups per CU, two rounds
+}
+
 bool mfma_causal_supported(int S, int d) {
     return (S == 64 || S == 128 || S == 256) && (d == 64 || d == 128);
 }
@@ -612,6 +564,17 @@ hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void*
                               float* records, float* state, const Problem& p, hipStream_t stream,
                               Marks* marks) {
     if (!mfma_causal_supported(p.S, p.d)) return hipErrorInvalidValue;
+    if (p.kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(p.S, p.d, p.dtype) &&
+        p.tile % 64 == 0) {
+        hipError_t err = launch_tile_sums_direct(k, v, records, p, stream);
+        if (err != hipSuccess) return err;
+        if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
+        if ((err = launch_tile_scan(records, state, p, stream)) != hipSuccess) return err;
+        if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
+        if ((err = launch_causal_output_direct(q, k, v, out, records, p, stream)) != hipSuccess)
+            return err;
+        return marks ? marks->mark(stream) : hipSuccess;
+    }
     if (p.dtype == RACE_BF16)
         return dispatch_mfma<bf16_t>(q, k, v, out, records, state, p, stream, marks);
     return dispatch_mfma<float>(q, k, v, out, records, state, p, stream, marks);

@@ -1,0 +1,140 @@
+// mfma_common.h -- device helpers shared by the MFMA kernels of the RACE
+// attention library (gfx950): bf16 hi/lo splitting, the permuted-k fragment
+// order, buffer-resource loads and stores.  Not part of the ABI.
+//
+// Conventions.  A lane l of a wave64 has group g = l / 16 and row lr = l % 16.
+// v_mfma_f32_16x16x32_bf16 takes from each lane 8 bf16 of the A operand (row
+// m = lr, 8 values of the contraction index k), 8 bf16 of the B operand
+// (column n = lr, the same 8 k values) and returns the 4 accumulator values
+// D[4 g + r][lr], r = 0..3.  The kernels permute the contraction index of one
+// 32-wide step kk: lane group g, element e carries
+//     k = 32 kk + 4 g + (e % 4) + 16 (e / 4),
+// which is the set of rows two stacked accumulator blocks give a lane, so an
+// fp32 accumulator (the carried state) feeds the next product directly.  LDS
+// operand rows store elements in that order: element k of a row sits at
+//     fpos(k) = 32 (k / 32) + 8 ((k / 4) % 4) + 4 ((k / 16) % 2) + k % 4
+// of its bf16 plane, and one fragment is one 16-byte read per plane.
+#pragma once
+
+#include <type_traits>
+
+#include "race_internal.h"
+
+namespace race {
+namespace mfma {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// acc += A B with optional hi/lo operands: lo*hi and hi*lo first, then hi*hi.
+template <bool kSplit>
+__device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                       const bf16x8& bl, f32x4 acc) {
+    if constexpr (kSplit) {
+        acc = mfma16(al, bh, acc);
+        acc = mfma16(ah, bl, acc);
+    }
+    return mfma16(ah, bh, acc);
+}
+
+__device__ __forceinline__ constexpr int fpos(int k) {
+    return (k & ~31) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
+}
+
+// Two floats to a packed pair of bf16 (round to nearest even).
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
+    return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ float lo_half(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ uint32_t word(const uint2& u, int i) { return i ? u.y : u.x; }
+__device__ __forceinline__ uint32_t half16(uint32_t w, int h) { return h ? (w >> 16) : (w & 0xffffu); }
+__device__ __forceinline__ float hi_half(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// Four consecutive elements split into packed hi (and lo) pairs.
+template <bool kSplit>
+__device__ __forceinline__ void split4(float x0, float x1, float x2, float x3, uint2& hi, uint2& lo) {
+    hi.x = pack2(x0, x1);
+    hi.y = pack2(x2, x3);
+    if constexpr (kSplit) {
+        lo.x = pack2(x0 - lo_half(hi.x), x1 - hi_half(hi.x));
+        lo.y = pack2(x2 - lo_half(hi.y), x3 - hi_half(hi.y));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Global -> register traffic.  Token rows of one stream are contiguous.
+
+template <typename TIn>
+struct Elem;
+template <>
+struct Elem<float> {
+    static constexpr int kPerVec = 4;  // elements per 16-byte vector
+    __device__ static float get(const uint4& v, int i) {
+        return __uint_as_float(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+    }
+};
+template <>
+struct Elem<bf16_t> {
+    static constexpr int kPerVec = 8;
+    __device__ static float get(const uint4& v, int i) {
+        const uint32_t w = (i >> 1) == 0 ? v.x : (i >> 1) == 1 ? v.y : (i >> 1) == 2 ? v.z : v.w;
+        return (i & 1) ? hi_half(w) : lo_half(w);
+    }
+};
+
+// Buffer resource over `bytes` bytes from `base`: loads past the end return
+// zero and stores past the end are dropped, which is how a ragged last
+// sub-chunk reads zero rows and writes nothing past the sequence.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(bytes),
+                                             0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+// Four consecutive Q values at byte offset `off` of a buffer, as floats.
+template <typename TIn>
+__device__ __forceinline__ f32x4 load_q4(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (std::is_same<TIn, float>::value) {
+        return __builtin_bit_cast(f32x4, buf_load16(r, off));
+    } else {
+        const uint2 u = buf_load8(r, off);
+        return f32x4{lo_half(u.x), hi_half(u.x), lo_half(u.y), hi_half(u.y)};
+    }
+}
+
+// Four consecutive output values at byte offset `off` of a buffer.
+template <typename TIn>
+__device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t r, int off, const f32x4& x) {
+    if constexpr (std::is_same<TIn, float>::value) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, off, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2(x[0], x[1]), pack2(x[2], x[3])}, r, off, 0, 0);
+    }
+}
+
+// Lower-triangular ones as a B operand for the running mass: element e of
+// lane (g, lr) is (j' <= i') with j' = 4 g + e % 4 + 16 (e / 4) and
+// i' = off + lr (off = 0 or 16).
+__device__ __forceinline__ bf16x8 tril_frag(int off, int g, int lr) {
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (4 * g + (e & 3) + 16 * (e >> 2) <= off + lr) ? __bf16(1.0f) : __bf16(0.0f);
+    return f;
+}
+
+}  // namespace mfma
+}  // namespace race

@@ -42,11 +42,13 @@ int kernel_choice(const race_options* o) { return o ? o->kernel : RACE_KERNEL_AU
 // Resolves which kernel family runs; INVALID_VALUE if the request cannot be met.
 race_status resolve_kernel(const race_shape* sh, int causal, const race_options* o, bool* mfma) {
     const int k = kernel_choice(o);
-    if (k != RACE_KERNEL_AUTO && k != RACE_KERNEL_VALU && k != RACE_KERNEL_MFMA)
+    if (k != RACE_KERNEL_AUTO && k != RACE_KERNEL_VALU && k != RACE_KERNEL_MFMA &&
+        k != RACE_KERNEL_MFMA_WG)
         return RACE_ERROR_INVALID_VALUE;
     const bool has = causal && mfma_causal_supported(sub(sh), sh->head_dim);
-    if (k == RACE_KERNEL_MFMA && !has) return RACE_ERROR_INVALID_VALUE;
-    *mfma = (k == RACE_KERNEL_MFMA) || (k == RACE_KERNEL_AUTO && has);
+    const bool forced = k == RACE_KERNEL_MFMA || k == RACE_KERNEL_MFMA_WG;
+    if (forced && !has) return RACE_ERROR_INVALID_VALUE;
+    *mfma = forced || (k == RACE_KERNEL_AUTO && has);
     return RACE_SUCCESS;
 }
 
@@ -78,7 +80,8 @@ race_status resolve_tile(const race_shape* sh, int causal, const race_options* o
     // Aim for a few resident workgroups per compute unit so the output pass
     // streams HBM from every CU; longer tiles amortize the tile record
     // (4*(S*d+S) bytes read and written per tile) over more tokens.
-    const int64_t per_cu = (causal && mfma) ? 4 : 2;
+    const int64_t per_cu =
+        (causal && mfma) ? mfma_tiles_per_cu(sub(sh), sh->head_dim, sh->dtype, kernel_choice(o)) : 2;
     int t = pow2_floor(work / (per_cu * cus));
     if (t < RACE_SUB_CHUNK_TOKENS) t = RACE_SUB_CHUNK_TOKENS;
     if (t > kMaxAutoTile) t = kMaxAutoTile;
@@ -99,6 +102,7 @@ race_status make_problem(const race_shape* sh, int causal, const race_options* o
     p->S = sub(sh);
     p->d = sh->head_dim;
     p->dtype = sh->dtype;
+    p->kernel = kernel_choice(o);
     p->tile = tile;
     p->tiles = sh->seq_len == 0 ? 0 : (sh->seq_len + tile - 1) / tile;
     p->rec = record_floats(p->S, p->d);

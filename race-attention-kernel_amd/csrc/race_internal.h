@@ -45,6 +45,7 @@ struct Problem {
     int64_t N, T;
     int S, d;
     int dtype;       // race_dtype
+    int kernel;      // race_kernel as requested
     int tile;        // tokens per tile (multiple of RACE_SUB_CHUNK_TOKENS)
     int64_t tiles;   // ceil(T / tile)
     int64_t rec;     // record_floats(S, d)
@@ -93,7 +94,22 @@ size_t token_map_lds_bytes(int Wa);
 hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
                                float* dB, float* dA, const Problem& p, hipStream_t stream);
 
-// ---- MFMA kernels (mfma_causal.hip) ----
+// ---- MFMA kernels: mfma_direct.hip (one wave per tile, operands straight
+// from global memory into registers) and mfma_causal.hip (workgroup-
+// cooperative tiles staged through LDS, every supported shape) ----
+
+// Register-direct per-tile totals: (S, d) in {(64, 64), (64, 128), (128, 64)}.
+bool direct_sums_supported(int S, int d);
+hipError_t launch_tile_sums_direct(const void* k, const void* v, float* records, const Problem& p,
+                                   hipStream_t stream);
+// Register-direct causal output pass: S = d = 64, bf16.
+bool direct_output_supported(int S, int d, int dtype);
+// Tiles per compute unit the direct output pass wants resident (8 wave64s).
+int direct_output_tiles_per_cu();
+// Tiles per compute unit the MFMA causal path of this problem wants.
+int mfma_tiles_per_cu(int S, int d, int dtype, int kernel);
+hipError_t launch_causal_output_direct(const void* q, const void* k, const void* v, void* out,
+                                       const float* records, const Problem& p, hipStream_t stream);
 
 // Whether the MFMA causal path has a specialization for (S, d).
 bool mfma_causal_supported(int S, int d);

@@ -76,7 +76,8 @@ race_options make_options(int64_t tile_tokens, int64_t kernel) {
                     tile_tokens <= (int64_t(1) << 30),
                 "tile_tokens must be 0 (automatic) or a positive multiple of ",
                 RACE_SUB_CHUNK_TOKENS, ", got ", tile_tokens);
-    TORCH_CHECK(kernel >= 0 && kernel <= 2, "kernel must be 0 (auto), 1 (valu) or 2 (mfma)");
+    TORCH_CHECK(kernel >= 0 && kernel <= 3,
+                "kernel must be 0 (auto), 1 (valu), 2 (mfma) or 3 (mfma_wg)");
     race_options o;
     o.tile_tokens = static_cast<int32_t>(tile_tokens);
     o.kernel = static_cast<int32_t>(kernel);

@@ -102,34 +102,63 @@ __global__ __launch_bounds__(kThreads) void tile_outer_sums_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Exclusive scan over tiles, one thread per record element (the element-
-// parallel scan of docs/causal_v2_design.md:242-261), tiles walked in order
-// with 8 loads in flight.
+// Exclusive scan of the tile records over tiles, element-parallel like the
+// reference's scan (docs/causal_v2_design.md:242-261) but two-level so that a
+// long run of tiles is not one serial chain of loads: a workgroup owns 32
+// record elements of one stream and splits the tiles into kScanGroups
+// contiguous groups.  Thread (element, group) sums its group; the group sums
+// meet in LDS; each thread then walks its group again writing
+//     prefix(t) = sum of the earlier groups (in group order)
+//               + the earlier tiles of its group (in tile order).
+// Every sum has a fixed order, so the result is bitwise reproducible.
+constexpr int kScanGroups = 8;
+constexpr int kScanElems = kThreads / kScanGroups;  // 32
+
 __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__ records,
                                                              float* __restrict__ state,
                                                              int64_t tiles, int64_t rec, int used) {
-    const int e = blockIdx.x * kThreads + threadIdx.x;
+    __shared__ float gsum[kScanGroups][kScanElems];
+    const int el = threadIdx.x % kScanElems, gi = threadIdx.x / kScanElems;
+    const int e = blockIdx.x * kScanElems + el;
     const int64_t n = blockIdx.y;
-    if (e >= used) return;
+    const int64_t per = (tiles + kScanGroups - 1) / kScanGroups;
+    const int64_t t_begin = gi * per;
+    const int64_t t_end = min(tiles, t_begin + per);
     float* r = records + n * tiles * rec + e;
+    float sum = 0.f;
+    if (e < used) {
+        int64_t t = t_begin;
+        for (; t + 16 <= t_end; t += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * rec];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) sum += v[u];
+        }
+        for (; t < t_end; ++t) sum += r[t * rec];
+    }
+    gsum[gi][el] = sum;
+    __syncthreads();
+    if (e >= used) return;
     float run = 0.f;
-    int64_t t = 0;
-    for (; t + 8 <= tiles; t += 8) {
-        float v[8];
+    for (int j = 0; j < gi; ++j) run += gsum[j][el];
+    int64_t t = t_begin;
+    for (; t + 16 <= t_end; t += 16) {
+        float v[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = r[(t + u) * rec];
+        for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * rec];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
             r[(t + u) * rec] = run;
             run += v[u];
         }
     }
-    for (; t < tiles; ++t) {
+    for (; t < t_end; ++t) {
         const float v = r[t * rec];
         r[t * rec] = run;
         run += v;
     }
-    if (state) state[n * used + e] = run;
+    if (state && gi == kScanGroups - 1) state[n * used + e] = run;
 }
 
 __device__ __forceinline__ float sum_over_tiles(const float* __restrict__ r, int64_t tiles,
@@ -374,7 +403,7 @@ hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, 
 
 hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream) {
     const int used = p.S * p.d + p.S;
-    const dim3 grid(unsigned((used + kThreads - 1) / kThreads), unsigned(p.N));
+    const dim3 grid(unsigned((used + kScanElems - 1) / kScanElems), unsigned(p.N));
     tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.tiles, p.rec, used);
     return hipGetLastError();
 }

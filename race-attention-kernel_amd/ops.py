@@ -24,7 +24,7 @@ from torch.autograd.function import once_differentiable
 
 from . import _lib
 
-KERNELS = {"auto": 0, "valu": 1, "mfma": 2}
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3}
 
 
 def _kernel_id(kernel: str | int) -> int:

@@ -18,7 +18,7 @@ from gpu_util import FP32_TOL, per_stream_rel_err, say, to_np, tol_for
 
 pytestmark = pytest.mark.gpu
 
-KERNELS = ["valu", "mfma"]
+KERNELS = ["valu", "mfma", "mfma_wg"]
 
 
 def has_mfma(ext, L, R, d):
@@ -26,7 +26,7 @@ def has_mfma(ext, L, R, d):
 
 
 def skip_unless_kernel(ext, kernel, L, R, d):
-    if kernel == "mfma" and not has_mfma(ext, L, R, d):
+    if kernel in ("mfma", "mfma_wg") and not has_mfma(ext, L, R, d):
         pytest.skip(f"no MFMA specialization for S={L * R}, d={d}")
 
 
