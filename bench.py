@@ -1,10 +1,10 @@
 #!/usr/bin/env python3
 """Benchmark of race_fused_fwd on one MI355X; prints ONE JSON line.
 
-Default workload (the config its metric is quoted
-on): causal forward, N = 8 streams, L = 4, R = 16 (S = 64), d = 64,
-T = 65536, fp32, synthetic inputs from the BASELINE distribution generated
-on the GPU (resident in HBM before the timed region).  A "step" is one
+Default workload (cfg2, the configuration the headline metric is quoted on):
+causal forward, N = 8 streams, L = 4, R = 16 (S = 64), d = 64, T = 65536,
+fp32, synthetic inputs (softmax probabilities of N(0,1)*4 logits, N(0,1)
+values) generated on the GPU and resident in HBM before the timed region.  A "step" is one
 race_fused_fwd pass over that batch: every kernel of the op, through the C
 ABI (include/race_mi355x.h), with caller-owned output and workspace.
 
@@ -15,18 +15,23 @@ first kernel and after every kernel, so the per-kernel durations behind
 `roofline` come from the same timed region.  `value` = N*T / (mean step time)
 in M tokens/s.
 
-roofline: the dominant kernel's algorithmic HBM bytes per launch (inputs read
-once, output written once: bytes_per_stream_token * N * T, plus its workspace
-records) / its mean duration, against MI355X's 8 TB/s.  traffic: HBM bytes
-per launch measured with rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, read from
-profiles/traffic.json when a measurement for this workload exists, else null.
+roofline: the dominant kernel's algorithmic HBM bytes per launch (each
+operand it streams read once, its output written once: bytes per
+stream-token * N * T; workspace records excluded) / its mean duration,
+against MI355X's 8 TB/s.  traffic: HBM bytes per launch measured with
+rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (scaled by the same counters on a
+plain copy of known size, --calibrate-copy), read from profiles/traffic.json
+when a measurement for this workload exists, else null.
 
 cpu_baseline: the reference's CPU path -- the fp32 torch cumsum + bmm
 composition of src/race_baseline.py:45-51, as restated in oracle/ -- timed on
-this host at BASELINE config 1 (N = 8, T = 4096): 1 warmup, median of 3.
+this host's cores on the bench workload itself (cfg2: N = 8, T = 65536; a
+shorter T when the host has too little free memory for its 5-D tensors):
+1 warmup, median of 3.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
-                       [--T T] [--kernel auto|valu|mfma] [--tile N] [--no-cpu-baseline]
+                       [--T T] [--kernel auto|valu|mfma|mfma_wg] [--tile N] [--no-cpu-baseline]
+                       [--calibrate-copy MIB]
 """
 from __future__ import annotations
 
@@ -47,7 +52,8 @@ import __graft_entry__ as entry  # noqa: E402
 METRIC = "causal fwd M tokens/s at N=8,S=64,d_k=64,T=64K on 1 GPU; max T that fits"
 UNIT = "M tokens/s"
 PEAK_HBM_GBPS = 8000.0
-# the reference's PyTorch path, T = 65536, A100-SXM4-40GB.
+# The reference's published number for this shape: its PyTorch cumsum + bmm
+# path at T = 65536 on an A100-SXM4-40GB (README.md:65-77 of the reference).
 REFERENCE_MTOKS_T65536 = 5.25
 
 WORKLOADS = {
@@ -112,6 +118,8 @@ def parse_args():
     ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB before timing (rocprofv3 counter scale)")
     return ap.parse_args()
 
 
@@ -121,13 +129,12 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
     S, d = cfg.S, cfg.d
     state = 4.0 * cfg.N * tiles * rec
     return {
-        "tile_sums": es * (S + d) * NT + state,
-        "tile_sums_mfma": es * (S + d) * NT + state,
+        "tile_sums": es * (S + d) * NT,
+        "tile_sums_mfma": es * (S + d) * NT,
         "tile_scan": 2 * state,
         "tile_reduce": state,
-        "output_pass_valu": es * (2 * S + 2 * d) * NT + state,
-        "output_pass_mfma": es * (2 * S + 2 * d) * NT + state,
-        "fused_mfma": es * (2 * S + 2 * d) * NT,
+        "output_pass_valu": es * (2 * S + 2 * d) * NT,
+        "output_pass_mfma": es * (2 * S + 2 * d) * NT,
         "token_map": es * (S + d) * NT,
     }.get(name, es * (2 * S + 2 * d) * NT)
 
@@ -145,12 +152,24 @@ def traffic_for(workload_key: str, kernel_name: str):
 
 
 def cpu_baseline():
-    """The reference CPU path (torch fp32 cumsum + bmm) at BASELINE config 1."""
+    """The reference CPU path (torch fp32 cumsum + bmm) on the cfg2 workload.
+
+    Its 5-D prefix tensors need about 2.2 * N * T * S * d * 4 bytes
+    (src/race_baseline.py:46-47); T is halved until that fits in a third of
+    the host's available memory."""
     import torch
 
     race = entry.load_package()
     oracle = entry.load_oracle()
-    N, T, L, R, d = 8, 4096, 4, 16, 64
+    N, T, L, R, d = 8, 65536, 4, 16, 64
+    try:
+        import psutil
+
+        avail = psutil.virtual_memory().available
+    except ImportError:
+        avail = 64 << 30
+    while T > 1024 and 3 * 2.2 * N * T * L * R * d * 4 > avail:
+        T //= 2
     q, k, v = race.make_inputs(N, T, L, R, d, seed=1)
     q, k = q.flatten(2), k.flatten(2)
     threads = torch.get_num_threads()
@@ -167,7 +186,8 @@ def cpu_baseline():
         "unit": UNIT,
         "cores": threads,
         "kind": "port",
-        "sample": (f"BASELINE config 1: causal N={N} T={T} L={L} R={R} d={d} fp32, the torch-CPU "
+        "sample": (f"causal N={N} T={T} L={L} R={R} d={d} fp32 (the cfg2 workload"
+                   f"{'' if T == 65536 else ', T reduced to fit host memory'}), the torch-CPU "
                    f"cumsum+bmm composition of src/race_baseline.py:45-51 (oracle/oracle.py "
                    f"torch_reference_path), {threads} threads, median of 3 after 1 warmup: "
                    f"{med * 1e3:.1f} ms per call"),
@@ -178,7 +198,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
-              "multi-GPU sharding of the op is a design in DESIGN.md, not a measured path.",
+              "multi-GPU sharding of the op is designed but not measured here.",
               file=sys.stderr)
         return 2
     import torch
@@ -211,6 +231,15 @@ def main() -> int:
     out = torch.empty_like(v)
     stream = torch.cuda.current_stream().cuda_stream
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+
+    if args.calibrate_copy:
+        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE counters give
+        # the scale of those counters on this device.
+        src = torch.ones(args.calibrate_copy << 18, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     events = HipEvents()
     max_launches = 8

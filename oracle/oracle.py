@@ -24,7 +24,7 @@ What is here, and which reference lines each piece restates
   (src/race_baseline.py:45-51 verbatim in semantics).  It is the timed CPU
   baseline of bench.py and the fp32 comparison point of the tests.
 * ``torch_noncausal_autograd`` -- torch.autograd on the non-causal formula
-  (analysis/hot-path.md:157-162), the oracle BASELINE config 4 names for the
+  (analysis/hot-path.md:157-162), the oracle the non-causal benchmark names for the
   gradients.
 
 Layouts: probsQ/probsK [N, T, S] (S = L*R, table-major), V/out [N, T, d].

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs of the BASELINE configurations.
+"""Seeded synthetic inputs of the benchmark configurations cfg1 .. cfg5.
 
 probsQ and probsK are each a softmax over R of logits ~ N(0, 1) * 4
 (temperature 0.25), V ~ N(0, 1), the upstream gradient ~ N(0, 1); generated
@@ -31,7 +31,9 @@ class Config:
         return self.L * self.R
 
 
-# BASELINE.json "configs", in order.
+# The benchmark configurations, in order: cfg1 the reference's CPU path,
+# cfg2 the headline causal fp32 sweep (T = 512 .. 65536), cfg3 long-context
+# bf16, cfg4 non-causal forward + backward, cfg5 large buckets (S = 256).
 CONFIGS = {
     "cfg1_cpu_causal_fp32": Config("cfg1_cpu_causal_fp32", 8, 4096, 4, 16, 64, torch.float32, True),
     "cfg2_causal_fp32": Config("cfg2_causal_fp32", 8, 65536, 4, 16, 64, torch.float32, True),

@@ -39,7 +39,7 @@ def run(race, q, k, v, kernel="auto", tile=0):
 @pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("T", [512, 1024, 2048, 4096, 8192, 16384, 32768, 65536])
 def test_cfg2_sweep_matches_oracle(race, ext, oracle, cuda, kernel, T):
-    # N=8, L=4, R=16, d=64, fp32, every T in 512..65536.
+    # cfg2: N=8, L=4, R=16, d=64, fp32, every T in 512..65536.
     skip_unless_kernel(ext, kernel, 4, 16, 64)
     say("cfg2", kernel, "T", T)
     q, k, v = race.make_inputs(8, T, 4, 16, 64, seed=T)
@@ -210,7 +210,7 @@ def test_golden_vectors(race, cuda, name):
 
 
 def test_cfg3_bf16_long_context(race, oracle, cuda):
-    # bf16 inputs, T = 2^17, 2^18 and 2^20, N = 8.  Inputs are
+    # cfg3: bf16 inputs, T = 2^17, 2^18 and 2^20, N = 8.  Inputs are
     # generated on the GPU; streams 0 and 7 are copied back and checked against
     # the fp64 oracle on the same bf16 values.
     for T in (1 << 17, 1 << 18, 1 << 20):
@@ -229,7 +229,7 @@ def test_cfg3_bf16_long_context(race, oracle, cuda):
 
 
 def test_cfg5_bf16_large_buckets(race, oracle, cuda):
-    # N = 128, L = 8, R = 32 (S = 256), d = 128, T = 16384, bf16.
+    # cfg5: N = 128, L = 8, R = 32 (S = 256), d = 128, T = 16384, bf16.
     say("cfg5")
     q, k, v = race.make_inputs(128, 16384, 8, 32, 128, seed=5, dtype=torch.bfloat16, device=cuda,
                                gen_device="cuda")

@@ -1,6 +1,6 @@
 """GPU parity of the non-causal forward and backward against the CPU oracle.
 
-BASELINE config 4 (N = 384, T = 1024, L = 4, R = 16, d = 64, fp32): outputs
+cfg4 (N = 384, T = 1024, L = 4, R = 16, d = 64, fp32): outputs
 against the fp64 oracle, gradients w.r.t. probsQ, probsK and V against the
 oracle's closed-form VJP and against torch.autograd on the reference formula
 (analysis/hot-path.md:157-162).  The property tests follow the reference's
@@ -40,8 +40,8 @@ def test_cfg4_forward_and_backward_match_oracle(race, oracle, cuda):
 
 
 def test_cfg4_gradients_match_torch_autograd(race, oracle, cuda):
-    # BASELINE config 4 names torch autograd on the reference formula as the
-    # gradient check; run it on 16 of the 384 streams (fp64, CPU).
+    # The cfg4 gradient check is torch autograd on the reference formula; run
+    # it on 16 of the 384 streams (fp64, CPU).
     say("cfg4 autograd")
     q, k, v, g = race.make_inputs(384, 1024, 4, 16, 64, seed=4, grad_out=True)
     out, dq, dk, dv = forward_backward(race, q, k, v, g, cuda)
