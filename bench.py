@@ -8,12 +8,13 @@ values) generated on the GPU and resident in HBM before the timed region.  A "st
 race_fused_fwd pass over that batch: every kernel of the op, through the C
 ABI (include/race_mi355x.h), with caller-owned output and workspace.
 
-Timing: W untimed warmup steps, then K steps bracketed by
-torch.cuda.synchronize() on both sides.  Each timed step runs through
-race_fwd_profiled, which records a HIP event on the launch stream before the
-first kernel and after every kernel, so the per-kernel durations behind
-`roofline` come from the same timed region.  `value` = N*T / (mean step time)
-in M tokens/s.
+Timing: W untimed warmup steps, then two timed regions, each of K steps
+bracketed by torch.cuda.synchronize() on both sides.  The first runs plain
+race_fwd steps back to back on the stream between two HIP events: `value` =
+N*T / (mean step time) in M tokens/s.  The second runs race_fwd_profiled,
+which records a HIP event on the launch stream before the first kernel and
+after every kernel; the per-kernel durations behind `roofline` come from it
+(its step time, with the extra events, is `profiled_ms_per_step`).
 
 roofline: the dominant kernel's algorithmic HBM bytes per launch (each
 operand it streams read once, its output written once: bytes per
@@ -82,7 +83,12 @@ class HipEvents:
                                                  ctypes.c_void_p]
         self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.created = []
+
+    def record(self, h, stream) -> None:
+        if self.lib.hipEventRecord(h, stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
 
     def array(self, n):
         arr = (ctypes.c_void_p * n)()
@@ -246,25 +252,38 @@ def main() -> int:
     per_step = [events.array(max_launches + 1) for _ in range(args.steps)]
     warm = events.array(max_launches + 1)
 
-    for _ in range(args.warmup):
-        st, _ = abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream, warm)
+    def check(st):
         if st != 0:
             raise RuntimeError(abi.status_string(st))
+
+    for _ in range(args.warmup):
+        check(abi.fwd(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
+        check(abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream,
+                               warm)[0])
     torch.cuda.synchronize()
 
-    n_events = 0
+    # Timed region 1 (`value`): K plain race_fwd steps, back to back on one
+    # stream, between two events.
+    bracket = events.array(2)
     t0 = time.perf_counter()
+    events.record(bracket[0], stream)
+    for _ in range(args.steps):
+        check(abi.fwd(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
+    events.record(bracket[1], stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
+
+    # Timed region 2 (per-kernel durations): K race_fwd_profiled steps, which
+    # put an event before the first launch and after every launch.
+    n_events = 0
     for i in range(args.steps):
         st, n_events = abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
                                         stream, per_step[i])
-        if st != 0:
-            raise RuntimeError(abi.status_string(st))
+        check(st)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
 
-    gpu_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1])
-    # Steps are back to back on one stream: first event of step 0 to last of step K-1.
-    ms_per_step = gpu_ms / args.steps
+    profiled_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1]) / args.steps
     n_launch = n_events - 1
     phase_ms = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step)
                 for j in range(n_launch)]
@@ -302,6 +321,7 @@ def main() -> int:
             "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch,
             "kernel_ms": {names[j]: round(phase_ms[j], 5) for j in range(n_launch)},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+            "profiled_ms_per_step": round(profiled_ms, 5),
             "peak_hbm_bytes_per_token": round(bytes_per_token, 1),
             "workspace_bytes_per_token": round(ws_bytes / T, 2),
             "max_T_fits_est": int(0.95 * total_mem / bytes_per_token),

@@ -99,7 +99,7 @@ struct Geo {
 };
 
 // Raw K and V registers of one sub-chunk.
-template <typename TIn, int S, int D, int C>
+template <typename TIn, int S, int D, int C, int P>
 struct KVStage {
     using G = Geo<TIn, S, D, C>;
     uint4 k[G::kKPer][4];
@@ -116,7 +116,7 @@ struct KVStage {
             if (G::kKBlk % kThreads == 0 || blk < G::kKBlk) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
-                    k[p][rr] = buf_load16(kr, ((r0 + 4 * a + rr) * S + b * G::E) * int(sizeof(TIn)));
+                    k[p][rr] = buf_load16<P>(kr, ((r0 + 4 * a + rr) * S + b * G::E) * int(sizeof(TIn)));
             }
         }
 #pragma unroll
@@ -126,7 +126,7 @@ struct KVStage {
             if (G::kVBlk % kThreads == 0 || blk < G::kVBlk) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
-                    v[p][rr] = buf_load16(vr, ((r0 + 4 * a + rr) * D + b * G::E) * int(sizeof(TIn)));
+                    v[p][rr] = buf_load16<P>(vr, ((r0 + 4 * a + rr) * D + b * G::E) * int(sizeof(TIn)));
             }
         }
     }
@@ -209,7 +209,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
     unsigned char* VTs = KTs + G::kKTBytes;
     float* Apart = reinterpret_cast<float*>(VTs + G::kVTBytes);  // [16][S]
 
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, lr = l & 15;
+    const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t n = blockIdx.y, ti = blockIdx.x;
     const int64_t t_begin = ti * tile;
     const int64_t t_end = min(T, t_begin + tile);
@@ -226,12 +227,12 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < G::kKPer * G::E; ++i) asum[i] = 0.f;
 
-    KVStage<TIn, S, D, C> st;
+    KVStage<TIn, S, D, C, kSumsLoadPolicy> st;
     st.load(kr, vr, 0);
     for (int r0 = 0; r0 < rows; r0 += C) {
         __syncthreads();
         st.store(nullptr, KTs, VTs, asum);
-        if (r0 + C < rows) st.load(kr, vr, r0 + C);
+        st.load(kr, vr, r0 + C);  // past the tile: zeros, never used
         __syncthreads();
         bf16x8 vh[CBW][NKC], vl[CBW][NKC];
 #pragma unroll
@@ -311,7 +312,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     unsigned char* KTs = Ks + G::kKBytes;
     unsigned char* VTs = KTs + G::kKTBytes;
 
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, lr = l & 15;
+    const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t n = blockIdx.y, ti = blockIdx.x;
     const int64_t t_begin = ti * tile;
     const int64_t t_end = min(T, t_begin + tile);
@@ -345,20 +347,19 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
 
     // Q of a sub-chunk in the layout of step 2: lane (g, lr) holds
     // Q[16 bi + lr][16 (w + 4 sbw) + 4 g .. + 3].
-    f32x4 qr[SBW][NBI];
-    auto load_q = [&](int r0) {
+    using QRegs = f32x4[SBW][NBI];
+    auto load_q = [&](QRegs& qr, int r0) {
 #pragma unroll
         for (int sbw = 0; sbw < SBW; ++sbw)
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi)
-                qr[sbw][bi] = load_q4<TIn>(
+                qr[sbw][bi] = load_q4<TIn, kOutQPolicy>(
                     qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + 4 * sbw) + 4 * g) * int(sizeof(TIn)));
     };
 
-    KVStage<TIn, S, D, C> st;
-    st.load(kr, vr, 0);
-    load_q(0);
-    for (int r0 = 0; r0 < rows; r0 += C) {
+    // One sub-chunk from the raw registers `st` / `qr`, which are then
+    // refilled with the next sub-chunk (a deeper prefetch measured slower).
+    auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy>& st, QRegs& qr, int r0) {
         __syncthreads();
         st.store(Ks, KTs, VTs, nullptr);
         f32x4 qc[SBW][NBI];
@@ -366,10 +367,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         for (int sbw = 0; sbw < SBW; ++sbw)
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) qc[sbw][bi] = qr[sbw][bi];
-        if (r0 + C < rows) {
-            st.load(kr, vr, r0 + C);
-            load_q(r0 + C);
-        }
+        // Prefetch (past the tile: zeros, never used).
+        st.load(kr, vr, r0 + C);
+        load_q(qr, r0 + C);
         __syncthreads();
 
         // 1 + 2: running mass and W.
@@ -485,7 +485,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
                     }
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
-                store4<TIn>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * int(sizeof(TIn)), o[bi]);
+                store4<TIn, kOutStorePolicy>(
+                    or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * int(sizeof(TIn)), o[bi]);
             }
 #pragma unroll
             for (int sb = 0; sb < NSB; ++sb)
@@ -496,7 +497,13 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
                     b0[sb][cbw] = mfma3<kSplit>(kh, kl, vh[kk], vl[kk], b0[sb][cbw]);
                 }
         }
-    }
+    };
+
+    KVStage<TIn, S, D, C, kOutKVPolicy> st;
+    QRegs qr;
+    st.load(kr, vr, 0);
+    load_q(qr, 0);
+    for (int r0 = 0; r0 < rows; r0 += C) sub_chunk(st, qr, r0);
 }
 
 template <typename TIn, int S, int D, int C, int kMinBlocks>

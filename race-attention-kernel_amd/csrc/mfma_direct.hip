@@ -34,7 +34,7 @@ __device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& 
 }
 
 // One sub-chunk of a [tokens][W] tensor in the lane layout above.
-template <typename TIn, int W>
+template <typename TIn, int W, int P>
 struct DRows {
     static constexpr int NG = W / 64;
     f32x4 x[NG][2][4];  // [column group][h][r]: columns 64 gg + 4 lr .. + 3 of row 16 h + 4 g + r
@@ -46,7 +46,7 @@ struct DRows {
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    x[gg][h][r] = load_q4<TIn>(
+                    x[gg][h][r] = load_q4<TIn, P>(
                         rs, ((r0 + 16 * h + 4 * g + r) * W + 64 * gg + 4 * lr) * int(sizeof(TIn)));
     }
     // The 8 rows of column 64 gg + 4 lr + c, in permuted-k order.
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_direct_kernel(
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) asum[sg][sb] = 0.f;
 
-    auto chunk = [&](DRows<TIn, S>& kx, DRows<TIn, D>& vx, int r0) {
+    auto chunk = [&](DRows<TIn, S, kSumsLoadPolicy>& kx, DRows<TIn, D, kSumsLoadPolicy>& vx, int r0) {
         bf16x8 vh[NDG][4], vl[NDG][4];
 #pragma unroll
         for (int dg = 0; dg < NDG; ++dg)
@@ -131,8 +131,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_direct_kernel(
         kx.load(kr, r0 + 2 * C, g, lr);
     };
 
-    DRows<TIn, S> k0, k1;
-    DRows<TIn, D> v0, v1;
+    DRows<TIn, S, kSumsLoadPolicy> k0, k1;
+    DRows<TIn, D, kSumsLoadPolicy> v0, v1;
     k0.load(kr, 0, g, lr);
     v0.load(vr, 0, g, lr);
     k1.load(kr, C, g, lr);
@@ -201,20 +201,20 @@ struct DStage {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = r0 + 16 * h + 4 * g + r;
-                k1[h][r] = load_q4<TIn>(kr, (row * 64 + 4 * lr) * es);
-                v1[h][r] = load_q4<TIn>(vr, (row * 64 + 4 * lr) * es);
+                k1[h][r] = load_q4<TIn, kPolicyDefault>(kr, (row * 64 + 4 * lr) * es);
+                v1[h][r] = load_q4<TIn, kOutKVPolicy>(vr, (row * 64 + 4 * lr) * es);
             }
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) k2[b][u] = load_q4<TIn>(kr, ((r0 + 16 * b + lr) * 64 + 16 * g + 4 * u) * es);
+            for (int u = 0; u < 4; ++u) k2[b][u] = load_q4<TIn, kPolicyDefault>(kr, ((r0 + 16 * b + lr) * 64 + 16 * g + 4 * u) * es);
     }
     __device__ __forceinline__ void load_q(__amdgpu_buffer_rsrc_t qr, int r0, int g, int lr) {
         constexpr int es = int(sizeof(TIn));
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) q2[b][u] = load_q4<TIn>(qr, ((r0 + 16 * b + lr) * 64 + 16 * g + 4 * u) * es);
+            for (int u = 0; u < 4; ++u) q2[b][u] = load_q4<TIn, kOutQPolicy>(qr, ((r0 + 16 * b + lr) * 64 + 16 * g + 4 * u) * es);
     }
 };
 
@@ -222,9 +222,9 @@ struct DStage {
 template <typename TIn>
 __device__ __forceinline__ void store2(__amdgpu_buffer_rsrc_t r, int off, float x0, float x1) {
     if constexpr (std::is_same<TIn, float>::value) {
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(x0), __float_as_uint(x1)}, r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(x0), __float_as_uint(x1)}, r, off, 0, kOutStorePolicy);
     } else {
-        __builtin_amdgcn_raw_buffer_store_b32(pack2(x0, x1), r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(pack2(x0, x1), r, off, 0, kOutStorePolicy);
     }
 }
 
