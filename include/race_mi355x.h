@@ -11,7 +11,7 @@
  *     non-causal:  the same with A, B summed over all T tokens
  *                  (analysis/hot-path.md:157-162).
  *
- * plus the non-causal backward w.r.t. probsQ, probsK and V.  The name is the
+ * plus the backward of both w.r.t. probsQ, probsK and V.  The name is the
  * one of the upstream host wrapper the reference describes as taking
  * "probsK/probsQ precomputed in fp32 ([N,T,S])" (src/race_fused_fwd.cu:9-13).
  *
@@ -164,6 +164,32 @@ race_status race_noncausal_bwd(const void* probsQ, const void* probsK, const voi
                                const void* dOut, const float* state, void* dQ, void* dK, void* dV,
                                const race_shape* shape, const race_options* opts, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace of race_causal_bwd in bytes: two record arrays [N][tiles][rec],
+ * the running mass at every 16-token step ([N][tiles][tile/16][S]) and an
+ * fp32 copy of dQ ([N][T][S]) -- O(1) per token. */
+race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                            size_t* bytes);
+
+/* Gradients of the causal forward w.r.t. probsQ, probsK and V for the
+ * upstream gradient dOut.  The reference has no kernel for this: its design
+ * outline (docs/causal_v2_design.md:689-742, for the globally normalized
+ * function) walks prefix states forward and suffix states backward, which is
+ * what this does for the per-bucket function of src/race_baseline.py:45-51.
+ * With A_i, B_i the inclusive prefix sums, r_i = 1 / (A_i + eps), W_i = q_i r_i
+ * and g = dOut:
+ *   dq_i[s] = r_i[s] <B_i[s][:], g_i>,   alpha_i = -W_i dq_i (elementwise),
+ *   Z_j = sum_{i>=j} W_i (x) g_i,  Y_j = sum_{i>=j} alpha_i,
+ *   dk_j[s] = <Z_j[s][:], v_j> + Y_j[s],  dv_j[c] = sum_s k_j[s] Z_j[s][c].
+ * The forward prefix states are recomputed (tile totals and their scan), so
+ * only the forward's inputs are needed.  Any of dQ, dK, dV may be NULL to
+ * skip it.  Runs the fp32 vector-ALU kernels; shapes whose state S*(d+1)
+ * plus a 16-token sub-chunk do not fit one workgroup's LDS (e.g. S = 256,
+ * d = 128) return RACE_ERROR_INVALID_VALUE, as does RACE_KERNEL_MFMA. */
+race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* V,
+                            const void* dOut, void* dQ, void* dK, void* dV,
+                            const race_shape* shape, const race_options* opts, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

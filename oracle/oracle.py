@@ -26,6 +26,11 @@ What is here, and which reference lines each piece restates
 * ``torch_noncausal_autograd`` -- torch.autograd on the non-causal formula
   (analysis/hot-path.md:157-162), the oracle the non-causal benchmark names for the
   gradients.
+* ``causal_bwd`` -- the closed-form VJP of the causal function (race_oracle.c,
+  fp64).  The reference has no causal backward kernel; its outline is
+  docs/causal_v2_design.md:689-742.  ``torch_causal_autograd`` is
+  torch.autograd through the cumsum composition of src/race_baseline.py:45-51
+  in fp64, the independent check of it.
 
 Layouts: probsQ/probsK [N, T, S] (S = L*R, table-major), V/out [N, T, d].
 """
@@ -69,8 +74,9 @@ def _load():
         lib.race_oracle_causal_tiled.argtypes = [f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i64, i64, i]
         lib.race_oracle_noncausal_fwd.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i]
         lib.race_oracle_noncausal_bwd.argtypes = [f32p, f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i]
+        lib.race_oracle_causal_bwd.argtypes = [f32p, f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i]
         for name in ("race_oracle_causal_recurrence", "race_oracle_causal_chunked", "race_oracle_causal_tiled",
-                     "race_oracle_noncausal_fwd", "race_oracle_noncausal_bwd"):
+                     "race_oracle_noncausal_fwd", "race_oracle_noncausal_bwd", "race_oracle_causal_bwd"):
             getattr(lib, name).restype = None
         _lib = lib
     return _lib
@@ -154,6 +160,19 @@ def noncausal_bwd(q, k, v, g, eps: float = EPS, nthreads: int = 0):
     return dq, dk, dv
 
 
+def causal_bwd(q, k, v, g, eps: float = EPS, nthreads: int = 0):
+    """Closed-form VJP of the causal forward, fp64.  Returns (dq, dk, dv)."""
+    q, k, v, g = _f32(q), _f32(k), _f32(v), _f32(g)
+    N, T, S, d = _shape(q, v)
+    dq = np.empty((N, T, S), np.float64)
+    dk = np.empty((N, T, S), np.float64)
+    dv = np.empty((N, T, d), np.float64)
+    _load().race_oracle_causal_bwd(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(g, ctypes.c_float),
+        _ptr(dq, ctypes.c_double), _ptr(dk, ctypes.c_double), _ptr(dv, ctypes.c_double), N, T, S, d, eps, nthreads)
+    return dq, dk, dv
+
+
 def cumsum_bmm(q, k, v, eps: float = EPS, dtype=np.float64):
     """src/race_baseline.py:45-51 transcribed to numpy, in ``dtype``.
 
@@ -210,5 +229,29 @@ def torch_noncausal_autograd(q, k, v, g, eps: float = EPS):
     qt, kt, vt = (torch.as_tensor(np.asarray(x, np.float64)).requires_grad_(True) for x in (q, k, v))
     gt = torch.as_tensor(np.asarray(g, np.float64))
     out = torch_noncausal_reference(qt, kt, vt, eps)
+    dq, dk, dv = torch.autograd.grad(out, (qt, kt, vt), gt)
+    return out.detach().numpy(), dq.numpy(), dk.numpy(), dv.numpy()
+
+
+def torch_causal_reference(q, k, v, eps: float = EPS):
+    """src/race_baseline.py:45-51 as differentiable torch ops (any dtype)."""
+    import torch
+
+    N, T, S = q.shape
+    d = v.shape[2]
+    a_pref = k.cumsum(dim=1)
+    b_pref = (k.unsqueeze(-1) * v.unsqueeze(2)).cumsum(dim=1)
+    e_pref = b_pref / (a_pref.unsqueeze(-1) + eps)
+    return (q.unsqueeze(-1) * e_pref).sum(2)
+
+
+def torch_causal_autograd(q, k, v, g, eps: float = EPS):
+    """Gradients of the causal function by torch.autograd in fp64 (small T:
+    the composition holds [N, T, S, d] tensors)."""
+    import torch
+
+    qt, kt, vt = (torch.as_tensor(np.asarray(x, np.float64)).requires_grad_(True) for x in (q, k, v))
+    gt = torch.as_tensor(np.asarray(g, np.float64))
+    out = torch_causal_reference(qt, kt, vt, eps)
     dq, dk, dv = torch.autograd.grad(out, (qt, kt, vt), gt)
     return out.detach().numpy(), dq.numpy(), dk.numpy(), dv.numpy()

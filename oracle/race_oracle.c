@@ -38,6 +38,9 @@
  *                                   scan over tiles, chunk walk inside a tile
  *                                   (src/causal_v2/reference.py:84-103,144-159)
  *   race_oracle_noncausal_fwd/bwd  full-sequence totals and the closed-form VJP
+ *   race_oracle_causal_bwd         the closed-form VJP of the causal function (the
+ *                                   reference has no kernel for it; its design
+ *                                   outline is docs/causal_v2_design.md:689-742)
  */
 #include <math.h>
 #include <stdint.h>
@@ -340,5 +343,80 @@ void race_oracle_noncausal_bwd(const float* q, const float* k, const float* v, c
         free(E);
         free(dB);
         free(dA);
+    }
+}
+
+/* Causal backward, the closed-form VJP of the causal function for the
+ * upstream gradient g = dOut.  With the inclusive prefix sums A_i, B_i,
+ * r_i = 1 / (A_i + eps) and W_i = q_i * r_i (elementwise over buckets):
+ *   dq_i[s]    = r_i[s] * <B_i[s][:], g_i>
+ *   alpha_i[s] = -W_i[s] * dq_i[s]                  (dLoss/dA_i)
+ *   Z_j        = sum_{i>=j} W_i (x) g_i,  Y_j = sum_{i>=j} alpha_i   (suffix sums)
+ *   dk_j[s]    = <Z_j[s][:], v_j> + Y_j[s]
+ *   dv_j[c]    = sum_s k_j[s] Z_j[s][c]
+ * One forward pass over the tokens (prefix sums) stores W and alpha; one
+ * backward pass accumulates the suffix sums. */
+void race_oracle_causal_bwd(const float* q, const float* k, const float* v, const float* g,
+                            double* dq, double* dk, double* dv, i64 N, i64 T, i64 S, i64 d,
+                            double eps, int nthreads) {
+    set_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (i64 n = 0; n < N; ++n) {
+        double* A = (double*)calloc((size_t)S, sizeof(double));
+        double* B = (double*)calloc((size_t)(S * d), sizeof(double));
+        double* W = (double*)malloc((size_t)(T * S) * sizeof(double));
+        double* alpha = (double*)malloc((size_t)(T * S) * sizeof(double));
+        for (i64 t = 0; t < T; ++t) {
+            const float* qt = q + (n * T + t) * S;
+            const float* kt = k + (n * T + t) * S;
+            const float* vt = v + (n * T + t) * d;
+            const float* gt = g + (n * T + t) * d;
+            double* dqt = dq + (n * T + t) * S;
+            for (i64 s = 0; s < S; ++s) {
+                const double ks = kt[s];
+                A[s] += ks;
+                double* Bs = B + s * d;
+                double u = 0.0;
+                for (i64 c = 0; c < d; ++c) {
+                    Bs[c] += ks * (double)vt[c];
+                    u += Bs[c] * (double)gt[c];
+                }
+                const double r = 1.0 / (A[s] + eps);
+                dqt[s] = r * u;
+                W[t * S + s] = (double)qt[s] * r;
+                alpha[t * S + s] = -W[t * S + s] * dqt[s];
+            }
+        }
+        double* Z = (double*)calloc((size_t)(S * d), sizeof(double));
+        double* Y = (double*)calloc((size_t)S, sizeof(double));
+        for (i64 t = T - 1; t >= 0; --t) {
+            const float* kt = k + (n * T + t) * S;
+            const float* vt = v + (n * T + t) * d;
+            const float* gt = g + (n * T + t) * d;
+            double* dkt = dk + (n * T + t) * S;
+            double* dvt = dv + (n * T + t) * d;
+            for (i64 s = 0; s < S; ++s) {
+                const double ws = W[t * S + s];
+                double* Zs = Z + s * d;
+                double acc = 0.0;
+                for (i64 c = 0; c < d; ++c) {
+                    Zs[c] += ws * (double)gt[c];
+                    acc += Zs[c] * (double)vt[c];
+                }
+                Y[s] += alpha[t * S + s];
+                dkt[s] = acc + Y[s];
+            }
+            for (i64 c = 0; c < d; ++c) {
+                double acc = 0.0;
+                for (i64 s = 0; s < S; ++s) acc += (double)kt[s] * Z[s * d + c];
+                dvt[c] = acc;
+            }
+        }
+        free(A);
+        free(B);
+        free(W);
+        free(alpha);
+        free(Z);
+        free(Y);
     }
 }

@@ -1,15 +1,16 @@
 """MI355X-native per-bucket RACE attention: race_fused_fwd(probsQ, probsK, V, causal).
 
-The op and its non-causal backward run hand-written gfx950 HIP kernels behind
+The op and its backward (causal and non-causal) run hand-written gfx950 HIP kernels behind
 the C ABI of include/race_mi355x.h (librace_mi355x.so), reached from PyTorch
 through the _race_torch binding.  There is no CPU fallback.
 """
 from .batched_ace import BatchedACE
 from .inputs import CONFIGS, Config, config_inputs, make_inputs
-from .ops import (RaceFusedFunction, race_fused_fwd, race_fused_fwd_with_state,
-                  race_noncausal_backward, select_tile_tokens)
+from .ops import (RaceFusedFunction, race_causal_backward, race_fused_fwd,
+                  race_fused_fwd_with_state, race_noncausal_backward, select_tile_tokens)
 
 __all__ = [
     "BatchedACE", "CONFIGS", "Config", "RaceFusedFunction", "config_inputs", "make_inputs",
-    "race_fused_fwd", "race_fused_fwd_with_state", "race_noncausal_backward", "select_tile_tokens",
+    "race_fused_fwd", "race_fused_fwd_with_state", "race_noncausal_backward", "race_causal_backward",
+    "select_tile_tokens",
 ]

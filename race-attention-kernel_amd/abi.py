@@ -30,6 +30,8 @@ EXPORTED_SYMBOLS = (
     "race_fwd_profiled",
     "race_noncausal_bwd_workspace_bytes",
     "race_noncausal_bwd",
+    "race_causal_bwd_workspace_bytes",
+    "race_causal_bwd",
 )
 
 
@@ -70,6 +72,8 @@ def lib() -> ctypes.CDLL:
                                         ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         L.race_noncausal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_noncausal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
+        L.race_causal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
+        L.race_causal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         for name in EXPORTED_SYMBOLS[2:]:
             getattr(L, name).restype = i32
         _configured = True
@@ -138,3 +142,19 @@ def noncausal_bwd(q: int, k: int, v: int, g: int, state: int, dq: int | None, dk
     return lib().race_noncausal_bwd(q, k, v, g, state, dq, dk, dv, ctypes.byref(sh),
                                     ctypes.byref(opts) if opts is not None else None,
                                     workspace, workspace_bytes, stream)
+
+
+def causal_bwd_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):
+    b = ctypes.c_size_t(0)
+    st = lib().race_causal_bwd_workspace_bytes(ctypes.byref(sh),
+                                               ctypes.byref(opts) if opts is not None else None,
+                                               ctypes.byref(b))
+    return st, b.value
+
+
+def causal_bwd(q: int, k: int, v: int, g: int, dq: int | None, dk: int | None, dv: int | None,
+               sh: RaceShape, opts: RaceOptions | None, workspace: int | None, workspace_bytes: int,
+               stream: int) -> int:
+    return lib().race_causal_bwd(q, k, v, g, dq, dk, dv, ctypes.byref(sh),
+                                 ctypes.byref(opts) if opts is not None else None,
+                                 workspace, workspace_bytes, stream)

@@ -142,6 +142,23 @@ BwdLayout bwd_layout(const Problem& p) {
     return l;
 }
 
+// Causal backward workspace: forward prefix records, suffix records, the
+// running mass at every sub-chunk start (sized for the shortest sub-chunk,
+// 16 tokens) and an fp32 copy of dQ.
+struct CausalBwdLayout {
+    int64_t fwd = 0, bwd = 0, apre = 0, dq32 = 0;
+    int64_t total() const { return fwd + bwd + apre + dq32; }
+};
+
+CausalBwdLayout causal_bwd_layout(const Problem& p) {
+    CausalBwdLayout l;
+    l.fwd = p.N * p.tiles * p.rec;
+    l.bwd = p.N * p.tiles * p.rec;
+    l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(p.S));
+    l.dq32 = round64(p.N * p.T * int64_t(p.S));
+    return l;
+}
+
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.f;
@@ -352,6 +369,62 @@ race_status race_noncausal_bwd(const void* probsQ, const void* probsK, const voi
     // dV = K dB: M[a = s][b = c] = dB[s*d + c].
     if (dV) RACE_TRY(launch_token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
     return RACE_SUCCESS;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                            size_t* bytes) {
+    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    // The backward runs the vector-ALU kernels: the non-causal tile policy.
+    const race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(causal_bwd_layout(p).total()) * sizeof(float);
+    return RACE_SUCCESS;
+}
+
+race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* V,
+                            const void* dOut, void* dQ, void* dK, void* dV,
+                            const race_shape* shape, const race_options* opts, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+    Problem p;
+    bool mfma = false;
+    race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (p.N == 0 || p.T == 0 || (!dQ && !dK && !dV)) return RACE_SUCCESS;
+    if (!probsQ || !probsK || !V || !dOut) return RACE_ERROR_INVALID_VALUE;
+    if (!aligned16(probsQ) || !aligned16(probsK) || !aligned16(V) || !aligned16(dOut))
+        return RACE_ERROR_INVALID_VALUE;
+    if ((dQ && !aligned16(dQ)) || (dK && !aligned16(dK)) || (dV && !aligned16(dV)))
+        return RACE_ERROR_INVALID_VALUE;
+    const CausalBwdLayout l = causal_bwd_layout(p);
+    if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
+        return RACE_ERROR_INVALID_VALUE;
+    int lds_limit = 0;
+    RACE_TRY(max_lds(&lds_limit));
+    const int C = causal_bwd_chunk(p.S, p.d, lds_limit);
+    if (C == 0) return RACE_ERROR_INVALID_VALUE;
+    float* fwd_rec = static_cast<float*>(workspace);
+    float* bwd_rec = fwd_rec + l.fwd;
+    float* apre = bwd_rec + l.bwd;
+    float* dq32 = apre + l.apre;
+
+    // Prefix state at every tile start (the forward's tile totals and scan).
+    if (direct_sums_supported(p.S, p.d) && p.tile % 64 == 0)
+        RACE_TRY(launch_tile_sums_direct(probsK, V, fwd_rec, p, stream));
+    else
+        RACE_TRY(launch_tile_outer_sums(probsK, V, fwd_rec, p, p.S, p.d, stream));
+    RACE_TRY(launch_tile_scan(fwd_rec, nullptr, p, stream));
+    RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec, p, C,
+                                  stream));
+    if (!dK && !dV) return RACE_SUCCESS;
+    RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
+    return launch_causal_bwd_dkv(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p, C,
+                                 stream);
 }
 
 }  // extern "C"

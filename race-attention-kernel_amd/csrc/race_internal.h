@@ -70,8 +70,10 @@ struct Marks {
 hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, const Problem& p,
                                   int Wa, int Wb, hipStream_t stream);
 // In-place exclusive scan of the records over tiles (fixed tile order); the
-// inclusive total goes to state ([N][S*d+S]) when it is not null.
-hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream);
+// inclusive total goes to state ([N][S*d+S]) when it is not null.  With
+// `reverse` the scan runs from the last tile to the first.
+hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream,
+                            bool reverse = false);
 // Totals over tiles into `totals` ([N][rec]) and, when not null, into
 // `state` ([N][S*d+S]); E = B / (A + eps) into `E` ([N][S][d]) when not null.
 hipError_t launch_tile_reduce(const float* records, float* totals, float* state, float* E,
@@ -110,6 +112,24 @@ int direct_output_tiles_per_cu();
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel);
 hipError_t launch_causal_output_direct(const void* q, const void* k, const void* v, void* out,
                                        const float* records, const Problem& p, hipStream_t stream);
+
+// ---- causal backward (causal_bwd.hip): fp32 vector-ALU kernels ----
+
+// Sub-chunk length (32 or 16) of the causal backward kernels for (S, d) under
+// `lds_limit_bytes` of LDS per workgroup, or 0 if the state does not fit.
+int causal_bwd_chunk(int S, int d, int lds_limit_bytes);
+// Forward walk: dQ (nullable, caller dtype), dq32 [N][T][S] fp32, apre
+// [N][tiles][tile / C][S] (running mass at every sub-chunk start) and the
+// per-tile suffix totals (Z [S][d], Y [S]) into bwd_records, from the
+// forward's scanned prefix records.
+hipError_t launch_causal_bwd_dq(const void* q, const void* k, const void* v, const void* g,
+                                void* dQ, float* dq32, float* apre, const float* fwd_records,
+                                float* bwd_records, const Problem& p, int C, hipStream_t stream);
+// Backward walk from the suffix state at every tile end: dK, dV (each nullable).
+hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, const void* g,
+                                 const float* dq32, const float* apre,
+                                 const float* suffix_records, void* dK, void* dV, const Problem& p,
+                                 int C, hipStream_t stream);
 
 // Whether the MFMA causal path has a specialization for (S, d).
 bool mfma_causal_supported(int S, int d);

@@ -6,6 +6,8 @@
 //       -> (out, records [N, tiles, rec], state [N, S*d+S], tile_tokens)
 //   noncausal_backward(probsQ, probsK, V, dOut, state, need_q, need_k, need_v,
 //                      tile_tokens=0) -> (dQ or None, dK or None, dV or None)
+//   causal_backward(probsQ, probsK, V, dOut, need_q, need_k, need_v,
+//                   tile_tokens=0) -> (dQ or None, dK or None, dV or None)
 //   select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens=0, kernel=0) -> int
 //   shape_supported(L, R, d) -> (supported, has_mfma)
 //
@@ -175,6 +177,37 @@ noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
     return {opt(need_q, dq), opt(need_k, dk), opt(need_v, dv)};
 }
 
+std::tuple<c10::optional<at::Tensor>, c10::optional<at::Tensor>, c10::optional<at::Tensor>>
+causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                const at::Tensor& grad_out, bool need_q, bool need_k, bool need_v,
+                int64_t tile_tokens) {
+    const race_shape sh = validate(q, k, v);
+    check_token_tensor(grad_out, "dOut", q);
+    TORCH_CHECK(grad_out.sizes() == v.sizes(), "dOut shape ", grad_out.sizes(), " differs from V ",
+                v.sizes());
+    const race_options opts = make_options(tile_tokens, RACE_KERNEL_AUTO);
+    const c10::DeviceGuard guard(q.device());
+    at::Tensor dq, dk, dv;
+    if (need_q) dq = at::empty_like(q);
+    if (need_k) dk = at::empty_like(k);
+    if (need_v) dv = at::empty_like(v);
+    size_t bytes = 0;
+    check_status(race_causal_bwd_workspace_bytes(&sh, &opts, &bytes),
+                 "race_causal_bwd_workspace_bytes");
+    at::Tensor ws = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+    check_status(race_causal_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                                 need_q ? dq.data_ptr() : nullptr, need_k ? dk.data_ptr() : nullptr,
+                                 need_v ? dv.data_ptr() : nullptr, &sh, &opts, ws.data_ptr(), bytes,
+                                 stream),
+                 "race_causal_bwd");
+    auto opt = [](bool need, const at::Tensor& t) -> c10::optional<at::Tensor> {
+        if (need) return t;
+        return c10::nullopt;
+    };
+    return {opt(need_q, dq), opt(need_k, dk), opt(need_v, dv)};
+}
+
 int64_t select_tile_tokens(int64_t N, int64_t T, int64_t L, int64_t R, int64_t d, bool bf16,
                            bool causal, int64_t tile_tokens, int64_t kernel) {
     race_shape sh{N, T, static_cast<int32_t>(L), static_cast<int32_t>(R),
@@ -207,6 +240,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("tile_tokens") = 0, py::arg("kernel") = 0);
     m.def("noncausal_backward", &noncausal_backward, "Non-causal backward -> (dQ, dK, dV)",
           py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("dOut"), py::arg("state"),
+          py::arg("need_q") = true, py::arg("need_k") = true, py::arg("need_v") = true,
+          py::arg("tile_tokens") = 0);
+    m.def("causal_backward", &causal_backward, "Causal backward -> (dQ, dK, dV)",
+          py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("dOut"),
           py::arg("need_q") = true, py::arg("need_k") = true, py::arg("need_v") = true,
           py::arg("tile_tokens") = 0);
     m.def("select_tile_tokens", &select_tile_tokens, "Tile length a forward would use",

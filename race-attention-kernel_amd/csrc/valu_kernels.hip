@@ -110,13 +110,16 @@ __global__ __launch_bounds__(kThreads) void tile_outer_sums_kernel(
 // meet in LDS; each thread then walks its group again writing
 //     prefix(t) = sum of the earlier groups (in group order)
 //               + the earlier tiles of its group (in tile order).
-// Every sum has a fixed order, so the result is bitwise reproducible.
+// Every sum has a fixed order, so the result is bitwise reproducible.  With
+// `reverse` the tiles are scanned from the last to the first (the suffix
+// sums of the causal backward): record t receives the sum over tiles > t.
 constexpr int kScanGroups = 8;
 constexpr int kScanElems = kThreads / kScanGroups;  // 32
 
 __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__ records,
                                                              float* __restrict__ state,
-                                                             int64_t tiles, int64_t rec, int used) {
+                                                             int64_t tiles, int64_t rec, int used,
+                                                             int reverse) {
     __shared__ float gsum[kScanGroups][kScanElems];
     const int el = threadIdx.x % kScanElems, gi = threadIdx.x / kScanElems;
     const int e = blockIdx.x * kScanElems + el;
@@ -124,18 +127,20 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__
     const int64_t per = (tiles + kScanGroups - 1) / kScanGroups;
     const int64_t t_begin = gi * per;
     const int64_t t_end = min(tiles, t_begin + per);
-    float* r = records + n * tiles * rec + e;
+    // Scan position t is record r[t * step].
+    const int64_t step = reverse ? -rec : rec;
+    float* r = records + n * tiles * rec + (reverse ? (tiles - 1) * rec : 0) + e;
     float sum = 0.f;
     if (e < used) {
         int64_t t = t_begin;
         for (; t + 16 <= t_end; t += 16) {
             float v[16];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * rec];
+            for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * step];
 #pragma unroll
             for (int u = 0; u < 16; ++u) sum += v[u];
         }
-        for (; t < t_end; ++t) sum += r[t * rec];
+        for (; t < t_end; ++t) sum += r[t * step];
     }
     gsum[gi][el] = sum;
     __syncthreads();
@@ -146,16 +151,16 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__
     for (; t + 16 <= t_end; t += 16) {
         float v[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * rec];
+        for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * step];
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
-            r[(t + u) * rec] = run;
+            r[(t + u) * step] = run;
             run += v[u];
         }
     }
     for (; t < t_end; ++t) {
-        const float v = r[t * rec];
-        r[t * rec] = run;
+        const float v = r[t * step];
+        r[t * step] = run;
         run += v;
     }
     if (state && gi == kScanGroups - 1) state[n * used + e] = run;
@@ -401,10 +406,12 @@ hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, 
     return hipGetLastError();
 }
 
-hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream) {
+hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream,
+                            bool reverse) {
     const int used = p.S * p.d + p.S;
     const dim3 grid(unsigned((used + kScanElems - 1) / kScanElems), unsigned(p.N));
-    tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.tiles, p.rec, used);
+    tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.tiles, p.rec, used,
+                                                    reverse ? 1 : 0);
     return hipGetLastError();
 }
 

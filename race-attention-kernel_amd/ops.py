@@ -12,10 +12,12 @@ analysis/hot-path.md:157-162).  The 5-D prefix tensors of the reference never
 exist: the HIP kernels carry the per-bucket state on chip.
 
 The autograd wrapper follows the reference's non-causal op
-(src/noncausal/ops.py:20-63): it saves the inputs plus the small per-bucket
-state, is once_differentiable, makes the incoming gradient dense and returns
-only the gradients autograd asks for.  The causal backward does not exist in
-the reference either and raises.
+(src/noncausal/ops.py:20-63): it saves the inputs (plus, non-causal, the
+small per-bucket state), is once_differentiable, makes the incoming gradient
+dense and returns only the gradients autograd asks for.  The causal backward
+has no counterpart in the reference (its design outline is
+docs/causal_v2_design.md:689-742); here it recomputes the forward's prefix
+states from the saved inputs, so nothing O(T*S*d) is kept.
 """
 from __future__ import annotations
 
@@ -54,20 +56,25 @@ class RaceFusedFunction(torch.autograd.Function):
                                         int(kernel), want_state)
         ctx.causal = bool(causal)
         ctx.tile_tokens = int(tile_tokens)
-        if want_state:
-            ctx.save_for_backward(probsQ, probsK, V, state)
+        if needs:
+            if causal:
+                ctx.save_for_backward(probsQ, probsK, V)
+            else:
+                ctx.save_for_backward(probsQ, probsK, V, state)
         return out
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_out):
-        if ctx.causal:
-            raise RuntimeError(
-                "race_fused_fwd: the causal backward is not implemented (the reference has none "
-                "either); only causal=False is differentiable")
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
         if not (need_q or need_k or need_v):
             return None, None, None, None, None, None
+        if ctx.causal:
+            q, k, v = ctx.saved_tensors
+            grad_out = _dense(grad_out.to(v.dtype))
+            dq, dk, dv = _lib.ext().causal_backward(q, k, v, grad_out, need_q, need_k, need_v,
+                                                   0)
+            return dq, dk, dv, None, None, None
         q, k, v, state = ctx.saved_tensors
         grad_out = _dense(grad_out.to(v.dtype))
         dq, dk, dv = _lib.ext().noncausal_backward(q, k, v, grad_out, state, need_q, need_k,
@@ -108,6 +115,12 @@ def race_noncausal_backward(probsQ, probsK, V, dOut, state, *, need=(True, True,
     """(dQ, dK, dV) of the non-causal forward for upstream gradient dOut."""
     return _lib.ext().noncausal_backward(probsQ, probsK, V, _dense(dOut), state, *need,
                                          tile_tokens)
+
+
+def race_causal_backward(probsQ, probsK, V, dOut, *, need=(True, True, True),
+                         tile_tokens: int = 0):
+    """(dQ, dK, dV) of the causal forward for upstream gradient dOut."""
+    return _lib.ext().causal_backward(probsQ, probsK, V, _dense(dOut), *need, tile_tokens)
 
 
 def select_tile_tokens(N: int, T: int, L: int, R: int, d: int, *, bf16: bool = False,

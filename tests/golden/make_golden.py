@@ -8,10 +8,10 @@ from the definition of the reference's hot span (src/race_baseline.py:45-51):
                 out_t[c] = sum_s q_t[s] * B_t[s][c] / (A_t[s] + eps)
     non-causal: the same with sums over all T (analysis/hot-path.md:157-162)
 
-with eps the double nearest 1e-6.  Gradients of the non-causal case are
-computed by forward-mode differentiation with exact dual numbers (one pass
-per input element), so they do not share a derivation with the closed-form
-VJP the oracle and the kernels use.
+with eps the double nearest 1e-6.  Gradients of the non-causal and causal
+cases are computed by forward-mode differentiation with exact dual numbers
+(one pass per input element), so they do not share a derivation with the
+closed-form VJPs the oracle and the kernels use.
 
 Run: python tests/golden/make_golden.py  (seconds; deterministic)
 """
@@ -112,7 +112,7 @@ def forward_case(q, k, v, causal):
     return out
 
 
-def noncausal_grads(q, k, v, g):
+def exact_grads(q, k, v, g, causal):
     """Exact d/d(inputs) of sum(g * out) for one stream, by forward-mode duals."""
     T, S = q.shape
     d = v.shape[1]
@@ -123,7 +123,7 @@ def noncausal_grads(q, k, v, g):
                 for i, row in enumerate(arr)]
 
     def loss(qq, kk, vv):
-        o = exact_forward(qq, kk, vv, False)
+        o = exact_forward(qq, kk, vv, causal)
         acc = Dual(Fraction(0))
         for t in range(T):
             for c in range(d):
@@ -160,9 +160,17 @@ def main():
     # Non-causal gradients, one stream.
     q, k, v = case(rng, 1, 6, 2, 2, 3)
     g = rng.standard_normal((1, 6, 3)).astype(np.float32)
-    dq, dk, dv = noncausal_grads(q[0], k[0], v[0], g[0])
+    dq, dk, dv = exact_grads(q[0], k[0], v[0], g[0], causal=False)
     data.update(grad_q=q, grad_k=k, grad_v=v, grad_g=g, grad_dq=dq[None], grad_dk=dk[None],
                 grad_dv=dv[None], grad_out=forward_case(q, k, v, False))
+    # Causal gradients, one stream each (appended last so the cases above keep
+    # their random draws).
+    for name, T, L, R, d in [("cgrad", 7, 2, 2, 3), ("cgrad_wide", 5, 2, 4, 2)]:
+        q, k, v = case(rng, 1, T, L, R, d)
+        g = rng.standard_normal((1, T, d)).astype(np.float32)
+        dq, dk, dv = exact_grads(q[0], k[0], v[0], g[0], causal=True)
+        data.update({f"{name}_q": q, f"{name}_k": k, f"{name}_v": v, f"{name}_g": g,
+                     f"{name}_dq": dq[None], f"{name}_dk": dk[None], f"{name}_dv": dv[None]})
     np.savez(OUT, **data)
     print(f"wrote {OUT} ({len(data)} arrays)")
 

@@ -74,6 +74,11 @@ def test_workspace_bytes_for_explicit_tiles(race):
     assert st == 0 and nc_bytes == (8 * 64 * 4160 + 8 * 4160 + 8 * 64 * 64) * 4
     st, bwd_bytes = abi.noncausal_bwd_workspace_bytes(sh, abi.options(1024, 0))
     assert st == 0 and bwd_bytes > nc_bytes
+    # Causal backward: forward and suffix records, the running mass per 16
+    # tokens and an fp32 copy of dQ.
+    st, cb_bytes = abi.causal_bwd_workspace_bytes(sh, abi.options(1024, 0))
+    assert st == 0
+    assert cb_bytes == (2 * 8 * 64 * 4160 + 8 * 64 * (1024 // 16) * 64 + 8 * 65536 * 64) * 4
 
 
 def test_scratch_per_token_is_constant(race):
@@ -118,6 +123,17 @@ def test_invalid_arguments_are_rejected_before_any_launch(race):
     # Backward needs the state and dOut.
     assert abi.noncausal_bwd(16, 16, 16, 0, 0, 16, 16, 16, good, opts, 64, 1 << 30, 0) == \
         abi.RACE_ERROR_INVALID_VALUE
+    # Causal backward: dOut, aligned outputs and a large enough workspace; no
+    # MFMA kernel.
+    inv = abi.RACE_ERROR_INVALID_VALUE
+    assert abi.causal_bwd(16, 16, 16, 0, 16, 16, 16, good, opts, 64, 1 << 30, 0) == inv
+    assert abi.causal_bwd(16, 16, 16, 16, 16, 24, 16, good, opts, 64, 1 << 30, 0) == inv
+    assert abi.causal_bwd(16, 16, 16, 16, 16, 16, 16, good, opts, 64, 64, 0) == inv
+    assert abi.causal_bwd(16, 16, 16, 16, 16, 16, 16, good, abi.options(64, abi.RACE_KERNEL_MFMA),
+                          64, 1 << 30, 0) == inv
+    # Nothing requested, or nothing to do: success without a launch.
+    assert abi.causal_bwd(0, 0, 0, 0, None, None, None, good, opts, None, 0, 0) == 0
+    assert abi.causal_bwd(0, 0, 0, 0, 16, 16, 16, abi.shape(8, 0, 4, 16, 64), opts, None, 0, 0) == 0
 
 
 def test_torch_binding_validates_inputs_on_the_host(race, ext):

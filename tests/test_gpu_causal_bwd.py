@@ -1,0 +1,167 @@
+"""GPU parity of the causal backward against the CPU oracle.
+
+The reference has no causal backward (its design outline is
+docs/causal_v2_design.md:689-742); the oracle is the closed-form VJP of
+oracle/race_oracle.c, itself pinned to exact dual-number gradients and to
+torch.autograd through the reference's cumsum composition
+(tests/test_oracle.py).  Gradients are checked here through autograd on
+race_fused_fwd(causal=True), against:
+  - the oracle on a grid of shapes, ragged T and both dtypes,
+  - the exact golden gradients (tests/golden/race_golden.npz),
+  - torch.autograd on the reference formula in fp64,
+with the properties of the non-causal suite: bitwise reproducibility,
+needs_input_grad filtering, independence from the tile length.
+"""
+from __future__ import annotations
+
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import FP32_TOL, per_stream_rel_err, say, to_np, tol_for
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden" / "race_golden.npz"
+
+
+def forward_backward(race, q, k, v, g, cuda):
+    qg, kg, vg = (x.to(cuda).requires_grad_(True) for x in (q, k, v))
+    out = race.race_fused_fwd(qg, kg, vg, causal=True)
+    out.backward(g.to(cuda))
+    torch.cuda.synchronize()
+    return out.detach(), qg.grad, kg.grad, vg.grad
+
+
+def dk_term_scale(q, k, v, g, eps=1e-6):
+    """Per-stream max over (t, s) of the magnitude of the terms whose sum is
+    dK: sum_c |Z_t[s][c]| |v_t[c]| + |Y|_t[s] with |Z|, |Y| the suffix sums of
+    |W| (x) |g| and |alpha|.  Where they cancel (T = 1 gives dK = <v, g> q
+    eps / (k + eps)^2, ~1e-6 of each term) fp32 is only accurate relative to
+    this, so dK's error is bounded by tol * this scale."""
+    q, k, v, g = (np.asarray(x, np.float64) for x in (q, k, v, g))
+    a = np.cumsum(k, 1)
+    b = np.cumsum(k[..., :, None] * v[..., None, :], 1)
+    r = 1.0 / (a + eps)
+    w = q * r
+    alpha = w * r * np.abs(np.einsum("ntsc,ntc->nts", b, g))
+    zabs = np.cumsum((np.abs(w)[..., :, None] * np.abs(g)[..., None, :])[:, ::-1], 1)[:, ::-1]
+    yabs = np.cumsum(alpha[:, ::-1], 1)[:, ::-1]
+    terms = np.einsum("ntsc,ntc->nts", zabs, np.abs(v)) + yabs
+    return terms.reshape(terms.shape[0], -1).max(1)
+
+
+def check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol, dk_scale=True):
+    qn, kn, vn, gn = (to_np(x) for x in (q, k, v, g))
+    rq, rk, rv = oracle.causal_bwd(qn, kn, vn, gn, nthreads=16)
+    assert per_stream_rel_err(to_np(out), oracle.causal_recurrence(qn, kn, vn, nthreads=16)) <= tol
+    eq = per_stream_rel_err(to_np(dq), rq)
+    ev = per_stream_rel_err(to_np(dv), rv)
+    if dk_scale:
+        scale = dk_term_scale(qn, kn, vn, gn)
+        n = qn.shape[0]
+        ek = float((np.abs(to_np(dk).astype(np.float64) - rk).reshape(n, -1).max(1) / scale).max())
+    else:
+        ek = per_stream_rel_err(to_np(dk), rk)
+    say("errors", f"dQ {eq:.2e} dK {ek:.2e} dV {ev:.2e}")
+    assert eq <= tol, ("dQ", eq)
+    assert ek <= tol, ("dK", ek)
+    assert ev <= tol, ("dV", ev)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("L, R, d", [(1, 1, 1), (2, 8, 32), (4, 16, 64), (3, 5, 7), (8, 32, 64),
+                                     (4, 32, 128)])
+@pytest.mark.parametrize("T", [1, 63, 65, 700])
+def test_shapes(race, oracle, cuda, dtype, L, R, d, T):
+    say("c-bwd-shape", dtype, L, R, d, T)
+    q, k, v, g = race.make_inputs(3, T, L, R, d, seed=T + d + 1, dtype=dtype, grad_out=True)
+    out, dq, dk, dv = forward_backward(race, q, k, v, g, cuda)
+    assert dq.dtype == dtype and dk.dtype == dtype and dv.dtype == dtype
+    check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol_for(dtype))
+
+
+def test_cfg2_shape_long_sequence(race, oracle, cuda):
+    # The cfg2 shape (N = 8, S = 64, d = 64, fp32) at T = 16384: 32 tiles per
+    # stream, so the suffix scan crosses many tile boundaries.
+    say("c-bwd cfg2 T=16384")
+    q, k, v, g = race.make_inputs(8, 16384, 4, 16, 64, seed=21, grad_out=True)
+    out, dq, dk, dv = forward_backward(race, q, k, v, g, cuda)
+    check_grads(oracle, q, k, v, g, out, dq, dk, dv, FP32_TOL, dk_scale=False)
+
+
+@pytest.mark.parametrize("tile", [64, 128, 1024])
+def test_tile_lengths(race, oracle, cuda, tile):
+    say("c-bwd tile", tile)
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, 1500, 4, 16, 64, seed=22, grad_out=True))
+    dq, dk, dv = race.race_causal_backward(q, k, v, g, tile_tokens=tile)
+    out = race.race_fused_fwd(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    check_grads(oracle, q, k, v, g, out, dq, dk, dv, FP32_TOL)
+
+
+@pytest.mark.parametrize("name", ["cgrad", "cgrad_wide"])
+def test_golden_gradients(race, cuda, name):
+    say("c-bwd golden", name)
+    gd = np.load(GOLDEN)
+    q, k, v, g = (torch.from_numpy(gd[f"{name}_{x}"]) for x in "qkvg")
+    _, dq, dk, dv = forward_backward(race, q, k, v, g, cuda)
+    assert per_stream_rel_err(to_np(dq), gd[f"{name}_dq"]) <= 1e-5
+    assert per_stream_rel_err(to_np(dk), gd[f"{name}_dk"]) <= 1e-5
+    assert per_stream_rel_err(to_np(dv), gd[f"{name}_dv"]) <= 1e-5
+
+
+def test_matches_torch_autograd(race, oracle, cuda):
+    say("c-bwd autograd")
+    q, k, v, g = race.make_inputs(4, 300, 4, 16, 64, seed=23, grad_out=True)
+    out, dq, dk, dv = forward_backward(race, q, k, v, g, cuda)
+    a_out, aq, ak, av = oracle.torch_causal_autograd(to_np(q), to_np(k), to_np(v), to_np(g))
+    for got, want in ((out, a_out), (dq, aq), (dk, ak), (dv, av)):
+        assert per_stream_rel_err(to_np(got), want) <= FP32_TOL
+
+
+@pytest.mark.parametrize("need", [(True, False, False), (False, True, False), (False, False, True),
+                                  (False, True, True)])
+def test_only_requested_gradients(race, cuda, need):
+    say("c-bwd needs-grad", need)
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, 500, 4, 16, 64, seed=24, grad_out=True))
+    leaves = [x.clone().requires_grad_(n) for x, n in zip((q, k, v), need)]
+    race.race_fused_fwd(*leaves, causal=True).backward(g)
+    _, fq, fk, fv = forward_backward(race, q, k, v, g, cuda)
+    for leaf, n, full in zip(leaves, need, (fq, fk, fv)):
+        if n:
+            assert torch.equal(leaf.grad, full)
+        else:
+            assert leaf.grad is None
+
+
+def test_bitwise_reproducible(race, cuda):
+    say("c-bwd bitwise")
+    q, k, v, g = race.make_inputs(5, 3000, 4, 16, 64, seed=25, grad_out=True)
+    first = forward_backward(race, q, k, v, g, cuda)
+    for _ in range(2):
+        again = forward_backward(race, q, k, v, g, cuda)
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
+
+
+def test_future_gradients_do_not_reach_past_queries(race, cuda):
+    # dQ at token t depends on dOut at t only: zeroing dOut after t leaves
+    # dQ[:t] bitwise unchanged.
+    say("c-bwd dq locality")
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, 900, 4, 16, 64, seed=26, grad_out=True))
+    g2 = g.clone()
+    g2[:, 600:] = 0
+    dq1, _, _ = race.race_causal_backward(q, k, v, g, need=(True, False, False))
+    dq2, _, _ = race.race_causal_backward(q, k, v, g2, need=(True, False, False))
+    torch.cuda.synchronize()
+    assert torch.equal(dq1[:, :600], dq2[:, :600])
+
+
+def test_unsupported_shape_raises(race, cuda):
+    # S = 256, d = 128: the per-bucket state does not fit one workgroup's LDS.
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 64, 8, 32, 128, seed=27, grad_out=True))
+    with pytest.raises(RuntimeError, match="race_causal_bwd"):
+        race.race_causal_backward(q, k, v, g)

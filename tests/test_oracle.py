@@ -156,6 +156,64 @@ def test_noncausal_backward_gradcheck():
                                     (q, k, v))
 
 
+@pytest.mark.parametrize("name", ["cgrad", "cgrad_wide"])
+def test_causal_backward_matches_exact_dual_number_gradients(oracle, golden, name):
+    q, k, v, g = (golden[f"{name}_{x}"] for x in "qkvg")
+    dq, dk, dv = oracle.causal_bwd(q, k, v, g)
+    assert rel_err(dq, golden[f"{name}_dq"]) <= FP64_TOL
+    assert rel_err(dk, golden[f"{name}_dk"]) <= FP64_TOL
+    assert rel_err(dv, golden[f"{name}_dv"]) <= FP64_TOL
+
+
+@pytest.mark.parametrize("N,T,L,R,d", [(2, 150, 2, 8, 16), (1, 1, 4, 16, 8), (3, 33, 1, 1, 2)])
+def test_causal_backward_closed_form_equals_autograd(oracle, N, T, L, R, d):
+    q, k, v = inputs(30 + T, N, T, L, R, d)
+    g = np.random.default_rng(31).standard_normal((N, T, d)).astype(np.float32)
+    dq, dk, dv = oracle.causal_bwd(q, k, v, g)
+    out, aq, ak, av = oracle.torch_causal_autograd(q, k, v, g)
+    assert rel_err(out, oracle.causal_recurrence(q, k, v)) <= FP64_TOL
+    assert rel_err(dq, aq) <= 1e-11 and rel_err(dk, ak) <= 1e-11 and rel_err(dv, av) <= 1e-11
+
+
+def test_causal_backward_gradcheck():
+    import torch
+
+    torch.manual_seed(1)
+    q = torch.rand(1, 6, 4, dtype=torch.float64, requires_grad=True)
+    k = torch.rand(1, 6, 4, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(1, 6, 3, dtype=torch.float64, requires_grad=True)
+    import __graft_entry__ as entry
+
+    oracle = entry.load_oracle()
+    assert torch.autograd.gradcheck(lambda a, b, c: oracle.torch_causal_reference(a, b, c, eps=1e-3),
+                                    (q, k, v))
+
+
+def test_causal_backward_single_token_closed_form(oracle):
+    # T = 1: out = v * sum_s q_s k_s / (k_s + eps), so
+    #   dq_s = <v, g> k_s / (k_s + eps),  dk_s = <v, g> q_s eps / (k_s + eps)^2,
+    #   dv   = g * sum_s q_s k_s / (k_s + eps).
+    q, k, v = inputs(32, 2, 1, 4, 16, 8)
+    g = np.random.default_rng(33).standard_normal((2, 1, 8)).astype(np.float32)
+    q0, k0, v0, g0 = (x[:, 0].astype(np.float64) for x in (q, k, v, g))
+    vg = (v0 * g0).sum(-1, keepdims=True)
+    dq, dk, dv = oracle.causal_bwd(q, k, v, g)
+    assert rel_err(dq[:, 0], vg * k0 / (k0 + 1e-6)) <= FP64_TOL
+    assert rel_err(dk[:, 0], vg * q0 * 1e-6 / (k0 + 1e-6) ** 2) <= 1e-9
+    assert rel_err(dv[:, 0], g0 * (q0 * k0 / (k0 + 1e-6)).sum(-1, keepdims=True)) <= FP64_TOL
+
+
+def test_causal_backward_last_token_matches_noncausal(oracle):
+    # The gradient w.r.t. the last query only sees the totals: dq_{T-1} of the
+    # causal function equals dq_{T-1} of the non-causal one.
+    q, k, v = inputs(34, 2, 40, 2, 8, 4)
+    g = np.zeros((2, 40, 4), np.float32)
+    g[:, -1] = np.random.default_rng(35).standard_normal((2, 4)).astype(np.float32)
+    cq, ck, cv = oracle.causal_bwd(q, k, v, g)
+    nq, nk, nv = oracle.noncausal_bwd(q, k, v, g)
+    assert rel_err(cq, nq) <= FP64_TOL and rel_err(ck, nk) <= 1e-11 and rel_err(cv, nv) <= FP64_TOL
+
+
 # --- closed forms ---------------------------------------------------------------------------
 
 def test_single_token_closed_form(oracle):
@@ -263,3 +321,35 @@ def test_planted_mistakes_are_caught(oracle, golden):
     # Carry dropped at chunk boundaries: the recurrence/chunk agreement fails.
     q2, k2, v2 = inputs(16, 1, 64, 4, 16, 8)
     assert rel_err(_mutant(q2, k2, v2, drop_carry=True), oracle.causal_recurrence(q2, k2, v2)) > 1e-3
+
+
+def _mutant_bwd(q, k, v, g, *, exclusive_suffix=False, drop_alpha=False):
+    """A numpy causal backward with one plausible mistake switched on."""
+    q, k, v, g = (np.asarray(x, np.float64) for x in (q, k, v, g))
+    a = np.cumsum(k, 1)
+    b = np.cumsum(k[..., :, None] * v[..., None, :], 1)
+    r = 1.0 / (a + 1e-6)
+    dq = r * np.einsum("ntsc,ntc->nts", b, g)
+    w = q * r
+    alpha = np.zeros_like(dq) if drop_alpha else -w * dq
+    wg = w[..., :, None] * g[..., None, :]
+    z = np.cumsum(wg[:, ::-1], 1)[:, ::-1]
+    y = np.cumsum(alpha[:, ::-1], 1)[:, ::-1]
+    if exclusive_suffix:
+        z, y = z - wg, y - alpha
+    dk = np.einsum("ntsc,ntc->nts", z, v) + y
+    dv = np.einsum("nts,ntsc->ntc", k, z)
+    return dq, dk, dv
+
+
+def test_planted_backward_mistakes_are_caught(golden):
+    q, k, v, g = (golden[f"cgrad_{x}"] for x in "qkvg")
+    want = [golden[f"cgrad_{x}"] for x in ("dq", "dk", "dv")]
+    got = _mutant_bwd(q, k, v, g)
+    assert all(rel_err(a, b) <= FP64_TOL for a, b in zip(got, want))
+    # Suffix sums that skip the diagonal token: dk and dv fail.
+    got = _mutant_bwd(q, k, v, g, exclusive_suffix=True)
+    assert rel_err(got[1], want[1]) > 1e-3 and rel_err(got[2], want[2]) > 1e-3
+    # The denominator's gradient dropped: dk fails.
+    got = _mutant_bwd(q, k, v, g, drop_alpha=True)
+    assert rel_err(got[1], want[1]) > 1e-3
