@@ -30,9 +30,13 @@ this host's cores on the bench workload itself (cfg2: N = 8, T = 65536; a
 shorter T when the host has too little free memory for its 5-D tensors):
 1 warmup, median of 3.
 
+Other workloads and passes (--workload, --pass bwd|fwdbwd) print the same
+line for that configuration; the CPU baseline belongs to the headline
+(cfg2 forward) only.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
-                       [--T T] [--kernel auto|valu|mfma|mfma_wg] [--tile N] [--no-cpu-baseline]
-                       [--calibrate-copy MIB]
+                       [--pass fwd|bwd|fwdbwd] [--T T] [--kernel auto|valu|mfma|mfma_wg]
+                       [--tile N] [--no-cpu-baseline] [--calibrate-copy MIB]
 """
 from __future__ import annotations
 
@@ -70,6 +74,12 @@ PHASES = {
     (True, "valu"): ["tile_sums", "tile_scan", "output_pass_valu"],
     (False, "valu"): ["tile_sums", "tile_reduce", "token_map"],
     (True, "mfma"): ["tile_sums_mfma", "tile_scan", "output_pass_mfma"],
+}
+# Backward launch sequences (every gradient requested).
+BWD_PHASES = {
+    True: ["bwd_tile_sums", "tile_scan", "bwd_dq", "suffix_scan", "bwd_dkv"],
+    False: ["state_to_E", "token_map_dq", "tile_sums_dE", "tile_reduce_dE", "bwd_finalize",
+            "token_map_dk", "token_map_dv"],
 }
 
 
@@ -120,6 +130,9 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
+    ap.add_argument("--pass", dest="pass_", choices=["fwd", "bwd", "fwdbwd"], default="fwd",
+                    help="what one step runs: the forward (default), the backward (from the "
+                         "forward's inputs and a synthetic dOut) or both")
     ap.add_argument("--T", type=int, default=0)
     ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
@@ -134,6 +147,7 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
     NT = cfg.N * T
     S, d = cfg.S, cfg.d
     state = 4.0 * cfg.N * tiles * rec
+    small = 4.0 * cfg.N * (S * d + S) * 3
     return {
         "tile_sums": es * (S + d) * NT,
         "tile_sums_mfma": es * (S + d) * NT,
@@ -142,7 +156,27 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
         "output_pass_valu": es * (2 * S + 2 * d) * NT,
         "output_pass_mfma": es * (2 * S + 2 * d) * NT,
         "token_map": es * (S + d) * NT,
+        # backward: each launch's own operands (reads) and outputs (writes)
+        "bwd_tile_sums": es * (S + d) * NT,
+        "bwd_dq": es * (3 * S + 2 * d) * NT,       # q, k, v, dOut -> dQ
+        "suffix_scan": 2 * state,
+        "bwd_dkv": es * (3 * S + 3 * d) * NT,      # q, k, v, dOut -> dK, dV
+        "state_to_E": small,
+        "token_map_dq": es * (d + S) * NT,
+        "tile_sums_dE": es * (S + d) * NT,
+        "tile_reduce_dE": state,
+        "bwd_finalize": small,
+        "token_map_dk": es * (d + S) * NT,
+        "token_map_dv": es * (S + d) * NT,
     }.get(name, es * (2 * S + 2 * d) * NT)
+
+
+def op_bytes(pass_: str, cfg, T: int, es: int) -> float:
+    """Algorithmic bytes of one step: the forward reads Q, K, V and writes out;
+    the backward reads Q, K, V, dOut and writes dQ, dK, dV."""
+    S, d, NT = cfg.S, cfg.d, cfg.N * T
+    fwd, bwd = es * (2 * S + 2 * d) * NT, es * (4 * S + 3 * d) * NT
+    return {"fwd": fwd, "bwd": bwd, "fwdbwd": fwd + bwd}[pass_]
 
 
 def traffic_for(workload_key: str, kernel_name: str):
@@ -238,6 +272,67 @@ def main() -> int:
     stream = torch.cuda.current_stream().cuda_stream
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
 
+    def check(st_):
+        if st_ != 0:
+            raise RuntimeError(abi.status_string(st_))
+
+    # One step of the chosen pass: plain(), and profiled(events) -> events used.
+    run_fwd = args.pass_ in ("fwd", "fwdbwd")
+    run_bwd = args.pass_ in ("bwd", "fwdbwd")
+    state = None
+    if run_bwd:
+        g = torch.randn(v.shape, device=dev, dtype=torch.float32,
+                        generator=torch.Generator(device=dev).manual_seed(7)).to(v.dtype)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        bptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr())
+        gptrs = (dq.data_ptr(), dk.data_ptr(), dv.data_ptr())
+        bopts = abi.options(0, 0)
+        if cfg.causal:
+            st, bws_bytes = abi.causal_bwd_workspace_bytes(sh, bopts)
+        else:
+            st, bws_bytes = abi.noncausal_bwd_workspace_bytes(sh, bopts)
+            state = torch.empty(cfg.N * (cfg.S * cfg.d + cfg.S), device=dev, dtype=torch.float32)
+        check(st)
+        bws = torch.empty(max(bws_bytes // 4, 1), device=dev, dtype=torch.float32)
+        if state is not None:  # the non-causal backward consumes the forward's state
+            check(abi.fwd(*ptrs, state.data_ptr(), sh, False, opts, ws.data_ptr(), ws_bytes, stream))
+    sptr = state.data_ptr() if state is not None else None
+
+    def plain():
+        if run_fwd:
+            check(abi.fwd(*ptrs, sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
+        if run_bwd:
+            if cfg.causal:
+                check(abi.causal_bwd(*bptrs, *gptrs, sh, bopts, bws.data_ptr(), bws_bytes, stream))
+            else:
+                check(abi.noncausal_bwd(*bptrs, sptr, *gptrs, sh, bopts, bws.data_ptr(), bws_bytes,
+                                        stream))
+
+    def profiled(evs):
+        n_used = 0
+        if run_fwd:
+            st_, n = abi.fwd_profiled(*ptrs, sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
+                                      stream, evs)
+            check(st_)
+            n_used = n
+        if run_bwd:
+            tail = (ctypes.c_void_p * (len(evs) - n_used)).from_buffer(evs, n_used * ctypes.sizeof(ctypes.c_void_p))
+            if cfg.causal:
+                st_, n = abi.causal_bwd_profiled(*bptrs, *gptrs, sh, bopts, bws.data_ptr(), bws_bytes,
+                                                 stream, tail)
+            else:
+                st_, n = abi.noncausal_bwd_profiled(*bptrs, sptr, *gptrs, sh, bopts, bws.data_ptr(),
+                                                    bws_bytes, stream, tail)
+            check(st_)
+            n_used += n
+        return n_used
+
+    names = []
+    if run_fwd:
+        names += PHASES.get((cfg.causal, family), [])
+    if run_bwd:
+        names += BWD_PHASES[cfg.causal]
+
     if args.calibrate_copy:
         # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE counters give
         # the scale of those counters on this device.
@@ -248,46 +343,45 @@ def main() -> int:
         del src, dst
 
     events = HipEvents()
-    max_launches = 8
-    per_step = [events.array(max_launches + 1) for _ in range(args.steps)]
-    warm = events.array(max_launches + 1)
-
-    def check(st):
-        if st != 0:
-            raise RuntimeError(abi.status_string(st))
+    max_launches = 16
+    per_step = [events.array(max_launches + 2) for _ in range(args.steps)]
+    warm = events.array(max_launches + 2)
 
     for _ in range(args.warmup):
-        check(abi.fwd(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
-        check(abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream,
-                               warm)[0])
+        plain()
+        profiled(warm)
     torch.cuda.synchronize()
 
-    # Timed region 1 (`value`): K plain race_fwd steps, back to back on one
-    # stream, between two events.
+    # Timed region 1 (`value`): K plain steps, back to back on one stream,
+    # between two events.
     bracket = events.array(2)
     t0 = time.perf_counter()
     events.record(bracket[0], stream)
     for _ in range(args.steps):
-        check(abi.fwd(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
+        plain()
     events.record(bracket[1], stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
 
-    # Timed region 2 (per-kernel durations): K race_fwd_profiled steps, which
-    # put an event before the first launch and after every launch.
+    # Timed region 2 (per-kernel durations): K profiled steps, which put an
+    # event before the first launch and after every launch.
     n_events = 0
     for i in range(args.steps):
-        st, n_events = abi.fwd_profiled(*ptrs, None, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
-                                        stream, per_step[i])
-        check(st)
+        n_events = profiled(per_step[i])
     torch.cuda.synchronize()
 
     profiled_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1]) / args.steps
-    n_launch = n_events - 1
-    phase_ms = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step)
-                for j in range(n_launch)]
-    names = PHASES.get((cfg.causal, family), [f"kernel{j}" for j in range(n_launch)])
+    # Intervals between consecutive events; the forward's last event and the
+    # backward's first one bracket nothing and are dropped below.
+    n_gaps = n_events - 1
+    gaps = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step)
+            for j in range(n_gaps)]
+    n_fwd = len(PHASES.get((cfg.causal, family), [])) if run_fwd else 0
+    if run_fwd and run_bwd:
+        gaps = gaps[:n_fwd] + gaps[n_fwd + 1:]
+    n_launch = len(gaps)
+    phase_ms = gaps
     if len(names) != n_launch:
         names = [f"kernel{j}" for j in range(n_launch)]
     dom = max(range(n_launch), key=lambda j: phase_ms[j])
@@ -298,10 +392,14 @@ def main() -> int:
 
     NT = cfg.N * T
     value = NT / (ms_per_step * 1e-3) / 1e6
+    headline = args.workload == "cfg2" and args.pass_ == "fwd"
+    metric = METRIC if headline else (
+        f"{'causal' if cfg.causal else 'non-causal'} {args.pass_} M tokens/s at N={cfg.N},"
+        f"S={cfg.S},d_k={cfg.d},T={T} on 1 GPU")
     total_mem = torch.cuda.get_device_properties(dev).total_memory
     bytes_per_token = peak_bytes / T
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 3),
         "unit": UNIT,
         "n_gpus": 1,
@@ -311,13 +409,14 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": (round(value / REFERENCE_MTOKS_T65536, 2)
-                        if (args.workload == "cfg2" and T == 65536) else None),
+                        if (headline and T == 65536) else None),
         "dtype": "bf16" if es == 2 else "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.workload}: {'causal' if cfg.causal else 'non-causal'} fwd N={cfg.N} "
+            "workload": f"{args.workload}: {'causal' if cfg.causal else 'non-causal'} {args.pass_} N={cfg.N} "
                         f"L={cfg.L} R={cfg.R} d={cfg.d} T={T} {'bf16' if es == 2 else 'fp32'}",
             "N": cfg.N, "T": T, "L": cfg.L, "R": cfg.R, "d": cfg.d, "causal": cfg.causal,
+            "pass": args.pass_,
             "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch,
             "kernel_ms": {names[j]: round(phase_ms[j], 5) for j in range(n_launch)},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
@@ -325,7 +424,7 @@ def main() -> int:
             "peak_hbm_bytes_per_token": round(bytes_per_token, 1),
             "workspace_bytes_per_token": round(ws_bytes / T, 2),
             "max_T_fits_est": int(0.95 * total_mem / bytes_per_token),
-            "alg_bytes_per_stream_token": es * (2 * cfg.S + 2 * cfg.d),
+            "alg_bytes_per_stream_token": op_bytes(args.pass_, cfg, 1, es) / cfg.N,
         },
         "roofline": {
             "bound": "hbm",
@@ -334,16 +433,19 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": traffic_for(args.workload, names[dom]),
+            "traffic": traffic_for(args.workload if args.pass_ == "fwd" else
+                                   f"{args.workload}/{args.pass_}", names[dom]),
             "alg_bytes_per_launch": int(dom_bytes),
-            "whole_op_frac": round(es * (2 * cfg.S + 2 * cfg.d) * NT / (ms_per_step * 1e-3) / 1e9
+            "whole_op_frac": round(op_bytes(args.pass_, cfg, T, es) / (ms_per_step * 1e-3) / 1e9
                                    / PEAK_HBM_GBPS, 4),
         },
         "cpu_baseline": None,
     }
     del q, k, v, out, ws
+    if run_bwd:
+        del g, dq, dk, dv, bws
     torch.cuda.empty_cache()
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and headline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
     return 0

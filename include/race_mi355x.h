@@ -191,6 +191,21 @@ race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* 
                             const race_shape* shape, const race_options* opts, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* race_noncausal_bwd / race_causal_bwd with a hipEventRecord on `stream`
+ * before the first launch and after every launch, as race_fwd_profiled does.
+ * Profiling aids with no counterpart in the reference (used by bench.py). */
+race_status race_noncausal_bwd_profiled(const void* probsQ, const void* probsK, const void* V,
+                                        const void* dOut, const float* state, void* dQ, void* dK,
+                                        void* dV, const race_shape* shape,
+                                        const race_options* opts, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream,
+                                        hipEvent_t* events, int32_t max_events, int32_t* n_events);
+race_status race_causal_bwd_profiled(const void* probsQ, const void* probsK, const void* V,
+                                     const void* dOut, void* dQ, void* dK, void* dV,
+                                     const race_shape* shape, const race_options* opts,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                     hipEvent_t* events, int32_t max_events, int32_t* n_events);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,8 @@ EXPORTED_SYMBOLS = (
     "race_noncausal_bwd",
     "race_causal_bwd_workspace_bytes",
     "race_causal_bwd",
+    "race_noncausal_bwd_profiled",
+    "race_causal_bwd_profiled",
 )
 
 
@@ -74,6 +76,10 @@ def lib() -> ctypes.CDLL:
         L.race_noncausal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_causal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_causal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
+        L.race_noncausal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz,
+                                                  vp, ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
+        L.race_causal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp,
+                                               ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         for name in EXPORTED_SYMBOLS[2:]:
             getattr(L, name).restype = i32
         _configured = True
@@ -158,3 +164,23 @@ def causal_bwd(q: int, k: int, v: int, g: int, dq: int | None, dk: int | None, d
     return lib().race_causal_bwd(q, k, v, g, dq, dk, dv, ctypes.byref(sh),
                                  ctypes.byref(opts) if opts is not None else None,
                                  workspace, workspace_bytes, stream)
+
+
+def noncausal_bwd_profiled(q, k, v, g, state, dq, dk, dv, sh: RaceShape, opts, workspace,
+                           workspace_bytes: int, stream: int, events) -> tuple[int, int]:
+    n = ctypes.c_int32(0)
+    st = lib().race_noncausal_bwd_profiled(q, k, v, g, state, dq, dk, dv, ctypes.byref(sh),
+                                           ctypes.byref(opts) if opts is not None else None,
+                                           workspace, workspace_bytes, stream, events, len(events),
+                                           ctypes.byref(n))
+    return st, n.value
+
+
+def causal_bwd_profiled(q, k, v, g, dq, dk, dv, sh: RaceShape, opts, workspace,
+                        workspace_bytes: int, stream: int, events) -> tuple[int, int]:
+    n = ctypes.c_int32(0)
+    st = lib().race_causal_bwd_profiled(q, k, v, g, dq, dk, dv, ctypes.byref(sh),
+                                        ctypes.byref(opts) if opts is not None else None,
+                                        workspace, workspace_bytes, stream, events, len(events),
+                                        ctypes.byref(n))
+    return st, n.value

@@ -291,6 +291,61 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
     return marks->mark(stream);
 }
 
+race_status noncausal_bwd_impl(const void* probsQ, const void* probsK, const void* V,
+                               const void* dOut, const float* state, void* dQ, void* dK, void* dV,
+                               const race_shape* shape, const race_options* opts, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream, Marks* marks) {
+    Problem p;
+    bool mfma = false;
+    race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (p.N == 0 || p.T == 0) return RACE_SUCCESS;
+    if (!state || !dOut || !aligned16(state) || !aligned16(dOut)) return RACE_ERROR_INVALID_VALUE;
+    if (dQ && !aligned16(dQ)) return RACE_ERROR_INVALID_VALUE;
+    if ((dQ || dK || dV) && (!probsQ || !aligned16(probsQ))) return RACE_ERROR_INVALID_VALUE;
+    if (dK && (!V || !aligned16(V) || !aligned16(dK))) return RACE_ERROR_INVALID_VALUE;
+    if (dV && (!probsK || !aligned16(probsK) || !aligned16(dV))) return RACE_ERROR_INVALID_VALUE;
+    if (!dQ && !dK && !dV) return RACE_SUCCESS;
+    const BwdLayout l = bwd_layout(p);
+    if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
+        return RACE_ERROR_INVALID_VALUE;
+    float* records = static_cast<float*>(workspace);
+    float* totals = records + l.records;
+    float* E = totals + l.totals;
+    float* dB = E + l.E;
+    float* dA = dB + l.dB;
+    const int64_t Sd = int64_t(p.S) * p.d;
+
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_state_to_E(state, E, p, stream));
+    RACE_TRY(marks->mark(stream));
+    // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c].
+    if (dQ) {
+        RACE_TRY(launch_token_map(dOut, dQ, E, Sd, 1, p.d, nullptr, 0, p, p.d, p.S, stream));
+        RACE_TRY(marks->mark(stream));
+    }
+    if (!dK && !dV) return RACE_SUCCESS;
+    // dE = Q^T dOut, as per-tile partials then a fixed-order reduce.
+    RACE_TRY(launch_tile_outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_tile_reduce(records, totals, nullptr, nullptr, p, stream));
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_bwd_finalize(totals, state, E, dB, dA, p, stream));
+    RACE_TRY(marks->mark(stream));
+    // dK = V dB^T + dA: M[a = c][b = s] = dB[s*d + c].
+    if (dK) {
+        RACE_TRY(launch_token_map(V, dK, dB, Sd, 1, p.d, dA, p.S, p, p.d, p.S, stream));
+        RACE_TRY(marks->mark(stream));
+    }
+    // dV = K dB: M[a = s][b = c] = dB[s*d + c].
+    if (dV) {
+        RACE_TRY(launch_token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
+        RACE_TRY(marks->mark(stream));
+    }
+    return RACE_SUCCESS;
+}
+
+
 }  // namespace
 }  // namespace race
 
@@ -335,62 +390,37 @@ race_status race_noncausal_bwd(const void* probsQ, const void* probsK, const voi
                                const void* dOut, const float* state, void* dQ, void* dK, void* dV,
                                const race_shape* shape, const race_options* opts, void* workspace,
                                size_t workspace_bytes, hipStream_t stream) {
-    Problem p;
-    bool mfma = false;
-    race_status st = make_problem(shape, 0, opts, &mfma, &p);
-    if (st != RACE_SUCCESS) return st;
-    if (p.N == 0 || p.T == 0) return RACE_SUCCESS;
-    if (!state || !dOut || !aligned16(state) || !aligned16(dOut)) return RACE_ERROR_INVALID_VALUE;
-    if (dQ && !aligned16(dQ)) return RACE_ERROR_INVALID_VALUE;
-    if ((dQ || dK || dV) && (!probsQ || !aligned16(probsQ))) return RACE_ERROR_INVALID_VALUE;
-    if (dK && (!V || !aligned16(V) || !aligned16(dK))) return RACE_ERROR_INVALID_VALUE;
-    if (dV && (!probsK || !aligned16(probsK) || !aligned16(dV))) return RACE_ERROR_INVALID_VALUE;
-    if (!dQ && !dK && !dV) return RACE_SUCCESS;
-    const BwdLayout l = bwd_layout(p);
-    if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
-        return RACE_ERROR_INVALID_VALUE;
-    float* records = static_cast<float*>(workspace);
-    float* totals = records + l.records;
-    float* E = totals + l.totals;
-    float* dB = E + l.E;
-    float* dA = dB + l.dB;
-    const int64_t Sd = int64_t(p.S) * p.d;
+    Marks none;
+    return noncausal_bwd_impl(probsQ, probsK, V, dOut, state, dQ, dK, dV, shape, opts, workspace,
+                              workspace_bytes, stream, &none);
+}
 
-    RACE_TRY(launch_state_to_E(state, E, p, stream));
-    // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c].
-    if (dQ) RACE_TRY(launch_token_map(dOut, dQ, E, Sd, 1, p.d, nullptr, 0, p, p.d, p.S, stream));
-    if (!dK && !dV) return RACE_SUCCESS;
-    // dE = Q^T dOut, as per-tile partials then a fixed-order reduce.
-    RACE_TRY(launch_tile_outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
-    RACE_TRY(launch_tile_reduce(records, totals, nullptr, nullptr, p, stream));
-    RACE_TRY(launch_bwd_finalize(totals, state, E, dB, dA, p, stream));
-    // dK = V dB^T + dA: M[a = c][b = s] = dB[s*d + c].
-    if (dK) RACE_TRY(launch_token_map(V, dK, dB, Sd, 1, p.d, dA, p.S, p, p.d, p.S, stream));
-    // dV = K dB: M[a = s][b = c] = dB[s*d + c].
-    if (dV) RACE_TRY(launch_token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
-    return RACE_SUCCESS;
+race_status race_noncausal_bwd_profiled(const void* probsQ, const void* probsK, const void* V,
+                                        const void* dOut, const float* state, void* dQ, void* dK,
+                                        void* dV, const race_shape* shape,
+                                        const race_options* opts, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream,
+                                        hipEvent_t* events, int32_t max_events,
+                                        int32_t* n_events) {
+    if (!events || max_events < 2 || !n_events) return RACE_ERROR_INVALID_VALUE;
+    Marks marks;
+    marks.events = events;
+    marks.max = max_events;
+    const race_status st = noncausal_bwd_impl(probsQ, probsK, V, dOut, state, dQ, dK, dV, shape,
+                                              opts, workspace, workspace_bytes, stream, &marks);
+    *n_events = marks.n;
+    return st;
 }
 
 }  // extern "C"
 
-extern "C" {
+namespace race {
+namespace {
 
-race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
-                                            size_t* bytes) {
-    if (!bytes) return RACE_ERROR_INVALID_VALUE;
-    Problem p;
-    bool mfma = false;
-    // The backward runs the vector-ALU kernels: the non-causal tile policy.
-    const race_status st = make_problem(shape, 0, opts, &mfma, &p);
-    if (st != RACE_SUCCESS) return st;
-    *bytes = size_t(causal_bwd_layout(p).total()) * sizeof(float);
-    return RACE_SUCCESS;
-}
-
-race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* V,
+race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* V,
                             const void* dOut, void* dQ, void* dK, void* dV,
                             const race_shape* shape, const race_options* opts, void* workspace,
-                            size_t workspace_bytes, hipStream_t stream) {
+                            size_t workspace_bytes, hipStream_t stream, Marks* marks) {
     Problem p;
     bool mfma = false;
     race_status st = make_problem(shape, 0, opts, &mfma, &p);
@@ -414,17 +444,65 @@ race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* 
     float* dq32 = apre + l.apre;
 
     // Prefix state at every tile start (the forward's tile totals and scan).
+    RACE_TRY(marks->mark(stream));
     if (direct_sums_supported(p.S, p.d) && p.tile % 64 == 0)
         RACE_TRY(launch_tile_sums_direct(probsK, V, fwd_rec, p, stream));
     else
         RACE_TRY(launch_tile_outer_sums(probsK, V, fwd_rec, p, p.S, p.d, stream));
+    RACE_TRY(marks->mark(stream));
     RACE_TRY(launch_tile_scan(fwd_rec, nullptr, p, stream));
+    RACE_TRY(marks->mark(stream));
     RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec, p, C,
                                   stream));
+    RACE_TRY(marks->mark(stream));
     if (!dK && !dV) return RACE_SUCCESS;
     RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
-    return launch_causal_bwd_dkv(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p, C,
-                                 stream);
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_causal_bwd_dkv(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p, C,
+                                   stream));
+    return marks->mark(stream);
+}
+
+
+}  // namespace
+}  // namespace race
+
+extern "C" {
+
+race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                            size_t* bytes) {
+    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    // The backward runs the vector-ALU kernels: the non-causal tile policy.
+    const race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(causal_bwd_layout(p).total()) * sizeof(float);
+    return RACE_SUCCESS;
+}
+
+race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* V,
+                            const void* dOut, void* dQ, void* dK, void* dV,
+                            const race_shape* shape, const race_options* opts, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+    Marks none;
+    return causal_bwd_impl(probsQ, probsK, V, dOut, dQ, dK, dV, shape, opts, workspace,
+                           workspace_bytes, stream, &none);
+}
+
+race_status race_causal_bwd_profiled(const void* probsQ, const void* probsK, const void* V,
+                                     const void* dOut, void* dQ, void* dK, void* dV,
+                                     const race_shape* shape, const race_options* opts,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                     hipEvent_t* events, int32_t max_events, int32_t* n_events) {
+    if (!events || max_events < 2 || !n_events) return RACE_ERROR_INVALID_VALUE;
+    Marks marks;
+    marks.events = events;
+    marks.max = max_events;
+    const race_status st = causal_bwd_impl(probsQ, probsK, V, dOut, dQ, dK, dV, shape, opts,
+                                           workspace, workspace_bytes, stream, &marks);
+    *n_events = marks.n;
+    return st;
 }
 
 }  // extern "C"
