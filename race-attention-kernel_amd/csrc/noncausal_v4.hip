@@ -1,0 +1,344 @@
+// noncausal_v4.hip -- vector-ALU bucket reductions and token maps of the
+// non-causal forward and backward for widths that are multiples of 4.
+//
+// The non-causal function (analysis/hot-path.md:157-162) and its VJP are two
+// kinds of pass over the tokens:
+//   reduction  R[a][b] = sum_t x[t][a] y[t][b],  colsum[a] = sum_t x[t][a]
+//              (B = K^T V and A in the forward, dE = Q^T dOut in the backward)
+//   map        out[t][c] = sum_a x[t][a] M[a][c] (+ bias[c])
+//              (out = Q E, dQ = dOut E^T, dK = V dB^T + dA, dV = K dB)
+// Both are fp32 vector-ALU code (no matrix cores): every thread owns 4 x 4
+// register tiles, operands are read from LDS as 16-byte vectors, and tokens
+// are staged with 16-byte (fp32) or 8-byte (bf16) coalesced loads.  A
+// reduction workgroup owns one chunk of one stream's tokens and writes the
+// chunk's partial sums to a record; the fixed-order reduce over chunks
+// (tile_reduce_kernel) adds them, so results are bitwise reproducible.
+#include "race_internal.h"
+
+namespace race {
+namespace {
+
+constexpr int kRedTokens = 32;   // tokens staged per step of a reduction (64 measured slower)
+constexpr int kMapTokens4 = 64;  // tokens per map block (4-token tiles x 16)
+constexpr int kMapBlocks = 4;    // map blocks per workgroup (M staged once)
+
+// Four consecutive elements (16-byte aligned for fp32, 8-byte for bf16).
+__device__ __forceinline__ float4 load4(const float* __restrict__ p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ float4 load4(const bf16_t* __restrict__ p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+}
+
+__device__ __forceinline__ void store4(float* __restrict__ p, const float4& v) {
+    *reinterpret_cast<float4*>(p) = v;
+}
+__device__ __forceinline__ void store4(bf16_t* __restrict__ p, const float4& v) {
+    uint2 u;
+    u.x = uint32_t(f32_to_bf16(v.x)) | (uint32_t(f32_to_bf16(v.y)) << 16);
+    u.y = uint32_t(f32_to_bf16(v.z)) | (uint32_t(f32_to_bf16(v.w)) << 16);
+    *reinterpret_cast<uint2*>(p) = u;
+}
+
+// ---------------------------------------------------------------------------
+// Reduction over one (chunk, stream).  Tile u = tid + kThreads m covers rows
+// 4 (u / (Wb / 4)) .. + 3 and columns 4 (u % (Wb / 4)) .. + 3 of R.
+// NV: 16-byte token vectors each thread stages per step; NT: tiles per thread.
+template <typename TIn, int NV, int NT>
+__global__ __launch_bounds__(kThreads) void outer_sums4_kernel(
+    const TIn* __restrict__ x, const TIn* __restrict__ y, float* __restrict__ records, int64_t T,
+    int chunk, int64_t chunks, int64_t rec, int Wa, int Wb) {
+    extern __shared__ float smem[];
+    float* xs = smem;                      // [2][kRedTokens][Wa]
+    float* ys = xs + 2 * kRedTokens * Wa;  // [2][kRedTokens][Wb]
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y, ci = blockIdx.x;
+    const int64_t t_begin = ci * chunk;
+    const int64_t t_end = min(T, t_begin + chunk);
+    const int va = Wa / 4, vb = Wb / 4, vrow = va + vb;
+    const int nvec = kRedTokens * vrow;
+    const int ntiles = va * vb;
+    const TIn* xn = x + n * T * Wa;
+    const TIn* yn = y + n * T * Wb;
+
+    float4 pre[NV];
+    auto fetch = [&](int64_t t0) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e < nvec) {
+                const int i = e / vrow, u = e - i * vrow;
+                if (t0 + i < t_end)
+                    val = u < va ? load4(xn + (t0 + i) * Wa + 4 * u)
+                                 : load4(yn + (t0 + i) * Wb + 4 * (u - va));
+            }
+            pre[m] = val;
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            if (e < nvec) {
+                const int i = e / vrow, u = e - i * vrow;
+                if (u < va)
+                    store4(xs + (buf * kRedTokens + i) * Wa + 4 * u, pre[m]);
+                else
+                    store4(ys + (buf * kRedTokens + i) * Wb + 4 * (u - va), pre[m]);
+            }
+        }
+    };
+
+    float acc[NT][4][4];
+    float csum[NT][4];
+#pragma unroll
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            csum[m][r] = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[m][r][c] = 0.f;
+        }
+
+    fetch(t_begin);
+    stash(0);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kRedTokens) {
+        const bool more = t0 + kRedTokens < t_end;
+        if (more) fetch(t0 + kRedTokens);
+        const float* xb = xs + buf * kRedTokens * Wa;
+        const float* yb = ys + buf * kRedTokens * Wb;
+        for (int i = 0; i < kRedTokens; ++i) {
+#pragma unroll
+            for (int m = 0; m < NT; ++m) {
+                const int u = tid + m * kThreads;
+                if (u < ntiles) {
+                    const int a4 = u / vb, b4 = u - a4 * vb;
+                    const float4 xv = *reinterpret_cast<const float4*>(xb + i * Wa + 4 * a4);
+                    const float4 yv = *reinterpret_cast<const float4*>(yb + i * Wb + 4 * b4);
+                    const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
+                    const float yc[4] = {yv.x, yv.y, yv.z, yv.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        csum[m][r] += xr[r];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) acc[m][r][c] = fmaf(xr[r], yc[c], acc[m][r][c]);
+                    }
+                }
+            }
+        }
+        if (more) stash(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    float* rp = records + (n * chunks + ci) * rec;
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+        const int u = tid + m * kThreads;
+        if (u < ntiles) {
+            const int a4 = u / vb, b4 = u - a4 * vb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                store4(rp + int64_t(4 * a4 + r) * Wb + 4 * b4,
+                       make_float4(acc[m][r][0], acc[m][r][1], acc[m][r][2], acc[m][r][3]));
+                if (b4 == 0) rp[int64_t(Wa) * Wb + 4 * a4 + r] = csum[m][r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Map over kMapBlocks blocks of kMapTokens4 tokens of one stream, for one
+// slice of 64 output columns.  M slice [Wa][64] and the block's tokens,
+// transposed ([Wa][kMapTokens4 + 4]), sit in LDS; thread (tt, cc) =
+// (tid / 16, tid % 16) computes tokens 4 tt .. + 3, slice columns 4 cc .. + 3.
+// In row a of the transposed tile, the group of tokens 4 g .. 4 g + 3 sits at
+// group g ^ xsw(a): the staging stores of one instruction (16 rows 4 apart)
+// then spread over the banks, and the 16-byte reads stay aligned.
+// NV: 16-byte token vectors each thread stages per block.
+__device__ __forceinline__ int xsw(int a) { return (a >> 2) & 7; }
+
+template <typename TIn, int NV>
+__global__ __launch_bounds__(kThreads) void map4_kernel(
+    const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
+    int64_t m_stream_stride, int64_t ms_row, int64_t ms_col, const float* __restrict__ bias,
+    int64_t bias_stream_stride, int64_t T, int Wa, int Wb) {
+    extern __shared__ float smem[];
+    constexpr int TP = kMapTokens4 + 4;  // pitch of the transposed token tile
+    float* Ms = smem;                    // [Wa][64]
+    float* xt = Ms + Wa * kSliceCols;    // [Wa][TP]
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const int c0 = blockIdx.z * kSliceCols;
+    const int ncols = min(kSliceCols, Wb - c0);
+    const float* Mn = M + n * m_stream_stride;
+    for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
+        const int a = e / kSliceCols, c = e - a * kSliceCols;
+        Ms[e] = c < ncols ? Mn[a * ms_row + (c0 + c) * ms_col] : 0.f;
+    }
+    const int va = Wa / 4;
+    const int nvec = kMapTokens4 * va;
+    const int tt = tid >> 4, cc = tid & 15;
+    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bias && 4 * cc < ncols) {
+        const float* bn = bias + n * bias_stream_stride + c0 + 4 * cc;
+        bv = make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
+                         4 * cc + 3 < ncols ? bn[3] : 0.f);
+    }
+    const TIn* xn = x + n * T * Wa;
+    TIn* on = out + n * T * Wb;
+    const int64_t wg_t0 = int64_t(blockIdx.x) * kMapBlocks * kMapTokens4;
+
+    // The next block's token vectors are loaded into registers while the
+    // current block computes.
+    float4 pre[NV];
+    auto fetch = [&](int64_t t0) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e < nvec) {
+                const int i = e / va, u = e - i * va;
+                if (t0 + i < T) val = load4(xn + (t0 + i) * Wa + 4 * u);
+            }
+            pre[m] = val;
+        }
+    };
+    fetch(wg_t0);
+    for (int blk = 0; blk < kMapBlocks; ++blk) {
+        const int64_t t0 = wg_t0 + int64_t(blk) * kMapTokens4;
+        if (t0 >= T) break;
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            if (e < nvec) {
+                const int i = e / va, u = e - i * va;
+                const int col = i ^ (xsw(4 * u) << 2);  // rows 4u .. 4u+3 share xsw
+                xt[(4 * u + 0) * TP + col] = pre[m].x;
+                xt[(4 * u + 1) * TP + col] = pre[m].y;
+                xt[(4 * u + 2) * TP + col] = pre[m].z;
+                xt[(4 * u + 3) * TP + col] = pre[m].w;
+            }
+        }
+        __syncthreads();
+        if (blk + 1 < kMapBlocks) fetch(t0 + kMapTokens4);
+        float acc[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[r][0] = bv.x;
+            acc[r][1] = bv.y;
+            acc[r][2] = bv.z;
+            acc[r][3] = bv.w;
+        }
+        for (int a = 0; a < Wa; ++a) {
+            const float4 xv = *reinterpret_cast<const float4*>(xt + a * TP + 4 * (tt ^ xsw(a)));
+            const float4 mv = *reinterpret_cast<const float4*>(Ms + a * kSliceCols + 4 * cc);
+            const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
+            const float mc[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr[r], mc[c], acc[r][c]);
+        }
+        if (4 * cc < ncols) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t t = t0 + 4 * tt + r;
+                if (t < T) store4(on + t * Wb + c0 + 4 * cc,
+                                  make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
+            }
+        }
+    }
+}
+
+int pow2_at_least(int x) {
+    int m = 1;
+    while (m < x) m *= 2;
+    return m;
+}
+
+}  // namespace
+
+bool v4_widths(int Wa, int Wb) { return Wa % 4 == 0 && Wb % 4 == 0; }
+
+hipError_t launch_outer_sums4(const void* x, const void* y, float* records, const Problem& p,
+                              int Wa, int Wb, hipStream_t stream) {
+    const int nv = pow2_at_least((kRedTokens * (Wa + Wb) / 4 + kThreads - 1) / kThreads);
+    const int nt = pow2_at_least((Wa / 4 * (Wb / 4) + kThreads - 1) / kThreads);
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    const size_t lds = size_t(2 * kRedTokens * (Wa + Wb)) * sizeof(float);
+#define RACE_OS4(TIN, NV, NT)                                                                    \
+    outer_sums4_kernel<TIN, NV, NT><<<grid, kThreads, lds, stream>>>(                            \
+        static_cast<const TIN*>(x), static_cast<const TIN*>(y), records, p.T, p.tile, p.tiles, \
+        p.rec, Wa, Wb)
+#define RACE_OS4_NT(TIN, NV)                      \
+    switch (nt) {                                 \
+        case 1: RACE_OS4(TIN, NV, 1); break;      \
+        case 2: RACE_OS4(TIN, NV, 2); break;      \
+        case 4: RACE_OS4(TIN, NV, 4); break;      \
+        case 8: RACE_OS4(TIN, NV, 8); break;      \
+        default: return hipErrorInvalidValue;     \
+    }
+#define RACE_OS4_NV(TIN)                          \
+    switch (nv) {                                 \
+        case 1: RACE_OS4_NT(TIN, 1) break;        \
+        case 2: RACE_OS4_NT(TIN, 2) break;        \
+        case 4: RACE_OS4_NT(TIN, 4) break;        \
+        case 8: RACE_OS4_NT(TIN, 8) break;        \
+        case 16: RACE_OS4_NT(TIN, 16) break;      \
+        default: return hipErrorInvalidValue;     \
+    }
+    if (p.dtype == RACE_BF16) {
+        RACE_OS4_NV(bf16_t)
+    } else {
+        RACE_OS4_NV(float)
+    }
+#undef RACE_OS4_NV
+#undef RACE_OS4_NT
+#undef RACE_OS4
+    return hipGetLastError();
+}
+
+size_t map4_lds_bytes(int Wa) {
+    return size_t(Wa * kSliceCols + Wa * (kMapTokens4 + 4)) * sizeof(float);
+}
+
+hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_stream_stride,
+                       int64_t ms_row, int64_t ms_col, const float* bias,
+                       int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
+                       hipStream_t stream) {
+    const int64_t per_wg = int64_t(kMapBlocks) * kMapTokens4;
+    const dim3 grid(unsigned((p.T + per_wg - 1) / per_wg), unsigned(p.N),
+                    unsigned((Wb + kSliceCols - 1) / kSliceCols));
+    const size_t lds = map4_lds_bytes(Wa);
+    const int nv = pow2_at_least((kMapTokens4 * (Wa / 4) + kThreads - 1) / kThreads);
+#define RACE_MAP4(TIN, NV)                                                                     \
+    map4_kernel<TIN, NV><<<grid, kThreads, lds, stream>>>(                                     \
+        static_cast<const TIN*>(x), static_cast<TIN*>(out), M, m_stream_stride, ms_row, ms_col, \
+        bias, bias_stream_stride, p.T, Wa, Wb)
+#define RACE_MAP4_NV(TIN)                      \
+    switch (nv) {                              \
+        case 1: RACE_MAP4(TIN, 1); break;      \
+        case 2: RACE_MAP4(TIN, 2); break;      \
+        case 4: RACE_MAP4(TIN, 4); break;      \
+        case 8: RACE_MAP4(TIN, 8); break;      \
+        case 16: RACE_MAP4(TIN, 16); break;    \
+        default: return hipErrorInvalidValue;  \
+    }
+    if (p.dtype == RACE_BF16) {
+        RACE_MAP4_NV(bf16_t)
+    } else {
+        RACE_MAP4_NV(float)
+    }
+#undef RACE_MAP4_NV
+#undef RACE_MAP4
+    return hipGetLastError();
+}
+
+}  // namespace race

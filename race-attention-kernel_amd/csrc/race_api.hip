@@ -177,6 +177,24 @@ hipError_t max_lds(int* bytes) {
     return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
 }
 
+// The non-causal reduction and map: the 16-byte-vector kernels when both
+// widths are multiples of 4, the scalar ones otherwise.
+hipError_t outer_sums(const void* x, const void* y, float* records, const Problem& p, int Wa,
+                      int Wb, hipStream_t stream) {
+    if (v4_widths(Wa, Wb)) return launch_outer_sums4(x, y, records, p, Wa, Wb, stream);
+    return launch_tile_outer_sums(x, y, records, p, Wa, Wb, stream);
+}
+
+hipError_t token_map(const void* x, void* out, const float* M, int64_t m_stream_stride,
+                     int64_t ms_row, int64_t ms_col, const float* bias, int64_t bias_stream_stride,
+                     const Problem& p, int Wa, int Wb, hipStream_t stream) {
+    if (v4_widths(Wa, Wb))
+        return launch_map4(x, out, M, m_stream_stride, ms_row, ms_col, bias, bias_stream_stride, p,
+                           Wa, Wb, stream);
+    return launch_token_map(x, out, M, m_stream_stride, ms_row, ms_col, bias, bias_stream_stride,
+                            p, Wa, Wb, stream);
+}
+
 #define RACE_TRY(expr)                                   \
     do {                                                 \
         const hipError_t race_err_ = (expr);             \
@@ -281,13 +299,13 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
     float* totals = records + l.records;
     float* E = totals + l.totals;
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_tile_outer_sums(probsK, V, records, p, p.S, p.d, stream));
+    RACE_TRY(outer_sums(probsK, V, records, p, p.S, p.d, stream));
     RACE_TRY(marks->mark(stream));
     RACE_TRY(launch_tile_reduce(records, totals, state, E, p, stream));
     RACE_TRY(marks->mark(stream));
     // out = q . E: M[a][c] = E[a*d + c].
-    RACE_TRY(launch_token_map(probsQ, out, E, int64_t(p.S) * p.d, p.d, 1, nullptr, 0, p, p.S, p.d,
-                              stream));
+    RACE_TRY(token_map(probsQ, out, E, int64_t(p.S) * p.d, p.d, 1, nullptr, 0, p, p.S, p.d,
+                       stream));
     return marks->mark(stream);
 }
 
@@ -321,12 +339,12 @@ race_status noncausal_bwd_impl(const void* probsQ, const void* probsK, const voi
     RACE_TRY(marks->mark(stream));
     // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c].
     if (dQ) {
-        RACE_TRY(launch_token_map(dOut, dQ, E, Sd, 1, p.d, nullptr, 0, p, p.d, p.S, stream));
+        RACE_TRY(token_map(dOut, dQ, E, Sd, 1, p.d, nullptr, 0, p, p.d, p.S, stream));
         RACE_TRY(marks->mark(stream));
     }
     if (!dK && !dV) return RACE_SUCCESS;
     // dE = Q^T dOut, as per-tile partials then a fixed-order reduce.
-    RACE_TRY(launch_tile_outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
+    RACE_TRY(outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
     RACE_TRY(marks->mark(stream));
     RACE_TRY(launch_tile_reduce(records, totals, nullptr, nullptr, p, stream));
     RACE_TRY(marks->mark(stream));
@@ -334,12 +352,12 @@ race_status noncausal_bwd_impl(const void* probsQ, const void* probsK, const voi
     RACE_TRY(marks->mark(stream));
     // dK = V dB^T + dA: M[a = c][b = s] = dB[s*d + c].
     if (dK) {
-        RACE_TRY(launch_token_map(V, dK, dB, Sd, 1, p.d, dA, p.S, p, p.d, p.S, stream));
+        RACE_TRY(token_map(V, dK, dB, Sd, 1, p.d, dA, p.S, p, p.d, p.S, stream));
         RACE_TRY(marks->mark(stream));
     }
     // dV = K dB: M[a = s][b = c] = dB[s*d + c].
     if (dV) {
-        RACE_TRY(launch_token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
+        RACE_TRY(token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
         RACE_TRY(marks->mark(stream));
     }
     return RACE_SUCCESS;

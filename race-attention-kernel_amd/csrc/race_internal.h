@@ -113,6 +113,19 @@ int mfma_tiles_per_cu(int S, int d, int dtype, int kernel);
 hipError_t launch_causal_output_direct(const void* q, const void* k, const void* v, void* out,
                                        const float* records, const Problem& p, hipStream_t stream);
 
+// ---- non-causal reductions and maps for widths that are multiples of 4
+// (noncausal_v4.hip); the kernels above take every other width ----
+bool v4_widths(int Wa, int Wb);
+// Same records as launch_tile_outer_sums (per tile of p.tile tokens).
+hipError_t launch_outer_sums4(const void* x, const void* y, float* records, const Problem& p,
+                              int Wa, int Wb, hipStream_t stream);
+// Same result as launch_token_map.
+hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_stream_stride,
+                       int64_t ms_row, int64_t ms_col, const float* bias,
+                       int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
+                       hipStream_t stream);
+size_t map4_lds_bytes(int Wa);
+
 // ---- causal backward (causal_bwd.hip): fp32 vector-ALU kernels ----
 
 // Sub-chunk length (32 or 16) of the causal backward kernels for (S, d) under
