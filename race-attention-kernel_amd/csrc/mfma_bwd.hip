@@ -1,0 +1,714 @@
+// mfma_bwd.hip -- matrix-core (MFMA) kernels of the causal backward for
+// S = d = 64 on gfx950, in sub-chunks of 32 tokens.
+//
+// The function and its VJP are those of causal_bwd.hip (per stream;
+// r = 1 / (Abar + eps), W = Q r, g = dOut; in a sub-chunk with prefix state
+// (A0, B0) and suffix state (Z1, Y1)):
+//     Abar = A0 + tril(1) K,  M = tril(G V^T),  P = tril(W K^T)
+//     dQ = r (G B0^T + M K),  alpha = -W dQ
+//     dK = V Z1^T + 1 Y1^T + M^T W + triu(1) alpha,   dV = K Z1 + P^T G
+//     Z1 += W^T G,  Y1 += 1^T alpha,  B0 += K^T V,  A0 += 1^T K.
+// These kernels write exactly the buffers of the vector-ALU ones (dQ, the fp32
+// copy of dQ, the running mass per sub-chunk, the suffix records), so the two
+// families are interchangeable launch by launch.
+//
+// Layout.  Workgroups are 4 wave64s; wave w owns bucket block w
+// (s = 16 w .. 16 w + 15).  Products use v_mfma_f32_16x16x32_bf16 with the
+// permuted contraction order of mfma_common.h, fp32 operands as bf16 hi/lo.
+// The running mass is computed with tokens as rows (Abar[i][s]: M = tokens,
+// N = buckets), so a lane holds r, W, dQ and alpha at
+//     i = 16 bi + 4 g + rr,  s = 16 w + lr        (bi < 2, rr < 4),
+// which is also the B operand (column s, contraction over tokens) of
+// Z^T += G^T W.  The carried B0 is held transposed, B0^T[c][s] at
+// c = 16 cb + 4 g + rr, s = 16 w + lr, which is the B operand (column s,
+// contraction over c) of G B0^T; Z^T is held the same way.
+// The token tiles K, V, G are staged through LDS as bf16 planes: "T" planes
+// (rows = features, contraction over tokens) and "R" planes (rows = tokens,
+// contraction over features).
+#include "mfma_common.h"
+
+namespace race {
+namespace {
+
+using namespace mfma;
+
+constexpr int kBC = 32;  // tokens per sub-chunk
+constexpr int kBS = 64;  // buckets (S) and value columns (d)
+
+template <typename TIn>
+struct BwdGeo {
+    static constexpr bool kSplit = std::is_same<TIn, float>::value;
+    static constexpr int E = Elem<TIn>::kPerVec;  // elements per 16-byte load
+    using PT = Plane<kSplit, kBC>;                // rows = features, k = tokens
+    using PR = Plane<kSplit, kBS>;                // rows = tokens, k = features
+    using PM = Plane<kSplit, kBC>;                // rows = tokens, k = tokens
+    static constexpr int kTBytes = kBS * PT::kPitch;
+    static constexpr int kRBytes = kBC * PR::kPitch;
+    static constexpr int kMBytes = kBC * PM::kPitch;
+    // Staging: blocks of 4 tokens x E features per tensor.
+    static constexpr int kBlk = (kBC / 4) * (kBS / E);   // 128 (fp32) or 64 (bf16)
+    static constexpr int kWavesPerTensor = kBlk / 64;    // 2 or 1
+    static_assert(kBlk % 64 == 0, "a tensor's blocks fill whole waves");
+};
+
+// Raw registers of one staging block: rows 4 a + rr, features b E .. b E + E - 1.
+template <typename TIn>
+struct StageBlock {
+    uint4 x[4];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int r0, int a, int b) {
+        constexpr int E = BwdGeo<TIn>::E;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+            x[rr] = buf_load16<kPolicyDefault>(rs, ((r0 + 4 * a + rr) * kBS + b * E) * int(sizeof(TIn)));
+    }
+    // T plane: row = feature, 4 consecutive tokens.
+    template <typename P>
+    __device__ __forceinline__ void store_t(unsigned char* t, int a, int b) const {
+        constexpr int E = BwdGeo<TIn>::E;
+        constexpr bool kSplit = BwdGeo<TIn>::kSplit;
+#pragma unroll
+        for (int c = 0; c < E; ++c) {
+            uint2 hi, lo;
+            split4<kSplit>(Elem<TIn>::get(x[0], c), Elem<TIn>::get(x[1], c), Elem<TIn>::get(x[2], c),
+                           Elem<TIn>::get(x[3], c), hi, lo);
+            P::put4(t, b * E + c, 4 * a, hi, lo);
+        }
+    }
+    // R plane: row = token, 4 consecutive features.
+    template <typename P>
+    __device__ __forceinline__ void store_r(unsigned char* t, int a, int b) const {
+        constexpr int E = BwdGeo<TIn>::E;
+        constexpr bool kSplit = BwdGeo<TIn>::kSplit;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+            for (int h = 0; h < E / 4; ++h) {
+                uint2 hi, lo;
+                split4<kSplit>(Elem<TIn>::get(x[rr], 4 * h), Elem<TIn>::get(x[rr], 4 * h + 1),
+                               Elem<TIn>::get(x[rr], 4 * h + 2), Elem<TIn>::get(x[rr], 4 * h + 3), hi,
+                               lo);
+                P::put4(t, 4 * a + rr, b * E + 4 * h, hi, lo);
+            }
+    }
+};
+
+template <typename TIn>
+__device__ __forceinline__ float load1(__amdgpu_buffer_rsrc_t r, int elem) {
+    if constexpr (std::is_same<TIn, float>::value) {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, elem * 4, 0, 0));
+    } else {
+        return __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b16(r, elem * 2, 0, 0)) << 16);
+    }
+}
+
+template <typename TIn>
+__device__ __forceinline__ void store1(__amdgpu_buffer_rsrc_t r, int elem, float x) {
+    if constexpr (std::is_same<TIn, float>::value) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, elem * 4, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b16(uint16_t(pack2(x, 0.f) & 0xffffu), r, elem * 2, 0, 0);
+    }
+}
+
+// Eight fp32 values (permuted-k order) to bf16 hi/lo fragments.
+template <bool kSplit>
+__device__ __forceinline__ void split8v(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
+    uint2 h0, l0, h1, l1;
+    split4<kSplit>(a[0], a[1], a[2], a[3], h0, l0);
+    split4<kSplit>(b[0], b[1], b[2], b[3], h1, l1);
+    hi = __builtin_bit_cast(bf16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+    if constexpr (kSplit) lo = __builtin_bit_cast(bf16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+}
+
+// ---------------------------------------------------------------------------
+// B1, forward walk of one (tile, stream): dQ, its fp32 copy, the running mass
+// at every sub-chunk start, and the tile's suffix totals Z = sum W (x) g,
+// Y = sum alpha into its record.
+template <typename TIn>
+__global__ __launch_bounds__(kThreads, 2) void causal_bwd_dq_mfma_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
+    const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
+    float* __restrict__ apre, const float* __restrict__ fwd_records,
+    float* __restrict__ bwd_records, int64_t T, int tile, int64_t tiles, int64_t rec) {
+    using G = BwdGeo<TIn>;
+    using PT = typename G::PT;
+    using PR = typename G::PR;
+    using PM = typename G::PM;
+    constexpr bool kSplit = G::kSplit;
+    extern __shared__ __align__(16) unsigned char lds[];
+    unsigned char* KT = lds;
+    unsigned char* VT = KT + G::kTBytes;
+    unsigned char* GT = VT + G::kTBytes;
+    unsigned char* Gs = GT + G::kTBytes;
+    unsigned char* Vs = Gs + G::kRBytes;
+    unsigned char* Ms = Vs;  // M overlays V's R plane once M is computed
+
+    const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t n = blockIdx.y, ti = blockIdx.x;
+    const int64_t t_begin = ti * tile;
+    const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
+    const int64_t base = n * T + t_begin;
+    constexpr int es = int(sizeof(TIn));
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t dqr = make_rsrc(dQ ? dQ + base * kBS : nullptr,
+                                                 dQ ? int64_t(rows) * kBS * es : 0);
+    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+
+    // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][16 w + lr].
+    const float* fr = fwd_records + (n * tiles + ti) * rec;
+    f32x4 b0t[4], zt[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            b0t[cb][rr] = fr[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr];
+            zt[cb][rr] = 0.f;
+        }
+    float a0 = fr[kBS * kBS + 16 * w + lr];
+    float ypart = 0.f;
+    const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
+
+    // Staging: this wave's tensor (K, V or G) and block.
+    const int nslots = (3 * G::kBlk + kThreads - 1) / kThreads;
+    auto slot_tensor = [&](int s) { return __builtin_amdgcn_readfirstlane((tid + s * kThreads) / G::kBlk); };
+    StageBlock<TIn> st[2];
+    auto stage_load = [&](int r0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nslots) break;
+            const int tensor = slot_tensor(s);
+            if (tensor >= 3) continue;
+            const int blk = (tid + s * kThreads) % G::kBlk;
+            const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
+            st[s].load(tensor == 0 ? kr : tensor == 1 ? vr : gr, r0, a, b);
+        }
+    };
+    auto stage_store = [&]() {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nslots) break;
+            const int tensor = slot_tensor(s);
+            if (tensor >= 3) continue;
+            const int blk = (tid + s * kThreads) % G::kBlk;
+            const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
+            if (tensor == 0) {
+                st[s].template store_t<PT>(KT, a, b);
+            } else if (tensor == 1) {
+                st[s].template store_t<PT>(VT, a, b);
+                st[s].template store_r<PR>(Vs, a, b);
+            } else {
+                st[s].template store_t<PT>(GT, a, b);
+                st[s].template store_r<PR>(Gs, a, b);
+            }
+        }
+    };
+    // Q at this lane's (i, s) positions.
+    float qreg[2][4];
+    auto load_q = [&](int r0) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                qreg[bi][rr] = load1<TIn>(qr, (r0 + 16 * bi + 4 * gq + rr) * kBS + 16 * w + lr);
+    };
+
+    const int subs = tile / kBC;
+    float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS;
+    stage_load(0);
+    load_q(0);
+    for (int r0 = 0; r0 < rows; r0 += kBC) {
+        __syncthreads();
+        stage_store();
+        float qc[2][4];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
+        stage_load(r0 + kBC);  // past the tile: zeros, never used
+        load_q(r0 + kBC);
+        if (gq == 0) ap[(r0 / kBC) * kBS + 16 * w + lr] = a0;
+        __syncthreads();
+
+        // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
+        bf16x8 kh, kl;
+        PT::frag(KT, 16 * w + lr, 0, gq, kh, kl);
+        f32x4 ab[2];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            f32x4 acc = {a0, a0, a0, a0};
+            const bf16x8& tf = bi == 0 ? tri0 : tri1;
+            if constexpr (kSplit) acc = mfma16(tf, kl, acc);
+            ab[bi] = mfma16(tf, kh, acc);
+        }
+        a0 = __shfl(ab[1][3], 48 + lr);  // inclusive mass at the last token
+        f32x4 rv[2], wv[2];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                rv[bi][rr] = __builtin_amdgcn_rcpf(ab[bi][rr] + kEps);
+                wv[bi][rr] = qc[bi][rr] * rv[bi][rr];
+            }
+
+        // 2: M^T blocks (j-block, i-block) = V G^T, j <= i: (0,0), (0,1), (1,1) on waves 0..2.
+        f32x4 mt = {0.f, 0.f, 0.f, 0.f};
+        const int mbj = w == 2 ? 1 : 0, mbi = w >= 1 ? 1 : 0;
+        if (w < 3) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                bf16x8 ah, al, bh, bl;
+                PR::frag(Vs, 16 * mbj + lr, kk, gq, ah, al);
+                PR::frag(Gs, 16 * mbi + lr, kk, gq, bh, bl);
+                mt = mfma3<kSplit>(ah, al, bh, bl, mt);
+            }
+            if (mbj == mbi) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    if (4 * gq + rr > lr) mt[rr] = 0.f;
+            }
+        }
+        __syncthreads();  // V's R plane is dead; M goes over it
+        if (w < 3) {
+            uint2 hi, lo;
+            split4<kSplit>(mt[0], mt[1], mt[2], mt[3], hi, lo);
+            PM::put4(Ms, 16 * mbi + lr, 16 * mbj + 4 * gq, hi, lo);
+        }
+        __syncthreads();
+
+        // 3: U = G B0^T + M K;  dQ = r U;  alpha = -W dQ.
+        f32x4 u[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            bf16x8 bh, bl;
+            split8v<kSplit>(b0t[2 * kk], b0t[2 * kk + 1], bh, bl);
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi) {
+                bf16x8 gh, gl;
+                PR::frag(Gs, 16 * bi + lr, kk, gq, gh, gl);
+                u[bi] = mfma3<kSplit>(gh, gl, bh, bl, u[bi]);
+            }
+        }
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            bf16x8 mh, ml;
+            PM::frag(Ms, 16 * bi + lr, 0, gq, mh, ml);
+            if (bi == 0) {
+                // Tokens 16..31 of the first block's row are above the diagonal.
+#pragma unroll
+                for (int e = 4; e < 8; ++e) {
+                    mh[e] = __bf16(0.0f);
+                    if constexpr (kSplit) ml[e] = __bf16(0.0f);
+                }
+            }
+            u[bi] = mfma3<kSplit>(mh, ml, kh, kl, u[bi]);
+        }
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const float dqv = rv[bi][rr] * u[bi][rr];
+                const int elem = (r0 + 16 * bi + 4 * gq + rr) * kBS + 16 * w + lr;
+                if (dQ) store1<TIn>(dqr, elem, dqv);
+                store1<float>(d32r, elem, dqv);
+                ypart += -wv[bi][rr] * dqv;
+            }
+
+        // 4: Z^T += G^T W (contraction over the sub-chunk's tokens).
+        bf16x8 wh, wl;
+        split8v<kSplit>(wv[0], wv[1], wh, wl);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            bf16x8 gh, gl;
+            PT::frag(GT, 16 * cb + lr, 0, gq, gh, gl);
+            zt[cb] = mfma3<kSplit>(gh, gl, wh, wl, zt[cb]);
+        }
+        // 5: B0^T += V^T K.
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            bf16x8 vh, vl;
+            PT::frag(VT, 16 * cb + lr, 0, gq, vh, vl);
+            b0t[cb] = mfma3<kSplit>(vh, vl, kh, kl, b0t[cb]);
+        }
+    }
+
+    // Suffix totals of this tile: Z[s][c] (record layout B[s][c]) and Y[s].
+    float* br = bwd_records + (n * tiles + ti) * rec;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) br[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr] = zt[cb][rr];
+    float y = ypart + __shfl_xor(ypart, 16);
+    y = y + __shfl_xor(y, 32);
+    if (gq == 0) br[kBS * kBS + 16 * w + lr] = y;
+}
+
+// Upper-triangular ones as an A operand: element e of lane (g, lr) is
+// (i' >= j') with i' = 4 g + e % 4 + 16 (e / 4) (contraction index) and row
+// j' = off + lr.
+__device__ __forceinline__ bf16x8 triu_frag(int off, int g, int lr) {
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (4 * g + (e & 3) + 16 * (e >> 2) >= off + lr) ? __bf16(1.0f) : __bf16(0.0f);
+    return f;
+}
+
+// The bf16 hi (and lo) bit patterns of x.
+template <bool kSplit>
+__device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
+    const uint32_t h = pack2(x, 0.f) & 0xffffu;
+    hi = uint16_t(h);
+    if constexpr (kSplit) lo = uint16_t(pack2(x - __uint_as_float(h << 16), 0.f) & 0xffffu);
+}
+
+// ---------------------------------------------------------------------------
+// B3, backward walk of one (tile, stream) from the suffix state at the tile
+// end: dK (wave w: buckets 16 w ..) and dV (wave w: value columns 16 w ..).
+// Per sub-chunk, with the suffix state Z1 after it:
+//   1. Abar, r, W (as B1, from the running mass saved by B1); alpha = -W dQ;
+//      W also goes to an R plane (rows = tokens) for P
+//   2. M = tril(G V^T) and P = tril(W K^T) into T-oriented planes (rows = j)
+//   3. dK = V Z1^T + M^T W + triu(1) alpha + Y1        (Z1^T from registers)
+//   4. dV = K Z1 + P^T G                                (Z1 from an LDS plane)
+//   5. Z1^T += G^T W, Y1 += 1^T alpha
+template <typename TIn>
+__global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
+    const TIn* __restrict__ g, const float* __restrict__ dq32, const float* __restrict__ apre,
+    const float* __restrict__ suffix_records, TIn* __restrict__ dK, TIn* __restrict__ dV,
+    int64_t T, int tile, int64_t tiles, int64_t rec) {
+    using G = BwdGeo<TIn>;
+    using PT = typename G::PT;
+    using PR = typename G::PR;
+    using PM = typename G::PM;
+    constexpr bool kSplit = G::kSplit;
+    extern __shared__ __align__(16) unsigned char lds[];
+    unsigned char* KT = lds;
+    unsigned char* GT = KT + G::kTBytes;
+    unsigned char* Ks = GT + G::kTBytes;
+    unsigned char* Vs = Ks + G::kRBytes;
+    unsigned char* Gs = Vs + G::kRBytes;
+    unsigned char* Ws = Gs + G::kRBytes;
+    unsigned char* MT = Ws + G::kRBytes;     // rows j, contraction over i
+    unsigned char* PTp = MT + G::kMBytes;    // rows j, contraction over i
+    unsigned char* Zp = PTp + G::kMBytes;    // Z1^T: rows c, contraction over s
+
+    const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t n = blockIdx.y, ti = blockIdx.x;
+    const int64_t t_begin = ti * tile;
+    const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
+    const int64_t base = n * T + t_begin;
+    constexpr int es = int(sizeof(TIn));
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * kBS, int64_t(rows) * kBS * es);
+    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+    const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * kBS : nullptr,
+                                                 dK ? int64_t(rows) * kBS * es : 0);
+    const __amdgpu_buffer_rsrc_t dvr = make_rsrc(dV ? dV + base * kBS : nullptr,
+                                                 dV ? int64_t(rows) * kBS * es : 0);
+
+    // Suffix state at the tile end: Z1^T[16 cb + 4 g + rr][16 w + lr], Y1[16 w + lr].
+    const float* sr = suffix_records + (n * tiles + ti) * rec;
+    f32x4 zt[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) zt[cb][rr] = sr[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr];
+    float y1 = sr[kBS * kBS + 16 * w + lr];
+    const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
+    const bf16x8 up0 = triu_frag(0, gq, lr), up1 = triu_frag(16, gq, lr);
+
+    const int nslots = (3 * G::kBlk + kThreads - 1) / kThreads;
+    auto slot_tensor = [&](int s) { return __builtin_amdgcn_readfirstlane((tid + s * kThreads) / G::kBlk); };
+    StageBlock<TIn> st[2];
+    auto stage_load = [&](int r0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nslots) break;
+            const int tensor = slot_tensor(s);
+            if (tensor >= 3) continue;
+            const int blk = (tid + s * kThreads) % G::kBlk;
+            const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
+            st[s].load(tensor == 0 ? kr : tensor == 1 ? vr : gr, r0, a, b);
+        }
+    };
+    auto stage_store = [&]() {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nslots) break;
+            const int tensor = slot_tensor(s);
+            if (tensor >= 3) continue;
+            const int blk = (tid + s * kThreads) % G::kBlk;
+            const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
+            if (tensor == 0) {
+                st[s].template store_t<PT>(KT, a, b);
+                st[s].template store_r<PR>(Ks, a, b);
+            } else if (tensor == 1) {
+                st[s].template store_r<PR>(Vs, a, b);
+            } else {
+                st[s].template store_t<PT>(GT, a, b);
+                st[s].template store_r<PR>(Gs, a, b);
+            }
+        }
+    };
+    float qreg[2][4], dreg[2][4];
+    auto load_qd = [&](int r0) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int elem = (r0 + 16 * bi + 4 * gq + rr) * kBS + 16 * w + lr;
+                qreg[bi][rr] = load1<TIn>(qr, elem);
+                dreg[bi][rr] = load1<float>(d32r, elem);
+            }
+    };
+
+    const int subs = tile / kBC;
+    const float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS;
+    const int last = ((rows - 1) / kBC) * kBC;
+    stage_load(last);
+    load_qd(last);
+    for (int r0 = last; r0 >= 0; r0 -= kBC) {
+        __syncthreads();
+        stage_store();
+        float qc[2][4], dc[2][4];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                qc[bi][rr] = qreg[bi][rr];
+                dc[bi][rr] = dreg[bi][rr];
+            }
+        if (r0 > 0) {
+            stage_load(r0 - kBC);
+            load_qd(r0 - kBC);
+        }
+        // Z1 (the suffix state after this sub-chunk) as a plane for dV.
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                uint16_t hi, lo;
+                split1<kSplit>(zt[cb][rr], hi, lo);
+                PR::put1(Zp, 16 * cb + 4 * gq + rr, 16 * w + lr, hi, lo);
+            }
+        __syncthreads();
+
+        // 1: Abar, r, W, alpha; W into its R plane.
+        bf16x8 kh, kl;
+        PT::frag(KT, 16 * w + lr, 0, gq, kh, kl);
+        const float a0 = ap[(r0 / kBC) * kBS + 16 * w + lr];
+        f32x4 wv[2], al[2];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            f32x4 acc = {a0, a0, a0, a0};
+            const bf16x8& tf = bi == 0 ? tri0 : tri1;
+            if constexpr (kSplit) acc = mfma16(tf, kl, acc);
+            acc = mfma16(tf, kh, acc);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                wv[bi][rr] = qc[bi][rr] * __builtin_amdgcn_rcpf(acc[rr] + kEps);
+                al[bi][rr] = -wv[bi][rr] * dc[bi][rr];
+                uint16_t hi, lo;
+                split1<kSplit>(wv[bi][rr], hi, lo);
+                PR::put1(Ws, 16 * bi + 4 * gq + rr, 16 * w + lr, hi, lo);
+            }
+        }
+        __syncthreads();
+
+        // 2: M blocks (i-block, j-block) on waves 0..2, P blocks on waves 1..3,
+        //    blocks (0,0), (1,0), (1,1); written with rows j.
+        {
+            const int mb = w, pb = w - 1;  // block index 0..2
+            f32x4 m = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+            if (mb < 3) {
+                const int bi = mb >= 1 ? 1 : 0, bj = mb == 2 ? 1 : 0;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    bf16x8 ah, alo, bh, bl;
+                    PR::frag(Gs, 16 * bi + lr, kk, gq, ah, alo);
+                    PR::frag(Vs, 16 * bj + lr, kk, gq, bh, bl);
+                    m = mfma3<kSplit>(ah, alo, bh, bl, m);
+                }
+                if (bi == bj) {
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        if (lr > 4 * gq + rr) m[rr] = 0.f;
+                }
+                uint2 hi, lo;
+                split4<kSplit>(m[0], m[1], m[2], m[3], hi, lo);
+                PM::put4(MT, 16 * bj + lr, 16 * bi + 4 * gq, hi, lo);
+            }
+            if (pb >= 0) {
+                const int bi = pb >= 1 ? 1 : 0, bj = pb == 2 ? 1 : 0;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    bf16x8 ah, alo, bh, bl;
+                    PR::frag(Ws, 16 * bi + lr, kk, gq, ah, alo);
+                    PR::frag(Ks, 16 * bj + lr, kk, gq, bh, bl);
+                    pacc = mfma3<kSplit>(ah, alo, bh, bl, pacc);
+                }
+                if (bi == bj) {
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        if (lr > 4 * gq + rr) pacc[rr] = 0.f;
+                }
+                uint2 hi, lo;
+                split4<kSplit>(pacc[0], pacc[1], pacc[2], pacc[3], hi, lo);
+                PM::put4(PTp, 16 * bj + lr, 16 * bi + 4 * gq, hi, lo);
+            }
+        }
+        __syncthreads();
+
+        bf16x8 wh, wl, ah2, al2;
+        split8v<kSplit>(wv[0], wv[1], wh, wl);
+        split8v<kSplit>(al[0], al[1], ah2, al2);
+        // 3: dK[j][s] for s-block w.
+        f32x4 dk[2];
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) dk[bj] = f32x4{y1, y1, y1, y1};
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            bf16x8 zh, zl;
+            split8v<kSplit>(zt[2 * kk], zt[2 * kk + 1], zh, zl);
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) {
+                bf16x8 vh, vl;
+                PR::frag(Vs, 16 * bj + lr, kk, gq, vh, vl);
+                dk[bj] = mfma3<kSplit>(vh, vl, zh, zl, dk[bj]);
+            }
+        }
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+            bf16x8 mh, ml;
+            PM::frag(MT, 16 * bj + lr, 0, gq, mh, ml);
+            if (bj == 1) {
+                // Tokens i < 16 of the second j-block are above the diagonal.
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    mh[e] = __bf16(0.0f);
+                    if constexpr (kSplit) ml[e] = __bf16(0.0f);
+                }
+            }
+            dk[bj] = mfma3<kSplit>(mh, ml, wh, wl, dk[bj]);
+            const bf16x8& uf = bj == 0 ? up0 : up1;
+            if constexpr (kSplit) dk[bj] = mfma16(uf, al2, dk[bj]);
+            dk[bj] = mfma16(uf, ah2, dk[bj]);
+        }
+        if (dK) {
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    store1<TIn>(dkr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dk[bj][rr]);
+        }
+        // 4: dV[j][c] for c-block w.
+        if (dV) {
+            f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                bf16x8 zh, zl;
+                PR::frag(Zp, 16 * w + lr, kk, gq, zh, zl);
+#pragma unroll
+                for (int bj = 0; bj < 2; ++bj) {
+                    bf16x8 kh2, kl2;
+                    PR::frag(Ks, 16 * bj + lr, kk, gq, kh2, kl2);
+                    dv[bj] = mfma3<kSplit>(kh2, kl2, zh, zl, dv[bj]);
+                }
+            }
+            bf16x8 gh, gl;
+            PT::frag(GT, 16 * w + lr, 0, gq, gh, gl);
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) {
+                bf16x8 ph, pl;
+                PM::frag(PTp, 16 * bj + lr, 0, gq, ph, pl);
+                if (bj == 1) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ph[e] = __bf16(0.0f);
+                        if constexpr (kSplit) pl[e] = __bf16(0.0f);
+                    }
+                }
+                dv[bj] = mfma3<kSplit>(ph, pl, gh, gl, dv[bj]);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    store1<TIn>(dvr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dv[bj][rr]);
+            }
+        }
+        // 5: the suffix state before this sub-chunk.
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            bf16x8 gh, gl;
+            PT::frag(GT, 16 * cb + lr, 0, gq, gh, gl);
+            zt[cb] = mfma3<kSplit>(gh, gl, wh, wl, zt[cb]);
+        }
+        float ys = 0.f;
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) ys += al[bi][rr];
+        ys = ys + __shfl_xor(ys, 16);
+        ys = ys + __shfl_xor(ys, 32);
+        y1 += ys;
+    }
+}
+
+}  // namespace
+
+bool causal_bwd_mfma_supported(int S, int d) { return S == kBS && d == kBS; }
+
+hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
+                                     void* dQ, float* dq32, float* apre, const float* fwd_records,
+                                     float* bwd_records, const Problem& p, hipStream_t stream) {
+    if (!causal_bwd_mfma_supported(p.S, p.d) || p.tile % kBC != 0) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    if (p.dtype == RACE_BF16) {
+        using G = BwdGeo<bf16_t>;
+        const size_t lds = 3 * G::kTBytes + 2 * G::kRBytes;
+        causal_bwd_dq_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+            static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+            static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ),
+            dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec);
+    } else {
+        using G = BwdGeo<float>;
+        const size_t lds = 3 * G::kTBytes + 2 * G::kRBytes;
+        causal_bwd_dq_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
+            static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+            static_cast<const float*>(g), static_cast<float*>(dQ), dq32, apre, fwd_records,
+            bwd_records, p.T, p.tile, p.tiles, p.rec);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
+                                      const float* dq32, const float* apre,
+                                      const float* suffix_records, void* dK, void* dV,
+                                      const Problem& p, hipStream_t stream) {
+    if (!causal_bwd_mfma_supported(p.S, p.d) || p.tile % kBC != 0) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    if (p.dtype == RACE_BF16) {
+        using G = BwdGeo<bf16_t>;
+        const size_t lds = 2 * G::kTBytes + 4 * G::kRBytes + 2 * G::kMBytes + kBS * G::PR::kPitch;
+        causal_bwd_dkv_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+            static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+            static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), dq32, apre,
+            suffix_records, static_cast<bf16_t*>(dK), static_cast<bf16_t*>(dV), p.T, p.tile, p.tiles,
+            p.rec);
+    } else {
+        using G = BwdGeo<float>;
+        const size_t lds = 2 * G::kTBytes + 4 * G::kRBytes + 2 * G::kMBytes + kBS * G::PR::kPitch;
+        causal_bwd_dkv_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
+            static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+            static_cast<const float*>(g), dq32, apre, suffix_records, static_cast<float*>(dK),
+            static_cast<float*>(dV), p.T, p.tile, p.tiles, p.rec);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace race

@@ -46,36 +46,6 @@ namespace {
 using namespace mfma;
 
 
-// Plane tile geometry for rows of K elements.  A plane row is K / 8 chunks of
-// 16 bytes (8 elements).  Chunk u of row r is stored at chunk u ^ sw(r),
-//     sw(r) = ((r / 8) % 8 ^ (r / 4) % 2) & (K / 8 - 1),
-// and rows are 32 bytes longer than the planes.  With that layout the 16-byte
-// fragment reads (16 consecutive rows, one chunk) touch every bank once, and
-// the transposed staging stores (rows 4 apart, one 8-byte half chunk) are
-// spread over all banks instead of piling into two.
-template <bool kSplit, int K>
-struct Plane {
-    static constexpr int kLoOff = 2 * K;                       // bytes to the lo plane
-    static constexpr int kPitch = (kSplit ? 4 : 2) * K + 32;   // row pitch in bytes
-    static constexpr int kMask = (K / 8 < 8 ? K / 8 : 8) - 1;
-    __device__ __forceinline__ static int sw(int row) { return ((row >> 3) ^ ((row >> 2) & 1)) & kMask; }
-    // Store 4 consecutive elements k0..k0+3 (k0 % 4 == 0) of row `row`.
-    __device__ __forceinline__ static void put4(unsigned char* t, int row, int k0, const uint2& hi,
-                                                const uint2& lo) {
-        const int pos = fpos(k0);
-        unsigned char* p = t + row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 8 * ((pos >> 2) & 1);
-        *reinterpret_cast<uint2*>(p) = hi;
-        if constexpr (kSplit) *reinterpret_cast<uint2*>(p + kLoOff) = lo;
-    }
-    // Fragment of row `row` for contraction step kk.
-    __device__ __forceinline__ static void frag(const unsigned char* t, int row, int kk, int g,
-                                                bf16x8& hi, bf16x8& lo) {
-        const unsigned char* p = t + row * kPitch + 16 * ((4 * kk + g) ^ sw(row));
-        hi = *reinterpret_cast<const bf16x8*>(p);
-        if constexpr (kSplit) lo = *reinterpret_cast<const bf16x8*>(p + kLoOff);
-    }
-};
-
 // Geometry of one (S, D, C, dtype) specialization.
 template <typename TIn, int S, int D, int C>
 struct Geo {

@@ -439,10 +439,18 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
                             const void* dOut, void* dQ, void* dK, void* dV,
                             const race_shape* shape, const race_options* opts, void* workspace,
                             size_t workspace_bytes, hipStream_t stream, Marks* marks) {
+    // The tile policy is the vector-ALU one; the kernel family is chosen here.
+    const int kernel = kernel_choice(opts);
+    if (kernel != RACE_KERNEL_AUTO && kernel != RACE_KERNEL_VALU && kernel != RACE_KERNEL_MFMA)
+        return RACE_ERROR_INVALID_VALUE;
+    race_options topts = {opts ? opts->tile_tokens : 0, RACE_KERNEL_VALU};
     Problem p;
     bool mfma = false;
-    race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
+    const bool use_mfma = kernel != RACE_KERNEL_VALU && causal_bwd_mfma_supported(p.S, p.d) &&
+                          p.tile % 32 == 0;
+    if (kernel == RACE_KERNEL_MFMA && !use_mfma) return RACE_ERROR_INVALID_VALUE;
     if (p.N == 0 || p.T == 0 || (!dQ && !dK && !dV)) return RACE_SUCCESS;
     if (!probsQ || !probsK || !V || !dOut) return RACE_ERROR_INVALID_VALUE;
     if (!aligned16(probsQ) || !aligned16(probsK) || !aligned16(V) || !aligned16(dOut))
@@ -455,7 +463,7 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     int lds_limit = 0;
     RACE_TRY(max_lds(&lds_limit));
     const int C = causal_bwd_chunk(p.S, p.d, lds_limit);
-    if (C == 0) return RACE_ERROR_INVALID_VALUE;
+    if (C == 0 || (use_mfma && C != 32)) return RACE_ERROR_INVALID_VALUE;
     float* fwd_rec = static_cast<float*>(workspace);
     float* bwd_rec = fwd_rec + l.fwd;
     float* apre = bwd_rec + l.bwd;
@@ -470,14 +478,22 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     RACE_TRY(marks->mark(stream));
     RACE_TRY(launch_tile_scan(fwd_rec, nullptr, p, stream));
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec, p, C,
-                                  stream));
+    if (use_mfma)
+        RACE_TRY(launch_causal_bwd_dq_mfma(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec,
+                                           p, stream));
+    else
+        RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec, p,
+                                      C, stream));
     RACE_TRY(marks->mark(stream));
     if (!dK && !dV) return RACE_SUCCESS;
     RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_causal_bwd_dkv(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p, C,
-                                   stream));
+    if (use_mfma)
+        RACE_TRY(launch_causal_bwd_dkv_mfma(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p,
+                                            stream));
+    else
+        RACE_TRY(launch_causal_bwd_dkv(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p, C,
+                                       stream));
     return marks->mark(stream);
 }
 
@@ -492,8 +508,9 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
     if (!bytes) return RACE_ERROR_INVALID_VALUE;
     Problem p;
     bool mfma = false;
-    // The backward runs the vector-ALU kernels: the non-causal tile policy.
-    const race_status st = make_problem(shape, 0, opts, &mfma, &p);
+    // The backward uses the vector-ALU tile policy for both kernel families.
+    race_options topts = {opts ? opts->tile_tokens : 0, RACE_KERNEL_VALU};
+    const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
     *bytes = size_t(causal_bwd_layout(p).total()) * sizeof(float);
     return RACE_SUCCESS;

@@ -144,6 +144,17 @@ hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, co
                                  const float* suffix_records, void* dK, void* dV, const Problem& p,
                                  int C, hipStream_t stream);
 
+// Matrix-core kernels of the causal backward (mfma_bwd.hip): S = d = 64,
+// 32-token sub-chunks, the same buffers as the vector-ALU kernels.
+bool causal_bwd_mfma_supported(int S, int d);
+hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
+                                     void* dQ, float* dq32, float* apre, const float* fwd_records,
+                                     float* bwd_records, const Problem& p, hipStream_t stream);
+hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
+                                      const float* dq32, const float* apre,
+                                      const float* suffix_records, void* dK, void* dV,
+                                      const Problem& p, hipStream_t stream);
+
 // Whether the MFMA causal path has a specialization for (S, d).
 bool mfma_causal_supported(int S, int d);
 hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void* out,

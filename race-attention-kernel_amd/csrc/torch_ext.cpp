@@ -7,7 +7,7 @@
 //   noncausal_backward(probsQ, probsK, V, dOut, state, need_q, need_k, need_v,
 //                      tile_tokens=0) -> (dQ or None, dK or None, dV or None)
 //   causal_backward(probsQ, probsK, V, dOut, need_q, need_k, need_v,
-//                   tile_tokens=0) -> (dQ or None, dK or None, dV or None)
+//                   tile_tokens=0, kernel=0) -> (dQ or None, dK or None, dV or None)
 //   select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens=0, kernel=0) -> int
 //   shape_supported(L, R, d) -> (supported, has_mfma)
 //
@@ -180,12 +180,12 @@ noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
 std::tuple<c10::optional<at::Tensor>, c10::optional<at::Tensor>, c10::optional<at::Tensor>>
 causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                 const at::Tensor& grad_out, bool need_q, bool need_k, bool need_v,
-                int64_t tile_tokens) {
+                int64_t tile_tokens, int64_t kernel) {
     const race_shape sh = validate(q, k, v);
     check_token_tensor(grad_out, "dOut", q);
     TORCH_CHECK(grad_out.sizes() == v.sizes(), "dOut shape ", grad_out.sizes(), " differs from V ",
                 v.sizes());
-    const race_options opts = make_options(tile_tokens, RACE_KERNEL_AUTO);
+    const race_options opts = make_options(tile_tokens, kernel);
     const c10::DeviceGuard guard(q.device());
     at::Tensor dq, dk, dv;
     if (need_q) dq = at::empty_like(q);
@@ -245,7 +245,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("causal_backward", &causal_backward, "Causal backward -> (dQ, dK, dV)",
           py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("dOut"),
           py::arg("need_q") = true, py::arg("need_k") = true, py::arg("need_v") = true,
-          py::arg("tile_tokens") = 0);
+          py::arg("tile_tokens") = 0, py::arg("kernel") = 0);
     m.def("select_tile_tokens", &select_tile_tokens, "Tile length a forward would use",
           py::arg("N"), py::arg("T"), py::arg("L"), py::arg("R"), py::arg("d"),
           py::arg("bf16") = false, py::arg("causal") = true, py::arg("tile_tokens") = 0,

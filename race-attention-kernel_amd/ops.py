@@ -73,7 +73,7 @@ class RaceFusedFunction(torch.autograd.Function):
             q, k, v = ctx.saved_tensors
             grad_out = _dense(grad_out.to(v.dtype))
             dq, dk, dv = _lib.ext().causal_backward(q, k, v, grad_out, need_q, need_k, need_v,
-                                                   0)
+                                                   0, 0)
             return dq, dk, dv, None, None, None
         q, k, v, state = ctx.saved_tensors
         grad_out = _dense(grad_out.to(v.dtype))
@@ -118,9 +118,11 @@ def race_noncausal_backward(probsQ, probsK, V, dOut, state, *, need=(True, True,
 
 
 def race_causal_backward(probsQ, probsK, V, dOut, *, need=(True, True, True),
-                         tile_tokens: int = 0):
-    """(dQ, dK, dV) of the causal forward for upstream gradient dOut."""
-    return _lib.ext().causal_backward(probsQ, probsK, V, _dense(dOut), *need, tile_tokens)
+                         tile_tokens: int = 0, kernel: str | int = "auto"):
+    """(dQ, dK, dV) of the causal forward for upstream gradient dOut.  kernel:
+    "auto" (matrix cores where a specialization exists), "valu" or "mfma"."""
+    return _lib.ext().causal_backward(probsQ, probsK, V, _dense(dOut), *need, tile_tokens,
+                                      _kernel_id(kernel))
 
 
 def select_tile_tokens(N: int, T: int, L: int, R: int, d: int, *, bf16: bool = False,

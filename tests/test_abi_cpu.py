@@ -123,13 +123,16 @@ def test_invalid_arguments_are_rejected_before_any_launch(race):
     # Backward needs the state and dOut.
     assert abi.noncausal_bwd(16, 16, 16, 0, 0, 16, 16, 16, good, opts, 64, 1 << 30, 0) == \
         abi.RACE_ERROR_INVALID_VALUE
-    # Causal backward: dOut, aligned outputs and a large enough workspace; no
-    # MFMA kernel.
+    # Causal backward: dOut, aligned outputs and a large enough workspace; the
+    # MFMA kernels only for S = d = 64.
     inv = abi.RACE_ERROR_INVALID_VALUE
     assert abi.causal_bwd(16, 16, 16, 0, 16, 16, 16, good, opts, 64, 1 << 30, 0) == inv
     assert abi.causal_bwd(16, 16, 16, 16, 16, 24, 16, good, opts, 64, 1 << 30, 0) == inv
     assert abi.causal_bwd(16, 16, 16, 16, 16, 16, 16, good, opts, 64, 64, 0) == inv
-    assert abi.causal_bwd(16, 16, 16, 16, 16, 16, 16, good, abi.options(64, abi.RACE_KERNEL_MFMA),
+    no_mfma = abi.shape(8, 1024, 2, 8, 32)
+    assert abi.causal_bwd(16, 16, 16, 16, 16, 16, 16, no_mfma, abi.options(64, abi.RACE_KERNEL_MFMA),
+                          64, 1 << 30, 0) == inv
+    assert abi.causal_bwd(16, 16, 16, 16, 16, 16, 16, good, abi.options(64, abi.RACE_KERNEL_MFMA_WG),
                           64, 1 << 30, 0) == inv
     # Nothing requested, or nothing to do: success without a launch.
     assert abi.causal_bwd(0, 0, 0, 0, None, None, None, good, opts, None, 0, 0) == 0

@@ -102,6 +102,21 @@ def test_tile_lengths(race, oracle, cuda, tile):
     check_grads(oracle, q, k, v, g, out, dq, dk, dv, FP32_TOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+@pytest.mark.parametrize("T", [1, 31, 33, 100, 2000])
+def test_kernel_families(race, oracle, cuda, dtype, kernel, T):
+    # Both kernel families at S = d = 64 (the matrix-core specialization),
+    # ragged T around the 32-token sub-chunk.
+    say("c-bwd family", kernel, dtype, T)
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(3, T, 4, 16, 64, seed=28 + T, dtype=dtype,
+                                                       grad_out=True))
+    dq, dk, dv = race.race_causal_backward(q, k, v, g, kernel=kernel)
+    out = race.race_fused_fwd(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol_for(dtype))
+
+
 @pytest.mark.parametrize("name", ["cgrad", "cgrad_wide"])
 def test_golden_gradients(race, cuda, name):
     say("c-bwd golden", name)
@@ -158,6 +173,12 @@ def test_future_gradients_do_not_reach_past_queries(race, cuda):
     dq2, _, _ = race.race_causal_backward(q, k, v, g2, need=(True, False, False))
     torch.cuda.synchronize()
     assert torch.equal(dq1[:, :600], dq2[:, :600])
+
+
+def test_mfma_backward_needs_its_specialization(race, cuda):
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 64, 2, 8, 32, seed=29, grad_out=True))
+    with pytest.raises(RuntimeError, match="race_causal_bwd"):
+        race.race_causal_backward(q, k, v, g, kernel="mfma")
 
 
 def test_unsupported_shape_raises(race, cuda):
