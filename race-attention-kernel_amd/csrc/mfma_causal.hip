@@ -530,7 +530,9 @@ hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out,
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel) {
     if (kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(S, d, dtype))
         return direct_output_tiles_per_cu();
-    return 4;  // two resident workgroups per CU, two rounds
+    // Two resident workgroups per CU, two rounds; S = 256 runs one workgroup
+    // per CU and prefers longer tiles (fewer 132 KB records to scan).
+    return S >= 256 ? 2 : 4;
 }
 
 bool mfma_causal_supported(int S, int d) {

@@ -13,7 +13,10 @@ namespace race {
 namespace {
 
 constexpr int64_t kMaxStreams = 65535;  // grid.y
-constexpr int kMaxAutoTile = 4096;
+// Longest automatic tile: the MFMA causal forward takes up to 16384 tokens
+// (fewer tile records; measured faster at cfg3), every other path 4096.
+constexpr int kMaxAutoTile = 16384;
+constexpr int kMaxAutoTileOther = 4096;
 
 int64_t round64(int64_t floats) { return ((floats + 63) / 64) * 64; }
 
@@ -83,8 +86,9 @@ race_status resolve_tile(const race_shape* sh, int causal, const race_options* o
     const int64_t per_cu =
         (causal && mfma) ? mfma_tiles_per_cu(sub(sh), sh->head_dim, sh->dtype, kernel_choice(o)) : 2;
     int t = pow2_floor(work / (per_cu * cus));
+    const int cap = (causal && mfma) ? kMaxAutoTile : kMaxAutoTileOther;
     if (t < RACE_SUB_CHUNK_TOKENS) t = RACE_SUB_CHUNK_TOKENS;
-    if (t > kMaxAutoTile) t = kMaxAutoTile;
+    if (t > cap) t = cap;
     *tile = t;
     return RACE_SUCCESS;
 }

@@ -106,7 +106,7 @@ hipError_t launch_tile_sums_direct(const void* k, const void* v, float* records,
                                    hipStream_t stream);
 // Register-direct causal output pass: S = d = 64, bf16.
 bool direct_output_supported(int S, int d, int dtype);
-// Tiles per compute unit the direct output pass wants resident (8 wave64s).
+// Tiles per compute unit the direct output pass wants resident (one wave64 per SIMD).
 int direct_output_tiles_per_cu();
 // Tiles per compute unit the MFMA causal path of this problem wants.
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel);
