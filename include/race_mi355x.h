@@ -191,6 +191,20 @@ race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* 
                             const race_shape* shape, const race_options* opts, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* The bucket probabilities the op consumes, from the token rows: the hashing
+ * of the reference's BatchedACE.forward (src/race_baseline.py:41-44).  For
+ * each of `rows` rows x (head_dim values) and table l < num_tables, with
+ * K = planes_per_table, R = 2^K and planes_T [head_dim][num_tables * K] fp32
+ * (the reference's planes_T buffer, src/race_baseline.py:27):
+ *   u_k = tanh(<x, planes_T[:, l K + k]>) / sqrt(head_dim),
+ *   probs[row][l][r] = softmax_r(sum_k u_k s_{r,k}),
+ * s_r the r-th of itertools.product([-1, 1], repeat=K) (s_{r,k} = +1 iff bit
+ * K-1-k of r is set).  x and probs share `dtype`.  Limits: head_dim <= 128,
+ * K <= 8, num_tables * K <= 64, num_tables * 2^K <= 256. */
+race_status race_hash_probs(const void* x, const float* planes_T, void* probs, int64_t rows,
+                            int32_t head_dim, int32_t num_tables, int32_t planes_per_table,
+                            int32_t dtype, hipStream_t stream);
+
 /* race_noncausal_bwd / race_causal_bwd with a hipEventRecord on `stream`
  * before the first launch and after every launch, as race_fwd_profiled does.
  * Profiling aids with no counterpart in the reference (used by bench.py). */

@@ -26,6 +26,10 @@ What is here, and which reference lines each piece restates
 * ``torch_noncausal_autograd`` -- torch.autograd on the non-causal formula
   (analysis/hot-path.md:157-162), the oracle the non-causal benchmark names for the
   gradients.
+* ``hash_probs`` -- numpy restatement (fp64) of the hashing that produces the
+  probabilities, src/race_baseline.py:41-44; ``hash_probs_product_form`` is
+  the same function through the product identity softmax_r(sum_k u_k s_rk) =
+  prod_k sigmoid(2 u_k s_rk), an independent evaluation that pins it.
 * ``causal_bwd`` -- the closed-form VJP of the causal function (race_oracle.c,
   fp64).  The reference has no causal backward kernel; its outline is
   docs/causal_v2_design.md:689-742.  ``torch_causal_autograd`` is
@@ -255,3 +259,33 @@ def torch_causal_autograd(q, k, v, g, eps: float = EPS):
     out = torch_causal_reference(qt, kt, vt, eps)
     dq, dk, dv = torch.autograd.grad(out, (qt, kt, vt), gt)
     return out.detach().numpy(), dq.numpy(), dk.numpy(), dv.numpy()
+
+
+def corners(K: int) -> np.ndarray:
+    """[2^K, K] corners in itertools.product([-1, 1], repeat=K) order
+    (src/race_baseline.py:28-30): s[r, k] = +1 iff bit K-1-k of r is set."""
+    r = np.arange(1 << K)[:, None]
+    return np.where((r >> (K - 1 - np.arange(K))[None, :]) & 1, 1.0, -1.0)
+
+
+def hash_probs(x, planes_T, L: int, K: int):
+    """src/race_baseline.py:41-44 in fp64: softmax over the corners of
+    tanh(x planes_T) / sqrt(d_k) projected on the corners.  x [..., d_k] ->
+    [..., L, 2^K]."""
+    x = np.asarray(x, np.float64)
+    dk = x.shape[-1]
+    proj = (x @ np.asarray(planes_T, np.float64)).reshape(*x.shape[:-1], L, K)
+    logits = (np.tanh(proj) / np.sqrt(dk)) @ corners(K).T
+    logits = logits - logits.max(-1, keepdims=True)
+    e = np.exp(logits)
+    return e / e.sum(-1, keepdims=True)
+
+
+def hash_probs_product_form(x, planes_T, L: int, K: int):
+    """The same probabilities as prod_k sigmoid(2 u_k s_{r,k})."""
+    x = np.asarray(x, np.float64)
+    dk = x.shape[-1]
+    u = np.tanh((x @ np.asarray(planes_T, np.float64)).reshape(*x.shape[:-1], L, K)) / np.sqrt(dk)
+    s = corners(K)                                          # [R, K]
+    z = 2.0 * u[..., None, :] * s                           # [..., L, R, K]
+    return (1.0 / (1.0 + np.exp(-z))).prod(-1)

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "race_causal_bwd",
     "race_noncausal_bwd_profiled",
     "race_causal_bwd_profiled",
+    "race_hash_probs",
 )
 
 
@@ -80,6 +81,7 @@ def lib() -> ctypes.CDLL:
                                                   vp, ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         L.race_causal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp,
                                                ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
+        L.race_hash_probs.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32, vp]
         for name in EXPORTED_SYMBOLS[2:]:
             getattr(L, name).restype = i32
         _configured = True
@@ -184,3 +186,9 @@ def causal_bwd_profiled(q, k, v, g, dq, dk, dv, sh: RaceShape, opts, workspace,
                                         workspace, workspace_bytes, stream, events, len(events),
                                         ctypes.byref(n))
     return st, n.value
+
+
+def hash_probs(x: int, planes_T: int, probs: int, rows: int, head_dim: int, num_tables: int,
+               planes_per_table: int, dtype: int, stream: int) -> int:
+    return lib().race_hash_probs(x, planes_T, probs, rows, head_dim, num_tables, planes_per_table,
+                                 dtype, stream)

@@ -1,20 +1,18 @@
 """Drop-in BatchedACE (src/race_baseline.py:21-52) running the op on MI355X.
 
-Same constructor and forward signature as the reference module.  Lines 35-44
-of the reference (permutes, shared hash planes, tanh, corner softmax) run as
-torch ops, exactly as there; lines 45-51 (the cumsum/bmm hot span) are
-replaced by race_fused_fwd; line 52 (permute back) is kept.
+Same constructor and forward signature as the reference module.  The
+permutes of lines 35-40 and 52 stay torch ops; the hashing of lines 41-44
+(shared hash planes, tanh, corner softmax) runs as the race_hash_probs HIP
+kernel and lines 45-51 (the cumsum/bmm hot span) as race_fused_fwd.
 """
 from __future__ import annotations
 
 import itertools
-import math
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
-from .ops import race_fused_fwd
+from .ops import race_fused_fwd, race_hash_probs
 
 
 class BatchedACE(nn.Module):
@@ -31,9 +29,7 @@ class BatchedACE(nn.Module):
 
     def bucket_probs(self, x2: torch.Tensor) -> torch.Tensor:
         """[N, T, d] -> [N, T, L, R] corner probabilities (reference lines 41-44)."""
-        N, T, dk = x2.shape
-        proj = (x2 @ self.planes_T).view(N, T, self.L, self.K)
-        return F.softmax(proj.tanh().div(math.sqrt(dk)) @ self.protos_T, dim=-1)
+        return race_hash_probs(x2, self.planes_T.float(), self.L, self.K)
 
     def forward(self, Khf, Vhf, Qhf):
         M, B, T, H, dk = Khf.shape

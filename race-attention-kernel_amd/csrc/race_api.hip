@@ -545,3 +545,23 @@ race_status race_causal_bwd_profiled(const void* probsQ, const void* probsK, con
 }
 
 }  // extern "C"
+
+extern "C" {
+
+race_status race_hash_probs(const void* x, const float* planes_T, void* probs, int64_t rows,
+                            int32_t head_dim, int32_t num_tables, int32_t planes_per_table,
+                            int32_t dtype, hipStream_t stream) {
+    if (!hash_shape_ok(rows, head_dim, num_tables, planes_per_table)) return RACE_ERROR_INVALID_VALUE;
+    if (dtype != RACE_F32 && dtype != RACE_BF16) return RACE_ERROR_INVALID_VALUE;
+    if (rows == 0) return RACE_SUCCESS;
+    if (!x || !planes_T || !probs) return RACE_ERROR_INVALID_VALUE;
+    if (!aligned16(x) || !aligned16(planes_T) || !aligned16(probs)) return RACE_ERROR_INVALID_VALUE;
+    int lds_limit = 0;
+    RACE_TRY(max_lds(&lds_limit));
+    if (hash_lds_bytes(head_dim, num_tables, planes_per_table) > size_t(lds_limit))
+        return RACE_ERROR_INVALID_VALUE;
+    return launch_hash_probs(x, planes_T, probs, rows, head_dim, num_tables, planes_per_table,
+                             dtype, stream);
+}
+
+}  // extern "C"

@@ -155,6 +155,12 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
                                       const float* suffix_records, void* dK, void* dV,
                                       const Problem& p, hipStream_t stream);
 
+// ---- bucket-probability front end (hashing.hip) ----
+bool hash_shape_ok(int64_t rows, int dk, int L, int K);
+size_t hash_lds_bytes(int dk, int L, int K);
+hipError_t launch_hash_probs(const void* x, const float* planes_T, void* probs, int64_t rows,
+                            int dk, int L, int K, int dtype, hipStream_t stream);
+
 // Whether the MFMA causal path has a specialization for (S, d).
 bool mfma_causal_supported(int S, int d);
 hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void* out,

@@ -8,6 +8,7 @@
 //                      tile_tokens=0) -> (dQ or None, dK or None, dV or None)
 //   causal_backward(probsQ, probsK, V, dOut, need_q, need_k, need_v,
 //                   tile_tokens=0, kernel=0) -> (dQ or None, dK or None, dV or None)
+//   hash_probs(x, planes_T, L, K) -> [..., L, 2^K] bucket probabilities
 //   select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens=0, kernel=0) -> int
 //   shape_supported(L, R, d) -> (supported, has_mfma)
 //
@@ -24,6 +25,7 @@
 
 #include <cstdint>
 #include <tuple>
+#include <vector>
 
 #include "race_mi355x.h"
 
@@ -208,6 +210,36 @@ causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
     return {opt(need_q, dq), opt(need_k, dk), opt(need_v, dv)};
 }
 
+// [..., d_k] rows -> [..., L, 2^K] bucket probabilities (src/race_baseline.py:41-44).
+at::Tensor hash_probs(const at::Tensor& x, const at::Tensor& planes_T, int64_t L, int64_t K) {
+    TORCH_CHECK(x.is_cuda(), "x must be a GPU tensor");
+    TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kBFloat16,
+                "x must be float32 or bfloat16");
+    TORCH_CHECK(x.is_contiguous() && reinterpret_cast<uintptr_t>(x.data_ptr()) % kAlignment == 0,
+                "x must be contiguous and 16-byte aligned");
+    TORCH_CHECK(x.dim() >= 1, "x must have a feature dimension");
+    const int64_t dk = x.size(-1);
+    TORCH_CHECK(planes_T.is_cuda() && planes_T.device() == x.device() &&
+                    planes_T.scalar_type() == at::kFloat && planes_T.is_contiguous() &&
+                    planes_T.dim() == 2 && planes_T.size(0) == dk && planes_T.size(1) == L * K,
+                "planes_T must be a contiguous fp32 [d_k, L*K] tensor on x's device");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(planes_T.data_ptr()) % kAlignment == 0,
+                "planes_T must be 16-byte aligned");
+    const int64_t rows = x.numel() / dk;
+    std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end() - 1);
+    shape.push_back(L);
+    shape.push_back(int64_t(1) << K);
+    const c10::DeviceGuard guard(x.device());
+    at::Tensor probs = at::empty(shape, x.options());
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+    check_status(race_hash_probs(x.data_ptr(), planes_T.data_ptr<float>(), probs.data_ptr(), rows,
+                                 static_cast<int32_t>(dk), static_cast<int32_t>(L),
+                                 static_cast<int32_t>(K),
+                                 x.scalar_type() == at::kBFloat16 ? RACE_BF16 : RACE_F32, stream),
+                 "race_hash_probs");
+    return probs;
+}
+
 int64_t select_tile_tokens(int64_t N, int64_t T, int64_t L, int64_t R, int64_t d, bool bf16,
                            bool causal, int64_t tile_tokens, int64_t kernel) {
     race_shape sh{N, T, static_cast<int32_t>(L), static_cast<int32_t>(R),
@@ -246,6 +278,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("dOut"),
           py::arg("need_q") = true, py::arg("need_k") = true, py::arg("need_v") = true,
           py::arg("tile_tokens") = 0, py::arg("kernel") = 0);
+    m.def("hash_probs", &hash_probs, "Bucket probabilities of token rows -> [..., L, 2^K]",
+          py::arg("x"), py::arg("planes_T"), py::arg("L"), py::arg("K"));
     m.def("select_tile_tokens", &select_tile_tokens, "Tile length a forward would use",
           py::arg("N"), py::arg("T"), py::arg("L"), py::arg("R"), py::arg("d"),
           py::arg("bf16") = false, py::arg("causal") = true, py::arg("tile_tokens") = 0,

@@ -129,3 +129,10 @@ def select_tile_tokens(N: int, T: int, L: int, R: int, d: int, *, bf16: bool = F
                        causal: bool = True, tile_tokens: int = 0, kernel: str | int = "auto") -> int:
     return _lib.ext().select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens,
                                          _kernel_id(kernel))
+
+
+def race_hash_probs(x: torch.Tensor, planes_T: torch.Tensor, L: int, K: int) -> torch.Tensor:
+    """Bucket probabilities [..., L, 2^K] of token rows x [..., d_k]: the
+    hashing of src/race_baseline.py:41-44 (tanh of the shared-plane
+    projections over sqrt(d_k), softmax over the 2^K corners), on the GPU."""
+    return _lib.ext().hash_probs(_dense(x), planes_T.contiguous(), int(L), int(K))

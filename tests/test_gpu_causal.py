@@ -252,7 +252,7 @@ def test_final_state_is_the_decode_handoff(race, oracle, cuda):
 
 
 def test_batched_ace_dropin(race, oracle, cuda):
-    # The drop-in module: the reference's hashing in torch, the op on the GPU.
+    # The drop-in module's op against the oracle on the module's own probabilities.
     say("batched-ace")
     torch.manual_seed(1234)
     ace = race.BatchedACE(64, 4, 4, 1).to(cuda)

@@ -353,3 +353,43 @@ def test_planted_backward_mistakes_are_caught(golden):
     # The denominator's gradient dropped: dk fails.
     got = _mutant_bwd(q, k, v, g, drop_alpha=True)
     assert rel_err(got[1], want[1]) > 1e-3
+
+
+# --- the hashing front end (src/race_baseline.py:41-44) --------------------------------------
+
+@pytest.mark.parametrize("dk, L, K", [(64, 4, 4), (8, 1, 1), (128, 8, 5), (16, 2, 8)])
+def test_hash_probs_product_identity_and_invariants(oracle, dk, L, K):
+    rng = np.random.default_rng(40 + K)
+    x = rng.standard_normal((3, 17, dk)).astype(np.float32)
+    planes_T = rng.standard_normal((dk, L * K)).astype(np.float32)
+    p = oracle.hash_probs(x, planes_T, L, K)
+    assert p.shape == (3, 17, L, 1 << K)
+    assert rel_err(p, oracle.hash_probs_product_form(x, planes_T, L, K)) <= FP64_TOL
+    np.testing.assert_allclose(p.sum(-1), 1.0, atol=1e-13)
+    # x = 0 gives uniform probabilities; -x maps corner r to its complement.
+    np.testing.assert_allclose(oracle.hash_probs(np.zeros((2, dk)), planes_T, L, K), 1.0 / (1 << K))
+    assert rel_err(oracle.hash_probs(-x, planes_T, L, K), p[..., ::-1]) <= FP64_TOL
+
+
+def test_hash_probs_corner_order(oracle):
+    # itertools.product([-1, 1], repeat=3): r = 0 is (-1,-1,-1), r = 1 is (-1,-1,+1), r = 7 all +1.
+    s = oracle.corners(3)
+    assert s[0].tolist() == [-1, -1, -1] and s[1].tolist() == [-1, -1, 1] and s[7].tolist() == [1, 1, 1]
+    # One positive projection on plane k=0 favours the corners with s_0 = +1 (r >= 4).
+    planes_T = np.zeros((2, 3))
+    planes_T[0, 0] = 50.0
+    p = oracle.hash_probs(np.array([[1.0, 0.0]]), planes_T, 1, 3)[0, 0]
+    assert p[4:].min() > p[:4].max()
+
+
+def test_hash_probs_matches_torch_composition(oracle):
+    import torch
+
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((2, 33, 64))
+    planes_T = rng.standard_normal((64, 16))
+    protos_T = torch.from_numpy(oracle.corners(4).T.copy())
+    xt = torch.from_numpy(x)
+    proj = (xt @ torch.from_numpy(planes_T)).view(2, 33, 4, 4)
+    want = torch.softmax(proj.tanh().div(8.0) @ protos_T, dim=-1).numpy()
+    assert rel_err(oracle.hash_probs(x, planes_T, 4, 4), want) <= FP64_TOL
