@@ -35,7 +35,7 @@ line for that configuration; the CPU baseline belongs to the headline
 (cfg2 forward) only.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
-                       [--pass fwd|bwd|fwdbwd] [--T T] [--kernel auto|valu|mfma|mfma_wg]
+                       [--pass fwd|bwd|fwdbwd|module] [--T T] [--kernel auto|valu|mfma|mfma_wg]
                        [--tile N] [--no-cpu-baseline] [--calibrate-copy MIB]
 """
 from __future__ import annotations
@@ -130,9 +130,11 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
-    ap.add_argument("--pass", dest="pass_", choices=["fwd", "bwd", "fwdbwd"], default="fwd",
+    ap.add_argument("--pass", dest="pass_", choices=["fwd", "bwd", "fwdbwd", "module"],
+                    default="fwd",
                     help="what one step runs: the forward (default), the backward (from the "
-                         "forward's inputs and a synthetic dOut) or both")
+                         "forward's inputs and a synthetic dOut), both, or the module's hot "
+                         "span (hashing of Q and K rows, then the forward)")
     ap.add_argument("--T", type=int, default=0)
     ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
@@ -168,6 +170,8 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
         "bwd_finalize": small,
         "token_map_dk": es * (d + S) * NT,
         "token_map_dv": es * (S + d) * NT,
+        "hash_q": es * (d + S) * NT,               # rows of d_k = d -> probabilities
+        "hash_k": es * (d + S) * NT,
     }.get(name, es * (2 * S + 2 * d) * NT)
 
 
@@ -176,7 +180,8 @@ def op_bytes(pass_: str, cfg, T: int, es: int) -> float:
     the backward reads Q, K, V, dOut and writes dQ, dK, dV."""
     S, d, NT = cfg.S, cfg.d, cfg.N * T
     fwd, bwd = es * (2 * S + 2 * d) * NT, es * (4 * S + 3 * d) * NT
-    return {"fwd": fwd, "bwd": bwd, "fwdbwd": fwd + bwd}[pass_]
+    hashing = 2 * es * (d + S) * NT
+    return {"fwd": fwd, "bwd": bwd, "fwdbwd": fwd + bwd, "module": hashing + fwd}[pass_]
 
 
 def traffic_for(workload_key: str, kernel_name: str):
@@ -277,7 +282,24 @@ def main() -> int:
             raise RuntimeError(abi.status_string(st_))
 
     # One step of the chosen pass: plain(), and profiled(events) -> events used.
-    run_fwd = args.pass_ in ("fwd", "fwdbwd")
+    run_hash = args.pass_ == "module"
+    if run_hash:
+        # The module's inputs: Q and K rows [N, T, d_k] and the shared planes;
+        # the hashing writes the probabilities the forward then reads.
+        if not cfg.causal or cfg.R & (cfg.R - 1):
+            raise SystemExit("--pass module needs a causal workload with R a power of two")
+        Kp = cfg.R.bit_length() - 1
+        gen = torch.Generator(device=dev).manual_seed(11)
+        xq = torch.randn(cfg.N, T, cfg.d, device=dev, generator=gen).to(v.dtype)
+        xk = torch.randn(cfg.N, T, cfg.d, device=dev, generator=gen).to(v.dtype)
+        planes_T = torch.randn(cfg.d, cfg.L * Kp, device=dev, generator=gen)
+        hdt = abi.RACE_BF16 if es == 2 else abi.RACE_F32
+
+        def hash_both():
+            for x_, p_ in ((xq, q), (xk, k)):
+                check(abi.hash_probs(x_.data_ptr(), planes_T.data_ptr(), p_.data_ptr(), cfg.N * T,
+                                     cfg.d, cfg.L, Kp, hdt, stream))
+    run_fwd = args.pass_ in ("fwd", "fwdbwd", "module")
     run_bwd = args.pass_ in ("bwd", "fwdbwd")
     state = None
     if run_bwd:
@@ -299,6 +321,8 @@ def main() -> int:
     sptr = state.data_ptr() if state is not None else None
 
     def plain():
+        if run_hash:
+            hash_both()
         if run_fwd:
             check(abi.fwd(*ptrs, sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
         if run_bwd:
@@ -310,11 +334,19 @@ def main() -> int:
 
     def profiled(evs):
         n_used = 0
+        if run_hash:
+            events.record(evs[0], stream)
+            for j, (x_, p_) in enumerate(((xq, q), (xk, k))):
+                check(abi.hash_probs(x_.data_ptr(), planes_T.data_ptr(), p_.data_ptr(), cfg.N * T,
+                                     cfg.d, cfg.L, Kp, hdt, stream))
+                events.record(evs[j + 1], stream)
+            n_used = 3
         if run_fwd:
+            tail = (ctypes.c_void_p * (len(evs) - n_used)).from_buffer(evs, n_used * ctypes.sizeof(ctypes.c_void_p))
             st_, n = abi.fwd_profiled(*ptrs, sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
-                                      stream, evs)
+                                      stream, tail)
             check(st_)
-            n_used = n
+            n_used += n
         if run_bwd:
             tail = (ctypes.c_void_p * (len(evs) - n_used)).from_buffer(evs, n_used * ctypes.sizeof(ctypes.c_void_p))
             if cfg.causal:
@@ -328,6 +360,8 @@ def main() -> int:
         return n_used
 
     names = []
+    if run_hash:
+        names += ["hash_q", "hash_k"]
     if run_fwd:
         names += PHASES.get((cfg.causal, family), [])
     if run_bwd:
@@ -380,6 +414,8 @@ def main() -> int:
     n_fwd = len(PHASES.get((cfg.causal, family), [])) if run_fwd else 0
     if run_fwd and run_bwd:
         gaps = gaps[:n_fwd] + gaps[n_fwd + 1:]
+    if run_hash:  # the forward's first event follows the hashing's last one
+        gaps = gaps[:2] + gaps[3:]
     n_launch = len(gaps)
     phase_ms = gaps
     if len(names) != n_launch:
@@ -444,6 +480,8 @@ def main() -> int:
     del q, k, v, out, ws
     if run_bwd:
         del g, dq, dk, dv, bws
+    if run_hash:
+        del xq, xk, planes_T
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline and headline:
         result["cpu_baseline"] = cpu_baseline()

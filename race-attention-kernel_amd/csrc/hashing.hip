@@ -7,10 +7,17 @@
 //     u_k      = tanh(<x, planes_T[:, l K + k]>) / sqrt(d_k)
 //     logit_r  = sum_k u_k s_{r,k}
 //     probs[l] = softmax_r(logit)
-// One workgroup owns 64 token rows: the rows and the planes are staged in
-// LDS (rows padded by one float so the per-table dot products are
-// conflict-free), each thread computes one (row, table) pair, and the 64 x
-// L x R probabilities are written back through LDS with coalesced stores.
+// The corner softmax factorises: exp(sum_k s_k u_k) / prod_k (e^u_k + e^-u_k)
+// = prod_k sigma(2 s_k u_k), so a table costs K exponentials, not 2^K.
+// One workgroup owns 256 token rows, one per thread:
+//   1. the rows are staged in LDS 32 columns at a time (coalesced 16-byte
+//      loads, the next chunk prefetched into registers), and each thread
+//      accumulates its row's L*K projections against LDS broadcasts of the
+//      planes;
+//   2. the sigmoids sigma(2 u_k) are written to LDS, one row per thread;
+//   3. the L x 2^K probabilities of the 256 rows are written out in memory
+//      order, four per thread per step (16-byte stores for fp32).
+#include <algorithm>
 #include <cmath>
 
 #include "race_internal.h"
@@ -18,64 +25,155 @@
 namespace race {
 namespace {
 
-constexpr int kHashRows = 64;
+constexpr int kHashRows = kThreads;
+constexpr int kChunk = 32;              // x columns staged per step
+constexpr int kXPitch = kChunk + 4;     // odd count of 16-byte words: b128 reads conflict-free
+constexpr int kGroups = kChunk / 4;     // 4-column groups per staged row
 
 template <typename TIn>
+struct Quad;
+template <>
+struct Quad<float> {
+    float4 v;
+    __device__ void load(const float* p) { v = *reinterpret_cast<const float4*>(p); }
+    __device__ float4 f32() const { return v; }
+};
+template <>
+struct Quad<bf16_t> {
+    uint2 v;
+    __device__ void load(const bf16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+    __device__ float4 f32() const {
+        return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+    }
+};
+
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+__device__ __forceinline__ void store4(bf16_t* p, float a, float b, float c, float d) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16),
+                                              uint32_t(f32_to_bf16(c)) | (uint32_t(f32_to_bf16(d)) << 16));
+}
+
+// Loads the 4-column groups of one staged chunk owned by this thread: group
+// g = tid + 256 i is row g / 8, columns c0 + 4 (g % 8) .. + 3.  Vec: d_k is a
+// multiple of 4, so a group is one aligned vector load; columns past d_k and
+// rows past the tile read as zero.
+template <typename TIn, bool Vec>
+__device__ __forceinline__ void load_chunk(float4 (&xr)[kGroups], const TIn* __restrict__ x,
+                                           int64_t row0, int cnt, int dk, int c0, int tid) {
+#pragma unroll
+    for (int i = 0; i < kGroups; ++i) {
+        const int g = tid + kThreads * i, row = g / kGroups, col = c0 + 4 * (g % kGroups);
+        const TIn* src = x + (row0 + row) * dk + col;
+        if (Vec) {
+            if (row < cnt && col < dk) {
+                Quad<TIn> q;
+                q.load(src);
+                xr[i] = q.f32();
+            } else {
+                xr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        } else {
+            float e[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = (row < cnt && col + t < dk) ? to_f32(src[t]) : 0.f;
+            xr[i] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    }
+}
+
+template <typename TIn, int LKT, bool Vec>
 __global__ __launch_bounds__(kThreads) void hash_probs_kernel(const TIn* __restrict__ x,
                                                               const float* __restrict__ planes_T,
                                                               TIn* __restrict__ probs, int64_t rows,
                                                               int dk, int L, int K) {
     extern __shared__ float smem[];
-    const int LK = L * K, R = 1 << K, LR = L * R;
-    const int xp = dk + 1;  // padded row pitch
-    float* xs = smem;                  // [kHashRows][dk + 1]
-    float* pl = xs + kHashRows * xp;   // [dk][L*K]
-    float* os = pl + dk * LK;          // [kHashRows][L*R]
+    const int LK = L * K, R = 1 << K, LR = L * R, dk4 = (dk + 3) & ~3;
+    float* pl = smem;                  // [dk4][LKT], zero past d_k rows and L*K columns
+    float* xs = pl + dk4 * LKT;        // [256][kXPitch] staged x, then [256][LK + 1] sigmoids
     const int tid = threadIdx.x;
     const int64_t row0 = int64_t(blockIdx.x) * kHashRows;
     const int cnt = int(min<int64_t>(kHashRows, rows - row0));
 
-    for (int e = tid; e < dk * LK; e += kThreads) pl[e] = planes_T[e];
-    for (int e = tid; e < cnt * dk; e += kThreads) {
-        const int i = e / dk, c = e - i * dk;
-        xs[i * xp + c] = to_f32(x[row0 * dk + e]);
+    for (int e = tid; e < dk4 * LKT; e += kThreads) {
+        const int c = e / LKT, j = e - c * LKT;
+        pl[e] = (j < LK && c < dk) ? planes_T[c * LK + j] : 0.f;
     }
-    __syncthreads();
-    const float inv_scale = 1.0f / sqrtf(float(dk));
-    for (int e = tid; e < cnt * L; e += kThreads) {
-        const int i = e / L, l = e - i * L;
-        float u[8];
+
+    float acc[LKT];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (k >= K) break;
-            float acc = 0.f;
-            for (int c = 0; c < dk; ++c) acc = fmaf(xs[i * xp + c], pl[c * LK + l * K + k], acc);
-            u[k] = tanhf(acc) * inv_scale;
+    for (int j = 0; j < LKT; ++j) acc[j] = 0.f;
+    float4 xr[kGroups];
+    load_chunk<TIn, Vec>(xr, x, row0, cnt, dk, 0, tid);
+    for (int c0 = 0; c0 < dk; c0 += kChunk) {
+        __syncthreads();  // the previous chunk has been read
+#pragma unroll
+        for (int i = 0; i < kGroups; ++i) {
+            const int g = tid + kThreads * i;
+            *reinterpret_cast<float4*>(xs + (g / kGroups) * kXPitch + 4 * (g % kGroups)) = xr[i];
         }
-        // logit_r = sum_k u_k s_{r,k}; softmax over the corners.
-        float mx = -INFINITY;
-        for (int r = 0; r < R; ++r) {
-            float lg = 0.f;
+        __syncthreads();
+        if (c0 + kChunk < dk) load_chunk<TIn, Vec>(xr, x, row0, cnt, dk, c0 + kChunk, tid);
+        const int width = min(kChunk, dk4 - c0);
+        const float* xrow = xs + tid * kXPitch;
+        for (int cc = 0; cc < width; cc += 4) {
+            const float4 xv = *reinterpret_cast<const float4*>(xrow + cc);
+            const float xc[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float* prow = pl + (c0 + cc + u) * LKT;
+#pragma unroll
+                for (int j = 0; j < LKT; j += 4) {
+                    const float4 pv = *reinterpret_cast<const float4*>(prow + j);
+                    acc[j] = fmaf(xc[u], pv.x, acc[j]);
+                    acc[j + 1] = fmaf(xc[u], pv.y, acc[j + 1]);
+                    acc[j + 2] = fmaf(xc[u], pv.z, acc[j + 2]);
+                    acc[j + 3] = fmaf(xc[u], pv.w, acc[j + 3]);
+                }
+            }
+        }
+    }
+
+    // sigma(2 u) with u = tanh(projection) / sqrt(d_k); |u| <= 1, no overflow.
+    const float two_over_scale = 2.0f / sqrtf(float(dk));
+    __syncthreads();  // the staged x is dead: its space takes the sigmoids
+    float* sg = xs + tid * (LK + 1);
+#pragma unroll
+    for (int j = 0; j < LKT; ++j)
+        if (j < LK) sg[j] = 1.0f / (1.0f + expf(-two_over_scale * tanhf(acc[j])));
+    __syncthreads();
+
+    // probs[row][l][r] = prod_k (bit K-1-k of r ? sigma_k : 1 - sigma_k).
+    if (K >= 2) {  // L * R is a multiple of 4: four corners of one table per step
+        const int quads = LR / 4, total = cnt * quads;
+        for (int g = tid; g < total; g += kThreads) {
+            const int row = g / quads, c = 4 * (g - row * quads);
+            const int l = c >> K, r0 = c & (R - 1);
+            const float* s = xs + row * (LK + 1) + l * K;
+            float p[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                if (k >= K) break;
-                lg += ((r >> (K - 1 - k)) & 1) ? u[k] : -u[k];
+                if (k < K) {
+                    const float sk = s[k], sn = 1.0f - sk;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) p[t] *= (((r0 + t) >> (K - 1 - k)) & 1) ? sk : sn;
+                }
             }
-            os[i * LR + l * R + r] = lg;
-            mx = fmaxf(mx, lg);
+            store4(probs + (row0 + row) * LR + c, p[0], p[1], p[2], p[3]);
         }
-        float sum = 0.f;
-        for (int r = 0; r < R; ++r) {
-            const float ex = expf(os[i * LR + l * R + r] - mx);
-            os[i * LR + l * R + r] = ex;
-            sum += ex;
+    } else {  // K = 1: two corners per table
+        const int total = cnt * LR;
+        for (int e = tid; e < total; e += kThreads) {
+            const int row = e / LR, c = e - row * LR;
+            const float sk = xs[row * (LK + 1) + (c >> 1)];
+            store_val(probs + (row0 + row) * LR + c, (c & 1) ? sk : 1.0f - sk);
         }
-        const float inv = 1.0f / sum;
-        for (int r = 0; r < R; ++r) os[i * LR + l * R + r] *= inv;
     }
-    __syncthreads();
-    for (int e = tid; e < cnt * LR; e += kThreads) store_val(probs + row0 * LR + e, os[e]);
 }
+
+int lk_tier(int LK) { return LK <= 16 ? 16 : LK <= 32 ? 32 : 64; }
 
 }  // namespace
 
@@ -85,20 +183,39 @@ bool hash_shape_ok(int64_t rows, int dk, int L, int K) {
 }
 
 size_t hash_lds_bytes(int dk, int L, int K) {
-    return size_t(kHashRows * (dk + 1) + dk * L * K + kHashRows * L * (1 << K)) * sizeof(float);
+    const int dk4 = (dk + 3) & ~3;
+    return size_t(dk4 * lk_tier(L * K) + kHashRows * std::max(kXPitch, L * K + 1)) * sizeof(float);
 }
 
 hipError_t launch_hash_probs(const void* x, const float* planes_T, void* probs, int64_t rows,
                             int dk, int L, int K, int dtype, hipStream_t stream) {
     const dim3 grid(unsigned((rows + kHashRows - 1) / kHashRows));
     const size_t lds = hash_lds_bytes(dk, L, K);
-    if (dtype == RACE_BF16) {
-        hash_probs_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
-            static_cast<const bf16_t*>(x), planes_T, static_cast<bf16_t*>(probs), rows, dk, L, K);
-    } else {
-        hash_probs_kernel<float><<<grid, kThreads, lds, stream>>>(
-            static_cast<const float*>(x), planes_T, static_cast<float*>(probs), rows, dk, L, K);
+    const bool vec = dk % 4 == 0;
+#define RACE_HASH(TIN, LKT, VEC)                                                             \
+    hash_probs_kernel<TIN, LKT, VEC><<<grid, kThreads, lds, stream>>>(                       \
+        static_cast<const TIN*>(x), planes_T, static_cast<TIN*>(probs), rows, dk, L, K)
+#define RACE_HASH_LK(TIN, VEC)                         \
+    switch (lk_tier(L * K)) {                          \
+        case 16: RACE_HASH(TIN, 16, VEC); break;       \
+        case 32: RACE_HASH(TIN, 32, VEC); break;       \
+        default: RACE_HASH(TIN, 64, VEC); break;       \
     }
+    if (dtype == RACE_BF16) {
+        if (vec) {
+            RACE_HASH_LK(bf16_t, true)
+        } else {
+            RACE_HASH_LK(bf16_t, false)
+        }
+    } else {
+        if (vec) {
+            RACE_HASH_LK(float, true)
+        } else {
+            RACE_HASH_LK(float, false)
+        }
+    }
+#undef RACE_HASH_LK
+#undef RACE_HASH
     return hipGetLastError();
 }
 
