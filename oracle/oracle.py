@@ -30,6 +30,15 @@ What is here, and which reference lines each piece restates
   probabilities, src/race_baseline.py:41-44; ``hash_probs_product_form`` is
   the same function through the product identity softmax_r(sum_k u_k s_rk) =
   prod_k sigmoid(2 u_k s_rk), an independent evaluation that pins it.
+* ``alg1_causal`` -- the causal forward with the hashing inside and one
+  global normalization per query (paper Algorithm 1 made causal), fp64
+  (race_oracle.c), following src/causal_v2/reference.py:100-128 with the
+  softmax feature map of src/noncausal/reference.py:89-100; ``perbucket=True``
+  is the per-bucket bridge of src/causal_v2/reference.py:144-159.  Pinned by
+  ``alg1_dense`` (the masked T x T form of src/causal_v2/reference.py:131-141),
+  ``alg1_features(form="bernoulli")`` (the product form of
+  src/noncausal/reference.py:103-125), the closed forms T = 1 and constant V,
+  and the bridge to ``hash_probs`` + ``causal_recurrence`` at beta = 1/sqrt(d).
 * ``causal_bwd`` -- the closed-form VJP of the causal function (race_oracle.c,
   fp64).  The reference has no causal backward kernel; its outline is
   docs/causal_v2_design.md:689-742.  ``torch_causal_autograd`` is
@@ -79,8 +88,11 @@ def _load():
         lib.race_oracle_noncausal_fwd.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i]
         lib.race_oracle_noncausal_bwd.argtypes = [f32p, f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i]
         lib.race_oracle_causal_bwd.argtypes = [f32p, f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i]
+        lib.race_oracle_alg1_causal.argtypes = [f32p, f32p, f32p, f32p, d, f64p, f64p, f64p, i64, i64, i64, i64,
+                                                i64, i, d, i64, i]
         for name in ("race_oracle_causal_recurrence", "race_oracle_causal_chunked", "race_oracle_causal_tiled",
-                     "race_oracle_noncausal_fwd", "race_oracle_noncausal_bwd", "race_oracle_causal_bwd"):
+                     "race_oracle_noncausal_fwd", "race_oracle_noncausal_bwd", "race_oracle_causal_bwd",
+                     "race_oracle_alg1_causal"):
             getattr(lib, name).restype = None
         _lib = lib
     return _lib
@@ -289,3 +301,64 @@ def hash_probs_product_form(x, planes_T, L: int, K: int):
     s = corners(K)                                          # [R, K]
     z = 2.0 * u[..., None, :] * s                           # [..., L, R, K]
     return (1.0 / (1.0 + np.exp(-z))).prod(-1)
+
+
+def alg1_causal(q, k, v, W, beta: float, *, perbucket: bool = False, eps: float = EPS, tile: int = 0,
+                want_state: bool = False, nthreads: int = 0):
+    """Algorithm 1 with hashing, fp64 (race_oracle.c).  q, k, v [N, T, D]
+    (bf16 values widened exactly), W [L, P, D].  Returns out [N, T, D], plus
+    (prefix [N, tiles, S*D+S], final [N, S*D+S]) when tile > 0 or want_state
+    (prefix is None without a tile)."""
+    q, k, v, W = _f32(q), _f32(k), _f32(v), _f32(W)
+    N, T, D = q.shape
+    L, P = W.shape[0], W.shape[1]
+    assert W.shape[2] == D and k.shape == q.shape and v.shape == q.shape
+    S = L << P
+    rec = S * D + S
+    out = np.empty((N, T, D), np.float64)
+    tiles = -(-T // tile) if tile > 0 else 0
+    pref = np.empty((N, tiles, rec), np.float64) if tile > 0 else None
+    fin = np.empty((N, rec), np.float64) if (want_state or tile > 0) else None
+    _load().race_oracle_alg1_causal(
+        _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(W, ctypes.c_float),
+        float(beta), _ptr(out, ctypes.c_double), _ptr(pref, ctypes.c_double) if pref is not None else None,
+        _ptr(fin, ctypes.c_double) if fin is not None else None, N, T, D, L, P, int(perbucket), eps,
+        int(tile), nthreads)
+    if fin is None:
+        return out
+    return out, pref, fin
+
+
+def alg1_features(x, W, beta: float, form: str = "softmax"):
+    """Phi(x) [..., L*2^P] in fp64: the direct softmax over the corners
+    (src/noncausal/reference.py:89-100) or the Bernoulli product
+    prod_p sigmoid(+-2 beta u_p), built plane by plane with plane 0 as the
+    most significant bit (src/noncausal/reference.py:103-125)."""
+    x = np.asarray(x, np.float64)
+    W = np.asarray(W, np.float64)
+    L, P, _ = W.shape
+    u = np.tanh(np.einsum("...d,lpd->...lp", x, W))
+    if form == "softmax":
+        logits = beta * (u @ corners(P).T)
+        logits = logits - logits.max(-1, keepdims=True)
+        e = np.exp(logits)
+        phi = e / e.sum(-1, keepdims=True)
+    else:
+        plus = 1.0 / (1.0 + np.exp(-2.0 * beta * u))
+        minus = 1.0 / (1.0 + np.exp(2.0 * beta * u))
+        phi = np.ones(u.shape[:-1] + (1,))
+        for p in range(P):
+            phi = np.stack([phi * minus[..., p:p + 1], phi * plus[..., p:p + 1]], -1).reshape(
+                *u.shape[:-1], -1)
+    return phi.reshape(*x.shape[:-1], L * (1 << P))
+
+
+def alg1_dense(q, k, v, W, beta: float):
+    """Algorithm 1 as masked attention with kernel k_ij = <Phi(q_i), Phi(k_j)>,
+    j <= i (src/causal_v2/reference.py:131-141), fp64; tiny T only."""
+    fq, fk = alg1_features(q, W, beta), alg1_features(k, W, beta)
+    T = fq.shape[-2]
+    scores = fq @ np.swapaxes(fk, -1, -2) * np.tril(np.ones((T, T)))
+    den = scores.sum(-1, keepdims=True)
+    num = scores @ np.asarray(v, np.float64)
+    return np.where(den == 0, 0.0, num / np.where(den == 0, 1.0, den))

@@ -420,3 +420,100 @@ void race_oracle_causal_bwd(const float* q, const float* k, const float* v, cons
         free(Y);
     }
 }
+
+/* ------------------------------------------------------------------------
+ * Algorithm 1 with the hashing inside (the reference's causal v2 forward,
+ * src/causal_v2/kernels/race_causal_fwd.h:6-10; ground truth
+ * src/causal_v2/reference.py:100-128).  Token rows q, k, v are [N][T][D];
+ * the planes W are [L][P][D].  The feature map of a row x, table-major
+ * (s = l R + r, R = 2^P), is the direct length-R softmax of
+ * src/noncausal/reference.py:89-100:
+ *     u_p        = tanh(<W[l][p], x>)
+ *     phi_l[r]   = softmax_r(beta sum_p u_p c_{r,p}),
+ * c_{r,p} = +1 iff bit P-1-p of r is set (plane 0 the most significant,
+ * src/noncausal/reference.py:66-77).  With A_t, B_t the inclusive sums of
+ * phi(k_j) and phi(k_j) (x) v_j over j <= t:
+ *     global normalization (perbucket = 0):
+ *         out_t = (phi(q_t) . B_t) / (phi(q_t) . A_t), 0 where the
+ *         denominator is exactly 0 (src/causal_v2/reference.py:81-86);
+ *     per-bucket normalization (perbucket = 1, the bridge to
+ *     src/race_baseline.py:45-51, src/causal_v2/reference.py:144-159):
+ *         out_t = sum_s phi(q_t)[s] B_t[s][:] / (A_t[s] + eps).
+ * prefix (nullable, tile > 0): [N][ceil(T / tile)][S*D + S], the state before
+ * the first token of every tile (B then A); final_state (nullable):
+ * [N][S*D + S], the state after the last token.
+ */
+static void alg1_features(const float* x, const float* W, double beta, i64 D, i64 L, i64 P,
+                          double* u, double* phi) {
+    const i64 R = (i64)1 << P;
+    for (i64 l = 0; l < L; ++l) {
+        for (i64 p = 0; p < P; ++p) {
+            const float* w = W + (l * P + p) * D;
+            double acc = 0.0;
+            for (i64 c = 0; c < D; ++c) acc += (double)w[c] * (double)x[c];
+            u[p] = tanh(acc);
+        }
+        double* ph = phi + l * R;
+        double mx = -INFINITY;
+        for (i64 r = 0; r < R; ++r) {
+            double lg = 0.0;
+            for (i64 p = 0; p < P; ++p) lg += ((r >> (P - 1 - p)) & 1) ? u[p] : -u[p];
+            ph[r] = beta * lg;
+            if (ph[r] > mx) mx = ph[r];
+        }
+        double sum = 0.0;
+        for (i64 r = 0; r < R; ++r) {
+            ph[r] = exp(ph[r] - mx);
+            sum += ph[r];
+        }
+        for (i64 r = 0; r < R; ++r) ph[r] /= sum;
+    }
+}
+
+void race_oracle_alg1_causal(const float* q, const float* k, const float* v, const float* W,
+                             double beta, double* out, double* prefix, double* final_state, i64 N,
+                             i64 T, i64 D, i64 L, i64 P, int perbucket, double eps, i64 tile,
+                             int nthreads) {
+    const i64 S = L * ((i64)1 << P), rec = S * D + S;
+    const i64 tiles = tile > 0 ? (T + tile - 1) / tile : 0;
+    set_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (i64 n = 0; n < N; ++n) {
+        double* st = (double*)calloc((size_t)rec, sizeof(double));  /* B [S][D] then A [S] */
+        double* fq = (double*)malloc((size_t)S * sizeof(double));
+        double* fk = (double*)malloc((size_t)S * sizeof(double));
+        double* u = (double*)malloc((size_t)P * sizeof(double));
+        double* o = (double*)malloc((size_t)D * sizeof(double));
+        double* B = st;
+        double* A = st + S * D;
+        for (i64 t = 0; t < T; ++t) {
+            if (prefix && tile > 0 && t % tile == 0)
+                memcpy(prefix + (n * tiles + t / tile) * rec, st, (size_t)rec * sizeof(double));
+            const float* vt = v + (n * T + t) * D;
+            alg1_features(k + (n * T + t) * D, W, beta, D, L, P, u, fk);
+            alg1_features(q + (n * T + t) * D, W, beta, D, L, P, u, fq);
+            for (i64 s = 0; s < S; ++s) {
+                A[s] += fk[s];
+                double* Bs = B + s * D;
+                for (i64 c = 0; c < D; ++c) Bs[c] += fk[s] * (double)vt[c];
+            }
+            for (i64 c = 0; c < D; ++c) o[c] = 0.0;
+            double den = 0.0;
+            for (i64 s = 0; s < S; ++s) {
+                const double ws = perbucket ? fq[s] / (A[s] + eps) : fq[s];
+                const double* Bs = B + s * D;
+                for (i64 c = 0; c < D; ++c) o[c] += ws * Bs[c];
+                den += fq[s] * A[s];
+            }
+            double* ot = out + (n * T + t) * D;
+            for (i64 c = 0; c < D; ++c)
+                ot[c] = perbucket ? o[c] : (den == 0.0 ? 0.0 : o[c] / den);
+        }
+        if (final_state) memcpy(final_state + n * rec, st, (size_t)rec * sizeof(double));
+        free(st);
+        free(fq);
+        free(fk);
+        free(u);
+        free(o);
+    }
+}
