@@ -205,6 +205,89 @@ race_status race_hash_probs(const void* x, const float* planes_T, void* probs, i
                             int32_t head_dim, int32_t num_tables, int32_t planes_per_table,
                             int32_t dtype, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Algorithm 1 with the hashing inside: the reference's causal v2 forward,
+ * race_causal_forward(q, k, v, planes, beta, ...)
+ * (src/causal_v2/kernels/race_causal_fwd.h:6-10, :126-130), for bf16 token
+ * rows.  Per stream and token t, with Phi(x) in R^S (S = L R, R = 2^P,
+ * table-major) the L tables' corner probabilities
+ *     Phi_l(x)[r] = softmax_r(beta sum_p tanh(<W[l][p], x>) c_{r,p}),
+ * c_{r,p} = +1 iff bit P-1-p of r is set, and A_t, B_t the inclusive sums of
+ * Phi(k_j) and Phi(k_j) (x) v_j over j <= t:
+ *     out_t = (Phi(q_t) . B_t) / (Phi(q_t) . A_t)   (0 where that is 0).
+ * Layouts: q, k, v, out [BH][T][D] bf16, 16-byte aligned; W [L][P][D] fp32,
+ * 16-byte aligned; beta one fp32 value in device memory (read by the kernels,
+ * so a trainable beta never needs a host sync).  Limits (the reference's,
+ * race_causal_fwd.h:45-47): D in {64, 128}, P in 1..5, L in 1..4,
+ * BH <= 65535, T <= INT_MAX - 4097.
+ * ------------------------------------------------------------------------ */
+
+/* Shape of one call; mirrors CausalShape (race_causal_fwd.h:60-66). */
+typedef struct race_alg1_shape {
+    int64_t batch_heads; /* BH */
+    int64_t seq_len;     /* T */
+    int32_t head_dim;    /* D */
+    int32_t num_planes;  /* P, R = 2^P corners per table */
+    int32_t num_tables;  /* L */
+} race_alg1_shape;
+
+/* Rounding of the matrix-core products; mirrors Variant
+ * (race_causal_fwd.h:68-70).  FP32: the features Phi enter every product as
+ * bf16 hi/lo pairs (fp32-accurate; the reference's v2a accuracy).  BF16: the
+ * features are rounded to bf16 once, the carried state and the masked Gram
+ * matrix stay hi/lo (the rounding points of the reference's v2b). */
+typedef enum race_alg1_variant {
+    RACE_ALG1_FP32 = 0,
+    RACE_ALG1_BF16 = 1
+} race_alg1_variant;
+
+/* Tile lengths are multiples of this many tokens (the sub-chunk C). */
+#define RACE_ALG1_SUB_CHUNK_TOKENS 64
+/* Largest automatic tile length (race_causal_fwd.h:74). */
+#define RACE_ALG1_MAX_AUTO_TILE 4096
+
+/* Whether the shape is within the limits above.  Host logic only. */
+race_status race_alg1_shape_supported(const race_alg1_shape* shape, int32_t* supported);
+
+/* Dynamic LDS of the output pass in bytes for (D, P, L) and `variant`;
+ * mirrors output_pass_smem_bytes (race_causal_fwd.h:82-83).  Host logic. */
+race_status race_alg1_output_lds_bytes(const race_alg1_shape* shape, int32_t variant,
+                                       size_t* bytes);
+
+/* Tile length an automatic call uses on the current device (a multiple of
+ * RACE_ALG1_SUB_CHUNK_TOKENS, at most RACE_ALG1_MAX_AUTO_TILE, the smallest
+ * for short sequences); mirrors race_causal_select_tile_tokens
+ * (race_causal_fwd.h:90-95). */
+race_status race_alg1_select_tile_tokens(const race_alg1_shape* shape, int32_t variant,
+                                         int32_t* tile_tokens);
+
+/* Workspace of race_alg1_fwd in bytes for a tile length (0 = automatic):
+ * the tile records [BH][tiles][rec] fp32, rec = S*D + S rounded up to 64
+ * floats, B [S][D] then A [S].  After the call record (n, t) holds the
+ * exclusive prefix state at the first token of tile t of stream n (the
+ * reference's debug prefix states, torch_binding.cpp:186-203). */
+race_status race_alg1_workspace_bytes(const race_alg1_shape* shape, int32_t variant,
+                                      int32_t tile_tokens, size_t* bytes, int64_t* tiles,
+                                      int64_t* record_floats);
+
+/* The forward.  tile_tokens: 0 automatic, else a positive multiple of
+ * RACE_ALG1_SUB_CHUNK_TOKENS.  final_state (nullable): [BH][S*D + S] fp32,
+ * the state after all T tokens (race_causal_fwd.h:20-21, layout B then A).
+ * Replaces race_causal_forward (race_causal_fwd.h:126-130). */
+race_status race_alg1_fwd(const void* q, const void* k, const void* v, const float* W,
+                          const float* beta, void* out, float* final_state,
+                          const race_alg1_shape* shape, int32_t tile_tokens, int32_t variant,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* race_alg1_fwd with hipEventRecord marks around every launch, as
+ * race_fwd_profiled.  A profiling aid with no counterpart in the reference. */
+race_status race_alg1_fwd_profiled(const void* q, const void* k, const void* v, const float* W,
+                                   const float* beta, void* out, float* final_state,
+                                   const race_alg1_shape* shape, int32_t tile_tokens,
+                                   int32_t variant, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream, hipEvent_t* events, int32_t max_events,
+                                   int32_t* n_events);
+
 /* race_noncausal_bwd / race_causal_bwd with a hipEventRecord on `stream`
  * before the first launch and after every launch, as race_fwd_profiled does.
  * Profiling aids with no counterpart in the reference (used by bench.py). */

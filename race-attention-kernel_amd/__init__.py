@@ -4,6 +4,7 @@ The op and its backward (causal and non-causal) run hand-written gfx950 HIP kern
 the C ABI of include/race_mi355x.h (librace_mi355x.so), reached from PyTorch
 through the _race_torch binding.  There is no CPU fallback.
 """
+from . import causal_v2
 from .batched_ace import BatchedACE
 from .inputs import CONFIGS, Config, config_inputs, make_inputs
 from .ops import (RaceFusedFunction, race_causal_backward, race_fused_fwd,
@@ -13,5 +14,5 @@ from .ops import (RaceFusedFunction, race_causal_backward, race_fused_fwd,
 __all__ = [
     "BatchedACE", "CONFIGS", "Config", "RaceFusedFunction", "config_inputs", "make_inputs",
     "race_fused_fwd", "race_fused_fwd_with_state", "race_noncausal_backward", "race_causal_backward",
-    "race_hash_probs", "select_tile_tokens",
+    "race_hash_probs", "select_tile_tokens", "causal_v2",
 ]

@@ -19,6 +19,10 @@ RACE_KERNEL_VALU = 1
 RACE_KERNEL_MFMA = 2
 RACE_KERNEL_MFMA_WG = 3
 RACE_SUB_CHUNK_TOKENS = 64
+RACE_ALG1_FP32 = 0
+RACE_ALG1_BF16 = 1
+RACE_ALG1_SUB_CHUNK_TOKENS = 64
+RACE_ALG1_MAX_AUTO_TILE = 4096
 
 EXPORTED_SYMBOLS = (
     "race_abi_version",
@@ -35,7 +39,23 @@ EXPORTED_SYMBOLS = (
     "race_noncausal_bwd_profiled",
     "race_causal_bwd_profiled",
     "race_hash_probs",
+    "race_alg1_shape_supported",
+    "race_alg1_output_lds_bytes",
+    "race_alg1_select_tile_tokens",
+    "race_alg1_workspace_bytes",
+    "race_alg1_fwd",
+    "race_alg1_fwd_profiled",
 )
+
+
+class RaceAlg1Shape(ctypes.Structure):
+    _fields_ = [
+        ("batch_heads", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("head_dim", ctypes.c_int32),
+        ("num_planes", ctypes.c_int32),
+        ("num_tables", ctypes.c_int32),
+    ]
 
 
 class RaceShape(ctypes.Structure):
@@ -82,6 +102,15 @@ def lib() -> ctypes.CDLL:
         L.race_causal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp,
                                                ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         L.race_hash_probs.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32, vp]
+        a1 = ctypes.POINTER(RaceAlg1Shape)
+        L.race_alg1_shape_supported.argtypes = [a1, ctypes.POINTER(i32)]
+        L.race_alg1_output_lds_bytes.argtypes = [a1, i32, ctypes.POINTER(sz)]
+        L.race_alg1_select_tile_tokens.argtypes = [a1, i32, ctypes.POINTER(i32)]
+        L.race_alg1_workspace_bytes.argtypes = [a1, i32, i32, ctypes.POINTER(sz), ctypes.POINTER(i64),
+                                                ctypes.POINTER(i64)]
+        L.race_alg1_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, a1, i32, i32, vp, sz, vp]
+        L.race_alg1_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, a1, i32, i32, vp, sz, vp,
+                                             ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         for name in EXPORTED_SYMBOLS[2:]:
             getattr(L, name).restype = i32
         _configured = True
@@ -192,3 +221,48 @@ def hash_probs(x: int, planes_T: int, probs: int, rows: int, head_dim: int, num_
                planes_per_table: int, dtype: int, stream: int) -> int:
     return lib().race_hash_probs(x, planes_T, probs, rows, head_dim, num_tables, planes_per_table,
                                  dtype, stream)
+
+
+def alg1_shape(BH: int, T: int, D: int, P: int, L: int) -> RaceAlg1Shape:
+    return RaceAlg1Shape(BH, T, D, P, L)
+
+
+def alg1_shape_supported(sh: RaceAlg1Shape) -> bool:
+    ok = ctypes.c_int32(0)
+    st = lib().race_alg1_shape_supported(ctypes.byref(sh), ctypes.byref(ok))
+    if st != RACE_SUCCESS:
+        raise RuntimeError(status_string(st))
+    return bool(ok.value)
+
+
+def alg1_output_lds_bytes(sh: RaceAlg1Shape, variant: int = RACE_ALG1_FP32):
+    """(status, bytes)."""
+    b = ctypes.c_size_t(0)
+    st = lib().race_alg1_output_lds_bytes(ctypes.byref(sh), variant, ctypes.byref(b))
+    return st, b.value
+
+
+def alg1_workspace_bytes(sh: RaceAlg1Shape, variant: int = RACE_ALG1_FP32, tile_tokens: int = 0):
+    """(status, bytes, tiles, record_floats)."""
+    b, t, r = ctypes.c_size_t(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    st = lib().race_alg1_workspace_bytes(ctypes.byref(sh), variant, tile_tokens, ctypes.byref(b),
+                                         ctypes.byref(t), ctypes.byref(r))
+    return st, b.value, t.value, r.value
+
+
+def alg1_fwd(q: int, k: int, v: int, W: int, beta: int, out: int, final_state: int | None,
+             sh: RaceAlg1Shape, tile_tokens: int, variant: int, workspace: int | None,
+             workspace_bytes: int, stream: int) -> int:
+    """race_alg1_fwd on raw device addresses; returns the status."""
+    return lib().race_alg1_fwd(q, k, v, W, beta, out, final_state, ctypes.byref(sh), tile_tokens,
+                               variant, workspace, workspace_bytes, stream)
+
+
+def alg1_fwd_profiled(q, k, v, W, beta, out, final_state, sh: RaceAlg1Shape, tile_tokens: int,
+                      variant: int, workspace, workspace_bytes: int, stream: int, events):
+    """race_alg1_fwd_profiled; returns (status, n_events)."""
+    n = ctypes.c_int32(0)
+    st = lib().race_alg1_fwd_profiled(q, k, v, W, beta, out, final_state, ctypes.byref(sh), tile_tokens,
+                                      variant, workspace, workspace_bytes, stream, events, len(events),
+                                      ctypes.byref(n))
+    return st, n.value

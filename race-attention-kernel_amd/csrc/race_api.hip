@@ -565,3 +565,172 @@ race_status race_hash_probs(const void* x, const float* planes_T, void* probs, i
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Algorithm 1 with the hashing inside (alg1.hip), the reference's causal v2
+// forward (src/causal_v2/kernels/race_causal_fwd.h:110-130).
+
+namespace race {
+namespace {
+
+constexpr int kAlg1Chunk = RACE_ALG1_SUB_CHUNK_TOKENS;
+
+bool alg1_shape_valid(const race_alg1_shape* sh) {
+    if (!sh) return false;
+    if (sh->batch_heads < 0 || sh->batch_heads > kMaxStreams) return false;
+    if (sh->seq_len < 0 || sh->seq_len > int64_t(INT_MAX) - RACE_ALG1_MAX_AUTO_TILE - 1) return false;
+    return alg1_shape_ok(sh->head_dim, sh->num_planes, sh->num_tables);
+}
+
+// Tile length: a few resident output-pass workgroups per CU, never below
+// the sub-chunk and never above RACE_ALG1_MAX_AUTO_TILE (the reference's
+// policy, race_causal_fwd.h:90-95, with this device's CU count).
+race_status alg1_resolve_tile(const race_alg1_shape* sh, int variant, int32_t requested, int* tile) {
+    if (requested != 0) {
+        if (requested < 0 || requested % kAlg1Chunk != 0) return RACE_ERROR_INVALID_VALUE;
+        *tile = requested;
+        return RACE_SUCCESS;
+    }
+    const int64_t work = sh->batch_heads * sh->seq_len;
+    if (work == 0) {
+        *tile = kAlg1Chunk;
+        return RACE_SUCCESS;
+    }
+    int dev = 0, cus = 0;
+    RACE_TRY(hipGetDevice(&dev));
+    RACE_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (cus < 1) cus = 1;
+    const int64_t per_cu =
+        2 * int64_t(alg1_blocks_per_cu(sh->head_dim, sh->num_planes, sh->num_tables, variant));
+    int t = pow2_floor(work / (per_cu * cus));
+    if (t < kAlg1Chunk) t = kAlg1Chunk;
+    if (t > RACE_ALG1_MAX_AUTO_TILE) t = RACE_ALG1_MAX_AUTO_TILE;
+    *tile = t;
+    return RACE_SUCCESS;
+}
+
+race_status alg1_problem(const race_alg1_shape* sh, int32_t variant, int32_t tile_tokens,
+                         Problem* p) {
+    if (!alg1_shape_valid(sh)) return RACE_ERROR_INVALID_VALUE;
+    if (variant != RACE_ALG1_FP32 && variant != RACE_ALG1_BF16) return RACE_ERROR_INVALID_VALUE;
+    int tile = 0;
+    const race_status st = alg1_resolve_tile(sh, variant, tile_tokens, &tile);
+    if (st != RACE_SUCCESS) return st;
+    p->N = sh->batch_heads;
+    p->T = sh->seq_len;
+    p->S = sh->num_tables << sh->num_planes;
+    p->d = sh->head_dim;
+    p->dtype = RACE_BF16;
+    p->kernel = RACE_KERNEL_MFMA;
+    p->tile = tile;
+    p->tiles = sh->seq_len == 0 ? 0 : (sh->seq_len + tile - 1) / tile;
+    p->rec = record_floats(p->S, p->d);
+    return RACE_SUCCESS;
+}
+
+race_status alg1_fwd_impl(const void* q, const void* k, const void* v, const float* W,
+                          const float* beta, void* out, float* final_state,
+                          const race_alg1_shape* sh, int32_t tile_tokens, int32_t variant,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream,
+                          Marks* marks) {
+    Problem p;
+    const race_status st = alg1_problem(sh, variant, tile_tokens, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (final_state && !aligned16(final_state)) return RACE_ERROR_INVALID_VALUE;
+    if (p.N == 0 || p.T == 0) {
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(zero_fill(final_state, p.N * state_floats(p.S, p.d), stream));
+        return marks->mark(stream);
+    }
+    if (!q || !k || !v || !W || !beta || !out) return RACE_ERROR_INVALID_VALUE;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !aligned16(W))
+        return RACE_ERROR_INVALID_VALUE;
+    const size_t need = size_t(p.N * p.tiles * p.rec) * sizeof(float);
+    if (!workspace || !aligned16(workspace) || workspace_bytes < need) return RACE_ERROR_INVALID_VALUE;
+    int lds_limit = 0;
+    RACE_TRY(max_lds(&lds_limit));
+    if (alg1_output_lds_bytes(p.d, sh->num_planes, sh->num_tables, variant) > size_t(lds_limit))
+        return RACE_ERROR_INVALID_VALUE;
+    Alg1Args a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.W = W;
+    a.beta = beta;
+    a.out = out;
+    a.records = static_cast<float*>(workspace);
+    a.state = final_state;
+    a.L = sh->num_tables;
+    a.P = sh->num_planes;
+    RACE_TRY(marks->mark(stream));
+    return launch_alg1(a, p, variant, stream, marks);
+}
+
+}  // namespace
+}  // namespace race
+
+extern "C" {
+
+race_status race_alg1_shape_supported(const race_alg1_shape* shape, int32_t* supported) {
+    if (!shape || !supported) return RACE_ERROR_INVALID_VALUE;
+    *supported = alg1_shape_valid(shape) ? 1 : 0;
+    return RACE_SUCCESS;
+}
+
+race_status race_alg1_output_lds_bytes(const race_alg1_shape* shape, int32_t variant,
+                                       size_t* bytes) {
+    if (!bytes || !alg1_shape_valid(shape)) return RACE_ERROR_INVALID_VALUE;
+    if (variant != RACE_ALG1_FP32 && variant != RACE_ALG1_BF16) return RACE_ERROR_INVALID_VALUE;
+    *bytes = alg1_output_lds_bytes(shape->head_dim, shape->num_planes, shape->num_tables, variant);
+    return RACE_SUCCESS;
+}
+
+race_status race_alg1_select_tile_tokens(const race_alg1_shape* shape, int32_t variant,
+                                         int32_t* tile_tokens) {
+    if (!tile_tokens) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    const race_status st = alg1_problem(shape, variant, 0, &p);
+    if (st != RACE_SUCCESS) return st;
+    *tile_tokens = p.tile;
+    return RACE_SUCCESS;
+}
+
+race_status race_alg1_workspace_bytes(const race_alg1_shape* shape, int32_t variant,
+                                      int32_t tile_tokens, size_t* bytes, int64_t* tiles,
+                                      int64_t* record_floats_out) {
+    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    const race_status st = alg1_problem(shape, variant, tile_tokens, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(p.N * p.tiles * p.rec) * sizeof(float);
+    if (tiles) *tiles = p.tiles;
+    if (record_floats_out) *record_floats_out = p.rec;
+    return RACE_SUCCESS;
+}
+
+race_status race_alg1_fwd(const void* q, const void* k, const void* v, const float* W,
+                          const float* beta, void* out, float* final_state,
+                          const race_alg1_shape* shape, int32_t tile_tokens, int32_t variant,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    Marks none;
+    return alg1_fwd_impl(q, k, v, W, beta, out, final_state, shape, tile_tokens, variant,
+                         workspace, workspace_bytes, stream, &none);
+}
+
+race_status race_alg1_fwd_profiled(const void* q, const void* k, const void* v, const float* W,
+                                   const float* beta, void* out, float* final_state,
+                                   const race_alg1_shape* shape, int32_t tile_tokens,
+                                   int32_t variant, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream, hipEvent_t* events, int32_t max_events,
+                                   int32_t* n_events) {
+    if (!events || max_events < 2 || !n_events) return RACE_ERROR_INVALID_VALUE;
+    Marks marks;
+    marks.events = events;
+    marks.max = max_events;
+    const race_status st = alg1_fwd_impl(q, k, v, W, beta, out, final_state, shape, tile_tokens,
+                                         variant, workspace, workspace_bytes, stream, &marks);
+    *n_events = marks.n;
+    return st;
+}
+
+}  // extern "C"

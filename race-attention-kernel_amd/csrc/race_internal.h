@@ -161,6 +161,29 @@ size_t hash_lds_bytes(int dk, int L, int K);
 hipError_t launch_hash_probs(const void* x, const float* planes_T, void* probs, int64_t rows,
                             int dk, int L, int K, int dtype, hipStream_t stream);
 
+// ---- Algorithm 1 with the hashing inside (alg1.hip): bf16 q, k, v, out ----
+struct Alg1Args {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* W;     // [L][P][D] fp32
+    const float* beta;  // one fp32 value in device memory
+    void* out;
+    float* records;     // [N][tiles][rec]
+    float* state;       // nullable: [N][S*D + S]
+    int L, P;
+};
+// D in {64, 128}, P in 1..5, L in 1..4.
+bool alg1_shape_ok(int D, int P, int L);
+// Dynamic LDS of the output pass (0 if unsupported); variant 0 = hi/lo
+// features, 1 = bf16 features.
+size_t alg1_output_lds_bytes(int D, int P, int L, int variant);
+// Output-pass workgroups resident per compute unit.
+int alg1_blocks_per_cu(int D, int P, int L, int variant);
+// Tile sums, scan (final state into a.state when not null) and output pass.
+hipError_t launch_alg1(const Alg1Args& a, const Problem& p, int variant, hipStream_t stream,
+                       Marks* marks);
+
 // Whether the MFMA causal path has a specialization for (S, d).
 bool mfma_causal_supported(int S, int d);
 hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void* out,

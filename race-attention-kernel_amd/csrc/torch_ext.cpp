@@ -11,6 +11,12 @@
 //   hash_probs(x, planes_T, L, K) -> [..., L, 2^K] bucket probabilities
 //   select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens=0, kernel=0) -> int
 //   shape_supported(L, R, d) -> (supported, has_mfma)
+//   alg1_forward(q, k, v, W, beta, tile_tokens=0, tensor_cores=False) -> out
+//   alg1_forward_debug(q, k, v, W, beta, tile_tokens=0, tensor_cores=False)
+//       -> (out, prefix_A, prefix_B, final_A, final_B, tile_tokens)
+//   alg1_sub_chunk_tokens / alg1_select_tile_tokens / alg1_output_lds_bytes /
+//   alg1_fits_on_device: the queries of the reference's causal v2 binding
+//       (src/causal_v2/kernels/torch_binding.cpp:1-25)
 //
 // probsQ, probsK: [N, T, L, R] (or [N, T, S], read as L = 1, R = S) and V:
 // [N, T, d], all float32 or all bfloat16, on one HIP device, contiguous,
@@ -258,6 +264,173 @@ std::tuple<bool, bool> shape_supported(int64_t L, int64_t R, int64_t d) {
     return {ok != 0, mfma != 0};
 }
 
+// ---- Algorithm 1 with the hashing inside (race_alg1_*): the surface of the
+// reference's causal v2 binding (src/causal_v2/kernels/torch_binding.cpp) ----
+
+void check_alg1_token(const at::Tensor& t, const char* name, const at::Tensor& like) {
+    TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+    TORCH_CHECK(t.scalar_type() == at::kBFloat16, name, " must be bfloat16, got ", t.scalar_type());
+    TORCH_CHECK(t.dim() == 4, name, " must be [B, H, T, d], got ", t.sizes());
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+    TORCH_CHECK(t.sizes() == like.sizes(), name, " shape ", t.sizes(), " differs from q ", like.sizes());
+    TORCH_CHECK(t.device() == like.device(), name, " must be on the same device as q");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(t.data_ptr()) % kAlignment == 0, name,
+                " data must be 16-byte aligned (clone the tensor if it is a view)");
+}
+
+race_alg1_shape alg1_make_shape(int64_t batch_heads, int64_t seq_len, int64_t head_dim,
+                                int64_t num_planes, int64_t num_tables) {
+    TORCH_CHECK(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128, got ", head_dim);
+    TORCH_CHECK(num_planes >= 1 && num_planes <= 5, "num_planes P must be in 1..5, got ", num_planes);
+    TORCH_CHECK(num_tables >= 1 && num_tables <= 4, "num_tables L must be in 1..4, got ", num_tables);
+    TORCH_CHECK(batch_heads >= 0 && batch_heads <= 65535, "batch * heads must be <= 65535, got ",
+                batch_heads);
+    TORCH_CHECK(seq_len >= 0 && seq_len <= int64_t(INT32_MAX) - RACE_ALG1_MAX_AUTO_TILE - 1,
+                "sequence length out of range: ", seq_len);
+    race_alg1_shape sh;
+    sh.batch_heads = batch_heads;
+    sh.seq_len = seq_len;
+    sh.head_dim = static_cast<int32_t>(head_dim);
+    sh.num_planes = static_cast<int32_t>(num_planes);
+    sh.num_tables = static_cast<int32_t>(num_tables);
+    return sh;
+}
+
+race_alg1_shape alg1_validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                              const at::Tensor& W, const at::Tensor& beta) {
+    check_alg1_token(q, "q", q);
+    check_alg1_token(k, "k", q);
+    check_alg1_token(v, "v", q);
+    TORCH_CHECK(W.device() == q.device(), "W must be on the same device as q");
+    TORCH_CHECK(W.scalar_type() == at::kFloat, "W must be float32, got ", W.scalar_type());
+    TORCH_CHECK(W.dim() == 3, "W must be [L, P, d], got ", W.sizes());
+    TORCH_CHECK(W.is_contiguous(), "W must be contiguous");
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(W.data_ptr()) % kAlignment == 0, "W must be 16-byte aligned");
+    TORCH_CHECK(W.size(2) == q.size(3), "W head_dim ", W.size(2), " differs from q ", q.size(3));
+    TORCH_CHECK(beta.numel() == 1, "beta must have exactly one element");
+    TORCH_CHECK(at::isFloatingType(beta.scalar_type()), "beta must be a floating tensor");
+    return alg1_make_shape(q.size(0) * q.size(1), q.size(2), q.size(3), W.size(1), W.size(0));
+}
+
+int32_t alg1_variant(bool tensor_cores) { return tensor_cores ? RACE_ALG1_BF16 : RACE_ALG1_FP32; }
+
+int device_lds_limit() {
+    int dev = 0, bytes = 0;
+    TORCH_CHECK(hipGetDevice(&dev) == hipSuccess, "hipGetDevice failed");
+    TORCH_CHECK(hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+                    hipSuccess,
+                "hipDeviceGetAttribute failed");
+    return bytes;
+}
+
+void alg1_check_fits(const race_alg1_shape& sh, bool tensor_cores) {
+    size_t bytes = 0;
+    check_status(race_alg1_output_lds_bytes(&sh, alg1_variant(tensor_cores), &bytes),
+                 "race_alg1_output_lds_bytes");
+    const int limit = device_lds_limit();
+    TORCH_CHECK(bytes <= size_t(limit), "the output pass needs ", bytes,
+                " bytes of LDS per workgroup for d=", sh.head_dim, ", P=", sh.num_planes, ", L=",
+                sh.num_tables, "; this GPU allows ", limit);
+}
+
+struct Alg1Result {
+    at::Tensor out, workspace, final_state;
+    int64_t tiles = 0, rec = 0;
+    int32_t tile = 0;
+};
+
+Alg1Result alg1_run(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                    const at::Tensor& W, const at::Tensor& beta, int64_t tile_tokens,
+                    bool tensor_cores, bool want_final) {
+    const race_alg1_shape sh = alg1_validate(q, k, v, W, beta);
+    const c10::DeviceGuard guard(q.device());
+    Alg1Result r;
+    r.out = at::empty_like(q);
+    if (sh.batch_heads == 0 || sh.seq_len == 0) return r;
+    alg1_check_fits(sh, tensor_cores);
+    TORCH_CHECK(tile_tokens == 0 || (tile_tokens > 0 && tile_tokens <= (int64_t(1) << 30) &&
+                                     tile_tokens % RACE_ALG1_SUB_CHUNK_TOKENS == 0),
+                "tile_tokens must be a positive multiple of ", RACE_ALG1_SUB_CHUNK_TOKENS, ", got ",
+                tile_tokens);
+    const int32_t variant = alg1_variant(tensor_cores);
+    size_t bytes = 0;
+    check_status(race_alg1_workspace_bytes(&sh, variant, static_cast<int32_t>(tile_tokens), &bytes,
+                                           &r.tiles, &r.rec),
+                 "race_alg1_workspace_bytes");
+    r.tile = static_cast<int32_t>(tile_tokens);
+    if (r.tile == 0) check_status(race_alg1_select_tile_tokens(&sh, variant, &r.tile), "race_alg1_select_tile_tokens");
+    const auto fopt = q.options().dtype(at::kFloat);
+    const at::Tensor beta_dev = beta.to(q.device(), at::kFloat).contiguous();
+    r.workspace = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, fopt);
+    const int64_t S = int64_t(sh.num_tables) << sh.num_planes;
+    if (want_final) r.final_state = at::empty({sh.batch_heads, S * sh.head_dim + S}, fopt);
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+    check_status(race_alg1_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), W.data_ptr<float>(),
+                               beta_dev.data_ptr<float>(), r.out.data_ptr(),
+                               want_final ? r.final_state.data_ptr<float>() : nullptr, &sh, r.tile,
+                               variant, r.workspace.data_ptr(), bytes, stream),
+                 "race_alg1_fwd");
+    return r;
+}
+
+at::Tensor alg1_forward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                        const at::Tensor& W, const at::Tensor& beta, int64_t tile_tokens,
+                        bool tensor_cores) {
+    return alg1_run(q, k, v, W, beta, tile_tokens, tensor_cores, false).out;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, int64_t> alg1_forward_debug(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& W,
+    const at::Tensor& beta, int64_t tile_tokens, bool tensor_cores) {
+    Alg1Result r = alg1_run(q, k, v, W, beta, tile_tokens, tensor_cores, true);
+    const int64_t B = q.size(0), H = q.size(1), D = q.size(3);
+    const int64_t L = W.size(0), R = int64_t(1) << W.size(1), S = L * R;
+    const auto fopt = q.options().dtype(at::kFloat);
+    if (!r.final_state.defined()) {
+        return {r.out, at::zeros({B, H, 0, L, R}, fopt), at::zeros({B, H, 0, L, R, D}, fopt),
+                at::zeros({B, H, L, R}, fopt), at::zeros({B, H, L, R, D}, fopt), 0};
+    }
+    // Records [BH][tiles][rec]: B [S][D] then A [S].
+    const at::Tensor recs = r.workspace.narrow(0, 0, B * H * r.tiles * r.rec).view({B, H, r.tiles, r.rec});
+    at::Tensor prefix_B = recs.narrow(3, 0, S * D).reshape({B, H, r.tiles, L, R, D}).clone();
+    at::Tensor prefix_A = recs.narrow(3, S * D, S).reshape({B, H, r.tiles, L, R}).clone();
+    const at::Tensor fin = r.final_state.view({B, H, S * D + S});
+    at::Tensor final_B = fin.narrow(2, 0, S * D).reshape({B, H, L, R, D}).clone();
+    at::Tensor final_A = fin.narrow(2, S * D, S).reshape({B, H, L, R}).clone();
+    return {r.out, prefix_A, prefix_B, final_A, final_B, r.tile};
+}
+
+int64_t alg1_sub_chunk_tokens(int64_t head_dim, int64_t num_planes, bool tensor_cores) {
+    alg1_make_shape(1, 1, head_dim, num_planes, 1);
+    (void)tensor_cores;
+    return RACE_ALG1_SUB_CHUNK_TOKENS;
+}
+
+int64_t alg1_select_tile_tokens(int64_t batch_heads, int64_t seq_len, int64_t head_dim,
+                                int64_t num_planes, int64_t num_tables, bool tensor_cores) {
+    const race_alg1_shape sh = alg1_make_shape(batch_heads, seq_len, head_dim, num_planes, num_tables);
+    TORCH_CHECK(seq_len > 0 && batch_heads > 0, "empty shape has no tiles");
+    alg1_check_fits(sh, tensor_cores);
+    int32_t tile = 0;
+    check_status(race_alg1_select_tile_tokens(&sh, alg1_variant(tensor_cores), &tile),
+                 "race_alg1_select_tile_tokens");
+    return tile;
+}
+
+int64_t alg1_output_lds_bytes(int64_t head_dim, int64_t num_planes, int64_t num_tables,
+                              bool tensor_cores) {
+    const race_alg1_shape sh = alg1_make_shape(1, 1, head_dim, num_planes, num_tables);
+    size_t bytes = 0;
+    check_status(race_alg1_output_lds_bytes(&sh, alg1_variant(tensor_cores), &bytes),
+                 "race_alg1_output_lds_bytes");
+    return static_cast<int64_t>(bytes);
+}
+
+bool alg1_fits_on_device(int64_t head_dim, int64_t num_planes, int64_t num_tables,
+                         bool tensor_cores) {
+    return alg1_output_lds_bytes(head_dim, num_planes, num_tables, tensor_cores) <= device_lds_limit();
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -286,5 +459,25 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("kernel") = 0);
     m.def("shape_supported", &shape_supported, "(supported, has_mfma) for (L, R, d)", py::arg("L"),
           py::arg("R"), py::arg("d"));
+    m.def("alg1_forward", &alg1_forward,
+          "Causal Algorithm 1 with hashing: o = race_causal(q, k, v, W, beta)", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("tile_tokens") = 0,
+          py::arg("tensor_cores") = false);
+    m.def("alg1_forward_debug", &alg1_forward_debug,
+          "alg1_forward plus (prefix_A, prefix_B, final_A, final_B, tile_tokens)", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("tile_tokens") = 0,
+          py::arg("tensor_cores") = false);
+    m.def("alg1_sub_chunk_tokens", &alg1_sub_chunk_tokens, "Sub-chunk length C of the output pass",
+          py::arg("head_dim"), py::arg("num_planes"), py::arg("tensor_cores") = false);
+    m.def("alg1_select_tile_tokens", &alg1_select_tile_tokens,
+          "Tile length the forward picks for this shape on the current device",
+          py::arg("batch_heads"), py::arg("seq_len"), py::arg("head_dim"), py::arg("num_planes"),
+          py::arg("num_tables"), py::arg("tensor_cores") = false);
+    m.def("alg1_output_lds_bytes", &alg1_output_lds_bytes, "Dynamic LDS of the output pass in bytes",
+          py::arg("head_dim"), py::arg("num_planes"), py::arg("num_tables"),
+          py::arg("tensor_cores") = false);
+    m.def("alg1_fits_on_device", &alg1_fits_on_device,
+          "Whether the output pass fits this GPU's LDS", py::arg("head_dim"), py::arg("num_planes"),
+          py::arg("num_tables"), py::arg("tensor_cores") = false);
     m.def("abi_version", &race_abi_version, "ABI version of the loaded librace_mi355x");
 }

@@ -183,3 +183,83 @@ def test_product_path_never_imports_the_oracle():
         text = path.read_text(errors="ignore")
         hit = re.search(r"liboracle|race_oracle|oracle\.py|load_oracle|from oracle|import oracle", text)
         assert hit is None, f"{path.name} reaches the oracle: {hit.group(0)}"
+
+
+# --- Algorithm 1 with the hashing inside (race_alg1_*) -------------------------------------
+
+@pytest.mark.parametrize("D, P, L, ok", [(64, 4, 4, True), (128, 5, 4, True), (64, 1, 1, True),
+                                         (96, 4, 4, False), (64, 6, 1, False), (64, 0, 1, False),
+                                         (64, 4, 5, False), (64, 4, 0, False)])
+def test_alg1_shape_limits(race, D, P, L, ok):
+    from race_attention_kernel_amd import abi
+
+    assert abi.alg1_shape_supported(abi.alg1_shape(8, 4096, D, P, L)) is ok
+
+
+def test_alg1_lds_and_workspace_sizes(race):
+    from race_attention_kernel_amd import abi
+
+    sh = abi.alg1_shape(8, 5000, 64, 4, 4)
+    for variant in (abi.RACE_ALG1_FP32, abi.RACE_ALG1_BF16):
+        st, lds = abi.alg1_output_lds_bytes(sh, variant)
+        assert st == 0 and 0 < lds <= 160 * 1024
+    # The bf16-feature variant keeps single-term feature planes: less LDS.
+    assert abi.alg1_output_lds_bytes(sh, abi.RACE_ALG1_BF16)[1] < abi.alg1_output_lds_bytes(sh, abi.RACE_ALG1_FP32)[1]
+    # Every supported shape fits the MI355X's 160 KB of LDS per workgroup.
+    for D in (64, 128):
+        for P in range(1, 6):
+            for L in range(1, 5):
+                for variant in (0, 1):
+                    st, lds = abi.alg1_output_lds_bytes(abi.alg1_shape(1, 1, D, P, L), variant)
+                    assert st == 0 and lds <= 160 * 1024, (D, P, L, variant, lds)
+    st, nbytes, tiles, rec = abi.alg1_workspace_bytes(sh, 0, 128)
+    S = 4 * 16
+    assert st == 0 and tiles == 40 and rec == -(-(S * 64 + S) // 64) * 64
+    assert nbytes == 8 * tiles * rec * 4
+
+
+@pytest.mark.parametrize("tile", [-64, 48, 100])
+def test_alg1_invalid_tiles_and_variants(race, tile):
+    from race_attention_kernel_amd import abi
+
+    inv = abi.RACE_ERROR_INVALID_VALUE
+    sh = abi.alg1_shape(8, 4096, 64, 4, 4)
+    assert abi.alg1_workspace_bytes(sh, 0, tile)[0] == inv
+    assert abi.alg1_workspace_bytes(sh, 2, 64)[0] == inv
+
+
+def test_alg1_invalid_arguments_are_rejected_before_any_launch(race):
+    from race_attention_kernel_amd import abi
+
+    inv = abi.RACE_ERROR_INVALID_VALUE
+    good = abi.alg1_shape(8, 1024, 64, 4, 4)
+    bad = abi.alg1_shape(8, 1024, 96, 4, 4)
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, bad, 64, 0, 64, 1 << 30, 0) == inv
+    # Null inputs, planes or beta; misaligned pointers; missing or short workspace.
+    assert abi.alg1_fwd(0, 16, 16, 16, 16, 16, None, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 0, 16, 16, None, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 16, 0, 16, None, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 18, None, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 20, 16, 16, None, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, 20, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, good, 64, 0, None, 0, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, good, 64, 0, 64, 64, 0) == inv
+    # Bad variant or tile.
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, good, 64, 3, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, good, 96, 0, 64, 1 << 30, 0) == inv
+
+
+def test_alg1_torch_binding_validates_inputs_on_the_host(race, ext):
+    import torch
+
+    q = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16)
+    W = torch.zeros(2, 3, 64)
+    with pytest.raises(RuntimeError, match="must be a GPU tensor"):
+        race.causal_v2.forward(q, q, q, W, torch.tensor(1.0))
+    with pytest.raises(RuntimeError, match="head_dim must be 64 or 128"):
+        race.causal_v2.sub_chunk_tokens(96, 4)
+    with pytest.raises(RuntimeError, match="num_planes"):
+        race.causal_v2.output_pass_smem_bytes(64, 6, 1)
+    assert race.causal_v2.sub_chunk_tokens(64, 4) == 64
+    assert race.causal_v2.output_pass_smem_bytes(64, 4, 4) > 0
+    assert race.causal_v2.precise_carry()
