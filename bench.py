@@ -130,11 +130,14 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
-    ap.add_argument("--pass", dest="pass_", choices=["fwd", "bwd", "fwdbwd", "module"],
+    ap.add_argument("--pass", dest="pass_", choices=["fwd", "bwd", "fwdbwd", "module", "alg1"],
                     default="fwd",
                     help="what one step runs: the forward (default), the backward (from the "
-                         "forward's inputs and a synthetic dOut), both, or the module's hot "
-                         "span (hashing of Q and K rows, then the forward)")
+                         "forward's inputs and a synthetic dOut), both, the module's hot "
+                         "span (hashing of Q and K rows, then the forward), or the "
+                         "Algorithm-1 forward with the hashing inside (race_alg1_fwd)")
+    ap.add_argument("--alg1-variant", choices=["fp32", "bf16"], default="bf16",
+                    help="rounding variant of --pass alg1 (fp32-accurate or bf16 features)")
     ap.add_argument("--T", type=int, default=0)
     ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
@@ -239,6 +242,132 @@ def cpu_baseline():
     }
 
 
+# The reference's own benchmark of its causal v2 forward
+# (src/causal_v2/bench/bench_causal.py:37-39): B*H = 8 streams, d = 64,
+# P = 4, L = 4, beta = 1/sqrt(d); its "2M-token" job is T = 2^21.
+ALG1_JOB = {"BH": 8, "T": 1 << 21, "D": 64, "P": 4, "L": 4}
+# Its published times for that job on an H100 80GB (benchmarks/h100_run.md:63-69);
+# context only, a different GPU.
+ALG1_REFERENCE_H100_MS = {"bf16": 14.7, "fp32": 55.0}
+
+
+def bench_alg1(args) -> int:
+    """--pass alg1: race_alg1_fwd on the reference's causal v2 job."""
+    import torch
+
+    race = entry.load_package()
+    from race_attention_kernel_amd import abi
+
+    BH, D, P, L = ALG1_JOB["BH"], ALG1_JOB["D"], ALG1_JOB["P"], ALG1_JOB["L"]
+    T = args.T or ALG1_JOB["T"]
+    S = L << P
+    variant = abi.RACE_ALG1_BF16 if args.alg1_variant == "bf16" else abi.RACE_ALG1_FP32
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(BH, T, D, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3))
+    W = torch.randn(L, P, D, device=dev, generator=gen)
+    beta = torch.tensor([1.0 / D ** 0.5], device=dev)
+    out = torch.empty_like(v)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    sh = abi.alg1_shape(BH, T, D, P, L)
+    st, ws_bytes, tiles, rec = abi.alg1_workspace_bytes(sh, variant, args.tile)
+    if st != 0:
+        raise RuntimeError(abi.status_string(st))
+    tile = race.causal_v2.select_tile_tokens(BH, T, D, P, L, variant == abi.RACE_ALG1_BF16) \
+        if args.tile == 0 else args.tile
+    ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), W.data_ptr(), beta.data_ptr(), out.data_ptr())
+
+    def check(st_):
+        if st_ != 0:
+            raise RuntimeError(abi.status_string(st_))
+
+    def plain():
+        check(abi.alg1_fwd(*ptrs, None, sh, args.tile, variant, ws.data_ptr(), ws_bytes, stream))
+
+    events = HipEvents()
+    per_step = [events.array(8) for _ in range(args.steps)]
+    warm = events.array(8)
+    for _ in range(args.warmup):
+        plain()
+        check(abi.alg1_fwd_profiled(*ptrs, None, sh, args.tile, variant, ws.data_ptr(), ws_bytes,
+                                    stream, warm)[0])
+    torch.cuda.synchronize()
+    bracket = events.array(2)
+    t0 = time.perf_counter()
+    events.record(bracket[0], stream)
+    for _ in range(args.steps):
+        plain()
+    events.record(bracket[1], stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
+    n = 0
+    for i in range(args.steps):
+        st_, n = abi.alg1_fwd_profiled(*ptrs, None, sh, args.tile, variant, ws.data_ptr(), ws_bytes,
+                                       stream, per_step[i])
+        check(st_)
+    torch.cuda.synchronize()
+    names = ["alg1_sums", "tile_scan", "alg1_output"]
+    gaps = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step) for j in range(n - 1)]
+    if len(gaps) != len(names):
+        names = [f"kernel{j}" for j in range(len(gaps))]
+    NT = BH * T
+    state = 4.0 * BH * tiles * rec
+    kbytes = {"alg1_sums": 2 * 2 * D * NT, "tile_scan": 2 * state, "alg1_output": 4 * 2 * D * NT}
+    dom = max(range(len(gaps)), key=lambda j: gaps[j])
+    dom_bytes = kbytes.get(names[dom], 0.0)
+    achieved = dom_bytes / (gaps[dom] * 1e-3) / 1e9
+    peak_bytes = torch.cuda.max_memory_allocated(dev)
+    events.destroy()
+    value = NT / (ms_per_step * 1e-3) / 1e6
+    # Whole-op algorithmic bytes: read q, k, v once and write out once (8 d
+    # bytes per stream-token, the reference's "minimum" model,
+    # bench_causal.py:11-17).
+    op_min = 8 * D * NT
+    result = {
+        "metric": f"causal Algorithm-1 fwd (hashing inside) M tokens/s at BH={BH},d={D},P={P},L={L},T={T} on 1 GPU",
+        "value": round(value, 3),
+        "unit": UNIT,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"alg1: causal Algorithm 1 with hashing, BH={BH} T={T} d={D} P={P} L={L} "
+                        f"beta=1/sqrt(d) bf16, {args.alg1_variant} variant",
+            "BH": BH, "T": T, "D": D, "P": P, "L": L, "S": S, "variant": args.alg1_variant,
+            "tile_tokens": tile, "launches_per_step": len(gaps),
+            "kernel_ms": {names[j]: round(gaps[j], 5) for j in range(len(gaps))},
+            "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+            "peak_hbm_bytes_per_token": round(peak_bytes / T, 1),
+            "alg_bytes_per_stream_token": 8 * D,
+            "whole_op_frac": round(op_min / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "reference_h100_ms_same_job": ALG1_REFERENCE_H100_MS[args.alg1_variant] if T == 1 << 21 else None,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": names[dom],
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic_for(f"alg1_{args.alg1_variant}", names[dom]),
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -246,6 +375,8 @@ def main() -> int:
               "multi-GPU sharding of the op is designed but not measured here.",
               file=sys.stderr)
         return 2
+    if args.pass_ == "alg1":
+        return bench_alg1(args)
     import torch
 
     race = entry.load_package()

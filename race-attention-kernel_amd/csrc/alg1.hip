@@ -92,15 +92,12 @@ __device__ __forceinline__ f32x4 get4(const unsigned char* t, int row, int k0) {
     return r;
 }
 
-// Corner probability r of one table from the per-plane sigmoid pairs
-// pm[p] = (sigma(2 beta u_p), sigma(-2 beta u_p)): the product over planes in
-// order p = 0 .. P-1, plane 0 the most significant bit of r.
-__device__ __forceinline__ float corner_prob(const float2 (&pm)[5], int P, int r) {
-    float pr = 1.f;
-#pragma unroll
-    for (int p = 0; p < 5; ++p)
-        if (p < P) pr *= ((r >> (P - 1 - p)) & 1) ? pm[p].x : pm[p].y;
-    return pr;
+// The sigmoid pair (sigma(z), sigma(-z)) of a plane from its stored value
+// s = copysign(sigma(-|z|), z): sigma(|z|) = 1 - sigma(-|z|) >= 1/2 is formed
+// without cancellation, and the sign bit (also of -0) picks the order.
+__device__ __forceinline__ float2 sigma_pair(float s) {
+    const float b = fabsf(s), a = 1.0f - b;
+    return (__float_as_uint(s) >> 31) ? make_float2(b, a) : make_float2(a, b);
 }
 
 template <bool kPhiSplit, int SP, int D, int LPP>
@@ -113,7 +110,7 @@ struct A1Geo {
     using PC = Plane<kPhiSplit, C>;   // bucket rows over tokens: Phi_K^T
     using PG = Plane<true, C>;        // query rows over keys: G
     using PV = Plane<false, C>;       // feature rows over tokens: V^T
-    static constexpr int kUPitch = 2 * (LPP + 1);  // floats per token: (plus, minus) per plane
+    static constexpr int kUPitch = LPP + 1;  // floats per token: one per plane
     static constexpr int kUBytes = C * kUPitch * 4;
     static constexpr int kXBytes = C * PX::kPitch;
     static constexpr int kPhiBytes = C * PS::kPitch;
@@ -121,17 +118,22 @@ struct A1Geo {
     static constexpr int kKTBytes = SP * PC::kPitch;
     static constexpr int kVTBytes = D * PV::kPitch;
     using PW3 = Plane<false, D>;      // plane rows over features: third bf16 term of W
-    // W = hi + mid + lo in the fp32 variant (the projection is then exact in
-    // fp32 arithmetic), hi + mid in the bf16 one.
-    static constexpr int kWBytes = LPP * PW::kPitch + (kPhiSplit ? LPP * PW3::kPitch : 0);
     static constexpr int kDenBytes = 4 * C * 4;
     static constexpr int mx(int a, int b) { return a > b ? a : b; }
-    // Region A of the output pass holds in turn the x planes of q and k, their
-    // sigmoid pairs, then Phi_Q and Phi_K (G over Phi_K).
-    static constexpr int kRegionOut = mx(mx(2 * kXBytes, 2 * kUBytes), kPhiBytes + mx(kPhiBytes, kGBytes));
-    static constexpr int kOutputLds = kRegionOut + kKTBytes + kVTBytes + kWBytes + kDenBytes;
-    static constexpr int kRegionSums = mx(kXBytes, kUBytes);
-    static constexpr int kSumsLds = kRegionSums + kKTBytes + kVTBytes + kWBytes;
+    // Region A of the output pass holds the x planes of q and k, then Phi_Q
+    // and Phi_K (G over Phi_K); region U the plane values of q and k, then
+    // the partial denominators.
+    static constexpr int kRegionOut = mx(2 * kXBytes, kPhiBytes + mx(kPhiBytes, kGBytes));
+    static constexpr int kRegionU = mx(2 * kUBytes, kDenBytes);
+    // W = hi + mid + lo in the fp32 variant where the output pass still fits
+    // 160 KB of LDS (the projection is then exact in fp32 arithmetic), hi + mid
+    // otherwise (every shape but d = 128, S = 128, L P > 16) and in the bf16
+    // variant.
+    static constexpr int kOutBase = kRegionOut + kRegionU + kKTBytes + kVTBytes + LPP * PW::kPitch;
+    static constexpr bool kW3 = kPhiSplit && kOutBase + LPP * PW3::kPitch <= 160 * 1024;
+    static constexpr int kWBytes = LPP * PW::kPitch + (kW3 ? LPP * PW3::kPitch : 0);
+    static constexpr int kOutputLds = kOutBase + kWBytes - LPP * PW::kPitch;
+    static constexpr int kSumsLds = kXBytes + kUBytes + kKTBytes + kVTBytes + kWBytes;
     static constexpr int kOutBlocks = kOutputLds <= 80 * 1024 ? 2 : 1;
     static constexpr int kSumsBlocks = kSumsLds <= 80 * 1024 ? 2 : 1;
     static constexpr int NSB = SP / 16, NBI = C / 16, NKS = SP / 32, NKC = C / 32, NKD = D / 32;
@@ -197,7 +199,7 @@ struct A1Stage {
 };
 
 // The planes W [L][P][D] as bf16 plane rows j = l P + p (rows past L*P
-// zero): hi and mid in the hi/lo plane Ws, and with kPhiSplit the third term
+// zero): hi and mid in the hi/lo plane Ws, and with G::kW3 the third term
 // lo = bf16(W - hi - mid) in the plane after it.
 template <typename G, bool kPhiSplit>
 __device__ __forceinline__ void load_planes(unsigned char* Ws, const float* __restrict__ W, int LP) {
@@ -210,7 +212,7 @@ __device__ __forceinline__ void load_planes(unsigned char* Ws, const float* __re
         uint2 hi, mid;
         split4<true>(x[0], x[1], x[2], x[3], hi, mid);
         G::PW::put4(Ws, j, c0, hi, mid);
-        if constexpr (kPhiSplit) {
+        if constexpr (G::kW3) {
             const f32x4 r = {(x[0] - lo_half(hi.x)) - lo_half(mid.x), (x[1] - hi_half(hi.x)) - hi_half(mid.x),
                              (x[2] - lo_half(hi.y)) - lo_half(mid.y), (x[3] - hi_half(hi.y)) - hi_half(mid.y)};
             const uint2 lo = make_uint2(pack2(r[0], r[1]), pack2(r[2], r[3]));
@@ -236,7 +238,7 @@ __device__ __forceinline__ void project(const unsigned char* X, const unsigned c
         for (int pb = 0; pb < G::NPB; ++pb) {
             bf16x8 wh, wm;
             G::PW::frag(Ws, 16 * pb + lr, kk, g, wh, wm);
-            if constexpr (kPhiSplit) {
+            if constexpr (G::kW3) {
                 bf16x8 wl, unused;
                 G::PW3::frag(W3, 16 * pb + lr, kk, g, wl, unused);
                 acc[pb] = mfma16(wl, xh, acc[pb]);
@@ -246,69 +248,93 @@ __device__ __forceinline__ void project(const unsigned char* X, const unsigned c
     }
 }
 
-// Sigmoid pairs (sigma(z), sigma(-z)), z = 2 beta tanh(u), of the projections
-// in `acc` into U [C][kUPitch].  Computed from e = exp(-|z|) <= 1 so that no
-// beta overflows.
+// z = 2 beta tanh(u) of the projections in `acc`, stored as
+// copysign(sigma(-|z|), z) in U [C][kUPitch] (one float per token and plane).
+// tanh |u| = (1 - e1) / (1 + e1) with e1 = exp(-2|u|), sigma(-|z|) = e / (1 + e)
+// with e = exp(-|z|): every exponential is <= 1, so nothing overflows at any
+// beta, and both are accurate to a few fp32 ulps in absolute terms.
 template <typename G>
-__device__ __forceinline__ void write_pairs(float* U, const f32x4 (&acc)[G::NPB], float beta2, int w,
-                                            int g, int lr) {
+__device__ __forceinline__ void write_sigmas(float* U, const f32x4 (&acc)[G::NPB], float beta2, int w,
+                                             int g, int lr) {
+    constexpr float kLog2e = 1.4426950408889634f;
     const int t = 16 * w + lr;
 #pragma unroll
     for (int pb = 0; pb < G::NPB; ++pb)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const float z = beta2 * tanhf(acc[pb][rr]);
-            const float e = expf(-fabsf(z));
-            const float a = 1.0f / (1.0f + e), b = e * a;
-            *reinterpret_cast<float2*>(U + t * G::kUPitch + 2 * (16 * pb + 4 * g + rr)) =
-                z >= 0.f ? make_float2(a, b) : make_float2(b, a);
+            const float x = acc[pb][rr];
+            const float e1 = __builtin_amdgcn_exp2f(-2.0f * kLog2e * fabsf(x));
+            const float th = (1.0f - e1) * __builtin_amdgcn_rcpf(1.0f + e1);
+            const float z = beta2 * copysignf(th, x);
+            const float e = __builtin_amdgcn_exp2f(-kLog2e * fabsf(z));
+            const float b = e * __builtin_amdgcn_rcpf(1.0f + e);
+            U[t * G::kUPitch + 16 * pb + 4 * g + rr] = copysignf(b, z);
         }
 }
 
-// The pairs of planes l P .. l P + P - 1 of token t.
-template <typename G>
-__device__ __forceinline__ void read_pairs(const float* U, int t, int l, int P, float2 (&pm)[5]) {
-#pragma unroll
-    for (int p = 0; p < 5; ++p)
-        pm[p] = p < P ? *reinterpret_cast<const float2*>(U + t * G::kUPitch + 2 * (l * P + p))
-                      : make_float2(0.f, 0.f);
-}
-
-// Buckets l R .. l R + R - 1 of token t: into row t of the token-row plane
-// Ph (when not null) and column t of the bucket-row plane KTs (when not
-// null); all zero when `zero` (rows past the sequence).
+// Phi of the sub-chunk's C tokens from U: into the token-row plane Ph
+// (nullable) and the bucket-row plane KTs (nullable); tokens >= valid get 0.
+// With R >= 4, item (tq, l, m) covers tokens 4 tq .. 4 tq + 3, table l and
+// corners 4 m .. 4 m + 3: the planes above the last two select by the bits
+// of m (plane 0 the most significant bit of r), the last two give the quad,
+// and both layouts take 4-element stores.  R = 2 (P = 1) goes element-wise.
 template <typename PS, typename PC, bool kSplit>
-__device__ __forceinline__ void put_phi(unsigned char* Ph, unsigned char* KTs, int t, int l, int P,
-                                        const float2 (&pm)[5], bool zero) {
+__device__ __forceinline__ void build_phi(const float* U, int kUP, unsigned char* Ph, unsigned char* KTs,
+                                          int L, int P, int valid) {
     const int R = 1 << P;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        if (4 * m >= R) continue;
-        const int n4 = R >= 4 ? 4 : 2;
-        float x[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) x[u] = (u < n4 && !zero) ? corner_prob(pm, P, 4 * m + u) : 0.f;
-        if (n4 == 4) {
-            if (Ph) {
-                uint2 hi, lo;
-                split4<kSplit>(x[0], x[1], x[2], x[3], hi, lo);
-                PS::put4(Ph, t, l * R + 4 * m, hi, lo);
-            }
-        } else if (Ph) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                uint16_t hi, lo;
-                split1<kSplit>(x[u], hi, lo);
-                PS::put1(Ph, t, l * R + u, hi, lo);
-            }
-        }
-        if (KTs) {
+    if (P >= 2) {
+        const int RQ = R / 4, items = (kA1Chunk / 4) * L * RQ;
+        for (int e = threadIdx.x; e < items; e += kThreads) {
+            const int m = e % RQ, l = (e / RQ) % L, tq = e / (RQ * L);
+            float pr[4][4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                if (u >= n4) continue;
+                const int t = 4 * tq + u;
+                const float* ur = U + t * kUP + l * P;
+                float base = 1.f;
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    if (p < P - 2) {
+                        const float2 sp = sigma_pair(ur[p]);
+                        base *= ((m >> (P - 3 - p)) & 1) ? sp.x : sp.y;
+                    }
+                }
+                const float2 s1 = sigma_pair(ur[P - 2]), s2 = sigma_pair(ur[P - 1]);
+                const bool live = t < valid;
+                pr[u][0] = live ? base * (s1.y * s2.y) : 0.f;
+                pr[u][1] = live ? base * (s1.y * s2.x) : 0.f;
+                pr[u][2] = live ? base * (s1.x * s2.y) : 0.f;
+                pr[u][3] = live ? base * (s1.x * s2.x) : 0.f;
+            }
+            if (Ph) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    uint2 hi, lo;
+                    split4<kSplit>(pr[u][0], pr[u][1], pr[u][2], pr[u][3], hi, lo);
+                    PS::put4(Ph, 4 * tq + u, l * R + 4 * m, hi, lo);
+                }
+            }
+            if (KTs) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    uint2 hi, lo;
+                    split4<kSplit>(pr[0][c], pr[1][c], pr[2][c], pr[3][c], hi, lo);
+                    PC::put4(KTs, l * R + 4 * m + c, 4 * tq, hi, lo);
+                }
+            }
+        }
+    } else {
+        for (int e = threadIdx.x; e < kA1Chunk * L; e += kThreads) {
+            const int t = e % kA1Chunk, l = e / kA1Chunk;
+            const float2 sp = sigma_pair(U[t * kUP + l]);
+            const bool live = t < valid;
+            const float x[2] = {live ? sp.y : 0.f, live ? sp.x : 0.f};
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
                 uint16_t hi, lo;
-                split1<kSplit>(x[u], hi, lo);
-                PC::put1(KTs, l * R + 4 * m + u, t, hi, lo);
+                split1<kSplit>(x[r], hi, lo);
+                if (Ph) PS::put1(Ph, t, 2 * l + r, hi, lo);
+                if (KTs) PC::put1(KTs, 2 * l + r, t, hi, lo);
             }
         }
     }
@@ -337,8 +363,8 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
     using PC = typename G::PC;
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Xk = lds;
-    float* U = reinterpret_cast<float*>(lds);
-    unsigned char* KTs = lds + G::kRegionSums;
+    float* U = reinterpret_cast<float*>(lds + G::kXBytes);
+    unsigned char* KTs = lds + G::kXBytes + G::kUBytes;
     unsigned char* VTs = KTs + G::kKTBytes;
     unsigned char* Ws = VTs + G::kVTBytes;
 
@@ -367,7 +393,6 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
     unsigned char* const Xs[1] = {Xk};
-    const int bt = tid % kA1Chunk, bl = tid / kA1Chunk;  // builder item: token, table
 
     A1Stage<D, 1> st;
     st.load(xr, vr, 0);
@@ -378,14 +403,9 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
         __syncthreads();
         f32x4 uk[G::NPB];
         project<G, kPhiSplit>(Xk, Ws, w, g, lr, uk);
+        write_sigmas<G>(U, uk, beta2, w, g, lr);
         __syncthreads();
-        write_pairs<G>(U, uk, beta2, w, g, lr);
-        __syncthreads();
-        if (bl < L) {
-            float2 pm[5];
-            read_pairs<G>(U, bt, bl, P, pm);
-            put_phi<typename G::PS, PC, kPhiSplit>(nullptr, KTs, bt, bl, P, pm, bt >= rows - r0);
-        }
+        build_phi<typename G::PS, PC, kPhiSplit>(U, G::kUPitch, nullptr, KTs, L, P, rows - r0);
         __syncthreads();
 #pragma unroll
         for (int cbw = 0; cbw < G::CBW; ++cbw) {
@@ -441,10 +461,9 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
 
 // ---------------------------------------------------------------------------
 // K3: the output pass, one workgroup per (tile, stream).  Per sub-chunk (the
-// numbers are the barriers):
-//   stage q, k rows and V^T (1) -> project q, k (2) -> sigmoid pairs (3, 4)
-//   -> Phi_Q, Phi_K, Phi_K^T (5, 6) -> running mass, den, G^T blocks (7)
-//   -> G plane (8) -> output and state update.
+// numbers are the barriers): stage q, k rows and V^T (1) -> project q, k and
+// store their plane values (2) -> Phi_Q, Phi_K, Phi_K^T (3) -> running mass,
+// denominators, G^T blocks (4) -> G plane (5) -> output and state update.
 template <bool kPhiSplit, int SP, int D, int LPP>
 __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks)) void alg1_output_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -461,15 +480,15 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Xq = lds;
     unsigned char* Xk = lds + G::kXBytes;
-    float* Uq = reinterpret_cast<float*>(lds);
-    float* Uk = Uq + C * G::kUPitch;
     unsigned char* PhQ = lds;
     unsigned char* PhK = lds + G::kPhiBytes;
     unsigned char* Gs = PhK;
-    unsigned char* KTs = lds + G::kRegionOut;
+    float* Uq = reinterpret_cast<float*>(lds + G::kRegionOut);
+    float* Uk = Uq + C * G::kUPitch;
+    float* denp = Uq;  // [4][C], once the builder has read U
+    unsigned char* KTs = lds + G::kRegionOut + G::kRegionU;
     unsigned char* VTs = KTs + G::kKTBytes;
     unsigned char* Ws = VTs + G::kVTBytes;
-    float* denp = reinterpret_cast<float*>(Ws + G::kWBytes);  // [4][C]
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -513,7 +532,6 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
     unsigned char* const Xs[2] = {Xq, Xk};
-    const int bt = tid % C, bl = tid / C;  // builder item: token, table
 
     A1Stage<D, 2> st;
     st.load(xr, vr, 0);
@@ -525,25 +543,16 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
         f32x4 uq[G::NPB], uk[G::NPB];
         project<G, kPhiSplit>(Xq, Ws, w, g, lr, uq);
         project<G, kPhiSplit>(Xk, Ws, w, g, lr, uk);
-        __syncthreads();  // (2) the x planes are dead
-        write_pairs<G>(Uq, uq, beta2, w, g, lr);
-        write_pairs<G>(Uk, uk, beta2, w, g, lr);
-        __syncthreads();  // (3)
-        float2 pq[5], pk[5];
-        if (bl < L) {
-            read_pairs<G>(Uq, bt, bl, P, pq);
-            read_pairs<G>(Uk, bt, bl, P, pk);
-        }
-        __syncthreads();  // (4) the pairs are dead: Phi_Q and Phi_K take their space
-        if (bl < L) {
-            put_phi<PS, PC, kPhiSplit>(PhQ, nullptr, bt, bl, P, pq, false);
-            put_phi<PS, PC, kPhiSplit>(PhK, KTs, bt, bl, P, pk, bt >= rows - r0);
-        }
+        write_sigmas<G>(Uq, uq, beta2, w, g, lr);
+        write_sigmas<G>(Uk, uk, beta2, w, g, lr);
+        __syncthreads();  // (2) the x planes are dead: Phi_Q and Phi_K take their space
+        build_phi<PS, PC, kPhiSplit>(Uq, G::kUPitch, PhQ, nullptr, L, P, C);
+        build_phi<PS, PC, kPhiSplit>(Uk, G::kUPitch, PhK, KTs, L, P, rows - r0);
         if (SP > S) {
             zero_pad_rows<PS, SP>(PhQ, S);
             zero_pad_rows<PS, SP>(PhK, S);
         }
-        __syncthreads();  // (5)
+        __syncthreads();  // (3) U is dead: the partial denominators take its space
 
         // Running mass Abar^T [s][i] = A0 + Phi_K^T tril(1) for this wave's
         // s-blocks, and the partial denominators sum_s Phi_Q[i][s] Abar[s][i].
@@ -614,7 +623,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
                     if (4 * g + rr > lr) pacc[pb][rr] = 0.f;
             }
         }
-        __syncthreads();  // (6) Phi_K is dead: G takes its space
+        __syncthreads();  // (4) Phi_K is dead: G takes its space
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
             if (w + 4 * pb >= NLB) continue;
@@ -622,7 +631,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
             split4<true>(pacc[pb][0], pacc[pb][1], pacc[pb][2], pacc[pb][3], hi, lo);
             PG::put4(Gs, 16 * pbi[pb] + lr, 16 * pbj[pb] + 4 * g, hi, lo);
         }
-        __syncthreads();  // (7)
+        __syncthreads();  // (5)
 
         // Reciprocal denominators of this lane's query rows (fixed wave order).
         float rden[NBI];
