@@ -288,6 +288,13 @@ def bench_alg1(args) -> int:
     def plain():
         check(abi.alg1_fwd(*ptrs, None, sh, args.tile, variant, ws.data_ptr(), ws_bytes, stream))
 
+    if args.calibrate_copy:
+        src = torch.ones(args.calibrate_copy << 18, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     events = HipEvents()
     per_step = [events.array(8) for _ in range(args.steps)]
     warm = events.array(8)
