@@ -30,6 +30,11 @@
 // then tanh and the two sigmoids of every plane, then the corner products
 // (plane 0 the most significant bit).
 //
+// Every LDS tile is stored with tokens as rows (q, k, v rows, Phi_Q, Phi_K).
+// The products that contract over tokens (Phi_K^T V, Phi_K^T tril(1), V^T G^T)
+// take their operand fragments with gfx950's transposing LDS read
+// (ds_read_b64_tr_b16, Plane::frag_tr), so no tile is ever written twice.
+//
 // Two rounding variants, chosen by the template flag kPhiSplit (the
 // reference's v2a / v2b split, race_causal_fwd.h:33-41):
 //   kPhiSplit = true   Phi_Q and Phi_K enter every product as bf16 hi/lo
@@ -104,95 +109,73 @@ template <bool kPhiSplit, int SP, int D, int LPP>
 struct A1Geo {
     static constexpr int C = kA1Chunk;
     static constexpr int kD = D;
-    using PX = Plane<false, D>;       // token rows over features: the q / k rows (bf16)
+    using PX = Plane<false, D>;       // token rows over features: the q, k, v rows (bf16)
     using PW = Plane<true, D>;        // plane rows over features: W as hi/lo
+    using PW3 = Plane<false, D>;      // plane rows over features: third bf16 term of W
     using PS = Plane<kPhiSplit, SP>;  // token rows over buckets: Phi_Q, Phi_K
-    using PC = Plane<kPhiSplit, C>;   // bucket rows over tokens: Phi_K^T
     using PG = Plane<true, C>;        // query rows over keys: G
-    using PV = Plane<false, C>;       // feature rows over tokens: V^T
     static constexpr int kUPitch = LPP + 1;  // floats per token: one per plane
     static constexpr int kUBytes = C * kUPitch * 4;
     static constexpr int kXBytes = C * PX::kPitch;
     static constexpr int kPhiBytes = C * PS::kPitch;
     static constexpr int kGBytes = C * PG::kPitch;
-    static constexpr int kKTBytes = SP * PC::kPitch;
-    static constexpr int kVTBytes = D * PV::kPitch;
-    using PW3 = Plane<false, D>;      // plane rows over features: third bf16 term of W
     static constexpr int kDenBytes = 4 * C * 4;
     static constexpr int mx(int a, int b) { return a > b ? a : b; }
-    // Region A of the output pass holds the x planes of q and k, then Phi_Q
-    // and Phi_K (G over Phi_K); region U the plane values of q and k, then
-    // the partial denominators.
-    static constexpr int kRegionOut = mx(2 * kXBytes, kPhiBytes + mx(kPhiBytes, kGBytes));
+    // Output pass: region A holds the q and k rows, then Phi_Q and Phi_K;
+    // then G; region U the plane values of q and k, then the partial
+    // denominators; the V rows; W.
+    static constexpr int kRegionOut = mx(2 * kXBytes, 2 * kPhiBytes);
     static constexpr int kRegionU = mx(2 * kUBytes, kDenBytes);
     // W = hi + mid + lo in the fp32 variant where the output pass still fits
     // 160 KB of LDS (the projection is then exact in fp32 arithmetic), hi + mid
-    // otherwise (every shape but d = 128, S = 128, L P > 16) and in the bf16
-    // variant.
-    static constexpr int kOutBase = kRegionOut + kRegionU + kKTBytes + kVTBytes + LPP * PW::kPitch;
+    // otherwise and in the bf16 variant.
+    static constexpr int kOutBase = kRegionOut + kGBytes + kRegionU + kXBytes + LPP * PW::kPitch;
     static constexpr bool kW3 = kPhiSplit && kOutBase + LPP * PW3::kPitch <= 160 * 1024;
     static constexpr int kWBytes = LPP * PW::kPitch + (kW3 ? LPP * PW3::kPitch : 0);
     static constexpr int kOutputLds = kOutBase + kWBytes - LPP * PW::kPitch;
-    static constexpr int kSumsLds = kXBytes + kUBytes + kKTBytes + kVTBytes + kWBytes;
+    // Tile sums: the k rows, then Phi_K; U; the V rows; W.
+    static constexpr int kRegionSums = mx(kXBytes, kPhiBytes);
+    static constexpr int kSumsLds = kRegionSums + kUBytes + kXBytes + kWBytes;
     static constexpr int kOutBlocks = kOutputLds <= 80 * 1024 ? 2 : 1;
-    static constexpr int kSumsBlocks = kSumsLds <= 80 * 1024 ? 2 : 1;
+    // (S = D = 128 holds a 128 x 128 accumulator tile: one workgroup per CU.)
+    static constexpr int kSumsBlocks = kSumsLds <= 80 * 1024 && SP * D < 128 * 128 ? 2 : 1;
     static constexpr int NSB = SP / 16, NBI = C / 16, NKS = SP / 32, NKC = C / 32, NKD = D / 32;
     static constexpr int CBW = D / 64;         // c-blocks per wave
     static constexpr int SBW = (NSB + 3) / 4;  // s-blocks per wave
     static constexpr int NPB = LPP / 16;       // plane blocks
-    static constexpr int kXPer = C * D / 8 / kThreads;        // 16-byte vectors per thread per x tensor
-    static constexpr int kVBlk = (C / 4) * (D / 8);           // V blocks of 4 tokens x 8 features
-    static_assert(kXPer * kThreads * 8 == C * D, "x staging");
-    static_assert(kVBlk <= kThreads, "V staging");
+    static_assert(C * D % (8 * kThreads) == 0, "row staging");
     static_assert(kOutputLds <= 160 * 1024, "output pass LDS");
 };
 
-// Raw registers of one sub-chunk: the x rows of up to two tensors and V.
+// Raw registers of one sub-chunk: the token rows of NX bf16 tensors, as
+// 16-byte vectors (8 features); vector e of a thread is row e / (D / 8).
 template <int D, int NX>
 struct A1Stage {
-    static constexpr int kXPer = kA1Chunk * D / 8 / kThreads;
-    static constexpr int kVBlk = (kA1Chunk / 4) * (D / 8);
-    uint4 x[NX][kXPer];
-    uint4 v[4];
+    static constexpr int kPer = kA1Chunk * D / 8 / kThreads;
+    uint4 x[NX][kPer];
 
-    __device__ __forceinline__ void load(const __amdgpu_buffer_rsrc_t (&xr)[NX], __amdgpu_buffer_rsrc_t vr,
-                                         int r0) {
+    __device__ __forceinline__ void load(const __amdgpu_buffer_rsrc_t (&xr)[NX], int r0) {
         const int tid = threadIdx.x;
 #pragma unroll
-        for (int p = 0; p < kXPer; ++p) {
+        for (int p = 0; p < kPer; ++p) {
             const int e = tid + p * kThreads, t = e / (D / 8), b = e % (D / 8);
 #pragma unroll
             for (int i = 0; i < NX; ++i)
                 x[i][p] = buf_load16<kOutKVPolicy>(xr[i], ((r0 + t) * D + 8 * b) * 2);
         }
-        if (tid < kVBlk) {
-            const int a = tid / (D / 8), b = tid % (D / 8);
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) v[rr] = buf_load16<kOutKVPolicy>(vr, ((r0 + 4 * a + rr) * D + 8 * b) * 2);
-        }
     }
 
-    // x rows into token-row planes, V into the transposed feature-row plane.
-    template <typename PX, typename PV>
-    __device__ __forceinline__ void store(unsigned char* const (&X)[NX], unsigned char* VTs) const {
+    // Rows into token-row planes.
+    template <typename PX>
+    __device__ __forceinline__ void store(unsigned char* const (&X)[NX]) const {
         const int tid = threadIdx.x;
 #pragma unroll
-        for (int p = 0; p < kXPer; ++p) {
+        for (int p = 0; p < kPer; ++p) {
             const int e = tid + p * kThreads, t = e / (D / 8), b = e % (D / 8);
 #pragma unroll
             for (int i = 0; i < NX; ++i) {
                 PX::put4(X[i], t, 8 * b, make_uint2(x[i][p].x, x[i][p].y), make_uint2(0, 0));
                 PX::put4(X[i], t, 8 * b + 4, make_uint2(x[i][p].z, x[i][p].w), make_uint2(0, 0));
-            }
-        }
-        if (tid < kVBlk) {
-            const int a = tid / (D / 8), b = tid % (D / 8);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                uint2 h;
-                h.x = half16(word4(v[0], c >> 1), c & 1) | (half16(word4(v[1], c >> 1), c & 1) << 16);
-                h.y = half16(word4(v[2], c >> 1), c & 1) | (half16(word4(v[3], c >> 1), c & 1) << 16);
-                PV::put4(VTs, 8 * b + c, 4 * a, h, h);
             }
         }
     }
@@ -272,70 +255,46 @@ __device__ __forceinline__ void write_sigmas(float* U, const f32x4 (&acc)[G::NPB
         }
 }
 
-// Phi of the sub-chunk's C tokens from U: into the token-row plane Ph
-// (nullable) and the bucket-row plane KTs (nullable); tokens >= valid get 0.
-// With R >= 4, item (tq, l, m) covers tokens 4 tq .. 4 tq + 3, table l and
-// corners 4 m .. 4 m + 3: the planes above the last two select by the bits
-// of m (plane 0 the most significant bit of r), the last two give the quad,
-// and both layouts take 4-element stores.  R = 2 (P = 1) goes element-wise.
-template <typename PS, typename PC, bool kSplit>
-__device__ __forceinline__ void build_phi(const float* U, int kUP, unsigned char* Ph, unsigned char* KTs,
-                                          int L, int P, int valid) {
+// Phi of the sub-chunk's C tokens from U into the token-row plane Ph; tokens
+// >= valid get 0.  Item (t, l), one per thread: the P sigmoid pairs of
+// token t, table l are decoded once; the corners go out in quads, the planes
+// above the last two selecting by the bits of the quad index (plane 0 the
+// most significant bit of r) and the last two giving the quad's four corners.
+template <typename PS, bool kSplit>
+__device__ __forceinline__ void build_rows(const float* U, int kUP, unsigned char* Ph, int L, int P,
+                                           int valid) {
     const int R = 1 << P;
+    const int e = threadIdx.x;
+    if (e >= kA1Chunk * L) return;
+    const int t = e % kA1Chunk, l = e / kA1Chunk;
+    const bool live = t < valid;
+    const float* ur = U + t * kUP + l * P;
     if (P >= 2) {
-        const int RQ = R / 4, items = (kA1Chunk / 4) * L * RQ;
-        for (int e = threadIdx.x; e < items; e += kThreads) {
-            const int m = e % RQ, l = (e / RQ) % L, tq = e / (RQ * L);
-            float pr[4][4];
+        float2 hp[3];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int t = 4 * tq + u;
-                const float* ur = U + t * kUP + l * P;
-                float base = 1.f;
+        for (int p = 0; p < 3; ++p) hp[p] = p < P - 2 ? sigma_pair(ur[p]) : make_float2(1.f, 1.f);
+        const float2 s1 = sigma_pair(ur[P - 2]), s2 = sigma_pair(ur[P - 1]);
+        const float q0 = s1.y * s2.y, q1 = s1.y * s2.x, q2 = s1.x * s2.y, q3 = s1.x * s2.x;
 #pragma unroll
-                for (int p = 0; p < 3; ++p) {
-                    if (p < P - 2) {
-                        const float2 sp = sigma_pair(ur[p]);
-                        base *= ((m >> (P - 3 - p)) & 1) ? sp.x : sp.y;
-                    }
-                }
-                const float2 s1 = sigma_pair(ur[P - 2]), s2 = sigma_pair(ur[P - 1]);
-                const bool live = t < valid;
-                pr[u][0] = live ? base * (s1.y * s2.y) : 0.f;
-                pr[u][1] = live ? base * (s1.y * s2.x) : 0.f;
-                pr[u][2] = live ? base * (s1.x * s2.y) : 0.f;
-                pr[u][3] = live ? base * (s1.x * s2.x) : 0.f;
-            }
-            if (Ph) {
+        for (int m = 0; m < 8; ++m) {
+            if (4 * m >= R) continue;
+            float base = 1.f;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    uint2 hi, lo;
-                    split4<kSplit>(pr[u][0], pr[u][1], pr[u][2], pr[u][3], hi, lo);
-                    PS::put4(Ph, 4 * tq + u, l * R + 4 * m, hi, lo);
-                }
-            }
-            if (KTs) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    uint2 hi, lo;
-                    split4<kSplit>(pr[0][c], pr[1][c], pr[2][c], pr[3][c], hi, lo);
-                    PC::put4(KTs, l * R + 4 * m + c, 4 * tq, hi, lo);
-                }
-            }
+            for (int p = 0; p < 3; ++p)
+                if (p < P - 2) base *= ((m >> (P - 3 - p)) & 1) ? hp[p].x : hp[p].y;
+            uint2 hi, lo;
+            split4<kSplit>(live ? base * q0 : 0.f, live ? base * q1 : 0.f, live ? base * q2 : 0.f,
+                           live ? base * q3 : 0.f, hi, lo);
+            PS::put4(Ph, t, l * R + 4 * m, hi, lo);
         }
     } else {
-        for (int e = threadIdx.x; e < kA1Chunk * L; e += kThreads) {
-            const int t = e % kA1Chunk, l = e / kA1Chunk;
-            const float2 sp = sigma_pair(U[t * kUP + l]);
-            const bool live = t < valid;
-            const float x[2] = {live ? sp.y : 0.f, live ? sp.x : 0.f};
+        const float2 sp = sigma_pair(ur[0]);
+        const float x[2] = {live ? sp.y : 0.f, live ? sp.x : 0.f};
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                uint16_t hi, lo;
-                split1<kSplit>(x[r], hi, lo);
-                if (Ph) PS::put1(Ph, t, 2 * l + r, hi, lo);
-                if (KTs) PC::put1(KTs, 2 * l + r, t, hi, lo);
-            }
+        for (int r = 0; r < 2; ++r) {
+            uint16_t hi, lo;
+            split1<kSplit>(x[r], hi, lo);
+            PS::put1(Ph, t, 2 * l + r, hi, lo);
         }
     }
 }
@@ -360,13 +319,13 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
     const float* __restrict__ beta_p, float* __restrict__ records, int64_t T, int tile, int64_t tiles,
     int64_t rec, int L, int P) {
     using G = A1Geo<kPhiSplit, SP, D, LPP>;
-    using PC = typename G::PC;
+    using PS = typename G::PS;
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Xk = lds;
-    float* U = reinterpret_cast<float*>(lds + G::kXBytes);
-    unsigned char* KTs = lds + G::kXBytes + G::kUBytes;
-    unsigned char* VTs = KTs + G::kKTBytes;
-    unsigned char* Ws = VTs + G::kVTBytes;
+    unsigned char* PhK = lds;  // once the k rows are projected
+    float* U = reinterpret_cast<float*>(lds + G::kRegionSums);
+    unsigned char* Vs = lds + G::kRegionSums + G::kUBytes;
+    unsigned char* Ws = Vs + G::kXBytes;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -375,12 +334,10 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
     const int rows = int(min(T, t_begin + tile) - t_begin);
     const int S = L << P;
     const float beta2 = 2.0f * beta_p[0];
-    const __amdgpu_buffer_rsrc_t xr[1] = {make_rsrc(k + (n * T + t_begin) * D, int64_t(rows) * D * 2)};
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + (n * T + t_begin) * D, int64_t(rows) * D * 2);
+    const __amdgpu_buffer_rsrc_t xr[2] = {make_rsrc(k + (n * T + t_begin) * D, int64_t(rows) * D * 2),
+                                          make_rsrc(v + (n * T + t_begin) * D, int64_t(rows) * D * 2)};
 
     load_planes<G, kPhiSplit>(Ws, W, L * P);
-    for (int e = tid; e < (SP - S) * kA1Chunk; e += kThreads)
-        PC::put1(KTs, S + e / kA1Chunk, e % kA1Chunk, 0, 0);
 
     f32x4 bacc[G::NSB][G::CBW], aacc[G::SBW];
 #pragma unroll
@@ -392,35 +349,37 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
     bf16x8 ones;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
-    unsigned char* const Xs[1] = {Xk};
+    unsigned char* const Xs[2] = {Xk, Vs};
 
-    A1Stage<D, 1> st;
-    st.load(xr, vr, 0);
+    A1Stage<D, 2> st;
+    st.load(xr, 0);
     for (int r0 = 0; r0 < rows; r0 += kA1Chunk) {
         __syncthreads();
-        st.template store<typename G::PX, typename G::PV>(Xs, VTs);
-        st.load(xr, vr, r0 + kA1Chunk);  // past the tile: zeros, never used
+        st.template store<typename G::PX>(Xs);
+        st.load(xr, r0 + kA1Chunk);  // past the tile: zeros, never used
         __syncthreads();
         f32x4 uk[G::NPB];
         project<G, kPhiSplit>(Xk, Ws, w, g, lr, uk);
         write_sigmas<G>(U, uk, beta2, w, g, lr);
+        __syncthreads();  // the k rows are dead: Phi_K takes their space
+        build_rows<PS, kPhiSplit>(U, G::kUPitch, PhK, L, P, rows - r0);
+        if (SP > S) zero_pad_rows<PS, SP>(PhK, S);
         __syncthreads();
-        build_phi<typename G::PS, PC, kPhiSplit>(U, G::kUPitch, nullptr, KTs, L, P, rows - r0);
-        __syncthreads();
+        // Phi_K^T and V fragments straight from the token-row planes.
 #pragma unroll
         for (int cbw = 0; cbw < G::CBW; ++cbw) {
             bf16x8 vh[G::NKC];
 #pragma unroll
             for (int kk = 0; kk < G::NKC; ++kk) {
                 bf16x8 dummy;
-                G::PV::frag(VTs, 16 * (w + 4 * cbw) + lr, kk, g, vh[kk], dummy);
+                G::PX::frag_tr(Vs, 32 * kk, 16 * (w + 4 * cbw), g, lr, vh[kk], dummy);
             }
 #pragma unroll
             for (int sb = 0; sb < G::NSB; ++sb)
 #pragma unroll
                 for (int kk = 0; kk < G::NKC; ++kk) {
                     bf16x8 kh, kl;
-                    PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
+                    PS::frag_tr(PhK, 32 * kk, 16 * sb, g, lr, kh, kl);
                     bacc[sb][cbw] = mfma_mix<kPhiSplit, false>(kh, kl, vh[kk], vh[kk], bacc[sb][cbw]);
                 }
         }
@@ -431,7 +390,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
 #pragma unroll
             for (int kk = 0; kk < G::NKC; ++kk) {
                 bf16x8 kh, kl;
-                PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
+                PS::frag_tr(PhK, 32 * kk, 16 * sb, g, lr, kh, kl);
                 aacc[j] = mfma_mix<kPhiSplit, false>(kh, kl, ones, ones, aacc[j]);
             }
         }
@@ -461,9 +420,9 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
 
 // ---------------------------------------------------------------------------
 // K3: the output pass, one workgroup per (tile, stream).  Per sub-chunk (the
-// numbers are the barriers): stage q, k rows and V^T (1) -> project q, k and
-// store their plane values (2) -> Phi_Q, Phi_K, Phi_K^T (3) -> running mass,
-// denominators, G^T blocks (4) -> G plane (5) -> output and state update.
+// numbers are the barriers): stage the q, k, v rows (1) -> project q, k and
+// store their plane values (2) -> Phi_Q, Phi_K (3) -> running mass,
+// denominators, G blocks (4) -> output and state update.
 template <bool kPhiSplit, int SP, int D, int LPP>
 __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks)) void alg1_output_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -471,7 +430,6 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
     const float* __restrict__ records, int64_t T, int tile, int64_t tiles, int64_t rec, int L, int P) {
     using G = A1Geo<kPhiSplit, SP, D, LPP>;
     using PS = typename G::PS;
-    using PC = typename G::PC;
     using PG = typename G::PG;
     constexpr int NSB = G::NSB, NBI = G::NBI, NKS = G::NKS, NKC = G::NKC, CBW = G::CBW, SBW = G::SBW;
     constexpr int NLB = NBI * (NBI + 1) / 2;  // lower-triangular G blocks
@@ -480,15 +438,14 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Xq = lds;
     unsigned char* Xk = lds + G::kXBytes;
-    unsigned char* PhQ = lds;
+    unsigned char* PhQ = lds;  // once the q and k rows are projected
     unsigned char* PhK = lds + G::kPhiBytes;
-    unsigned char* Gs = PhK;
-    float* Uq = reinterpret_cast<float*>(lds + G::kRegionOut);
+    unsigned char* Gs = lds + G::kRegionOut;
+    float* Uq = reinterpret_cast<float*>(Gs + G::kGBytes);
     float* Uk = Uq + C * G::kUPitch;
     float* denp = Uq;  // [4][C], once the builder has read U
-    unsigned char* KTs = lds + G::kRegionOut + G::kRegionU;
-    unsigned char* VTs = KTs + G::kKTBytes;
-    unsigned char* Ws = VTs + G::kVTBytes;
+    unsigned char* Vs = Gs + G::kGBytes + G::kRegionU;
+    unsigned char* Ws = Vs + G::kXBytes;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -498,13 +455,12 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
     const int S = L << P;
     const float beta2 = 2.0f * beta_p[0];
     const int64_t bytes = int64_t(rows) * D * 2;
-    const __amdgpu_buffer_rsrc_t xr[2] = {make_rsrc(q + (n * T + t_begin) * D, bytes),
-                                          make_rsrc(k + (n * T + t_begin) * D, bytes)};
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + (n * T + t_begin) * D, bytes);
+    const __amdgpu_buffer_rsrc_t xr[3] = {make_rsrc(q + (n * T + t_begin) * D, bytes),
+                                          make_rsrc(k + (n * T + t_begin) * D, bytes),
+                                          make_rsrc(v + (n * T + t_begin) * D, bytes)};
     const __amdgpu_buffer_rsrc_t or_ = make_rsrc(out + (n * T + t_begin) * D, bytes);
 
     load_planes<G, kPhiSplit>(Ws, W, L * P);
-    for (int e = tid; e < (SP - S) * C; e += kThreads) PC::put1(KTs, S + e / C, e % C, 0, 0);
 
     // Carried state from the tile's exclusive prefix record (zero past S).
     const float* rp = records + (n * tiles + ti) * rec;
@@ -531,14 +487,14 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
     bf16x8 ones;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
-    unsigned char* const Xs[2] = {Xq, Xk};
+    unsigned char* const Xs[3] = {Xq, Xk, Vs};
 
-    A1Stage<D, 2> st;
-    st.load(xr, vr, 0);
+    A1Stage<D, 3> st;
+    st.load(xr, 0);
     for (int r0 = 0; r0 < rows; r0 += C) {
         __syncthreads();
-        st.template store<typename G::PX, typename G::PV>(Xs, VTs);
-        st.load(xr, vr, r0 + C);  // past the tile: zeros, never used
+        st.template store<typename G::PX>(Xs);
+        st.load(xr, r0 + C);  // past the tile: zeros, never used
         __syncthreads();  // (1)
         f32x4 uq[G::NPB], uk[G::NPB];
         project<G, kPhiSplit>(Xq, Ws, w, g, lr, uq);
@@ -546,8 +502,8 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
         write_sigmas<G>(Uq, uq, beta2, w, g, lr);
         write_sigmas<G>(Uk, uk, beta2, w, g, lr);
         __syncthreads();  // (2) the x planes are dead: Phi_Q and Phi_K take their space
-        build_phi<PS, PC, kPhiSplit>(Uq, G::kUPitch, PhQ, nullptr, L, P, C);
-        build_phi<PS, PC, kPhiSplit>(Uk, G::kUPitch, PhK, KTs, L, P, rows - r0);
+        build_rows<PS, kPhiSplit>(Uq, G::kUPitch, PhQ, L, P, C);
+        build_rows<PS, kPhiSplit>(Uk, G::kUPitch, PhK, L, P, rows - r0);
         if (SP > S) {
             zero_pad_rows<PS, SP>(PhQ, S);
             zero_pad_rows<PS, SP>(PhK, S);
@@ -565,7 +521,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
             if (sb >= NSB) continue;
             bf16x8 kh[NKC], kl[NKC];
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) PC::frag(KTs, 16 * sb + lr, kk, g, kh[kk], kl[kk]);
+            for (int kk = 0; kk < NKC; ++kk) PS::frag_tr(PhK, 32 * kk, 16 * sb, g, lr, kh[kk], kl[kk]);
             f32x4 last;
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) {
@@ -623,7 +579,6 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
                     if (4 * g + rr > lr) pacc[pb][rr] = 0.f;
             }
         }
-        __syncthreads();  // (4) Phi_K is dead: G takes its space
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
             if (w + 4 * pb >= NLB) continue;
@@ -631,7 +586,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
             split4<true>(pacc[pb][0], pacc[pb][1], pacc[pb][2], pacc[pb][3], hi, lo);
             PG::put4(Gs, 16 * pbi[pb] + lr, 16 * pbj[pb] + 4 * g, hi, lo);
         }
-        __syncthreads();  // (5)
+        __syncthreads();  // (4)
 
         // Reciprocal denominators of this lane's query rows (fixed wave order).
         float rden[NBI];
@@ -650,7 +605,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
 #pragma unroll
             for (int kk = 0; kk < NKC; ++kk) {
                 bf16x8 dummy;
-                G::PV::frag(VTs, 16 * cb + lr, kk, g, vh[kk], dummy);
+                G::PX::frag_tr(Vs, 32 * kk, 16 * cb, g, lr, vh[kk], dummy);
             }
             f32x4 o[NBI];
 #pragma unroll
@@ -696,7 +651,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
 #pragma unroll
                 for (int kk = 0; kk < NKC; ++kk) {
                     bf16x8 kh, kl;
-                    PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
+                    PS::frag_tr(PhK, 32 * kk, 16 * sb, g, lr, kh, kl);
                     b0[sb][cbw] = mfma_mix<kPhiSplit, false>(kh, kl, vh[kk], vh[kk], b0[sb][cbw]);
                 }
         }

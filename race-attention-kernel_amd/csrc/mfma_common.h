@@ -186,6 +186,34 @@ struct Plane {
         hi = *reinterpret_cast<const bf16x8*>(p);
         if constexpr (kSplit) lo = *reinterpret_cast<const bf16x8*>(p + kLoOff);
     }
+    // Byte offset of the 8-byte group holding elements k0 .. k0 + 3 (k0 % 4 == 0)
+    // of row `row` in the hi plane.
+    __device__ __forceinline__ static int off4(int row, int k0) {
+        const int pos = fpos(k0);
+        return row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 8 * ((pos >> 2) & 1);
+    }
+    // Fragment of the transposed tile, whose contraction index runs over this
+    // plane's rows: lane (g, lr) gets elements (row0 + 4 g + e % 4 + 16 (e / 4),
+    // col0 + lr), e = 0..7 (row0 % 32 == 0, col0 % 16 == 0).  Two
+    // ds_read_b64_tr_b16 per plane: within each 16-lane group, lane 4 r + q
+    // addresses row r, columns 4 q .. 4 q + 3 of a 4 x 16 block, and lane i
+    // receives column i.
+    __device__ __forceinline__ static void frag_tr(const unsigned char* t, int row0, int col0, int g,
+                                                   int lr, bf16x8& hi, bf16x8& lo) {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        const int r = row0 + 4 * g + (lr >> 2), k0 = col0 + 4 * (lr & 3);
+        const unsigned char* p0 = t + off4(r, k0);
+        const unsigned char* p1 = t + off4(r + 16, k0);
+        const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+        const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+        hi = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+        if constexpr (kSplit) {
+            const s16x4 c = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + kLoOff));
+            const s16x4 d = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + kLoOff));
+            lo = __builtin_bit_cast(bf16x8, __builtin_shufflevector(c, d, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    }
 };
 
 // Lower-triangular ones as a B operand for the running mass: element e of
