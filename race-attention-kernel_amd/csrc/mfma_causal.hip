@@ -37,7 +37,9 @@
 //     fpos(k) = 32 (k / 32) + 8 ((k / 4) % 4) + 4 ((k / 16) % 2) + k % 4
 // of each plane and one fragment is a single 16-byte read per plane (the
 // chunk swizzle of Plane keeps those reads and the staging stores spread over
-// the banks).
+// the banks).  Tiles are stored with tokens as rows only; the operands that
+// contract over tokens (K^T, V^T) are read transposed from the same tiles with
+// ds_read_b64_tr_b16 (Plane::frag_tr), two reads per fragment and plane.
 #include "mfma_common.h"
 
 namespace race {
@@ -46,26 +48,28 @@ namespace {
 using namespace mfma;
 
 
-// Geometry of one (S, D, C, dtype) specialization.
+// Geometry of one (S, D, C, dtype) specialization.  Every tile is stored with
+// tokens as rows (W, K, V; P with queries as rows); products that contract
+// over tokens read their fragments transposed (Plane::frag_tr).
 template <typename TIn, int S, int D, int C>
 struct Geo {
     static constexpr bool kSplit = std::is_same<TIn, float>::value;
     static constexpr int E = Elem<TIn>::kPerVec;
-    using PS = Plane<kSplit, S>;  // rows over buckets: W, K
-    using PC = Plane<kSplit, C>;  // rows over tokens: K^T, V^T, P
+    using PS = Plane<kSplit, S>;  // token rows over buckets: W, K
+    using PC = Plane<kSplit, C>;  // query rows over keys: P
+    using PD = Plane<kSplit, D>;  // token rows over value columns: V
     static constexpr int kWBytes = C * PS::kPitch;
-    static constexpr int kKBytes = C * (PS::kPitch > PC::kPitch ? PS::kPitch : PC::kPitch);
-    static constexpr int kKTBytes = S * PC::kPitch;
-    static constexpr int kVTBytes = D * PC::kPitch;
-    static constexpr int kOutputLds = kWBytes + kKBytes + kKTBytes + kVTBytes;
-    static constexpr int kSumsLds = kKTBytes + kVTBytes + 16 * S * 4;
+    static constexpr int kKBytes = C * PS::kPitch;
+    static constexpr int kPBytes = C * PC::kPitch;
+    static constexpr int kVBytes = C * PD::kPitch;
+    static constexpr int kOutputLds = kWBytes + kKBytes + kPBytes + kVBytes;
+    static constexpr int kSumsLds = kKBytes + kVBytes + 16 * S * 4;
     // Register staging of K and V: blocks of 4 rows x E columns.
     static constexpr int kKBlk = (C / 4) * (S / E);
     static constexpr int kKPer = (kKBlk + kThreads - 1) / kThreads;
     static constexpr int kVBlk = (C / 4) * (D / E);
     static constexpr int kVPer = (kVBlk + kThreads - 1) / kThreads;
     static_assert(S % 64 == 0 && D % 64 == 0 && (C == 32 || C == 64), "unsupported tile");
-    static_assert(S >= C, "P overlays the K tile");
 };
 
 // Raw K and V registers of one sub-chunk.
@@ -101,10 +105,9 @@ struct KVStage {
         }
     }
 
-    // K^T [S][C] and V^T [D][C] plane tiles, K [C][S] too when Ks is given,
-    // column sums of K into asum when given.  Each element is split once.
-    __device__ __forceinline__ void store(unsigned char* Ks, unsigned char* KTs, unsigned char* VTs,
-                                          float* asum) const {
+    // The K rows [C][S] and V rows [C][D] as plane tiles (each element split
+    // once), and the column sums of K into asum when given.
+    __device__ __forceinline__ void store(unsigned char* Ks, unsigned char* Vs, float* asum) const {
         constexpr bool kSplit = G::kSplit;
         constexpr int E = G::E;
         const int tid = threadIdx.x;
@@ -120,29 +123,21 @@ struct KVStage {
                 for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
                     for (int c = 0; c < 4; ++c) x[rr][c] = Elem<TIn>::get(k[p][rr], 4 * h + c);
-                const int s0 = b * E + 4 * h;
-                // Column slots (4 tokens of one bucket) for K^T.
-                uint2 chi[4], clo[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    split4<kSplit>(x[0][c], x[1][c], x[2][c], x[3][c], chi[c], clo[c]);
-                    G::PC::put4(KTs, s0 + c, 4 * a, chi[c], clo[c]);
-                    if (asum) asum[p * E + 4 * h + c] += ((x[0][c] + x[1][c]) + x[2][c]) + x[3][c];
-                }
-                if (Ks) {
-                    // Row slots (4 buckets of one token) for K, from the same split:
-                    // element (rr, c) is half rr % 2 of word rr / 2 of chi[c].
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        uint2 rhi, rlo;
-                        rhi.x = half16(word(chi[0], rr >> 1), rr & 1) | (half16(word(chi[1], rr >> 1), rr & 1) << 16);
-                        rhi.y = half16(word(chi[2], rr >> 1), rr & 1) | (half16(word(chi[3], rr >> 1), rr & 1) << 16);
-                        if constexpr (kSplit) {
-                            rlo.x = half16(word(clo[0], rr >> 1), rr & 1) | (half16(word(clo[1], rr >> 1), rr & 1) << 16);
-                            rlo.y = half16(word(clo[2], rr >> 1), rr & 1) | (half16(word(clo[3], rr >> 1), rr & 1) << 16);
-                        }
-                        G::PS::put4(Ks, 4 * a + rr, s0, rhi, rlo);
+                for (int rr = 0; rr < 4; ++rr) {
+                    uint2 hi, lo;
+                    if constexpr (kSplit) {
+                        split4<true>(x[rr][0], x[rr][1], x[rr][2], x[rr][3], hi, lo);
+                    } else {  // bf16 rows go in as they are
+                        hi = make_uint2(h ? k[p][rr].z : k[p][rr].x, h ? k[p][rr].w : k[p][rr].y);
+                        lo = hi;
                     }
+                    G::PS::put4(Ks, 4 * a + rr, b * E + 4 * h, hi, lo);
+                }
+                if (asum) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        asum[p * E + 4 * h + c] += ((x[0][c] + x[1][c]) + x[2][c]) + x[3][c];
                 }
             }
         }
@@ -152,12 +147,20 @@ struct KVStage {
             if (blk >= G::kVBlk) continue;
             const int a = blk / (D / E), b = blk % (D / E);
 #pragma unroll
-            for (int c = 0; c < E; ++c) {
-                uint2 hi, lo;
-                split4<kSplit>(Elem<TIn>::get(v[p][0], c), Elem<TIn>::get(v[p][1], c),
-                               Elem<TIn>::get(v[p][2], c), Elem<TIn>::get(v[p][3], c), hi, lo);
-                G::PC::put4(VTs, b * E + c, 4 * a, hi, lo);
-            }
+            for (int h = 0; h < E / 4; ++h)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    uint2 hi, lo;
+                    if constexpr (kSplit) {
+                        split4<true>(Elem<TIn>::get(v[p][rr], 4 * h), Elem<TIn>::get(v[p][rr], 4 * h + 1),
+                                     Elem<TIn>::get(v[p][rr], 4 * h + 2), Elem<TIn>::get(v[p][rr], 4 * h + 3),
+                                     hi, lo);
+                    } else {
+                        hi = make_uint2(h ? v[p][rr].z : v[p][rr].x, h ? v[p][rr].w : v[p][rr].y);
+                        lo = hi;
+                    }
+                    G::PD::put4(Vs, 4 * a + rr, b * E + 4 * h, hi, lo);
+                }
         }
     }
 };
@@ -171,13 +174,14 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
     const TIn* __restrict__ k, const TIn* __restrict__ v, float* __restrict__ records, int64_t T,
     int tile, int64_t tiles, int64_t rec) {
     using G = Geo<TIn, S, D, C>;
-    using PC = typename G::PC;
+    using PS = typename G::PS;
+    using PD = typename G::PD;
     constexpr bool kSplit = G::kSplit;
     constexpr int NSB = S / 16, NKC = C / 32, CBW = D / 64;
     extern __shared__ __align__(16) unsigned char lds[];
-    unsigned char* KTs = lds;
-    unsigned char* VTs = KTs + G::kKTBytes;
-    float* Apart = reinterpret_cast<float*>(VTs + G::kVTBytes);  // [16][S]
+    unsigned char* Ks = lds;
+    unsigned char* Vs = Ks + G::kKBytes;
+    float* Apart = reinterpret_cast<float*>(Vs + G::kVBytes);  // [16][S]
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -201,20 +205,20 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
     st.load(kr, vr, 0);
     for (int r0 = 0; r0 < rows; r0 += C) {
         __syncthreads();
-        st.store(nullptr, KTs, VTs, asum);
+        st.store(Ks, Vs, asum);
         st.load(kr, vr, r0 + C);  // past the tile: zeros, never used
         __syncthreads();
         bf16x8 vh[CBW][NKC], vl[CBW][NKC];
 #pragma unroll
         for (int cbw = 0; cbw < CBW; ++cbw)
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) PC::frag(VTs, 16 * (w + 4 * cbw) + lr, kk, g, vh[cbw][kk], vl[cbw][kk]);
+            for (int kk = 0; kk < NKC; ++kk) PD::frag_tr(Vs, 32 * kk, 16 * (w + 4 * cbw), g, lr, vh[cbw][kk], vl[cbw][kk]);
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
             for (int kk = 0; kk < NKC; ++kk) {
                 bf16x8 kh, kl;
-                PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
+                PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh, kl);
 #pragma unroll
                 for (int cbw = 0; cbw < CBW; ++cbw)
                     acc[sb][cbw] = mfma3<kSplit>(kh, kl, vh[cbw][kk], vl[cbw][kk], acc[sb][cbw]);
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 //   2. W [C][S] = Q / (Abar + eps)             Q read from global memory in
 //      the accumulator layout, W written as a plane tile
 //   3. P^T blocks (j-block <= i-block) = K W^T, masked j > i, written as the
-//      plane tile P [C][C] over the dead K tile
+//      plane tile P [C][C]
 //   4. O^T [D][C] = B0^T W^T + V^T P^T         wave w: c-blocks w, w+4, ..
 //   5. B0 += K^T V                             same c-blocks, all s-blocks
 template <typename TIn, int S, int D, int C, int kMinBlocks>
@@ -270,6 +274,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     using G = Geo<TIn, S, D, C>;
     using PS = typename G::PS;
     using PC = typename G::PC;
+    using PD = typename G::PD;
     constexpr bool kSplit = G::kSplit;
     constexpr int NSB = S / 16, NBI = C / 16, NKS = S / 32, NKC = C / 32;
     constexpr int SBW = S / 64, CBW = D / 64;
@@ -278,9 +283,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Ws = lds;
     unsigned char* Ks = Ws + G::kWBytes;
-    unsigned char* Ps = Ks;
-    unsigned char* KTs = Ks + G::kKBytes;
-    unsigned char* VTs = KTs + G::kKTBytes;
+    unsigned char* Ps = Ks + G::kKBytes;
+    unsigned char* Vs = Ps + G::kPBytes;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -331,7 +335,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     // refilled with the next sub-chunk (a deeper prefetch measured slower).
     auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy>& st, QRegs& qr, int r0) {
         __syncthreads();
-        st.store(Ks, KTs, VTs, nullptr);
+        st.store(Ks, Vs, nullptr);
         f32x4 qc[SBW][NBI];
 #pragma unroll
         for (int sbw = 0; sbw < SBW; ++sbw)
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
             const int sb = w + 4 * sbw;
             bf16x8 kh[NKC], kl[NKC];
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) PC::frag(KTs, 16 * sb + lr, kk, g, kh[kk], kl[kk]);
+            for (int kk = 0; kk < NKC; ++kk) PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh[kk], kl[kk]);
             f32x4 last;
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) {
@@ -401,7 +405,6 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
                     if (4 * g + rr > lr) pacc[pb][rr] = 0.f;
             }
         }
-        __syncthreads();
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
             if (w + 4 * pb >= NLB) continue;
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
             const int cb = w + 4 * cbw;
             bf16x8 vh[NKC], vl[NKC];
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) PC::frag(VTs, 16 * cb + lr, kk, g, vh[kk], vl[kk]);
+            for (int kk = 0; kk < NKC; ++kk) PD::frag_tr(Vs, 32 * kk, 16 * cb, g, lr, vh[kk], vl[kk]);
             f32x4 o[NBI];
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) o[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -459,13 +462,17 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
                     or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * int(sizeof(TIn)), o[bi]);
             }
 #pragma unroll
-            for (int sb = 0; sb < NSB; ++sb)
+            for (int sb = 0; sb < NSB; ++sb) {
 #pragma unroll
                 for (int kk = 0; kk < NKC; ++kk) {
                     bf16x8 kh, kl;
-                    PC::frag(KTs, 16 * sb + lr, kk, g, kh, kl);
+                    PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh, kl);
                     b0[sb][cbw] = mfma3<kSplit>(kh, kl, vh[kk], vl[kk], b0[sb][cbw]);
                 }
+                // Where the carried state fills the register file, keep the
+                // scheduler from hoisting every s-block's operand reads.
+                if constexpr (kSplit && S * D >= 128 * 128) __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
 
