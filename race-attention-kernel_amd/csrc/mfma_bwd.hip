@@ -22,9 +22,10 @@
 // Z^T += G^T W.  The carried B0 is held transposed, B0^T[c][s] at
 // c = 16 cb + 4 g + rr, s = 16 w + lr, which is the B operand (column s,
 // contraction over c) of G B0^T; Z^T is held the same way.
-// The token tiles K, V, G are staged through LDS as bf16 planes: "T" planes
-// (rows = features, contraction over tokens) and "R" planes (rows = tokens,
-// contraction over features).
+// The token tiles K, V, G are staged through LDS as bf16 "R" planes (rows =
+// tokens, contraction over features); products that contract over tokens
+// read them transposed (ds_read_b64_tr_b16, Plane::frag_tr).  W and Z1 are
+// stored the same way, with their first index as rows: W^T [s][i], Z1 [s][c].
 #include "mfma_common.h"
 
 namespace race {
@@ -39,12 +40,14 @@ template <typename TIn>
 struct BwdGeo {
     static constexpr bool kSplit = std::is_same<TIn, float>::value;
     static constexpr int E = Elem<TIn>::kPerVec;  // elements per 16-byte load
-    using PT = Plane<kSplit, kBC>;                // rows = features, k = tokens
     using PR = Plane<kSplit, kBS>;                // rows = tokens, k = features
-    using PM = Plane<kSplit, kBC>;                // rows = tokens, k = tokens
-    static constexpr int kTBytes = kBS * PT::kPitch;
+    using PM = Plane<kSplit, kBC>;                // rows = tokens or features, k = tokens
     static constexpr int kRBytes = kBC * PR::kPitch;
     static constexpr int kMBytes = kBC * PM::kPitch;
+    static constexpr int kWTBytes = kBS * PM::kPitch;  // W^T [s][i]
+    static constexpr int kZBytes = kBS * PR::kPitch;   // Z1 [s][c]
+    static constexpr int kDqLds = 3 * kRBytes + kMBytes;
+    static constexpr int kDkvLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
     // Staging: blocks of 4 tokens x E features per tensor.
     static constexpr int kBlk = (kBC / 4) * (kBS / E);   // 128 (fp32) or 64 (bf16)
     static constexpr int kWavesPerTensor = kBlk / 64;    // 2 or 1
@@ -60,19 +63,6 @@ struct StageBlock {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
             x[rr] = buf_load16<kPolicyDefault>(rs, ((r0 + 4 * a + rr) * kBS + b * E) * int(sizeof(TIn)));
-    }
-    // T plane: row = feature, 4 consecutive tokens.
-    template <typename P>
-    __device__ __forceinline__ void store_t(unsigned char* t, int a, int b) const {
-        constexpr int E = BwdGeo<TIn>::E;
-        constexpr bool kSplit = BwdGeo<TIn>::kSplit;
-#pragma unroll
-        for (int c = 0; c < E; ++c) {
-            uint2 hi, lo;
-            split4<kSplit>(Elem<TIn>::get(x[0], c), Elem<TIn>::get(x[1], c), Elem<TIn>::get(x[2], c),
-                           Elem<TIn>::get(x[3], c), hi, lo);
-            P::put4(t, b * E + c, 4 * a, hi, lo);
-        }
     }
     // R plane: row = token, 4 consecutive features.
     template <typename P>
@@ -125,23 +115,20 @@ __device__ __forceinline__ void split8v(const f32x4& a, const f32x4& b, bf16x8& 
 // at every sub-chunk start, and the tile's suffix totals Z = sum W (x) g,
 // Y = sum alpha into its record.
 template <typename TIn>
-__global__ __launch_bounds__(kThreads, 2) void causal_bwd_dq_mfma_kernel(
+__global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
     float* __restrict__ apre, const float* __restrict__ fwd_records,
     float* __restrict__ bwd_records, int64_t T, int tile, int64_t tiles, int64_t rec) {
     using G = BwdGeo<TIn>;
-    using PT = typename G::PT;
     using PR = typename G::PR;
     using PM = typename G::PM;
     constexpr bool kSplit = G::kSplit;
     extern __shared__ __align__(16) unsigned char lds[];
-    unsigned char* KT = lds;
-    unsigned char* VT = KT + G::kTBytes;
-    unsigned char* GT = VT + G::kTBytes;
-    unsigned char* Gs = GT + G::kTBytes;
-    unsigned char* Vs = Gs + G::kRBytes;
-    unsigned char* Ms = Vs;  // M overlays V's R plane once M is computed
+    unsigned char* Ks = lds;
+    unsigned char* Vs = Ks + G::kRBytes;
+    unsigned char* Gs = Vs + G::kRBytes;
+    unsigned char* Ms = Gs + G::kRBytes;
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -195,15 +182,7 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dq_mfma_kernel(
             if (tensor >= 3) continue;
             const int blk = (tid + s * kThreads) % G::kBlk;
             const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
-            if (tensor == 0) {
-                st[s].template store_t<PT>(KT, a, b);
-            } else if (tensor == 1) {
-                st[s].template store_t<PT>(VT, a, b);
-                st[s].template store_r<PR>(Vs, a, b);
-            } else {
-                st[s].template store_t<PT>(GT, a, b);
-                st[s].template store_r<PR>(Gs, a, b);
-            }
+            st[s].template store_r<PR>(tensor == 0 ? Ks : tensor == 1 ? Vs : Gs, a, b);
         }
     };
     // Q at this lane's (i, s) positions.
@@ -235,7 +214,7 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dq_mfma_kernel(
 
         // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
         bf16x8 kh, kl;
-        PT::frag(KT, 16 * w + lr, 0, gq, kh, kl);
+        PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         f32x4 ab[2];
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi) {
@@ -271,7 +250,6 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dq_mfma_kernel(
                     if (4 * gq + rr > lr) mt[rr] = 0.f;
             }
         }
-        __syncthreads();  // V's R plane is dead; M goes over it
         if (w < 3) {
             uint2 hi, lo;
             split4<kSplit>(mt[0], mt[1], mt[2], mt[3], hi, lo);
@@ -323,14 +301,14 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dq_mfma_kernel(
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
             bf16x8 gh, gl;
-            PT::frag(GT, 16 * cb + lr, 0, gq, gh, gl);
+            PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
             zt[cb] = mfma3<kSplit>(gh, gl, wh, wl, zt[cb]);
         }
         // 5: B0^T += V^T K.
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
             bf16x8 vh, vl;
-            PT::frag(VT, 16 * cb + lr, 0, gq, vh, vl);
+            PR::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
             b0t[cb] = mfma3<kSplit>(vh, vl, kh, kl, b0t[cb]);
         }
     }
@@ -356,14 +334,6 @@ __device__ __forceinline__ bf16x8 triu_frag(int off, int g, int lr) {
     return f;
 }
 
-// The bf16 hi (and lo) bit patterns of x.
-template <bool kSplit>
-__device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
-    const uint32_t h = pack2(x, 0.f) & 0xffffu;
-    hi = uint16_t(h);
-    if constexpr (kSplit) lo = uint16_t(pack2(x - __uint_as_float(h << 16), 0.f) & 0xffffu);
-}
-
 // ---------------------------------------------------------------------------
 // B3, backward walk of one (tile, stream) from the suffix state at the tile
 // end: dK (wave w: buckets 16 w ..) and dV (wave w: value columns 16 w ..).
@@ -375,26 +345,23 @@ __device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
 //   4. dV = K Z1 + P^T G                                (Z1 from an LDS plane)
 //   5. Z1^T += G^T W, Y1 += 1^T alpha
 template <typename TIn>
-__global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
+__global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, const float* __restrict__ dq32, const float* __restrict__ apre,
     const float* __restrict__ suffix_records, TIn* __restrict__ dK, TIn* __restrict__ dV,
     int64_t T, int tile, int64_t tiles, int64_t rec) {
     using G = BwdGeo<TIn>;
-    using PT = typename G::PT;
     using PR = typename G::PR;
     using PM = typename G::PM;
     constexpr bool kSplit = G::kSplit;
     extern __shared__ __align__(16) unsigned char lds[];
-    unsigned char* KT = lds;
-    unsigned char* GT = KT + G::kTBytes;
-    unsigned char* Ks = GT + G::kTBytes;
+    unsigned char* Ks = lds;
     unsigned char* Vs = Ks + G::kRBytes;
     unsigned char* Gs = Vs + G::kRBytes;
-    unsigned char* Ws = Gs + G::kRBytes;
-    unsigned char* MT = Ws + G::kRBytes;     // rows j, contraction over i
+    unsigned char* WT = Gs + G::kRBytes;     // W^T: rows s, elements i
+    unsigned char* MT = WT + G::kWTBytes;    // rows j, contraction over i
     unsigned char* PTp = MT + G::kMBytes;    // rows j, contraction over i
-    unsigned char* Zp = PTp + G::kMBytes;    // Z1^T: rows c, contraction over s
+    unsigned char* Zr = PTp + G::kMBytes;    // Z1: rows s, elements c
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -446,15 +413,7 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
             if (tensor >= 3) continue;
             const int blk = (tid + s * kThreads) % G::kBlk;
             const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
-            if (tensor == 0) {
-                st[s].template store_t<PT>(KT, a, b);
-                st[s].template store_r<PR>(Ks, a, b);
-            } else if (tensor == 1) {
-                st[s].template store_r<PR>(Vs, a, b);
-            } else {
-                st[s].template store_t<PT>(GT, a, b);
-                st[s].template store_r<PR>(Gs, a, b);
-            }
+            st[s].template store_r<PR>(tensor == 0 ? Ks : tensor == 1 ? Vs : Gs, a, b);
         }
     };
     float qreg[2][4], dreg[2][4];
@@ -489,20 +448,19 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
             stage_load(r0 - kBC);
             load_qd(r0 - kBC);
         }
-        // Z1 (the suffix state after this sub-chunk) as a plane for dV.
+        // Z1 (the suffix state after this sub-chunk) as a plane for dV: row s,
+        // four consecutive c per lane.
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                uint16_t hi, lo;
-                split1<kSplit>(zt[cb][rr], hi, lo);
-                PR::put1(Zp, 16 * cb + 4 * gq + rr, 16 * w + lr, hi, lo);
-            }
+        for (int cb = 0; cb < 4; ++cb) {
+            uint2 hi, lo;
+            split4<kSplit>(zt[cb][0], zt[cb][1], zt[cb][2], zt[cb][3], hi, lo);
+            PR::put4(Zr, 16 * w + lr, 16 * cb + 4 * gq, hi, lo);
+        }
         __syncthreads();
 
-        // 1: Abar, r, W, alpha; W into its R plane.
+        // 1: Abar, r, W, alpha; W^T into its plane (row s, four consecutive i).
         bf16x8 kh, kl;
-        PT::frag(KT, 16 * w + lr, 0, gq, kh, kl);
+        PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         const float a0 = ap[(r0 / kBC) * kBS + 16 * w + lr];
         f32x4 wv[2], al[2];
 #pragma unroll
@@ -515,10 +473,10 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
             for (int rr = 0; rr < 4; ++rr) {
                 wv[bi][rr] = qc[bi][rr] * __builtin_amdgcn_rcpf(acc[rr] + kEps);
                 al[bi][rr] = -wv[bi][rr] * dc[bi][rr];
-                uint16_t hi, lo;
-                split1<kSplit>(wv[bi][rr], hi, lo);
-                PR::put1(Ws, 16 * bi + 4 * gq + rr, 16 * w + lr, hi, lo);
             }
+            uint2 hi, lo;
+            split4<kSplit>(wv[bi][0], wv[bi][1], wv[bi][2], wv[bi][3], hi, lo);
+            PM::put4(WT, 16 * w + lr, 16 * bi + 4 * gq, hi, lo);
         }
         __syncthreads();
 
@@ -550,7 +508,7 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     bf16x8 ah, alo, bh, bl;
-                    PR::frag(Ws, 16 * bi + lr, kk, gq, ah, alo);
+                    PM::frag_tr(WT, 32 * kk, 16 * bi, gq, lr, ah, alo);
                     PR::frag(Ks, 16 * bj + lr, kk, gq, bh, bl);
                     pacc = mfma3<kSplit>(ah, alo, bh, bl, pacc);
                 }
@@ -614,7 +572,7 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 bf16x8 zh, zl;
-                PR::frag(Zp, 16 * w + lr, kk, gq, zh, zl);
+                PR::frag_tr(Zr, 32 * kk, 16 * w, gq, lr, zh, zl);
 #pragma unroll
                 for (int bj = 0; bj < 2; ++bj) {
                     bf16x8 kh2, kl2;
@@ -623,7 +581,7 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
                 }
             }
             bf16x8 gh, gl;
-            PT::frag(GT, 16 * w + lr, 0, gq, gh, gl);
+            PR::frag_tr(Gs, 0, 16 * w, gq, lr, gh, gl);
 #pragma unroll
             for (int bj = 0; bj < 2; ++bj) {
                 bf16x8 ph, pl;
@@ -645,7 +603,7 @@ __global__ __launch_bounds__(kThreads, 1) void causal_bwd_dkv_mfma_kernel(
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
             bf16x8 gh, gl;
-            PT::frag(GT, 16 * cb + lr, 0, gq, gh, gl);
+            PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
             zt[cb] = mfma3<kSplit>(gh, gl, wh, wl, zt[cb]);
         }
         float ys = 0.f;
@@ -670,14 +628,14 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     if (p.dtype == RACE_BF16) {
         using G = BwdGeo<bf16_t>;
-        const size_t lds = 3 * G::kTBytes + 2 * G::kRBytes;
+        const size_t lds = G::kDqLds;
         causal_bwd_dq_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
             static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
             static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ),
             dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec);
     } else {
         using G = BwdGeo<float>;
-        const size_t lds = 3 * G::kTBytes + 2 * G::kRBytes;
+        const size_t lds = G::kDqLds;
         causal_bwd_dq_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
             static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
             static_cast<const float*>(g), static_cast<float*>(dQ), dq32, apre, fwd_records,
@@ -694,7 +652,7 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     if (p.dtype == RACE_BF16) {
         using G = BwdGeo<bf16_t>;
-        const size_t lds = 2 * G::kTBytes + 4 * G::kRBytes + 2 * G::kMBytes + kBS * G::PR::kPitch;
+        const size_t lds = G::kDkvLds;
         causal_bwd_dkv_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
             static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
             static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), dq32, apre,
@@ -702,7 +660,7 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
             p.rec);
     } else {
         using G = BwdGeo<float>;
-        const size_t lds = 2 * G::kTBytes + 4 * G::kRBytes + 2 * G::kMBytes + kBS * G::PR::kPitch;
+        const size_t lds = G::kDkvLds;
         causal_bwd_dkv_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
             static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
             static_cast<const float*>(g), dq32, apre, suffix_records, static_cast<float*>(dK),
