@@ -255,49 +255,65 @@ __device__ __forceinline__ void write_sigmas(float* U, const f32x4 (&acc)[G::NPB
         }
 }
 
-// Phi of the sub-chunk's C tokens from U into the token-row plane Ph; tokens
-// >= valid get 0.  Item (t, l), one per thread: the P sigmoid pairs of
-// token t, table l are decoded once; the corners go out in quads, the planes
-// above the last two selecting by the bits of the quad index (plane 0 the
-// most significant bit of r) and the last two giving the quad's four corners.
-template <typename PS, bool kSplit>
-__device__ __forceinline__ void build_rows(const float* U, int kUP, unsigned char* Ph, int L, int P,
-                                           int valid) {
-    const int R = 1 << P;
-    const int e = threadIdx.x;
-    if (e >= kA1Chunk * L) return;
-    const int t = e % kA1Chunk, l = e / kA1Chunk;
-    const bool live = t < valid;
-    const float* ur = U + t * kUP + l * P;
-    if (P >= 2) {
-        float2 hp[3];
+// Phi of the sub-chunk's C tokens from U into a token-row plane; tokens >=
+// valid get 0.  Item (t, l) = (tid % 64, tid / 64), one per thread: the P
+// sigmoid pairs of token t, table l are decoded once; the corners go out in
+// quads, the planes above the last two selecting by the bits of the quad
+// index (plane 0 the most significant bit of r) and the last two giving the
+// quad's four corners.  The item's U offset and its quads' LDS offsets are
+// fixed for the whole tile and computed once.
+template <typename PS, bool kSplit, int kUP>
+struct RowBuilder {
+    int t, uoff, P, R;
+    bool active;
+    int poff[8];  // byte offsets of corners 4 m .. 4 m + 3 of row t
+
+    __device__ __forceinline__ void init(int L, int P_) {
+        const int e = threadIdx.x, l = e / kA1Chunk;
+        t = e % kA1Chunk;
+        P = P_;
+        R = 1 << P_;
+        active = e < kA1Chunk * L;
+        uoff = t * kUP + l * P_;
 #pragma unroll
-        for (int p = 0; p < 3; ++p) hp[p] = p < P - 2 ? sigma_pair(ur[p]) : make_float2(1.f, 1.f);
-        const float2 s1 = sigma_pair(ur[P - 2]), s2 = sigma_pair(ur[P - 1]);
-        const float q0 = s1.y * s2.y, q1 = s1.y * s2.x, q2 = s1.x * s2.y, q3 = s1.x * s2.x;
+        for (int m = 0; m < 8; ++m) poff[m] = 4 * m < R ? PS::off4(t, (l << P_) + 4 * m) : 0;
+    }
+
+    __device__ __forceinline__ void build(const float* U, unsigned char* Ph, int valid) const {
+        if (!active) return;
+        const float* ur = U + uoff;
+        const float live = t < valid ? 1.f : 0.f;
+        if (P >= 2) {
+            float2 hp[3];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            if (4 * m >= R) continue;
-            float base = 1.f;
+            for (int p = 0; p < 3; ++p) hp[p] = p < P - 2 ? sigma_pair(ur[p]) : make_float2(1.f, 1.f);
+            const float2 s1 = sigma_pair(ur[P - 2]), s2 = sigma_pair(ur[P - 1]);
+            const float q0 = s1.y * s2.y, q1 = s1.y * s2.x, q2 = s1.x * s2.y, q3 = s1.x * s2.x;
 #pragma unroll
-            for (int p = 0; p < 3; ++p)
-                if (p < P - 2) base *= ((m >> (P - 3 - p)) & 1) ? hp[p].x : hp[p].y;
-            uint2 hi, lo;
-            split4<kSplit>(live ? base * q0 : 0.f, live ? base * q1 : 0.f, live ? base * q2 : 0.f,
-                           live ? base * q3 : 0.f, hi, lo);
-            PS::put4(Ph, t, l * R + 4 * m, hi, lo);
-        }
-    } else {
-        const float2 sp = sigma_pair(ur[0]);
-        const float x[2] = {live ? sp.y : 0.f, live ? sp.x : 0.f};
+            for (int m = 0; m < 8; ++m) {
+                if (4 * m >= R) continue;
+                float base = live;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            uint16_t hi, lo;
-            split1<kSplit>(x[r], hi, lo);
-            PS::put1(Ph, t, 2 * l + r, hi, lo);
+                for (int p = 0; p < 3; ++p)
+                    if (p < P - 2) base *= ((m >> (P - 3 - p)) & 1) ? hp[p].x : hp[p].y;
+                uint2 hi, lo;
+                split4<kSplit>(base * q0, base * q1, base * q2, base * q3, hi, lo);
+                *reinterpret_cast<uint2*>(Ph + poff[m]) = hi;
+                if constexpr (kSplit) *reinterpret_cast<uint2*>(Ph + poff[m] + PS::kLoOff) = lo;
+            }
+        } else {
+            const float2 sp = sigma_pair(ur[0]);
+            const float x[2] = {live * sp.y, live * sp.x};
+            const int l = threadIdx.x / kA1Chunk;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                uint16_t hi, lo;
+                split1<kSplit>(x[r], hi, lo);
+                PS::put1(Ph, t, 2 * l + r, hi, lo);
+            }
         }
     }
-}
+};
 
 // Zero buckets S .. SP - 1 of every row of a token-row Phi plane.
 template <typename PL, int SP>
@@ -351,6 +367,9 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
     unsigned char* const Xs[2] = {Xk, Vs};
 
+    RowBuilder<PS, kPhiSplit, G::kUPitch> rb;
+    rb.init(L, P);
+
     A1Stage<D, 2> st;
     st.load(xr, 0);
     for (int r0 = 0; r0 < rows; r0 += kA1Chunk) {
@@ -362,7 +381,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kSumsBlock
         project<G, kPhiSplit>(Xk, Ws, w, g, lr, uk);
         write_sigmas<G>(U, uk, beta2, w, g, lr);
         __syncthreads();  // the k rows are dead: Phi_K takes their space
-        build_rows<PS, kPhiSplit>(U, G::kUPitch, PhK, L, P, rows - r0);
+        rb.build(U, PhK, rows - r0);
         if (SP > S) zero_pad_rows<PS, SP>(PhK, S);
         __syncthreads();
         // Phi_K^T and V fragments straight from the token-row planes.
@@ -489,6 +508,22 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
     unsigned char* const Xs[3] = {Xq, Xk, Vs};
 
+    RowBuilder<PS, kPhiSplit, G::kUPitch> rb;
+    rb.init(L, P);
+    // The lower-triangular G blocks of this wave, round robin: block index
+    // w + 4 pb is (bi, bj) with bj <= bi.
+    int pbi[PBW], pbj[PBW];
+#pragma unroll
+    for (int pb = 0; pb < PBW; ++pb) {
+        int bi = 0, rem = w + 4 * pb;
+        while (rem > bi) {
+            rem -= bi + 1;
+            ++bi;
+        }
+        pbi[pb] = bi;
+        pbj[pb] = rem;
+    }
+
     A1Stage<D, 3> st;
     st.load(xr, 0);
     for (int r0 = 0; r0 < rows; r0 += C) {
@@ -502,8 +537,8 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
         write_sigmas<G>(Uq, uq, beta2, w, g, lr);
         write_sigmas<G>(Uk, uk, beta2, w, g, lr);
         __syncthreads();  // (2) the x planes are dead: Phi_Q and Phi_K take their space
-        build_rows<PS, kPhiSplit>(Uq, G::kUPitch, PhQ, L, P, C);
-        build_rows<PS, kPhiSplit>(Uk, G::kUPitch, PhK, L, P, rows - r0);
+        rb.build(Uq, PhQ, C);
+        rb.build(Uk, PhK, rows - r0);
         if (SP > S) {
             zero_pad_rows<PS, SP>(PhQ, S);
             zero_pad_rows<PS, SP>(PhK, S);
@@ -553,19 +588,11 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
         // G^T blocks of the lower triangle, round robin over the waves:
         // lane (g, lr) of block (bi, bj) holds G[16 bi + lr][16 bj + 4 g + r].
         f32x4 pacc[PBW];
-        int pbi[PBW], pbj[PBW];
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
-            const int idx = w + 4 * pb;
-            int bi = 0, rem = idx;
-            while (rem > bi) {
-                rem -= bi + 1;
-                ++bi;
-            }
-            pbi[pb] = bi;
-            pbj[pb] = rem;
+            const int bi = pbi[pb], rem = pbj[pb];
             pacc[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (idx >= NLB) continue;
+            if (w + 4 * pb >= NLB) continue;
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
                 bf16x8 ah, al, bh, bl_;
@@ -594,7 +621,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
         for (int bi = 0; bi < NBI; ++bi) {
             const int i = 16 * bi + lr;
             const float den = ((denp[i] + denp[C + i]) + denp[2 * C + i]) + denp[3 * C + i];
-            rden[bi] = den == 0.f ? 0.f : 1.0f / den;
+            rden[bi] = den == 0.f ? 0.f : __builtin_amdgcn_rcpf(den);  // 1 ulp; the output is bf16
         }
 
         // Output and state update for this wave's c-blocks.
