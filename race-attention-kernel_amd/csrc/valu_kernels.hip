@@ -104,49 +104,53 @@ __global__ __launch_bounds__(kThreads) void tile_outer_sums_kernel(
 // ---------------------------------------------------------------------------
 // Exclusive scan of the tile records over tiles, element-parallel like the
 // reference's scan (docs/causal_v2_design.md:242-261) but two-level so that a
-// long run of tiles is not one serial chain of loads: a workgroup owns 32
-// record elements of one stream and splits the tiles into kScanGroups
-// contiguous groups.  Thread (element, group) sums its group; the group sums
-// meet in LDS; each thread then walks its group again writing
+// long run of tiles is not one serial chain of loads: a workgroup owns
+// kThreads / groups record elements of one stream and splits the tiles into
+// `groups` contiguous groups (8 for long runs; 1 for runs of at most 32 tiles,
+// where each thread walks all of them and a workgroup covers 256 contiguous
+// elements).  Thread (element, group) sums its group; the group sums meet in
+// LDS; each thread then walks its group again writing
 //     prefix(t) = sum of the earlier groups (in group order)
 //               + the earlier tiles of its group (in tile order).
 // Every sum has a fixed order, so the result is bitwise reproducible.  With
 // `reverse` the tiles are scanned from the last to the first (the suffix
 // sums of the causal backward): record t receives the sum over tiles > t.
-constexpr int kScanGroups = 8;
-constexpr int kScanElems = kThreads / kScanGroups;  // 32
+constexpr int kScanGroupsMax = 8;
 
 __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__ records,
                                                              float* __restrict__ state,
                                                              int64_t tiles, int64_t rec, int used,
-                                                             int reverse) {
-    __shared__ float gsum[kScanGroups][kScanElems];
-    const int el = threadIdx.x % kScanElems, gi = threadIdx.x / kScanElems;
-    const int e = blockIdx.x * kScanElems + el;
+                                                             int reverse, int groups) {
+    __shared__ float gsum[kThreads];
+    const int elems = kThreads / groups;
+    const int el = threadIdx.x % elems, gi = threadIdx.x / elems;
+    const int e = blockIdx.x * elems + el;
     const int64_t n = blockIdx.y;
-    const int64_t per = (tiles + kScanGroups - 1) / kScanGroups;
+    const int64_t per = (tiles + groups - 1) / groups;
     const int64_t t_begin = gi * per;
     const int64_t t_end = min(tiles, t_begin + per);
     // Scan position t is record r[t * step].
     const int64_t step = reverse ? -rec : rec;
     float* r = records + n * tiles * rec + (reverse ? (tiles - 1) * rec : 0) + e;
-    float sum = 0.f;
-    if (e < used) {
-        int64_t t = t_begin;
-        for (; t + 16 <= t_end; t += 16) {
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * step];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) sum += v[u];
-        }
-        for (; t < t_end; ++t) sum += r[t * step];
-    }
-    gsum[gi][el] = sum;
-    __syncthreads();
-    if (e >= used) return;
     float run = 0.f;
-    for (int j = 0; j < gi; ++j) run += gsum[j][el];
+    if (groups > 1) {
+        float sum = 0.f;
+        if (e < used) {
+            int64_t t = t_begin;
+            for (; t + 16 <= t_end; t += 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v[u] = r[(t + u) * step];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) sum += v[u];
+            }
+            for (; t < t_end; ++t) sum += r[t * step];
+        }
+        gsum[gi * elems + el] = sum;
+        __syncthreads();
+        for (int j = 0; j < gi; ++j) run += gsum[j * elems + el];
+    }
+    if (e >= used) return;
     int64_t t = t_begin;
     for (; t + 16 <= t_end; t += 16) {
         float v[16];
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__
         r[t * step] = run;
         run += v;
     }
-    if (state && gi == kScanGroups - 1) state[n * used + e] = run;
+    if (state && gi == groups - 1) state[n * used + e] = run;
 }
 
 __device__ __forceinline__ float sum_over_tiles(const float* __restrict__ r, int64_t tiles,
@@ -409,9 +413,11 @@ hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, 
 hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream,
                             bool reverse) {
     const int used = p.S * p.d + p.S;
-    const dim3 grid(unsigned((used + kScanElems - 1) / kScanElems), unsigned(p.N));
+    const int groups = p.tiles <= 32 ? 1 : kScanGroupsMax;
+    const int elems = kThreads / groups;
+    const dim3 grid(unsigned((used + elems - 1) / elems), unsigned(p.N));
     tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.tiles, p.rec, used,
-                                                    reverse ? 1 : 0);
+                                                    reverse ? 1 : 0, groups);
     return hipGetLastError();
 }
 
