@@ -517,8 +517,11 @@ hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void*
 template <typename TIn>
 hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out, float* records,
                          float* state, const Problem& p, hipStream_t stream, Marks* marks) {
+    // S = d = 64: 32-token sub-chunks halve every LDS plane (32 KB per
+    // workgroup) so four workgroups share a CU and keep four times the loads
+    // in flight; the output pass there is bound by bytes in flight, not math.
     if (p.S == 64 && p.d == 64)
-        return launch_mfma_family<TIn, 64, 64, 64, 2>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, 64, 64, 32, 4>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 64 && p.d == 128)
         return launch_mfma_family<TIn, 64, 128, 64, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 128 && p.d == 64)
@@ -537,8 +540,9 @@ hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out,
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel) {
     if (kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(S, d, dtype))
         return direct_output_tiles_per_cu();
-    // Two resident workgroups per CU, two rounds; S = 256 runs one workgroup
-    // per CU and prefers longer tiles (fewer 132 KB records to scan).
+    // S = d = 64 keeps four workgroups resident per CU (one round); the others
+    // run one or two per CU over two or more rounds; S = 256 prefers longer
+    // tiles (fewer 132 KB records to scan).
     return S >= 256 ? 2 : 4;
 }
 
