@@ -73,7 +73,8 @@ typedef enum race_kernel {
     RACE_KERNEL_AUTO = 0,
     RACE_KERNEL_VALU = 1,
     RACE_KERNEL_MFMA = 2,
-    RACE_KERNEL_MFMA_WG = 3
+    RACE_KERNEL_MFMA_WG = 3,
+    RACE_KERNEL_DECODE = 4 /* race_fwd_carry only: the one-launch token-serial kernel */
 } race_kernel;
 
 /* Shape of one call.  Mirrors CausalShape
@@ -145,6 +146,42 @@ race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void
                               const race_options* opts, void* workspace, size_t workspace_bytes,
                               hipStream_t stream, hipEvent_t* events, int32_t max_events,
                               int32_t* n_events);
+
+/* Calls of race_fwd_carry with at most this many tokens (and an automatic
+ * kernel and tile length) run the decode kernel. */
+#define RACE_DECODE_TOKENS 16
+
+/* Workspace of race_fwd_carry in bytes (0 when the call runs the decode
+ * kernel; race_fwd's causal workspace otherwise). */
+race_status race_fwd_carry_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                           size_t* bytes);
+
+/* The causal race_fused_fwd continued from a carried state: the carry of the
+ * reference's chunked forward (src/race_chunked.py:54-63, A_state and B_state
+ * taken into the next chunk), fed by the hand-off state
+ * (src/causal_v2/kernels/race_causal_fwd.h:20-21; race_fwd's `state`).  For
+ * the T tokens of this call,
+ *     out[t] = sum_s probsQ[t,s] * (B0 + B_t)[s,:] / (A0[s] + A_t[s] + 1e-6)
+ * with (B0, A0) = init_state ([N][S*d + S] fp32, B then A, 16-byte aligned)
+ * and A_t, B_t the inclusive sums over this call's tokens.  state (nullable)
+ * receives init_state plus the sums over all T tokens and may equal
+ * init_state (an in-place step).  Splitting a sequence anywhere and carrying
+ * the state gives the unsplit result up to fp32 rounding.  Short calls
+ * (decode: T <= RACE_DECODE_TOKENS) run one launch with one workgroup per
+ * stream and no workspace; longer ones run race_fwd's causal kernels with the
+ * tile scan started from init_state.  The reference has no kernel for this. */
+race_status race_fwd_carry(const void* probsQ, const void* probsK, const void* V, void* out,
+                           const float* init_state, float* state, const race_shape* shape,
+                           const race_options* opts, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+/* race_fwd_carry with the events of race_fwd_profiled (a profiling aid, no
+ * counterpart in the reference). */
+race_status race_fwd_carry_profiled(const void* probsQ, const void* probsK, const void* V,
+                                    void* out, const float* init_state, float* state,
+                                    const race_shape* shape, const race_options* opts,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                    hipEvent_t* events, int32_t max_events, int32_t* n_events);
 
 /* Workspace of race_noncausal_bwd in bytes. */
 race_status race_noncausal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,

@@ -82,7 +82,7 @@ def _load():
         i64 = ctypes.c_int64
         d = ctypes.c_double
         i = ctypes.c_int
-        lib.race_oracle_causal_recurrence.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i]
+        lib.race_oracle_causal_recurrence.argtypes = [f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i]
         lib.race_oracle_causal_chunked.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i64, i]
         lib.race_oracle_causal_tiled.argtypes = [f32p, f32p, f32p, f64p, f64p, f64p, i64, i64, i64, i64, d, i64, i64, i]
         lib.race_oracle_noncausal_fwd.argtypes = [f32p, f32p, f32p, f64p, f64p, i64, i64, i64, i64, d, i]
@@ -114,15 +114,23 @@ def _shape(q, v):
     return N, T, S, d
 
 
-def causal_recurrence(q, k, v, eps: float = EPS, nthreads: int = 0, want_state: bool = False):
-    """Per-token scan, fp64.  Returns out [N,T,d] (and the final state [N, S*d+S])."""
+def causal_recurrence(q, k, v, eps: float = EPS, nthreads: int = 0, want_state: bool = False,
+                      init_state=None):
+    """Per-token scan, fp64.  Returns out [N,T,d] (and the final state [N, S*d+S]).
+    init_state [N, S*d+S] (B then A): the state carried in from earlier tokens
+    (src/race_chunked.py:54-63); zero when None."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     N, T, S, d = _shape(q, v)
     out = np.empty((N, T, d), np.float64)
     st = np.empty((N, S * d + S), np.float64) if want_state else None
+    init = None
+    if init_state is not None:
+        init = np.ascontiguousarray(np.asarray(init_state, dtype=np.float64))
+        assert init.shape == (N, S * d + S), init.shape
     _load().race_oracle_causal_recurrence(
         _ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float), _ptr(out, ctypes.c_double),
-        _ptr(st, ctypes.c_double) if st is not None else None, N, T, S, d, eps, nthreads)
+        _ptr(st, ctypes.c_double) if st is not None else None,
+        _ptr(init, ctypes.c_double) if init is not None else None, N, T, S, d, eps, nthreads)
     return (out, st) if want_state else out
 
 

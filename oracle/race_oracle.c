@@ -30,7 +30,9 @@
  *
  * Four independent formulations are provided so that each pins the others:
  *   race_oracle_causal_recurrence  per-token scan (src/race_fused_fwd.cu:131-146,
- *                                   mirrored in src/test_kernel_math.py:32-39)
+ *                                   mirrored in src/test_kernel_math.py:32-39),
+ *                                   optionally continued from a carried state
+ *                                   (the carry of src/race_chunked.py:54-63)
  *   race_oracle_causal_chunked     carried state + chunk identity
  *                                   (src/race_chunked.py:41-63,
  *                                   docs/causal_v2_design.md:70-77)
@@ -62,16 +64,24 @@ static void set_threads(int nthreads) {
 }
 
 /* Per-token recurrence.  For every token: A += k_t, B += k_t (x) v_t, then
- * out_t = sum_s (q_t[s] / (A[s] + eps)) * B[s][:].  final_state (nullable)
- * receives the state after the last token. */
+ * out_t = sum_s (q_t[s] / (A[s] + eps)) * B[s][:].  init_state (nullable,
+ * [N][S*d + S]) is the state before the first token (zero when null), as
+ * chunked_forward carries A_state, B_state into its next chunk
+ * (src/race_chunked.py:54-63); final_state (nullable) receives the state
+ * after the last token. */
 void race_oracle_causal_recurrence(const float* q, const float* k, const float* v, double* out,
-                                   double* final_state, i64 N, i64 T, i64 S, i64 d, double eps,
-                                   int nthreads) {
+                                   double* final_state, const double* init_state, i64 N, i64 T,
+                                   i64 S, i64 d, double eps, int nthreads) {
     set_threads(nthreads);
 #pragma omp parallel for schedule(dynamic, 1)
     for (i64 n = 0; n < N; ++n) {
         double* A = (double*)calloc((size_t)S, sizeof(double));
         double* B = (double*)calloc((size_t)(S * d), sizeof(double));
+        if (init_state) {
+            const double* st = init_state + n * (S * d + S);
+            memcpy(B, st, (size_t)(S * d) * sizeof(double));
+            memcpy(A, st + S * d, (size_t)S * sizeof(double));
+        }
         double* w = (double*)malloc((size_t)S * sizeof(double));
         double* o = (double*)malloc((size_t)d * sizeof(double));
         for (i64 t = 0; t < T; ++t) {

@@ -18,6 +18,8 @@ RACE_KERNEL_AUTO = 0
 RACE_KERNEL_VALU = 1
 RACE_KERNEL_MFMA = 2
 RACE_KERNEL_MFMA_WG = 3
+RACE_KERNEL_DECODE = 4
+RACE_DECODE_TOKENS = 16
 RACE_SUB_CHUNK_TOKENS = 64
 RACE_ALG1_FP32 = 0
 RACE_ALG1_BF16 = 1
@@ -32,6 +34,9 @@ EXPORTED_SYMBOLS = (
     "race_fwd_workspace_bytes",
     "race_fwd",
     "race_fwd_profiled",
+    "race_fwd_carry_workspace_bytes",
+    "race_fwd_carry",
+    "race_fwd_carry_profiled",
     "race_noncausal_bwd_workspace_bytes",
     "race_noncausal_bwd",
     "race_causal_bwd_workspace_bytes",
@@ -93,6 +98,10 @@ def lib() -> ctypes.CDLL:
         L.race_fwd.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp]
         L.race_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp,
                                         ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
+        L.race_fwd_carry_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
+        L.race_fwd_carry.argtypes = [vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
+        L.race_fwd_carry_profiled.argtypes = [vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp, vp, i32,
+                                              ctypes.POINTER(i32)]
         L.race_noncausal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_noncausal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_causal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
@@ -170,6 +179,33 @@ def fwd_profiled(q: int, k: int, v: int, out: int, state: int | None, sh: RaceSh
     st = lib().race_fwd_profiled(q, k, v, out, state, ctypes.byref(sh), int(causal),
                                  ctypes.byref(opts) if opts is not None else None, workspace,
                                  workspace_bytes, stream, events, len(events), ctypes.byref(n))
+    return st, n.value
+
+
+def fwd_carry_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):
+    b = ctypes.c_size_t(0)
+    st = lib().race_fwd_carry_workspace_bytes(ctypes.byref(sh),
+                                              ctypes.byref(opts) if opts is not None else None,
+                                              ctypes.byref(b))
+    return st, b.value
+
+
+def fwd_carry(q: int, k: int, v: int, out: int, init_state: int, state: int | None, sh: RaceShape,
+              opts: RaceOptions | None, workspace: int | None, workspace_bytes: int, stream: int) -> int:
+    """race_fwd_carry on raw device addresses; returns the status."""
+    return lib().race_fwd_carry(q, k, v, out, init_state, state, ctypes.byref(sh),
+                                ctypes.byref(opts) if opts is not None else None,
+                                workspace, workspace_bytes, stream)
+
+
+def fwd_carry_profiled(q: int, k: int, v: int, out: int, init_state: int, state: int | None,
+                       sh: RaceShape, opts: RaceOptions | None, workspace: int | None,
+                       workspace_bytes: int, stream: int, events) -> tuple[int, int]:
+    """race_fwd_carry_profiled; returns (status, n_events)."""
+    n = ctypes.c_int32(0)
+    st = lib().race_fwd_carry_profiled(q, k, v, out, init_state, state, ctypes.byref(sh),
+                                       ctypes.byref(opts) if opts is not None else None, workspace,
+                                       workspace_bytes, stream, events, len(events), ctypes.byref(n))
     return st, n.value
 
 

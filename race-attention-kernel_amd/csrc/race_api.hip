@@ -174,6 +174,18 @@ hipError_t zero_fill(float* p, int64_t n, hipStream_t stream) {
     return hipGetLastError();
 }
 
+__global__ void copy_floats_kernel(const float* src, float* dst, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+// dst = src elementwise (a no-op when dst is null or is src).
+hipError_t copy_floats(const float* src, float* dst, int64_t n, hipStream_t stream) {
+    if (n <= 0 || !dst || dst == src) return hipSuccess;
+    copy_floats_kernel<<<unsigned((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(src, dst, n);
+    return hipGetLastError();
+}
+
 hipError_t max_lds(int* bytes) {
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
@@ -262,16 +274,22 @@ namespace race {
 namespace {
 
 race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void* out, float* state,
-                     const race_shape* shape, int32_t causal, const race_options* opts,
-                     void* workspace, size_t workspace_bytes, hipStream_t stream, Marks* marks) {
+                     const float* init, const race_shape* shape, int32_t causal,
+                     const race_options* opts, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream, Marks* marks) {
     Problem p;
     bool mfma = false;
     race_status st = make_problem(shape, causal, opts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
     if (state && !aligned16(state)) return RACE_ERROR_INVALID_VALUE;
+    if (init && (!causal || !aligned16(init))) return RACE_ERROR_INVALID_VALUE;
+    p.init = init;
     if (p.N == 0 || p.T == 0) {
         RACE_TRY(marks->mark(stream));
-        RACE_TRY(zero_fill(state, p.N * state_floats(p.S, p.d), stream));
+        if (init)
+            RACE_TRY(copy_floats(init, state, p.N * state_floats(p.S, p.d), stream));
+        else
+            RACE_TRY(zero_fill(state, p.N * state_floats(p.S, p.d), stream));
         return marks->mark(stream);
     }
     if (!probsQ || !probsK || !V || !out) return RACE_ERROR_INVALID_VALUE;
@@ -310,6 +328,56 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
     // out = q . E: M[a][c] = E[a*d + c].
     RACE_TRY(token_map(probsQ, out, E, int64_t(p.S) * p.d, p.d, 1, nullptr, 0, p, p.S, p.d,
                        stream));
+    return marks->mark(stream);
+}
+
+// race_fwd_carry runs the decode kernel when asked to, and by default for
+// calls of at most RACE_DECODE_TOKENS tokens that leave the tile length
+// automatic; otherwise the causal tile path with the scan seeded from init.
+bool carry_runs_decode(const race_shape* sh, const race_options* o) {
+    const int k = kernel_choice(o);
+    if (k == RACE_KERNEL_DECODE) return true;
+    return k == RACE_KERNEL_AUTO && (!o || o->tile_tokens == 0) && sh->seq_len <= RACE_DECODE_TOKENS;
+}
+
+// The decode kernel has no tiles; a tile length, if given, must still be a
+// valid one.
+bool decode_options_ok(const race_options* o) {
+    return !o || (o->tile_tokens >= 0 && o->tile_tokens % RACE_SUB_CHUNK_TOKENS == 0);
+}
+
+race_status carry_impl(const void* probsQ, const void* probsK, const void* V, void* out,
+                       const float* init, float* state, const race_shape* shape,
+                       const race_options* opts, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream, Marks* marks) {
+    if (!shape || !init || !aligned16(init)) return RACE_ERROR_INVALID_VALUE;
+    if (state && !aligned16(state)) return RACE_ERROR_INVALID_VALUE;
+    if (!carry_runs_decode(shape, opts))
+        return fwd_impl(probsQ, probsK, V, out, state, init, shape, 1, opts, workspace,
+                        workspace_bytes, stream, marks);
+    if (!shape_ok(shape) || !decode_options_ok(opts)) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    p.N = shape->num_streams;
+    p.T = shape->seq_len;
+    p.S = sub(shape);
+    p.d = shape->head_dim;
+    p.dtype = shape->dtype;
+    p.kernel = RACE_KERNEL_DECODE;
+    p.tile = 0;
+    p.tiles = 0;
+    p.rec = record_floats(p.S, p.d);
+    p.init = init;
+    if (p.N == 0 || (p.T == 0 && (!state || state == init))) {
+        RACE_TRY(marks->mark(stream));
+        return marks->mark(stream);
+    }
+    if (p.T > 0) {
+        if (!probsQ || !probsK || !V || !out) return RACE_ERROR_INVALID_VALUE;
+        if (!aligned16(probsQ) || !aligned16(probsK) || !aligned16(V) || !aligned16(out))
+            return RACE_ERROR_INVALID_VALUE;
+    }
+    RACE_TRY(marks->mark(stream));
+    RACE_TRY(launch_decode(probsQ, probsK, V, out, init, state, p, stream));
     return marks->mark(stream);
 }
 
@@ -378,8 +446,8 @@ race_status race_fwd(const void* probsQ, const void* probsK, const void* V, void
                      const race_options* opts, void* workspace, size_t workspace_bytes,
                      hipStream_t stream) {
     Marks none;
-    return fwd_impl(probsQ, probsK, V, out, state, shape, causal, opts, workspace, workspace_bytes,
-                    stream, &none);
+    return fwd_impl(probsQ, probsK, V, out, state, nullptr, shape, causal, opts, workspace,
+                    workspace_bytes, stream, &none);
 }
 
 race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void* V, void* out,
@@ -391,8 +459,43 @@ race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void
     Marks marks;
     marks.events = events;
     marks.max = max_events;
-    const race_status st = fwd_impl(probsQ, probsK, V, out, state, shape, causal, opts, workspace,
-                                    workspace_bytes, stream, &marks);
+    const race_status st = fwd_impl(probsQ, probsK, V, out, state, nullptr, shape, causal, opts,
+                                    workspace, workspace_bytes, stream, &marks);
+    *n_events = marks.n;
+    return st;
+}
+
+race_status race_fwd_carry_workspace_bytes(const race_shape* shape, const race_options* opts,
+                                           size_t* bytes) {
+    if (!bytes || !shape) return RACE_ERROR_INVALID_VALUE;
+    if (carry_runs_decode(shape, opts)) {
+        if (!decode_options_ok(opts) || !shape_ok(shape)) return RACE_ERROR_INVALID_VALUE;
+        *bytes = 0;
+        return RACE_SUCCESS;
+    }
+    return race_fwd_workspace_bytes(shape, 1, opts, bytes, nullptr, nullptr);
+}
+
+race_status race_fwd_carry(const void* probsQ, const void* probsK, const void* V, void* out,
+                           const float* init_state, float* state, const race_shape* shape,
+                           const race_options* opts, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
+    Marks none;
+    return carry_impl(probsQ, probsK, V, out, init_state, state, shape, opts, workspace,
+                      workspace_bytes, stream, &none);
+}
+
+race_status race_fwd_carry_profiled(const void* probsQ, const void* probsK, const void* V,
+                                    void* out, const float* init_state, float* state,
+                                    const race_shape* shape, const race_options* opts,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream,
+                                    hipEvent_t* events, int32_t max_events, int32_t* n_events) {
+    if (!events || max_events < 2 || !n_events) return RACE_ERROR_INVALID_VALUE;
+    Marks marks;
+    marks.events = events;
+    marks.max = max_events;
+    const race_status st = carry_impl(probsQ, probsK, V, out, init_state, state, shape, opts,
+                                      workspace, workspace_bytes, stream, &marks);
     *n_events = marks.n;
     return st;
 }

@@ -49,6 +49,9 @@ struct Problem {
     int tile;        // tokens per tile (multiple of RACE_SUB_CHUNK_TOKENS)
     int64_t tiles;   // ceil(T / tile)
     int64_t rec;     // record_floats(S, d)
+    // Causal forward continued from a carried state ([N][S*d+S], B then A):
+    // the scan starts every stream from it instead of zero.  Null otherwise.
+    const float* init = nullptr;
 };
 
 // Optional hipEventRecord after each launch (race_fwd_profiled).
@@ -69,9 +72,10 @@ struct Marks {
 // rec[Wa*Wb + a] = sum_t x[t][a], over the tokens of the tile.
 hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, const Problem& p,
                                   int Wa, int Wb, hipStream_t stream);
-// In-place exclusive scan of the records over tiles (fixed tile order); the
-// inclusive total goes to state ([N][S*d+S]) when it is not null.  With
-// `reverse` the scan runs from the last tile to the first.
+// In-place exclusive scan of the records over tiles (fixed tile order),
+// starting from p.init when it is not null; the inclusive total goes to state
+// ([N][S*d+S]) when it is not null (state may be p.init).  With `reverse` the
+// scan runs from the last tile to the first.
 hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream,
                             bool reverse = false);
 // Totals over tiles into `totals` ([N][rec]) and, when not null, into
@@ -87,6 +91,10 @@ hipError_t launch_token_map(const void* x, void* out, const float* M, int64_t m_
                             int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
                             hipStream_t stream);
 // E = B / (A + eps) from state records ([N][S*d+S]) into E ([N][S][d]).
+// The causal op continued from init ([N][S*d+S]) token by token in one
+// launch (decode.hip); the advanced state goes to `state`, which may be init.
+hipError_t launch_decode(const void* q, const void* k, const void* v, void* out,
+                         const float* init, float* state, const Problem& p, hipStream_t stream);
 hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hipStream_t stream);
 // Dynamic LDS of the VALU output pass and map kernels.
 size_t causal_output_valu_lds_bytes(int S);

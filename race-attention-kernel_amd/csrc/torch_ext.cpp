@@ -4,6 +4,8 @@
 //       -> (out, state or None)
 //   forward_debug(probsQ, probsK, V, causal, tile_tokens=0, kernel=0)
 //       -> (out, records [N, tiles, rec], state [N, S*d+S], tile_tokens)
+//   forward_carry(probsQ, probsK, V, state, tile_tokens=0, kernel=0, inplace=False)
+//       -> (out, state advanced over these tokens)
 //   noncausal_backward(probsQ, probsK, V, dOut, state, need_q, need_k, need_v,
 //                      tile_tokens=0) -> (dQ or None, dK or None, dV or None)
 //   causal_backward(probsQ, probsK, V, dOut, need_q, need_k, need_v,
@@ -81,13 +83,18 @@ race_shape validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
     return sh;
 }
 
-race_options make_options(int64_t tile_tokens, int64_t kernel) {
+race_options make_options(int64_t tile_tokens, int64_t kernel, bool allow_decode = false) {
     TORCH_CHECK(tile_tokens >= 0 && tile_tokens % RACE_SUB_CHUNK_TOKENS == 0 &&
                     tile_tokens <= (int64_t(1) << 30),
                 "tile_tokens must be 0 (automatic) or a positive multiple of ",
                 RACE_SUB_CHUNK_TOKENS, ", got ", tile_tokens);
-    TORCH_CHECK(kernel >= 0 && kernel <= 3,
-                "kernel must be 0 (auto), 1 (valu), 2 (mfma) or 3 (mfma_wg)");
+    if (allow_decode) {
+        TORCH_CHECK(kernel >= 0 && kernel <= RACE_KERNEL_DECODE,
+                    "kernel must be 0 (auto), 1 (valu), 2 (mfma), 3 (mfma_wg) or 4 (decode)");
+    } else {
+        TORCH_CHECK(kernel >= 0 && kernel <= RACE_KERNEL_MFMA_WG,
+                    "kernel must be 0 (auto), 1 (valu), 2 (mfma) or 3 (mfma_wg)");
+    }
     race_options o;
     o.tile_tokens = static_cast<int32_t>(tile_tokens);
     o.kernel = static_cast<int32_t>(kernel);
@@ -146,6 +153,41 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, int64_t> forward_debug(const at::
     else
         records = at::zeros({N, 0, r.rec}, v.options().dtype(at::kFloat));
     return {r.out, records, r.state, r.tile};
+}
+
+// Causal forward continued from a carried state [N, S*d + S] (B then A):
+// returns (out, state after these tokens); with inplace the state is
+// advanced in init_state itself and that tensor is returned.
+std::tuple<at::Tensor, at::Tensor> forward_carry(const at::Tensor& q, const at::Tensor& k,
+                                                 const at::Tensor& v, const at::Tensor& init_state,
+                                                 int64_t tile_tokens, int64_t kernel, bool inplace) {
+    const race_shape sh = validate(q, k, v);
+    const race_options opts = make_options(tile_tokens, kernel, /*allow_decode=*/true);
+    const int64_t S = int64_t(sh.num_tables) * sh.num_buckets;
+    TORCH_CHECK(init_state.is_cuda() && init_state.scalar_type() == at::kFloat &&
+                    init_state.is_contiguous() && init_state.device() == q.device(),
+                "state must be a contiguous float32 tensor on the device of probsQ");
+    TORCH_CHECK(init_state.dim() == 2 && init_state.size(0) == sh.num_streams &&
+                    init_state.size(1) == S * sh.head_dim + S,
+                "state must be [N, S*d + S] = [", sh.num_streams, ", ", S * sh.head_dim + S,
+                "], got ", init_state.sizes());
+    TORCH_CHECK(reinterpret_cast<uintptr_t>(init_state.data_ptr()) % kAlignment == 0,
+                "state data must be 16-byte aligned");
+    const c10::DeviceGuard guard(q.device());
+    at::Tensor out = at::empty_like(v);
+    at::Tensor state = inplace ? init_state : at::empty_like(init_state);
+    size_t bytes = 0;
+    check_status(race_fwd_carry_workspace_bytes(&sh, &opts, &bytes),
+                 "race_fwd_carry_workspace_bytes");
+    at::Tensor ws;
+    if (bytes > 0)
+        ws = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+    check_status(race_fwd_carry(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                init_state.data_ptr<float>(), state.data_ptr<float>(), &sh, &opts,
+                                bytes > 0 ? ws.data_ptr() : nullptr, bytes, stream),
+                 "race_fwd_carry");
+    return {out, state};
 }
 
 std::tuple<c10::optional<at::Tensor>, c10::optional<at::Tensor>, c10::optional<at::Tensor>>
@@ -443,6 +485,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Forward that also returns the scanned tile records, the state and the tile length",
           py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("causal"),
           py::arg("tile_tokens") = 0, py::arg("kernel") = 0);
+    m.def("forward_carry", &forward_carry,
+          "Causal forward continued from a carried state -> (out, state)", py::arg("probsQ"),
+          py::arg("probsK"), py::arg("V"), py::arg("state"), py::arg("tile_tokens") = 0,
+          py::arg("kernel") = 0, py::arg("inplace") = false);
     m.def("noncausal_backward", &noncausal_backward, "Non-causal backward -> (dQ, dK, dV)",
           py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("dOut"), py::arg("state"),
           py::arg("need_q") = true, py::arg("need_k") = true, py::arg("need_v") = true,

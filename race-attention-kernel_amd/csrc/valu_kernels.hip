@@ -115,10 +115,13 @@ __global__ __launch_bounds__(kThreads) void tile_outer_sums_kernel(
 // Every sum has a fixed order, so the result is bitwise reproducible.  With
 // `reverse` the tiles are scanned from the last to the first (the suffix
 // sums of the causal backward): record t receives the sum over tiles > t.
+// `init` (nullable) is a carried state added before the first tile; every
+// thread reads its element before the group barrier and only the last group
+// writes `state`, so `state` may be `init`.
 constexpr int kScanGroupsMax = 8;
 
 __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__ records,
-                                                             float* __restrict__ state,
+                                                             float* state, const float* init,
                                                              int64_t tiles, int64_t rec, int used,
                                                              int reverse, int groups) {
     __shared__ float gsum[kThreads];
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__
     // Scan position t is record r[t * step].
     const int64_t step = reverse ? -rec : rec;
     float* r = records + n * tiles * rec + (reverse ? (tiles - 1) * rec : 0) + e;
-    float run = 0.f;
+    float run = (init && e < used) ? init[n * used + e] : 0.f;
     if (groups > 1) {
         float sum = 0.f;
         if (e < used) {
@@ -416,7 +419,7 @@ hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipS
     const int groups = p.tiles <= 32 ? 1 : kScanGroupsMax;
     const int elems = kThreads / groups;
     const dim3 grid(unsigned((used + elems - 1) / elems), unsigned(p.N));
-    tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.tiles, p.rec, used,
+    tile_scan_kernel<<<grid, kThreads, 0, stream>>>(records, state, p.init, p.tiles, p.rec, used,
                                                     reverse ? 1 : 0, groups);
     return hipGetLastError();
 }

@@ -26,7 +26,7 @@ from torch.autograd.function import once_differentiable
 
 from . import _lib
 
-KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3}
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3, "decode": 4}
 
 
 def _kernel_id(kernel: str | int) -> int:
@@ -108,6 +108,24 @@ def race_fused_fwd_with_state(probsQ, probsK, V, causal: bool = True, *, tile_to
     src/causal_v2/kernels/race_causal_fwd.h:20-21).  No autograd."""
     return _lib.ext().forward(probsQ, probsK, V, bool(causal), int(tile_tokens),
                               _kernel_id(kernel), True)
+
+
+def race_fused_fwd_carry(probsQ, probsK, V, state, *, inplace: bool = False, tile_tokens: int = 0,
+                         kernel: str | int = "auto"):
+    """(out, new_state): the causal op continued from a carried state.
+
+    state [N, S*d + S] fp32 (B [S, d] then A [S] per stream, as
+    race_fused_fwd_with_state returns it) holds the sums over all earlier
+    tokens; the call advances it over these T tokens, as the reference's
+    chunked forward carries A_state, B_state into its next chunk
+    (src/race_chunked.py:54-63).  Splitting a sequence anywhere and carrying
+    the state gives the unsplit outputs up to fp32 rounding.  With
+    inplace=True the state tensor itself is advanced (a decode step) and
+    returned.  Calls of at most 16 tokens run one decode launch; kernel
+    "decode" forces it for any T, the other kernels force the tile path.
+    No autograd."""
+    return _lib.ext().forward_carry(probsQ, probsK, V, state, int(tile_tokens), _kernel_id(kernel),
+                                    bool(inplace))
 
 
 def race_noncausal_backward(probsQ, probsK, V, dOut, state, *, need=(True, True, True),

@@ -139,6 +139,44 @@ def test_invalid_arguments_are_rejected_before_any_launch(race):
     assert abi.causal_bwd(0, 0, 0, 0, 16, 16, 16, abi.shape(8, 0, 4, 16, 64), opts, None, 0, 0) == 0
 
 
+def test_carry_workspace_and_argument_checks(race):
+    from race_attention_kernel_amd import abi
+
+    inv = abi.RACE_ERROR_INVALID_VALUE
+    # Decode calls (at most RACE_DECODE_TOKENS tokens, automatic choice, or the
+    # decode kernel forced at any length) need no workspace.
+    for T, opts in [(1, None), (abi.RACE_DECODE_TOKENS, None), (0, None),
+                    (5000, abi.options(0, abi.RACE_KERNEL_DECODE))]:
+        st, b = abi.fwd_carry_workspace_bytes(abi.shape(8, T, 4, 16, 64), opts)
+        assert (st, b) == (0, 0), (T, st, b)
+    # Longer calls use race_fwd's causal workspace for the same tile.
+    sh = abi.shape(8, 4096, 4, 16, 64)
+    opts = abi.options(512, abi.RACE_KERNEL_VALU)
+    st, b = abi.fwd_carry_workspace_bytes(sh, opts)
+    st2, b2, *_ = abi.fwd_workspace_bytes(sh, True, opts)
+    assert st == st2 == 0 and b == b2 > 0
+    assert abi.fwd_carry_workspace_bytes(sh, abi.options(100, abi.RACE_KERNEL_DECODE))[0] == inv
+    assert abi.fwd_carry_workspace_bytes(abi.shape(8, 4, 4, 16, 300))[0] == inv
+    one = abi.shape(8, 1, 4, 16, 64)
+    # The carried state is required and 16-byte aligned; the advanced state
+    # (when given) too; token pointers as in race_fwd.
+    assert abi.fwd_carry(16, 16, 16, 16, 0, 16, one, None, None, 0, 0) == inv
+    assert abi.fwd_carry(16, 16, 16, 16, 24, 16, one, None, None, 0, 0) == inv
+    assert abi.fwd_carry(16, 16, 16, 16, 16, 24, one, None, None, 0, 0) == inv
+    assert abi.fwd_carry(0, 16, 16, 16, 16, 16, one, None, None, 0, 0) == inv
+    assert abi.fwd_carry(16, 16, 16, 18, 16, 16, one, None, None, 0, 0) == inv
+    assert abi.fwd_carry(16, 16, 16, 16, 16, 16, one, abi.options(0, 9), None, 0, 0) == inv
+    # The tile path wants its workspace.
+    assert abi.fwd_carry(16, 16, 16, 16, 16, 16, sh, opts, None, 0, 0) == inv
+    # race_fwd itself has no decode kernel.
+    assert abi.fwd(16, 16, 16, 16, None, sh, True, abi.options(64, abi.RACE_KERNEL_DECODE), 64, 1 << 30,
+                   0) == inv
+    # Nothing to do: no streams, or no tokens and the state advanced in place.
+    assert abi.fwd_carry(0, 0, 0, 0, 16, 16, abi.shape(0, 1, 4, 16, 64), None, None, 0, 0) == 0
+    assert abi.fwd_carry(0, 0, 0, 0, 16, 16, abi.shape(8, 0, 4, 16, 64), None, None, 0, 0) == 0
+    assert abi.fwd_carry(0, 0, 0, 0, 16, None, abi.shape(8, 0, 4, 16, 64), None, None, 0, 0) == 0
+
+
 def test_torch_binding_validates_inputs_on_the_host(race, ext):
     import torch
 

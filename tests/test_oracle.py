@@ -106,6 +106,23 @@ def test_tiled_decomposition_equals_recurrence(oracle, T, tile, chunk):
     assert pref.shape[2] == S * d + S
 
 
+@pytest.mark.parametrize("split", [0, 1, 63, 200, 299, 300])
+def test_recurrence_continued_from_carried_state(oracle, split):
+    # Running tokens [0, split) and then [split, T) from the carried state is
+    # the unsplit run (the carry of src/race_chunked.py:54-63): outputs of the
+    # second part and the final state both match.
+    q, k, v = inputs(split + 11, 3, 300, 2, 16, 24)
+    full, fin = oracle.causal_recurrence(q, k, v, want_state=True)
+    _, mid = oracle.causal_recurrence(q[:, :split], k[:, :split], v[:, :split], want_state=True)
+    out2, fin2 = oracle.causal_recurrence(q[:, split:], k[:, split:], v[:, split:], want_state=True,
+                                          init_state=mid)
+    assert rel_err(fin2, fin) <= FP64_TOL
+    if split < 300:
+        assert rel_err(out2, full[:, split:]) <= FP64_TOL
+    # A zero carried state is no carried state.
+    assert np.array_equal(oracle.causal_recurrence(q, k, v, init_state=np.zeros_like(fin)), full)
+
+
 def test_cumsum_bmm_and_dense_forms_agree(oracle):
     q, k, v = inputs(5, 3, 200, 2, 8, 16)
     rec = oracle.causal_recurrence(q, k, v)
