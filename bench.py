@@ -130,16 +130,19 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
-    ap.add_argument("--pass", dest="pass_", choices=["fwd", "bwd", "fwdbwd", "module", "alg1"],
+    ap.add_argument("--pass", dest="pass_",
+                    choices=["fwd", "bwd", "fwdbwd", "module", "alg1", "decode"],
                     default="fwd",
                     help="what one step runs: the forward (default), the backward (from the "
                          "forward's inputs and a synthetic dOut), both, the module's hot "
-                         "span (hashing of Q and K rows, then the forward), or the "
-                         "Algorithm-1 forward with the hashing inside (race_alg1_fwd)")
+                         "span (hashing of Q and K rows, then the forward), the "
+                         "Algorithm-1 forward with the hashing inside (race_alg1_fwd), or "
+                         "one decode step (race_fwd_carry of --T tokens per stream, default 1, "
+                         "advancing the carried state in place) at the workload's N, S, d")
     ap.add_argument("--alg1-variant", choices=["fp32", "bf16"], default="bf16",
                     help="rounding variant of --pass alg1 (fp32-accurate or bf16 features)")
     ap.add_argument("--T", type=int, default=0)
-    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg"], default="auto")
+    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg", "decode"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -375,6 +378,110 @@ def bench_alg1(args) -> int:
     return 0
 
 
+def bench_decode(args) -> int:
+    """--pass decode: race_fwd_carry steps on a state carried in place."""
+    import torch
+
+    race = entry.load_package()
+    from race_attention_kernel_amd import abi
+
+    cfg = race.CONFIGS[WORKLOADS[args.workload][0]]
+    T = args.T or 1
+    N, S, d = cfg.N, cfg.L * cfg.R, cfg.d
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v = race.config_inputs(cfg, T, seed=0, device=dev, gen_device="cuda")
+    # The state of a 4096-token prompt of the same distribution.
+    pq, pk, pv = race.config_inputs(cfg, 4096, seed=1, device=dev, gen_device="cuda")
+    _, state = race.race_fused_fwd_with_state(pq, pk, pv, True)
+    del pq, pk, pv
+    out = torch.empty_like(v)
+    sh = abi.shape(N, T, cfg.L, cfg.R, d, abi.RACE_BF16 if es == 2 else abi.RACE_F32)
+    kernel_id = race.ops.KERNELS["decode" if args.kernel == "auto" else args.kernel]
+    opts = abi.options(args.tile, kernel_id)
+    st, ws_bytes = abi.fwd_carry_workspace_bytes(sh, opts)
+    if st != 0:
+        raise RuntimeError(abi.status_string(st))
+    ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), state.data_ptr(), state.data_ptr())
+    torch.cuda.synchronize()
+
+    def check(st_):
+        if st_ != 0:
+            raise RuntimeError(abi.status_string(st_))
+
+    def plain():
+        check(abi.fwd_carry(*ptrs, sh, opts, ws.data_ptr(), ws_bytes, stream))
+
+    events = HipEvents()
+    per_step = [events.array(8) for _ in range(args.steps)]
+    for _ in range(args.warmup):
+        plain()
+    torch.cuda.synchronize()
+    bracket = events.array(2)
+    t0 = time.perf_counter()
+    events.record(bracket[0], stream)
+    for _ in range(args.steps):
+        plain()
+    events.record(bracket[1], stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
+    n = 0
+    for i in range(args.steps):
+        st_, n = abi.fwd_carry_profiled(*ptrs, sh, opts, ws.data_ptr(), ws_bytes, stream, per_step[i])
+        check(st_)
+    torch.cuda.synchronize()
+    gaps = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step) for j in range(n - 1)]
+    names = ["decode"] if len(gaps) == 1 else [f"kernel{j}" for j in range(len(gaps))]
+    events.destroy()
+    # One launch reads and writes the state (B [S][d] and A [S], fp32) once
+    # and reads the tokens' q, k, v rows and writes their outputs once.
+    state_bytes = 4.0 * N * (S * d + S)
+    launch_bytes = 2 * state_bytes + es * N * T * (2 * S + 2 * d)
+    dom = max(range(len(gaps)), key=lambda j: gaps[j])
+    achieved = launch_bytes / (gaps[dom] * 1e-3) / 1e9 if len(gaps) == 1 else None
+    value = N * T / (ms_per_step * 1e-3) / 1e6
+    result = {
+        "metric": f"causal decode step M tokens/s at N={N},S={S},d={d},{T} token(s) per stream on 1 GPU",
+        "value": round(value, 3),
+        "unit": UNIT,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if es == 2 else "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload} decode: race_fwd_carry of {T} token(s) per stream, N={N} "
+                        f"S={S} d={d}, state carried in place from a 4096-token prompt",
+            "N": N, "S": S, "d": d, "T": T, "kernel": args.kernel if args.kernel != "auto" else "decode",
+            "launches_per_step": len(gaps),
+            "kernel_ms": {names[j]: round(gaps[j], 6) for j in range(len(gaps))},
+            "wall_ms_per_step": round(wall * 1e3 / args.steps, 6),
+            "state_bytes": state_bytes,
+            "alg_bytes_per_launch": launch_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": names[dom],
+            "achieved": round(achieved, 1) if achieved is not None else None,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4) if achieved is not None else None,
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -384,6 +491,8 @@ def main() -> int:
         return 2
     if args.pass_ == "alg1":
         return bench_alg1(args)
+    if args.pass_ == "decode":
+        return bench_decode(args)
     import torch
 
     race = entry.load_package()
