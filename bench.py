@@ -406,6 +406,11 @@ def bench_decode(args) -> int:
     ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)
     stream = torch.cuda.current_stream().cuda_stream
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), state.data_ptr(), state.data_ptr())
+    if args.calibrate_copy:
+        src = torch.ones(args.calibrate_copy << 18, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        del src, dst
     torch.cuda.synchronize()
 
     def check(st_):
@@ -474,7 +479,7 @@ def bench_decode(args) -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4) if achieved is not None else None,
-            "traffic": None,
+            "traffic": traffic_for(f"decode_{args.workload}_T{T}", names[dom]),
         },
         "cpu_baseline": None,
     }
