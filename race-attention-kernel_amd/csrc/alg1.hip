@@ -670,7 +670,7 @@ __global__ __launch_bounds__(kThreads, (A1Geo<kPhiSplit, SP, D, LPP>::kOutBlocks
                     }
                     o[bi] = mfma_mix<false, true>(vh[kk], vh[kk], gh, gl, o[bi]);
                 }
-                store4<bf16_t, kOutStorePolicy>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * 2,
+                store4<bf16_t, kAlg1StorePolicy>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * 2,
                                                 o[bi] * rden[bi]);
             }
 #pragma unroll

@@ -458,7 +458,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
                     }
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
-                store4<TIn, kOutStorePolicy>(
+                store4<TIn, std::is_same<TIn, float>::value ? kOutWgStorePolicyF32 : kOutStorePolicy>(
                     or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * int(sizeof(TIn)), o[bi]);
             }
 #pragma unroll

@@ -115,10 +115,21 @@ constexpr int kPolicyStream = 2;
 #ifndef RACE_OUT_STORE_POLICY
 #define RACE_OUT_STORE_POLICY 0
 #endif
+#ifndef RACE_OUT_WG_STORE_POLICY
+#define RACE_OUT_WG_STORE_POLICY 2
+#endif
+#ifndef RACE_ALG1_STORE_POLICY
+#define RACE_ALG1_STORE_POLICY 0
+#endif
 constexpr int kSumsLoadPolicy = RACE_SUMS_LOAD_POLICY;  // K1 reads of K and V
 constexpr int kOutKVPolicy = RACE_OUT_KV_POLICY;        // K3 reads of K and V read once
 constexpr int kOutQPolicy = RACE_OUT_Q_POLICY;          // K3 reads of Q
-constexpr int kOutStorePolicy = RACE_OUT_STORE_POLICY;  // K3 writes of out
+constexpr int kOutStorePolicy = RACE_OUT_STORE_POLICY;  // register-direct K3 writes of out
+// Workgroup K3 writes of fp32 out: `nt` measured 120 -> 116 us at cfg2; bf16
+// writes keep the default (the S = 256 kernel at cfg5 ran 997 -> 1015 us with
+// `nt`, the register-direct kernel at cfg3 866 -> 881 us).
+constexpr int kOutWgStorePolicyF32 = RACE_OUT_WG_STORE_POLICY;
+constexpr int kAlg1StorePolicy = RACE_ALG1_STORE_POLICY;  // Algorithm-1 K3 writes of out
 
 template <int P>
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
