@@ -51,8 +51,9 @@ using namespace mfma;
 // Geometry of one (S, D, C, dtype) specialization.  Every tile is stored with
 // tokens as rows (W, K, V; P with queries as rows); products that contract
 // over tokens read their fragments transposed (Plane::frag_tr).
-template <typename TIn, int S, int D, int C>
+template <typename TIn, int S, int D, int C, int NW = 4>
 struct Geo {
+    static constexpr int kT = 64 * NW;  // threads per workgroup (NW wave64s)
     static constexpr bool kSplit = std::is_same<TIn, float>::value;
     static constexpr int E = Elem<TIn>::kPerVec;
     using PS = Plane<kSplit, S>;  // token rows over buckets: W, K
@@ -66,16 +67,17 @@ struct Geo {
     static constexpr int kSumsLds = kKBytes + kVBytes + 16 * S * 4;
     // Register staging of K and V: blocks of 4 rows x E columns.
     static constexpr int kKBlk = (C / 4) * (S / E);
-    static constexpr int kKPer = (kKBlk + kThreads - 1) / kThreads;
+    static constexpr int kKPer = (kKBlk + kT - 1) / kT;
     static constexpr int kVBlk = (C / 4) * (D / E);
-    static constexpr int kVPer = (kVBlk + kThreads - 1) / kThreads;
+    static constexpr int kVPer = (kVBlk + kT - 1) / kT;
     static_assert(S % 64 == 0 && D % 64 == 0 && (C == 32 || C == 64), "unsupported tile");
+    static_assert(S % (16 * NW) == 0 && D % (16 * NW) == 0, "every wave owns whole 16-blocks");
 };
 
 // Raw K and V registers of one sub-chunk.
-template <typename TIn, int S, int D, int C, int P>
+template <typename TIn, int S, int D, int C, int P, int NW = 4>
 struct KVStage {
-    using G = Geo<TIn, S, D, C>;
+    using G = Geo<TIn, S, D, C, NW>;
     uint4 k[G::kKPer][4];
     uint4 v[G::kVPer][4];
 
@@ -85,9 +87,9 @@ struct KVStage {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < G::kKPer; ++p) {
-            const int blk = tid + p * kThreads;
+            const int blk = tid + p * G::kT;
             const int a = blk / (S / G::E), b = blk % (S / G::E);
-            if (G::kKBlk % kThreads == 0 || blk < G::kKBlk) {
+            if (G::kKBlk % G::kT == 0 || blk < G::kKBlk) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
                     k[p][rr] = buf_load16<P>(kr, ((r0 + 4 * a + rr) * S + b * G::E) * int(sizeof(TIn)));
@@ -95,9 +97,9 @@ struct KVStage {
         }
 #pragma unroll
         for (int p = 0; p < G::kVPer; ++p) {
-            const int blk = tid + p * kThreads;
+            const int blk = tid + p * G::kT;
             const int a = blk / (D / G::E), b = blk % (D / G::E);
-            if (G::kVBlk % kThreads == 0 || blk < G::kVBlk) {
+            if (G::kVBlk % G::kT == 0 || blk < G::kVBlk) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
                     v[p][rr] = buf_load16<P>(vr, ((r0 + 4 * a + rr) * D + b * G::E) * int(sizeof(TIn)));
@@ -113,7 +115,7 @@ struct KVStage {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < G::kKPer; ++p) {
-            const int blk = tid + p * kThreads;
+            const int blk = tid + p * G::kT;
             if (blk >= G::kKBlk) continue;
             const int a = blk / (S / E), b = blk % (S / E);
 #pragma unroll
@@ -143,7 +145,7 @@ struct KVStage {
         }
 #pragma unroll
         for (int p = 0; p < G::kVPer; ++p) {
-            const int blk = tid + p * kThreads;
+            const int blk = tid + p * G::kT;
             if (blk >= G::kVBlk) continue;
             const int a = blk / (D / E), b = blk % (D / E);
 #pragma unroll
@@ -264,22 +266,24 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 //      the accumulator layout, W written as a plane tile
 //   3. P^T blocks (j-block <= i-block) = K W^T, masked j > i, written as the
 //      plane tile P [C][C]
-//   4. O^T [D][C] = B0^T W^T + V^T P^T         wave w: c-blocks w, w+4, ..
+//   4. O^T [D][C] = B0^T W^T + V^T P^T         wave w: c-blocks w, w+NW, ..
 //   5. B0 += K^T V                             same c-blocks, all s-blocks
-template <typename TIn, int S, int D, int C, int kMinBlocks>
-__global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kernel(
+// NW waves per workgroup (4, or 8 where the carried state would otherwise
+// fill the register file: two waves per SIMD then share the CU's work).
+template <typename TIn, int S, int D, int C, int kMinBlocks, int NW>
+__global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     TIn* __restrict__ out, const float* __restrict__ records, int64_t T, int tile, int64_t tiles,
     int64_t rec) {
-    using G = Geo<TIn, S, D, C>;
+    using G = Geo<TIn, S, D, C, NW>;
     using PS = typename G::PS;
     using PC = typename G::PC;
     using PD = typename G::PD;
     constexpr bool kSplit = G::kSplit;
     constexpr int NSB = S / 16, NBI = C / 16, NKS = S / 32, NKC = C / 32;
-    constexpr int SBW = S / 64, CBW = D / 64;
+    constexpr int SBW = S / (16 * NW), CBW = D / (16 * NW);
     constexpr int NLB = NBI * (NBI + 1) / 2;       // lower-triangular P blocks
-    constexpr int PBW = (NLB + 3) / 4;             // P blocks per wave
+    constexpr int PBW = (NLB + NW - 1) / NW;       // P blocks per wave
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Ws = lds;
     unsigned char* Ks = Ws + G::kWBytes;
@@ -306,12 +310,12 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         for (int cbw = 0; cbw < CBW; ++cbw)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
-                b0[sb][cbw][rr] = rec_p[(16 * sb + 4 * g + rr) * D + 16 * (w + 4 * cbw) + lr];
+                b0[sb][cbw][rr] = rec_p[(16 * sb + 4 * g + rr) * D + 16 * (w + NW * cbw) + lr];
     float a0[SBW][4];
 #pragma unroll
     for (int sbw = 0; sbw < SBW; ++sbw)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) a0[sbw][rr] = rec_p[S * D + 16 * (w + 4 * sbw) + 4 * g + rr];
+        for (int rr = 0; rr < 4; ++rr) a0[sbw][rr] = rec_p[S * D + 16 * (w + NW * sbw) + 4 * g + rr];
 
     // The two partial triangles of the running-mass operand (i - j offset 0 or 16).
     const bf16x8 tri0 = tril_frag(0, g, lr), tri1 = tril_frag(16, g, lr);
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
 
     // Q of a sub-chunk in the layout of step 2: lane (g, lr) holds
-    // Q[16 bi + lr][16 (w + 4 sbw) + 4 g .. + 3].
+    // Q[16 bi + lr][16 (w + NW sbw) + 4 g .. + 3].
     using QRegs = f32x4[SBW][NBI];
     auto load_q = [&](QRegs& qr, int r0) {
 #pragma unroll
@@ -328,12 +332,12 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi)
                 qr[sbw][bi] = load_q4<TIn, kOutQPolicy>(
-                    qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + 4 * sbw) + 4 * g) * int(sizeof(TIn)));
+                    qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + NW * sbw) + 4 * g) * int(sizeof(TIn)));
     };
 
     // One sub-chunk from the raw registers `st` / `qr`, which are then
     // refilled with the next sub-chunk (a deeper prefetch measured slower).
-    auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy>& st, QRegs& qr, int r0) {
+    auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy, NW>& st, QRegs& qr, int r0) {
         __syncthreads();
         st.store(Ks, Vs, nullptr);
         f32x4 qc[SBW][NBI];
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         // 1 + 2: running mass and W.
 #pragma unroll
         for (int sbw = 0; sbw < SBW; ++sbw) {
-            const int sb = w + 4 * sbw;
+            const int sb = w + NW * sbw;
             bf16x8 kh[NKC], kl[NKC];
 #pragma unroll
             for (int kk = 0; kk < NKC; ++kk) PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh[kk], kl[kk]);
@@ -385,7 +389,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         int pbi[PBW], pbj[PBW];
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
-            const int idx = w + 4 * pb;
+            const int idx = w + NW * pb;
             int bi = 0, rem = idx;
             while (rem > bi) { rem -= bi + 1; ++bi; }
             pbi[pb] = bi;
@@ -407,7 +411,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         }
 #pragma unroll
         for (int pb = 0; pb < PBW; ++pb) {
-            if (w + 4 * pb >= NLB) continue;
+            if (w + NW * pb >= NLB) continue;
             uint2 hi, lo;
             split4<kSplit>(pacc[pb][0], pacc[pb][1], pacc[pb][2], pacc[pb][3], hi, lo);
             PC::put4(Ps, 16 * pbi[pb] + lr, 16 * pbj[pb] + 4 * g, hi, lo);
@@ -417,7 +421,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         // 4 + 5: output and state update for this wave's c-blocks.
 #pragma unroll
         for (int cbw = 0; cbw < CBW; ++cbw) {
-            const int cb = w + 4 * cbw;
+            const int cb = w + NW * cbw;
             bf16x8 vh[NKC], vl[NKC];
 #pragma unroll
             for (int kk = 0; kk < NKC; ++kk) PD::frag_tr(Vs, 32 * kk, 16 * cb, g, lr, vh[kk], vl[kk]);
@@ -476,17 +480,18 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void causal_output_mfma_kerne
         }
     };
 
-    KVStage<TIn, S, D, C, kOutKVPolicy> st;
+    KVStage<TIn, S, D, C, kOutKVPolicy, NW> st;
     QRegs qr;
     st.load(kr, vr, 0);
     load_q(qr, 0);
     for (int r0 = 0; r0 < rows; r0 += C) sub_chunk(st, qr, r0);
 }
 
-template <typename TIn, int S, int D, int C, int kMinBlocks>
+template <typename TIn, int S, int D, int C, int kMinBlocks, int NW = 4>
 hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void* out, float* records,
                               float* state, const Problem& p, hipStream_t stream, Marks* marks) {
     using G = Geo<TIn, S, D, C>;
+    using GO = Geo<TIn, S, D, C, NW>;
     // Tiles are whole sub-chunks, and a tile's bytes fit a 32-bit buffer range.
     if (p.tile % C != 0) return hipErrorInvalidValue;
     if (int64_t(p.tile) * (S > D ? S : D) * int64_t(sizeof(TIn)) >= (int64_t(1) << 31))
@@ -505,7 +510,7 @@ hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void*
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
     if ((err = launch_tile_scan(records, state, p, stream)) != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
-    causal_output_mfma_kernel<TIn, S, D, C, kMinBlocks><<<grid, kThreads, G::kOutputLds, stream>>>(
+    causal_output_mfma_kernel<TIn, S, D, C, kMinBlocks, NW><<<grid, GO::kT, GO::kOutputLds, stream>>>(
         static_cast<const TIn*>(q), static_cast<const TIn*>(k), static_cast<const TIn*>(v),
         static_cast<TIn*>(out), records, p.T, p.tile, p.tiles, p.rec);
     err = hipGetLastError();
@@ -531,7 +536,7 @@ hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out,
     if (p.S == 256 && p.d == 64)
         return launch_mfma_family<TIn, 256, 64, 32, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 256 && p.d == 128)
-        return launch_mfma_family<TIn, 256, 128, 32, 1>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, 256, 128, 32, 1, 8>(q, k, v, out, records, state, p, stream, marks);
     return hipErrorInvalidValue;
 }
 
