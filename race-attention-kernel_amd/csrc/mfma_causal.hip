@@ -63,7 +63,10 @@ struct Geo {
     static constexpr int kKBytes = C * PS::kPitch;
     static constexpr int kPBytes = C * PC::kPitch;
     static constexpr int kVBytes = C * PD::kPitch;
-    static constexpr int kOutputLds = kWBytes + kKBytes + kPBytes + kVBytes;
+    // The output tile [C][D] in TIn, rows of 16-byte chunks swizzled by row
+    // (OutTile), staged so that global stores cover whole rows.
+    static constexpr int kOBytes = C * D * int(sizeof(TIn));
+    static constexpr int kOutputLds = kWBytes + kKBytes + kPBytes + kVBytes + kOBytes;
     static constexpr int kSumsLds = kKBytes + kVBytes + 16 * S * 4;
     // Register staging of K and V: blocks of 4 rows x E columns.
     static constexpr int kKBlk = (C / 4) * (S / E);
@@ -163,6 +166,46 @@ struct KVStage {
                     }
                     G::PD::put4(Vs, 4 * a + rr, b * E + 4 * h, hi, lo);
                 }
+        }
+    }
+};
+
+// The output tile of one sub-chunk in LDS: [C][D] elements of TIn, row r a run
+// of D * sizeof(TIn) / 16 chunks of 16 bytes with chunk u stored at u ^ (r mod
+// the chunk count, at most 16).  The accumulator-layout writes (16 rows, 4
+// values each) and the row-contiguous reads of the flush both meet every bank
+// once per 128 bytes.
+template <typename TIn, int D, int C>
+struct OutTile {
+    static constexpr int kRowBytes = D * int(sizeof(TIn));
+    static constexpr int kChunks = kRowBytes / 16;
+    static constexpr int kMask = (kChunks < 16 ? kChunks : 16) - 1;
+    __device__ __forceinline__ static int at(int row, int byte) {
+        return row * kRowBytes + 16 * ((byte >> 4) ^ (row & kMask)) + (byte & 15);
+    }
+    // Values [row][col .. col + 3] (col % 4 == 0) from the accumulator layout.
+    __device__ __forceinline__ static void put(unsigned char* t, int row, int col, const f32x4& x) {
+        unsigned char* p = t + at(row, col * int(sizeof(TIn)));
+        if constexpr (std::is_same<TIn, float>::value) {
+            *reinterpret_cast<f32x4*>(p) = x;
+        } else {
+            *reinterpret_cast<uint2*>(p) = make_uint2(pack2(x[0], x[1]), pack2(x[2], x[3]));
+        }
+    }
+    // Store the tile to rows r0 .. r0 + C - 1 of `o` (rows past the tile are
+    // dropped by the buffer range), 16 bytes per thread and step.
+    template <int P, int NT>
+    __device__ __forceinline__ static void flush(const unsigned char* t, __amdgpu_buffer_rsrc_t o,
+                                                 int r0) {
+        constexpr int kTotal = C * kChunks;
+#pragma unroll
+        for (int i = 0; i < (kTotal + NT - 1) / NT; ++i) {
+            const int q = int(threadIdx.x) + i * NT;
+            if (kTotal % NT != 0 && q >= kTotal) break;
+            const int row = q / kChunks, u = q % kChunks;
+            const uint4 x = *reinterpret_cast<const uint4*>(t + row * kRowBytes + 16 * (u ^ (row & kMask)));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), o,
+                                                   (r0 + row) * kRowBytes + 16 * u, 0, P);
         }
     }
 };
@@ -289,6 +332,9 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     unsigned char* Ks = Ws + G::kWBytes;
     unsigned char* Ps = Ks + G::kKBytes;
     unsigned char* Vs = Ps + G::kPBytes;
+    unsigned char* Os = Vs + G::kVBytes;
+    using OT = OutTile<TIn, D, C>;
+    constexpr int kStoreP = std::is_same<TIn, float>::value ? kOutWgStorePolicyF32 : kOutStorePolicy;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -337,8 +383,10 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
 
     // One sub-chunk from the raw registers `st` / `qr`, which are then
     // refilled with the next sub-chunk (a deeper prefetch measured slower).
+    // The previous sub-chunk's output tile is flushed after the first barrier.
     auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy, NW>& st, QRegs& qr, int r0) {
         __syncthreads();
+        if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
         st.store(Ks, Vs, nullptr);
         f32x4 qc[SBW][NBI];
 #pragma unroll
@@ -462,8 +510,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
                     }
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
-                store4<TIn, std::is_same<TIn, float>::value ? kOutWgStorePolicyF32 : kOutStorePolicy>(
-                    or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * int(sizeof(TIn)), o[bi]);
+                OT::put(Os, 16 * bi + lr, 16 * cb + 4 * g, o[bi]);
             }
 #pragma unroll
             for (int sb = 0; sb < NSB; ++sb) {
@@ -484,7 +531,10 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     QRegs qr;
     st.load(kr, vr, 0);
     load_q(qr, 0);
-    for (int r0 = 0; r0 < rows; r0 += C) sub_chunk(st, qr, r0);
+    int r0 = 0;
+    for (; r0 < rows; r0 += C) sub_chunk(st, qr, r0);
+    __syncthreads();
+    if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
 }
 
 template <typename TIn, int S, int D, int C, int kMinBlocks, int NW = 4>
