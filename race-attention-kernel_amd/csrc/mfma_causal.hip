@@ -66,7 +66,13 @@ struct Geo {
     // The output tile [C][D] in TIn, rows of 16-byte chunks swizzled by row
     // (OutTile), staged so that global stores cover whole rows.
     static constexpr int kOBytes = C * D * int(sizeof(TIn));
-    static constexpr int kOutputLds = kWBytes + kKBytes + kPBytes + kVBytes + kOBytes;
+    // bf16 Q is staged through LDS as well ([C][S], the same row swizzle), so
+    // its global loads cover whole rows: read in the accumulator layout it
+    // would be 32-byte pieces of 16 rows per instruction (10% slower at
+    // cfg5).  fp32 Q (64-byte pieces) measured no faster staged.
+    static constexpr bool kQStage = !kSplit;
+    static constexpr int kQBytes = kQStage ? C * S * int(sizeof(TIn)) : 0;
+    static constexpr int kOutputLds = kWBytes + kKBytes + kPBytes + kVBytes + kOBytes + kQBytes;
     static constexpr int kSumsLds = kKBytes + kVBytes + 16 * S * 4;
     // Register staging of K and V: blocks of 4 rows x E columns.
     static constexpr int kKBlk = (C / 4) * (S / E);
@@ -192,6 +198,21 @@ struct OutTile {
             *reinterpret_cast<uint2*>(p) = make_uint2(pack2(x[0], x[1]), pack2(x[2], x[3]));
         }
     }
+    // Values [row][col .. col + 3] (col % 4 == 0) as floats.
+    __device__ __forceinline__ static f32x4 get4(const unsigned char* t, int row, int col) {
+        const unsigned char* p = t + at(row, col * int(sizeof(TIn)));
+        if constexpr (std::is_same<TIn, float>::value) {
+            return *reinterpret_cast<const f32x4*>(p);
+        } else {
+            const uint2 u = *reinterpret_cast<const uint2*>(p);
+            return f32x4{lo_half(u.x), hi_half(u.x), lo_half(u.y), hi_half(u.y)};
+        }
+    }
+    // 16-byte chunk q (row-major over the tile) to or from its swizzled place.
+    __device__ __forceinline__ static int chunk_at(int q) {
+        const int row = q / kChunks, u = q % kChunks;
+        return row * kRowBytes + 16 * (u ^ (row & kMask));
+    }
     // Store the tile to rows r0 .. r0 + C - 1 of `o` (rows past the tile are
     // dropped by the buffer range), 16 bytes per thread and step.
     template <int P, int NT>
@@ -202,10 +223,9 @@ struct OutTile {
         for (int i = 0; i < (kTotal + NT - 1) / NT; ++i) {
             const int q = int(threadIdx.x) + i * NT;
             if (kTotal % NT != 0 && q >= kTotal) break;
-            const int row = q / kChunks, u = q % kChunks;
-            const uint4 x = *reinterpret_cast<const uint4*>(t + row * kRowBytes + 16 * (u ^ (row & kMask)));
+            const uint4 x = *reinterpret_cast<const uint4*>(t + chunk_at(q));
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), o,
-                                                   (r0 + row) * kRowBytes + 16 * u, 0, P);
+                                                   r0 * kRowBytes + 16 * q, 0, P);
         }
     }
 };
@@ -333,7 +353,12 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     unsigned char* Ps = Ks + G::kKBytes;
     unsigned char* Vs = Ps + G::kPBytes;
     unsigned char* Os = Vs + G::kVBytes;
+    unsigned char* Qs = Os + G::kOBytes;
     using OT = OutTile<TIn, D, C>;
+    using QT = OutTile<TIn, S, C>;
+    constexpr bool kQStage = G::kQStage;
+    constexpr int kQChunks = C * QT::kChunks;
+    constexpr int kQPer = (kQChunks + G::kT - 1) / G::kT;
     constexpr int kStoreP = std::is_same<TIn, float>::value ? kOutWgStorePolicyF32 : kOutStorePolicy;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
@@ -369,16 +394,26 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = __bf16(1.0f);
 
-    // Q of a sub-chunk in the layout of step 2: lane (g, lr) holds
-    // Q[16 bi + lr][16 (w + NW sbw) + 4 g .. + 3].
-    using QRegs = f32x4[SBW][NBI];
+    // Q of a sub-chunk: staged (bf16) as 16-byte chunks of whole rows, or in
+    // the layout of step 2, lane (g, lr) holding Q[16 bi + lr][16 (w + NW sbw)
+    // + 4 g .. + 3].
+    using QRegs = std::conditional_t<kQStage, uint4[kQPer], f32x4[SBW][NBI]>;
     auto load_q = [&](QRegs& qr, int r0) {
+        if constexpr (kQStage) {
 #pragma unroll
-        for (int sbw = 0; sbw < SBW; ++sbw)
+            for (int i = 0; i < kQPer; ++i) {
+                const int qi = tid + i * G::kT;
+                if (kQChunks % G::kT == 0 || qi < kQChunks)
+                    qr[i] = buf_load16<kOutQPolicy>(qr_, r0 * S * int(sizeof(TIn)) + 16 * qi);
+            }
+        } else {
 #pragma unroll
-            for (int bi = 0; bi < NBI; ++bi)
-                qr[sbw][bi] = load_q4<TIn, kOutQPolicy>(
-                    qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + NW * sbw) + 4 * g) * int(sizeof(TIn)));
+            for (int sbw = 0; sbw < SBW; ++sbw)
+#pragma unroll
+                for (int bi = 0; bi < NBI; ++bi)
+                    qr[sbw][bi] = load_q4<TIn, kOutQPolicy>(
+                        qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + NW * sbw) + 4 * g) * int(sizeof(TIn)));
+        }
     };
 
     // One sub-chunk from the raw registers `st` / `qr`, which are then
@@ -389,10 +424,19 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
         if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
         st.store(Ks, Vs, nullptr);
         f32x4 qc[SBW][NBI];
+        if constexpr (kQStage) {
 #pragma unroll
-        for (int sbw = 0; sbw < SBW; ++sbw)
+            for (int i = 0; i < kQPer; ++i) {
+                const int qi = tid + i * G::kT;
+                if (kQChunks % G::kT == 0 || qi < kQChunks)
+                    *reinterpret_cast<uint4*>(Qs + QT::chunk_at(qi)) = qr[i];
+            }
+        } else {
 #pragma unroll
-            for (int bi = 0; bi < NBI; ++bi) qc[sbw][bi] = qr[sbw][bi];
+            for (int sbw = 0; sbw < SBW; ++sbw)
+#pragma unroll
+                for (int bi = 0; bi < NBI; ++bi) qc[sbw][bi] = qr[sbw][bi];
+        }
         // Prefetch (past the tile: zeros, never used).
         st.load(kr, vr, r0 + C);
         load_q(qr, r0 + C);
@@ -417,7 +461,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
                     if constexpr (kSplit) acc = mfma16(kl[kk], lf, acc);
                     acc = mfma16(kh[kk], lf, acc);
                 }
-                const f32x4 qv = qc[sbw][bi];
+                const f32x4 qv = kQStage ? QT::get4(Qs, 16 * bi + lr, 16 * sb + 4 * g) : qc[sbw][bi];
                 uint2 hi, lo;
                 split4<kSplit>(qv[0] * __builtin_amdgcn_rcpf(acc[0] + kEps),
                                qv[1] * __builtin_amdgcn_rcpf(acc[1] + kEps),
