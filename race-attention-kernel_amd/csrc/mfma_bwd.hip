@@ -35,6 +35,12 @@ using namespace mfma;
 
 constexpr int kBC = 32;  // tokens per sub-chunk
 constexpr int kBS = 64;  // buckets (S) and value columns (d)
+#ifndef RACE_BWD_DQ_BLOCKS
+#define RACE_BWD_DQ_BLOCKS 2
+#endif
+// Resident B1 workgroups per CU: two since dQ is staged through LDS (three
+// spill registers there; measured 139 against 170 us at cfg2).
+constexpr int kDqBlocks = RACE_BWD_DQ_BLOCKS;
 
 template <typename TIn>
 struct BwdGeo {
@@ -46,7 +52,12 @@ struct BwdGeo {
     static constexpr int kMBytes = kBC * PM::kPitch;
     static constexpr int kWTBytes = kBS * PM::kPitch;  // W^T [s][i]
     static constexpr int kZBytes = kBS * PR::kPitch;   // Z1 [s][c]
-    static constexpr int kDqLds = 3 * kRBytes + kMBytes;
+    // B1's dQ tile [kBC][kBS] fp32 staged in LDS (OutTile) and stored as
+    // whole rows, as the fp32 copy and (bf16 tokens) converted to dQ at the
+    // store (164 -> 139 us at cfg2).  B3 stores dK and dV from registers:
+    // staged the same way it measured slower (196 -> 260 us).
+    static constexpr int kT32Bytes = kBC * kBS * 4;
+    static constexpr int kDqLds = 3 * kRBytes + kMBytes + kT32Bytes;
     static constexpr int kDkvLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
     // Staging: blocks of 4 tokens x E features per tensor.
     static constexpr int kBlk = (kBC / 4) * (kBS / E);   // 128 (fp32) or 64 (bf16)
@@ -113,9 +124,10 @@ __device__ __forceinline__ void split8v(const f32x4& a, const f32x4& b, bf16x8& 
 // ---------------------------------------------------------------------------
 // B1, forward walk of one (tile, stream): dQ, its fp32 copy, the running mass
 // at every sub-chunk start, and the tile's suffix totals Z = sum W (x) g,
-// Y = sum alpha into its record.
+// Y = sum alpha into its record.  For fp32 tokens the fp32 copy is the only
+// dQ output (the caller passes its dQ as dq32 and no dQ).
 template <typename TIn>
-__global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
+__global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
     float* __restrict__ apre, const float* __restrict__ fwd_records,
@@ -129,6 +141,8 @@ __global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
     unsigned char* Vs = Ks + G::kRBytes;
     unsigned char* Gs = Vs + G::kRBytes;
     unsigned char* Ms = Gs + G::kRBytes;
+    unsigned char* D32s = Ms + G::kMBytes;
+    using T32 = OutTile<float, kBS, kBC>;
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -197,9 +211,33 @@ __global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
 
     const int subs = tile / kBC;
     float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS;
+    // The previous sub-chunk's gradient tiles are stored after the first
+    // barrier of the next one (and after the loop).
+    // The fp32 tile's 16-byte chunks go to dq32 as they are and, for bf16
+    // tokens, to dQ as 8-byte bf16 chunks (chunk q holds elements 4 q .. 4 q + 3
+    // of the row-major tile).
+    auto flush = [&](int r0) {
+        typename T32::template Chunks<kThreads> c32;
+        T32::template read<kThreads>(D32s, c32);
+        if constexpr (!kSplit) {
+            if (dQ) {
+#pragma unroll
+                for (int i = 0; i < T32::template Chunks<kThreads>::kPer; ++i) {
+                    const int qi = tid + i * kThreads;
+                    const uint4 x = c32.x[i];
+                    __builtin_amdgcn_raw_buffer_store_b64(
+                        u32x2{pack2(__uint_as_float(x.x), __uint_as_float(x.y)),
+                              pack2(__uint_as_float(x.z), __uint_as_float(x.w))},
+                        dqr, r0 * kBS * 2 + 8 * qi, 0, kPolicyDefault);
+                }
+            }
+        }
+        T32::template write<kPolicyDefault, kThreads>(c32, d32r, r0);
+    };
     stage_load(0);
     load_q(0);
-    for (int r0 = 0; r0 < rows; r0 += kBC) {
+    int r0 = 0;
+    for (; r0 < rows; r0 += kBC) {
         __syncthreads();
         stage_store();
         float qc[2][4];
@@ -209,6 +247,13 @@ __global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
             for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
         stage_load(r0 + kBC);  // past the tile: zeros, never used
         load_q(r0 + kBC);
+        // After the prefetch: a wait for those loads then leaves these stores
+        // in flight (one counter covers both, in issue order).  Unconditional:
+        // at r0 = 0 the offsets are negative, outside the buffer ranges, and
+        // the stores are dropped.  With `if (r0 > 0)` the compiler peeled the
+        // first iteration, and the bf16 build of that peel returned wrong dQ
+        // rows 16..31 (tests/test_gpu_causal_bwd.py covers it).
+        flush(r0 - kBC);
         if (gq == 0) ap[(r0 / kBC) * kBS + 16 * w + lr] = a0;
         __syncthreads();
 
@@ -289,9 +334,7 @@ __global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const float dqv = rv[bi][rr] * u[bi][rr];
-                const int elem = (r0 + 16 * bi + 4 * gq + rr) * kBS + 16 * w + lr;
-                if (dQ) store1<TIn>(dqr, elem, dqv);
-                store1<float>(d32r, elem, dqv);
+                T32::put1(D32s, 16 * bi + 4 * gq + rr, 16 * w + lr, dqv);
                 ypart += -wv[bi][rr] * dqv;
             }
 
@@ -312,6 +355,8 @@ __global__ __launch_bounds__(kThreads, 3) void causal_bwd_dq_mfma_kernel(
             b0t[cb] = mfma3<kSplit>(vh, vl, kh, kl, b0t[cb]);
         }
     }
+    __syncthreads();
+    if (r0 > 0) flush(r0 - kBC);
 
     // Suffix totals of this tile: Z[s][c] (record layout B[s][c]) and Y[s].
     float* br = bwd_records + (n * tiles + ti) * rec;
@@ -625,6 +670,8 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
                                      float* bwd_records, const Problem& p, hipStream_t stream) {
     if (!causal_bwd_mfma_supported(p.S, p.d) || p.tile % kBC != 0) return hipErrorInvalidValue;
+    // fp32: dQ is written only as the fp32 copy (pass the caller's dQ as dq32).
+    if (p.dtype != RACE_BF16 && dQ) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     if (p.dtype == RACE_BF16) {
         using G = BwdGeo<bf16_t>;

@@ -176,60 +176,6 @@ struct KVStage {
     }
 };
 
-// The output tile of one sub-chunk in LDS: [C][D] elements of TIn, row r a run
-// of D * sizeof(TIn) / 16 chunks of 16 bytes with chunk u stored at u ^ (r mod
-// the chunk count, at most 16).  The accumulator-layout writes (16 rows, 4
-// values each) and the row-contiguous reads of the flush both meet every bank
-// once per 128 bytes.
-template <typename TIn, int D, int C>
-struct OutTile {
-    static constexpr int kRowBytes = D * int(sizeof(TIn));
-    static constexpr int kChunks = kRowBytes / 16;
-    static constexpr int kMask = (kChunks < 16 ? kChunks : 16) - 1;
-    __device__ __forceinline__ static int at(int row, int byte) {
-        return row * kRowBytes + 16 * ((byte >> 4) ^ (row & kMask)) + (byte & 15);
-    }
-    // Values [row][col .. col + 3] (col % 4 == 0) from the accumulator layout.
-    __device__ __forceinline__ static void put(unsigned char* t, int row, int col, const f32x4& x) {
-        unsigned char* p = t + at(row, col * int(sizeof(TIn)));
-        if constexpr (std::is_same<TIn, float>::value) {
-            *reinterpret_cast<f32x4*>(p) = x;
-        } else {
-            *reinterpret_cast<uint2*>(p) = make_uint2(pack2(x[0], x[1]), pack2(x[2], x[3]));
-        }
-    }
-    // Values [row][col .. col + 3] (col % 4 == 0) as floats.
-    __device__ __forceinline__ static f32x4 get4(const unsigned char* t, int row, int col) {
-        const unsigned char* p = t + at(row, col * int(sizeof(TIn)));
-        if constexpr (std::is_same<TIn, float>::value) {
-            return *reinterpret_cast<const f32x4*>(p);
-        } else {
-            const uint2 u = *reinterpret_cast<const uint2*>(p);
-            return f32x4{lo_half(u.x), hi_half(u.x), lo_half(u.y), hi_half(u.y)};
-        }
-    }
-    // 16-byte chunk q (row-major over the tile) to or from its swizzled place.
-    __device__ __forceinline__ static int chunk_at(int q) {
-        const int row = q / kChunks, u = q % kChunks;
-        return row * kRowBytes + 16 * (u ^ (row & kMask));
-    }
-    // Store the tile to rows r0 .. r0 + C - 1 of `o` (rows past the tile are
-    // dropped by the buffer range), 16 bytes per thread and step.
-    template <int P, int NT>
-    __device__ __forceinline__ static void flush(const unsigned char* t, __amdgpu_buffer_rsrc_t o,
-                                                 int r0) {
-        constexpr int kTotal = C * kChunks;
-#pragma unroll
-        for (int i = 0; i < (kTotal + NT - 1) / NT; ++i) {
-            const int q = int(threadIdx.x) + i * NT;
-            if (kTotal % NT != 0 && q >= kTotal) break;
-            const uint4 x = *reinterpret_cast<const uint4*>(t + chunk_at(q));
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), o,
-                                                   r0 * kRowBytes + 16 * q, 0, P);
-        }
-    }
-};
-
 // ---------------------------------------------------------------------------
 // K1: per (tile, stream) totals B_tile = K^T V and A_tile = colsum(K) into the
 // tile record (B [S][D] then A [S]).  Wave w owns the V columns of c-blocks
@@ -418,10 +364,15 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
 
     // One sub-chunk from the raw registers `st` / `qr`, which are then
     // refilled with the next sub-chunk (a deeper prefetch measured slower).
-    // The previous sub-chunk's output tile is flushed after the first barrier.
+    // The previous sub-chunk's output tile is flushed after the first barrier
+    // (measured: issuing it after the prefetch instead was slower at cfg5).
     auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy, NW>& st, QRegs& qr, int r0) {
         __syncthreads();
-        if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
+        // Unconditional: at r0 = 0 the offsets are negative, outside the
+        // buffer range, so those stores are dropped.  (A conditional flush
+        // gives the compiler a peeled first iteration; in the backward's bf16
+        // dQ kernel that peel produced wrong values.)
+        OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
         st.store(Ks, Vs, nullptr);
         f32x4 qc[SBW][NBI];
         if constexpr (kQStage) {

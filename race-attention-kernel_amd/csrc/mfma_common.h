@@ -237,5 +237,92 @@ __device__ __forceinline__ bf16x8 tril_frag(int off, int g, int lr) {
     return f;
 }
 
+// A token-row tile in LDS staged between global memory and the accumulator
+// layout: [C][D] elements of TIn, row r a run of D * sizeof(TIn) / 16 chunks
+// of 16 bytes with chunk u stored at u ^ (r mod the chunk count, at most 16).
+// Accumulator-layout accesses (16 rows, 4 values each, or 4 rows of 16 single
+// values) and the row-contiguous transfers both spread over the banks, and the
+// global side moves whole rows: 16 bytes per thread, consecutive threads on
+// consecutive bytes.
+template <typename TIn, int D, int C>
+struct OutTile {
+    static constexpr int kRowBytes = D * int(sizeof(TIn));
+    static constexpr int kChunks = kRowBytes / 16;
+    static constexpr int kMask = (kChunks < 16 ? kChunks : 16) - 1;
+    __device__ __forceinline__ static int at(int row, int byte) {
+        return row * kRowBytes + 16 * ((byte >> 4) ^ (row & kMask)) + (byte & 15);
+    }
+    // Values [row][col .. col + 3] (col % 4 == 0) from the accumulator layout.
+    __device__ __forceinline__ static void put(unsigned char* t, int row, int col, const f32x4& x) {
+        unsigned char* p = t + at(row, col * int(sizeof(TIn)));
+        if constexpr (std::is_same<TIn, float>::value) {
+            *reinterpret_cast<f32x4*>(p) = x;
+        } else {
+            *reinterpret_cast<uint2*>(p) = make_uint2(pack2(x[0], x[1]), pack2(x[2], x[3]));
+        }
+    }
+    // One value at [row][col].
+    __device__ __forceinline__ static void put1(unsigned char* t, int row, int col, float x) {
+        unsigned char* p = t + at(row, col * int(sizeof(TIn)));
+        if constexpr (std::is_same<TIn, float>::value) {
+            *reinterpret_cast<float*>(p) = x;
+        } else {
+            *reinterpret_cast<uint16_t*>(p) = uint16_t(pack2(x, 0.f) & 0xffffu);
+        }
+    }
+    // Values [row][col .. col + 3] (col % 4 == 0) as floats.
+    __device__ __forceinline__ static f32x4 get4(const unsigned char* t, int row, int col) {
+        const unsigned char* p = t + at(row, col * int(sizeof(TIn)));
+        if constexpr (std::is_same<TIn, float>::value) {
+            return *reinterpret_cast<const f32x4*>(p);
+        } else {
+            const uint2 u = *reinterpret_cast<const uint2*>(p);
+            return f32x4{lo_half(u.x), hi_half(u.x), lo_half(u.y), hi_half(u.y)};
+        }
+    }
+    // 16-byte chunk q (row-major over the tile) to or from its swizzled place.
+    __device__ __forceinline__ static int chunk_at(int q) {
+        const int row = q / kChunks, u = q % kChunks;
+        return row * kRowBytes + 16 * (u ^ (row & kMask));
+    }
+    // A thread's chunks of the tile (NT threads): chunk q = threadIdx.x + i NT.
+    template <int NT>
+    struct Chunks {
+        static constexpr int kTotal = C * kChunks;
+        static constexpr int kPer = (kTotal + NT - 1) / NT;
+        uint4 x[kPer];
+    };
+    template <int NT>
+    __device__ __forceinline__ static void read(const unsigned char* t, Chunks<NT>& c) {
+#pragma unroll
+        for (int i = 0; i < Chunks<NT>::kPer; ++i) {
+            const int q = int(threadIdx.x) + i * NT;
+            if (Chunks<NT>::kTotal % NT != 0 && q >= Chunks<NT>::kTotal) break;
+            c.x[i] = *reinterpret_cast<const uint4*>(t + chunk_at(q));
+        }
+    }
+    // Store chunks to rows r0 .. r0 + C - 1 of `o` (rows past the tile are
+    // dropped by the buffer range), 16 bytes per thread and step.
+    template <int P, int NT>
+    __device__ __forceinline__ static void write(const Chunks<NT>& c, __amdgpu_buffer_rsrc_t o, int r0) {
+#pragma unroll
+        for (int i = 0; i < Chunks<NT>::kPer; ++i) {
+            const int q = int(threadIdx.x) + i * NT;
+            if (Chunks<NT>::kTotal % NT != 0 && q >= Chunks<NT>::kTotal) break;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, c.x[i]), o,
+                                                   r0 * kRowBytes + 16 * q, 0, P);
+        }
+    }
+    // The whole tile: every chunk is read before any is stored, so no store's
+    // data registers are reused by a later read of the same flush.
+    template <int P, int NT>
+    __device__ __forceinline__ static void flush(const unsigned char* t, __amdgpu_buffer_rsrc_t o,
+                                                 int r0) {
+        Chunks<NT> c;
+        read<NT>(t, c);
+        write<P, NT>(c, o, r0);
+    }
+};
+
 }  // namespace mfma
 }  // namespace race

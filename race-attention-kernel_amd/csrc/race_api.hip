@@ -575,6 +575,13 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     float* bwd_rec = fwd_rec + l.fwd;
     float* apre = bwd_rec + l.bwd;
     float* dq32 = apre + l.apre;
+    // B3 reads dQ back in fp32.  An fp32 dQ is that copy: B1 writes it once,
+    // into the caller's buffer, and B3 reads it from there.
+    void* dq_out = dQ;
+    if (dQ && p.dtype == RACE_F32) {
+        dq32 = static_cast<float*>(dQ);
+        dq_out = nullptr;
+    }
 
     // Prefix state at every tile start (the forward's tile totals and scan).
     RACE_TRY(marks->mark(stream));
@@ -586,11 +593,11 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     RACE_TRY(launch_tile_scan(fwd_rec, nullptr, p, stream));
     RACE_TRY(marks->mark(stream));
     if (use_mfma)
-        RACE_TRY(launch_causal_bwd_dq_mfma(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec,
-                                           p, stream));
+        RACE_TRY(launch_causal_bwd_dq_mfma(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec,
+                                           bwd_rec, p, stream));
     else
-        RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dQ, dq32, apre, fwd_rec, bwd_rec, p,
-                                      C, stream));
+        RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec, bwd_rec,
+                                      p, C, stream));
     RACE_TRY(marks->mark(stream));
     if (!dK && !dV) return RACE_SUCCESS;
     RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));

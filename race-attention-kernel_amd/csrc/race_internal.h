@@ -153,7 +153,8 @@ hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, co
                                  int C, hipStream_t stream);
 
 // Matrix-core kernels of the causal backward (mfma_bwd.hip): S = d = 64,
-// 32-token sub-chunks, the same buffers as the vector-ALU kernels.
+// 32-token sub-chunks, the same buffers as the vector-ALU kernels.  With fp32
+// tokens the dQ kernel writes dQ only through dq32 (dQ must be null).
 bool causal_bwd_mfma_supported(int S, int d);
 hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
