@@ -316,6 +316,21 @@ race_status race_alg1_fwd(const void* q, const void* k, const void* v, const flo
                           const race_alg1_shape* shape, int32_t tile_tokens, int32_t variant,
                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* race_alg1_fwd continued from a carried state: init_state [BH][S*D + S]
+ * fp32 (B then A, the final_state layout) holds the sums of Phi(k) (x) v and
+ * Phi(k) over all earlier tokens, and every output of this call is
+ * (Phi(q_t) . (B0 + B_t)) / (Phi(q_t) . (A0 + A_t)) with A_t, B_t the inclusive
+ * sums over this call's tokens.  final_state (nullable) receives the state
+ * after them and may equal init_state.  The reference hands final_state off
+ * for incremental generation (race_causal_fwd.h:20-21) but has no launcher
+ * that takes it back; this one seeds the tile scan with it.  Workspace as for
+ * race_alg1_fwd. */
+race_status race_alg1_fwd_carry(const void* q, const void* k, const void* v, const float* W,
+                                const float* beta, void* out, const float* init_state,
+                                float* final_state, const race_alg1_shape* shape,
+                                int32_t tile_tokens, int32_t variant, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
+
 /* race_alg1_fwd with hipEventRecord marks around every launch, as
  * race_fwd_profiled.  A profiling aid with no counterpart in the reference. */
 race_status race_alg1_fwd_profiled(const void* q, const void* k, const void* v, const float* W,

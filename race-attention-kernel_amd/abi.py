@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "race_alg1_select_tile_tokens",
     "race_alg1_workspace_bytes",
     "race_alg1_fwd",
+    "race_alg1_fwd_carry",
     "race_alg1_fwd_profiled",
 )
 
@@ -118,6 +119,7 @@ def lib() -> ctypes.CDLL:
         L.race_alg1_workspace_bytes.argtypes = [a1, i32, i32, ctypes.POINTER(sz), ctypes.POINTER(i64),
                                                 ctypes.POINTER(i64)]
         L.race_alg1_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, a1, i32, i32, vp, sz, vp]
+        L.race_alg1_fwd_carry.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, a1, i32, i32, vp, sz, vp]
         L.race_alg1_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, a1, i32, i32, vp, sz, vp,
                                              ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         for name in EXPORTED_SYMBOLS[2:]:
@@ -292,6 +294,14 @@ def alg1_fwd(q: int, k: int, v: int, W: int, beta: int, out: int, final_state: i
     """race_alg1_fwd on raw device addresses; returns the status."""
     return lib().race_alg1_fwd(q, k, v, W, beta, out, final_state, ctypes.byref(sh), tile_tokens,
                                variant, workspace, workspace_bytes, stream)
+
+
+def alg1_fwd_carry(q: int, k: int, v: int, W: int, beta: int, out: int, init_state: int,
+                   final_state: int | None, sh: RaceAlg1Shape, tile_tokens: int, variant: int,
+                   workspace: int | None, workspace_bytes: int, stream: int) -> int:
+    """race_alg1_fwd_carry on raw device addresses; returns the status."""
+    return lib().race_alg1_fwd_carry(q, k, v, W, beta, out, init_state, final_state, ctypes.byref(sh),
+                                     tile_tokens, variant, workspace, workspace_bytes, stream)
 
 
 def alg1_fwd_profiled(q, k, v, W, beta, out, final_state, sh: RaceAlg1Shape, tile_tokens: int,

@@ -8,6 +8,8 @@ the C ABI (race_alg1_fwd):
     forward(q, k, v, W, beta, tile_tokens=0, tensor_cores=False) -> o
     forward_debug(q, k, v, W, beta, tile_tokens=0, tensor_cores=False)
         -> (o, prefix_A, prefix_B, final_A, final_B, tile_tokens)
+    forward_carry(q, k, v, W, beta, state_A, state_B, tile_tokens=0, tensor_cores=False)
+        -> (o, final_A, final_B)      (no counterpart in the reference binding)
     sub_chunk_tokens(head_dim, num_planes, tensor_cores=False) -> C
     select_tile_tokens(batch_heads, seq_len, head_dim, num_planes, num_tables,
                        tensor_cores=False) -> T_blk
@@ -48,6 +50,19 @@ def forward_debug(q, k, v, W, beta, tile_tokens: int = 0, tensor_cores: bool = F
     final_A [B, H, L, R], final_B [B, H, L, R, d], tile_tokens): the exclusive
     prefix state at every tile start and the state after all T tokens (fp32)."""
     return _lib.ext().alg1_forward_debug(q, k, v, W, beta, int(tile_tokens), bool(tensor_cores))
+
+
+def forward_carry(q, k, v, W, beta, state_A, state_B, tile_tokens: int = 0, tensor_cores: bool = False):
+    """(o, final_A, final_B): the forward of these tokens continued from a carried
+    state, (state_A [B, H, L, R], state_B [B, H, L, R, d]) fp32 as forward_debug
+    returns final_A, final_B for the earlier tokens.  Every output sees the sums
+    over the earlier tokens plus those of this call up to itself, so splitting a
+    sequence anywhere gives the unsplit outputs; the returned state continues
+    the next call.  The reference hands its final state off for incremental
+    generation (race_causal_fwd.h:20-21) without a function that takes it back;
+    this is that function."""
+    return _lib.ext().alg1_forward_carry(q, k, v, W, beta, state_A, state_B, int(tile_tokens),
+                                         bool(tensor_cores))
 
 
 def sub_chunk_tokens(head_dim: int, num_planes: int, tensor_cores: bool = False) -> int:

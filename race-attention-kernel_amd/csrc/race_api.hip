@@ -739,7 +739,7 @@ race_status alg1_problem(const race_alg1_shape* sh, int32_t variant, int32_t til
 }
 
 race_status alg1_fwd_impl(const void* q, const void* k, const void* v, const float* W,
-                          const float* beta, void* out, float* final_state,
+                          const float* beta, void* out, const float* init, float* final_state,
                           const race_alg1_shape* sh, int32_t tile_tokens, int32_t variant,
                           void* workspace, size_t workspace_bytes, hipStream_t stream,
                           Marks* marks) {
@@ -747,9 +747,14 @@ race_status alg1_fwd_impl(const void* q, const void* k, const void* v, const flo
     const race_status st = alg1_problem(sh, variant, tile_tokens, &p);
     if (st != RACE_SUCCESS) return st;
     if (final_state && !aligned16(final_state)) return RACE_ERROR_INVALID_VALUE;
+    if (init && !aligned16(init)) return RACE_ERROR_INVALID_VALUE;
+    p.init = init;
     if (p.N == 0 || p.T == 0) {
         RACE_TRY(marks->mark(stream));
-        RACE_TRY(zero_fill(final_state, p.N * state_floats(p.S, p.d), stream));
+        if (init)
+            RACE_TRY(copy_floats(init, final_state, p.N * state_floats(p.S, p.d), stream));
+        else
+            RACE_TRY(zero_fill(final_state, p.N * state_floats(p.S, p.d), stream));
         return marks->mark(stream);
     }
     if (!q || !k || !v || !W || !beta || !out) return RACE_ERROR_INVALID_VALUE;
@@ -823,8 +828,19 @@ race_status race_alg1_fwd(const void* q, const void* k, const void* v, const flo
                           const race_alg1_shape* shape, int32_t tile_tokens, int32_t variant,
                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
     Marks none;
-    return alg1_fwd_impl(q, k, v, W, beta, out, final_state, shape, tile_tokens, variant,
+    return alg1_fwd_impl(q, k, v, W, beta, out, nullptr, final_state, shape, tile_tokens, variant,
                          workspace, workspace_bytes, stream, &none);
+}
+
+race_status race_alg1_fwd_carry(const void* q, const void* k, const void* v, const float* W,
+                                const float* beta, void* out, const float* init_state,
+                                float* final_state, const race_alg1_shape* shape,
+                                int32_t tile_tokens, int32_t variant, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+    if (!init_state) return RACE_ERROR_INVALID_VALUE;
+    Marks none;
+    return alg1_fwd_impl(q, k, v, W, beta, out, init_state, final_state, shape, tile_tokens,
+                         variant, workspace, workspace_bytes, stream, &none);
 }
 
 race_status race_alg1_fwd_profiled(const void* q, const void* k, const void* v, const float* W,
@@ -837,7 +853,7 @@ race_status race_alg1_fwd_profiled(const void* q, const void* k, const void* v, 
     Marks marks;
     marks.events = events;
     marks.max = max_events;
-    const race_status st = alg1_fwd_impl(q, k, v, W, beta, out, final_state, shape, tile_tokens,
+    const race_status st = alg1_fwd_impl(q, k, v, W, beta, out, nullptr, final_state, shape, tile_tokens,
                                          variant, workspace, workspace_bytes, stream, &marks);
     *n_events = marks.n;
     return st;

@@ -16,6 +16,8 @@
 //   alg1_forward(q, k, v, W, beta, tile_tokens=0, tensor_cores=False) -> out
 //   alg1_forward_debug(q, k, v, W, beta, tile_tokens=0, tensor_cores=False)
 //       -> (out, prefix_A, prefix_B, final_A, final_B, tile_tokens)
+//   alg1_forward_carry(q, k, v, W, beta, state_A, state_B, tile_tokens=0, tensor_cores=False)
+//       -> (out, final_A, final_B): continued from (state_A, state_B)
 //   alg1_sub_chunk_tokens / alg1_select_tile_tokens / alg1_output_lds_bytes /
 //   alg1_fits_on_device: the queries of the reference's causal v2 binding
 //       (src/causal_v2/kernels/torch_binding.cpp:1-25)
@@ -383,7 +385,7 @@ struct Alg1Result {
 
 Alg1Result alg1_run(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                     const at::Tensor& W, const at::Tensor& beta, int64_t tile_tokens,
-                    bool tensor_cores, bool want_final) {
+                    bool tensor_cores, bool want_final, const at::Tensor* init = nullptr) {
     const race_alg1_shape sh = alg1_validate(q, k, v, W, beta);
     const c10::DeviceGuard guard(q.device());
     Alg1Result r;
@@ -407,12 +409,48 @@ Alg1Result alg1_run(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
     const int64_t S = int64_t(sh.num_tables) << sh.num_planes;
     if (want_final) r.final_state = at::empty({sh.batch_heads, S * sh.head_dim + S}, fopt);
     const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
-    check_status(race_alg1_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), W.data_ptr<float>(),
-                               beta_dev.data_ptr<float>(), r.out.data_ptr(),
-                               want_final ? r.final_state.data_ptr<float>() : nullptr, &sh, r.tile,
-                               variant, r.workspace.data_ptr(), bytes, stream),
-                 "race_alg1_fwd");
+    float* fin = want_final ? r.final_state.data_ptr<float>() : nullptr;
+    if (init) {
+        check_status(race_alg1_fwd_carry(q.data_ptr(), k.data_ptr(), v.data_ptr(), W.data_ptr<float>(),
+                                         beta_dev.data_ptr<float>(), r.out.data_ptr(),
+                                         init->data_ptr<float>(), fin, &sh, r.tile, variant,
+                                         r.workspace.data_ptr(), bytes, stream),
+                     "race_alg1_fwd_carry");
+    } else {
+        check_status(race_alg1_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), W.data_ptr<float>(),
+                                   beta_dev.data_ptr<float>(), r.out.data_ptr(), fin, &sh, r.tile,
+                                   variant, r.workspace.data_ptr(), bytes, stream),
+                     "race_alg1_fwd");
+    }
     return r;
+}
+
+// Causal Algorithm 1 continued from a carried state (final_A [B, H, L, R] and
+// final_B [B, H, L, R, D] fp32, as forward_debug returns them) -> (out,
+// final_A, final_B) after these tokens.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> alg1_forward_carry(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& W,
+    const at::Tensor& beta, const at::Tensor& state_A, const at::Tensor& state_B,
+    int64_t tile_tokens, bool tensor_cores) {
+    const race_alg1_shape sh = alg1_validate(q, k, v, W, beta);
+    const int64_t B = q.size(0), H = q.size(1), D = q.size(3);
+    const int64_t L = W.size(0), R = int64_t(1) << W.size(1), S = L * R;
+    TORCH_CHECK(state_A.is_cuda() && state_A.scalar_type() == at::kFloat && state_A.device() == q.device() &&
+                    state_A.sizes() == at::IntArrayRef({B, H, L, R}),
+                "state_A must be a float32 [B, H, L, R] tensor on the device of q");
+    TORCH_CHECK(state_B.is_cuda() && state_B.scalar_type() == at::kFloat && state_B.device() == q.device() &&
+                    state_B.sizes() == at::IntArrayRef({B, H, L, R, D}),
+                "state_B must be a float32 [B, H, L, R, D] tensor on the device of q");
+    const c10::DeviceGuard guard(q.device());
+    // The ABI's layout per stream: B [S][D] then A [S].
+    const at::Tensor init = at::cat({state_B.reshape({B * H, S * D}), state_A.reshape({B * H, S})}, 1)
+                                .contiguous();
+    if (sh.batch_heads == 0 || sh.seq_len == 0)
+        return {at::empty_like(q), state_A.clone(), state_B.clone()};
+    Alg1Result r = alg1_run(q, k, v, W, beta, tile_tokens, tensor_cores, true, &init);
+    const at::Tensor fin = r.final_state.view({B, H, S * D + S});
+    return {r.out, fin.narrow(2, S * D, S).reshape({B, H, L, R}),
+            fin.narrow(2, 0, S * D).reshape({B, H, L, R, D})};
 }
 
 at::Tensor alg1_forward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
@@ -509,6 +547,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Causal Algorithm 1 with hashing: o = race_causal(q, k, v, W, beta)", py::arg("q"),
           py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("tile_tokens") = 0,
           py::arg("tensor_cores") = false);
+    m.def("alg1_forward_carry", &alg1_forward_carry,
+          "alg1_forward continued from a carried state -> (out, final_A, final_B)", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("state_A"),
+          py::arg("state_B"), py::arg("tile_tokens") = 0, py::arg("tensor_cores") = false);
     m.def("alg1_forward_debug", &alg1_forward_debug,
           "alg1_forward plus (prefix_A, prefix_B, final_A, final_B, tile_tokens)", py::arg("q"),
           py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("tile_tokens") = 0,

@@ -285,6 +285,10 @@ def test_alg1_invalid_arguments_are_rejected_before_any_launch(race):
     # Bad variant or tile.
     assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, good, 64, 3, 64, 1 << 30, 0) == inv
     assert abi.alg1_fwd(16, 16, 16, 16, 16, 16, None, good, 96, 0, 64, 1 << 30, 0) == inv
+    # The continuation needs its carried state, 16-byte aligned.
+    assert abi.alg1_fwd_carry(16, 16, 16, 16, 16, 16, 0, 16, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd_carry(16, 16, 16, 16, 16, 16, 24, 16, good, 64, 0, 64, 1 << 30, 0) == inv
+    assert abi.alg1_fwd_carry(16, 16, 16, 16, 16, 16, 16, 16, bad, 64, 0, 64, 1 << 30, 0) == inv
 
 
 def test_alg1_torch_binding_validates_inputs_on_the_host(race, ext):

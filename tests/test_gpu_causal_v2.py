@@ -247,6 +247,45 @@ def test_debug_prefix_states_match_oracle(race, oracle, variant, D, P, L, T, til
                                                    tensor_cores=tc(variant)))
 
 
+@pytest.mark.parametrize("T0, T1, tile", [(0, 65, 0), (63, 1, 0), (777, 300, 64), (2049, 4000, 0),
+                                          (5000, 1, 128), (64, 64, 64)])
+@pytest.mark.parametrize("D, P, L", [(64, 4, 4), (128, 5, 2), (64, 2, 3)])
+def test_carried_state_continues_the_sequence(race, oracle, variant, D, P, L, T0, T1, tile):
+    # The hand-off: forward_debug's final state over the first T0 tokens, then
+    # forward_carry over the next T1 from it.  The continued outputs and the
+    # state after them are the unsplit run's (fp64 oracle over all T0 + T1).
+    skip_unless_fits(race, D, P, L, variant)
+    say("alg1 carry", variant, D, P, L, T0, T1, tile)
+    q, k, v, W = make_inputs(T0 * 3 + T1 + D + P + L, 1, 2, T0 + T1, D, L, P)
+    beta = 1.0
+    bt = torch.tensor(beta)
+    head = [x[:, :, :T0].contiguous() for x in (q, k, v)]
+    tail = [x[:, :, T0:].contiguous() for x in (q, k, v)]
+    _, _, _, fA, fB, _ = race.causal_v2.forward_debug(*head, W, bt, tile_tokens=tile, tensor_cores=tc(variant))
+    out, gA, gB = race.causal_v2.forward_carry(*tail, W, bt, fA, fB, tile_tokens=tile, tensor_cores=tc(variant))
+    assert out.shape == tail[0].shape and out.dtype == torch.bfloat16
+    ref, _, fin = reference(oracle, q, k, v, W, beta, tile=64)
+    assert_within_floor(out, np.ascontiguousarray(ref[:, :, T0:]), tail[2], beta, variant)
+    R, S = 1 << P, L << P
+    vmax = v.float().abs().amax(dim=(2, 3)).double().cpu().numpy().reshape(1, 2, 1, 1)
+    assert_states_close(gA, gB, fin[..., S * D:].reshape(1, 2, L, R), fin[..., : S * D].reshape(1, 2, L, R, D),
+                        vmax[..., None], T0 + T1, variant)
+    # A zero state is no state: the carry from zeros is the plain forward.
+    z, _, _ = race.causal_v2.forward_carry(*tail, W, bt, torch.zeros_like(fA), torch.zeros_like(fB),
+                                           tile_tokens=tile, tensor_cores=tc(variant))
+    assert torch.equal(z, race.causal_v2.forward(*tail, W, bt, tile_tokens=tile, tensor_cores=tc(variant)))
+
+
+def test_carry_rejects_bad_states(race, variant):
+    q, k, v, W = make_inputs(3, 1, 2, 10, 64, 2, 3)
+    A = torch.zeros(1, 2, 2, 8, device="cuda")
+    Bs = torch.zeros(1, 2, 2, 8, 64, device="cuda")
+    with pytest.raises(RuntimeError, match="state_A"):
+        race.causal_v2.forward_carry(q, k, v, W, torch.tensor(1.0), A[:, :, :1], Bs, tensor_cores=tc(variant))
+    with pytest.raises(RuntimeError, match="state_B"):
+        race.causal_v2.forward_carry(q, k, v, W, torch.tensor(1.0), A, Bs.double(), tensor_cores=tc(variant))
+
+
 def test_other_streams_cannot_leak_into_a_stream(race, oracle, variant):
     T = 3000
     q, k, v, W = make_inputs(14, 1, 3, T, 64, 4, 4)
