@@ -119,6 +119,7 @@ __global__ __launch_bounds__(kThreads) void tile_outer_sums_kernel(
 // thread reads its element before the group barrier and only the last group
 // writes `state`, so `state` may be `init`.
 constexpr int kScanGroupsMax = 8;
+constexpr int kScanRegTiles = 16;  // tiles per group held in registers
 
 __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__ records,
                                                              float* state, const float* init,
@@ -136,6 +137,27 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(float* __restrict__
     const int64_t step = reverse ? -rec : rec;
     float* r = records + n * tiles * rec + (reverse ? (tiles - 1) * rec : 0) + e;
     float run = (init && e < used) ? init[n * used + e] : 0.f;
+    if (groups > 1 && per <= kScanRegTiles) {
+        // A group of at most kScanRegTiles tiles stays in registers between
+        // its sum and its prefix pass: the records are read once.
+        float v[kScanRegTiles];
+        float sum = 0.f;
+        const int cnt = e < used ? int(max<int64_t>(0, t_end - t_begin)) : 0;
+#pragma unroll
+        for (int u = 0; u < kScanRegTiles; ++u) v[u] = u < cnt ? r[(t_begin + u) * step] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kScanRegTiles; ++u) sum += v[u];
+        gsum[gi * elems + el] = sum;
+        __syncthreads();
+        for (int j = 0; j < gi; ++j) run += gsum[j * elems + el];
+#pragma unroll
+        for (int u = 0; u < kScanRegTiles; ++u) {
+            if (u < cnt) r[(t_begin + u) * step] = run;
+            run += v[u];
+        }
+        if (e < used && state && gi == groups - 1) state[n * used + e] = run;
+        return;
+    }
     if (groups > 1) {
         float sum = 0.f;
         if (e < used) {
