@@ -257,6 +257,111 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
     }
 }
 
+// Maps with a 64-wide contraction (Wa = 64: every map of the S = d = 64
+// shapes).  Each thread owns 8 tokens x 4 columns, so three 16-byte LDS reads
+// feed 32 FMAs (4 x 4 tiles need two for 16), and the swizzled addresses are
+// computed once per group of four contraction rows.  Blocks of 128 tokens, the
+// same transposed and swizzled token tile as map4_kernel.
+constexpr int kMap64Tokens = 128;
+constexpr int kMap64Blocks = 4;
+
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void map64_kernel(
+    const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
+    int64_t m_stream_stride, int64_t ms_row, int64_t ms_col, const float* __restrict__ bias,
+    int64_t bias_stream_stride, int64_t T, int Wb) {
+    constexpr int Wa = 64;
+    constexpr int TP = kMap64Tokens + 4;                   // pitch of the transposed token tile
+    constexpr int NV = kMap64Tokens * (Wa / 4) / kThreads;  // 16-byte token vectors per thread
+    extern __shared__ float smem[];
+    float* Ms = smem;                  // [64][64]
+    float* xt = Ms + Wa * kSliceCols;  // [64][TP]
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const int c0 = blockIdx.z * kSliceCols;
+    const int ncols = min(kSliceCols, Wb - c0);
+    const float* Mn = M + n * m_stream_stride;
+    for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
+        const int a = e / kSliceCols, c = e - a * kSliceCols;
+        Ms[e] = c < ncols ? Mn[a * ms_row + (c0 + c) * ms_col] : 0.f;
+    }
+    const int tt = tid >> 4, cc = tid & 15;  // tokens 8 tt .. 8 tt + 7, columns 4 cc .. 4 cc + 3
+    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bias && 4 * cc < ncols) {
+        const float* bn = bias + n * bias_stream_stride + c0 + 4 * cc;
+        bv = make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
+                         4 * cc + 3 < ncols ? bn[3] : 0.f);
+    }
+    const TIn* xn = x + n * T * Wa;
+    TIn* on = out + n * T * Wb;
+    const int64_t wg_t0 = int64_t(blockIdx.x) * kMap64Blocks * kMap64Tokens;
+
+    float4 pre[NV];
+    auto fetch = [&](int64_t t0) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            const int i = e >> 4, u = e & 15;
+            pre[m] = t0 + i < T ? load4(xn + (t0 + i) * Wa + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    fetch(wg_t0);
+    for (int blk = 0; blk < kMap64Blocks; ++blk) {
+        const int64_t t0 = wg_t0 + int64_t(blk) * kMap64Tokens;
+        if (t0 >= T) break;
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            const int i = e >> 4, u = e & 15;
+            const int col = i ^ (xsw(4 * u) << 2);  // rows 4u .. 4u+3 share xsw
+            xt[(4 * u + 0) * TP + col] = pre[m].x;
+            xt[(4 * u + 1) * TP + col] = pre[m].y;
+            xt[(4 * u + 2) * TP + col] = pre[m].z;
+            xt[(4 * u + 3) * TP + col] = pre[m].w;
+        }
+        __syncthreads();
+        if (blk + 1 < kMap64Blocks) fetch(t0 + kMap64Tokens);
+        float acc[8][4];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            acc[r][0] = bv.x;
+            acc[r][1] = bv.y;
+            acc[r][2] = bv.z;
+            acc[r][3] = bv.w;
+        }
+        // Rows 4 j .. 4 j + 3 share one swizzle: the group's addresses are
+        // computed once and its four steps unrolled.
+#pragma unroll 2
+        for (int j = 0; j < Wa / 4; ++j) {
+            const int sw = (j & 7) << 2;
+            const float* xa = xt + 4 * j * TP;
+            const int o0 = (8 * tt) ^ sw, o1 = (8 * tt + 4) ^ sw;
+            const float* ma = Ms + 4 * j * kSliceCols + 4 * cc;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 x0 = *reinterpret_cast<const float4*>(xa + k * TP + o0);
+                const float4 x1 = *reinterpret_cast<const float4*>(xa + k * TP + o1);
+                const float4 mv = *reinterpret_cast<const float4*>(ma + k * kSliceCols);
+                const float xr[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const float mc[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr[r], mc[c], acc[r][c]);
+            }
+        }
+        if (4 * cc < ncols) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const int64_t t = t0 + 8 * tt + r;
+                if (t < T) store4(on + t * Wb + c0 + 4 * cc,
+                                  make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
+            }
+        }
+    }
+}
+
 int pow2_at_least(int x) {
     int m = 1;
     while (m < x) m *= 2;
@@ -306,6 +411,7 @@ hipError_t launch_outer_sums4(const void* x, const void* y, float* records, cons
 }
 
 size_t map4_lds_bytes(int Wa) {
+    if (Wa == 64) return size_t(Wa * kSliceCols + Wa * (kMap64Tokens + 4)) * sizeof(float);
     return size_t(Wa * kSliceCols + Wa * (kMapTokens4 + 4)) * sizeof(float);
 }
 
@@ -313,6 +419,21 @@ hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_strea
                        int64_t ms_row, int64_t ms_col, const float* bias,
                        int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
                        hipStream_t stream) {
+    if (Wa == 64) {
+        const int64_t per_wg64 = int64_t(kMap64Blocks) * kMap64Tokens;
+        const dim3 grid64(unsigned((p.T + per_wg64 - 1) / per_wg64), unsigned(p.N),
+                          unsigned((Wb + kSliceCols - 1) / kSliceCols));
+        const size_t lds64 = map4_lds_bytes(64);
+        if (p.dtype == RACE_BF16)
+            map64_kernel<bf16_t><<<grid64, kThreads, lds64, stream>>>(
+                static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), M, m_stream_stride, ms_row,
+                ms_col, bias, bias_stream_stride, p.T, Wb);
+        else
+            map64_kernel<float><<<grid64, kThreads, lds64, stream>>>(
+                static_cast<const float*>(x), static_cast<float*>(out), M, m_stream_stride, ms_row,
+                ms_col, bias, bias_stream_stride, p.T, Wb);
+        return hipGetLastError();
+    }
     const int64_t per_wg = int64_t(kMapBlocks) * kMapTokens4;
     const dim3 grid(unsigned((p.T + per_wg - 1) / per_wg), unsigned(p.N),
                     unsigned((Wb + kSliceCols - 1) / kSliceCols));
