@@ -152,6 +152,116 @@ __global__ __launch_bounds__(kThreads) void outer_sums4_kernel(
     }
 }
 
+// Reductions with Wa = Wb = 64 (every reduction of the S = d = 64 shapes).
+// Threads 0..127 take tokens 0..15 of each staged block of kRedTokens and
+// threads 128..255 tokens 16..31; each owns an 8 x 4 tile of R (rows
+// 8 (u / 16) .., columns 4 (u % 16) .., u = tid % 128), so three 16-byte LDS
+// reads feed 32 FMAs.  The column sums of x are taken once per block, thread
+// tid summing 8 tokens of column tid % 64.  At the end the two halves of R and
+// the four token groups of the column sums are added in a fixed order through
+// LDS, so results stay bitwise reproducible.
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void outer64_kernel(
+    const TIn* __restrict__ x, const TIn* __restrict__ y, float* __restrict__ records, int64_t T,
+    int chunk, int64_t chunks, int64_t rec) {
+    constexpr int W = 64;
+    constexpr int NV = kRedTokens * (2 * W / 4) / kThreads;  // 16-byte vectors per thread and block
+    extern __shared__ float smem[];
+    float* xs = smem;                      // [2][kRedTokens][W]
+    float* ys = xs + 2 * kRedTokens * W;   // [2][kRedTokens][W]
+    float* part = smem;                    // [W][W] + [4][W], after the loop
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y, ci = blockIdx.x;
+    const int64_t t_begin = ci * chunk;
+    const int64_t t_end = min(T, t_begin + chunk);
+    const TIn* xn = x + n * T * W;
+    const TIn* yn = y + n * T * W;
+    const int half = tid >> 7, u = tid & 127;
+    const int a8 = u >> 4, b4 = u & 15;
+    const int ca = tid & 63, cg = tid >> 6;  // column-sum column and token group
+
+    float4 pre[NV];
+    auto fetch = [&](int64_t t0) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            const int i = e >> 5, v = e & 31;  // token, vector (16 of x, then 16 of y)
+            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t0 + i < t_end)
+                val = v < 16 ? load4(xn + (t0 + i) * W + 4 * v) : load4(yn + (t0 + i) * W + 4 * (v - 16));
+            pre[m] = val;
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = tid + m * kThreads;
+            const int i = e >> 5, v = e & 31;
+            if (v < 16)
+                store4(xs + (buf * kRedTokens + i) * W + 4 * v, pre[m]);
+            else
+                store4(ys + (buf * kRedTokens + i) * W + 4 * (v - 16), pre[m]);
+        }
+    };
+
+    float acc[8][4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
+    float csum = 0.f;
+
+    fetch(t_begin);
+    stash(0);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kRedTokens) {
+        const bool more = t0 + kRedTokens < t_end;
+        if (more) fetch(t0 + kRedTokens);
+        const float* xb = xs + (buf * kRedTokens + 16 * half) * W;
+        const float* yb = ys + (buf * kRedTokens + 16 * half) * W;
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const float4 x0 = *reinterpret_cast<const float4*>(xb + i * W + 8 * a8);
+            const float4 x1 = *reinterpret_cast<const float4*>(xb + i * W + 8 * a8 + 4);
+            const float4 yv = *reinterpret_cast<const float4*>(yb + i * W + 4 * b4);
+            const float xr[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float yc[4] = {yv.x, yv.y, yv.z, yv.w};
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr[r], yc[c], acc[r][c]);
+        }
+        const float* xc = xs + (buf * kRedTokens + 8 * cg) * W + ca;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) csum += xc[i * W];
+        if (more) stash(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    // Fixed-order combination: R = half 0 + half 1, colsum = groups 0 + 1 + 2 + 3.
+    float* rp = records + (n * chunks + ci) * rec;
+    float* cs = part + W * W;
+    cs[cg * W + ca] = csum;
+    if (half == 1) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            store4(part + (8 * a8 + r) * W + 4 * b4, make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const float4 o = *reinterpret_cast<const float4*>(part + (8 * a8 + r) * W + 4 * b4);
+            store4(rp + (8 * a8 + r) * W + 4 * b4,
+                   make_float4(acc[r][0] + o.x, acc[r][1] + o.y, acc[r][2] + o.z, acc[r][3] + o.w));
+        }
+    } else if (u < W) {
+        rp[W * W + u] = ((cs[u] + cs[W + u]) + cs[2 * W + u]) + cs[3 * W + u];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Map over kMapBlocks blocks of kMapTokens4 tokens of one stream, for one
 // slice of 64 output columns.  M slice [Wa][64] and the block's tokens,
@@ -374,6 +484,21 @@ bool v4_widths(int Wa, int Wb) { return Wa % 4 == 0 && Wb % 4 == 0; }
 
 hipError_t launch_outer_sums4(const void* x, const void* y, float* records, const Problem& p,
                               int Wa, int Wb, hipStream_t stream) {
+    if (Wa == 64 && Wb == 64) {
+        const dim3 grid64(unsigned(p.tiles), unsigned(p.N));
+        // The double-buffered staging; the final partial sums reuse it.
+        const size_t lds64 = size_t(2 * 2 * kRedTokens * 64) * sizeof(float);
+        static_assert(64 * 64 + 4 * 64 <= 2 * 2 * kRedTokens * 64, "part fits the staging");
+        if (p.dtype == RACE_BF16)
+            outer64_kernel<bf16_t><<<grid64, kThreads, lds64, stream>>>(
+                static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(y), records, p.T, p.tile,
+                p.tiles, p.rec);
+        else
+            outer64_kernel<float><<<grid64, kThreads, lds64, stream>>>(
+                static_cast<const float*>(x), static_cast<const float*>(y), records, p.T, p.tile,
+                p.tiles, p.rec);
+        return hipGetLastError();
+    }
     const int nv = pow2_at_least((kRedTokens * (Wa + Wb) / 4 + kThreads - 1) / kThreads);
     const int nt = pow2_at_least((Wa / 4 * (Wb / 4) + kThreads - 1) / kThreads);
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
