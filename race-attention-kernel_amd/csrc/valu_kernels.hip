@@ -247,19 +247,24 @@ __global__ __launch_bounds__(kThreads) void bwd_finalize_kernel(
     const float* __restrict__ dE_totals, const float* __restrict__ state,
     const float* __restrict__ E, float* __restrict__ dB, float* __restrict__ dA, int64_t rec,
     int S, int d) {
-    const int e = blockIdx.x * kThreads + threadIdx.x;
-    const int64_t n = blockIdx.y;
+    // One workgroup per stream: dB elementwise; dA[s] one row per wave, the
+    // row's products summed by a fixed shuffle tree (d <= 128: two per lane).
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t n = blockIdx.x;
     const float* dE = dE_totals + n * rec;
     const float* A = state + n * (S * d + S) + S * d;
-    if (e < S * d) {
-        dB[n * S * d + e] = dE[e] / (A[e / d] + kEps);
-    } else if (e < S * d + S) {
-        const int s = e - S * d;
-        const float den = A[s] + kEps;
-        const float* En = E + n * S * d + int64_t(s) * d;
+    // Unrolled so that each thread's loads are in flight together rather than
+    // one round trip per element.
+#pragma unroll 8
+    for (int e = tid; e < S * d; e += kThreads) dB[n * S * d + e] = dE[e] / (A[e / d] + kEps);
+    const float* En = E + n * S * d;
+#pragma unroll 4
+    for (int s = w; s < S; s += kThreads / 64) {
         float acc = 0.f;
-        for (int c = 0; c < d; ++c) acc = fmaf(dE[s * d + c], En[c], acc);
-        dA[n * S + s] = -acc / den;
+        for (int c = lane; c < d; c += 64) acc = fmaf(dE[s * d + c], En[int64_t(s) * d + c], acc);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (lane == 0) dA[n * S + s] = -acc / (A[s] + kEps);
     }
 }
 
@@ -463,10 +468,8 @@ hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hip
 
 hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
                                float* dB, float* dA, const Problem& p, hipStream_t stream) {
-    const int used = p.S * p.d + p.S;
-    const dim3 grid(unsigned((used + kThreads - 1) / kThreads), unsigned(p.N));
-    bwd_finalize_kernel<<<grid, kThreads, 0, stream>>>(dE_totals, state, E, dB, dA, p.rec, p.S,
-                                                       p.d);
+    bwd_finalize_kernel<<<dim3(unsigned(p.N)), kThreads, 0, stream>>>(dE_totals, state, E, dB, dA,
+                                                                     p.rec, p.S, p.d);
     return hipGetLastError();
 }
 
