@@ -116,18 +116,14 @@ race_status make_problem(const race_shape* sh, int causal, const race_options* o
 // Workspace regions, in floats, each a multiple of 64 floats.
 struct FwdLayout {
     int64_t records = 0;  // [N][tiles][rec]
-    int64_t totals = 0;   // non-causal: [N][rec]
     int64_t E = 0;        // non-causal: [N][S*d]
-    int64_t total() const { return records + totals + E; }
+    int64_t total() const { return records + E; }
 };
 
 FwdLayout fwd_layout(const Problem& p, int causal) {
     FwdLayout l;
     l.records = p.N * p.tiles * p.rec;
-    if (!causal) {
-        l.totals = p.N * p.rec;
-        l.E = round64(p.N * p.S * p.d);
-    }
+    if (!causal) l.E = round64(p.N * p.S * p.d);
     return l;
 }
 
@@ -318,12 +314,12 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
         return marks->mark(stream);
     }
 
-    float* totals = records + l.records;
-    float* E = totals + l.totals;
+    // The totals go straight to E (and to the state when asked for).
+    float* E = records + l.records;
     RACE_TRY(marks->mark(stream));
     RACE_TRY(outer_sums(probsK, V, records, p, p.S, p.d, stream));
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_tile_reduce(records, totals, state, E, p, stream));
+    RACE_TRY(launch_tile_reduce(records, nullptr, state, E, p, stream));
     RACE_TRY(marks->mark(stream));
     // out = q . E: M[a][c] = E[a*d + c].
     RACE_TRY(token_map(probsQ, out, E, int64_t(p.S) * p.d, p.d, 1, nullptr, 0, p, p.S, p.d,

@@ -210,9 +210,10 @@ __device__ __forceinline__ float sum_over_tiles(const float* __restrict__ r, int
     return sum;
 }
 
-// Totals over tiles (fixed order).  The thread of B element (s, c) also sums
-// A[s] in the same order as the thread of A element s, so E uses exactly the
-// A that is stored.
+// Totals over tiles (fixed order) into whichever of totals (the record
+// layout) and state ([S*d + S]) are given.  The thread of B element (s, c)
+// also sums A[s] in the same order as the thread of A element s, so E uses
+// exactly the A that is stored.
 __global__ __launch_bounds__(kThreads) void tile_reduce_kernel(
     const float* __restrict__ records, float* __restrict__ totals, float* __restrict__ state,
     float* __restrict__ E, int64_t tiles, int64_t rec, int S, int d) {
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void tile_reduce_kernel(
     if (e >= used) return;
     const float* r = records + n * tiles * rec;
     const float sum = sum_over_tiles(r + e, tiles, rec);
-    totals[n * rec + e] = sum;
+    if (totals) totals[n * rec + e] = sum;
     if (state) state[n * used + e] = sum;
     if (E && e < S * d) {
         const int s = e / d;
@@ -241,31 +242,32 @@ __global__ __launch_bounds__(kThreads) void state_to_E_kernel(const float* __res
     E[n * S * d + e] = st[e] / (st[S * d + e / d] + kEps);
 }
 
-// dB = dE / (A + eps); dA[s] = -sum_c dE[s][c] E[s][c] / (A[s] + eps)
-// (the sum over c in order, one thread per s).
+// dB = dE / (A + eps); dA[s] = -sum_c dE[s][c] E[s][c] / (A[s] + eps).
+// One wave per bucket row s (kThreads / 64 rows per workgroup): lanes over
+// the columns c (d <= 128: at most two per lane), every load of the row issued
+// before any result is needed, the row's products summed by a fixed shuffle
+// tree.
 __global__ __launch_bounds__(kThreads) void bwd_finalize_kernel(
     const float* __restrict__ dE_totals, const float* __restrict__ state,
     const float* __restrict__ E, float* __restrict__ dB, float* __restrict__ dA, int64_t rec,
     int S, int d) {
-    // One workgroup per stream: dB elementwise; dA[s] one row per wave, the
-    // row's products summed by a fixed shuffle tree (d <= 128: two per lane).
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int64_t n = blockIdx.x;
-    const float* dE = dE_totals + n * rec;
-    const float* A = state + n * (S * d + S) + S * d;
-    // Unrolled so that each thread's loads are in flight together rather than
-    // one round trip per element.
-#pragma unroll 8
-    for (int e = tid; e < S * d; e += kThreads) dB[n * S * d + e] = dE[e] / (A[e / d] + kEps);
-    const float* En = E + n * S * d;
-#pragma unroll 4
-    for (int s = w; s < S; s += kThreads / 64) {
-        float acc = 0.f;
-        for (int c = lane; c < d; c += 64) acc = fmaf(dE[s * d + c], En[int64_t(s) * d + c], acc);
+    const int lane = threadIdx.x & 63;
+    const int s = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int64_t n = blockIdx.y;
+    if (s >= S) return;
+    const float* dE = dE_totals + n * rec + int64_t(s) * d;
+    const float* En = E + (n * S + s) * d;
+    float* dBn = dB + (n * S + s) * d;
+    const float den = state[n * (S * d + S) + S * d + s] + kEps;
+    const bool lo = lane < d, hi = lane + 64 < d;
+    const float g0 = lo ? dE[lane] : 0.f, e0 = lo ? En[lane] : 0.f;
+    const float g1 = hi ? dE[lane + 64] : 0.f, e1 = hi ? En[lane + 64] : 0.f;
+    if (lo) dBn[lane] = g0 / den;
+    if (hi) dBn[lane + 64] = g1 / den;
+    float acc = fmaf(g1, e1, g0 * e0);
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-        if (lane == 0) dA[n * S + s] = -acc / (A[s] + kEps);
-    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) dA[n * S + s] = -acc / den;
 }
 
 // ---------------------------------------------------------------------------
@@ -468,8 +470,10 @@ hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hip
 
 hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
                                float* dB, float* dA, const Problem& p, hipStream_t stream) {
-    bwd_finalize_kernel<<<dim3(unsigned(p.N)), kThreads, 0, stream>>>(dE_totals, state, E, dB, dA,
-                                                                     p.rec, p.S, p.d);
+    static_assert(kThreads % 64 == 0, "whole waves");
+    const dim3 grid(unsigned((p.S + kThreads / 64 - 1) / (kThreads / 64)), unsigned(p.N));
+    bwd_finalize_kernel<<<grid, kThreads, 0, stream>>>(dE_totals, state, E, dB, dA, p.rec, p.S,
+                                                       p.d);
     return hipGetLastError();
 }
 

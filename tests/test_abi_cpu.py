@@ -69,9 +69,9 @@ def test_workspace_bytes_for_explicit_tiles(race):
     # Ragged T: ceil division.
     st, _, tiles, _ = abi.fwd_workspace_bytes(abi.shape(2, 1025, 4, 16, 64), True, abi.options(512, 1))
     assert st == 0 and tiles == 3
-    # Non-causal adds the totals and E regions.
+    # Non-causal adds the E region.
     st, nc_bytes, _, _ = abi.fwd_workspace_bytes(sh, False, abi.options(1024, abi.RACE_KERNEL_VALU))
-    assert st == 0 and nc_bytes == (8 * 64 * 4160 + 8 * 4160 + 8 * 64 * 64) * 4
+    assert st == 0 and nc_bytes == (8 * 64 * 4160 + 8 * 64 * 64) * 4
     st, bwd_bytes = abi.noncausal_bwd_workspace_bytes(sh, abi.options(1024, 0))
     assert st == 0 and bwd_bytes > nc_bytes
     # Causal backward: forward and suffix records, the running mass per 16
