@@ -13,7 +13,7 @@
 // reduction workgroup owns one chunk of one stream's tokens and writes the
 // chunk's partial sums to a record; the fixed-order reduce over chunks
 // (tile_reduce_kernel) adds them, so results are bitwise reproducible.
-#include "race_internal.h"
+#include "mfma_common.h"
 
 namespace race {
 namespace {
@@ -40,6 +40,29 @@ __device__ __forceinline__ void store4(bf16_t* __restrict__ p, const float4& v) 
     u.x = uint32_t(f32_to_bf16(v.x)) | (uint32_t(f32_to_bf16(v.y)) << 16);
     u.y = uint32_t(f32_to_bf16(v.z)) | (uint32_t(f32_to_bf16(v.w)) << 16);
     *reinterpret_cast<uint2*>(p) = u;
+}
+
+// The same through a buffer view (offsets in bytes): out-of-range loads read
+// zeros and out-of-range stores are dropped.
+template <typename TIn>
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (std::is_same<TIn, float>::value) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    } else {
+        const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+        return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                           __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    }
+}
+template <typename TIn>
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, const float4& v) {
+    if constexpr (std::is_same<TIn, float>::value) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(mfma::u32x4, v), r, off, 0, 0);
+    } else {
+        const mfma::u32x2 u{uint32_t(f32_to_bf16(v.x)) | (uint32_t(f32_to_bf16(v.y)) << 16),
+                            uint32_t(f32_to_bf16(v.z)) | (uint32_t(f32_to_bf16(v.w)) << 16)};
+        __builtin_amdgcn_raw_buffer_store_b64(u, r, off, 0, 0);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -180,27 +203,28 @@ __global__ __launch_bounds__(kThreads) void outer64_kernel(
     const int a8 = u >> 4, b4 = u & 15;
     const int ca = tid & 63, cg = tid >> 6;  // column-sum column and token group
 
+    // Staging: vectors m < NV / 2 are x rows, the rest y rows, so each load
+    // instruction reads one tensor (whole 256-byte rows, no divergence), and
+    // rows past the chunk read as zero through the buffer views.
+    static_assert(NV % 2 == 0 && (NV / 2) * kThreads == kRedTokens * (W / 4), "x, y halves");
+    const int rows = int(t_end - t_begin);
+    const auto xr = mfma::make_rsrc(xn + t_begin * W, int64_t(rows) * W * int64_t(sizeof(TIn)));
+    const auto yr = mfma::make_rsrc(yn + t_begin * W, int64_t(rows) * W * int64_t(sizeof(TIn)));
     float4 pre[NV];
-    auto fetch = [&](int64_t t0) {
+    auto fetch = [&](int r0) {
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
-            const int e = tid + m * kThreads;
-            const int i = e >> 5, v = e & 31;  // token, vector (16 of x, then 16 of y)
-            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t0 + i < t_end)
-                val = v < 16 ? load4(xn + (t0 + i) * W + 4 * v) : load4(yn + (t0 + i) * W + 4 * (v - 16));
-            pre[m] = val;
+            const int e = tid + (m % (NV / 2)) * kThreads;
+            const int i = e >> 4, v = e & 15;  // token, vector
+            pre[m] = buf_load4<TIn>(m < NV / 2 ? xr : yr, ((r0 + i) * W + 4 * v) * int(sizeof(TIn)));
         }
     };
     auto stash = [&](int buf) {
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
-            const int e = tid + m * kThreads;
-            const int i = e >> 5, v = e & 31;
-            if (v < 16)
-                store4(xs + (buf * kRedTokens + i) * W + 4 * v, pre[m]);
-            else
-                store4(ys + (buf * kRedTokens + i) * W + 4 * (v - 16), pre[m]);
+            const int e = tid + (m % (NV / 2)) * kThreads;
+            const int i = e >> 4, v = e & 15;
+            store4((m < NV / 2 ? xs : ys) + (buf * kRedTokens + i) * W + 4 * v, pre[m]);
         }
     };
 
@@ -211,13 +235,13 @@ __global__ __launch_bounds__(kThreads) void outer64_kernel(
         for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
     float csum = 0.f;
 
-    fetch(t_begin);
+    fetch(0);
     stash(0);
     __syncthreads();
     int buf = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kRedTokens) {
-        const bool more = t0 + kRedTokens < t_end;
-        if (more) fetch(t0 + kRedTokens);
+    for (int r0 = 0; r0 < rows; r0 += kRedTokens) {
+        const bool more = r0 + kRedTokens < rows;
+        if (more) fetch(r0 + kRedTokens);
         const float* xb = xs + (buf * kRedTokens + 16 * half) * W;
         const float* yb = ys + (buf * kRedTokens + 16 * half) * W;
 #pragma unroll 4
@@ -402,23 +426,32 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
         bv = make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
                          4 * cc + 3 < ncols ? bn[3] : 0.f);
     }
-    const TIn* xn = x + n * T * Wa;
-    TIn* on = out + n * T * Wb;
+    // Buffer views of the workgroup's rows: rows past T read as zero and
+    // their stores are dropped, so every load and store is unconditional.
+    // With the block loop unrolled the compiler then counts the stores
+    // issued after each prefetch and waits for the prefetched tokens only; a
+    // rolled loop with conditional stores waited for the previous block's
+    // stores too (10% slower).
     const int64_t wg_t0 = int64_t(blockIdx.x) * kMap64Blocks * kMap64Tokens;
+    const int64_t wg_rows = min(T - wg_t0, int64_t(kMap64Blocks) * kMap64Tokens);
+    const auto xr = mfma::make_rsrc(x + (n * T + wg_t0) * Wa, wg_rows * Wa * int64_t(sizeof(TIn)));
+    const auto orr = mfma::make_rsrc(out + (n * T + wg_t0) * Wb, wg_rows * Wb * int64_t(sizeof(TIn)));
+    constexpr int kOutside = 0x7ffffff0;  // past any buffer: the store is dropped
 
     float4 pre[NV];
-    auto fetch = [&](int64_t t0) {
+    auto fetch = [&](int r0) {
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
             const int e = tid + m * kThreads;
             const int i = e >> 4, u = e & 15;
-            pre[m] = t0 + i < T ? load4(xn + (t0 + i) * Wa + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+            pre[m] = buf_load4<TIn>(xr, ((r0 + i) * Wa + 4 * u) * int(sizeof(TIn)));
         }
     };
-    fetch(wg_t0);
+    fetch(0);
+#pragma unroll
     for (int blk = 0; blk < kMap64Blocks; ++blk) {
-        const int64_t t0 = wg_t0 + int64_t(blk) * kMap64Tokens;
-        if (t0 >= T) break;
+        const int r0 = blk * kMap64Tokens;
+        if (r0 >= wg_rows) break;
         __syncthreads();
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
@@ -431,7 +464,7 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
             xt[(4 * u + 3) * TP + col] = pre[m].w;
         }
         __syncthreads();
-        if (blk + 1 < kMap64Blocks) fetch(t0 + kMap64Tokens);
+        if (blk + 1 < kMap64Blocks) fetch(r0 + kMap64Tokens);
         float acc[8][4];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
@@ -453,21 +486,20 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
                 const float4 x0 = *reinterpret_cast<const float4*>(xa + k * TP + o0);
                 const float4 x1 = *reinterpret_cast<const float4*>(xa + k * TP + o1);
                 const float4 mv = *reinterpret_cast<const float4*>(ma + k * kSliceCols);
-                const float xr[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const float xr8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                 const float mc[4] = {mv.x, mv.y, mv.z, mv.w};
 #pragma unroll
                 for (int r = 0; r < 8; ++r)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr[r], mc[c], acc[r][c]);
+                    for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr8[r], mc[c], acc[r][c]);
             }
         }
-        if (4 * cc < ncols) {
+        const bool col_ok = 4 * cc < ncols;
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const int64_t t = t0 + 8 * tt + r;
-                if (t < T) store4(on + t * Wb + c0 + 4 * cc,
-                                  make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
-            }
+        for (int r = 0; r < 8; ++r) {
+            const int off = ((r0 + 8 * tt + r) * Wb + c0 + 4 * cc) * int(sizeof(TIn));
+            buf_store4<TIn>(orr, col_ok ? off : kOutside,
+                            make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
         }
     }
 }
