@@ -86,31 +86,30 @@ __global__ __launch_bounds__(kThreads) void outer_sums4_kernel(
     const TIn* xn = x + n * T * Wa;
     const TIn* yn = y + n * T * Wb;
 
+    // One load per vector from a per-lane address (x or y row; a valid row
+    // when out of range, zeroed when staged): branches around the loads, or
+    // zeroing right after them, made the compiler wait for each load in turn.
     float4 pre[NV];
     auto fetch = [&](int64_t t0) {
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
             const int e = tid + m * kThreads;
-            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (e < nvec) {
-                const int i = e / vrow, u = e - i * vrow;
-                if (t0 + i < t_end)
-                    val = u < va ? load4(xn + (t0 + i) * Wa + 4 * u)
-                                 : load4(yn + (t0 + i) * Wb + 4 * (u - va));
-            }
-            pre[m] = val;
+            const int i = e / vrow, u = e - i * vrow;
+            const int64_t t = e < nvec && t0 + i < t_end ? t0 + i : t_begin;
+            pre[m] = load4(u < va ? xn + t * Wa + 4 * u : yn + t * Wb + 4 * (u - va));
         }
     };
-    auto stash = [&](int buf) {
+    auto stash = [&](int buf, int64_t t0) {
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
             const int e = tid + m * kThreads;
             if (e < nvec) {
                 const int i = e / vrow, u = e - i * vrow;
+                const float4 val = t0 + i < t_end ? pre[m] : make_float4(0.f, 0.f, 0.f, 0.f);
                 if (u < va)
-                    store4(xs + (buf * kRedTokens + i) * Wa + 4 * u, pre[m]);
+                    store4(xs + (buf * kRedTokens + i) * Wa + 4 * u, val);
                 else
-                    store4(ys + (buf * kRedTokens + i) * Wb + 4 * (u - va), pre[m]);
+                    store4(ys + (buf * kRedTokens + i) * Wb + 4 * (u - va), val);
             }
         }
     };
@@ -127,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void outer_sums4_kernel(
         }
 
     fetch(t_begin);
-    stash(0);
+    stash(0, t_begin);
     __syncthreads();
     int buf = 0;
     for (int64_t t0 = t_begin; t0 < t_end; t0 += kRedTokens) {
@@ -154,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void outer_sums4_kernel(
                 }
             }
         }
-        if (more) stash(buf ^ 1);
+        if (more) stash(buf ^ 1, t0 + kRedTokens);
         __syncthreads();
         buf ^= 1;
     }
@@ -297,6 +296,32 @@ __global__ __launch_bounds__(kThreads) void outer64_kernel(
 // NV: 16-byte token vectors each thread stages per block.
 __device__ __forceinline__ int xsw(int a) { return (a >> 2) & 7; }
 
+// Ms[a][c] = M[a * ms_row + (c0 + c) * ms_col] for the slice's columns
+// c < ncols, zero beyond, a < Wa (a multiple of kThreads / kSliceCols).  The
+// loads go out in groups of 8 before their LDS stores: a plain loop waited
+// for each load before the next (one memory round trip per element).
+__device__ __forceinline__ void stage_slice(float* __restrict__ Ms, const float* __restrict__ Mn,
+                                            int Wa, int64_t ms_row, int64_t ms_col, int c0,
+                                            int ncols) {
+    constexpr int kRows = kThreads / kSliceCols;  // rows of the slice per pass
+    const int c = threadIdx.x % kSliceCols, a0 = threadIdx.x / kSliceCols;
+    const bool ok = c < ncols;
+    const float* col = Mn + (c0 + (ok ? c : 0)) * ms_col;  // in bounds either way
+    for (int ab = 0; ab < Wa; ab += 8 * kRows) {
+        float v[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int a = min(ab + a0 + m * kRows, Wa - 1);  // clamped: no branch
+            v[m] = col[a * ms_row];
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int a = ab + a0 + m * kRows;
+            if (a < Wa) Ms[a * kSliceCols + c] = ok ? v[m] : 0.f;
+        }
+    }
+}
+
 template <typename TIn, int NV>
 __global__ __launch_bounds__(kThreads) void map4_kernel(
     const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
@@ -311,10 +336,7 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
     const int c0 = blockIdx.z * kSliceCols;
     const int ncols = min(kSliceCols, Wb - c0);
     const float* Mn = M + n * m_stream_stride;
-    for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
-        const int a = e / kSliceCols, c = e - a * kSliceCols;
-        Ms[e] = c < ncols ? Mn[a * ms_row + (c0 + c) * ms_col] : 0.f;
-    }
+    stage_slice(Ms, Mn, Wa, ms_row, ms_col, c0, ncols);
     const int va = Wa / 4;
     const int nvec = kMapTokens4 * va;
     const int tt = tid >> 4, cc = tid & 15;
@@ -324,29 +346,32 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
         bv = make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
                          4 * cc + 3 < ncols ? bn[3] : 0.f);
     }
-    const TIn* xn = x + n * T * Wa;
-    TIn* on = out + n * T * Wb;
+    // Buffer views of the workgroup's rows (rows past T read as zero, their
+    // stores are dropped): every load and store is unconditional, so the
+    // compiler neither waits for each load in turn nor, with the block loop
+    // unrolled, for the previous block's stores before using a prefetch.
     const int64_t wg_t0 = int64_t(blockIdx.x) * kMapBlocks * kMapTokens4;
+    const int64_t wg_rows = min(T - wg_t0, int64_t(kMapBlocks) * kMapTokens4);
+    const auto xr = mfma::make_rsrc(x + (n * T + wg_t0) * Wa, wg_rows * Wa * int64_t(sizeof(TIn)));
+    const auto orr = mfma::make_rsrc(out + (n * T + wg_t0) * Wb, wg_rows * Wb * int64_t(sizeof(TIn)));
+    constexpr int kOutside = 0x7ffffff0;  // past any buffer
 
     // The next block's token vectors are loaded into registers while the
     // current block computes.
     float4 pre[NV];
-    auto fetch = [&](int64_t t0) {
+    auto fetch = [&](int r0) {
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
             const int e = tid + m * kThreads;
-            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (e < nvec) {
-                const int i = e / va, u = e - i * va;
-                if (t0 + i < T) val = load4(xn + (t0 + i) * Wa + 4 * u);
-            }
-            pre[m] = val;
+            const int i = e / va, u = e - i * va;
+            pre[m] = buf_load4<TIn>(xr, e < nvec ? ((r0 + i) * Wa + 4 * u) * int(sizeof(TIn)) : kOutside);
         }
     };
-    fetch(wg_t0);
+    fetch(0);
+#pragma unroll
     for (int blk = 0; blk < kMapBlocks; ++blk) {
-        const int64_t t0 = wg_t0 + int64_t(blk) * kMapTokens4;
-        if (t0 >= T) break;
+        const int r0 = blk * kMapTokens4;
+        if (r0 >= wg_rows) break;
         __syncthreads();
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
@@ -361,7 +386,7 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
             }
         }
         __syncthreads();
-        if (blk + 1 < kMapBlocks) fetch(t0 + kMapTokens4);
+        if (blk + 1 < kMapBlocks) fetch(r0 + kMapTokens4);
         float acc[4][4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -380,13 +405,12 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
 #pragma unroll
                 for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr[r], mc[c], acc[r][c]);
         }
-        if (4 * cc < ncols) {
+        const bool col_ok = 4 * cc < ncols;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t t = t0 + 4 * tt + r;
-                if (t < T) store4(on + t * Wb + c0 + 4 * cc,
-                                  make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
-            }
+        for (int r = 0; r < 4; ++r) {
+            const int off = ((r0 + 4 * tt + r) * Wb + c0 + 4 * cc) * int(sizeof(TIn));
+            buf_store4<TIn>(orr, col_ok ? off : kOutside,
+                            make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
         }
     }
 }
@@ -415,10 +439,7 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
     const int c0 = blockIdx.z * kSliceCols;
     const int ncols = min(kSliceCols, Wb - c0);
     const float* Mn = M + n * m_stream_stride;
-    for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
-        const int a = e / kSliceCols, c = e - a * kSliceCols;
-        Ms[e] = c < ncols ? Mn[a * ms_row + (c0 + c) * ms_col] : 0.f;
-    }
+    stage_slice(Ms, Mn, Wa, ms_row, ms_col, c0, ncols);
     const int tt = tid >> 4, cc = tid & 15;  // tokens 8 tt .. 8 tt + 7, columns 4 cc .. 4 cc + 3
     float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (bias && 4 * cc < ncols) {
