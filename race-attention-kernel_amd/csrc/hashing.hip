@@ -56,33 +56,45 @@ __device__ __forceinline__ void store4(bf16_t* p, float a, float b, float c, flo
                                               uint32_t(f32_to_bf16(c)) | (uint32_t(f32_to_bf16(d)) << 16));
 }
 
-// Loads the 4-column groups of one staged chunk owned by this thread: group
+// The 4-column groups of one staged chunk owned by this thread: group
 // g = tid + 256 i is row g / 8, columns c0 + 4 (g % 8) .. + 3.  Vec: d_k is a
-// multiple of 4, so a group is one aligned vector load; columns past d_k and
-// rows past the tile read as zero.
+// multiple of 4, so a group is one aligned vector load.  The loads are
+// unconditional (rows past the tile and columns past d_k read a valid
+// element) and keep the raw input; the conversion, with those positions
+// zeroed, happens when the chunk is staged.  (Converting or zeroing right
+// after each load made the compiler wait for every bf16 load in turn.)
 template <typename TIn, bool Vec>
-__device__ __forceinline__ void load_chunk(float4 (&xr)[kGroups], const TIn* __restrict__ x,
-                                           int64_t row0, int cnt, int dk, int c0, int tid) {
+struct RawChunk {
+    Quad<TIn> q[kGroups];
+    TIn e[Vec ? 1 : kGroups][4];
+
+    __device__ __forceinline__ void load(const TIn* __restrict__ x, int64_t row0, int cnt, int dk,
+                                         int c0, int tid) {
 #pragma unroll
-    for (int i = 0; i < kGroups; ++i) {
-        const int g = tid + kThreads * i, row = g / kGroups, col = c0 + 4 * (g % kGroups);
-        const TIn* src = x + (row0 + row) * dk + col;
-        if (Vec) {
-            if (row < cnt && col < dk) {
-                Quad<TIn> q;
-                q.load(src);
-                xr[i] = q.f32();
+        for (int i = 0; i < kGroups; ++i) {
+            const int g = tid + kThreads * i;
+            const int row = min(g / kGroups, cnt - 1), col = c0 + 4 * (g % kGroups);
+            if constexpr (Vec) {
+                q[i].load(x + (row0 + row) * dk + (col < dk ? col : 0));
             } else {
-                xr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-        } else {
-            float e[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) e[t] = (row < cnt && col + t < dk) ? to_f32(src[t]) : 0.f;
-            xr[i] = make_float4(e[0], e[1], e[2], e[3]);
+                for (int t = 0; t < 4; ++t) e[i][t] = x[(row0 + row) * dk + (col + t < dk ? col + t : 0)];
+            }
         }
     }
-}
+    // Group i as floats, zero past the tile's rows and past d_k.
+    __device__ __forceinline__ float4 get(int i, int cnt, int dk, int c0, int tid) const {
+        const int g = tid + kThreads * i, row = g / kGroups, col = c0 + 4 * (g % kGroups);
+        if constexpr (Vec) {
+            return row < cnt && col < dk ? q[i].f32() : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            float v[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = row < cnt && col + t < dk ? to_f32(e[i][t]) : 0.f;
+            return make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+};
 
 template <typename TIn, int LKT, bool Vec>
 __global__ __launch_bounds__(kThreads) void hash_probs_kernel(const TIn* __restrict__ x,
@@ -97,25 +109,39 @@ __global__ __launch_bounds__(kThreads) void hash_probs_kernel(const TIn* __restr
     const int64_t row0 = int64_t(blockIdx.x) * kHashRows;
     const int cnt = int(min<int64_t>(kHashRows, rows - row0));
 
-    for (int e = tid; e < dk4 * LKT; e += kThreads) {
-        const int c = e / LKT, j = e - c * LKT;
-        pl[e] = (j < LK && c < dk) ? planes_T[c * LK + j] : 0.f;
+    // Planes staged with their loads in groups of 8 (clamped addresses, the
+    // padding zeroed at the store), not one memory round trip per element.
+    for (int e0 = 0; e0 < dk4 * LKT; e0 += 8 * kThreads) {
+        float v[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int e = e0 + tid + m * kThreads;
+            const int c = min(e / LKT, dk - 1), j = min(e % LKT, LK - 1);
+            v[m] = planes_T[c * LK + j];
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int e = e0 + tid + m * kThreads;
+            const int c = e / LKT, j = e % LKT;
+            if (e < dk4 * LKT) pl[e] = (j < LK && c < dk) ? v[m] : 0.f;
+        }
     }
 
     float acc[LKT];
 #pragma unroll
     for (int j = 0; j < LKT; ++j) acc[j] = 0.f;
-    float4 xr[kGroups];
-    load_chunk<TIn, Vec>(xr, x, row0, cnt, dk, 0, tid);
+    RawChunk<TIn, Vec> xr;
+    xr.load(x, row0, cnt, dk, 0, tid);
     for (int c0 = 0; c0 < dk; c0 += kChunk) {
         __syncthreads();  // the previous chunk has been read
 #pragma unroll
         for (int i = 0; i < kGroups; ++i) {
             const int g = tid + kThreads * i;
-            *reinterpret_cast<float4*>(xs + (g / kGroups) * kXPitch + 4 * (g % kGroups)) = xr[i];
+            *reinterpret_cast<float4*>(xs + (g / kGroups) * kXPitch + 4 * (g % kGroups)) =
+                xr.get(i, cnt, dk, c0, tid);
         }
         __syncthreads();
-        if (c0 + kChunk < dk) load_chunk<TIn, Vec>(xr, x, row0, cnt, dk, c0 + kChunk, tid);
+        if (c0 + kChunk < dk) xr.load(x, row0, cnt, dk, c0 + kChunk, tid);
         const int width = min(kChunk, dk4 - c0);
         const float* xrow = xs + tid * kXPitch;
         for (int cc = 0; cc < width; cc += 4) {
