@@ -78,8 +78,7 @@ PHASES = {
 # Backward launch sequences (every gradient requested).
 BWD_PHASES = {
     True: ["bwd_tile_sums", "tile_scan", "bwd_dq", "suffix_scan", "bwd_dkv"],
-    False: ["state_to_E", "token_map_dq", "tile_sums_dE", "tile_reduce_dE", "bwd_finalize",
-            "token_map_dk", "token_map_dv"],
+    False: ["token_map_dq", "tile_sums_dE", "bwd_finalize", "token_map_dk", "token_map_dv"],
 }
 
 
@@ -169,11 +168,9 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
         "bwd_dq": es * (3 * S + 2 * d) * NT,       # q, k, v, dOut -> dQ
         "suffix_scan": 2 * state,
         "bwd_dkv": es * (3 * S + 3 * d) * NT,      # q, k, v, dOut -> dK, dV
-        "state_to_E": small,
         "token_map_dq": es * (d + S) * NT,
         "tile_sums_dE": es * (S + d) * NT,
-        "tile_reduce_dE": state,
-        "bwd_finalize": small,
+        "bwd_finalize": state + small,             # dE tile records, state -> dB, dA
         "token_map_dk": es * (d + S) * NT,
         "token_map_dv": es * (S + d) * NT,
         "hash_q": es * (d + S) * NT,               # rows of d_k = d -> probabilities

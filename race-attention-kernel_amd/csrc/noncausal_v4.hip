@@ -296,37 +296,49 @@ __global__ __launch_bounds__(kThreads) void outer64_kernel(
 // NV: 16-byte token vectors each thread stages per block.
 __device__ __forceinline__ int xsw(int a) { return (a >> 2) & 7; }
 
-// Ms[a][c] = M[a * ms_row + (c0 + c) * ms_col] for the slice's columns
-// c < ncols, zero beyond, a < Wa (a multiple of kThreads / kSliceCols).  The
-// loads go out in groups of 8 before their LDS stores: a plain loop waited
-// for each load before the next (one memory round trip per element).
-__device__ __forceinline__ void stage_slice(float* __restrict__ Ms, const float* __restrict__ Mn,
-                                            int Wa, int64_t ms_row, int64_t ms_col, int c0,
-                                            int ncols) {
+// Ms[a][c] = M[a][c0 + c] of the map operand for stream n (divided by its
+// divisor when it has one) for the slice's columns c < ncols, zero beyond,
+// a < Wa.  The loads go out in groups of 8 before their LDS stores: a plain
+// loop waited for each load before the next (one memory round trip per
+// element).
+__device__ __forceinline__ void stage_slice(float* __restrict__ Ms, const MapOperand& op,
+                                            int64_t n, int Wa, int c0, int ncols) {
     constexpr int kRows = kThreads / kSliceCols;  // rows of the slice per pass
     const int c = threadIdx.x % kSliceCols, a0 = threadIdx.x / kSliceCols;
     const bool ok = c < ncols;
-    const float* col = Mn + (c0 + (ok ? c : 0)) * ms_col;  // in bounds either way
+    const int cg = c0 + (ok ? c : 0);  // in bounds either way
+    const float* col = op.m + n * op.stream + cg * op.col;
+    const float* dv = op.div ? op.div + n * op.div_stream : nullptr;
     for (int ab = 0; ab < Wa; ab += 8 * kRows) {
-        float v[8];
+        float v[8], q[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const int a = min(ab + a0 + m * kRows, Wa - 1);  // clamped: no branch
-            v[m] = col[a * ms_row];
+            v[m] = col[a * op.row];
+            q[m] = dv ? dv[op.div_by_col ? cg : a] : 0.f;
         }
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const int a = ab + a0 + m * kRows;
-            if (a < Wa) Ms[a * kSliceCols + c] = ok ? v[m] : 0.f;
+            if (a < Wa) Ms[a * kSliceCols + c] = ok ? (dv ? v[m] / (q[m] + kEps) : v[m]) : 0.f;
         }
     }
 }
 
+// The bias of the slice's 4 columns 4 cc .. + 3 (zero past ncols or without
+// a bias).
+__device__ __forceinline__ float4 slice_bias(const MapOperand& op, int64_t n, int c0, int cc,
+                                             int ncols) {
+    if (!op.bias || 4 * cc >= ncols) return make_float4(0.f, 0.f, 0.f, 0.f);
+    const float* bn = op.bias + n * op.bias_stream + c0 + 4 * cc;
+    return make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
+                       4 * cc + 3 < ncols ? bn[3] : 0.f);
+}
+
 template <typename TIn, int NV>
 __global__ __launch_bounds__(kThreads) void map4_kernel(
-    const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
-    int64_t m_stream_stride, int64_t ms_row, int64_t ms_col, const float* __restrict__ bias,
-    int64_t bias_stream_stride, int64_t T, int Wa, int Wb) {
+    const TIn* __restrict__ x, TIn* __restrict__ out, const MapOperand op, int64_t T, int Wa,
+    int Wb) {
     extern __shared__ float smem[];
     constexpr int TP = kMapTokens4 + 4;  // pitch of the transposed token tile
     float* Ms = smem;                    // [Wa][64]
@@ -335,17 +347,11 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
     const int64_t n = blockIdx.y;
     const int c0 = blockIdx.z * kSliceCols;
     const int ncols = min(kSliceCols, Wb - c0);
-    const float* Mn = M + n * m_stream_stride;
-    stage_slice(Ms, Mn, Wa, ms_row, ms_col, c0, ncols);
+    stage_slice(Ms, op, n, Wa, c0, ncols);
     const int va = Wa / 4;
     const int nvec = kMapTokens4 * va;
     const int tt = tid >> 4, cc = tid & 15;
-    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (bias && 4 * cc < ncols) {
-        const float* bn = bias + n * bias_stream_stride + c0 + 4 * cc;
-        bv = make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
-                         4 * cc + 3 < ncols ? bn[3] : 0.f);
-    }
+    const float4 bv = slice_bias(op, n, c0, cc, ncols);
     // Buffer views of the workgroup's rows (rows past T read as zero, their
     // stores are dropped): every load and store is unconditional, so the
     // compiler neither waits for each load in turn nor, with the block loop
@@ -425,9 +431,7 @@ constexpr int kMap64Blocks = 4;
 
 template <typename TIn>
 __global__ __launch_bounds__(kThreads) void map64_kernel(
-    const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
-    int64_t m_stream_stride, int64_t ms_row, int64_t ms_col, const float* __restrict__ bias,
-    int64_t bias_stream_stride, int64_t T, int Wb) {
+    const TIn* __restrict__ x, TIn* __restrict__ out, const MapOperand op, int64_t T, int Wb) {
     constexpr int Wa = 64;
     constexpr int TP = kMap64Tokens + 4;                   // pitch of the transposed token tile
     constexpr int NV = kMap64Tokens * (Wa / 4) / kThreads;  // 16-byte token vectors per thread
@@ -438,15 +442,9 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
     const int64_t n = blockIdx.y;
     const int c0 = blockIdx.z * kSliceCols;
     const int ncols = min(kSliceCols, Wb - c0);
-    const float* Mn = M + n * m_stream_stride;
-    stage_slice(Ms, Mn, Wa, ms_row, ms_col, c0, ncols);
+    stage_slice(Ms, op, n, Wa, c0, ncols);
     const int tt = tid >> 4, cc = tid & 15;  // tokens 8 tt .. 8 tt + 7, columns 4 cc .. 4 cc + 3
-    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (bias && 4 * cc < ncols) {
-        const float* bn = bias + n * bias_stream_stride + c0 + 4 * cc;
-        bv = make_float4(bn[0], 4 * cc + 1 < ncols ? bn[1] : 0.f, 4 * cc + 2 < ncols ? bn[2] : 0.f,
-                         4 * cc + 3 < ncols ? bn[3] : 0.f);
-    }
+    const float4 bv = slice_bias(op, n, c0, cc, ncols);
     // Buffer views of the workgroup's rows: rows past T read as zero and
     // their stores are dropped, so every load and store is unconditional.
     // With the block loop unrolled the compiler then counts the stores
@@ -593,10 +591,8 @@ size_t map4_lds_bytes(int Wa) {
     return size_t(Wa * kSliceCols + Wa * (kMapTokens4 + 4)) * sizeof(float);
 }
 
-hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_stream_stride,
-                       int64_t ms_row, int64_t ms_col, const float* bias,
-                       int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
-                       hipStream_t stream) {
+hipError_t launch_map4(const void* x, void* out, const MapOperand& op, const Problem& p, int Wa,
+                       int Wb, hipStream_t stream) {
     if (Wa == 64) {
         const int64_t per_wg64 = int64_t(kMap64Blocks) * kMap64Tokens;
         const dim3 grid64(unsigned((p.T + per_wg64 - 1) / per_wg64), unsigned(p.N),
@@ -604,12 +600,10 @@ hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_strea
         const size_t lds64 = map4_lds_bytes(64);
         if (p.dtype == RACE_BF16)
             map64_kernel<bf16_t><<<grid64, kThreads, lds64, stream>>>(
-                static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), M, m_stream_stride, ms_row,
-                ms_col, bias, bias_stream_stride, p.T, Wb);
+                static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), op, p.T, Wb);
         else
             map64_kernel<float><<<grid64, kThreads, lds64, stream>>>(
-                static_cast<const float*>(x), static_cast<float*>(out), M, m_stream_stride, ms_row,
-                ms_col, bias, bias_stream_stride, p.T, Wb);
+                static_cast<const float*>(x), static_cast<float*>(out), op, p.T, Wb);
         return hipGetLastError();
     }
     const int64_t per_wg = int64_t(kMapBlocks) * kMapTokens4;
@@ -619,8 +613,7 @@ hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_strea
     const int nv = pow2_at_least((kMapTokens4 * (Wa / 4) + kThreads - 1) / kThreads);
 #define RACE_MAP4(TIN, NV)                                                                     \
     map4_kernel<TIN, NV><<<grid, kThreads, lds, stream>>>(                                     \
-        static_cast<const TIN*>(x), static_cast<TIN*>(out), M, m_stream_stride, ms_row, ms_col, \
-        bias, bias_stream_stride, p.T, Wa, Wb)
+        static_cast<const TIN*>(x), static_cast<TIN*>(out), op, p.T, Wa, Wb)
 #define RACE_MAP4_NV(TIN)                      \
     switch (nv) {                              \
         case 1: RACE_MAP4(TIN, 1); break;      \

@@ -128,15 +128,13 @@ FwdLayout fwd_layout(const Problem& p, int causal) {
 }
 
 struct BwdLayout {
-    int64_t records = 0, totals = 0, E = 0, dB = 0, dA = 0;
-    int64_t total() const { return records + totals + E + dB + dA; }
+    int64_t records = 0, dB = 0, dA = 0;
+    int64_t total() const { return records + dB + dA; }
 };
 
 BwdLayout bwd_layout(const Problem& p) {
     BwdLayout l;
     l.records = p.N * p.tiles * p.rec;
-    l.totals = p.N * p.rec;
-    l.E = round64(p.N * p.S * p.d);
     l.dB = round64(p.N * p.S * p.d);
     l.dA = round64(p.N * p.S);
     return l;
@@ -197,14 +195,19 @@ hipError_t outer_sums(const void* x, const void* y, float* records, const Proble
     return launch_tile_outer_sums(x, y, records, p, Wa, Wb, stream);
 }
 
-hipError_t token_map(const void* x, void* out, const float* M, int64_t m_stream_stride,
-                     int64_t ms_row, int64_t ms_col, const float* bias, int64_t bias_stream_stride,
-                     const Problem& p, int Wa, int Wb, hipStream_t stream) {
-    if (v4_widths(Wa, Wb))
-        return launch_map4(x, out, M, m_stream_stride, ms_row, ms_col, bias, bias_stream_stride, p,
-                           Wa, Wb, stream);
-    return launch_token_map(x, out, M, m_stream_stride, ms_row, ms_col, bias, bias_stream_stride,
-                            p, Wa, Wb, stream);
+hipError_t token_map(const void* x, void* out, const MapOperand& op, const Problem& p, int Wa,
+                     int Wb, hipStream_t stream) {
+    if (v4_widths(Wa, Wb)) return launch_map4(x, out, op, p, Wa, Wb, stream);
+    return launch_token_map(x, out, op, p, Wa, Wb, stream);
+}
+
+MapOperand map_operand(const float* m, int64_t stream, int64_t row, int64_t col) {
+    MapOperand op;
+    op.m = m;
+    op.stream = stream;
+    op.row = row;
+    op.col = col;
+    return op;
 }
 
 #define RACE_TRY(expr)                                   \
@@ -322,7 +325,7 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
     RACE_TRY(launch_tile_reduce(records, nullptr, state, E, p, stream));
     RACE_TRY(marks->mark(stream));
     // out = q . E: M[a][c] = E[a*d + c].
-    RACE_TRY(token_map(probsQ, out, E, int64_t(p.S) * p.d, p.d, 1, nullptr, 0, p, p.S, p.d,
+    RACE_TRY(token_map(probsQ, out, map_operand(E, int64_t(p.S) * p.d, p.d, 1), p, p.S, p.d,
                        stream));
     return marks->mark(stream);
 }
@@ -396,36 +399,40 @@ race_status noncausal_bwd_impl(const void* probsQ, const void* probsK, const voi
     if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
         return RACE_ERROR_INVALID_VALUE;
     float* records = static_cast<float*>(workspace);
-    float* totals = records + l.records;
-    float* E = totals + l.totals;
-    float* dB = E + l.E;
+    float* dB = records + l.records;
     float* dA = dB + l.dB;
     const int64_t Sd = int64_t(p.S) * p.d;
+    const int64_t state_stride = Sd + p.S;
 
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_state_to_E(state, E, p, stream));
-    RACE_TRY(marks->mark(stream));
-    // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c].
+    // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c] = B[s*d + c] / (A[s] + eps),
+    // read straight from the state.
     if (dQ) {
-        RACE_TRY(token_map(dOut, dQ, E, Sd, 1, p.d, nullptr, 0, p, p.d, p.S, stream));
+        MapOperand op = map_operand(state, state_stride, 1, p.d);
+        op.div = state + Sd;
+        op.div_stream = state_stride;
+        op.div_by_col = true;
+        RACE_TRY(token_map(dOut, dQ, op, p, p.d, p.S, stream));
         RACE_TRY(marks->mark(stream));
     }
     if (!dK && !dV) return RACE_SUCCESS;
-    // dE = Q^T dOut, as per-tile partials then a fixed-order reduce.
+    // dE = Q^T dOut as per-tile partials; the finalize adds them in a fixed
+    // order.
     RACE_TRY(outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_tile_reduce(records, totals, nullptr, nullptr, p, stream));
-    RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_bwd_finalize(totals, state, E, dB, dA, p, stream));
+    RACE_TRY(launch_bwd_finalize(records, state, dB, dA, p, stream));
     RACE_TRY(marks->mark(stream));
     // dK = V dB^T + dA: M[a = c][b = s] = dB[s*d + c].
     if (dK) {
-        RACE_TRY(token_map(V, dK, dB, Sd, 1, p.d, dA, p.S, p, p.d, p.S, stream));
+        MapOperand op = map_operand(dB, Sd, 1, p.d);
+        op.bias = dA;
+        op.bias_stream = p.S;
+        RACE_TRY(token_map(V, dK, op, p, p.d, p.S, stream));
         RACE_TRY(marks->mark(stream));
     }
     // dV = K dB: M[a = s][b = c] = dB[s*d + c].
     if (dV) {
-        RACE_TRY(token_map(probsK, dV, dB, Sd, p.d, 1, nullptr, 0, p, p.S, p.d, stream));
+        RACE_TRY(token_map(probsK, dV, map_operand(dB, Sd, p.d, 1), p, p.S, p.d, stream));
         RACE_TRY(marks->mark(stream));
     }
     return RACE_SUCCESS;

@@ -85,24 +85,35 @@ hipError_t launch_tile_reduce(const float* records, float* totals, float* state,
 // Causal output pass from the scanned records.
 hipError_t launch_causal_output_valu(const void* q, const void* k, const void* v, void* out,
                                      const float* records, const Problem& p, hipStream_t stream);
-// out[n][t][c] = sum_a x[n][t][a] * M[n][a*ms_row + c*ms_col] (+ bias[n][c]).
-hipError_t launch_token_map(const void* x, void* out, const float* M, int64_t m_stream_stride,
-                            int64_t ms_row, int64_t ms_col, const float* bias,
-                            int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
-                            hipStream_t stream);
-// E = B / (A + eps) from state records ([N][S*d+S]) into E ([N][S][d]).
+// The matrix of a token map for stream n:
+//     M[a][c] = m[n * stream + a * row + c * col]
+// divided by (div[n * div_stream + (div_by_col ? c : a)] + eps) when div is
+// given (E = B / (A + eps) read straight from a state), and bias[n *
+// bias_stream + c] added to every output row when bias is given.
+struct MapOperand {
+    const float* m = nullptr;
+    int64_t stream = 0, row = 0, col = 0;
+    const float* div = nullptr;
+    int64_t div_stream = 0;
+    bool div_by_col = false;
+    const float* bias = nullptr;
+    int64_t bias_stream = 0;
+};
+// out[n][t][c] = sum_a x[n][t][a] * M[a][c] (+ bias[c]) for the operand's M.
+hipError_t launch_token_map(const void* x, void* out, const MapOperand& op, const Problem& p,
+                            int Wa, int Wb, hipStream_t stream);
 // The causal op continued from init ([N][S*d+S]) token by token in one
 // launch (decode.hip); the advanced state goes to `state`, which may be init.
 hipError_t launch_decode(const void* q, const void* k, const void* v, void* out,
                          const float* init, float* state, const Problem& p, hipStream_t stream);
-hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hipStream_t stream);
 // Dynamic LDS of the VALU output pass and map kernels.
 size_t causal_output_valu_lds_bytes(int S);
 size_t token_map_lds_bytes(int Wa);
-// Backward finalize: from dE totals ([N][rec]), the forward state (B, A) and
-// E: dB = dE / (A + eps) into dB ([N][S][d]), dA into dA ([N][S]).
-hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
-                               float* dB, float* dA, const Problem& p, hipStream_t stream);
+// Backward finalize: dE = the sum of the tile records of Q^T dOut ([N][tiles]
+// [rec], fixed order), E = B / (A + eps) from the forward state ([N][S*d+S]);
+// dB = dE / (A + eps) into dB ([N][S][d]), dA into dA ([N][S]).
+hipError_t launch_bwd_finalize(const float* dE_records, const float* state, float* dB, float* dA,
+                               const Problem& p, hipStream_t stream);
 
 // ---- MFMA kernels: mfma_direct.hip (one wave per tile, operands straight
 // from global memory into registers) and mfma_causal.hip (workgroup-
@@ -128,10 +139,8 @@ bool v4_widths(int Wa, int Wb);
 hipError_t launch_outer_sums4(const void* x, const void* y, float* records, const Problem& p,
                               int Wa, int Wb, hipStream_t stream);
 // Same result as launch_token_map.
-hipError_t launch_map4(const void* x, void* out, const float* M, int64_t m_stream_stride,
-                       int64_t ms_row, int64_t ms_col, const float* bias,
-                       int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
-                       hipStream_t stream);
+hipError_t launch_map4(const void* x, void* out, const MapOperand& op, const Problem& p, int Wa,
+                       int Wb, hipStream_t stream);
 size_t map4_lds_bytes(int Wa);
 
 // ---- causal backward (causal_bwd.hip): fp32 vector-ALU kernels ----

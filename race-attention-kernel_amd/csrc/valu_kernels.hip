@@ -232,36 +232,28 @@ __global__ __launch_bounds__(kThreads) void tile_reduce_kernel(
     }
 }
 
-// E = B / (A + eps) from a state record [S*d + S].
-__global__ __launch_bounds__(kThreads) void state_to_E_kernel(const float* __restrict__ state,
-                                                              float* __restrict__ E, int S, int d) {
-    const int e = blockIdx.x * kThreads + threadIdx.x;
-    const int64_t n = blockIdx.y;
-    if (e >= S * d) return;
-    const float* st = state + n * (S * d + S);
-    E[n * S * d + e] = st[e] / (st[S * d + e / d] + kEps);
-}
-
+// dE[s][c] = sum over the tiles of the dE records (in tile order);
+// E[s][c] = B[s][c] / (A[s] + eps) from the forward state;
 // dB = dE / (A + eps); dA[s] = -sum_c dE[s][c] E[s][c] / (A[s] + eps).
 // One wave per bucket row s (kThreads / 64 rows per workgroup): lanes over
-// the columns c (d <= 128: at most two per lane), every load of the row issued
-// before any result is needed, the row's products summed by a fixed shuffle
-// tree.
+// the columns c (d <= 128: at most two per lane), the row's tile records
+// loaded together, its products summed by a fixed shuffle tree.
 __global__ __launch_bounds__(kThreads) void bwd_finalize_kernel(
-    const float* __restrict__ dE_totals, const float* __restrict__ state,
-    const float* __restrict__ E, float* __restrict__ dB, float* __restrict__ dA, int64_t rec,
-    int S, int d) {
+    const float* __restrict__ dE_records, const float* __restrict__ state, float* __restrict__ dB,
+    float* __restrict__ dA, int64_t tiles, int64_t rec, int S, int d) {
     const int lane = threadIdx.x & 63;
     const int s = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     const int64_t n = blockIdx.y;
     if (s >= S) return;
-    const float* dE = dE_totals + n * rec + int64_t(s) * d;
-    const float* En = E + (n * S + s) * d;
+    const float* r = dE_records + n * tiles * rec + int64_t(s) * d;
+    const float* Bn = state + n * (S * d + S) + int64_t(s) * d;
     float* dBn = dB + (n * S + s) * d;
     const float den = state[n * (S * d + S) + S * d + s] + kEps;
     const bool lo = lane < d, hi = lane + 64 < d;
-    const float g0 = lo ? dE[lane] : 0.f, e0 = lo ? En[lane] : 0.f;
-    const float g1 = hi ? dE[lane + 64] : 0.f, e1 = hi ? En[lane + 64] : 0.f;
+    const int c0 = lo ? lane : 0, c1 = hi ? lane + 64 : 0;  // in bounds either way
+    const float g0 = lo ? sum_over_tiles(r + c0, tiles, rec) : 0.f;
+    const float g1 = hi ? sum_over_tiles(r + c1, tiles, rec) : 0.f;
+    const float e0 = lo ? Bn[c0] / den : 0.f, e1 = hi ? Bn[c1] / den : 0.f;
     if (lo) dBn[lane] = g0 / den;
     if (hi) dBn[lane + 64] = g1 / den;
     float acc = fmaf(g1, e1, g0 * e0);
@@ -359,14 +351,13 @@ __global__ __launch_bounds__(kThreads) void causal_output_valu_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// out[t][c] = sum_a x[t][a] * M[a*ms_row + c*ms_col] (+ bias[c]), one
-// workgroup per (kMapTokens tokens, stream, 64-column slice).  Thread
+// out[t][c] = sum_a x[t][a] * M[a][c] (+ bias[c]) for the map operand's M,
+// one workgroup per (kMapTokens tokens, stream, 64-column slice).  Thread
 // (i, tc) = (tid / 8, tid % 8) computes token i, slice columns tc + 8 j.
 template <typename TIn>
 __global__ __launch_bounds__(kThreads) void token_map_kernel(
-    const TIn* __restrict__ x, TIn* __restrict__ out, const float* __restrict__ M,
-    int64_t m_stream_stride, int64_t ms_row, int64_t ms_col, const float* __restrict__ bias,
-    int64_t bias_stream_stride, int64_t T, int Wa, int Wb) {
+    const TIn* __restrict__ x, TIn* __restrict__ out, const MapOperand op, int64_t T, int Wa,
+    int Wb) {
     extern __shared__ float smem[];
     float* Ms = smem;                    // [Wa][64]
     float* xs = Ms + Wa * kSliceCols;    // [kMapTokens][Wa]
@@ -376,10 +367,13 @@ __global__ __launch_bounds__(kThreads) void token_map_kernel(
     const int ncols = min(kSliceCols, Wb - c0);
     const int64_t t0 = int64_t(blockIdx.x) * kMapTokens;
     const int cnt = int(min<int64_t>(kMapTokens, T - t0));
-    const float* Mn = M + n * m_stream_stride;
+    const float* Mn = op.m + n * op.stream;
+    const float* dv = op.div ? op.div + n * op.div_stream : nullptr;
     for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
         const int a = e / kSliceCols, c = e - a * kSliceCols;
-        Ms[e] = c < ncols ? Mn[a * ms_row + (c0 + c) * ms_col] : 0.f;
+        float v = c < ncols ? Mn[a * op.row + (c0 + c) * op.col] : 0.f;
+        if (dv && c < ncols) v = v / (dv[op.div_by_col ? c0 + c : a] + kEps);
+        Ms[e] = v;
     }
     const TIn* xn = x + n * T * Wa;
     for (int e = tid; e < cnt * Wa; e += kThreads) xs[e] = ld(xn, t0 * Wa + e);
@@ -400,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void token_map_kernel(
         const int c = tc + 8 * j;
         if (c < ncols) {
             float val = acc[j];
-            if (bias) val += bias[n * bias_stream_stride + c0 + c];
+            if (op.bias) val += op.bias[n * op.bias_stream + c0 + c];
             store_val(on + c0 + c, val);
         }
     }
@@ -462,18 +456,12 @@ hipError_t launch_tile_reduce(const float* records, float* totals, float* state,
     return hipGetLastError();
 }
 
-hipError_t launch_state_to_E(const float* state, float* E, const Problem& p, hipStream_t stream) {
-    const dim3 grid(unsigned((p.S * p.d + kThreads - 1) / kThreads), unsigned(p.N));
-    state_to_E_kernel<<<grid, kThreads, 0, stream>>>(state, E, p.S, p.d);
-    return hipGetLastError();
-}
-
-hipError_t launch_bwd_finalize(const float* dE_totals, const float* state, const float* E,
-                               float* dB, float* dA, const Problem& p, hipStream_t stream) {
+hipError_t launch_bwd_finalize(const float* dE_records, const float* state, float* dB, float* dA,
+                               const Problem& p, hipStream_t stream) {
     static_assert(kThreads % 64 == 0, "whole waves");
     const dim3 grid(unsigned((p.S + kThreads / 64 - 1) / (kThreads / 64)), unsigned(p.N));
-    bwd_finalize_kernel<<<grid, kThreads, 0, stream>>>(dE_totals, state, E, dB, dA, p.rec, p.S,
-                                                       p.d);
+    bwd_finalize_kernel<<<grid, kThreads, 0, stream>>>(dE_records, state, dB, dA, p.tiles, p.rec,
+                                                       p.S, p.d);
     return hipGetLastError();
 }
 
@@ -504,21 +492,17 @@ size_t token_map_lds_bytes(int Wa) {
     return size_t(Wa * kSliceCols + kMapTokens * Wa) * sizeof(float);
 }
 
-hipError_t launch_token_map(const void* x, void* out, const float* M, int64_t m_stream_stride,
-                            int64_t ms_row, int64_t ms_col, const float* bias,
-                            int64_t bias_stream_stride, const Problem& p, int Wa, int Wb,
-                            hipStream_t stream) {
+hipError_t launch_token_map(const void* x, void* out, const MapOperand& op, const Problem& p,
+                            int Wa, int Wb, hipStream_t stream) {
     const dim3 grid(unsigned((p.T + kMapTokens - 1) / kMapTokens), unsigned(p.N),
                     unsigned((Wb + kSliceCols - 1) / kSliceCols));
     const size_t lds = token_map_lds_bytes(Wa);
     if (p.dtype == RACE_BF16) {
         token_map_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
-            static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), M, m_stream_stride, ms_row,
-            ms_col, bias, bias_stream_stride, p.T, Wa, Wb);
+            static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), op, p.T, Wa, Wb);
     } else {
         token_map_kernel<float><<<grid, kThreads, lds, stream>>>(
-            static_cast<const float*>(x), static_cast<float*>(out), M, m_stream_stride, ms_row,
-            ms_col, bias, bias_stream_stride, p.T, Wa, Wb);
+            static_cast<const float*>(x), static_cast<float*>(out), op, p.T, Wa, Wb);
     }
     return hipGetLastError();
 }
