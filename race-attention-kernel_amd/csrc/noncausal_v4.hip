@@ -42,14 +42,26 @@ __device__ __forceinline__ void store4(bf16_t* __restrict__ p, const float4& v) 
     *reinterpret_cast<uint2*>(p) = u;
 }
 
+// Cache policy of the token loads and of the fp32 token stores of these
+// kernels (0 default, 2 nontemporal).  Nontemporal fp32 stores measured about
+// 5% faster on the cfg4 maps; nontemporal loads no different.
+#ifndef RACE_NC_LOAD_POLICY
+#define RACE_NC_LOAD_POLICY 0
+#endif
+#ifndef RACE_NC_STORE_POLICY
+#define RACE_NC_STORE_POLICY 2
+#endif
+constexpr int kNcLoadPolicy = RACE_NC_LOAD_POLICY;
+constexpr int kNcStorePolicy = RACE_NC_STORE_POLICY;
+
 // The same through a buffer view (offsets in bytes): out-of-range loads read
 // zeros and out-of-range stores are dropped.
 template <typename TIn>
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
     if constexpr (std::is_same<TIn, float>::value) {
-        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNcLoadPolicy));
     } else {
-        const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+        const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNcLoadPolicy));
         return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
                            __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
     }
@@ -57,7 +69,7 @@ __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
 template <typename TIn>
 __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, const float4& v) {
     if constexpr (std::is_same<TIn, float>::value) {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(mfma::u32x4, v), r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(mfma::u32x4, v), r, off, 0, kNcStorePolicy);
     } else {
         const mfma::u32x2 u{uint32_t(f32_to_bf16(v.x)) | (uint32_t(f32_to_bf16(v.y)) << 16),
                             uint32_t(f32_to_bf16(v.z)) | (uint32_t(f32_to_bf16(v.w)) << 16)};
