@@ -474,10 +474,15 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     };
 
     const int subs = tile / kBC;
-    const float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS;
+    const float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS + 16 * w + lr;
     const int last = ((rows - 1) / kBC) * kBC;
+    // The running mass at a sub-chunk's start is prefetched with its tokens:
+    // loaded where it is used, its wait would also wait for the prefetch of
+    // the next sub-chunk issued just before it.
+    float a0n;
     stage_load(last);
     load_qd(last);
+    a0n = ap[(last / kBC) * kBS];
     for (int r0 = last; r0 >= 0; r0 -= kBC) {
         __syncthreads();
         stage_store();
@@ -489,9 +494,11 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
                 qc[bi][rr] = qreg[bi][rr];
                 dc[bi][rr] = dreg[bi][rr];
             }
+        const float a0 = a0n;
         if (r0 > 0) {
             stage_load(r0 - kBC);
             load_qd(r0 - kBC);
+            a0n = ap[(r0 / kBC - 1) * kBS];
         }
         // Z1 (the suffix state after this sub-chunk) as a plane for dV: row s,
         // four consecutive c per lane.
@@ -506,7 +513,6 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
         // 1: Abar, r, W, alpha; W^T into its plane (row s, four consecutive i).
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
-        const float a0 = ap[(r0 / kBC) * kBS + 16 * w + lr];
         f32x4 wv[2], al[2];
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi) {
@@ -604,15 +610,17 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
             if constexpr (kSplit) dk[bj] = mfma16(uf, al2, dk[bj]);
             dk[bj] = mfma16(uf, ah2, dk[bj]);
         }
-        if (dK) {
+        // The stores are unconditional (a gradient not asked for has an empty
+        // buffer view, which drops them): with one path through the loop the
+        // compiler counts them, and the waits for the prefetched sub-chunk
+        // at the loop's end leave them in flight.
 #pragma unroll
-            for (int bj = 0; bj < 2; ++bj)
+        for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    store1<TIn>(dkr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dk[bj][rr]);
-        }
+            for (int rr = 0; rr < 4; ++rr)
+                store1<TIn>(dkr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dk[bj][rr]);
         // 4: dV[j][c] for c-block w.
-        if (dV) {
+        {
             f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
