@@ -75,6 +75,9 @@ PHASES = {
     (False, "valu"): ["tile_sums", "tile_reduce", "token_map"],
     (True, "mfma"): ["tile_sums_mfma", "tile_scan", "output_pass_mfma"],
 }
+# Non-causal forwards with at most this many tiles per stream add the tile
+# records inside the map (no tile_reduce launch), as race_api.hip does.
+NONCAUSAL_FOLD_TILES = 4
 # Backward launch sequences (every gradient requested).
 BWD_PHASES = {
     True: ["bwd_tile_sums", "tile_scan", "bwd_dq", "suffix_scan", "bwd_dkv"],
@@ -608,11 +611,14 @@ def main() -> int:
             n_used += n
         return n_used
 
+    fwd_names = PHASES.get((cfg.causal, family), [])
+    if not cfg.causal and tiles <= NONCAUSAL_FOLD_TILES:
+        fwd_names = [n for n in fwd_names if n != "tile_reduce"]
     names = []
     if run_hash:
         names += ["hash_q", "hash_k"]
     if run_fwd:
-        names += PHASES.get((cfg.causal, family), [])
+        names += fwd_names
     if run_bwd:
         names += BWD_PHASES[cfg.causal]
 
@@ -660,7 +666,7 @@ def main() -> int:
     n_gaps = n_events - 1
     gaps = [statistics.fmean(events.elapsed_ms(ev[j], ev[j + 1]) for ev in per_step)
             for j in range(n_gaps)]
-    n_fwd = len(PHASES.get((cfg.causal, family), [])) if run_fwd else 0
+    n_fwd = len(fwd_names) if run_fwd else 0
     if run_fwd and run_bwd:
         gaps = gaps[:n_fwd] + gaps[n_fwd + 1:]
     if run_hash:  # the forward's first event follows the hashing's last one

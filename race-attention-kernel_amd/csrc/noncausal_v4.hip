@@ -308,11 +308,19 @@ __global__ __launch_bounds__(kThreads) void outer64_kernel(
 // NV: 16-byte token vectors each thread stages per block.
 __device__ __forceinline__ int xsw(int a) { return (a >> 2) & 7; }
 
+// Sum of `parts` values `stride` apart, in order (parts = 1: one load).
+__device__ __forceinline__ float sum_parts(const float* __restrict__ p, int parts, int64_t stride) {
+    float v = p[0];
+    for (int t = 1; t < parts; ++t) v += p[t * stride];
+    return v;
+}
+
 // Ms[a][c] = M[a][c0 + c] of the map operand for stream n (divided by its
 // divisor when it has one) for the slice's columns c < ncols, zero beyond,
-// a < Wa.  The loads go out in groups of 8 before their LDS stores: a plain
-// loop waited for each load before the next (one memory round trip per
-// element).
+// a < Wa; the first token block's workgroups also save the undivided values
+// when the operand asks for it.  The loads go out in groups of 8 before
+// their LDS stores: a plain loop waited for each load before the next (one
+// memory round trip per element).
 __device__ __forceinline__ void stage_slice(float* __restrict__ Ms, const MapOperand& op,
                                             int64_t n, int Wa, int c0, int ncols) {
     constexpr int kRows = kThreads / kSliceCols;  // rows of the slice per pass
@@ -321,18 +329,27 @@ __device__ __forceinline__ void stage_slice(float* __restrict__ Ms, const MapOpe
     const int cg = c0 + (ok ? c : 0);  // in bounds either way
     const float* col = op.m + n * op.stream + cg * op.col;
     const float* dv = op.div ? op.div + n * op.div_stream : nullptr;
+    float* sv = op.save && blockIdx.x == 0 ? op.save + n * op.save_stream : nullptr;
     for (int ab = 0; ab < Wa; ab += 8 * kRows) {
         float v[8], q[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const int a = min(ab + a0 + m * kRows, Wa - 1);  // clamped: no branch
-            v[m] = col[a * op.row];
-            q[m] = dv ? dv[op.div_by_col ? cg : a] : 0.f;
+            v[m] = sum_parts(col + a * op.row, op.parts, op.part_stride);
+            q[m] = dv ? sum_parts(dv + (op.div_by_col ? cg : a), op.parts, op.part_stride) : 0.f;
         }
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const int a = ab + a0 + m * kRows;
-            if (a < Wa) Ms[a * kSliceCols + c] = ok ? (dv ? v[m] / (q[m] + kEps) : v[m]) : 0.f;
+            if (a >= Wa) continue;
+            Ms[a * kSliceCols + c] = ok ? (dv ? v[m] / (q[m] + kEps) : v[m]) : 0.f;
+            if (sv && ok) {
+                sv[a * op.row + cg * op.col] = v[m];
+                // Each divisor once: by its column's threads in the first
+                // slice (by column) or by column 0 of the first slice (by row).
+                if (dv && (op.div_by_col ? a == 0 : (c == 0 && blockIdx.z == 0)))
+                    sv[op.save_div_off + (op.div_by_col ? cg : a)] = q[m];
+            }
         }
     }
 }

@@ -127,6 +127,11 @@ FwdLayout fwd_layout(const Problem& p, int causal) {
     return l;
 }
 
+// Non-causal forwards with at most this many tiles per stream sum the tile
+// records as the map stages its matrix (every map workgroup of a stream sums
+// them again); longer ones reduce them once into E first.
+constexpr int64_t kFoldTiles = 4;
+
 struct BwdLayout {
     int64_t records = 0, dB = 0, dA = 0;
     int64_t total() const { return records + dB + dA; }
@@ -317,16 +322,31 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
         return marks->mark(stream);
     }
 
-    // The totals go straight to E (and to the state when asked for).
-    float* E = records + l.records;
     RACE_TRY(marks->mark(stream));
     RACE_TRY(outer_sums(probsK, V, records, p, p.S, p.d, stream));
     RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_tile_reduce(records, nullptr, state, E, p, stream));
-    RACE_TRY(marks->mark(stream));
-    // out = q . E: M[a][c] = E[a*d + c].
-    RACE_TRY(token_map(probsQ, out, map_operand(E, int64_t(p.S) * p.d, p.d, 1), p, p.S, p.d,
-                       stream));
+    const int64_t Sd = int64_t(p.S) * p.d;
+    if (p.tiles > kFoldTiles) {
+        float* E = records + l.records;
+        RACE_TRY(launch_tile_reduce(records, nullptr, state, E, p, stream));
+        RACE_TRY(marks->mark(stream));
+        // out = q . E: M[a][c] = E[a*d + c].
+        RACE_TRY(token_map(probsQ, out, map_operand(E, Sd, p.d, 1), p, p.S, p.d, stream));
+        return marks->mark(stream);
+    }
+    // out = q . E with E[s][c] = B[s][c] / (A[s] + eps), B and A the sums of
+    // the tile records in tile order, formed as the map stages its matrix
+    // (M[a = s][c]); the first token block's workgroups also write the
+    // totals to the state when it is asked for.
+    MapOperand op = map_operand(records, p.tiles * p.rec, p.d, 1);
+    op.parts = int(p.tiles);
+    op.part_stride = p.rec;
+    op.div = records + Sd;
+    op.div_stream = p.tiles * p.rec;
+    op.save = state;
+    op.save_stream = Sd + p.S;
+    op.save_div_off = Sd;
+    RACE_TRY(token_map(probsQ, out, op, p, p.S, p.d, stream));
     return marks->mark(stream);
 }
 

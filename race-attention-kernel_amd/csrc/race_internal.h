@@ -89,15 +89,24 @@ hipError_t launch_causal_output_valu(const void* q, const void* k, const void* v
 //     M[a][c] = m[n * stream + a * row + c * col]
 // divided by (div[n * div_stream + (div_by_col ? c : a)] + eps) when div is
 // given (E = B / (A + eps) read straight from a state), and bias[n *
-// bias_stream + c] added to every output row when bias is given.
+// bias_stream + c] added to every output row when bias is given.  With
+// parts > 1 every read of m and div is the sum, in order, of `parts` values
+// part_stride apart (per-tile records summed on the fly).  When save is
+// given, the workgroups of the first token block also write the (summed,
+// undivided) values to save[n * save_stream + a * row + c * col] and the
+// divisors to save[n * save_stream + save_div_off + (div_by_col ? c : a)].
 struct MapOperand {
     const float* m = nullptr;
     int64_t stream = 0, row = 0, col = 0;
+    int parts = 1;
+    int64_t part_stride = 0;
     const float* div = nullptr;
     int64_t div_stream = 0;
     bool div_by_col = false;
     const float* bias = nullptr;
     int64_t bias_stream = 0;
+    float* save = nullptr;
+    int64_t save_stream = 0, save_div_off = 0;
 };
 // out[n][t][c] = sum_a x[n][t][a] * M[a][c] (+ bias[c]) for the operand's M.
 hipError_t launch_token_map(const void* x, void* out, const MapOperand& op, const Problem& p,

@@ -369,10 +369,24 @@ __global__ __launch_bounds__(kThreads) void token_map_kernel(
     const int cnt = int(min<int64_t>(kMapTokens, T - t0));
     const float* Mn = op.m + n * op.stream;
     const float* dv = op.div ? op.div + n * op.div_stream : nullptr;
+    float* sv = op.save && blockIdx.x == 0 ? op.save + n * op.save_stream : nullptr;
     for (int e = tid; e < Wa * kSliceCols; e += kThreads) {
         const int a = e / kSliceCols, c = e - a * kSliceCols;
-        float v = c < ncols ? Mn[a * op.row + (c0 + c) * op.col] : 0.f;
-        if (dv && c < ncols) v = v / (dv[op.div_by_col ? c0 + c : a] + kEps);
+        float v = 0.f;
+        if (c < ncols) {
+            const int64_t mi = a * op.row + (c0 + c) * op.col;
+            v = Mn[mi];
+            for (int t = 1; t < op.parts; ++t) v += Mn[mi + t * op.part_stride];
+            if (sv) sv[mi] = v;
+            if (dv) {
+                const int di = op.div_by_col ? c0 + c : a;
+                float q = dv[di];
+                for (int t = 1; t < op.parts; ++t) q += dv[di + t * op.part_stride];
+                if (sv && (op.div_by_col ? a == 0 : (c == 0 && blockIdx.z == 0)))
+                    sv[op.save_div_off + di] = q;
+                v = v / (q + kEps);
+            }
+        }
         Ms[e] = v;
     }
     const TIn* xn = x + n * T * Wa;
