@@ -55,7 +55,8 @@ constexpr int kNcLoadPolicy = RACE_NC_LOAD_POLICY;
 constexpr int kNcStorePolicy = RACE_NC_STORE_POLICY;
 
 // The same through a buffer view (offsets in bytes): out-of-range loads read
-// zeros and out-of-range stores are dropped.
+// zeros and out-of-range stores are dropped.  kOutside is past any view.
+constexpr int kOutside = 0x7ffffff0;
 template <typename TIn>
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
     if constexpr (std::is_same<TIn, float>::value) {
@@ -389,7 +390,6 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
     const int64_t wg_rows = min(T - wg_t0, int64_t(kMapBlocks) * kMapTokens4);
     const auto xr = mfma::make_rsrc(x + (n * T + wg_t0) * Wa, wg_rows * Wa * int64_t(sizeof(TIn)));
     const auto orr = mfma::make_rsrc(out + (n * T + wg_t0) * Wb, wg_rows * Wb * int64_t(sizeof(TIn)));
-    constexpr int kOutside = 0x7ffffff0;  // past any buffer
 
     // The next block's token vectors are loaded into registers while the
     // current block computes.
@@ -484,7 +484,6 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
     const int64_t wg_rows = min(T - wg_t0, int64_t(kMap64Blocks) * kMap64Tokens);
     const auto xr = mfma::make_rsrc(x + (n * T + wg_t0) * Wa, wg_rows * Wa * int64_t(sizeof(TIn)));
     const auto orr = mfma::make_rsrc(out + (n * T + wg_t0) * Wb, wg_rows * Wb * int64_t(sizeof(TIn)));
-    constexpr int kOutside = 0x7ffffff0;  // past any buffer: the store is dropped
 
     float4 pre[NV];
     auto fetch = [&](int r0) {
