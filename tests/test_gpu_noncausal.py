@@ -142,3 +142,27 @@ def test_golden_gradients(race, cuda):
     assert per_stream_rel_err(to_np(dk), gd["grad_dk"]) <= 1e-5
     assert per_stream_rel_err(to_np(dv), gd["grad_dv"]) <= 1e-5
 
+
+
+@pytest.mark.parametrize("L, R, d", [(4, 16, 64), (2, 8, 32), (3, 5, 7)])
+def test_tile_sums_inside_the_map_match_the_separate_reduce(race, cuda, L, R, d):
+    # With at most 4 tiles per stream the forward's map adds the tile records
+    # itself (and writes the saved state); with more, a separate reduce forms
+    # E first.  Both must give the oracle's totals and the same output.
+    say("nc-fold", L, R, d)
+    T = 2000
+    q, k, v = race.make_inputs(3, T, L, R, d, seed=12)
+    qc, kc, vc = (x.to(cuda) for x in (q, k, v))
+    runs = {tile: race.race_fused_fwd_with_state(qc, kc, vc, causal=False, tile_tokens=tile)
+            for tile in (64, 512, 2048)}  # 32 tiles (reduce), 4 and 1 (in the map)
+    torch.cuda.synchronize()
+    k64, v64 = to_np(k).astype(np.float64), to_np(v).astype(np.float64)
+    S = L * R
+    B = np.einsum("nts,ntc->nsc", k64, v64).reshape(3, S * d)
+    A = k64.sum(1)
+    want_state = np.concatenate([B, A], axis=1)
+    out64, _ = runs[64]
+    # fp32 sums of up to 2000 terms: about 2e-6 of the largest total.
+    for tile, (out, state) in runs.items():
+        assert per_stream_rel_err(to_np(state), want_state) <= 1e-5, tile
+        assert per_stream_rel_err(to_np(out), to_np(out64).astype(np.float64)) <= 1e-5, tile
