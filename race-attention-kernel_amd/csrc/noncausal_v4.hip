@@ -7,12 +7,14 @@
 //              (B = K^T V and A in the forward, dE = Q^T dOut in the backward)
 //   map        out[t][c] = sum_a x[t][a] M[a][c] (+ bias[c])
 //              (out = Q E, dQ = dOut E^T, dK = V dB^T + dA, dV = K dB)
-// Both are fp32 vector-ALU code (no matrix cores): every thread owns 4 x 4
-// register tiles, operands are read from LDS as 16-byte vectors, and tokens
-// are staged with 16-byte (fp32) or 8-byte (bf16) coalesced loads.  A
-// reduction workgroup owns one chunk of one stream's tokens and writes the
-// chunk's partial sums to a record; the fixed-order reduce over chunks
-// (tile_reduce_kernel) adds them, so results are bitwise reproducible.
+// Both are fp32 vector-ALU code (no matrix cores): every thread owns a
+// register tile (8 x 4 for 64-wide operands, 4 x 4 otherwise), operands are
+// read from LDS as 16-byte vectors, and tokens are staged with 16-byte
+// (fp32) or 8-byte (bf16) coalesced loads.  A reduction workgroup owns one
+// chunk of one stream's tokens and writes the chunk's partial sums to a
+// record; the records are added in chunk order (by the map that stages the
+// matrix, by the backward's finalize, or by tile_reduce_kernel for long
+// sequences), so results are bitwise reproducible.
 #include "mfma_common.h"
 
 namespace race {

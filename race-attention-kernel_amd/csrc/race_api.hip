@@ -328,7 +328,7 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
     const int64_t Sd = int64_t(p.S) * p.d;
     if (p.tiles > kFoldTiles) {
         float* E = records + l.records;
-        RACE_TRY(launch_tile_reduce(records, nullptr, state, E, p, stream));
+        RACE_TRY(launch_tile_reduce(records, state, E, p, stream));
         RACE_TRY(marks->mark(stream));
         // out = q . E: M[a][c] = E[a*d + c].
         RACE_TRY(token_map(probsQ, out, map_operand(E, Sd, p.d, 1), p, p.S, p.d, stream));

@@ -78,10 +78,10 @@ hipError_t launch_tile_outer_sums(const void* x, const void* y, float* records, 
 // scan runs from the last tile to the first.
 hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipStream_t stream,
                             bool reverse = false);
-// Totals over tiles into `totals` ([N][rec]) and, when not null, into
-// `state` ([N][S*d+S]); E = B / (A + eps) into `E` ([N][S][d]) when not null.
-hipError_t launch_tile_reduce(const float* records, float* totals, float* state, float* E,
-                              const Problem& p, hipStream_t stream);
+// Totals over tiles into `state` ([N][S*d+S]) when not null, and E = B /
+// (A + eps) into `E` ([N][S][d]).
+hipError_t launch_tile_reduce(const float* records, float* state, float* E, const Problem& p,
+                              hipStream_t stream);
 // Causal output pass from the scanned records.
 hipError_t launch_causal_output_valu(const void* q, const void* k, const void* v, void* out,
                                      const float* records, const Problem& p, hipStream_t stream);

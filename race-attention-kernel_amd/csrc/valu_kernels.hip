@@ -210,20 +210,19 @@ __device__ __forceinline__ float sum_over_tiles(const float* __restrict__ r, int
     return sum;
 }
 
-// Totals over tiles (fixed order) into whichever of totals (the record
-// layout) and state ([S*d + S]) are given.  The thread of B element (s, c)
-// also sums A[s] in the same order as the thread of A element s, so E uses
-// exactly the A that is stored.
+// Totals over tiles (fixed order) into the state ([S*d + S]) when it is
+// given, and E = B / (A + eps).  The thread of B element (s, c) also sums
+// A[s] in the same order as the thread of A element s, so E uses exactly the
+// A that is stored.
 __global__ __launch_bounds__(kThreads) void tile_reduce_kernel(
-    const float* __restrict__ records, float* __restrict__ totals, float* __restrict__ state,
-    float* __restrict__ E, int64_t tiles, int64_t rec, int S, int d) {
+    const float* __restrict__ records, float* __restrict__ state, float* __restrict__ E,
+    int64_t tiles, int64_t rec, int S, int d) {
     const int e = blockIdx.x * kThreads + threadIdx.x;
     const int64_t n = blockIdx.y;
     const int used = S * d + S;
     if (e >= used) return;
     const float* r = records + n * tiles * rec;
     const float sum = sum_over_tiles(r + e, tiles, rec);
-    if (totals) totals[n * rec + e] = sum;
     if (state) state[n * used + e] = sum;
     if (E && e < S * d) {
         const int s = e / d;
@@ -461,12 +460,11 @@ hipError_t launch_tile_scan(float* records, float* state, const Problem& p, hipS
     return hipGetLastError();
 }
 
-hipError_t launch_tile_reduce(const float* records, float* totals, float* state, float* E,
-                              const Problem& p, hipStream_t stream) {
+hipError_t launch_tile_reduce(const float* records, float* state, float* E, const Problem& p,
+                              hipStream_t stream) {
     const int used = p.S * p.d + p.S;
     const dim3 grid(unsigned((used + kThreads - 1) / kThreads), unsigned(p.N));
-    tile_reduce_kernel<<<grid, kThreads, 0, stream>>>(records, totals, state, E, p.tiles, p.rec,
-                                                      p.S, p.d);
+    tile_reduce_kernel<<<grid, kThreads, 0, stream>>>(records, state, E, p.tiles, p.rec, p.S, p.d);
     return hipGetLastError();
 }
 
