@@ -379,11 +379,9 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
     const int64_t n = blockIdx.y;
     const int c0 = blockIdx.z * kSliceCols;
     const int ncols = min(kSliceCols, Wb - c0);
-    stage_slice(Ms, op, n, Wa, c0, ncols);
     const int va = Wa / 4;
     const int nvec = kMapTokens4 * va;
     const int tt = tid >> 4, cc = tid & 15;
-    const float4 bv = slice_bias(op, n, c0, cc, ncols);
     // Buffer views of the workgroup's rows (rows past T read as zero, their
     // stores are dropped): every load and store is unconditional, so the
     // compiler neither waits for each load in turn nor, with the block loop
@@ -404,7 +402,11 @@ __global__ __launch_bounds__(kThreads) void map4_kernel(
             pre[m] = buf_load4<TIn>(xr, e < nvec ? ((r0 + i) * Wa + 4 * u) * int(sizeof(TIn)) : kOutside);
         }
     };
+    // The first block's tokens are requested before the matrix slice is
+    // staged, so the two round trips overlap.
     fetch(0);
+    stage_slice(Ms, op, n, Wa, c0, ncols);
+    const float4 bv = slice_bias(op, n, c0, cc, ncols);
 #pragma unroll
     for (int blk = 0; blk < kMapBlocks; ++blk) {
         const int r0 = blk * kMapTokens4;
@@ -473,9 +475,7 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
     const int64_t n = blockIdx.y;
     const int c0 = blockIdx.z * kSliceCols;
     const int ncols = min(kSliceCols, Wb - c0);
-    stage_slice(Ms, op, n, Wa, c0, ncols);
     const int tt = tid >> 4, cc = tid & 15;  // tokens 8 tt .. 8 tt + 7, columns 4 cc .. 4 cc + 3
-    const float4 bv = slice_bias(op, n, c0, cc, ncols);
     // Buffer views of the workgroup's rows: rows past T read as zero and
     // their stores are dropped, so every load and store is unconditional.
     // With the block loop unrolled the compiler then counts the stores
@@ -496,7 +496,11 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
             pre[m] = buf_load4<TIn>(xr, ((r0 + i) * Wa + 4 * u) * int(sizeof(TIn)));
         }
     };
+    // The first block's tokens are requested before the matrix slice is
+    // staged, so the two round trips overlap.
     fetch(0);
+    stage_slice(Ms, op, n, Wa, c0, ncols);
+    const float4 bv = slice_bias(op, n, c0, cc, ncols);
 #pragma unroll
     for (int blk = 0; blk < kMap64Blocks; ++blk) {
         const int r0 = blk * kMap64Tokens;
