@@ -73,7 +73,9 @@ def test_workspace_bytes_for_explicit_tiles(race):
     st, nc_bytes, _, _ = abi.fwd_workspace_bytes(sh, False, abi.options(1024, abi.RACE_KERNEL_VALU))
     assert st == 0 and nc_bytes == (8 * 64 * 4160 + 8 * 64 * 64) * 4
     st, bwd_bytes = abi.noncausal_bwd_workspace_bytes(sh, abi.options(1024, 0))
-    assert st == 0 and bwd_bytes > nc_bytes
+    # The dE tile records, then dB [N][S*d] and dA [N][S] (each region a
+    # multiple of 64 floats).
+    assert st == 0 and bwd_bytes == (8 * 64 * 4160 + 8 * 64 * 64 + 8 * 64) * 4
     # Causal backward: forward and suffix records, the running mass per 16
     # tokens and an fp32 copy of dQ.
     st, cb_bytes = abi.causal_bwd_workspace_bytes(sh, abi.options(1024, 0))
