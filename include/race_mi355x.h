@@ -228,6 +228,20 @@ race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* 
                             const race_shape* shape, const race_options* opts, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* race_causal_bwd from the forward's scanned tile records instead of
+ * recomputing them: fwd_records is race_fwd's workspace after a causal call
+ * with the same inputs and tile length ([N][tiles][rec], the exclusive prefix
+ * state at each tile start), and opts->tile_tokens must be that tile length
+ * (explicit, > 0).  The workspace is race_causal_bwd_workspace_bytes for the
+ * same opts.  An autograd forward that keeps its records (260 B per token at
+ * the cfg2 shape) then skips the backward's tile totals and scan.  No
+ * counterpart in the reference, which has no causal backward kernel. */
+race_status race_causal_bwd_from_records(const void* probsQ, const void* probsK, const void* V,
+                                         const void* dOut, const float* fwd_records, void* dQ,
+                                         void* dK, void* dV, const race_shape* shape,
+                                         const race_options* opts, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream);
+
 /* The bucket probabilities the op consumes, from the token rows: the hashing
  * of the reference's BatchedACE.forward (src/race_baseline.py:41-44).  For
  * each of `rows` rows x (head_dim values) and table l < num_tables, with

@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "race_noncausal_bwd",
     "race_causal_bwd_workspace_bytes",
     "race_causal_bwd",
+    "race_causal_bwd_from_records",
     "race_noncausal_bwd_profiled",
     "race_causal_bwd_profiled",
     "race_hash_probs",
@@ -107,6 +108,8 @@ def lib() -> ctypes.CDLL:
         L.race_noncausal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_causal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_causal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
+        L.race_causal_bwd_from_records.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp,
+                                                   sz, vp]
         L.race_noncausal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz,
                                                   vp, ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         L.race_causal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp,
@@ -233,6 +236,15 @@ def causal_bwd(q: int, k: int, v: int, g: int, dq: int | None, dk: int | None, d
     return lib().race_causal_bwd(q, k, v, g, dq, dk, dv, ctypes.byref(sh),
                                  ctypes.byref(opts) if opts is not None else None,
                                  workspace, workspace_bytes, stream)
+
+
+def causal_bwd_from_records(q: int, k: int, v: int, g: int, fwd_records: int | None,
+                            dq: int | None, dk: int | None, dv: int | None, sh: RaceShape,
+                            opts: RaceOptions | None, workspace: int | None, workspace_bytes: int,
+                            stream: int) -> int:
+    return lib().race_causal_bwd_from_records(q, k, v, g, fwd_records, dq, dk, dv, ctypes.byref(sh),
+                                              ctypes.byref(opts) if opts is not None else None,
+                                              workspace, workspace_bytes, stream)
 
 
 def noncausal_bwd_profiled(q, k, v, g, state, dq, dk, dv, sh: RaceShape, opts, workspace,

@@ -566,9 +566,10 @@ namespace race {
 namespace {
 
 race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* V,
-                            const void* dOut, void* dQ, void* dK, void* dV,
-                            const race_shape* shape, const race_options* opts, void* workspace,
-                            size_t workspace_bytes, hipStream_t stream, Marks* marks) {
+                            const void* dOut, const float* fwd_records, void* dQ, void* dK,
+                            void* dV, const race_shape* shape, const race_options* opts,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream,
+                            Marks* marks) {
     // The tile policy is the vector-ALU one; the kernel family is chosen here.
     const int kernel = kernel_choice(opts);
     if (kernel != RACE_KERNEL_AUTO && kernel != RACE_KERNEL_VALU && kernel != RACE_KERNEL_MFMA)
@@ -581,6 +582,9 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     const bool use_mfma = kernel != RACE_KERNEL_VALU && causal_bwd_mfma_supported(p.S, p.d) &&
                           p.tile % 32 == 0;
     if (kernel == RACE_KERNEL_MFMA && !use_mfma) return RACE_ERROR_INVALID_VALUE;
+    // Saved forward records come with the forward's (explicit) tile length.
+    if (fwd_records && (!opts || opts->tile_tokens <= 0 || !aligned16(fwd_records)))
+        return RACE_ERROR_INVALID_VALUE;
     if (p.N == 0 || p.T == 0 || (!dQ && !dK && !dV)) return RACE_SUCCESS;
     if (!probsQ || !probsK || !V || !dOut) return RACE_ERROR_INVALID_VALUE;
     if (!aligned16(probsQ) || !aligned16(probsK) || !aligned16(V) || !aligned16(dOut))
@@ -594,8 +598,8 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     RACE_TRY(max_lds(&lds_limit));
     const int C = causal_bwd_chunk(p.S, p.d, lds_limit);
     if (C == 0 || (use_mfma && C != 32)) return RACE_ERROR_INVALID_VALUE;
-    float* fwd_rec = static_cast<float*>(workspace);
-    float* bwd_rec = fwd_rec + l.fwd;
+    float* fwd_ws = static_cast<float*>(workspace);
+    float* bwd_rec = fwd_ws + l.fwd;
     float* apre = bwd_rec + l.bwd;
     float* dq32 = apre + l.apre;
     // B3 reads dQ back in fp32.  An fp32 dQ is that copy: B1 writes it once,
@@ -606,15 +610,20 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         dq_out = nullptr;
     }
 
-    // Prefix state at every tile start (the forward's tile totals and scan).
+    // Prefix state at every tile start: the saved forward records, or the
+    // forward's tile totals and scan again.
     RACE_TRY(marks->mark(stream));
-    if (direct_sums_supported(p.S, p.d) && p.tile % 64 == 0)
-        RACE_TRY(launch_tile_sums_direct(probsK, V, fwd_rec, p, stream));
-    else
-        RACE_TRY(launch_tile_outer_sums(probsK, V, fwd_rec, p, p.S, p.d, stream));
-    RACE_TRY(marks->mark(stream));
-    RACE_TRY(launch_tile_scan(fwd_rec, nullptr, p, stream));
-    RACE_TRY(marks->mark(stream));
+    const float* fwd_rec = fwd_records;
+    if (!fwd_rec) {
+        if (direct_sums_supported(p.S, p.d) && p.tile % 64 == 0)
+            RACE_TRY(launch_tile_sums_direct(probsK, V, fwd_ws, p, stream));
+        else
+            RACE_TRY(launch_tile_outer_sums(probsK, V, fwd_ws, p, p.S, p.d, stream));
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(launch_tile_scan(fwd_ws, nullptr, p, stream));
+        RACE_TRY(marks->mark(stream));
+        fwd_rec = fwd_ws;
+    }
     if (use_mfma)
         RACE_TRY(launch_causal_bwd_dq_mfma(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec,
                                            bwd_rec, p, stream));
@@ -658,8 +667,19 @@ race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* 
                             const race_shape* shape, const race_options* opts, void* workspace,
                             size_t workspace_bytes, hipStream_t stream) {
     Marks none;
-    return causal_bwd_impl(probsQ, probsK, V, dOut, dQ, dK, dV, shape, opts, workspace,
+    return causal_bwd_impl(probsQ, probsK, V, dOut, nullptr, dQ, dK, dV, shape, opts, workspace,
                            workspace_bytes, stream, &none);
+}
+
+race_status race_causal_bwd_from_records(const void* probsQ, const void* probsK, const void* V,
+                                         const void* dOut, const float* fwd_records, void* dQ,
+                                         void* dK, void* dV, const race_shape* shape,
+                                         const race_options* opts, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+    Marks none;
+    if (!fwd_records) return RACE_ERROR_INVALID_VALUE;
+    return causal_bwd_impl(probsQ, probsK, V, dOut, fwd_records, dQ, dK, dV, shape, opts,
+                           workspace, workspace_bytes, stream, &none);
 }
 
 race_status race_causal_bwd_profiled(const void* probsQ, const void* probsK, const void* V,
@@ -671,7 +691,7 @@ race_status race_causal_bwd_profiled(const void* probsQ, const void* probsK, con
     Marks marks;
     marks.events = events;
     marks.max = max_events;
-    const race_status st = causal_bwd_impl(probsQ, probsK, V, dOut, dQ, dK, dV, shape, opts,
+    const race_status st = causal_bwd_impl(probsQ, probsK, V, dOut, nullptr, dQ, dK, dV, shape, opts,
                                            workspace, workspace_bytes, stream, &marks);
     *n_events = marks.n;
     return st;

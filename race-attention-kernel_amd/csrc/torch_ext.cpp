@@ -229,15 +229,42 @@ noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
     return {opt(need_q, dq), opt(need_k, dk), opt(need_v, dv)};
 }
 
+// Causal forward for autograd: (out, scanned tile records [N, tiles, rec],
+// tile length), the records being what the backward can start from.
+std::tuple<at::Tensor, at::Tensor, int64_t> forward_with_records(const at::Tensor& q,
+                                                                 const at::Tensor& k,
+                                                                 const at::Tensor& v,
+                                                                 int64_t tile_tokens,
+                                                                 int64_t kernel) {
+    FwdResult r = run_forward(q, k, v, true, tile_tokens, kernel, false);
+    const int64_t N = q.size(0);
+    at::Tensor records;
+    if (r.tiles > 0 && N > 0)
+        records = r.workspace.narrow(0, 0, N * r.tiles * r.rec).view({N, r.tiles, r.rec});
+    else
+        records = at::zeros({N, 0, r.rec}, v.options().dtype(at::kFloat));
+    return {r.out, records, r.tile};
+}
+
 std::tuple<c10::optional<at::Tensor>, c10::optional<at::Tensor>, c10::optional<at::Tensor>>
 causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                 const at::Tensor& grad_out, bool need_q, bool need_k, bool need_v,
-                int64_t tile_tokens, int64_t kernel) {
+                int64_t tile_tokens, int64_t kernel, const c10::optional<at::Tensor>& fwd_records) {
     const race_shape sh = validate(q, k, v);
     check_token_tensor(grad_out, "dOut", q);
     TORCH_CHECK(grad_out.sizes() == v.sizes(), "dOut shape ", grad_out.sizes(), " differs from V ",
                 v.sizes());
     const race_options opts = make_options(tile_tokens, kernel);
+    if (fwd_records) {
+        const at::Tensor& rec = *fwd_records;
+        TORCH_CHECK(tile_tokens > 0, "saved forward records need the forward's tile length");
+        TORCH_CHECK(rec.device() == q.device() && rec.scalar_type() == at::kFloat &&
+                        rec.is_contiguous() && rec.dim() == 3 && rec.size(0) == q.size(0),
+                    "fwd_records must be the forward's contiguous fp32 [N, tiles, rec] records");
+        const int64_t tiles = (q.size(1) + tile_tokens - 1) / tile_tokens;
+        TORCH_CHECK(rec.size(1) == tiles, "fwd_records has ", rec.size(1), " tiles, the tile length ",
+                    tile_tokens, " gives ", tiles);
+    }
     const c10::DeviceGuard guard(q.device());
     at::Tensor dq, dk, dv;
     if (need_q) dq = at::empty_like(q);
@@ -248,11 +275,20 @@ causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                  "race_causal_bwd_workspace_bytes");
     at::Tensor ws = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
     const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
-    check_status(race_causal_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
-                                 need_q ? dq.data_ptr() : nullptr, need_k ? dk.data_ptr() : nullptr,
-                                 need_v ? dv.data_ptr() : nullptr, &sh, &opts, ws.data_ptr(), bytes,
-                                 stream),
-                 "race_causal_bwd");
+    if (fwd_records && fwd_records->numel() > 0)
+        check_status(race_causal_bwd_from_records(
+                         q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                         fwd_records->data_ptr<float>(), need_q ? dq.data_ptr() : nullptr,
+                         need_k ? dk.data_ptr() : nullptr, need_v ? dv.data_ptr() : nullptr, &sh,
+                         &opts, ws.data_ptr(), bytes, stream),
+                     "race_causal_bwd_from_records");
+    else
+        check_status(race_causal_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                                     need_q ? dq.data_ptr() : nullptr,
+                                     need_k ? dk.data_ptr() : nullptr,
+                                     need_v ? dv.data_ptr() : nullptr, &sh, &opts, ws.data_ptr(),
+                                     bytes, stream),
+                     "race_causal_bwd");
     auto opt = [](bool need, const at::Tensor& t) -> c10::optional<at::Tensor> {
         if (need) return t;
         return c10::nullopt;
@@ -534,7 +570,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("causal_backward", &causal_backward, "Causal backward -> (dQ, dK, dV)",
           py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("dOut"),
           py::arg("need_q") = true, py::arg("need_k") = true, py::arg("need_v") = true,
-          py::arg("tile_tokens") = 0, py::arg("kernel") = 0);
+          py::arg("tile_tokens") = 0, py::arg("kernel") = 0, py::arg("fwd_records") = py::none());
+    m.def("forward_with_records", &forward_with_records,
+          "Causal forward -> (out, scanned tile records, tile length) for the backward",
+          py::arg("probsQ"), py::arg("probsK"), py::arg("V"), py::arg("tile_tokens") = 0,
+          py::arg("kernel") = 0);
     m.def("hash_probs", &hash_probs, "Bucket probabilities of token rows -> [..., L, 2^K]",
           py::arg("x"), py::arg("planes_T"), py::arg("L"), py::arg("K"));
     m.def("select_tile_tokens", &select_tile_tokens, "Tile length a forward would use",

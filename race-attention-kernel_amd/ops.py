@@ -16,8 +16,10 @@ The autograd wrapper follows the reference's non-causal op
 small per-bucket state), is once_differentiable, makes the incoming gradient
 dense and returns only the gradients autograd asks for.  The causal backward
 has no counterpart in the reference (its design outline is
-docs/causal_v2_design.md:689-742); here it recomputes the forward's prefix
-states from the saved inputs, so nothing O(T*S*d) is kept.
+docs/causal_v2_design.md:689-742); here the forward keeps its scanned tile
+records (the prefix state at every tile start, O(S*d) per tile, 260 bytes
+per token at the cfg2 shape) and the backward starts from them instead of
+recomputing them; nothing O(T*S*d) is kept.
 """
 from __future__ import annotations
 
@@ -51,16 +53,21 @@ class RaceFusedFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, probsQ, probsK, V, causal, tile_tokens, kernel):
         needs = any(ctx.needs_input_grad[:3])
+        ctx.causal = bool(causal)
+        ctx.tile_tokens = int(tile_tokens)
+        if needs and causal:
+            # The scanned tile records (the prefix state at every tile start)
+            # are kept, so the backward does not recompute them.
+            out, records, tile = _lib.ext().forward_with_records(probsQ, probsK, V,
+                                                                 int(tile_tokens), int(kernel))
+            ctx.tile_tokens = int(tile)
+            ctx.save_for_backward(probsQ, probsK, V, records)
+            return out
         want_state = needs and not causal
         out, state = _lib.ext().forward(probsQ, probsK, V, bool(causal), int(tile_tokens),
                                         int(kernel), want_state)
-        ctx.causal = bool(causal)
-        ctx.tile_tokens = int(tile_tokens)
         if needs:
-            if causal:
-                ctx.save_for_backward(probsQ, probsK, V)
-            else:
-                ctx.save_for_backward(probsQ, probsK, V, state)
+            ctx.save_for_backward(probsQ, probsK, V, state)
         return out
 
     @staticmethod
@@ -70,10 +77,10 @@ class RaceFusedFunction(torch.autograd.Function):
         if not (need_q or need_k or need_v):
             return None, None, None, None, None, None
         if ctx.causal:
-            q, k, v = ctx.saved_tensors
+            q, k, v, records = ctx.saved_tensors
             grad_out = _dense(grad_out.to(v.dtype))
             dq, dk, dv = _lib.ext().causal_backward(q, k, v, grad_out, need_q, need_k, need_v,
-                                                   0, 0)
+                                                   ctx.tile_tokens, 0, records)
             return dq, dk, dv, None, None, None
         q, k, v, state = ctx.saved_tensors
         grad_out = _dense(grad_out.to(v.dtype))

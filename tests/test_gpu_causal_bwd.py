@@ -186,3 +186,31 @@ def test_unsupported_shape_raises(race, cuda):
     q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 64, 8, 32, 128, seed=27, grad_out=True))
     with pytest.raises(RuntimeError, match="race_causal_bwd"):
         race.race_causal_backward(q, k, v, g)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("L, R, d, T", [(4, 16, 64, 3000), (2, 8, 32, 700), (3, 5, 7, 200)])
+def test_backward_from_saved_records_equals_recomputing_them(race, ext, cuda, dtype, L, R, d, T):
+    # Autograd keeps the forward's scanned tile records and the backward
+    # starts from them; recomputing them at the same tile length runs the
+    # same sums and scan, so the gradients are bitwise equal.
+    say("c-bwd records", L, R, d, T, dtype)
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, T, L, R, d, seed=40 + T, dtype=dtype,
+                                                       grad_out=True))
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    race.race_fused_fwd(qg, kg, vg, causal=True).backward(g)
+    _, records, tile = ext.forward_with_records(q, k, v)
+    dq, dk, dv = race.race_causal_backward(q, k, v, g, tile_tokens=tile)
+    torch.cuda.synchronize()
+    assert records.shape == (2, -(-T // tile), records.shape[2])
+    for got, want in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+        assert torch.equal(got, want)
+
+
+def test_saved_records_must_match_the_tile_length(race, ext, cuda):
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 1000, 4, 16, 64, seed=41, grad_out=True))
+    _, records, tile = ext.forward_with_records(q, k, v, tile_tokens=128)
+    with pytest.raises(RuntimeError, match="tiles"):
+        ext.causal_backward(q, k, v, g, True, True, True, 256, 0, records)
+    with pytest.raises(RuntimeError, match="tile length"):
+        ext.causal_backward(q, k, v, g, True, True, True, 0, 0, records)
