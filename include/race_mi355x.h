@@ -228,14 +228,23 @@ race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* 
                             const race_shape* shape, const race_options* opts, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* Workspace of race_causal_bwd_from_records in bytes: race_causal_bwd's
+ * without the forward records region (the caller supplies those).
+ * opts->tile_tokens must be the forward's tile length (explicit, > 0). */
+race_status race_causal_bwd_from_records_workspace_bytes(const race_shape* shape,
+                                                         const race_options* opts, size_t* bytes);
+
 /* race_causal_bwd from the forward's scanned tile records instead of
  * recomputing them: fwd_records is race_fwd's workspace after a causal call
  * with the same inputs and tile length ([N][tiles][rec], the exclusive prefix
  * state at each tile start), and opts->tile_tokens must be that tile length
- * (explicit, > 0).  The workspace is race_causal_bwd_workspace_bytes for the
- * same opts.  An autograd forward that keeps its records (260 B per token at
- * the cfg2 shape) then skips the backward's tile totals and scan.  No
- * counterpart in the reference, which has no causal backward kernel. */
+ * (explicit, > 0).  The workspace is at least
+ * race_causal_bwd_from_records_workspace_bytes for the same opts.  Keeping
+ * the records costs 4 * rec / tile bytes per stream-token (rec = S*d + S
+ * rounded up to 64 floats): 32.5 B at S = d = 64 and a tile of 512, about
+ * 2 KB at S = 256, d = 128 and the minimum tile of 64.  The backward then
+ * skips its own tile totals and scan.  No counterpart in the reference,
+ * which has no causal backward kernel. */
 race_status race_causal_bwd_from_records(const void* probsQ, const void* probsK, const void* V,
                                          const void* dOut, const float* fwd_records, void* dQ,
                                          void* dK, void* dV, const race_shape* shape,

@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "race_noncausal_bwd_workspace_bytes",
     "race_noncausal_bwd",
     "race_causal_bwd_workspace_bytes",
+    "race_causal_bwd_from_records_workspace_bytes",
     "race_causal_bwd",
     "race_causal_bwd_from_records",
     "race_noncausal_bwd_profiled",
@@ -107,6 +108,7 @@ def lib() -> ctypes.CDLL:
         L.race_noncausal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_noncausal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_causal_bwd_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
+        L.race_causal_bwd_from_records_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_causal_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_causal_bwd_from_records.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, shp, opp, vp,
                                                    sz, vp]
@@ -227,6 +229,13 @@ def causal_bwd_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):
     st = lib().race_causal_bwd_workspace_bytes(ctypes.byref(sh),
                                                ctypes.byref(opts) if opts is not None else None,
                                                ctypes.byref(b))
+    return st, b.value
+
+
+def causal_bwd_from_records_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):
+    b = ctypes.c_size_t(0)
+    st = lib().race_causal_bwd_from_records_workspace_bytes(
+        ctypes.byref(sh), ctypes.byref(opts) if opts is not None else None, ctypes.byref(b))
     return st, b.value
 
 

@@ -38,6 +38,12 @@ bool shape_ok(const race_shape* sh) {
 
 int sub(const race_shape* sh) { return sh->num_tables * sh->num_buckets; }
 
+// Whether `tile` rows of `width` elements of `elem` bytes stay below 2^31
+// bytes, the range of one buffer resource.
+bool tile_fits_buffer(int64_t tile, int64_t width, int64_t elem) {
+    return tile * width * elem < (int64_t(1) << 31);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int kernel_choice(const race_options* o) { return o ? o->kernel : RACE_KERNEL_AUTO; }
@@ -101,6 +107,11 @@ race_status make_problem(const race_shape* sh, int causal, const race_options* o
     int tile = 0;
     st = resolve_tile(sh, causal, o, *mfma, &tile);
     if (st != RACE_SUCCESS) return st;
+    // Kernels address a tile's rows through one buffer resource, whose range
+    // is a 32-bit byte count.
+    if (!tile_fits_buffer(tile, sub(sh) > sh->head_dim ? sub(sh) : sh->head_dim,
+                          sh->dtype == RACE_BF16 ? 2 : 4))
+        return RACE_ERROR_INVALID_VALUE;
     p->N = sh->num_streams;
     p->T = sh->seq_len;
     p->S = sub(sh);
@@ -145,17 +156,18 @@ BwdLayout bwd_layout(const Problem& p) {
     return l;
 }
 
-// Causal backward workspace: forward prefix records, suffix records, the
-// running mass at every sub-chunk start (sized for the shortest sub-chunk,
-// 16 tokens) and an fp32 copy of dQ.
+// Causal backward workspace: suffix records, the running mass at every
+// sub-chunk start (sized for the shortest sub-chunk, 16 tokens), an fp32 copy
+// of dQ and, unless the caller hands in the forward's records, the forward
+// prefix records (last, so the two layouts share every other offset).
 struct CausalBwdLayout {
-    int64_t fwd = 0, bwd = 0, apre = 0, dq32 = 0;
-    int64_t total() const { return fwd + bwd + apre + dq32; }
+    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0;
+    int64_t total() const { return bwd + apre + dq32 + fwd; }
 };
 
-CausalBwdLayout causal_bwd_layout(const Problem& p) {
+CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given) {
     CausalBwdLayout l;
-    l.fwd = p.N * p.tiles * p.rec;
+    l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
     l.bwd = p.N * p.tiles * p.rec;
     l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(p.S));
     l.dq32 = round64(p.N * p.T * int64_t(p.S));
@@ -591,17 +603,17 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         return RACE_ERROR_INVALID_VALUE;
     if ((dQ && !aligned16(dQ)) || (dK && !aligned16(dK)) || (dV && !aligned16(dV)))
         return RACE_ERROR_INVALID_VALUE;
-    const CausalBwdLayout l = causal_bwd_layout(p);
+    const CausalBwdLayout l = causal_bwd_layout(p, fwd_records != nullptr);
     if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
         return RACE_ERROR_INVALID_VALUE;
     int lds_limit = 0;
     RACE_TRY(max_lds(&lds_limit));
     const int C = causal_bwd_chunk(p.S, p.d, lds_limit);
     if (C == 0 || (use_mfma && C != 32)) return RACE_ERROR_INVALID_VALUE;
-    float* fwd_ws = static_cast<float*>(workspace);
-    float* bwd_rec = fwd_ws + l.fwd;
+    float* bwd_rec = static_cast<float*>(workspace);
     float* apre = bwd_rec + l.bwd;
     float* dq32 = apre + l.apre;
+    float* fwd_ws = dq32 + l.dq32;
     // B3 reads dQ back in fp32.  An fp32 dQ is that copy: B1 writes it once,
     // into the caller's buffer, and B3 reads it from there.
     void* dq_out = dQ;
@@ -658,7 +670,19 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
     race_options topts = {opts ? opts->tile_tokens : 0, RACE_KERNEL_VALU};
     const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
-    *bytes = size_t(causal_bwd_layout(p).total()) * sizeof(float);
+    *bytes = size_t(causal_bwd_layout(p, false).total()) * sizeof(float);
+    return RACE_SUCCESS;
+}
+
+race_status race_causal_bwd_from_records_workspace_bytes(const race_shape* shape,
+                                                         const race_options* opts, size_t* bytes) {
+    if (!bytes || !opts || opts->tile_tokens <= 0) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    race_options topts = {opts->tile_tokens, RACE_KERNEL_VALU};
+    const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(causal_bwd_layout(p, true).total()) * sizeof(float);
     return RACE_SUCCESS;
 }
 
@@ -769,6 +793,7 @@ race_status alg1_problem(const race_alg1_shape* sh, int32_t variant, int32_t til
     int tile = 0;
     const race_status st = alg1_resolve_tile(sh, variant, tile_tokens, &tile);
     if (st != RACE_SUCCESS) return st;
+    if (!tile_fits_buffer(tile, sh->head_dim, 2)) return RACE_ERROR_INVALID_VALUE;
     p->N = sh->batch_heads;
     p->T = sh->seq_len;
     p->S = sh->num_tables << sh->num_planes;

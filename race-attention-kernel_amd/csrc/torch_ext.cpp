@@ -24,16 +24,21 @@
 //
 // probsQ, probsK: [N, T, L, R] (or [N, T, S], read as L = 1, R = S) and V:
 // [N, T, d], all float32 or all bfloat16, on one HIP device, contiguous,
-// 16-byte aligned.  out has V's dtype; state is fp32.  The pattern follows the
-// reference's binding (src/causal_v2/kernels/torch_binding.cpp:41-53 checks,
-// :139-168 device guard, output and workspace allocation, current stream):
-// TORCH_CHECK failures surface as RuntimeError.
+// 16-byte aligned.  out has V's dtype; state is fp32.  As the reference's
+// binding does (src/causal_v2/kernels/torch_binding.cpp:139-168), every entry
+// point checks its arguments on the host, allocates the outputs and the
+// workspace itself and launches on PyTorch's current stream under a device
+// guard; a rejected argument raises RuntimeError naming the entry point, the
+// argument and the rule it broke.
 #include <torch/extension.h>
 
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <c10/core/DeviceGuard.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <sstream>
+#include <string>
 #include <tuple>
 #include <vector>
 
@@ -41,48 +46,100 @@
 
 namespace {
 
-constexpr int64_t kAlignment = 16;
+// ---- argument checking ----------------------------------------------------
+// The kernels address token rows through 16-byte buffer loads and stores, so
+// every tensor handed to the library is dense row-major storage on the GPU
+// with a 16-byte aligned base.  ArgCheck walks an entry point's arguments,
+// keeps the first requirement that fails and raises it as one RuntimeError
+// naming the entry point, the argument and the requirement.
+class ArgCheck {
+  public:
+    explicit ArgCheck(const char* entry) : entry_(entry) {}
+
+    // Dense, 16-byte aligned storage on a GPU.
+    ArgCheck& on_gpu(const char* name, const at::Tensor& t) {
+        if (!t.is_cuda())
+            fail(name, "lives on the CPU; the library reads it on the GPU");
+        else if (!t.is_contiguous())
+            fail(name, "is a strided view; pass a contiguous tensor");
+        else if (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 != 0)
+            fail(name, "starts at an address that is not a multiple of 16 bytes; pass a fresh copy");
+        return *this;
+    }
+    // One of the accepted element types.
+    ArgCheck& dtype_is(const char* name, const at::Tensor& t, bool allow_f32) {
+        const auto st = t.scalar_type();
+        if (st != at::kBFloat16 && !(allow_f32 && st == at::kFloat))
+            fail(name, allow_f32 ? "holds neither float32 nor bfloat16 elements"
+                                 : "holds elements other than bfloat16");
+        return *this;
+    }
+    // Same element type and device as the reference argument.
+    ArgCheck& matches(const char* name, const at::Tensor& t, const char* ref_name,
+                      const at::Tensor& ref) {
+        if (t.scalar_type() != ref.scalar_type()) fail(name, std::string("has another dtype than ") + ref_name);
+        if (t.device() != ref.device()) fail(name, std::string("lives on another device than ") + ref_name);
+        return *this;
+    }
+    // A free-form requirement.
+    ArgCheck& require(bool ok, const char* name, const std::string& what) {
+        if (!ok) fail(name, what);
+        return *this;
+    }
+    void raise() const {
+        TORCH_CHECK(reason_.empty(), entry_, ": ", reason_);
+    }
+
+  private:
+    void fail(const char* name, const std::string& what) {
+        if (reason_.empty()) reason_ = std::string(name) + " " + what;
+    }
+    const char* entry_;
+    std::string reason_;
+};
+
+std::string dims(const at::Tensor& t) {
+    std::ostringstream s;
+    s << t.sizes();
+    return s.str();
+}
 
 void check_status(race_status st, const char* what) {
     TORCH_CHECK(st == RACE_SUCCESS, what, " failed: ", race_status_string(st), " (status ", st, ")");
 }
 
-void check_token_tensor(const at::Tensor& t, const char* name, const at::Tensor& like) {
-    TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
-    TORCH_CHECK(t.scalar_type() == at::kFloat || t.scalar_type() == at::kBFloat16, name,
-                " must be float32 or bfloat16, got ", t.scalar_type());
-    TORCH_CHECK(t.scalar_type() == like.scalar_type(), name, " dtype ", t.scalar_type(),
-                " differs from probsQ ", like.scalar_type());
-    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
-    TORCH_CHECK(t.device() == like.device(), name, " must be on the same device as probsQ");
-    TORCH_CHECK(reinterpret_cast<uintptr_t>(t.data_ptr()) % kAlignment == 0, name,
-                " data must be 16-byte aligned (clone the tensor if it is a view)");
-}
-
+// The per-bucket op's three token tensors: probs [N, T, L, R] (or [N, T, S])
+// and V [N, T, d], all float32 or all bfloat16 on one device.
 race_shape validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-    TORCH_CHECK(q.dim() == 4 || q.dim() == 3, "probsQ must be [N, T, L, R] or [N, T, S], got ",
-                q.sizes());
-    check_token_tensor(q, "probsQ", q);
-    check_token_tensor(k, "probsK", q);
-    check_token_tensor(v, "V", q);
-    TORCH_CHECK(k.sizes() == q.sizes(), "probsK shape ", k.sizes(), " differs from probsQ ",
-                q.sizes());
-    TORCH_CHECK(v.dim() == 3, "V must be [N, T, d], got ", v.sizes());
-    TORCH_CHECK(v.size(0) == q.size(0) && v.size(1) == q.size(1), "V ", v.sizes(),
-                " does not match probsQ ", q.sizes(), " in N and T");
+    ArgCheck c("race_fused_fwd");
+    c.require(q.dim() == 3 || q.dim() == 4, "probsQ", "has shape " + dims(q) + ", not [N, T, L, R] or [N, T, S]")
+        .on_gpu("probsQ", q).dtype_is("probsQ", q, true)
+        .on_gpu("probsK", k).matches("probsK", k, "probsQ", q)
+        .require(k.sizes() == q.sizes(), "probsK", "has shape " + dims(k) + ", probsQ " + dims(q))
+        .on_gpu("V", v).matches("V", v, "probsQ", q)
+        .require(v.dim() == 3 && v.size(0) == q.size(0) && v.size(1) == q.size(1), "V",
+                 "has shape " + dims(v) + ", not [N, T, d] with probsQ's N and T");
+    c.raise();
     race_shape sh;
     sh.num_streams = q.size(0);
     sh.seq_len = q.size(1);
     sh.num_tables = q.dim() == 4 ? static_cast<int32_t>(q.size(2)) : 1;
-    sh.num_buckets = static_cast<int32_t>(q.dim() == 4 ? q.size(3) : q.size(2));
+    sh.num_buckets = static_cast<int32_t>(q.size(q.dim() - 1));
     sh.head_dim = static_cast<int32_t>(v.size(2));
     sh.dtype = q.scalar_type() == at::kBFloat16 ? RACE_BF16 : RACE_F32;
     int32_t supported = 0;
     check_status(race_shape_supported(&sh, &supported, nullptr), "race_shape_supported");
-    TORCH_CHECK(supported, "unsupported shape: N=", sh.num_streams, " T=", sh.seq_len,
-                " L=", sh.num_tables, " R=", sh.num_buckets, " d=", sh.head_dim,
-                " (limits: N <= 65535, L*R <= 256, d <= 128)");
+    TORCH_CHECK(supported, "race_fused_fwd: no kernel takes N=", sh.num_streams, ", T=", sh.seq_len,
+                ", S=L*R=", int64_t(sh.num_tables) * sh.num_buckets, ", d=", sh.head_dim,
+                "; the library covers N <= 65535 streams, S <= 256 buckets, d <= 128 columns");
     return sh;
+}
+
+// A gradient or upstream tensor that must agree with the forward's V.
+void validate_like_v(const char* entry, const char* name, const at::Tensor& t, const at::Tensor& v) {
+    ArgCheck(entry).on_gpu(name, t).matches(name, t, "V", v)
+        .require(t.sizes() == v.sizes(), name, "has shape " + dims(t) + ", V " + dims(v))
+        .raise();
 }
 
 race_options make_options(int64_t tile_tokens, int64_t kernel, bool allow_decode = false) {
@@ -166,15 +223,16 @@ std::tuple<at::Tensor, at::Tensor> forward_carry(const at::Tensor& q, const at::
     const race_shape sh = validate(q, k, v);
     const race_options opts = make_options(tile_tokens, kernel, /*allow_decode=*/true);
     const int64_t S = int64_t(sh.num_tables) * sh.num_buckets;
-    TORCH_CHECK(init_state.is_cuda() && init_state.scalar_type() == at::kFloat &&
-                    init_state.is_contiguous() && init_state.device() == q.device(),
-                "state must be a contiguous float32 tensor on the device of probsQ");
-    TORCH_CHECK(init_state.dim() == 2 && init_state.size(0) == sh.num_streams &&
-                    init_state.size(1) == S * sh.head_dim + S,
-                "state must be [N, S*d + S] = [", sh.num_streams, ", ", S * sh.head_dim + S,
-                "], got ", init_state.sizes());
-    TORCH_CHECK(reinterpret_cast<uintptr_t>(init_state.data_ptr()) % kAlignment == 0,
-                "state data must be 16-byte aligned");
+    ArgCheck("race_fused_fwd_carry")
+        .on_gpu("state", init_state)
+        .require(init_state.scalar_type() == at::kFloat && init_state.device() == q.device(), "state",
+                 "must be float32 on probsQ's device")
+        .require(init_state.dim() == 2 && init_state.size(0) == sh.num_streams &&
+                     init_state.size(1) == S * sh.head_dim + S,
+                 "state", "has shape " + dims(init_state) + ", not [N, S*d + S] = [" +
+                              std::to_string(sh.num_streams) + ", " +
+                              std::to_string(S * sh.head_dim + S) + "]")
+        .raise();
     const c10::DeviceGuard guard(q.device());
     at::Tensor out = at::empty_like(v);
     at::Tensor state = inplace ? init_state : at::empty_like(init_state);
@@ -197,14 +255,14 @@ noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
                    const at::Tensor& grad_out, const at::Tensor& state, bool need_q, bool need_k,
                    bool need_v, int64_t tile_tokens) {
     const race_shape sh = validate(q, k, v);
-    check_token_tensor(grad_out, "dOut", q);
-    TORCH_CHECK(grad_out.sizes() == v.sizes(), "dOut shape ", grad_out.sizes(), " differs from V ",
-                v.sizes());
+    validate_like_v("race_noncausal_backward", "dOut", grad_out, v);
     const int64_t S = int64_t(sh.num_tables) * sh.num_buckets;
-    TORCH_CHECK(state.is_cuda() && state.scalar_type() == at::kFloat && state.is_contiguous() &&
-                    state.numel() == sh.num_streams * (S * sh.head_dim + S) &&
-                    state.device() == q.device(),
-                "state must be the forward's fp32 [N, S*d + S] state on the same device");
+    ArgCheck("race_noncausal_backward")
+        .on_gpu("state", state)
+        .require(state.scalar_type() == at::kFloat && state.device() == q.device() &&
+                     state.numel() == sh.num_streams * (S * sh.head_dim + S),
+                 "state", "is not the forward's float32 [N, S*d + S] state on probsQ's device")
+        .raise();
     const race_options opts = make_options(tile_tokens, RACE_KERNEL_AUTO);
     const c10::DeviceGuard guard(q.device());
     at::Tensor dq, dk, dv;
@@ -241,8 +299,8 @@ std::tuple<at::Tensor, at::Tensor, int64_t> forward_with_records(const at::Tenso
     at::Tensor records;
     if (r.tiles > 0 && N > 0)
         records = r.workspace.narrow(0, 0, N * r.tiles * r.rec).view({N, r.tiles, r.rec});
-    else
-        records = at::zeros({N, 0, r.rec}, v.options().dtype(at::kFloat));
+    else  // empty, but with the tile count the backward expects
+        records = at::zeros({N, r.tiles, r.rec}, v.options().dtype(at::kFloat));
     return {r.out, records, r.tile};
 }
 
@@ -251,31 +309,48 @@ causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                 const at::Tensor& grad_out, bool need_q, bool need_k, bool need_v,
                 int64_t tile_tokens, int64_t kernel, const c10::optional<at::Tensor>& fwd_records) {
     const race_shape sh = validate(q, k, v);
-    check_token_tensor(grad_out, "dOut", q);
-    TORCH_CHECK(grad_out.sizes() == v.sizes(), "dOut shape ", grad_out.sizes(), " differs from V ",
-                v.sizes());
+    validate_like_v("race_causal_backward", "dOut", grad_out, v);
     const race_options opts = make_options(tile_tokens, kernel);
     if (fwd_records) {
         const at::Tensor& rec = *fwd_records;
         TORCH_CHECK(tile_tokens > 0, "saved forward records need the forward's tile length");
-        TORCH_CHECK(rec.device() == q.device() && rec.scalar_type() == at::kFloat &&
-                        rec.is_contiguous() && rec.dim() == 3 && rec.size(0) == q.size(0),
-                    "fwd_records must be the forward's contiguous fp32 [N, tiles, rec] records");
-        const int64_t tiles = (q.size(1) + tile_tokens - 1) / tile_tokens;
-        TORCH_CHECK(rec.size(1) == tiles, "fwd_records has ", rec.size(1), " tiles, the tile length ",
-                    tile_tokens, " gives ", tiles);
+        // The layout the forward wrote for this shape at this tile length.
+        race_options fwd_opts = opts;
+        fwd_opts.kernel = RACE_KERNEL_AUTO;
+        size_t bytes = 0;
+        int64_t tiles = 0, rec_floats = 0;
+        check_status(race_fwd_workspace_bytes(&sh, 1, &fwd_opts, &bytes, &tiles, &rec_floats),
+                     "race_fwd_workspace_bytes");
+        ArgCheck("race_causal_backward")
+            .on_gpu("fwd_records", rec)
+            .require(rec.device() == q.device() && rec.scalar_type() == at::kFloat &&
+                         rec.dim() == 3 && rec.size(0) == q.size(0),
+                     "fwd_records", "is not the forward's float32 [N, tiles, rec] records")
+            .require(rec.dim() != 3 || rec.size(1) == tiles, "fwd_records",
+                     "has " + std::to_string(rec.dim() == 3 ? rec.size(1) : 0) +
+                         " tiles; the tile length " + std::to_string(tile_tokens) + " gives " +
+                         std::to_string(tiles))
+            .require(rec.dim() != 3 || rec.size(2) == rec_floats, "fwd_records",
+                     "has records of " + std::to_string(rec.dim() == 3 ? rec.size(2) : 0) +
+                         " floats; this (S, d) needs " + std::to_string(rec_floats))
+            .raise();
     }
     const c10::DeviceGuard guard(q.device());
     at::Tensor dq, dk, dv;
     if (need_q) dq = at::empty_like(q);
     if (need_k) dk = at::empty_like(k);
     if (need_v) dv = at::empty_like(v);
+    const bool from_records = fwd_records && fwd_records->numel() > 0;
     size_t bytes = 0;
-    check_status(race_causal_bwd_workspace_bytes(&sh, &opts, &bytes),
-                 "race_causal_bwd_workspace_bytes");
+    if (from_records)
+        check_status(race_causal_bwd_from_records_workspace_bytes(&sh, &opts, &bytes),
+                     "race_causal_bwd_from_records_workspace_bytes");
+    else
+        check_status(race_causal_bwd_workspace_bytes(&sh, &opts, &bytes),
+                     "race_causal_bwd_workspace_bytes");
     at::Tensor ws = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
     const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
-    if (fwd_records && fwd_records->numel() > 0)
+    if (from_records)
         check_status(race_causal_bwd_from_records(
                          q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
                          fwd_records->data_ptr<float>(), need_q ? dq.data_ptr() : nullptr,
@@ -298,19 +373,16 @@ causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
 
 // [..., d_k] rows -> [..., L, 2^K] bucket probabilities (src/race_baseline.py:41-44).
 at::Tensor hash_probs(const at::Tensor& x, const at::Tensor& planes_T, int64_t L, int64_t K) {
-    TORCH_CHECK(x.is_cuda(), "x must be a GPU tensor");
-    TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kBFloat16,
-                "x must be float32 or bfloat16");
-    TORCH_CHECK(x.is_contiguous() && reinterpret_cast<uintptr_t>(x.data_ptr()) % kAlignment == 0,
-                "x must be contiguous and 16-byte aligned");
-    TORCH_CHECK(x.dim() >= 1, "x must have a feature dimension");
+    ArgCheck c("race_hash_probs");
+    c.on_gpu("x", x).dtype_is("x", x, true).require(x.dim() >= 1, "x", "has no feature dimension");
+    c.raise();
     const int64_t dk = x.size(-1);
-    TORCH_CHECK(planes_T.is_cuda() && planes_T.device() == x.device() &&
-                    planes_T.scalar_type() == at::kFloat && planes_T.is_contiguous() &&
-                    planes_T.dim() == 2 && planes_T.size(0) == dk && planes_T.size(1) == L * K,
-                "planes_T must be a contiguous fp32 [d_k, L*K] tensor on x's device");
-    TORCH_CHECK(reinterpret_cast<uintptr_t>(planes_T.data_ptr()) % kAlignment == 0,
-                "planes_T must be 16-byte aligned");
+    c.on_gpu("planes_T", planes_T)
+        .require(planes_T.scalar_type() == at::kFloat && planes_T.device() == x.device(), "planes_T",
+                 "must be float32 on x's device")
+        .require(planes_T.dim() == 2 && planes_T.size(0) == dk && planes_T.size(1) == L * K,
+                 "planes_T", "has shape " + dims(planes_T) + ", not [d_k, L*K]")
+        .raise();
     const int64_t rows = x.numel() / dk;
     std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end() - 1);
     shape.push_back(L);
@@ -347,48 +419,45 @@ std::tuple<bool, bool> shape_supported(int64_t L, int64_t R, int64_t d) {
 // ---- Algorithm 1 with the hashing inside (race_alg1_*): the surface of the
 // reference's causal v2 binding (src/causal_v2/kernels/torch_binding.cpp) ----
 
-void check_alg1_token(const at::Tensor& t, const char* name, const at::Tensor& like) {
-    TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
-    TORCH_CHECK(t.scalar_type() == at::kBFloat16, name, " must be bfloat16, got ", t.scalar_type());
-    TORCH_CHECK(t.dim() == 4, name, " must be [B, H, T, d], got ", t.sizes());
-    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
-    TORCH_CHECK(t.sizes() == like.sizes(), name, " shape ", t.sizes(), " differs from q ", like.sizes());
-    TORCH_CHECK(t.device() == like.device(), name, " must be on the same device as q");
-    TORCH_CHECK(reinterpret_cast<uintptr_t>(t.data_ptr()) % kAlignment == 0, name,
-                " data must be 16-byte aligned (clone the tensor if it is a view)");
-}
-
+// The reference binding's limits for Algorithm 1 (race_causal_fwd.h:45-47),
+// applied by the C ABI (race_alg1_shape_supported); this wraps that query
+// with a message listing them.
 race_alg1_shape alg1_make_shape(int64_t batch_heads, int64_t seq_len, int64_t head_dim,
                                 int64_t num_planes, int64_t num_tables) {
-    TORCH_CHECK(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128, got ", head_dim);
-    TORCH_CHECK(num_planes >= 1 && num_planes <= 5, "num_planes P must be in 1..5, got ", num_planes);
-    TORCH_CHECK(num_tables >= 1 && num_tables <= 4, "num_tables L must be in 1..4, got ", num_tables);
-    TORCH_CHECK(batch_heads >= 0 && batch_heads <= 65535, "batch * heads must be <= 65535, got ",
-                batch_heads);
-    TORCH_CHECK(seq_len >= 0 && seq_len <= int64_t(INT32_MAX) - RACE_ALG1_MAX_AUTO_TILE - 1,
-                "sequence length out of range: ", seq_len);
     race_alg1_shape sh;
     sh.batch_heads = batch_heads;
     sh.seq_len = seq_len;
-    sh.head_dim = static_cast<int32_t>(head_dim);
-    sh.num_planes = static_cast<int32_t>(num_planes);
-    sh.num_tables = static_cast<int32_t>(num_tables);
+    sh.head_dim = static_cast<int32_t>(std::clamp<int64_t>(head_dim, -1, 1 << 20));
+    sh.num_planes = static_cast<int32_t>(std::clamp<int64_t>(num_planes, -1, 1 << 20));
+    sh.num_tables = static_cast<int32_t>(std::clamp<int64_t>(num_tables, -1, 1 << 20));
+    int32_t ok = 0;
+    check_status(race_alg1_shape_supported(&sh, &ok), "race_alg1_shape_supported");
+    TORCH_CHECK(ok, "causal_v2: no Algorithm-1 kernel for batch*heads=", batch_heads,
+                ", tokens=", seq_len, ", head_dim=", head_dim, ", num_planes=", num_planes,
+                ", num_tables=", num_tables, " (supported: head_dim 64 or 128, num_planes 1..5, ",
+                "num_tables 1..4, batch*heads <= 65535, tokens < 2^31 - ",
+                RACE_ALG1_MAX_AUTO_TILE + 1, ")");
     return sh;
 }
 
+// q, k, v: bf16 token rows [B, H, T, D] of one shape; W: float32 [L, P, D]
+// hash planes; beta: one floating-point value (any device).
 race_alg1_shape alg1_validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                               const at::Tensor& W, const at::Tensor& beta) {
-    check_alg1_token(q, "q", q);
-    check_alg1_token(k, "k", q);
-    check_alg1_token(v, "v", q);
-    TORCH_CHECK(W.device() == q.device(), "W must be on the same device as q");
-    TORCH_CHECK(W.scalar_type() == at::kFloat, "W must be float32, got ", W.scalar_type());
-    TORCH_CHECK(W.dim() == 3, "W must be [L, P, d], got ", W.sizes());
-    TORCH_CHECK(W.is_contiguous(), "W must be contiguous");
-    TORCH_CHECK(reinterpret_cast<uintptr_t>(W.data_ptr()) % kAlignment == 0, "W must be 16-byte aligned");
-    TORCH_CHECK(W.size(2) == q.size(3), "W head_dim ", W.size(2), " differs from q ", q.size(3));
-    TORCH_CHECK(beta.numel() == 1, "beta must have exactly one element");
-    TORCH_CHECK(at::isFloatingType(beta.scalar_type()), "beta must be a floating tensor");
+    ArgCheck c("causal_v2.forward");
+    const std::pair<const char*, const at::Tensor*> rows[] = {{"q", &q}, {"k", &k}, {"v", &v}};
+    for (const auto& [name, t] : rows)
+        c.on_gpu(name, *t).dtype_is(name, *t, false).matches(name, *t, "q", q)
+            .require(t->dim() == 4 && t->sizes() == q.sizes(), name,
+                     "has shape " + dims(*t) + "; q, k and v are [B, H, T, D] of one shape");
+    c.on_gpu("W", W)
+        .require(W.scalar_type() == at::kFloat && W.device() == q.device(), "W",
+                 "must be float32 on q's device")
+        .require(W.dim() == 3 && q.dim() == 4 && W.size(2) == q.size(3), "W",
+                 "has shape " + dims(W) + ", not [L, P, D] with q's D")
+        .require(beta.numel() == 1 && at::isFloatingType(beta.scalar_type()), "beta",
+                 "must be a single floating-point value")
+        .raise();
     return alg1_make_shape(q.size(0) * q.size(1), q.size(2), q.size(3), W.size(1), W.size(0));
 }
 
@@ -408,9 +477,10 @@ void alg1_check_fits(const race_alg1_shape& sh, bool tensor_cores) {
     check_status(race_alg1_output_lds_bytes(&sh, alg1_variant(tensor_cores), &bytes),
                  "race_alg1_output_lds_bytes");
     const int limit = device_lds_limit();
-    TORCH_CHECK(bytes <= size_t(limit), "the output pass needs ", bytes,
-                " bytes of LDS per workgroup for d=", sh.head_dim, ", P=", sh.num_planes, ", L=",
-                sh.num_tables, "; this GPU allows ", limit);
+    TORCH_CHECK(bytes <= size_t(limit), "causal_v2: ", limit, " bytes of LDS per workgroup on ",
+                "this GPU are fewer than the ", bytes, " an Algorithm-1 output-pass workgroup holds ",
+                "at (head_dim, num_planes, num_tables) = (", sh.head_dim, ", ", sh.num_planes, ", ",
+                sh.num_tables, ")");
 }
 
 struct Alg1Result {
@@ -584,7 +654,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("shape_supported", &shape_supported, "(supported, has_mfma) for (L, R, d)", py::arg("L"),
           py::arg("R"), py::arg("d"));
     m.def("alg1_forward", &alg1_forward,
-          "Causal Algorithm 1 with hashing: o = race_causal(q, k, v, W, beta)", py::arg("q"),
+          "Algorithm-1 causal attention, hashing inside the kernels -> out [B, H, T, D] bf16",
+          py::arg("q"),
           py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("tile_tokens") = 0,
           py::arg("tensor_cores") = false);
     m.def("alg1_forward_carry", &alg1_forward_carry,
@@ -595,17 +666,19 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "alg1_forward plus (prefix_A, prefix_B, final_A, final_B, tile_tokens)", py::arg("q"),
           py::arg("k"), py::arg("v"), py::arg("W"), py::arg("beta"), py::arg("tile_tokens") = 0,
           py::arg("tensor_cores") = false);
-    m.def("alg1_sub_chunk_tokens", &alg1_sub_chunk_tokens, "Sub-chunk length C of the output pass",
+    m.def("alg1_sub_chunk_tokens", &alg1_sub_chunk_tokens,
+          "Tokens per step of the Algorithm-1 kernels (tile lengths are multiples of it)",
           py::arg("head_dim"), py::arg("num_planes"), py::arg("tensor_cores") = false);
     m.def("alg1_select_tile_tokens", &alg1_select_tile_tokens,
-          "Tile length the forward picks for this shape on the current device",
+          "Automatic Algorithm-1 tile length for this shape on the current GPU",
           py::arg("batch_heads"), py::arg("seq_len"), py::arg("head_dim"), py::arg("num_planes"),
           py::arg("num_tables"), py::arg("tensor_cores") = false);
-    m.def("alg1_output_lds_bytes", &alg1_output_lds_bytes, "Dynamic LDS of the output pass in bytes",
+    m.def("alg1_output_lds_bytes", &alg1_output_lds_bytes,
+          "LDS bytes one Algorithm-1 output-pass workgroup allocates",
           py::arg("head_dim"), py::arg("num_planes"), py::arg("num_tables"),
           py::arg("tensor_cores") = false);
     m.def("alg1_fits_on_device", &alg1_fits_on_device,
-          "Whether the output pass fits this GPU's LDS", py::arg("head_dim"), py::arg("num_planes"),
+          "True when an Algorithm-1 output-pass workgroup fits this GPU's LDS", py::arg("head_dim"), py::arg("num_planes"),
           py::arg("num_tables"), py::arg("tensor_cores") = false);
     m.def("abi_version", &race_abi_version, "ABI version of the loaded librace_mi355x");
 }

@@ -81,6 +81,12 @@ def test_workspace_bytes_for_explicit_tiles(race):
     st, cb_bytes = abi.causal_bwd_workspace_bytes(sh, abi.options(1024, 0))
     assert st == 0
     assert cb_bytes == (2 * 8 * 64 * 4160 + 8 * 64 * (1024 // 16) * 64 + 8 * 65536 * 64) * 4
+    # Starting from the forward's saved records needs no region for them, and
+    # needs the forward's explicit tile length.
+    st, rb_bytes = abi.causal_bwd_from_records_workspace_bytes(sh, abi.options(1024, 0))
+    assert st == 0 and rb_bytes == cb_bytes - 8 * 64 * 4160 * 4
+    assert abi.causal_bwd_from_records_workspace_bytes(sh, abi.options(0, 0))[0] == 1
+    assert abi.causal_bwd_from_records_workspace_bytes(sh, None)[0] == 1
 
 
 def test_scratch_per_token_is_constant(race):
@@ -102,6 +108,27 @@ def test_invalid_tile_lengths_are_rejected(race, tile):
 
     st, *_ = abi.fwd_workspace_bytes(abi.shape(8, 4096, 4, 16, 64), True, abi.options(tile, 1))
     assert st == abi.RACE_ERROR_INVALID_VALUE
+
+
+def test_tiles_past_the_buffer_range_are_rejected(race):
+    # The kernels address a tile's rows through one buffer resource, whose
+    # range is a 32-bit byte count: 2^23 fp32 rows of 64 values are 2^31 bytes.
+    from race_attention_kernel_amd import abi
+
+    inv = abi.RACE_ERROR_INVALID_VALUE
+    for kernel in (abi.RACE_KERNEL_VALU, abi.RACE_KERNEL_MFMA):
+        big = abi.options(1 << 23, kernel)
+        assert abi.fwd_workspace_bytes(abi.shape(8, 1 << 24, 4, 16, 64), True, big)[0] == inv
+        assert abi.fwd_workspace_bytes(abi.shape(8, 1 << 24, 4, 16, 64), False, big)[0] == inv
+        # The same tile in bf16 is 2^30 bytes, inside the range.
+        assert abi.fwd_workspace_bytes(abi.shape(8, 1 << 24, 4, 16, 64, abi.RACE_BF16), True,
+                                       big)[0] == 0
+    # The widest operand sets the row length (S = 256 buckets here).
+    assert abi.fwd_workspace_bytes(abi.shape(1, 1 << 22, 16, 16, 64), True,
+                                   abi.options(1 << 21, 1))[0] == inv
+    st, _ = abi.causal_bwd_workspace_bytes(abi.shape(8, 1 << 24, 4, 16, 64), abi.options(1 << 23, 0))
+    assert st == inv
+    assert abi.alg1_workspace_bytes(abi.alg1_shape(1, 1 << 25, 64, 4, 4), 0, 1 << 24)[0] == inv
 
 
 def test_invalid_arguments_are_rejected_before_any_launch(race):
@@ -183,7 +210,7 @@ def test_torch_binding_validates_inputs_on_the_host(race, ext):
     import torch
 
     q, k, v = race.make_inputs(1, 64, 4, 16, 64)
-    with pytest.raises(RuntimeError, match="must be a GPU tensor"):
+    with pytest.raises(RuntimeError, match="race_fused_fwd: probsQ lives on the CPU"):
         ext.forward(q, k, v, True)
     with pytest.raises(ValueError):
         race.race_fused_fwd(q, k, v, True, kernel="tensor")
@@ -298,11 +325,11 @@ def test_alg1_torch_binding_validates_inputs_on_the_host(race, ext):
 
     q = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16)
     W = torch.zeros(2, 3, 64)
-    with pytest.raises(RuntimeError, match="must be a GPU tensor"):
+    with pytest.raises(RuntimeError, match="causal_v2.forward: q lives on the CPU"):
         race.causal_v2.forward(q, q, q, W, torch.tensor(1.0))
-    with pytest.raises(RuntimeError, match="head_dim must be 64 or 128"):
+    with pytest.raises(RuntimeError, match="no Algorithm-1 kernel .* head_dim=96"):
         race.causal_v2.sub_chunk_tokens(96, 4)
-    with pytest.raises(RuntimeError, match="num_planes"):
+    with pytest.raises(RuntimeError, match="num_planes=6"):
         race.causal_v2.output_pass_smem_bytes(64, 6, 1)
     assert race.causal_v2.sub_chunk_tokens(64, 4) == 64
     assert race.causal_v2.output_pass_smem_bytes(64, 4, 4) > 0

@@ -210,7 +210,25 @@ def test_backward_from_saved_records_equals_recomputing_them(race, ext, cuda, dt
 def test_saved_records_must_match_the_tile_length(race, ext, cuda):
     q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 1000, 4, 16, 64, seed=41, grad_out=True))
     _, records, tile = ext.forward_with_records(q, k, v, tile_tokens=128)
-    with pytest.raises(RuntimeError, match="tiles"):
+    with pytest.raises(RuntimeError, match="fwd_records has 8 tiles; the tile length 256 gives 4"):
         ext.causal_backward(q, k, v, g, True, True, True, 256, 0, records)
     with pytest.raises(RuntimeError, match="tile length"):
         ext.causal_backward(q, k, v, g, True, True, True, 0, 0, records)
+    # Records written for another (S, d) at the same tile count are refused on
+    # the host, before any kernel would index them with this shape's record size.
+    q2, k2, v2, g2 = (x.to(cuda) for x in race.make_inputs(1, 1000, 4, 16, 32, seed=41,
+                                                           grad_out=True))
+    with pytest.raises(RuntimeError, match="records of .* floats; this \\(S, d\\) needs"):
+        ext.causal_backward(q2, k2, v2, g2, True, True, True, 128, 0, records)
+
+
+@pytest.mark.parametrize("N, T", [(0, 5), (2, 0), (0, 0)])
+def test_autograd_backward_of_empty_inputs(race, cuda, N, T):
+    # Empty inputs: the forward keeps (empty) records with the tile count the
+    # backward expects, and the gradients come back empty.
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(N, T, 4, 16, 64, seed=3, grad_out=True))
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    race.race_fused_fwd(qg, kg, vg, causal=True).backward(g)
+    torch.cuda.synchronize()
+    for x, grad in ((q, qg.grad), (k, kg.grad), (v, vg.grad)):
+        assert grad.shape == x.shape

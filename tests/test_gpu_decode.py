@@ -178,11 +178,11 @@ def test_empty_carry_copies_the_state(race, cuda):
 
 def test_carry_rejects_bad_states(race, cuda):
     q, k, v = race.make_inputs(2, 4, 4, 16, 64, device=cuda)
-    with pytest.raises(RuntimeError, match="state must be"):
+    with pytest.raises(RuntimeError, match="race_fused_fwd_carry: state has shape"):
         race.race_fused_fwd_carry(q, k, v, torch.zeros(2, 64 * 64, device=cuda))
-    with pytest.raises(RuntimeError, match="state must be"):
+    with pytest.raises(RuntimeError, match="race_fused_fwd_carry: state must be float32"):
         race.race_fused_fwd_carry(q, k, v, torch.zeros(2, 64 * 65, device=cuda, dtype=torch.float64))
-    with pytest.raises(RuntimeError, match="state must be"):
+    with pytest.raises(RuntimeError, match="race_fused_fwd_carry: state lives on the CPU"):
         race.race_fused_fwd_carry(q, k, v, torch.zeros(2, 64 * 65))
 
 
