@@ -179,8 +179,9 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     if (i < n) p[i] = 0.f;
 }
 
+// p[0 .. n) = 0 (a no-op when p is null: an optional output not asked for).
 hipError_t zero_fill(float* p, int64_t n, hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
+    if (n <= 0 || !p) return hipSuccess;
     fill_zero_kernel<<<unsigned((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(p, n);
     return hipGetLastError();
 }

@@ -110,6 +110,18 @@ def test_invalid_tile_lengths_are_rejected(race, tile):
     assert st == abi.RACE_ERROR_INVALID_VALUE
 
 
+def test_empty_calls_without_optional_outputs_touch_no_device(race):
+    # An empty sequence with no state (or final state) asked for is a no-op:
+    # nothing is launched, so it succeeds here without a GPU.  (It once
+    # zero-filled the absent state through a null pointer.)
+    from race_attention_kernel_amd import abi
+
+    for causal in (True, False):
+        assert abi.fwd(0, 0, 0, 0, None, abi.shape(2, 0, 4, 16, 64), causal, None, None, 0, 0) == 0
+    assert abi.alg1_fwd(0, 0, 0, 0, 0, 0, None, abi.alg1_shape(2, 0, 64, 4, 4), 0, 0, None, 0,
+                        0) == 0
+
+
 def test_tiles_past_the_buffer_range_are_rejected(race):
     # The kernels address a tile's rows through one buffer resource, whose
     # range is a 32-bit byte count: 2^23 fp32 rows of 64 values are 2^31 bytes.
