@@ -55,6 +55,7 @@ extern "C" {
 typedef int32_t race_status;
 #define RACE_SUCCESS 0
 #define RACE_ERROR_INVALID_VALUE 1 /* equals hipErrorInvalidValue */
+#define RACE_ERROR_SCRATCH_TOO_SMALL 2 /* race_fwd_noalloc only; equals hipErrorOutOfMemory */
 
 typedef enum race_dtype {
     RACE_F32 = 0,
@@ -146,6 +147,27 @@ race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void
                               const race_options* opts, void* workspace, size_t workspace_bytes,
                               hipStream_t stream, hipEvent_t* events, int32_t max_events,
                               int32_t* n_events);
+
+/* Bytes of the per-GPU scratch array race_fwd_noalloc takes its workspace
+ * from.  32 MiB: at the automatic tile length on a 256-CU MI355X the cfg2
+ * shape (N = 8, S = d = 64) needs 17 MB of tile records for any T up to
+ * 2^21; race_fwd_workspace_bytes gives the need of any other call. */
+#define RACE_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* race_fwd for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  It has
+ * no counterpart in the reference.  The workspace comes from a device array
+ * of RACE_NOALLOC_SCRATCH_BYTES that the library holds per GPU until the
+ * process ends; the call itself allocates nothing.  A call whose
+ * race_fwd_workspace_bytes exceeds that returns RACE_ERROR_SCRATCH_TOO_SMALL
+ * before touching the device.  Outputs, their layouts and their values are
+ * race_fwd's (the same kernels and tile length give the same bits).  All
+ * calls on one GPU share its array: calls that overlap on one GPU (different
+ * streams, or host threads without ordering) race and must be serialized by
+ * the caller. */
+race_status race_fwd_noalloc(const void* probsQ, const void* probsK, const void* V, void* out,
+                             float* state, const race_shape* shape, int32_t causal,
+                             const race_options* opts, hipStream_t stream);
 
 /* Calls of race_fwd_carry with at most this many tokens (and an automatic
  * kernel and tile length) run the decode kernel. */

@@ -12,6 +12,8 @@ from . import _lib
 
 RACE_SUCCESS = 0
 RACE_ERROR_INVALID_VALUE = 1
+RACE_ERROR_SCRATCH_TOO_SMALL = 2
+RACE_NOALLOC_SCRATCH_BYTES = 32 << 20
 RACE_F32 = 0
 RACE_BF16 = 1
 RACE_KERNEL_AUTO = 0
@@ -34,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "race_fwd_workspace_bytes",
     "race_fwd",
     "race_fwd_profiled",
+    "race_fwd_noalloc",
     "race_fwd_carry_workspace_bytes",
     "race_fwd_carry",
     "race_fwd_carry_profiled",
@@ -101,6 +104,7 @@ def lib() -> ctypes.CDLL:
         L.race_fwd.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp]
         L.race_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp,
                                         ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
+        L.race_fwd_noalloc.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp]
         L.race_fwd_carry_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_fwd_carry.argtypes = [vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_fwd_carry_profiled.argtypes = [vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp, vp, i32,
@@ -160,6 +164,14 @@ def fwd_workspace_bytes(sh: RaceShape, causal: bool, opts: RaceOptions | None = 
                                         ctypes.byref(opts) if opts is not None else None,
                                         ctypes.byref(b), ctypes.byref(t), ctypes.byref(r))
     return st, b.value, t.value, r.value
+
+
+def fwd_noalloc(q: int, k: int, v: int, out: int, state: int | None, sh: RaceShape, causal: bool,
+                opts: RaceOptions | None, stream: int) -> int:
+    """race_fwd_noalloc on raw device addresses (workspace from the library's
+    per-GPU scratch array); returns the status."""
+    return lib().race_fwd_noalloc(q, k, v, out, state, ctypes.byref(sh), int(causal),
+                                  ctypes.byref(opts) if opts is not None else None, stream)
 
 
 def noncausal_bwd_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):

@@ -6,6 +6,7 @@
 // workspace, one stream, no allocation, no host synchronization, first error
 // returned, hipErrorInvalidValue for anything the kernels do not support.
 #include <climits>
+#include <mutex>
 
 #include "race_internal.h"
 
@@ -249,6 +250,10 @@ const char* race_status_string(race_status status) {
         return "invalid value: unsupported shape or kernel, null or misaligned pointer, "
                "workspace too small, or tile length not a positive multiple of "
                "RACE_SUB_CHUNK_TOKENS";
+    if (status == RACE_ERROR_SCRATCH_TOO_SMALL)
+        return "scratch too small: the call needs more workspace than the "
+               "RACE_NOALLOC_SCRATCH_BYTES race_fwd_noalloc holds per GPU; use race_fwd "
+               "with a caller-allocated workspace (race_fwd_workspace_bytes), or a longer tile";
     return hipGetErrorString(static_cast<hipError_t>(status));
 }
 
@@ -499,6 +504,68 @@ race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void
                                     workspace, workspace_bytes, stream, &marks);
     *n_events = marks.n;
     return st;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward: race_fwd with its workspace taken from `scratch`,
+// one file-scope device array per GPU, alive until the process ends.  In host
+// code the name `scratch` is a host-side stand-in, not a device address:
+// host code only ever uses the address hipGetSymbolAddress returns for the
+// current device (kept per device below), in kernel arguments and copies.
+// Every call on one GPU shares that GPU's array and leaves its contents
+// behind; race_fwd writes every record it later reads, so nothing needs
+// clearing first.  Calls that overlap on one GPU (other streams, other host
+// threads without ordering) race on the array.
+static __device__ __align__(256) float scratch[RACE_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace race {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+// The device address of the current GPU's scratch array, looked up once per
+// device with that device current.
+hipError_t current_scratch(void** addr) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_addr[dev] = p;
+    }
+    *addr = g_scratch_addr[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+}  // namespace race
+
+extern "C" {
+
+race_status race_fwd_noalloc(const void* probsQ, const void* probsK, const void* V, void* out,
+                             float* state, const race_shape* shape, int32_t causal,
+                             const race_options* opts, hipStream_t stream) {
+    // The size check is host arithmetic and comes first, so an oversized call
+    // is refused before any device is touched.
+    size_t need = 0;
+    race_status st = race_fwd_workspace_bytes(shape, causal, opts, &need, nullptr, nullptr);
+    if (st != RACE_SUCCESS) return st;
+    if (need > size_t(RACE_NOALLOC_SCRATCH_BYTES)) return RACE_ERROR_SCRATCH_TOO_SMALL;
+    void* ws = nullptr;
+    const hipError_t err = current_scratch(&ws);
+    if (err != hipSuccess) return err;
+    Marks none;
+    return fwd_impl(probsQ, probsK, V, out, state, nullptr, shape, causal, opts, ws,
+                    size_t(RACE_NOALLOC_SCRATCH_BYTES), stream, &none);
 }
 
 race_status race_fwd_carry_workspace_bytes(const race_shape* shape, const race_options* opts,
