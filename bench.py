@@ -74,6 +74,7 @@ PHASES = {
     (True, "valu"): ["tile_sums", "tile_scan", "output_pass_valu"],
     (False, "valu"): ["tile_sums", "tile_reduce", "token_map"],
     (True, "mfma"): ["tile_sums_mfma", "tile_scan", "output_pass_mfma"],
+    (True, "hashed"): ["hashed_sums", "tile_scan", "hashed_output"],
 }
 # Non-causal forwards with at most this many tiles per stream add the tile
 # records inside the map (no tile_reduce launch), as race_api.hip does.
@@ -133,7 +134,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
     ap.add_argument("--pass", dest="pass_",
-                    choices=["fwd", "bwd", "fwdbwd", "module", "alg1", "decode"],
+                    choices=["fwd", "bwd", "fwdbwd", "module", "module_twostep", "alg1", "decode"],
                     default="fwd",
                     help="what one step runs: the forward (default), the backward (from the "
                          "forward's inputs and a synthetic dOut), both, the module's hot "
@@ -178,16 +179,22 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
         "token_map_dv": es * (S + d) * NT,
         "hash_q": es * (d + S) * NT,               # rows of d_k = d -> probabilities
         "hash_k": es * (d + S) * NT,
+        "hashed_sums": es * 2 * d * NT,            # K rows, V (hashing inside)
+        "hashed_output": es * 4 * d * NT,          # Q, K, V rows -> out
     }.get(name, es * (2 * S + 2 * d) * NT)
 
 
 def op_bytes(pass_: str, cfg, T: int, es: int) -> float:
     """Algorithmic bytes of one step: the forward reads Q, K, V and writes out;
-    the backward reads Q, K, V, dOut and writes dQ, dK, dV."""
+    the backward reads Q, K, V, dOut and writes dQ, dK, dV.  The module's
+    hot span (hashing + forward, src/race_baseline.py:41-51) reads the Q, K
+    and V rows and writes out: 4 d values per stream-token, whichever path
+    runs it (the two-step path's probability round trip is its own cost)."""
     S, d, NT = cfg.S, cfg.d, cfg.N * T
     fwd, bwd = es * (2 * S + 2 * d) * NT, es * (4 * S + 3 * d) * NT
-    hashing = 2 * es * (d + S) * NT
-    return {"fwd": fwd, "bwd": bwd, "fwdbwd": fwd + bwd, "module": hashing + fwd}[pass_]
+    module = es * 4 * d * NT
+    return {"fwd": fwd, "bwd": bwd, "fwdbwd": fwd + bwd, "module": module,
+            "module_twostep": module}[pass_]
 
 
 def traffic_for(workload_key: str, kernel_name: str):
@@ -534,8 +541,9 @@ def main() -> int:
             raise RuntimeError(abi.status_string(st_))
 
     # One step of the chosen pass: plain(), and profiled(events) -> events used.
-    run_hash = args.pass_ == "module"
-    if run_hash:
+    run_hashed = args.pass_ == "module"
+    run_hash = args.pass_ == "module_twostep"
+    if run_hash or run_hashed:
         # The module's inputs: Q and K rows [N, T, d_k] and the shared planes;
         # the hashing writes the probabilities the forward then reads.
         if not cfg.causal or cfg.R & (cfg.R - 1):
@@ -545,13 +553,24 @@ def main() -> int:
         xq = torch.randn(cfg.N, T, cfg.d, device=dev, generator=gen).to(v.dtype)
         xk = torch.randn(cfg.N, T, cfg.d, device=dev, generator=gen).to(v.dtype)
         planes_T = torch.randn(cfg.d, cfg.L * Kp, device=dev, generator=gen)
+        planes = planes_T.t().contiguous()  # [L*K, d], the hashed op's layout
         hdt = abi.RACE_BF16 if es == 2 else abi.RACE_F32
+        hopts = abi.options(args.tile, 0)
+        st, hws_bytes, tiles, rec = abi.hashed_fwd_workspace_bytes(sh, Kp, hopts)
+        check(st)
+        if run_hashed:
+            ws = torch.empty(max(hws_bytes // 4, 1), device=dev, dtype=torch.float32)
+            ws_bytes = hws_bytes
+            tile = race.select_tile_tokens(cfg.N, T, cfg.L, cfg.R, cfg.d, bf16=(es == 2), causal=True,
+                                           tile_tokens=args.tile, kernel="mfma_wg")
+            family = "hashed"
+            hptrs = (xk.data_ptr(), xq.data_ptr(), v.data_ptr(), planes.data_ptr(), out.data_ptr())
 
         def hash_both():
             for x_, p_ in ((xq, q), (xk, k)):
                 check(abi.hash_probs(x_.data_ptr(), planes_T.data_ptr(), p_.data_ptr(), cfg.N * T,
                                      cfg.d, cfg.L, Kp, hdt, stream))
-    run_fwd = args.pass_ in ("fwd", "fwdbwd", "module")
+    run_fwd = args.pass_ in ("fwd", "fwdbwd", "module_twostep")
     run_bwd = args.pass_ in ("bwd", "fwdbwd")
     state = None
     if run_bwd:
@@ -573,6 +592,8 @@ def main() -> int:
     sptr = state.data_ptr() if state is not None else None
 
     def plain():
+        if run_hashed:
+            check(abi.hashed_fwd(*hptrs, None, sh, Kp, hopts, ws.data_ptr(), ws_bytes, stream))
         if run_hash:
             hash_both()
         if run_fwd:
@@ -586,6 +607,11 @@ def main() -> int:
 
     def profiled(evs):
         n_used = 0
+        if run_hashed:
+            st_, n = abi.hashed_fwd_profiled(*hptrs, None, sh, Kp, hopts, ws.data_ptr(), ws_bytes,
+                                             stream, evs)
+            check(st_)
+            n_used += n
         if run_hash:
             events.record(evs[0], stream)
             for j, (x_, p_) in enumerate(((xq, q), (xk, k))):
@@ -615,6 +641,8 @@ def main() -> int:
     if not cfg.causal and tiles <= NONCAUSAL_FOLD_TILES:
         fwd_names = [n for n in fwd_names if n != "tile_reduce"]
     names = []
+    if run_hashed:
+        names += PHASES[(True, "hashed")]
     if run_hash:
         names += ["hash_q", "hash_k"]
     if run_fwd:
@@ -735,8 +763,8 @@ def main() -> int:
     del q, k, v, out, ws
     if run_bwd:
         del g, dq, dk, dv, bws
-    if run_hash:
-        del xq, xk, planes_T
+    if run_hash or run_hashed:
+        del xq, xk, planes_T, planes
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline and headline:
         result["cpu_baseline"] = cpu_baseline()

@@ -287,6 +287,49 @@ race_status race_hash_probs(const void* x, const float* planes_T, void* probs, i
                             int32_t head_dim, int32_t num_tables, int32_t planes_per_table,
                             int32_t dtype, hipStream_t stream);
 
+/* Gradient of race_hash_probs w.r.t. the rows: given dprobs (the upstream
+ * gradient, [rows][num_tables * 2^K], dtype of x) writes dx [rows][head_dim].
+ * With z_k = 2 u_k and sigma_k = sigma(z_k) (recomputed from x), per table
+ *   du_k = 2 (sum_{r: s_{r,k} = +1} g_r - sigma_k sum_r g_r),  g_r = dprobs_r probs_r,
+ *   dx   = sum_k du_k (1 - tanh^2(<x, p_k>)) / sqrt(head_dim) p_k.
+ * The planes are a buffer in the reference (src/race_baseline.py:27), so no
+ * gradient w.r.t. them.  The reference has no kernel for this; autograd
+ * differentiates its torch composition (src/race_baseline.py:41-44).  Limits
+ * as race_hash_probs. */
+race_status race_hash_probs_bwd(const void* x, const float* planes_T, const void* dprobs, void* dx,
+                                int64_t rows, int32_t head_dim, int32_t num_tables,
+                                int32_t planes_per_table, int32_t dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * The causal op with the hashing inside: BatchedACE.forward's hashing and hot
+ * span (src/race_baseline.py:41-51) in one op, the reference's fused forward
+ * race_fused_fwd(K, Q, V, planes, L) (src/race_fused_fwd.cu:150-171, kernel
+ * :80-146).  Token rows k_rows, q_rows, v: [N][T][d] (shape->head_dim = d =
+ * d_k), one dtype; planes: [L*K][d] fp32 row-major (the reference's
+ * `planes`, = BatchedACE's planes_T transposed); shape->num_tables = L and
+ * shape->num_buckets = R = 2^planes_per_table.  The result is race_fwd
+ * (causal) on probsQ = hash(q_rows), probsK = hash(k_rows) as race_hash_probs
+ * defines them, without those probabilities ever written to memory.  The
+ * workspace, its tile records and `state` are race_fwd's.  Limits:
+ * planes_per_table K >= 2, L*K <= 64, S = L*2^K in {64, 128, 256},
+ * d in {64, 128}; the kernel option may be AUTO or MFMA_WG (the workgroup
+ * matrix-core kernels run). */
+race_status race_hashed_fwd_workspace_bytes(const race_shape* shape, int32_t planes_per_table,
+                                            const race_options* opts, size_t* bytes, int64_t* tiles,
+                                            int64_t* record_floats);
+race_status race_hashed_fwd(const void* k_rows, const void* q_rows, const void* v, const float* planes,
+                            void* out, float* state, const race_shape* shape, int32_t planes_per_table,
+                            const race_options* opts, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+/* race_hashed_fwd with the events of race_fwd_profiled (a profiling aid, no
+ * counterpart in the reference). */
+race_status race_hashed_fwd_profiled(const void* k_rows, const void* q_rows, const void* v,
+                                     const float* planes, void* out, float* state,
+                                     const race_shape* shape, int32_t planes_per_table,
+                                     const race_options* opts, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream, hipEvent_t* events,
+                                     int32_t max_events, int32_t* n_events);
+
 /* ------------------------------------------------------------------------
  * Algorithm 1 with the hashing inside: the reference's causal v2 forward,
  * race_causal_forward(q, k, v, planes, beta, ...)

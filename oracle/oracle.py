@@ -301,6 +301,35 @@ def hash_probs(x, planes_T, L: int, K: int):
     return e / e.sum(-1, keepdims=True)
 
 
+def torch_hash_probs(x, planes_T, L: int, K: int):
+    """src/race_baseline.py:41-44 as differentiable torch ops (any dtype):
+    softmax over the 2^K corners of tanh(x planes_T) / sqrt(d_k) projected on
+    the corners.  x [..., d_k] -> [..., L, 2^K]."""
+    import torch
+
+    dk = x.shape[-1]
+    proj = (x @ planes_T).reshape(*x.shape[:-1], L, K)
+    corner = torch.as_tensor(corners(K), dtype=x.dtype)     # [R, K]
+    return torch.softmax((torch.tanh(proj) / np.sqrt(dk)) @ corner.T, dim=-1)
+
+
+def torch_module_autograd(k_rows, q_rows, v, planes_T, L: int, K: int, g, eps: float = EPS):
+    """BatchedACE's hashing and causal hot span (src/race_baseline.py:41-51) in
+    fp64 torch, and its gradients w.r.t. the K, Q and V rows for upstream g
+    (small T: the composition holds [N, T, S, d] tensors).  Returns (out, dK,
+    dQ, dV) as numpy."""
+    import torch
+
+    kt, qt, vt = (torch.as_tensor(np.asarray(x, np.float64)).requires_grad_(True)
+                  for x in (k_rows, q_rows, v))
+    pt = torch.as_tensor(np.asarray(planes_T, np.float64))
+    pk = torch_hash_probs(kt, pt, L, K).flatten(-2)
+    pq = torch_hash_probs(qt, pt, L, K).flatten(-2)
+    out = torch_causal_reference(pq, pk, vt, eps)
+    dk, dq, dv = torch.autograd.grad(out, (kt, qt, vt), torch.as_tensor(np.asarray(g, np.float64)))
+    return out.detach().numpy(), dk.numpy(), dq.numpy(), dv.numpy()
+
+
 def hash_probs_product_form(x, planes_T, L: int, K: int):
     """The same probabilities as prod_k sigmoid(2 u_k s_{r,k})."""
     x = np.asarray(x, np.float64)

@@ -7,13 +7,14 @@ through the _race_torch binding.  There is no CPU fallback.
 from . import causal_v2
 from .batched_ace import BatchedACE
 from .inputs import CONFIGS, Config, config_inputs, make_inputs
-from .ops import (RaceFusedFunction, race_causal_backward, race_fused_fwd, race_fused_fwd_carry,
+from .ops import (HashedRaceFunction, HashProbsFunction, RaceFusedFunction, hashed_supported,
+                  race_causal_backward, race_fused_fwd, race_fused_fwd_carry, race_fused_fwd_hashed,
                   race_fused_fwd_with_state, race_hash_probs, race_noncausal_backward,
                   select_tile_tokens)
 
 __all__ = [
     "BatchedACE", "CONFIGS", "Config", "RaceFusedFunction", "config_inputs", "make_inputs",
     "race_fused_fwd", "race_fused_fwd_carry", "race_fused_fwd_with_state", "race_noncausal_backward",
-    "race_causal_backward",
-    "race_hash_probs", "select_tile_tokens", "causal_v2",
+    "race_causal_backward", "race_fused_fwd_hashed", "hashed_supported", "HashedRaceFunction",
+    "HashProbsFunction", "race_hash_probs", "select_tile_tokens", "causal_v2",
 ]

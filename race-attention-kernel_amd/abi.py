@@ -49,6 +49,10 @@ EXPORTED_SYMBOLS = (
     "race_noncausal_bwd_profiled",
     "race_causal_bwd_profiled",
     "race_hash_probs",
+    "race_hash_probs_bwd",
+    "race_hashed_fwd_workspace_bytes",
+    "race_hashed_fwd",
+    "race_hashed_fwd_profiled",
     "race_alg1_shape_supported",
     "race_alg1_output_lds_bytes",
     "race_alg1_select_tile_tokens",
@@ -121,6 +125,12 @@ def lib() -> ctypes.CDLL:
         L.race_causal_bwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp,
                                                ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         L.race_hash_probs.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32, vp]
+        L.race_hash_probs_bwd.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, i32, vp]
+        L.race_hashed_fwd_workspace_bytes.argtypes = [shp, i32, opp, ctypes.POINTER(sz),
+                                                      ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        L.race_hashed_fwd.argtypes = [vp, vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp]
+        L.race_hashed_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp,
+                                               ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         a1 = ctypes.POINTER(RaceAlg1Shape)
         L.race_alg1_shape_supported.argtypes = [a1, ctypes.POINTER(i32)]
         L.race_alg1_output_lds_bytes.argtypes = [a1, i32, ctypes.POINTER(sz)]
@@ -172,6 +182,36 @@ def fwd_noalloc(q: int, k: int, v: int, out: int, state: int | None, sh: RaceSha
     per-GPU scratch array); returns the status."""
     return lib().race_fwd_noalloc(q, k, v, out, state, ctypes.byref(sh), int(causal),
                                   ctypes.byref(opts) if opts is not None else None, stream)
+
+
+def hashed_fwd_workspace_bytes(sh: RaceShape, planes_per_table: int, opts: RaceOptions | None = None):
+    """(status, bytes, tiles, record_floats) of race_hashed_fwd."""
+    b, t, r = ctypes.c_size_t(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    st = lib().race_hashed_fwd_workspace_bytes(ctypes.byref(sh), planes_per_table,
+                                               ctypes.byref(opts) if opts is not None else None,
+                                               ctypes.byref(b), ctypes.byref(t), ctypes.byref(r))
+    return st, b.value, t.value, r.value
+
+
+def hashed_fwd(k: int, q: int, v: int, planes: int, out: int, state: int | None, sh: RaceShape,
+               planes_per_table: int, opts: RaceOptions | None, workspace: int | None,
+               workspace_bytes: int, stream: int) -> int:
+    """race_hashed_fwd on raw device addresses; returns the status."""
+    return lib().race_hashed_fwd(k, q, v, planes, out, state, ctypes.byref(sh), planes_per_table,
+                                 ctypes.byref(opts) if opts is not None else None, workspace,
+                                 workspace_bytes, stream)
+
+
+def hashed_fwd_profiled(k: int, q: int, v: int, planes: int, out: int, state: int | None,
+                        sh: RaceShape, planes_per_table: int, opts: RaceOptions | None,
+                        workspace: int | None, workspace_bytes: int, stream: int,
+                        events) -> tuple[int, int]:
+    """race_hashed_fwd_profiled; ``events`` a ctypes array of hipEvent_t.  Returns (status, n_events)."""
+    n = ctypes.c_int32(0)
+    st = lib().race_hashed_fwd_profiled(k, q, v, planes, out, state, ctypes.byref(sh), planes_per_table,
+                                        ctypes.byref(opts) if opts is not None else None, workspace,
+                                        workspace_bytes, stream, events, len(events), ctypes.byref(n))
+    return st, n.value
 
 
 def noncausal_bwd_workspace_bytes(sh: RaceShape, opts: RaceOptions | None = None):

@@ -1,9 +1,15 @@
 """Drop-in BatchedACE (src/race_baseline.py:21-52) running the op on MI355X.
 
 Same constructor and forward signature as the reference module.  The
-permutes of lines 35-40 and 52 stay torch ops; the hashing of lines 41-44
-(shared hash planes, tanh, corner softmax) runs as the race_hash_probs HIP
-kernel and lines 45-51 (the cumsum/bmm hot span) as race_fused_fwd.
+permutes of lines 35-40 and 52 stay torch ops.  For the causal module the
+hashing of lines 41-44 (shared hash planes, tanh, corner softmax) and the hot
+span of lines 45-51 run as one op, race_fused_fwd_hashed, whose kernels hash
+the Q and K rows themselves (the reference's fused forward,
+src/race_fused_fwd.cu:80-146), so the bucket probabilities never reach
+memory.  The non-causal module (and a causal one whose L, K, d_k the hashed
+kernels do not take) runs the race_hash_probs kernel and race_fused_fwd.
+Gradients reach Khf, Qhf and Vhf on both paths, as through the reference's
+torch composition; planes_T is a buffer there and here.
 """
 from __future__ import annotations
 
@@ -12,7 +18,7 @@ import itertools
 import torch
 from torch import nn
 
-from .ops import race_fused_fwd, race_hash_probs
+from .ops import hashed_supported, race_fused_fwd, race_fused_fwd_hashed, race_hash_probs
 
 
 class BatchedACE(nn.Module):
@@ -37,7 +43,11 @@ class BatchedACE(nn.Module):
         Kh2 = Khf.permute(0, 1, 3, 2, 4).contiguous().view(N, T, dk)
         Qh2 = Qhf.permute(0, 1, 3, 2, 4).contiguous().view(N, T, dk)
         V2 = Vhf.permute(0, 1, 3, 2, 4).contiguous().view(N, T, dk)
-        probsK = self.bucket_probs(Kh2).contiguous()
-        probsQ = self.bucket_probs(Qh2).contiguous()
-        out2 = race_fused_fwd(probsQ, probsK, V2, self.causal)
+        if self.causal and hashed_supported(self.L, self.K, dk):
+            planes = self.planes_T.t().contiguous().float()  # [L*K, d_k]
+            out2 = race_fused_fwd_hashed(Kh2, Qh2, V2, planes, self.L)
+        else:
+            probsK = self.bucket_probs(Kh2).contiguous()
+            probsQ = self.bucket_probs(Qh2).contiguous()
+            out2 = race_fused_fwd(probsQ, probsK, V2, self.causal)
         return out2.view(M, B, H, T, dk).permute(0, 1, 3, 2, 4)

@@ -199,6 +199,83 @@ __global__ __launch_bounds__(kThreads) void hash_probs_kernel(const TIn* __restr
     }
 }
 
+// Gradient of the hashing w.r.t. the rows, one row per thread.  The
+// projections and sigmoids are recomputed as the forward computes them; then
+// per table, with g_r = dprobs_r probs_r and sigma_k = sigma(2 u_k),
+//     du_k = 2 (sum_{r: bit K-1-k of r set} g_r - sigma_k sum_r g_r)
+// (d probs_r / d u_k = 2 probs_r ([s_{r,k} = +1] - sigma_k)), and
+//     dx = sum_k du_k (1 - tanh^2(p_k)) / sqrt(d_k) planes_T[:, k].
+template <typename TIn, int LKT>
+__global__ __launch_bounds__(kThreads) void hash_probs_bwd_kernel(
+    const TIn* __restrict__ x, const float* __restrict__ planes_T, const TIn* __restrict__ dprobs,
+    TIn* __restrict__ dx, int64_t rows, int dk, int L, int K) {
+    extern __shared__ float pl[];  // [dk][LKT], zero past L*K columns
+    const int LK = L * K, R = 1 << K, LR = L * R;
+    for (int e = threadIdx.x; e < dk * LKT; e += kThreads) {
+        const int c = e / LKT, j = e % LKT;
+        pl[e] = j < LK ? planes_T[c * LK + j] : 0.f;
+    }
+    __syncthreads();
+    const int64_t row = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (row >= rows) return;
+    const TIn* xr = x + row * dk;
+    float acc[LKT];
+#pragma unroll
+    for (int j = 0; j < LKT; ++j) acc[j] = 0.f;
+    for (int c = 0; c < dk; ++c) {
+        const float xc = to_f32(xr[c]);
+#pragma unroll
+        for (int j = 0; j < LKT; ++j) acc[j] = fmaf(xc, pl[c * LKT + j], acc[j]);
+    }
+    const float inv_scale = 1.0f / sqrtf(float(dk));
+    float th[LKT], sg[LKT];
+#pragma unroll
+    for (int j = 0; j < LKT; ++j) {
+        th[j] = tanhf(acc[j]);
+        sg[j] = 1.0f / (1.0f + expf(-2.0f * inv_scale * th[j]));
+    }
+    const TIn* gr = dprobs + row * LR;
+    float dpj[LKT];
+#pragma unroll
+    for (int j = 0; j < LKT; ++j) dpj[j] = 0.f;
+    for (int l = 0; l < L; ++l) {
+        float tot = 0.f, pos[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < R; ++r) {
+            // prod_k (bit K-1-k of r ? sigma_k : 1 - sigma_k) for table l.
+            float prob = 1.f;
+#pragma unroll
+            for (int j = 0; j < LKT; ++j) {
+                const int k = j - l * K;
+                if (k >= 0 && k < K) prob *= ((r >> (K - 1 - k)) & 1) ? sg[j] : 1.0f - sg[j];
+            }
+            const float gv = to_f32(gr[l * R + r]) * prob;
+            tot += gv;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (k < K && ((r >> (K - 1 - k)) & 1)) pos[k] += gv;
+        }
+#pragma unroll
+        for (int j = 0; j < LKT; ++j) {
+            const int k = j - l * K;
+            if (k >= 0 && k < K) {
+                float pk = 0.f;
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk)
+                    if (kk == k) pk = pos[kk];
+                const float du = 2.0f * (pk - sg[j] * tot);
+                dpj[j] = du * (1.0f - th[j] * th[j]) * inv_scale;
+            }
+        }
+    }
+    TIn* dxr = dx + row * dk;
+    for (int c = 0; c < dk; ++c) {
+        float v = 0.f;
+#pragma unroll
+        for (int j = 0; j < LKT; ++j) v = fmaf(dpj[j], pl[c * LKT + j], v);
+        store_val(dxr + c, v);
+    }
+}
+
 int lk_tier(int LK) { return LK <= 16 ? 16 : LK <= 32 ? 32 : 64; }
 
 }  // namespace
@@ -242,6 +319,28 @@ hipError_t launch_hash_probs(const void* x, const float* planes_T, void* probs, 
     }
 #undef RACE_HASH_LK
 #undef RACE_HASH
+    return hipGetLastError();
+}
+
+hipError_t launch_hash_probs_bwd(const void* x, const float* planes_T, const void* dprobs, void* dx,
+                                int64_t rows, int dk, int L, int K, int dtype, hipStream_t stream) {
+    const dim3 grid(unsigned((rows + kThreads - 1) / kThreads));
+    const int tier = lk_tier(L * K);
+    const size_t lds = size_t(dk) * tier * sizeof(float);
+#define RACE_HASH_BWD(TIN, LKT)                                                               \
+    hash_probs_bwd_kernel<TIN, LKT><<<grid, kThreads, lds, stream>>>(                         \
+        static_cast<const TIN*>(x), planes_T, static_cast<const TIN*>(dprobs), static_cast<TIN*>(dx), \
+        rows, dk, L, K)
+    if (dtype == RACE_BF16) {
+        if (tier == 16) RACE_HASH_BWD(bf16_t, 16);
+        else if (tier == 32) RACE_HASH_BWD(bf16_t, 32);
+        else RACE_HASH_BWD(bf16_t, 64);
+    } else {
+        if (tier == 16) RACE_HASH_BWD(float, 16);
+        else if (tier == 32) RACE_HASH_BWD(float, 32);
+        else RACE_HASH_BWD(float, 64);
+    }
+#undef RACE_HASH_BWD
     return hipGetLastError();
 }
 

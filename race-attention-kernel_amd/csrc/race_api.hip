@@ -809,6 +809,122 @@ race_status race_hash_probs(const void* x, const float* planes_T, void* probs, i
                              dtype, stream);
 }
 
+race_status race_hash_probs_bwd(const void* x, const float* planes_T, const void* dprobs, void* dx,
+                                int64_t rows, int32_t head_dim, int32_t num_tables,
+                                int32_t planes_per_table, int32_t dtype, hipStream_t stream) {
+    if (!hash_shape_ok(rows, head_dim, num_tables, planes_per_table)) return RACE_ERROR_INVALID_VALUE;
+    if (dtype != RACE_F32 && dtype != RACE_BF16) return RACE_ERROR_INVALID_VALUE;
+    if (rows == 0) return RACE_SUCCESS;
+    if (!x || !planes_T || !dprobs || !dx) return RACE_ERROR_INVALID_VALUE;
+    const int tier = num_tables * planes_per_table <= 16 ? 16 : num_tables * planes_per_table <= 32 ? 32 : 64;
+    int lds_limit = 0;
+    RACE_TRY(max_lds(&lds_limit));
+    if (size_t(head_dim) * tier * sizeof(float) > size_t(lds_limit)) return RACE_ERROR_INVALID_VALUE;
+    return launch_hash_probs_bwd(x, planes_T, dprobs, dx, rows, head_dim, num_tables,
+                                 planes_per_table, dtype, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The causal op with the hashing inside (hashed_causal.hip): the fused
+// forward of src/race_fused_fwd.cu:150-171, race_fused_fwd(K, Q, V, planes, L).
+
+namespace race {
+namespace {
+
+// The problem of a hashed call: R = 2^K buckets per table, the workgroup MFMA
+// kernels' tile policy.
+race_status hashed_problem(const race_shape* sh, int32_t K, const race_options* o, Problem* p) {
+    if (!shape_ok(sh)) return RACE_ERROR_INVALID_VALUE;
+    if (K < 1 || K > 8 || sh->num_buckets != (1 << K)) return RACE_ERROR_INVALID_VALUE;
+    if (!hashed_causal_supported(sh->num_tables, K, sh->head_dim)) return RACE_ERROR_INVALID_VALUE;
+    const int k = kernel_choice(o);
+    if (k != RACE_KERNEL_AUTO && k != RACE_KERNEL_MFMA && k != RACE_KERNEL_MFMA_WG)
+        return RACE_ERROR_INVALID_VALUE;
+    const race_options wg = {o ? o->tile_tokens : 0, RACE_KERNEL_MFMA_WG};
+    bool mfma = false;
+    return make_problem(sh, 1, &wg, &mfma, p);
+}
+
+race_status hashed_fwd_impl(const void* k_rows, const void* q_rows, const void* v, const float* planes,
+                            void* out, float* state, const race_shape* shape, int32_t K,
+                            const race_options* opts, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream, Marks* marks) {
+    Problem p;
+    const race_status st = hashed_problem(shape, K, opts, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (state && !aligned16(state)) return RACE_ERROR_INVALID_VALUE;
+    if (p.N == 0 || p.T == 0) {
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(zero_fill(state, p.N * state_floats(p.S, p.d), stream));
+        return marks->mark(stream);
+    }
+    if (!k_rows || !q_rows || !v || !planes || !out) return RACE_ERROR_INVALID_VALUE;
+    if (!aligned16(k_rows) || !aligned16(q_rows) || !aligned16(v) || !aligned16(planes) ||
+        !aligned16(out))
+        return RACE_ERROR_INVALID_VALUE;
+    const FwdLayout l = fwd_layout(p, 1);
+    if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
+        return RACE_ERROR_INVALID_VALUE;
+    HashedArgs a;
+    a.q = q_rows;
+    a.k = k_rows;
+    a.v = v;
+    a.planes = planes;
+    a.out = out;
+    a.records = static_cast<float*>(workspace);
+    a.state = state;
+    a.L = shape->num_tables;
+    a.K = K;
+    RACE_TRY(marks->mark(stream));
+    return launch_hashed_causal(a, p, stream, marks);
+}
+
+}  // namespace
+}  // namespace race
+
+extern "C" {
+
+race_status race_hashed_fwd_workspace_bytes(const race_shape* shape, int32_t planes_per_table,
+                                            const race_options* opts, size_t* bytes, int64_t* tiles,
+                                            int64_t* record_floats_out) {
+    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    const race_status st = hashed_problem(shape, planes_per_table, opts, &p);
+    if (st != RACE_SUCCESS) return st;
+    *bytes = size_t(fwd_layout(p, 1).total()) * sizeof(float);
+    if (tiles) *tiles = p.tiles;
+    if (record_floats_out) *record_floats_out = p.rec;
+    return RACE_SUCCESS;
+}
+
+race_status race_hashed_fwd(const void* k_rows, const void* q_rows, const void* v, const float* planes,
+                            void* out, float* state, const race_shape* shape, int32_t planes_per_table,
+                            const race_options* opts, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+    Marks none;
+    return hashed_fwd_impl(k_rows, q_rows, v, planes, out, state, shape, planes_per_table, opts,
+                           workspace, workspace_bytes, stream, &none);
+}
+
+race_status race_hashed_fwd_profiled(const void* k_rows, const void* q_rows, const void* v,
+                                     const float* planes, void* out, float* state,
+                                     const race_shape* shape, int32_t planes_per_table,
+                                     const race_options* opts, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream, hipEvent_t* events,
+                                     int32_t max_events, int32_t* n_events) {
+    if (!events || max_events < 2 || !n_events) return RACE_ERROR_INVALID_VALUE;
+    Marks marks;
+    marks.events = events;
+    marks.max = max_events;
+    const race_status st = hashed_fwd_impl(k_rows, q_rows, v, planes, out, state, shape,
+                                           planes_per_table, opts, workspace, workspace_bytes, stream,
+                                           &marks);
+    *n_events = marks.n;
+    return st;
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

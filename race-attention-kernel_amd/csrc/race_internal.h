@@ -187,6 +187,9 @@ bool hash_shape_ok(int64_t rows, int dk, int L, int K);
 size_t hash_lds_bytes(int dk, int L, int K);
 hipError_t launch_hash_probs(const void* x, const float* planes_T, void* probs, int64_t rows,
                             int dk, int L, int K, int dtype, hipStream_t stream);
+// dx of the hashing for the upstream gradient dprobs (same limits).
+hipError_t launch_hash_probs_bwd(const void* x, const float* planes_T, const void* dprobs, void* dx,
+                                int64_t rows, int dk, int L, int K, int dtype, hipStream_t stream);
 
 // ---- Algorithm 1 with the hashing inside (alg1.hip): bf16 q, k, v, out ----
 struct Alg1Args {
@@ -210,6 +213,22 @@ int alg1_blocks_per_cu(int D, int P, int L, int variant);
 // Tile sums, scan (final state into a.state when not null) and output pass.
 hipError_t launch_alg1(const Alg1Args& a, const Problem& p, int variant, hipStream_t stream,
                        Marks* marks);
+
+// ---- the causal op with the hashing inside (hashed_causal.hip) ----
+struct HashedArgs {
+    const void* q;        // query rows [N][T][d] (p.dtype)
+    const void* k;        // key rows [N][T][d]
+    const void* v;        // values [N][T][d]
+    const float* planes;  // hash planes [L*K][d] fp32, row j = l*K + k
+    void* out;
+    float* records;       // [N][tiles][rec]
+    float* state;         // nullable: [N][S*d + S]
+    int L, K;             // tables, planes per table (R = 2^K, S = L*R)
+};
+// K >= 2, L*K <= 64, and an MFMA specialization for (L * 2^K, d).
+bool hashed_causal_supported(int L, int K, int d);
+// Tile sums, scan (final state into a.state when not null) and output pass.
+hipError_t launch_hashed_causal(const HashedArgs& a, const Problem& p, hipStream_t stream, Marks* marks);
 
 // Whether the MFMA causal path has a specialization for (S, d).
 bool mfma_causal_supported(int S, int d);

@@ -11,6 +11,11 @@
 //   causal_backward(probsQ, probsK, V, dOut, need_q, need_k, need_v,
 //                   tile_tokens=0, kernel=0) -> (dQ or None, dK or None, dV or None)
 //   hash_probs(x, planes_T, L, K) -> [..., L, 2^K] bucket probabilities
+//   hash_probs_backward(x, planes_T, dprobs, L, K) -> dx
+//   hashed_forward(K, Q, V, planes, L, tile_tokens=0, want_records=False, want_state=False)
+//       -> (out, records or None, state or None, tile_tokens): the causal op
+//       with the hashing inside (race_hashed_fwd)
+//   hashed_supported(L, K, d) -> bool
 //   select_tile_tokens(N, T, L, R, d, bf16, causal, tile_tokens=0, kernel=0) -> int
 //   shape_supported(L, R, d) -> (supported, has_mfma)
 //   alg1_forward(q, k, v, W, beta, tile_tokens=0, tensor_cores=False) -> out
@@ -398,6 +403,120 @@ at::Tensor hash_probs(const at::Tensor& x, const at::Tensor& planes_T, int64_t L
     return probs;
 }
 
+// dprobs -> dx of the hashing (race_hash_probs_bwd).
+at::Tensor hash_probs_backward(const at::Tensor& x, const at::Tensor& planes_T,
+                               const at::Tensor& dprobs, int64_t L, int64_t K) {
+    ArgCheck c("race_hash_probs_backward");
+    c.on_gpu("x", x).dtype_is("x", x, true).require(x.dim() >= 1, "x", "has no feature dimension");
+    c.raise();
+    const int64_t dk = x.size(-1);
+    std::vector<int64_t> pshape(x.sizes().begin(), x.sizes().end() - 1);
+    pshape.push_back(L);
+    pshape.push_back(int64_t(1) << K);
+    c.on_gpu("planes_T", planes_T)
+        .require(planes_T.scalar_type() == at::kFloat && planes_T.device() == x.device(), "planes_T",
+                 "must be float32 on x's device")
+        .require(planes_T.dim() == 2 && planes_T.size(0) == dk && planes_T.size(1) == L * K,
+                 "planes_T", "has shape " + dims(planes_T) + ", not [d_k, L*K]")
+        .on_gpu("dprobs", dprobs)
+        .matches("dprobs", dprobs, "x", x)
+        .require(dprobs.sizes() == at::IntArrayRef(pshape), "dprobs",
+                 "has shape " + dims(dprobs) + ", not x's leading dimensions + [L, 2^K]")
+        .raise();
+    const c10::DeviceGuard guard(x.device());
+    at::Tensor dx = at::empty_like(x);
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+    check_status(race_hash_probs_bwd(x.data_ptr(), planes_T.data_ptr<float>(), dprobs.data_ptr(),
+                                     dx.data_ptr(), x.numel() / std::max<int64_t>(dk, 1),
+                                     static_cast<int32_t>(dk), static_cast<int32_t>(L),
+                                     static_cast<int32_t>(K),
+                                     x.scalar_type() == at::kBFloat16 ? RACE_BF16 : RACE_F32, stream),
+                 "race_hash_probs_bwd");
+    return dx;
+}
+
+// The hashed causal forward's arguments: K, Q, V token rows [N, T, d] of one
+// dtype, planes [L * Kp, d] float32 (the reference's race_fused_fwd(K, Q, V,
+// planes, L), src/race_fused_fwd.cu:150-171).  Returns the shape and Kp.
+std::pair<race_shape, int32_t> hashed_validate(const at::Tensor& k, const at::Tensor& q,
+                                               const at::Tensor& v, const at::Tensor& planes,
+                                               int64_t L) {
+    ArgCheck c("race_fused_fwd_hashed");
+    c.require(k.dim() == 3, "K", "has shape " + dims(k) + ", not [N, T, d]")
+        .on_gpu("K", k).dtype_is("K", k, true)
+        .on_gpu("Q", q).matches("Q", q, "K", k)
+        .require(q.sizes() == k.sizes(), "Q", "has shape " + dims(q) + ", K " + dims(k))
+        .on_gpu("V", v).matches("V", v, "K", k)
+        .require(v.sizes() == k.sizes(), "V", "has shape " + dims(v) + ", K " + dims(k))
+        .on_gpu("planes", planes)
+        .require(planes.scalar_type() == at::kFloat && planes.device() == k.device(), "planes",
+                 "must be float32 on K's device")
+        .require(L >= 1 && planes.dim() == 2 && k.dim() == 3 && planes.size(1) == k.size(2) &&
+                     planes.size(0) % L == 0 && planes.size(0) / L >= 1 && planes.size(0) / L <= 8,
+                 "planes", "has shape " + dims(planes) + ", not [L * K, d] for L = " +
+                               std::to_string(L) + " and 1 <= K <= 8");
+    c.raise();
+    const int32_t Kp = static_cast<int32_t>(planes.size(0) / L);
+    race_shape sh;
+    sh.num_streams = k.size(0);
+    sh.seq_len = k.size(1);
+    sh.num_tables = static_cast<int32_t>(L);
+    sh.num_buckets = 1 << Kp;
+    sh.head_dim = static_cast<int32_t>(k.size(2));
+    sh.dtype = k.scalar_type() == at::kBFloat16 ? RACE_BF16 : RACE_F32;
+    return {sh, Kp};
+}
+
+// race_fused_fwd_hashed -> (out, records [N, tiles, rec] or None, state or
+// None, tile length).
+std::tuple<at::Tensor, c10::optional<at::Tensor>, c10::optional<at::Tensor>, int64_t> hashed_forward(
+    const at::Tensor& k, const at::Tensor& q, const at::Tensor& v, const at::Tensor& planes, int64_t L,
+    int64_t tile_tokens, bool want_records, bool want_state) {
+    const auto [sh, Kp] = hashed_validate(k, q, v, planes, L);
+    const race_options opts = make_options(tile_tokens, RACE_KERNEL_AUTO);
+    size_t bytes = 0;
+    int64_t tiles = 0, rec = 0;
+    const race_status st = race_hashed_fwd_workspace_bytes(&sh, Kp, &opts, &bytes, &tiles, &rec);
+    TORCH_CHECK(st == RACE_SUCCESS, "race_fused_fwd_hashed: no kernel takes L=", L, ", K=", Kp,
+                ", d=", sh.head_dim, " (the hashed kernels need K >= 2, L*K <= 64, L*2^K in ",
+                "{64, 128, 256} and d in {64, 128}): ", race_status_string(st));
+    const c10::DeviceGuard guard(k.device());
+    at::Tensor out = at::empty_like(v);
+    const int64_t S = int64_t(sh.num_tables) * sh.num_buckets;
+    at::Tensor state;
+    if (want_state)
+        state = at::empty({sh.num_streams, S * sh.head_dim + S}, v.options().dtype(at::kFloat));
+    at::Tensor ws = at::empty({static_cast<int64_t>((bytes + 3) / 4)}, v.options().dtype(at::kFloat));
+    int32_t tile = 0;
+    race_options wg = opts;
+    wg.kernel = RACE_KERNEL_MFMA_WG;
+    check_status(race_select_tile_tokens(&sh, 1, &wg, &tile), "race_select_tile_tokens");
+    const hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+    check_status(race_hashed_fwd(k.data_ptr(), q.data_ptr(), v.data_ptr(), planes.data_ptr<float>(),
+                                 out.data_ptr(), want_state ? state.data_ptr<float>() : nullptr, &sh, Kp,
+                                 &opts, ws.data_ptr(), bytes, stream),
+                 "race_hashed_fwd");
+    c10::optional<at::Tensor> records, st_out;
+    if (want_records) {
+        const int64_t N = sh.num_streams;
+        records = (tiles > 0 && N > 0) ? ws.narrow(0, 0, N * tiles * rec).view({N, tiles, rec})
+                                       : at::zeros({N, tiles, rec}, v.options().dtype(at::kFloat));
+    }
+    if (want_state) st_out = state;
+    return {out, records, st_out, tile};
+}
+
+// Whether the hashed forward has kernels for (L, K, d).  Host logic only.
+bool hashed_supported(int64_t L, int64_t K, int64_t d) {
+    if (L < 1 || K < 1 || K > 8 || d < 1) return false;
+    race_shape sh{1, 1, static_cast<int32_t>(L), static_cast<int32_t>(1 << K), static_cast<int32_t>(d),
+                  RACE_F32};
+    race_options o{RACE_SUB_CHUNK_TOKENS, RACE_KERNEL_AUTO};
+    size_t bytes = 0;
+    return race_hashed_fwd_workspace_bytes(&sh, static_cast<int32_t>(K), &o, &bytes, nullptr, nullptr) ==
+           RACE_SUCCESS;
+}
+
 int64_t select_tile_tokens(int64_t N, int64_t T, int64_t L, int64_t R, int64_t d, bool bf16,
                            bool causal, int64_t tile_tokens, int64_t kernel) {
     race_shape sh{N, T, static_cast<int32_t>(L), static_cast<int32_t>(R),
@@ -647,6 +766,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("kernel") = 0);
     m.def("hash_probs", &hash_probs, "Bucket probabilities of token rows -> [..., L, 2^K]",
           py::arg("x"), py::arg("planes_T"), py::arg("L"), py::arg("K"));
+    m.def("hash_probs_backward", &hash_probs_backward,
+          "Gradient of hash_probs w.r.t. the rows: (x, planes_T, dprobs, L, K) -> dx", py::arg("x"),
+          py::arg("planes_T"), py::arg("dprobs"), py::arg("L"), py::arg("K"));
+    m.def("hashed_forward", &hashed_forward,
+          "race_fused_fwd_hashed(K, Q, V, planes, L): the causal op with the hashing inside "
+          "-> (out, records or None, state or None, tile length)",
+          py::arg("K"), py::arg("Q"), py::arg("V"), py::arg("planes"), py::arg("L"),
+          py::arg("tile_tokens") = 0, py::arg("want_records") = false, py::arg("want_state") = false);
+    m.def("hashed_supported", &hashed_supported,
+          "Whether the hashed causal forward has kernels for (L, K, d)", py::arg("L"), py::arg("K"),
+          py::arg("d"));
     m.def("select_tile_tokens", &select_tile_tokens, "Tile length a forward would use",
           py::arg("N"), py::arg("T"), py::arg("L"), py::arg("R"), py::arg("d"),
           py::arg("bf16") = false, py::arg("causal") = true, py::arg("tile_tokens") = 0,

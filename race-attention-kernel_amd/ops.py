@@ -156,8 +156,93 @@ def select_tile_tokens(N: int, T: int, L: int, R: int, d: int, *, bf16: bool = F
                                          _kernel_id(kernel))
 
 
+class HashProbsFunction(torch.autograd.Function):
+    """probs = race_hash_probs(x, planes_T, L, K), differentiable w.r.t. x.
+
+    The planes are a buffer in the reference module (src/race_baseline.py:27),
+    so they get no gradient.  The backward is race_hash_probs_bwd."""
+
+    @staticmethod
+    def forward(ctx, x, planes_T, L, K):
+        x = _dense(x)
+        planes_T = planes_T.float().contiguous()
+        ctx.L, ctx.K = int(L), int(K)
+        if ctx.needs_input_grad[0]:
+            ctx.save_for_backward(x, planes_T)
+        return _lib.ext().hash_probs(x, planes_T, ctx.L, ctx.K)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_probs):
+        x, planes_T = ctx.saved_tensors
+        dx = _lib.ext().hash_probs_backward(x, planes_T, _dense(grad_probs.to(x.dtype)), ctx.L, ctx.K)
+        return dx, None, None, None
+
+
 def race_hash_probs(x: torch.Tensor, planes_T: torch.Tensor, L: int, K: int) -> torch.Tensor:
     """Bucket probabilities [..., L, 2^K] of token rows x [..., d_k]: the
     hashing of src/race_baseline.py:41-44 (tanh of the shared-plane
-    projections over sqrt(d_k), softmax over the 2^K corners), on the GPU."""
-    return _lib.ext().hash_probs(_dense(x), planes_T.contiguous(), int(L), int(K))
+    projections over sqrt(d_k), softmax over the 2^K corners), on the GPU.
+    Differentiable w.r.t. x."""
+    return HashProbsFunction.apply(x, planes_T, int(L), int(K))
+
+
+class HashedRaceFunction(torch.autograd.Function):
+    """out = race_fused_fwd_hashed(K, Q, V, planes, L): the causal op with the
+    hashing inside the kernels (no probabilities in memory).
+
+    Backward: the probabilities are recomputed (race_hash_probs), the causal
+    backward starts from the forward's tile records, and the hashing backward
+    (race_hash_probs_bwd) takes dprobs to the rows."""
+
+    @staticmethod
+    def forward(ctx, K, Q, V, planes, L, tile_tokens):
+        needs = any(ctx.needs_input_grad[:3])
+        out, records, _, tile = _lib.ext().hashed_forward(K, Q, V, planes, int(L), int(tile_tokens),
+                                                          needs, False)
+        if needs:
+            ctx.save_for_backward(K, Q, V, planes, records)
+            ctx.L, ctx.tile = int(L), int(tile)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_out):
+        need_k, need_q, need_v = ctx.needs_input_grad[:3]
+        K, Q, V, planes, records = ctx.saved_tensors
+        L = ctx.L
+        Kp = planes.shape[0] // L
+        ext = _lib.ext()
+        planes_T = planes.t().contiguous()
+        probsK = ext.hash_probs(K, planes_T, L, Kp)
+        probsQ = ext.hash_probs(Q, planes_T, L, Kp)
+        g = _dense(grad_out.to(V.dtype))
+        dpq, dpk, dv = ext.causal_backward(probsQ, probsK, V, g, need_q, need_k, need_v, ctx.tile, 0,
+                                           records)
+        dk = ext.hash_probs_backward(K, planes_T, dpk, L, Kp) if need_k else None
+        dq = ext.hash_probs_backward(Q, planes_T, dpq, L, Kp) if need_q else None
+        return dk, dq, dv, None, None, None
+
+
+def race_fused_fwd_hashed(K: torch.Tensor, Q: torch.Tensor, V: torch.Tensor, planes: torch.Tensor,
+                          L: int, *, tile_tokens: int = 0) -> torch.Tensor:
+    """The causal op with the hashing inside: BatchedACE.forward's lines 41-51
+    (src/race_baseline.py) in one op, the reference's fused forward
+    race_fused_fwd(K, Q, V, planes, L) (src/race_fused_fwd.cu:150-171).
+
+    Args:
+        K, Q, V: [N, T, d] token rows (float32 or bfloat16, one dtype), d = d_k.
+        planes: [L * K_planes, d] float32 hash planes (the reference's
+            `planes`; BatchedACE's planes_T transposed).
+        L: hash tables; R = 2^K_planes buckets each.
+
+    Returns [N, T, d]: race_fused_fwd(hash(Q), hash(K), V, causal=True) with
+    the probabilities computed inside the kernels.  Differentiable w.r.t. K,
+    Q and V."""
+    return HashedRaceFunction.apply(_dense(K), _dense(Q), _dense(V), planes.float().contiguous(), int(L),
+                                    int(tile_tokens))
+
+
+def hashed_supported(L: int, K: int, d: int) -> bool:
+    """Whether race_fused_fwd_hashed has kernels for L tables of 2^K buckets, width d."""
+    return bool(_lib.ext().hashed_supported(int(L), int(K), int(d)))

@@ -346,3 +346,51 @@ def test_alg1_torch_binding_validates_inputs_on_the_host(race, ext):
     assert race.causal_v2.sub_chunk_tokens(64, 4) == 64
     assert race.causal_v2.output_pass_smem_bytes(64, 4, 4) > 0
     assert race.causal_v2.precise_carry()
+
+
+def test_hashed_forward_limits_and_workspace(race):
+    # The hashed causal forward takes R = 2^K buckets, K >= 2, L*K <= 64,
+    # S = L*2^K in {64, 128, 256} and d in {64, 128}; its workspace and tile
+    # records are race_fwd's at the workgroup kernels' tile policy.
+    from race_attention_kernel_amd import abi
+
+    inv = abi.RACE_ERROR_INVALID_VALUE
+    opts = abi.options(512, 0)
+    st, nbytes, tiles, rec = abi.hashed_fwd_workspace_bytes(abi.shape(8, 65536, 4, 16, 64), 4, opts)
+    assert st == 0 and tiles == 128 and rec == 4160 and nbytes == 8 * 128 * 4160 * 4
+    want = abi.fwd_workspace_bytes(abi.shape(8, 65536, 4, 16, 64), True, abi.options(512, 3))
+    assert (st, nbytes, tiles, rec) == want
+    for L, R, K, d in [(8, 32, 5, 128), (2, 32, 5, 64), (16, 16, 4, 64), (8, 16, 4, 128), (16, 4, 2, 128),
+                       (1, 256, 8, 64)]:
+        assert abi.hashed_fwd_workspace_bytes(abi.shape(2, 100, L, R, d), K, opts)[0] == 0, (L, R, d)
+    for L, R, K, d, why in [(4, 16, 3, 64, "R != 2^K"), (32, 2, 1, 64, "K = 1"), (4, 16, 4, 32, "d = 32"),
+                            (2, 16, 4, 64, "S = 32"), (32, 4, 2, 64, "L*K = 64 but S = 128 ok?")]:
+        st = abi.hashed_fwd_workspace_bytes(abi.shape(2, 100, L, R, d), K, opts)[0]
+        if why.startswith("L*K = 64"):
+            assert st == 0  # L = 32, K = 2: L*K = 64 and S = 128 are both in range
+        else:
+            assert st == inv, why
+    # L*K past 64 (S = 256 at L = 64, K = 2).
+    assert abi.hashed_fwd_workspace_bytes(abi.shape(2, 100, 64, 4, 128), 2, opts)[0] == inv
+    # Only the matrix-core kernels hash.
+    assert abi.hashed_fwd_workspace_bytes(abi.shape(2, 100, 4, 16, 64), 4,
+                                          abi.options(512, abi.RACE_KERNEL_VALU))[0] == inv
+    # Null or misaligned pointers are refused before any launch.
+    sh = abi.shape(2, 100, 4, 16, 64)
+    assert abi.hashed_fwd(0, 16, 16, 16, 16, None, sh, 4, opts, 16, 1 << 30, 0) == inv
+    assert abi.hashed_fwd(16, 16, 16, 24, 16, None, sh, 4, opts, 16, 1 << 30, 0) == inv
+    assert abi.hashed_fwd(16, 16, 16, 16, 16, None, sh, 4, opts, 16, 64, 0) == inv  # workspace
+    # An empty sequence without a state asked for is a no-op.
+    assert abi.hashed_fwd(0, 0, 0, 0, 0, None, abi.shape(2, 0, 4, 16, 64), 4, None, None, 0, 0) == 0
+
+
+def test_hashed_binding_validates_inputs_on_the_host(race, ext):
+    import torch
+
+    x = torch.zeros(2, 64, 64)
+    planes = torch.zeros(16, 64)
+    with pytest.raises(RuntimeError, match="race_fused_fwd_hashed: K lives on the CPU"):
+        ext.hashed_forward(x, x, x, planes, 4)
+    assert ext.hashed_supported(4, 4, 64) and ext.hashed_supported(8, 5, 128)
+    assert not ext.hashed_supported(4, 4, 32) and not ext.hashed_supported(8, 1, 64)
+    assert race.hashed_supported(4, 4, 64)
