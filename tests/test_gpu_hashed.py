@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import FP32_TOL, per_stream_rel_err, say, to_np, tol_for
+from gpu_util import FP32_TOL, assert_bf16_floor, per_stream_rel_err, say, to_np, tol_for
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +72,25 @@ def test_hashed_forward_cfg2_full_length(race, oracle, cuda):
     err = per_stream_rel_err(to_np(out), oracle_out(oracle, k, q, v, planes, 4, 4))
     say("hashed cfg2 max rel err", f"{err:.3e}")
     assert err <= FP32_TOL
+
+
+def test_hashed_forward_bf16_long(race, oracle, cuda):
+    # bf16 rows at T = 2^18, N = 8, L = 4, K = 4, d = 64 (rows generated on
+    # the GPU): every stream within the north-star bound and the rounding
+    # floor bound (max <= 2.5 F, rms <= 2.0 F_rms).
+    T = 1 << 18
+    say("hashed bf16 long", T)
+    gen = torch.Generator(device=cuda).manual_seed(9)
+    k, q, v = (torch.randn(8, T, 64, generator=gen, device=cuda).to(torch.bfloat16) for _ in range(3))
+    planes = torch.randn(16, 64, generator=gen, device=cuda)
+    out = race.race_fused_fwd_hashed(k, q, v, planes, 4)
+    torch.cuda.synchronize()
+    ref = oracle_out(oracle, k, q, v, planes, 4, 4)
+    o = to_np(out)
+    err = per_stream_rel_err(o, ref)
+    say("hashed bf16 long max rel err", f"{err:.3e}")
+    assert err <= tol_for(torch.bfloat16)
+    assert_bf16_floor(o, ref, float(v.float().abs().max()), "hashed bf16 long")
 
 
 def test_hashed_equals_hashing_then_the_op(race, cuda):
