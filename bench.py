@@ -26,17 +26,26 @@ when a measurement for this workload exists, else null.
 
 cpu_baseline: the reference's CPU path -- the fp32 torch cumsum + bmm
 composition of src/race_baseline.py:45-51, as restated in oracle/ -- timed on
-this host's cores on the bench workload itself (cfg2: N = 8, T = 65536; a
-shorter T when the host has too little free memory for its 5-D tensors):
-1 warmup, median of 3.
+this host's cores (os.cpu_count() bounded by the CPUs this job may use),
+each T in a fresh process (oracle/cpu_baseline.py, which also reports its
+peak RSS): cfg1 (T = 4096) and the cfg2 shape at T = 512 ... 65536 while the
+predicted peak fits in half the available memory; 1 warmup, median of 3.
+`value` is the T = 65536 point.  The CPU points run before the GPU is
+touched.
+
+config.max_T_measured: the headline also runs the cfg2 forward at the
+longest T (a multiple of 2^20) whose tensors fit the free device memory and
+reports its T and M tokens/s.
 
 Other workloads and passes (--workload, --pass bwd|fwdbwd) print the same
 line for that configuration; the CPU baseline belongs to the headline
-(cfg2 forward) only.
+(cfg2 forward) only.  --sweep prints a markdown table over T = 512 ... 65536
+instead of the JSON line.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
                        [--pass fwd|bwd|fwdbwd|module] [--T T] [--kernel auto|valu|mfma|mfma_wg]
-                       [--tile N] [--no-cpu-baseline] [--calibrate-copy MIB]
+                       [--tile N] [--no-cpu-baseline] [--no-max-t] [--sweep]
+                       [--calibrate-copy MIB]
 """
 from __future__ import annotations
 
@@ -148,6 +157,10 @@ def parse_args():
     ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg", "decode"], default="auto")
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-max-t", action="store_true",
+                    help="skip the headline's run at the longest T that fits (config.max_T_measured)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="measure the pass at T = 512 ... 65536 and print a markdown table instead")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before timing (rocprofv3 counter scale)")
     return ap.parse_args()
@@ -209,46 +222,126 @@ def traffic_for(workload_key: str, kernel_name: str):
     return None if entry_ is None else entry_.get("hbm_bytes_per_launch")
 
 
-def cpu_baseline():
-    """The reference CPU path (torch fp32 cumsum + bmm) on the cfg2 workload.
-
-    Its 5-D prefix tensors need about 2.2 * N * T * S * d * 4 bytes
-    (src/race_baseline.py:46-47); T is halved until that fits in a third of
-    the host's available memory."""
-    import torch
-
-    race = entry.load_package()
-    oracle = entry.load_oracle()
-    N, T, L, R, d = 8, 65536, 4, 16, 64
+def host_cpu_info() -> dict:
+    """os.cpu_count(), the CPUs this process may run on (affinity and the
+    cgroup quota), the thread count the baseline uses, the CPU model and
+    the available host memory."""
+    info = {"cpu_count": os.cpu_count()}
     try:
-        import psutil
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["affinity_cpus"] = os.cpu_count()
+    quota = None
+    try:
+        q, period = pathlib.Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
+    info["cgroup_cpus"] = quota
+    # Every core this job may use: os.cpu_count() (as BASELINE's plan asks),
+    # bounded by the affinity mask, the cgroup quota and the OMP_NUM_THREADS
+    # share the GPU box assigns to one GPU.
+    threads = os.cpu_count() or 1
+    for cap in (info["affinity_cpus"], quota, os.environ.get("OMP_NUM_THREADS")):
+        try:
+            if cap and int(cap) > 0:
+                threads = min(threads, int(cap))
+        except ValueError:
+            pass
+    info["threads"] = threads
+    model = None
+    try:
+        import subprocess
 
-        avail = psutil.virtual_memory().available
-    except ImportError:
-        avail = 64 << 30
-    while T > 1024 and 3 * 2.2 * N * T * L * R * d * 4 > avail:
-        T //= 2
-    q, k, v = race.make_inputs(N, T, L, R, d, seed=1)
-    q, k = q.flatten(2), k.flatten(2)
-    threads = torch.get_num_threads()
-    with torch.no_grad():
-        oracle.torch_reference_path(q, k, v)  # warmup
-        times = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            oracle.torch_reference_path(q, k, v)
-            times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, ValueError):
+        pass
+    if model is None:
+        try:
+            for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    info["cpu_model"] = model
+    try:
+        for line in pathlib.Path("/proc/meminfo").read_text().splitlines():
+            if line.startswith("MemAvailable:"):
+                info["mem_available_bytes"] = int(line.split()[1]) * 1024
+    except (OSError, ValueError):
+        info["mem_available_bytes"] = None
+    return info
+
+
+# The CPU sweep of the cfg2 shape (BASELINE's CPU plan): every T whose
+# predicted peak stays under half the available host memory; T = 4096 is
+# also cfg1, the reference's CPU-runnable configuration.
+CPU_SWEEP_T = [512, 1024, 2048, 4096, 8192, 16384, 32768, 65536]
+
+
+def cpu_point(N, T, L, R, d, threads, timeout=600) -> dict:
+    """One CPU point in a fresh interpreter (oracle/cpu_baseline.py)."""
+    import subprocess
+
+    cmd = [sys.executable, str(REPO / "oracle" / "cpu_baseline.py"), "--N", str(N), "--T", str(T),
+           "--L", str(L), "--R", str(R), "--d", str(d), "--threads", str(threads)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    if res.returncode != 0:
+        raise RuntimeError(f"cpu baseline at T={T} failed ({res.returncode}): {res.stderr[-2000:]}")
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def cpu_baseline():
+    """The reference CPU path (torch fp32 cumsum + bmm) on this host.
+
+    cfg1 (N = 8, T = 4096) always, then the cfg2 shape swept over T while its
+    predicted peak fits in half the available memory; each point in a fresh
+    process (its own peak RSS), 1 warmup + median of 3.  `value` is the
+    bench workload's T = 65536 point (the largest measured T if that one
+    does not fit)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("race_cpu_baseline", REPO / "oracle" / "cpu_baseline.py")
+    cb = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(cb)
+    info = host_cpu_info()
+    N, L, R, d = 8, 4, 16, 64
+    avail = info.get("mem_available_bytes") or (64 << 30)
+    sweep, skipped = [], []
+    for T in CPU_SWEEP_T:
+        if cb.predicted_peak_bytes(N, T, L * R, d) > avail / 2:
+            skipped.append(T)
+            continue
+        pt = cpu_point(N, T, L, R, d, info["threads"])
+        print(f"# cpu T={T}: {pt['ms']:.1f} ms, {pt['m_tokens_per_s']:.4f} {UNIT}, peak RSS "
+              f"{pt['peak_rss_bytes'] / 2**30:.2f} GiB", file=sys.stderr, flush=True)
+        sweep.append({"T": T, "ms": pt["ms"], "m_tokens_per_s": pt["m_tokens_per_s"],
+                      "peak_rss_bytes": pt["peak_rss_bytes"],
+                      "predicted_peak_bytes": pt["predicted_peak_bytes"]})
+    if not sweep:
+        raise RuntimeError("cpu baseline: no T fits in half the available host memory")
+    cfg1 = next((x for x in sweep if x["T"] == 4096), None)
+    head = next((x for x in sweep if x["T"] == 65536), sweep[-1])
     return {
-        "value": round(N * T / med / 1e6, 4),
+        "value": head["m_tokens_per_s"],
         "unit": UNIT,
-        "cores": threads,
+        "cores": info["threads"],
         "kind": "port",
-        "sample": (f"causal N={N} T={T} L={L} R={R} d={d} fp32 (the cfg2 workload"
-                   f"{'' if T == 65536 else ', T reduced to fit host memory'}), the torch-CPU "
-                   f"cumsum+bmm composition of src/race_baseline.py:45-51 (oracle/oracle.py "
-                   f"torch_reference_path), {threads} threads, median of 3 after 1 warmup: "
-                   f"{med * 1e3:.1f} ms per call"),
+        "sample": (f"causal N={N} T={head['T']} L={L} R={R} d={d} fp32 (the cfg2 workload), the "
+                   f"torch-CPU cumsum+bmm composition of src/race_baseline.py:45-51 "
+                   f"(oracle/oracle.py torch_reference_path) in a fresh process per T, "
+                   f"{info['threads']} threads, median of 3 after 1 warmup: {head['ms']:.1f} ms per "
+                   f"call, peak RSS {head['peak_rss_bytes'] / 2**30:.2f} GiB"),
+        "host": info,
+        "cfg1": cfg1,
+        "sweep": sweep,
+        "skipped_host_memory": skipped,
     }
 
 
@@ -494,25 +587,15 @@ def bench_decode(args) -> int:
     return 0
 
 
-def main() -> int:
-    args = parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
-              "multi-GPU sharding of the op is designed but not measured here.",
-              file=sys.stderr)
-        return 2
-    if args.pass_ == "alg1":
-        return bench_alg1(args)
-    if args.pass_ == "decode":
-        return bench_decode(args)
+def measure(args, T: int) -> dict:
+    """One bench line (without cpu_baseline) for args' workload and pass at T."""
     import torch
 
     race = entry.load_package()
     from race_attention_kernel_amd import abi
 
-    cfg_key, default_T = WORKLOADS[args.workload]
+    cfg_key, _ = WORKLOADS[args.workload]
     cfg = race.CONFIGS[cfg_key]
-    T = args.T or default_T
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     es = 2 if cfg.dtype == torch.bfloat16 else 4
@@ -766,8 +849,130 @@ def main() -> int:
     if run_hash or run_hashed:
         del xq, xk, planes_T, planes
     torch.cuda.empty_cache()
-    if not args.no_cpu_baseline and headline:
-        result["cpu_baseline"] = cpu_baseline()
+    return result
+
+
+def max_t_leg(steps: int = 3) -> dict:
+    """The cfg2 forward (fp32, N = 8, S = d = 64) at the longest T whose four
+    tensors and workspace fit in 92% of the free device memory, T a multiple
+    of 2^20: 1 warmup step, then `steps` timed ones between two HIP events.
+    Inputs are filled a chunk of tokens at a time (no full-size
+    temporaries) with the BASELINE distribution."""
+    import torch
+
+    race = entry.load_package()
+    from race_attention_kernel_amd import abi
+
+    N, L, R, d = 8, 4, 16, 64
+    S = L * R
+    dev = torch.device("cuda:0")
+    torch.cuda.empty_cache()
+    free, total = torch.cuda.mem_get_info(dev)
+    per_token = N * (2 * S + 2 * d) * 4
+    opts = abi.options(0, 0)
+    T = int(0.92 * free / per_token) >> 20 << 20
+    while T > 0:
+        sh = abi.shape(N, T, L, R, d, abi.RACE_F32)
+        st, ws_bytes, tiles, _ = abi.fwd_workspace_bytes(sh, True, opts)
+        if st != 0:
+            raise RuntimeError(abi.status_string(st))
+        if T * per_token + ws_bytes <= 0.92 * free:
+            break
+        T -= 1 << 20
+    if T <= 0:
+        return {"T": 0, "note": "no 2^20-token multiple fits"}
+    torch.cuda.reset_peak_memory_stats(dev)
+    q = torch.empty((N, T, L, R), device=dev, dtype=torch.float32)
+    k = torch.empty_like(q)
+    v = torch.empty((N, T, d), device=dev, dtype=torch.float32)
+    out = torch.empty_like(v)
+    ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)
+    g = torch.Generator(device=dev).manual_seed(3)
+    chunk = 1 << 22
+    for n in range(N):
+        for c in range(0, T, chunk):
+            e = min(T, c + chunk)
+            for x in (q, k):
+                x[n, c:e] = torch.softmax(torch.randn((e - c, L, R), generator=g, device=dev) * 4.0, -1)
+            v[n, c:e] = torch.randn((e - c, d), generator=g, device=dev)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+
+    def step():
+        st_ = abi.fwd(*ptrs, None, sh, True, opts, ws.data_ptr(), ws_bytes, stream)
+        if st_ != 0:
+            raise RuntimeError(abi.status_string(st_))
+
+    step()
+    torch.cuda.synchronize()
+    events = HipEvents()
+    ev = events.array(2)
+    events.record(ev[0], stream)
+    for _ in range(steps):
+        step()
+    events.record(ev[1], stream)
+    torch.cuda.synchronize()
+    ms = events.elapsed_ms(ev[0], ev[1]) / steps
+    events.destroy()
+    peak = torch.cuda.max_memory_allocated(dev)
+    del q, k, v, out, ws
+    torch.cuda.empty_cache()
+    return {
+        "T": T, "N": N, "dtype": "f32", "steps": steps, "ms_per_step": round(ms, 3),
+        "m_tokens_per_s": round(N * T / (ms * 1e-3) / 1e6, 1),
+        "peak_hbm_bytes": peak, "hbm_total_bytes": total, "tile_tokens": T // tiles,
+    }
+
+
+# The GPU sweep of the cfg2 shape (BASELINE's configuration 2: T = 512 to
+# 65536, powers of two).
+GPU_SWEEP_T = [512, 1024, 2048, 4096, 8192, 16384, 32768, 65536]
+
+
+def sweep(args) -> int:
+    """--sweep: one measurement per T of the workload's pass; prints a
+    markdown table (and no JSON line)."""
+    rows = []
+    for T in GPU_SWEEP_T:
+        r = measure(args, T)
+        print(f"# T={T}: {r['value']:.1f} {UNIT}", file=sys.stderr, flush=True)
+        rows.append(r)
+    print(f"{rows[0]['metric'].split(' at ')[0]} sweep, workload {args.workload}, "
+          f"{args.steps} timed steps after {args.warmup} warmup\n")
+    print("| T | M tokens/s | ms / step | peak HBM bytes / token (T) | whole-op HBM frac "
+          "| dominant kernel | its frac | kernel ms |")
+    print("|---|---|---|---|---|---|---|---|")
+    for r in rows:
+        c, rf = r["config"], r["roofline"]
+        kms = ", ".join(f"{k_}: {v_:.4f}" for k_, v_ in c["kernel_ms"].items())
+        print(f"| {c['T']} | {r['value']:.1f} | {r['ms_per_step']:.4f} | {c['peak_hbm_bytes_per_token']:.0f} "
+              f"| {rf['whole_op_frac']:.3f} | {rf['kernel']} | {rf['frac']:.3f} | {kms} |")
+    return 0
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding of the op is designed but not measured here.",
+              file=sys.stderr)
+        return 2
+    if args.pass_ == "alg1":
+        return bench_alg1(args)
+    if args.pass_ == "decode":
+        return bench_decode(args)
+    if args.sweep:
+        return sweep(args)
+    T = args.T or WORKLOADS[args.workload][1]
+    headline = args.workload == "cfg2" and args.pass_ == "fwd"
+    # The CPU points run first, in child processes started before this
+    # process touches the GPU.
+    cpu = cpu_baseline() if (headline and not args.no_cpu_baseline) else None
+    result = measure(args, T)
+    if headline and not args.no_max_t:
+        result["config"]["max_T_measured"] = max_t_leg()
+    result["cpu_baseline"] = cpu
     print(json.dumps(result), flush=True)
     return 0
 

@@ -14,6 +14,10 @@ What is here, and which reference lines each piece restates
   chunked form src/race_chunked.py:41-63; the tiled form the three-launch
   decomposition of src/causal_v2/kernels/race_causal_fwd.h:23-27 with the
   per-bucket function of src/causal_v2/reference.py:144-159.
+* ``causal_tail`` -- the last outputs of long streams: the state before them
+  summed in fp64 blocks, then ``causal_recurrence`` from it (the chunk
+  identity); for checks at lengths the per-token scan of a whole stream
+  would take minutes over.
 * ``cumsum_bmm`` -- numpy transcription of the unchunked composition of
   src/race_baseline.py:45-51 (cumsum, broadcast product, cumsum, divide,
   bmm), in a chosen dtype.  Memory O(N*T*S*d): small T only.
@@ -132,6 +136,33 @@ def causal_recurrence(q, k, v, eps: float = EPS, nthreads: int = 0, want_state: 
         _ptr(st, ctypes.c_double) if st is not None else None,
         _ptr(init, ctypes.c_double) if init is not None else None, N, T, S, d, eps, nthreads)
     return (out, st) if want_state else out
+
+
+def causal_tail(q, k, v, tail: int, eps: float = EPS, nthreads: int = 0, block: int = 1 << 20):
+    """Outputs of the last ``tail`` tokens of every stream, fp64, [N, tail, d].
+
+    The state before them, B = sum_t k_t v_t^T and A = sum_t k_t over the
+    first T - tail tokens, is summed in fp64 blocks of ``block`` tokens
+    (matrix products, so a stream of 2^24 tokens takes seconds); the tail
+    then runs the per-token recurrence from that state, as ``init_state``
+    of ``causal_recurrence`` (the chunk identity, src/race_chunked.py:54-63).
+    """
+    N, T, S = q.shape
+    d = v.shape[2]
+    t0 = T - tail
+    assert 0 <= t0 <= T
+    init = np.zeros((N, S * d + S), np.float64)
+    for n in range(N):
+        B = np.zeros((S, d), np.float64)
+        A = np.zeros(S, np.float64)
+        for b in range(0, t0, block):
+            e = min(t0, b + block)
+            kb = np.asarray(k[n, b:e], np.float64)
+            B += kb.T @ np.asarray(v[n, b:e], np.float64)
+            A += kb.sum(0)
+        init[n, :S * d] = B.ravel()
+        init[n, S * d:] = A
+    return causal_recurrence(q[:, t0:], k[:, t0:], v[:, t0:], eps, nthreads, init_state=init)
 
 
 def causal_chunked(q, k, v, chunk: int, eps: float = EPS, nthreads: int = 0):

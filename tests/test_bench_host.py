@@ -1,0 +1,43 @@
+"""The host side of bench.py's CPU baseline (no GPU): the per-T point in a
+fresh process reports its time, threads and peak RSS, and the host
+description holds what the CPU plan asks for (os.cpu_count(), the threads
+used, the CPU model)."""
+from __future__ import annotations
+
+import importlib.util
+import os
+import pathlib
+
+REPO = pathlib.Path(__file__).resolve().parents[1]
+
+
+def load_bench():
+    spec = importlib.util.spec_from_file_location("race_bench", REPO / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_host_info_names_cores_threads_and_model():
+    info = load_bench().host_cpu_info()
+    assert info["cpu_count"] == os.cpu_count()
+    assert 1 <= info["threads"] <= os.cpu_count()
+    assert info["affinity_cpus"] >= 1
+    assert "cpu_model" in info and "mem_available_bytes" in info
+
+
+def test_cpu_point_runs_in_a_fresh_process():
+    b = load_bench()
+    pt = b.cpu_point(2, 256, 2, 4, 16, 2, timeout=300)
+    assert pt["N"] == 2 and pt["T"] == 256 and pt["S"] == 8 and pt["d"] == 16
+    assert pt["threads"] == 2
+    assert pt["ms"] > 0 and pt["m_tokens_per_s"] > 0
+    # The child's own peak: at least its inputs, and a fresh interpreter's.
+    assert pt["peak_rss_bytes"] >= pt["input_bytes"]
+    assert pt["predicted_peak_bytes"] > pt["input_bytes"]
+
+
+def test_sweep_lengths_cover_cfg1_and_cfg2():
+    b = load_bench()
+    assert 4096 in b.CPU_SWEEP_T and b.CPU_SWEEP_T[-1] == 65536
+    assert b.GPU_SWEEP_T == [512 << i for i in range(8)]

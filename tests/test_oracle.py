@@ -123,6 +123,18 @@ def test_recurrence_continued_from_carried_state(oracle, split):
     assert np.array_equal(oracle.causal_recurrence(q, k, v, init_state=np.zeros_like(fin)), full)
 
 
+@pytest.mark.parametrize("tail, block", [(1, 7), (50, 64), (299, 1000), (300, 3), (120, 1)])
+def test_tail_from_block_sums_is_the_scan(oracle, tail, block):
+    # causal_tail (state from blocked k^T v products, then the scan) gives the
+    # last outputs of the full per-token scan, whatever the block length; a
+    # transposed B in the carried state would fail (S != d here).
+    q, k, v = inputs(tail + block, 3, 300, 2, 16, 24)
+    full = oracle.causal_recurrence(q, k, v)
+    got = oracle.causal_tail(q, k, v, tail, block=block)
+    assert got.shape == (3, tail, 24)
+    assert rel_err(got, full[:, 300 - tail:]) <= FP64_TOL
+
+
 def test_cumsum_bmm_and_dense_forms_agree(oracle):
     q, k, v = inputs(5, 3, 200, 2, 8, 16)
     rec = oracle.causal_recurrence(q, k, v)
