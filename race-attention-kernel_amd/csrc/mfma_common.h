@@ -239,18 +239,22 @@ __device__ __forceinline__ bf16x8 tril_frag(int off, int g, int lr) {
 
 // A token-row tile in LDS staged between global memory and the accumulator
 // layout: [C][D] elements of TIn, row r a run of D * sizeof(TIn) / 16 chunks
-// of 16 bytes with chunk u stored at u ^ (r mod the chunk count, at most 16).
-// Accumulator-layout accesses (16 rows, 4 values each, or 4 rows of 16 single
-// values) and the row-contiguous transfers both spread over the banks, and the
-// global side moves whole rows: 16 bytes per thread, consecutive threads on
-// consecutive bytes.
+// of 16 bytes with chunk u stored at u ^ swz(r).  swz runs over the 256-byte
+// spans the 64 banks cover: rows shorter than a span (bf16 rows of 64 values,
+// 128 bytes) share their span's value, swz(r) = (r / rows per span) mod the
+// chunk count (at most 16).  Accumulator-layout accesses (16 rows, 4 values
+// each, or 4 rows of 16 single values) and the row-contiguous transfers then
+// touch each bank at most once per 16 lanes, and the global side moves whole
+// rows: 16 bytes per thread, consecutive threads on consecutive bytes.
 template <typename TIn, int D, int C>
 struct OutTile {
     static constexpr int kRowBytes = D * int(sizeof(TIn));
     static constexpr int kChunks = kRowBytes / 16;
     static constexpr int kMask = (kChunks < 16 ? kChunks : 16) - 1;
+    static constexpr int kRowsPerSpan = kRowBytes >= 256 ? 1 : 256 / kRowBytes;
+    __device__ __forceinline__ static int swz(int row) { return (row / kRowsPerSpan) & kMask; }
     __device__ __forceinline__ static int at(int row, int byte) {
-        return row * kRowBytes + 16 * ((byte >> 4) ^ (row & kMask)) + (byte & 15);
+        return row * kRowBytes + 16 * ((byte >> 4) ^ swz(row)) + (byte & 15);
     }
     // Values [row][col .. col + 3] (col % 4 == 0) from the accumulator layout.
     __device__ __forceinline__ static void put(unsigned char* t, int row, int col, const f32x4& x) {
@@ -283,7 +287,7 @@ struct OutTile {
     // 16-byte chunk q (row-major over the tile) to or from its swizzled place.
     __device__ __forceinline__ static int chunk_at(int q) {
         const int row = q / kChunks, u = q % kChunks;
-        return row * kRowBytes + 16 * (u ^ (row & kMask));
+        return row * kRowBytes + 16 * (u ^ swz(row));
     }
     // A thread's chunks of the tile (NT threads): chunk q = threadIdx.x + i NT.
     template <int NT>

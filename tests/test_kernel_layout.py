@@ -1,0 +1,551 @@
+"""CPU emulation of the MFMA kernels' index math (no GPU).
+
+Each mapping the kernels rely on is restated here from its definition in
+race-attention-kernel_amd/csrc (the function or expression named in each
+test) and checked the way the reference checks its own kernels' layouts
+(src/causal_v2/tests/test_kernel_layout.py:96-201,317-441;
+src/noncausal/tests/test_kernel_emulation.py:64-153): every mapping covers
+its index space exactly once, composed mappings give the fragments the
+comments promise, and the LDS accesses the comments call conflict-free touch
+each bank once under the model of 64 banks of 4 bytes, a 16-lane group
+served per pass.
+
+Planted mistakes (a dropped or row-only swizzle, swapped lane roles of the
+transposed read, reversed corner bits, a missing final flush, unpadded plane
+rows) are shown to fail the same checks, so the checks are not vacuous.
+"""
+from __future__ import annotations
+
+import itertools
+import math
+from collections import Counter
+
+import numpy as np
+import pytest
+
+BANKS = 64
+BANK_BYTES = 4
+
+
+# ---------------------------------------------------------------------------
+# mfma_common.h: fpos, Plane, OutTile
+
+
+def fpos(k: int) -> int:
+    """mfma_common.h fpos(): element k of an LDS operand row sits at fpos(k)."""
+    return (k & ~31) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3)
+
+
+def k_of(kk: int, g: int, e: int) -> int:
+    """The permuted contraction index of step kk, lane group g, element e."""
+    return 32 * kk + 4 * g + (e % 4) + 16 * (e // 4)
+
+
+class Plane:
+    """mfma_common.h Plane<kSplit, K>: bf16 rows of K elements (hi plane, then
+    the lo plane at +2K bytes when split), chunk u of row r stored at
+    u ^ sw(r), rows 32 bytes longer than the planes."""
+
+    def __init__(self, split: bool, K: int, swizzle: bool = True):
+        self.split, self.K = split, K
+        self.lo_off = 2 * K
+        self.pitch = (4 if split else 2) * K + 32
+        self.mask = min(K // 8, 8) - 1
+        self.swizzle = swizzle
+
+    def sw(self, row: int) -> int:
+        return (((row >> 3) ^ ((row >> 2) & 1)) & self.mask) if self.swizzle else 0
+
+    def elem(self, row: int, k: int) -> int:   # put1
+        p = fpos(k)
+        return row * self.pitch + 16 * ((p >> 3) ^ self.sw(row)) + 2 * (p & 7)
+
+    def off4(self, row: int, k0: int) -> int:  # put4 / off4
+        p = fpos(k0)
+        return row * self.pitch + 16 * ((p >> 3) ^ self.sw(row)) + 8 * ((p >> 2) & 1)
+
+    def frag(self, row: int, kk: int, g: int) -> int:  # frag
+        return row * self.pitch + 16 * ((4 * kk + g) ^ self.sw(row))
+
+
+class OutTile:
+    """mfma_common.h OutTile<TIn, D, C>: [C][D] values, 16-byte chunk u of row
+    r stored at u ^ swz(r), swz(r) = (r / rows per 256-byte span) & kMask.
+    per_span=False gives the row-only swizzle swz(r) = r & kMask (a planted
+    mistake below)."""
+
+    def __init__(self, es: int, D: int, C: int, per_span: bool = True):
+        self.es, self.D, self.C = es, D, C
+        self.row_bytes = D * es
+        self.chunks = self.row_bytes // 16
+        self.mask = min(self.chunks, 16) - 1
+        self.rows_per_span = (1 if self.row_bytes >= 256 else 256 // self.row_bytes) if per_span else 1
+
+    def swz(self, row: int) -> int:
+        return (row // self.rows_per_span) & self.mask
+
+    def at(self, row: int, byte: int) -> int:
+        return row * self.row_bytes + 16 * ((byte >> 4) ^ self.swz(row)) + (byte & 15)
+
+    def chunk_at(self, q: int) -> int:
+        row, u = divmod(q, self.chunks)
+        return row * self.row_bytes + 16 * (u ^ self.swz(row))
+
+
+def bank_load(accesses) -> Counter:
+    """accesses: (byte offset, bytes) per lane -> dwords per bank."""
+    c = Counter()
+    for off, n in accesses:
+        assert off % 4 == 0 and n % 4 == 0
+        for j in range(n // 4):
+            c[(off // BANK_BYTES + j) % BANKS] += 1
+    return c
+
+
+PLANE_KS = [32, 64, 128, 256]  # S, D (64..256) and the P tile's C (32, 64)
+
+
+def test_fpos_permutes_each_32_block():
+    for K in (32, 64, 128, 256):
+        assert sorted(fpos(k) for k in range(K)) == list(range(K))
+        assert all(fpos(k) // 32 == k // 32 for k in range(K))
+
+
+def test_fragment_is_one_contiguous_run_and_two_accumulator_blocks():
+    # Lane group g, step kk: its 8 permuted k land on 8 consecutive positions
+    # (one 16-byte read), and they are exactly rows 4 g + r of two stacked
+    # accumulator blocks (D[4 g + r][lr] of block b = element e = 4 b + r).
+    for kk, g in itertools.product(range(4), range(4)):
+        assert [fpos(k_of(kk, g, e)) for e in range(8)] == [32 * kk + 8 * g + e for e in range(8)]
+        assert [k_of(kk, g, 4 * b + r) - 32 * kk for b in range(2) for r in range(4)] == \
+               [16 * b + 4 * g + r for b in range(2) for r in range(4)]
+    # Over the four lane groups a step covers its 32 k once.
+    for kk in range(4):
+        assert sorted(k_of(kk, g, e) for g in range(4) for e in range(8)) == list(range(32 * kk, 32 * kk + 32))
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", PLANE_KS)
+def test_plane_places_every_element_once_inside_its_row(split, K):
+    P = Plane(split, K)
+    for row in range(64):
+        offs = [P.elem(row, k) for k in range(K)]
+        assert len(set(offs)) == K
+        base = row * P.pitch
+        assert min(offs) >= base and max(offs) + 2 <= base + 2 * K  # hi plane
+        if split:  # the lo plane follows, inside the pitch
+            assert max(offs) + P.lo_off + 2 <= base + P.pitch
+        assert P.pitch >= (4 if split else 2) * K
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", PLANE_KS)
+def test_plane_put4_and_frag_read_what_put1_stored(split, K):
+    P = Plane(split, K)
+    for row in range(48):
+        for k0 in range(0, K, 4):  # put4: 4 consecutive elements, 8 contiguous bytes
+            assert [P.off4(row, k0) + 2 * j for j in range(4)] == [P.elem(row, k0 + j) for j in range(4)]
+        for kk, g in itertools.product(range(K // 32), range(4)):  # frag: the permuted 8
+            assert [P.frag(row, kk, g) + 2 * e for e in range(8)] == \
+                   [P.elem(row, k_of(kk, g, e)) for e in range(8)]
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", PLANE_KS)
+def test_plane_fragment_reads_touch_each_bank_once(split, K):
+    # frag(): 16 consecutive rows (lanes lr of a group), one 16-byte chunk.
+    P = Plane(split, K)
+    for r0, kk, g in itertools.product(range(0, 64, 16), range(K // 32), range(4)):
+        load = bank_load((P.frag(r0 + lr, kk, g), 16) for lr in range(16))
+        assert len(load) == BANKS and max(load.values()) == 1
+
+
+def test_plane_without_swizzle_conflicts():
+    # Planted mistake: without sw() the 16 rows of a fragment pile up.
+    P = Plane(False, 64, swizzle=False)
+    load = bank_load((P.frag(lr, 0, 0), 16) for lr in range(16))
+    assert max(load.values()) > 1
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", [64, 128, 256])
+def test_plane_staging_stores_spread_over_all_banks(split, K):
+    # causal_geo.h KVStage::store: thread tid owns block (a, b) = divmod(tid,
+    # K / E) of 4 rows x E columns and stores rows 4 a + rr, elements
+    # b E + 4 h .. + 3 with put4 (8 bytes).  A wave's 64 stores (512 bytes)
+    # load every bank exactly twice.
+    E = 4 if split else 8  # elements per 16-byte global vector: fp32 / bf16
+    P = Plane(split, K)
+    for rr, h in itertools.product(range(4), range(E // 4)):
+        load = bank_load((P.off4(4 * (t // (K // E)) + rr, (t % (K // E)) * E + 4 * h), 8) for t in range(64))
+        assert len(load) == BANKS and max(load.values()) == 2
+
+
+def ds_read_tr16_b64(mem: dict, addrs: list[int]) -> list[list]:
+    """Emulation of ds_read_b64_tr_b16 for one 16-lane group: lane 4 r + q
+    supplies the address of 4 bf16 values, forming row r, columns 4 q .. 4 q
+    + 3 of a 4 x 16 block; lane i receives column i (rows 0..3)."""
+    assert len(addrs) == 16
+    M = [[None] * 16 for _ in range(4)]
+    for lane, a in enumerate(addrs):
+        r, q = divmod(lane, 4)
+        for j in range(4):
+            M[r][4 * q + j] = mem[a + 2 * j]
+    return [[M[r][i] for r in range(4)] for i in range(16)]
+
+
+def frag_tr(P: Plane, mem: dict, row0: int, col0: int, g: int) -> list[list]:
+    """mfma_common.h Plane::frag_tr for lane group g: the 8 values of each
+    lane lr (two transposed reads, rows r and r + 16, shuffled a ++ b)."""
+    p0 = [P.off4(row0 + 4 * g + (lr >> 2), col0 + 4 * (lr & 3)) for lr in range(16)]
+    p1 = [P.off4(row0 + 4 * g + (lr >> 2) + 16, col0 + 4 * (lr & 3)) for lr in range(16)]
+    a, b = ds_read_tr16_b64(mem, p0), ds_read_tr16_b64(mem, p1)
+    return [a[lr] + b[lr] for lr in range(16)]
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", PLANE_KS)
+def test_frag_tr_hands_each_lane_its_transposed_fragment(split, K):
+    # Lane (g, lr) gets elements (row0 + 4 g + e % 4 + 16 (e / 4), col0 + lr),
+    # e = 0..7: the contraction runs over the plane's rows in the permuted
+    # order, the lane's column is its lr.
+    P = Plane(split, K)
+    rows = 64
+    mem = {P.elem(r, k) + o: (r, k) for r in range(rows) for k in range(K) for o in (0,)}
+    for row0, col0, g in itertools.product(range(0, rows, 32), range(0, K, 16), range(4)):
+        got = frag_tr(P, mem, row0, col0, g)
+        for lr in range(16):
+            assert got[lr] == [(row0 + 4 * g + e % 4 + 16 * (e // 4), col0 + lr) for e in range(8)]
+
+
+def test_frag_tr_with_swapped_lane_roles_fails():
+    # Planted mistake: lanes addressing column blocks by lr >> 2 and rows by
+    # lr & 3 hand out a different fragment.
+    P = Plane(False, 64)
+    mem = {P.elem(r, k): (r, k) for r in range(64) for k in range(64)}
+    p0 = [P.off4(4 * 0 + (lr & 3), 4 * (lr >> 2)) for lr in range(16)]
+    got = ds_read_tr16_b64(mem, p0)
+    assert any(got[lr] != [(e, lr) for e in range(4)] for lr in range(16))
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", PLANE_KS)
+def test_frag_tr_reads_at_most_two_way(split, K):
+    # The transposed reads (16 lanes x 8 bytes) put at most two dwords on a
+    # bank: a 2-way conflict at worst, never the pile-up of an unswizzled tile.
+    P = Plane(split, K)
+    for row0, col0, g in itertools.product(range(0, 64, 32), range(0, K, 16), range(4)):
+        load = bank_load((P.off4(row0 + 4 * g + (lr >> 2), col0 + 4 * (lr & 3)), 8) for lr in range(16))
+        assert max(load.values()) <= 2
+
+
+@pytest.mark.parametrize("es, D, C", [(4, 64, 32), (4, 64, 64), (4, 128, 32), (4, 128, 64), (2, 64, 32),
+                                      (2, 64, 64), (2, 128, 32), (2, 128, 64)])
+def test_out_tile_swizzle_is_a_bijection_and_spreads(es, D, C):
+    T = OutTile(es, D, C)
+    n = C * T.row_bytes
+    # Every byte of the tile exactly once; chunk_at is at() on chunk starts.
+    assert sorted(T.at(r, b) for r in range(C) for b in range(T.row_bytes)) == list(range(n))
+    assert [T.chunk_at(q) for q in range(C * T.chunks)] == \
+           [T.at(q // T.chunks, 16 * (q % T.chunks)) for q in range(C * T.chunks)]
+    # Accumulator-layout stores (mfma_causal.hip: OT::put(Os, 16 bi + lr,
+    # 16 cb + 4 g, .)): a 16-lane group writes 4 values of 16 rows.
+    vb = 4 * es
+    for bi, cb, g in itertools.product(range(C // 16), range(D // 16), range(4)):
+        load = bank_load((T.at(16 * bi + lr, (16 * cb + 4 * g) * es), vb) for lr in range(16))
+        assert max(load.values()) == 1
+    # Row-contiguous transfers: 16 consecutive threads move 16 consecutive chunks.
+    for q0 in range(0, C * T.chunks, 16):
+        load = bank_load((T.chunk_at(q), 16) for q in range(q0, q0 + 16))
+        assert len(load) == BANKS and max(load.values()) == 1
+
+
+def test_row_only_swizzle_conflicts_on_short_rows():
+    # Planted mistake (swz(r) = r & kMask): bf16 rows of 64 values are half a
+    # span, so rows r and r + 8 of an accumulator store share banks.
+    T = OutTile(2, 64, 32, per_span=False)
+    load = bank_load((T.at(lr, 0), 8) for lr in range(16))
+    assert max(load.values()) == 2
+
+
+def test_dq_tile_single_value_stores_spread():
+    # mfma_bwd.hip T32::put1(D32s, 16 bi + 4 gq + rr, 16 w + lr, .): 4 rows x
+    # 16 single fp32 values per wave and (bi, rr): 64 dwords, each bank once.
+    T = OutTile(4, 64, 32)
+    for bi, rr, w in itertools.product(range(2), range(4), range(4)):
+        load = bank_load((T.at(16 * bi + 4 * gq + rr, 4 * (16 * w + lr)), 4) for gq in range(4) for lr in range(16))
+        assert len(load) == BANKS and max(load.values()) == 1
+
+
+# ---------------------------------------------------------------------------
+# Tile and sub-chunk ownership; buffer ranges of the unconditional flush
+
+
+def tile_rows(T: int, tile: int):
+    tiles = -(-T // tile) if T else 0
+    return [(ti, ti * tile, min(T, ti * tile + tile)) for ti in range(tiles)]
+
+
+@pytest.mark.parametrize("T, tile", [(1, 32), (31, 32), (32, 32), (33, 32), (1000, 64), (4096, 512),
+                                     (65536, 512), (70001, 16384), (0, 64)])
+def test_tiles_cover_every_token_once(T, tile):
+    # grid (tiles, N): workgroup (ti, n) owns rows [ti tile, min(T, ti tile + tile)).
+    seen = Counter()
+    for _, b, e in tile_rows(T, tile):
+        assert e > b
+        seen.update(range(b, e))
+    assert sorted(seen) == list(range(T)) and all(v == 1 for v in seen.values())
+
+
+@pytest.mark.parametrize("N, tiles", [(1, 1), (3, 5), (8, 128), (128, 7), (5, 1024)])
+def test_direct_kernels_map_waves_to_tiles_once(N, tiles):
+    # mfma_direct.hip direct_tile(): id = 4 blockIdx.x + w -> (n, ti); grid
+    # (total + 3) / 4 blocks of 4 waves; ids past the total exit.
+    total = N * tiles
+    seen = Counter()
+    for bx in range((total + 3) // 4):
+        for w in range(4):
+            i = 4 * bx + w
+            if i >= total:
+                continue
+            n, ti = divmod(i, tiles)
+            assert 0 <= n < N and 0 <= ti < tiles
+            seen[(n, ti)] += 1
+    assert len(seen) == total and set(seen.values()) == {1}
+
+
+@pytest.mark.parametrize("tiles, groups", [(1, 1), (7, 4), (128, 8), (1000, 16), (3, 8)])
+def test_scan_groups_partition_the_tiles(tiles, groups):
+    # valu_kernels.hip tile_scan_kernel: group gi scans tiles
+    # [gi per, min(tiles, gi per + per)), per = ceil(tiles / groups).
+    per = -(-tiles // groups)
+    seen = Counter()
+    for gi in range(groups):
+        seen.update(range(gi * per, min(tiles, gi * per + per)))
+    assert sorted(seen) == list(range(tiles)) and set(seen.values()) == {1}
+
+
+def buffer_store_kept(offset: int, nbytes: int, num_records: int) -> bool:
+    """A raw buffer store of nbytes at a 32-bit offset: written iff it lies in
+    [0, num_records).  The offset is an unsigned 32-bit value, so a negative
+    int offset is 2^32 + offset, far past any range below 2^31."""
+    u = offset & 0xFFFFFFFF
+    if u >= num_records:
+        return False
+    assert u + nbytes <= num_records, "a store straddling the range end"
+    return True
+
+
+def flushed_rows(rows: int, C: int, es: int, D: int):
+    """Rows of a tile written by the output pass: the previous sub-chunk's
+    tile is flushed at the top of every sub-chunk r0 = 0, C, ... (at r0 = 0,
+    rows -C..-1) and once after the loop (mfma_causal.hip sub_chunk and its
+    caller; hashed_kernels.h likewise).  OutTile::write stores chunk q of the
+    [C][D] tile at r0 row_bytes + 16 q; the buffer covers the tile's rows."""
+    T = OutTile(es, D, C)
+    rng = rows * T.row_bytes
+    assert rng < 2 ** 31  # race_api.hip tile_fits_buffer
+    written = Counter()
+
+    def flush(r0):
+        for q in range(C * T.chunks):  # every chunk of the tile, over the threads
+            off = r0 * T.row_bytes + 16 * q
+            if buffer_store_kept(off, 16, rng):
+                written[off // T.row_bytes] += 1
+
+    r0 = 0
+    while r0 < rows:
+        flush(r0 - C)
+        r0 += C
+    if r0 > 0:
+        flush(r0 - C)
+    return written, T.chunks
+
+
+@pytest.mark.parametrize("es, D, C", [(4, 64, 32), (2, 64, 32), (4, 128, 64), (2, 128, 32)])
+@pytest.mark.parametrize("rows", [1, 15, 31, 32, 33, 63, 64, 100, 512])
+def test_unconditional_flush_writes_each_row_once(es, D, C, rows):
+    written, chunks = flushed_rows(rows, C, es, D)
+    # Every row of the tile gets all its chunks once; nothing outside it.
+    assert sorted(written) == list(range(rows))
+    assert set(written.values()) == {chunks}
+
+
+def test_flush_offsets_before_the_tile_are_dropped_for_every_range():
+    # The first flush (r0 = -C) has offsets -C row_bytes .. -16: as unsigned
+    # 32-bit values they are >= 2^32 - C row_bytes, beyond any range < 2^31.
+    for es, D, C in [(4, 64, 32), (4, 128, 64), (2, 128, 32)]:
+        row_bytes = D * es
+        worst = (-C * row_bytes) & 0xFFFFFFFF
+        assert worst >= 2 ** 31
+        assert not buffer_store_kept(-16, 16, 2 ** 31 - 16)
+
+
+def test_dq_flush_in_the_backward_writes_each_row_once():
+    # mfma_bwd.hip flush(r0): fp32 dq32 chunks (OutTile<float, 64, 32>) and,
+    # for bf16 tokens, 8-byte bf16 dQ chunks at r0 * 64 * 2 + 8 qi; called
+    # with r0 - kBC at the top of every sub-chunk and once after the loop.
+    kBC, kBS = 32, 64
+    for rows in (1, 16, 31, 32, 33, 63, 64, 65, 1000):
+        w32, w16 = Counter(), Counter()
+        rng32, rng16 = rows * kBS * 4, rows * kBS * 2
+
+        def flush(r0):
+            for qi in range(kBC * kBS // 4):
+                if buffer_store_kept(r0 * kBS * 4 + 16 * qi, 16, rng32):
+                    w32[(r0 * kBS * 4 + 16 * qi) // (kBS * 4)] += 1
+                if buffer_store_kept(r0 * kBS * 2 + 8 * qi, 8, rng16):
+                    w16[(r0 * kBS * 2 + 8 * qi) // (kBS * 2)] += 1
+
+        r0 = 0
+        while r0 < rows:
+            flush(r0 - kBC)
+            r0 += kBC
+        flush(r0 - kBC)
+        assert sorted(w32) == list(range(rows)) and set(w32.values()) == {kBS // 4}
+        assert sorted(w16) == list(range(rows)) and set(w16.values()) == {kBS // 4}
+
+
+def test_missing_final_flush_loses_the_last_sub_chunk():
+    # Planted mistake: without the flush after the loop the last sub-chunk's
+    # rows are never written.
+    rows, C, es, D = 100, 32, 4, 64
+    T = OutTile(es, D, C)
+    rng = rows * T.row_bytes
+    written = set()
+    for r0 in range(0, rows, C):
+        for q in range(C * T.chunks):
+            off = (r0 - C) * T.row_bytes + 16 * q
+            if buffer_store_kept(off, 16, rng):
+                written.add(off // T.row_bytes)
+    assert written != set(range(rows))
+
+
+def test_loads_past_the_tile_read_zero():
+    # KVStage::load of the sub-chunk after the last (r0 = rows rounded up):
+    # every 16-byte load at or past the range reads zero, none straddles.
+    for es, S in [(4, 64), (2, 64), (4, 256)]:
+        for rows in (1, 31, 32, 33, 500):
+            rng = rows * S * es
+            C = 32
+            r_next = -(-rows // C) * C
+            for row in range(r_next, r_next + C):
+                for c in range(0, S * es, 16):
+                    off = row * S * es + c
+                    assert off >= rng  # past the range: the load returns zeros
+
+
+# ---------------------------------------------------------------------------
+# hash_stage.h: projection ownership, plane staging layouts, corner table
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_projection_contracts_every_row_element_once(D):
+    kSeg = D // 4
+    # fp32: v_mfma_f32_16x16x4_f32, lane group g supplies element kSeg g + s
+    # at step s (Projector::project, s4 + j with j the step within 4).
+    fp32 = Counter(kSeg * g + s4 + j for g in range(4) for s4 in range(0, kSeg, 4) for j in range(4))
+    assert sorted(fp32) == list(range(D)) and set(fp32.values()) == {1}
+    # bf16: v_mfma_f32_16x16x32_bf16, step kk, lane group g: elements
+    # kSeg g + 8 kk .. + 7 (one 16-byte load of the row each).
+    bf16 = Counter(kSeg * g + 8 * kk + e for g in range(4) for kk in range(kSeg // 8) for e in range(8))
+    assert sorted(bf16) == list(range(D)) and set(bf16.values()) == {1}
+    # Each lane reads a 16-byte-aligned run of its row (Projector::load).
+    for es in (4, 2):
+        assert (kSeg * es) % 16 == 0
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_plane_stagings_spread_a_column_of_rows(D):
+    # PlanesLds: fp32 rows of D + 4 floats; get4 of 16 rows (lr) at one column
+    # touches each bank once.  PlanesB3: bf16 rows of D + 8; get8 likewise.
+    for c in range(0, D, 4):
+        load = bank_load((((16 + lr) * (D + 4) + c) * 4, 16) for lr in range(16))
+        assert len(load) == BANKS and max(load.values()) == 1
+    for c in range(0, D, 8):
+        load = bank_load((((16 + lr) * (D + 8) + c) * 2, 16) for lr in range(16))
+        assert len(load) == BANKS and max(load.values()) == 1
+    # Planted mistake: unpadded fp32 rows put all 16 rows on the same banks.
+    load = bank_load(((lr * D) * 4, 16) for lr in range(16))
+    assert max(load.values()) > 1
+
+
+def sigma(x):
+    return 1.0 / (1.0 + math.exp(-x))
+
+
+def stored_plane_value(z: float) -> float:
+    """hs_write_sigmas: copysign(sigma(-|z|), z)."""
+    return math.copysign(sigma(-abs(z)), z)
+
+
+def sigma_pair(s: float):
+    """hs_sigma_pair: (sigma(z), sigma(-z)) from the stored value."""
+    b = abs(s)
+    a = 1.0 - b
+    return (b, a) if math.copysign(1.0, s) < 0 else (a, b)
+
+
+def corner_quads(u: list[float]) -> list[float]:
+    """CornerTable<KP>::decode + quad(m) for m = 0 .. 2^(KP-2) - 1."""
+    KP = len(u)
+    sp = [sigma_pair(x) for x in u]
+    s1, s2 = sp[KP - 2], sp[KP - 1]
+    low = [s1[1] * s2[1], s1[1] * s2[0], s1[0] * s2[1], s1[0] * s2[0]]
+    out = []
+    for m in range(1 << (KP - 2)):
+        base = 1.0
+        for p in range(KP - 2):
+            base *= sp[p][0] if (m >> (KP - 3 - p)) & 1 else sp[p][1]
+        out += [base * x for x in low]
+    return out
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
+def test_corner_table_follows_the_reference_corner_order(K):
+    # probs[r] = softmax_r(sum_k s_rk u_k) with s_r the r-th element of
+    # itertools.product([-1, 1], repeat=K) (src/race_baseline.py:30-32,41-44);
+    # the kernels store z_k = 2 u_k and multiply sigmas.
+    rng = np.random.default_rng(K)
+    for _ in range(20):
+        u = rng.normal(size=K) * 0.7
+        z = 2 * u
+        got = corner_quads([stored_plane_value(x) for x in z])
+        signs = np.array(list(itertools.product([-1, 1], repeat=K)), float)
+        logits = signs @ u
+        want = np.exp(logits - logits.max())
+        want /= want.sum()
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-15)
+
+
+def test_corner_table_with_reversed_bits_fails():
+    # Planted mistake: plane 0 as the least significant bit of r.
+    u = [0.3, -1.1, 0.5]
+    z = [2 * x for x in u]
+    got = corner_quads([stored_plane_value(x) for x in z][::-1])
+    signs = np.array(list(itertools.product([-1, 1], repeat=3)), float)
+    want = np.exp(signs @ np.array(u))
+    want /= want.sum()
+    assert not np.allclose(got, want)
+
+
+def test_sigma_pair_reads_the_sign_of_zero():
+    # z = -0.0 stores -sigma(0) = -0.5; the pair is then (0.5, 0.5) either way,
+    # and for z != 0 the order follows the sign.
+    assert sigma_pair(stored_plane_value(-0.0)) == (0.5, 0.5)
+    s = stored_plane_value(1.5)
+    assert sigma_pair(s) == pytest.approx((sigma(1.5), sigma(-1.5)))
+    s = stored_plane_value(-1.5)
+    assert sigma_pair(s) == pytest.approx((sigma(-1.5), sigma(1.5)))
+
+
+@pytest.mark.parametrize("NPB", [1, 2, 4])
+def test_sigma_writes_cover_each_token_plane_once(NPB):
+    # hs_write_sigmas: lane (g, lr) holds D[4 g + r][lr] = plane 16 pb + 4 g + r
+    # of token lr and writes U[t pitch + 16 pb + 4 g + r].
+    pitch = 16 * NPB + 1
+    seen = Counter()
+    for g, lr, pb, r in itertools.product(range(4), range(16), range(NPB), range(4)):
+        seen[lr * pitch + 16 * pb + 4 * g + r] += 1
+    assert len(seen) == 16 * 16 * NPB and set(seen.values()) == {1}
+    assert max(seen) < 16 * pitch
