@@ -30,6 +30,15 @@
 //   4. causal_bwd_dkv_kernel: per tile, walk the sub-chunks backward: dK, dV
 // Every sum has a fixed order, so the gradients are bitwise reproducible for
 // a given tile length.
+//
+// Column groups.  Every term above is linear in the value columns: a group
+// of columns c0 .. c0 + dg - 1 of V and g (the forward prefix B0 restricted to
+// them, its own Z) yields dV of its columns exactly, and a partial dQ (hence a
+// partial alpha and Y) and a partial dK whose sum over the groups is the
+// whole.  Where the state of all d columns does not fit one workgroup's LDS,
+// race_api.hip runs the walks once per group, in group order, adding each
+// group's dQ and dK to an fp32 running sum (BwdCols); dq32 then holds the
+// current group's partial dQ, which is what its backward walk needs.
 #include "race_internal.h"
 
 namespace race {
@@ -39,6 +48,11 @@ template <typename TIn>
 __device__ __forceinline__ float ldf(const TIn* __restrict__ p, int64_t i) {
     return to_f32(p[i]);
 }
+
+// Buckets per stream the walks take (the library's limit): the forward walk
+// keeps Y in kBwdMaxS / kThreads registers per thread.
+constexpr int kBwdMaxS = 256;
+static_assert(kBwdMaxS % kThreads == 0, "whole register rows of Y");
 
 int64_t dq_lds_floats(int S, int d, int C) {
     return int64_t(S) * d + S + 3 * int64_t(C) * S + 2 * int64_t(C) * d + int64_t(C) * C;
@@ -56,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dq_kernel(
     const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
     float* __restrict__ apre, const float* __restrict__ fwd_records,
     float* __restrict__ bwd_records, int64_t T, int S, int d, int C, int tile, int64_t tiles,
-    int64_t rec) {
+    int64_t rec, BwdCols cols) {
     extern __shared__ float smem[];
     const int Sd = S * d;
     float* B0 = smem;          // [S][d]
@@ -70,12 +84,20 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dq_kernel(
     const int tid = threadIdx.x;
     const int64_t n = blockIdx.y, ti = blockIdx.x;
 
-    const float* fr = fwd_records + (n * tiles + ti) * rec;
-    for (int e = tid; e < Sd + S; e += kThreads) B0[e] = fr[e];  // B0, then A0
+    // B0: the group's columns of the forward prefix record (rows of
+    // cols.fwd_d values), then A0.
+    const float* fr = fwd_records + (n * tiles + ti) * cols.fwd_rec;
+    for (int e = tid; e < Sd; e += kThreads) {
+        const int s = e / d, c = e - s * d;
+        B0[e] = fr[int64_t(s) * cols.fwd_d + cols.c0 + c];
+    }
+    for (int s = tid; s < S; s += kThreads) A0[s] = fr[int64_t(S) * cols.fwd_d + s];
     float z[MZ];
 #pragma unroll
     for (int m = 0; m < MZ; ++m) z[m] = 0.f;
-    float y = 0.f;
+    float y[kBwdMaxS / kThreads];  // Y[tid + kThreads m]
+#pragma unroll
+    for (int m = 0; m < kBwdMaxS / kThreads; ++m) y[m] = 0.f;
 
     const int64_t t_begin = ti * tile;
     const int64_t t_end = min(T, t_begin + tile);
@@ -83,15 +105,16 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dq_kernel(
     for (int64_t t0 = t_begin; t0 < t_end; t0 += C) {
         const int cnt = int(min<int64_t>(C, t_end - t0));
         const int sub = int((t0 - t_begin) / C);
-        const int64_t rs = (n * T + t0) * S, rd = (n * T + t0) * d;
+        const int64_t rs = (n * T + t0) * S, rd = (n * T + t0) * cols.ld;
         __syncthreads();
         for (int e = tid; e < cnt * S; e += kThreads) {
             Wq[e] = ldf(q, rs + e);
             Ks[e] = ldf(k, rs + e);
         }
         for (int e = tid; e < cnt * d; e += kThreads) {
-            Vs[e] = ldf(v, rd + e);
-            Gs[e] = ldf(g, rd + e);
+            const int i = e / d, c = e - i * d;
+            Vs[e] = ldf(v, rd + int64_t(i) * cols.ld + c);
+            Gs[e] = ldf(g, rd + int64_t(i) * cols.ld + c);
         }
         __syncthreads();
         // Running mass (saved per sub-chunk for the backward walk), r and W.
@@ -122,7 +145,10 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dq_kernel(
             for (int j = 0; j <= i; ++j) u = fmaf(M[i * C + j], Ks[j * S + s], u);
             const float dqv = Rs[e] * u;
             dq32[rs + e] = dqv;
-            if (dQ) store_val(dQ + rs + e, dqv);
+            float tot = dqv;  // dQ over the groups so far
+            if (cols.acc_q_in) tot = cols.acc_q_in[rs + e] + dqv;
+            if (cols.acc_q_out) cols.acc_q_out[rs + e] = tot;
+            if (dQ) store_val(dQ + rs + e, tot);
             Rs[e] = -Wq[e] * dqv;
         }
         __syncthreads();
@@ -141,8 +167,12 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dq_kernel(
                 B0[e] += ba;
             }
         }
-        if (tid < S)
-            for (int i = 0; i < cnt; ++i) y += Rs[i * S + tid];
+#pragma unroll
+        for (int m = 0; m < kBwdMaxS / kThreads; ++m) {
+            const int sy = tid + m * kThreads;
+            if (sy < S)
+                for (int i = 0; i < cnt; ++i) y[m] += Rs[i * S + sy];
+        }
     }
     float* br = bwd_records + (n * tiles + ti) * rec;
 #pragma unroll
@@ -150,7 +180,9 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dq_kernel(
         const int e = tid + m * kThreads;
         if (e < Sd) br[e] = z[m];
     }
-    if (tid < S) br[Sd + tid] = y;
+#pragma unroll
+    for (int m = 0; m < kBwdMaxS / kThreads; ++m)
+        if (tid + m * kThreads < S) br[Sd + tid + m * kThreads] = y[m];
 }
 
 // ---------------------------------------------------------------------------
@@ -160,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dkv_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, const float* __restrict__ dq32, const float* __restrict__ apre,
     const float* __restrict__ suffix_records, TIn* __restrict__ dK, TIn* __restrict__ dV, int64_t T,
-    int S, int d, int C, int tile, int64_t tiles, int64_t rec) {
+    int S, int d, int C, int tile, int64_t tiles, int64_t rec, BwdCols cols) {
     extern __shared__ float smem[];
     const int Sd = S * d;
     float* Z1 = smem;          // [S][d]
@@ -185,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dkv_kernel(
     for (int sub = nsub - 1; sub >= 0; --sub) {
         const int64_t t0 = t_begin + int64_t(sub) * C;
         const int cnt = int(min<int64_t>(C, t_end - t0));
-        const int64_t rs = (n * T + t0) * S, rd = (n * T + t0) * d;
+        const int64_t rs = (n * T + t0) * S, rd = (n * T + t0) * cols.ld;
         __syncthreads();
         for (int e = tid; e < cnt * S; e += kThreads) {
             Ws[e] = ldf(q, rs + e);
@@ -193,8 +225,9 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dkv_kernel(
             Al[e] = dq32[rs + e];
         }
         for (int e = tid; e < cnt * d; e += kThreads) {
-            Vs[e] = ldf(v, rd + e);
-            Gs[e] = ldf(g, rd + e);
+            const int i = e / d, c = e - i * d;
+            Vs[e] = ldf(v, rd + int64_t(i) * cols.ld + c);
+            Gs[e] = ldf(g, rd + int64_t(i) * cols.ld + c);
         }
         __syncthreads();
         // W exactly as the forward walk computed it, and alpha = -W dQ.
@@ -233,12 +266,16 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dkv_kernel(
         }
         __syncthreads();
         // dK = V Z1^T + Y1 + M^T W + reverse running alpha.
-        for (int e = tid; dK && e < cnt * S; e += kThreads) {
+        const bool want_dk = dK || cols.acc_k_out;
+        for (int e = tid; want_dk && e < cnt * S; e += kThreads) {
             const int j = e / S, s = e - j * S;
             float acc = 0.f;
             for (int c = 0; c < d; ++c) acc = fmaf(Vs[j * d + c], Z1[s * d + c], acc);
             for (int i = j; i < cnt; ++i) acc = fmaf(M[i * C + j], Ws[i * S + s], acc);
-            store_val(dK + rs + e, acc + (Y1[s] + Al[e]));
+            float tot = acc + (Y1[s] + Al[e]);  // dK over the groups so far
+            if (cols.acc_k_in) tot = cols.acc_k_in[rs + e] + tot;
+            if (cols.acc_k_out) cols.acc_k_out[rs + e] = tot;
+            if (dK) store_val(dK + rs + e, tot);
         }
         // dV = K Z1 + P^T G.
         for (int e = tid; dV && e < cnt * d; e += kThreads) {
@@ -246,7 +283,7 @@ __global__ __launch_bounds__(kThreads) void causal_bwd_dkv_kernel(
             float acc = 0.f;
             for (int s = 0; s < S; ++s) acc = fmaf(Ks[j * S + s], Z1[s * d + c], acc);
             for (int i = j; i < cnt; ++i) acc = fmaf(P[i * C + j], Gs[i * d + c], acc);
-            store_val(dV + rd + e, acc);
+            store_val(dV + rd + int64_t(j) * cols.ld + c, acc);
         }
         __syncthreads();
         // Suffix state before this sub-chunk.
@@ -270,6 +307,7 @@ int z_regs(int S, int d) {
 }  // namespace
 
 int causal_bwd_chunk(int S, int d, int lds_limit_bytes) {
+    if (S > kBwdMaxS) return 0;
     for (int C : {32, 16}) {
         const int64_t need =
             (dq_lds_floats(S, d, C) > dkv_lds_floats(S, d, C) ? dq_lds_floats(S, d, C)
@@ -282,14 +320,15 @@ int causal_bwd_chunk(int S, int d, int lds_limit_bytes) {
 
 hipError_t launch_causal_bwd_dq(const void* q, const void* k, const void* v, const void* g,
                                 void* dQ, float* dq32, float* apre, const float* fwd_records,
-                                float* bwd_records, const Problem& p, int C, hipStream_t stream) {
+                                float* bwd_records, const Problem& p, int C, const BwdCols& cols,
+                                hipStream_t stream) {
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     const size_t lds = size_t(dq_lds_floats(p.S, p.d, C)) * sizeof(float);
 #define RACE_DQ(TIN, MZ)                                                                          \
     causal_bwd_dq_kernel<TIN, MZ><<<grid, kThreads, lds, stream>>>(                               \
         static_cast<const TIN*>(q), static_cast<const TIN*>(k), static_cast<const TIN*>(v),       \
         static_cast<const TIN*>(g), static_cast<TIN*>(dQ), dq32, apre, fwd_records, bwd_records, \
-        p.T, p.S, p.d, C, p.tile, p.tiles, p.rec)
+        p.T, p.S, p.d, C, p.tile, p.tiles, p.rec, cols)
 #define RACE_DQ_MZ(TIN)                         \
     switch (z_regs(p.S, p.d)) {                 \
         case 1: RACE_DQ(TIN, 1); break;         \
@@ -315,7 +354,7 @@ hipError_t launch_causal_bwd_dq(const void* q, const void* k, const void* v, con
 hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, const void* g,
                                  const float* dq32, const float* apre,
                                  const float* suffix_records, void* dK, void* dV, const Problem& p,
-                                 int C, hipStream_t stream) {
+                                 int C, const BwdCols& cols, hipStream_t stream) {
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     const size_t lds = size_t(dkv_lds_floats(p.S, p.d, C)) * sizeof(float);
     if (p.dtype == RACE_BF16) {
@@ -323,13 +362,13 @@ hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, co
             static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
             static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), dq32, apre,
             suffix_records, static_cast<bf16_t*>(dK), static_cast<bf16_t*>(dV), p.T, p.S, p.d, C,
-            p.tile, p.tiles, p.rec);
+            p.tile, p.tiles, p.rec, cols);
     } else {
         causal_bwd_dkv_kernel<float><<<grid, kThreads, lds, stream>>>(
             static_cast<const float*>(q), static_cast<const float*>(k),
             static_cast<const float*>(v), static_cast<const float*>(g), dq32, apre,
             suffix_records, static_cast<float*>(dK), static_cast<float*>(dV), p.T, p.S, p.d, C,
-            p.tile, p.tiles, p.rec);
+            p.tile, p.tiles, p.rec, cols);
     }
     return hipGetLastError();
 }

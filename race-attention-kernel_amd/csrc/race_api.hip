@@ -162,18 +162,42 @@ BwdLayout bwd_layout(const Problem& p) {
 // of dQ and, unless the caller hands in the forward's records, the forward
 // prefix records (last, so the two layouts share every other offset).
 struct CausalBwdLayout {
-    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0;
-    int64_t total() const { return bwd + apre + dq32 + fwd; }
+    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0, acc = 0;
+    int64_t total() const { return bwd + apre + dq32 + fwd + acc; }
 };
 
-CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given) {
+// Column groups of the causal backward: 1 where the state of every value
+// column fits one workgroup's LDS, else the fewest groups of equal width that
+// fit (each walk then takes one group; causal_bwd.hip), 0 where none does.
+// *C gets the groups' sub-chunk length.
+int causal_bwd_groups(int S, int d, int lds_limit, int* C) {
+    for (int G = 1; G <= d; ++G) {
+        if (d % G != 0) continue;
+        const int c = causal_bwd_chunk(S, d / G, lds_limit);
+        if (c != 0) {
+            *C = c;
+            return G;
+        }
+    }
+    *C = 0;
+    return 0;
+}
+
+// Workspace of the causal backward with `groups` column groups: the suffix
+// records (of one group's width; the groups take turns), the running mass,
+// dq32, the forward prefix records unless given, and with several groups of
+// bf16 tokens the fp32 running sums of dQ and dK.
+CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, int groups) {
     CausalBwdLayout l;
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
-    l.bwd = p.N * p.tiles * p.rec;
+    const int64_t rec_g = groups > 1 ? record_floats(p.S, p.d / groups) : p.rec;
+    l.bwd = p.N * p.tiles * rec_g;
     l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(p.S));
     l.dq32 = round64(p.N * p.T * int64_t(p.S));
+    l.acc = (groups > 1 && p.dtype == RACE_BF16) ? 2 * round64(p.N * p.T * int64_t(p.S)) : 0;
     return l;
 }
+
 
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -204,6 +228,14 @@ hipError_t max_lds(int* bytes) {
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;
     return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+}
+
+// The column groups of a backward problem (0 where none fits: the backward
+// refuses the shape, its workspace query sizes one group), planned for
+// gfx950's LDS per workgroup so that the workspace query needs no device.
+hipError_t causal_bwd_plan(const Problem& p, int* groups, int* C) {
+    *groups = causal_bwd_groups(p.S, p.d, kGfx950LdsBytes, C);
+    return hipSuccess;
 }
 
 // The non-causal reduction and map: the 16-byte-vector kernels when both
@@ -671,21 +703,22 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         return RACE_ERROR_INVALID_VALUE;
     if ((dQ && !aligned16(dQ)) || (dK && !aligned16(dK)) || (dV && !aligned16(dV)))
         return RACE_ERROR_INVALID_VALUE;
-    const CausalBwdLayout l = causal_bwd_layout(p, fwd_records != nullptr);
+    int groups = 0, C = 0;
+    RACE_TRY(causal_bwd_plan(p, &groups, &C));
+    const CausalBwdLayout l = causal_bwd_layout(p, fwd_records != nullptr, groups > 1 ? groups : 1);
     if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
         return RACE_ERROR_INVALID_VALUE;
-    int lds_limit = 0;
-    RACE_TRY(max_lds(&lds_limit));
-    const int C = causal_bwd_chunk(p.S, p.d, lds_limit);
-    if (C == 0 || (use_mfma && C != 32)) return RACE_ERROR_INVALID_VALUE;
+    if (groups == 0 || (use_mfma && (groups != 1 || C != 32))) return RACE_ERROR_INVALID_VALUE;
     float* bwd_rec = static_cast<float*>(workspace);
     float* apre = bwd_rec + l.bwd;
     float* dq32 = apre + l.apre;
     float* fwd_ws = dq32 + l.dq32;
-    // B3 reads dQ back in fp32.  An fp32 dQ is that copy: B1 writes it once,
-    // into the caller's buffer, and B3 reads it from there.
+    float* acc = fwd_ws + l.fwd;
+    // B3 reads dQ back in fp32.  With one column group an fp32 dQ is that
+    // copy: B1 writes it once, into the caller's buffer, and B3 reads it from
+    // there.  With several, dq32 holds the current group's part.
     void* dq_out = dQ;
-    if (dQ && p.dtype == RACE_F32) {
+    if (dQ && p.dtype == RACE_F32 && groups == 1) {
         dq32 = static_cast<float*>(dQ);
         dq_out = nullptr;
     }
@@ -704,23 +737,67 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         RACE_TRY(marks->mark(stream));
         fwd_rec = fwd_ws;
     }
-    if (use_mfma)
+    if (use_mfma) {
         RACE_TRY(launch_causal_bwd_dq_mfma(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec,
                                            bwd_rec, p, stream));
-    else
-        RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec, bwd_rec,
-                                      p, C, stream));
-    RACE_TRY(marks->mark(stream));
-    if (!dK && !dV) return RACE_SUCCESS;
-    RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
-    RACE_TRY(marks->mark(stream));
-    if (use_mfma)
+        RACE_TRY(marks->mark(stream));
+        if (!dK && !dV) return RACE_SUCCESS;
+        RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
+        RACE_TRY(marks->mark(stream));
         RACE_TRY(launch_causal_bwd_dkv_mfma(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p,
                                             stream));
-    else
+        return marks->mark(stream);
+    }
+    if (groups == 1) {
+        const BwdCols cols = all_columns(p);
+        RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec, bwd_rec,
+                                      p, C, cols, stream));
+        RACE_TRY(marks->mark(stream));
+        if (!dK && !dV) return RACE_SUCCESS;
+        RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
+        RACE_TRY(marks->mark(stream));
         RACE_TRY(launch_causal_bwd_dkv(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p, C,
-                                       stream));
-    return marks->mark(stream);
+                                       cols, stream));
+        return marks->mark(stream);
+    }
+    // Column groups, in order: each adds its dQ and dK to the fp32 running
+    // sums (the fp32 outputs themselves, or workspace for bf16 outputs, whose
+    // last group then writes the caller's buffers).
+    Problem pg = p;
+    pg.d = p.d / groups;
+    pg.rec = record_floats(p.S, pg.d);
+    const bool f32 = p.dtype == RACE_F32;
+    const int64_t es = f32 ? 4 : 2;
+    float* acc_q = f32 ? static_cast<float*>(dQ) : (dQ ? acc : nullptr);
+    float* acc_k = f32 ? static_cast<float*>(dK) : (dK ? acc + round64(p.N * p.T * int64_t(p.S)) : nullptr);
+    for (int gi = 0; gi < groups; ++gi) {
+        const bool first = gi == 0, last = gi == groups - 1;
+        BwdCols cols;
+        cols.ld = p.d;
+        cols.c0 = gi * pg.d;
+        cols.fwd_d = p.d;
+        cols.fwd_rec = p.rec;
+        cols.acc_q_in = first ? nullptr : acc_q;
+        cols.acc_q_out = (!f32 && last) ? nullptr : acc_q;
+        cols.acc_k_in = first ? nullptr : acc_k;
+        cols.acc_k_out = (!f32 && last) ? nullptr : acc_k;
+        void* dq_t = (!f32 && last) ? dQ : nullptr;
+        void* dk_t = (!f32 && last) ? dK : nullptr;
+        const int64_t off = int64_t(cols.c0) * es;
+        const void* vg = static_cast<const char*>(V) + off;
+        const void* gg = static_cast<const char*>(dOut) + off;
+        void* dvg = dV ? static_cast<void*>(static_cast<char*>(dV) + off) : nullptr;
+        RACE_TRY(launch_causal_bwd_dq(probsQ, probsK, vg, gg, dq_t, dq32, apre, fwd_rec, bwd_rec, pg,
+                                      C, cols, stream));
+        RACE_TRY(marks->mark(stream));
+        if (!dK && !dV) continue;
+        RACE_TRY(launch_tile_scan(bwd_rec, nullptr, pg, stream, /*reverse=*/true));
+        RACE_TRY(marks->mark(stream));
+        RACE_TRY(launch_causal_bwd_dkv(probsQ, probsK, vg, gg, dq32, apre, bwd_rec, dk_t, dvg, pg, C,
+                                       cols, stream));
+        RACE_TRY(marks->mark(stream));
+    }
+    return RACE_SUCCESS;
 }
 
 
@@ -738,7 +815,9 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
     race_options topts = {opts ? opts->tile_tokens : 0, RACE_KERNEL_VALU};
     const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
-    *bytes = size_t(causal_bwd_layout(p, false).total()) * sizeof(float);
+    int groups = 0, C = 0;
+    RACE_TRY(causal_bwd_plan(p, &groups, &C));
+    *bytes = size_t(causal_bwd_layout(p, false, groups > 1 ? groups : 1).total()) * sizeof(float);
     return RACE_SUCCESS;
 }
 
@@ -750,7 +829,9 @@ race_status race_causal_bwd_from_records_workspace_bytes(const race_shape* shape
     race_options topts = {opts->tile_tokens, RACE_KERNEL_VALU};
     const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
-    *bytes = size_t(causal_bwd_layout(p, true).total()) * sizeof(float);
+    int groups = 0, C = 0;
+    RACE_TRY(causal_bwd_plan(p, &groups, &C));
+    *bytes = size_t(causal_bwd_layout(p, true, groups > 1 ? groups : 1).total()) * sizeof(float);
     return RACE_SUCCESS;
 }
 

@@ -37,6 +37,9 @@ __device__ __forceinline__ void store_val(bf16_t* p, float x) { *p = f32_to_bf16
 // Floats in one tile record: B [S][d] then A [S], padded to 64 floats so every
 // record starts 256-byte aligned.
 inline int64_t record_floats(int64_t S, int64_t d) { return ((S * d + S + 63) / 64) * 64; }
+
+// LDS per workgroup on gfx950 (MI355X), the one target of this library.
+constexpr int kGfx950LdsBytes = 160 * 1024;
 inline int64_t state_floats(int64_t S, int64_t d) { return S * d + S; }
 
 // Problem description handed from the API layer to the launchers (all sizes
@@ -157,18 +160,44 @@ size_t map4_lds_bytes(int Wa);
 // Sub-chunk length (32 or 16) of the causal backward kernels for (S, d) under
 // `lds_limit_bytes` of LDS per workgroup, or 0 if the state does not fit.
 int causal_bwd_chunk(int S, int d, int lds_limit_bytes);
-// Forward walk: dQ (nullable, caller dtype), dq32 [N][T][S] fp32, apre
+// One column group of the vector-ALU causal backward walks (every term is
+// linear in the value columns).  The launches then take p.d = the group's
+// width, V, dOut and dV already offset to column c0, and these:
+struct BwdCols {
+    int64_t ld = 0;        // row stride, in elements, of V, dOut and dV (the full d)
+    int c0 = 0;            // first column of the group
+    int fwd_d = 0;         // row length of B0 in the forward prefix records (the full d)
+    int64_t fwd_rec = 0;   // stride of those records (record_floats(S, full d))
+    // fp32 running sums of dQ and dK over the groups, read before this group
+    // adds to them (null for the first) and written after (null to skip).
+    const float* acc_q_in = nullptr;
+    float* acc_q_out = nullptr;
+    const float* acc_k_in = nullptr;
+    float* acc_k_out = nullptr;
+};
+// The single group: every column at once.
+inline BwdCols all_columns(const Problem& p) {
+    BwdCols c;
+    c.ld = p.d;
+    c.fwd_d = p.d;
+    c.fwd_rec = p.rec;
+    return c;
+}
+// Forward walk: dQ (nullable, caller dtype; the running sum over the groups
+// when one is kept), dq32 [N][T][S] fp32 (this group's dQ), apre
 // [N][tiles][tile / C][S] (running mass at every sub-chunk start) and the
 // per-tile suffix totals (Z [S][d], Y [S]) into bwd_records, from the
 // forward's scanned prefix records.
 hipError_t launch_causal_bwd_dq(const void* q, const void* k, const void* v, const void* g,
                                 void* dQ, float* dq32, float* apre, const float* fwd_records,
-                                float* bwd_records, const Problem& p, int C, hipStream_t stream);
-// Backward walk from the suffix state at every tile end: dK, dV (each nullable).
+                                float* bwd_records, const Problem& p, int C, const BwdCols& cols,
+                                hipStream_t stream);
+// Backward walk from the suffix state at every tile end: dK, dV (each
+// nullable; dK the running sum over the groups when one is kept).
 hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, const void* g,
                                  const float* dq32, const float* apre,
                                  const float* suffix_records, void* dK, void* dV, const Problem& p,
-                                 int C, hipStream_t stream);
+                                 int C, const BwdCols& cols, hipStream_t stream);
 
 // Matrix-core kernels of the causal backward (mfma_bwd.hip): S = d = 64,
 // 32-token sub-chunks, the same buffers as the vector-ALU kernels.  With fp32

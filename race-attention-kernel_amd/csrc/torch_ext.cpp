@@ -115,8 +115,9 @@ void check_status(race_status st, const char* what) {
 
 // The per-bucket op's three token tensors: probs [N, T, L, R] (or [N, T, S])
 // and V [N, T, d], all float32 or all bfloat16 on one device.
-race_shape validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-    ArgCheck c("race_fused_fwd");
+race_shape validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                    const char* entry = "race_fused_fwd") {
+    ArgCheck c(entry);
     c.require(q.dim() == 3 || q.dim() == 4, "probsQ", "has shape " + dims(q) + ", not [N, T, L, R] or [N, T, S]")
         .on_gpu("probsQ", q).dtype_is("probsQ", q, true)
         .on_gpu("probsK", k).matches("probsK", k, "probsQ", q)
@@ -134,7 +135,7 @@ race_shape validate(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
     sh.dtype = q.scalar_type() == at::kBFloat16 ? RACE_BF16 : RACE_F32;
     int32_t supported = 0;
     check_status(race_shape_supported(&sh, &supported, nullptr), "race_shape_supported");
-    TORCH_CHECK(supported, "race_fused_fwd: no kernel takes N=", sh.num_streams, ", T=", sh.seq_len,
+    TORCH_CHECK(supported, entry, ": no kernel takes N=", sh.num_streams, ", T=", sh.seq_len,
                 ", S=L*R=", int64_t(sh.num_tables) * sh.num_buckets, ", d=", sh.head_dim,
                 "; the library covers N <= 65535 streams, S <= 256 buckets, d <= 128 columns");
     return sh;
@@ -259,7 +260,7 @@ std::tuple<c10::optional<at::Tensor>, c10::optional<at::Tensor>, c10::optional<a
 noncausal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                    const at::Tensor& grad_out, const at::Tensor& state, bool need_q, bool need_k,
                    bool need_v, int64_t tile_tokens) {
-    const race_shape sh = validate(q, k, v);
+    const race_shape sh = validate(q, k, v, "race_noncausal_backward");
     validate_like_v("race_noncausal_backward", "dOut", grad_out, v);
     const int64_t S = int64_t(sh.num_tables) * sh.num_buckets;
     ArgCheck("race_noncausal_backward")
@@ -313,7 +314,7 @@ std::tuple<c10::optional<at::Tensor>, c10::optional<at::Tensor>, c10::optional<a
 causal_backward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                 const at::Tensor& grad_out, bool need_q, bool need_k, bool need_v,
                 int64_t tile_tokens, int64_t kernel, const c10::optional<at::Tensor>& fwd_records) {
-    const race_shape sh = validate(q, k, v);
+    const race_shape sh = validate(q, k, v, "race_causal_backward");
     validate_like_v("race_causal_backward", "dOut", grad_out, v);
     const race_options opts = make_options(tile_tokens, kernel);
     if (fwd_records) {

@@ -73,9 +73,12 @@ def check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol, dk_scale=True):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("L, R, d", [(1, 1, 1), (2, 8, 32), (4, 16, 64), (3, 5, 7), (8, 32, 64),
-                                     (4, 32, 128)])
+                                     (4, 32, 128), (8, 32, 128), (4, 64, 128), (2, 128, 120)])
 @pytest.mark.parametrize("T", [1, 63, 65, 700])
 def test_shapes(race, oracle, cuda, dtype, L, R, d, T):
+    # S = 256 with d = 128 (cfg5) or d = 120: the state of all d columns does
+    # not fit one workgroup's LDS, the walks take two column groups (of 64 or
+    # 60 columns).
     say("c-bwd-shape", dtype, L, R, d, T)
     q, k, v, g = race.make_inputs(3, T, L, R, d, seed=T + d + 1, dtype=dtype, grad_out=True)
     out, dq, dk, dv = forward_backward(race, q, k, v, g, cuda)
@@ -182,10 +185,28 @@ def test_mfma_backward_needs_its_specialization(race, cuda):
 
 
 def test_unsupported_shape_raises(race, cuda):
-    # S = 256, d = 128: the per-bucket state does not fit one workgroup's LDS.
-    q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 64, 8, 32, 128, seed=27, grad_out=True))
-    with pytest.raises(RuntimeError, match="race_causal_bwd"):
+    # S = 512: past the library's 256 buckets.
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 64, 4, 128, 8, seed=27, grad_out=True))
+    with pytest.raises(RuntimeError, match="race_causal_backward: no kernel takes"):
         race.race_causal_backward(q, k, v, g)
+
+
+def test_cfg5_shape_backward(race, oracle, cuda):
+    # cfg5 (N = 128, L = 8, R = 32, d = 128, T = 16384, bf16) through
+    # autograd: two column groups of 64; 4 streams against the oracle VJP.
+    say("c-bwd cfg5")
+    q, k, v = race.make_inputs(128, 16384, 8, 32, 128, seed=5, dtype=torch.bfloat16, device=cuda,
+                               gen_device="cuda")
+    g = torch.randn(v.shape, device=cuda, generator=torch.Generator(device=cuda).manual_seed(6)).to(v.dtype)
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    race.race_fused_fwd(qg, kg, vg, causal=True).backward(g)
+    torch.cuda.synchronize()
+    pick = [0, 41, 86, 127]
+    qn, kn, vn, gn = (to_np(x[pick]) for x in (q, k, v, g))
+    rq, rk, rv = oracle.causal_bwd(qn, kn, vn, gn, nthreads=16)
+    errs = [per_stream_rel_err(to_np(x.grad[pick]), r) for x, r in ((qg, rq), (kg, rk), (vg, rv))]
+    say("c-bwd cfg5 errors", *(f"{e:.2e}" for e in errs))
+    assert max(errs) <= tol_for(torch.bfloat16)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
