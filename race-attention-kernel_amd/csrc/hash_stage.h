@@ -39,15 +39,18 @@ __device__ __forceinline__ float2 hs_sigma_pair(float s) {
 // Projection of one 16-token block of rows against the planes: U^T
 // [planes][tokens] = planes X^T, lane (g, lr) receiving D[4 g + r][lr] =
 // plane 16 pb + 4 g + r of row lr, as every MFMA here hands it out.  The
-// contraction index runs in a fixed bijection: lane group g owns the D / 4
-// consecutive elements c = (D / 4) g .. of its plane row and its token row,
-// so each lane reads a 16-byte-aligned run of its row.
-//   fp32 rows: v_mfma_f32_16x16x4_f32 (element c = (D / 4) g + s at step s)
-//     against fp32 planes; products are exact in the fp32 accumulation.
-//   bf16 rows: v_mfma_f32_16x16x32_bf16 (elements (D / 4) g + 8 kk .. + 7 at
-//     step kk) against the planes as three bf16 terms hi + mid + lo (their
-//     sum is the fp32 plane to 2^-24); the rows are exact in bf16, so the
-//     three products give fp32 accuracy at a quarter of the fp32 MFMA cost.
+// contraction index runs in a fixed bijection in which the four lane groups
+// of one 16-byte load instruction hold one contiguous 64-byte run of each
+// row (a row is 16 lanes' worth of whole cache lines over the instructions,
+// rather than 16-byte pieces 64 bytes apart):
+//   fp32 rows: v_mfma_f32_16x16x4_f32; load i of lane group g holds elements
+//     16 i + 4 g .. + 3, element j of it is the contraction index of step
+//     4 i + j; against fp32 planes, products exact in the fp32 accumulation.
+//   bf16 rows: v_mfma_f32_16x16x32_bf16; step kk takes elements 32 kk + 8 g
+//     .. + 7 (one 16-byte load) against the planes as three bf16 terms
+//     hi + mid + lo (their sum is the fp32 plane to 2^-24); the rows are
+//     exact in bf16, so the three products give fp32 accuracy at a quarter of
+//     the fp32 MFMA cost.
 //   TIn   row element type (float or bf16_t)
 //   D     row length (the contraction), a multiple of 32
 //   NPB   16-plane blocks (L K <= 16 NPB; planes past L K are zero)
@@ -56,14 +59,16 @@ struct Projector {
     static constexpr int kSeg = D / 4;                             // values per lane
     static constexpr int kVecs = kSeg * int(sizeof(TIn)) / 16;     // 16-byte loads per lane
     static constexpr bool kF32 = std::is_same<TIn, float>::value;
+    static constexpr int kPerVec = 16 / int(sizeof(TIn));          // elements per load
     uint4 x[kVecs];
 
-    // Rows r0 .. r0 + 15 of a row buffer (rows past its range read as zero).
+    // Rows r0 .. r0 + 15 of a row buffer (rows past its range read as zero):
+    // load i of lane group g is elements 4 kPerVec i + kPerVec g .. + kPerVec - 1.
     template <int P>
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t xr, int r0, int g, int lr) {
 #pragma unroll
         for (int i = 0; i < kVecs; ++i)
-            x[i] = buf_load16<P>(xr, ((r0 + lr) * D + kSeg * g) * int(sizeof(TIn)) + 16 * i);
+            x[i] = buf_load16<P>(xr, ((r0 + lr) * D + 4 * kPerVec * i + kPerVec * g) * int(sizeof(TIn)));
     }
 
     template <typename PW>
@@ -77,7 +82,7 @@ struct Projector {
                               {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
                 for (int s4 = 0; s4 < kSeg; s4 += 4) {
-                    const f32x4 w = wp.template get4<D>(row, kSeg * g + s4);
+                    const f32x4 w = wp.template get4<D>(row, 16 * (s4 / 4) + 4 * g);
                     const f32x4 xv = __builtin_bit_cast(f32x4, x[s4 / 4]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
@@ -89,7 +94,7 @@ struct Projector {
 #pragma unroll
                 for (int kk = 0; kk < kSeg / 8; ++kk) {
                     const bf16x8 xb = __builtin_bit_cast(bf16x8, x[kk]);
-                    const int c = kSeg * g + 8 * kk;
+                    const int c = 32 * kk + 8 * g;
                     f32x4& a = (kk & 1) ? a1 : a0;
                     // Smallest terms first.
                     a = mfma16(wp.template get8<D>(2, row, c), xb, a);

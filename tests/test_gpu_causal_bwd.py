@@ -76,6 +76,9 @@ def check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol, dk_scale=True):
                                      (4, 32, 128), (8, 32, 128), (4, 64, 128), (2, 128, 120)])
 @pytest.mark.parametrize("T", [1, 63, 65, 700])
 def test_shapes(race, oracle, cuda, dtype, L, R, d, T):
+    # Through autograd, so the backward starts from the forward's saved
+    # records: for (4, 32, 128) those come from the MFMA tile sums of S = d =
+    # 128, for S = d = 64 from the register-direct ones, else the VALU sums.
     # S = 256 with d = 128 (cfg5) or d = 120: the state of all d columns does
     # not fit one workgroup's LDS, the walks take two column groups (of 64 or
     # 60 columns).

@@ -439,20 +439,39 @@ def test_loads_past_the_tile_read_zero():
 # hash_stage.h: projection ownership, plane staging layouts, corner table
 
 
+def projector_loads(D: int, es: int):
+    """hash_stage.h Projector::load: (lane group g, load i) -> first element
+    of the 16-byte run, 4 kPerVec i + kPerVec g."""
+    per = 16 // es
+    return {(g, i): 4 * per * i + per * g for g in range(4) for i in range(D * es // 4 // 16)}
+
+
 @pytest.mark.parametrize("D", [32, 64, 128])
 def test_projection_contracts_every_row_element_once(D):
     kSeg = D // 4
-    # fp32: v_mfma_f32_16x16x4_f32, lane group g supplies element kSeg g + s
-    # at step s (Projector::project, s4 + j with j the step within 4).
-    fp32 = Counter(kSeg * g + s4 + j for g in range(4) for s4 in range(0, kSeg, 4) for j in range(4))
+    # fp32: v_mfma_f32_16x16x4_f32; load i of group g holds elements
+    # 16 i + 4 g .. + 3, element j the contraction index of step 4 i + j, and
+    # the planes are read at the same column (Projector::project, get4).
+    ld = projector_loads(D, 4)
+    fp32 = Counter(ld[(g, s4 // 4)] + j for g in range(4) for s4 in range(0, kSeg, 4) for j in range(4))
     assert sorted(fp32) == list(range(D)) and set(fp32.values()) == {1}
-    # bf16: v_mfma_f32_16x16x32_bf16, step kk, lane group g: elements
-    # kSeg g + 8 kk .. + 7 (one 16-byte load of the row each).
-    bf16 = Counter(kSeg * g + 8 * kk + e for g in range(4) for kk in range(kSeg // 8) for e in range(8))
+    assert all(ld[(g, s4 // 4)] == 16 * (s4 // 4) + 4 * g for g in range(4) for s4 in range(0, kSeg, 4))
+    # bf16: v_mfma_f32_16x16x32_bf16, step kk, group g: elements 32 kk + 8 g
+    # .. + 7, one 16-byte load, the planes' terms read at c = 32 kk + 8 g.
+    ld = projector_loads(D, 2)
+    bf16 = Counter(ld[(g, kk)] + e for g in range(4) for kk in range(kSeg // 8) for e in range(8))
     assert sorted(bf16) == list(range(D)) and set(bf16.values()) == {1}
-    # Each lane reads a 16-byte-aligned run of its row (Projector::load).
-    for es in (4, 2):
-        assert (kSeg * es) % 16 == 0
+    assert all(ld[(g, kk)] == 32 * kk + 8 * g for g in range(4) for kk in range(kSeg // 8))
+
+
+@pytest.mark.parametrize("D, es", [(64, 4), (128, 4), (64, 2), (128, 2)])
+def test_projection_loads_are_contiguous_per_instruction(D, es):
+    # One load instruction: the four lane groups of a row read one 64-byte
+    # run (16 rows, one per lr), not pieces 64 bytes apart.
+    ld = projector_loads(D, es)
+    for i in range(D * es // 64):
+        starts = sorted(ld[(g, i)] * es for g in range(4))
+        assert starts == list(range(starts[0], starts[0] + 64, 16)) and starts[0] % 64 == 0
 
 
 @pytest.mark.parametrize("D", [64, 128])
