@@ -321,7 +321,8 @@ def cpu_baseline():
         pt = cpu_point(N, T, L, R, d, info["threads"])
         print(f"# cpu T={T}: {pt['ms']:.1f} ms, {pt['m_tokens_per_s']:.4f} {UNIT}, peak RSS "
               f"{pt['peak_rss_bytes'] / 2**30:.2f} GiB", file=sys.stderr, flush=True)
-        sweep.append({"T": T, "ms": pt["ms"], "m_tokens_per_s": pt["m_tokens_per_s"],
+        sweep.append({"T": T, "ms": pt["ms"], "ms_min_max": pt["ms_min_max"],
+                      "m_tokens_per_s": pt["m_tokens_per_s"],
                       "peak_rss_bytes": pt["peak_rss_bytes"],
                       "predicted_peak_bytes": pt["predicted_peak_bytes"]})
     if not sweep:

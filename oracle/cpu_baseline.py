@@ -11,8 +11,8 @@ probsQ, probsK = softmax over R of N(0,1)*4 logits, V ~ N(0,1).
 
 Timing: 1 warmup call, then the median of ``--reps`` calls
 (time.perf_counter).  Prints one JSON line:
-    {"N", "T", "S", "d", "threads", "ms", "m_tokens_per_s", "peak_rss_bytes",
-     "input_bytes", "predicted_peak_bytes"}
+    {"N", "T", "S", "d", "threads", "ms", "ms_min_max", "m_tokens_per_s",
+     "peak_rss_bytes", "input_bytes", "predicted_peak_bytes"}
 
 Usage: python oracle/cpu_baseline.py --N 8 --T 4096 --L 4 --R 16 --d 64
                                      --threads 16 [--reps 3]
@@ -65,6 +65,7 @@ def main() -> int:
     print(json.dumps({
         "N": a.N, "T": a.T, "S": S, "d": a.d, "threads": torch.get_num_threads(),
         "ms": round(med * 1e3, 3),
+        "ms_min_max": [round(min(times) * 1e3, 3), round(max(times) * 1e3, 3)],
         "m_tokens_per_s": round(a.N * a.T / med / 1e6, 5),
         "peak_rss_bytes": resource.getrusage(resource.RUSAGE_SELF).ru_maxrss * 1024,
         "input_bytes": (2 * a.N * a.T * S + a.N * a.T * a.d) * 4,

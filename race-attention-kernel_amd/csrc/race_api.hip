@@ -5,6 +5,7 @@
 // (src/causal_v2/kernels/race_causal_fwd.h:40-49): caller-owned outputs and
 // workspace, one stream, no allocation, no host synchronization, first error
 // returned, hipErrorInvalidValue for anything the kernels do not support.
+#include <atomic>
 #include <climits>
 #include <mutex>
 
@@ -62,6 +63,36 @@ race_status resolve_kernel(const race_shape* sh, int causal, const race_options*
     return RACE_SUCCESS;
 }
 
+// Device attributes the tile policies read on every call, cached per device
+// (hipGetDevice is a thread-local read; the attribute query is not).
+constexpr int kMaxCachedDevices = 64;
+std::atomic<int> g_cu_count[kMaxCachedDevices];
+std::atomic<int> g_lds_bytes[kMaxCachedDevices];
+
+hipError_t cached_attribute(std::atomic<int>* table, hipDeviceAttribute_t attr, int* value) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    const bool cacheable = dev >= 0 && dev < kMaxCachedDevices;
+    if (cacheable) {
+        const int v = table[dev].load(std::memory_order_relaxed);
+        if (v > 0) {
+            *value = v;
+            return hipSuccess;
+        }
+    }
+    int v = 0;
+    err = hipDeviceGetAttribute(&v, attr, dev);
+    if (err != hipSuccess) return err;
+    if (cacheable && v > 0) table[dev].store(v, std::memory_order_relaxed);
+    *value = v;
+    return hipSuccess;
+}
+
+hipError_t cu_count(int* cus) {
+    return cached_attribute(g_cu_count, hipDeviceAttributeMultiprocessorCount, cus);
+}
+
 int pow2_floor(int64_t x) {
     int p = 1;
     while (int64_t(p) * 2 <= x && p < (1 << 30)) p *= 2;
@@ -81,10 +112,8 @@ race_status resolve_tile(const race_shape* sh, int causal, const race_options* o
         *tile = RACE_SUB_CHUNK_TOKENS;
         return RACE_SUCCESS;
     }
-    int dev = 0, cus = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err != hipSuccess) return err;
-    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    int cus = 0;
+    const hipError_t err = cu_count(&cus);
     if (err != hipSuccess) return err;
     if (cus < 1) cus = 1;
     // Aim for a few resident workgroups per compute unit so the output pass
@@ -224,10 +253,7 @@ hipError_t copy_floats(const float* src, float* dst, int64_t n, hipStream_t stre
 }
 
 hipError_t max_lds(int* bytes) {
-    int dev = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err != hipSuccess) return err;
-    return hipDeviceGetAttribute(bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    return cached_attribute(g_lds_bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, bytes);
 }
 
 // The column groups of a backward problem (0 where none fits: the backward
@@ -1038,9 +1064,8 @@ race_status alg1_resolve_tile(const race_alg1_shape* sh, int variant, int32_t re
         *tile = kAlg1Chunk;
         return RACE_SUCCESS;
     }
-    int dev = 0, cus = 0;
-    RACE_TRY(hipGetDevice(&dev));
-    RACE_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    int cus = 0;
+    RACE_TRY(cu_count(&cus));
     if (cus < 1) cus = 1;
     const int64_t per_cu =
         2 * int64_t(alg1_blocks_per_cu(sh->head_dim, sh->num_planes, sh->num_tables, variant));

@@ -32,6 +32,8 @@ def test_cpu_point_runs_in_a_fresh_process():
     assert pt["N"] == 2 and pt["T"] == 256 and pt["S"] == 8 and pt["d"] == 16
     assert pt["threads"] == 2
     assert pt["ms"] > 0 and pt["m_tokens_per_s"] > 0
+    lo, hi = pt["ms_min_max"]
+    assert lo <= pt["ms"] <= hi
     # The child's own peak: at least its inputs, and a fresh interpreter's.
     assert pt["peak_rss_bytes"] >= pt["input_bytes"]
     assert pt["predicted_peak_bytes"] > pt["input_bytes"]
