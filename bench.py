@@ -744,7 +744,7 @@ def measure(args, T: int) -> dict:
         del src, dst
 
     events = HipEvents()
-    max_launches = 16
+    max_launches = 64
     per_step = [events.array(max_launches + 2) for _ in range(args.steps)]
     warm = events.array(max_launches + 2)
 

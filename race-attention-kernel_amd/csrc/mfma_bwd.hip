@@ -12,6 +12,17 @@
 // copy of dQ, the running mass per sub-chunk, the suffix records), so the two
 // families are interchangeable launch by launch.
 //
+// Blocks.  The per-bucket function is a sum over buckets of independent
+// per-bucket terms, and each term is linear in the value columns, so a
+// problem with S and d multiples of 64 is the sum of (S / 64) (d / 64)
+// independent S = d = 64 problems: bucket group m (columns 64 m .. of probsQ
+// and probsK) with value group h (columns 64 h .. of V and dOut).  Block
+// (m, h) gives dQ and dK of bucket group m summed over h, and dV of value
+// group h summed over m.  The kernels take one block through BwdBlock: row
+// strides of the full tensors and where the block's state sits in the full
+// forward records; race_api.hip runs the blocks in a fixed order and adds
+// their fp32 parts (accumulate_block_kernel).
+//
 // Layout.  Workgroups are 4 wave64s; wave w owns bucket block w
 // (s = 16 w .. 16 w + 15).  Products use v_mfma_f32_16x16x32_bf16 with the
 // permuted contraction order of mfma_common.h, fp32 operands as bf16 hi/lo.
@@ -65,15 +76,16 @@ struct BwdGeo {
     static_assert(kBlk % 64 == 0, "a tensor's blocks fill whole waves");
 };
 
-// Raw registers of one staging block: rows 4 a + rr, features b E .. b E + E - 1.
+// Raw registers of one staging block: rows 4 a + rr, features b E .. b E + E - 1
+// of a tensor whose rows are `ld` elements apart.
 template <typename TIn>
 struct StageBlock {
     uint4 x[4];
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int r0, int a, int b) {
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int r0, int a, int b, int ld) {
         constexpr int E = BwdGeo<TIn>::E;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
-            x[rr] = buf_load16<kPolicyDefault>(rs, ((r0 + 4 * a + rr) * kBS + b * E) * int(sizeof(TIn)));
+            x[rr] = buf_load16<kPolicyDefault>(rs, ((r0 + 4 * a + rr) * ld + b * E) * int(sizeof(TIn)));
     }
     // R plane: row = token, 4 consecutive features.
     template <typename P>
@@ -131,7 +143,8 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
     float* __restrict__ apre, const float* __restrict__ fwd_records,
-    float* __restrict__ bwd_records, int64_t T, int tile, int64_t tiles, int64_t rec) {
+    float* __restrict__ bwd_records, int64_t T, int tile, int64_t tiles, int64_t rec,
+    BwdBlock blk) {
     using G = BwdGeo<TIn>;
     using PR = typename G::PR;
     using PM = typename G::PM;
@@ -151,25 +164,27 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
     const int64_t base = n * T + t_begin;
     constexpr int es = int(sizeof(TIn));
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * kBS, int64_t(rows) * kBS * es);
-    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * kBS, int64_t(rows) * kBS * es);
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * kBS, int64_t(rows) * kBS * es);
-    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * kBS, int64_t(rows) * kBS * es);
+    const int ldq = blk.ldq, ldv = blk.ldv;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * es);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * ldq, int64_t(rows) * ldq * es);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * ldv, int64_t(rows) * ldv * es);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * ldv, int64_t(rows) * ldv * es);
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(dQ ? dQ + base * kBS : nullptr,
                                                  dQ ? int64_t(rows) * kBS * es : 0);
     const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
 
-    // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][16 w + lr].
-    const float* fr = fwd_records + (n * tiles + ti) * rec;
+    // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][16 w + lr]
+    // (the block's rows and columns of the forward record).
+    const float* fr = fwd_records + (n * tiles + ti) * blk.fwd_rec;
     f32x4 b0t[4], zt[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            b0t[cb][rr] = fr[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr];
+            b0t[cb][rr] = fr[int64_t(blk.s0 + 16 * w + lr) * blk.fwd_d + blk.c0 + 16 * cb + 4 * gq + rr];
             zt[cb][rr] = 0.f;
         }
-    float a0 = fr[kBS * kBS + 16 * w + lr];
+    float a0 = fr[blk.fwd_a + blk.s0 + 16 * w + lr];
     float ypart = 0.f;
     const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
 
@@ -185,7 +200,15 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
             if (tensor >= 3) continue;
             const int blk = (tid + s * kThreads) % G::kBlk;
             const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
-            st[s].load(tensor == 0 ? kr : tensor == 1 ? vr : gr, r0, a, b);
+            // One call per tensor: choosing the buffer and the row stride
+            // with conditional expressions put the captured locals (and the
+            // staging registers) in scratch memory, 3x slower.
+            if (tensor == 0)
+                st[s].load(kr, r0, a, b, ldq);
+            else if (tensor == 1)
+                st[s].load(vr, r0, a, b, ldv);
+            else
+                st[s].load(gr, r0, a, b, ldv);
         }
     };
     auto stage_store = [&]() {
@@ -206,7 +229,7 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
-                qreg[bi][rr] = load1<TIn>(qr, (r0 + 16 * bi + 4 * gq + rr) * kBS + 16 * w + lr);
+                qreg[bi][rr] = load1<TIn>(qr, (r0 + 16 * bi + 4 * gq + rr) * ldq + 16 * w + lr);
     };
 
     const int subs = tile / kBC;
@@ -389,12 +412,12 @@ __device__ __forceinline__ bf16x8 triu_frag(int off, int g, int lr) {
 //   3. dK = V Z1^T + M^T W + triu(1) alpha + Y1        (Z1^T from registers)
 //   4. dV = K Z1 + P^T G                                (Z1 from an LDS plane)
 //   5. Z1^T += G^T W, Y1 += 1^T alpha
-template <typename TIn>
+template <typename TIn, typename TOut>
 __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, const float* __restrict__ dq32, const float* __restrict__ apre,
-    const float* __restrict__ suffix_records, TIn* __restrict__ dK, TIn* __restrict__ dV,
-    int64_t T, int tile, int64_t tiles, int64_t rec) {
+    const float* __restrict__ suffix_records, TOut* __restrict__ dK, TOut* __restrict__ dV,
+    int64_t T, int tile, int64_t tiles, int64_t rec, BwdBlock blk) {
     using G = BwdGeo<TIn>;
     using PR = typename G::PR;
     using PM = typename G::PM;
@@ -414,16 +437,19 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const int64_t t_begin = ti * tile;
     const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
     const int64_t base = n * T + t_begin;
-    constexpr int es = int(sizeof(TIn));
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * kBS, int64_t(rows) * kBS * es);
-    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * kBS, int64_t(rows) * kBS * es);
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * kBS, int64_t(rows) * kBS * es);
-    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * kBS, int64_t(rows) * kBS * es);
+    constexpr int es = int(sizeof(TIn)), eo = int(sizeof(TOut));
+    const int ldq = blk.ldq, ldv = blk.ldv;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * es);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * ldq, int64_t(rows) * ldq * es);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * ldv, int64_t(rows) * ldv * es);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * ldv, int64_t(rows) * ldv * es);
     const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+    // dK and dV: the caller's gradients (one block) or the block's fp32 parts,
+    // rows of kBS values either way.
     const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * kBS : nullptr,
-                                                 dK ? int64_t(rows) * kBS * es : 0);
+                                                 dK ? int64_t(rows) * kBS * eo : 0);
     const __amdgpu_buffer_rsrc_t dvr = make_rsrc(dV ? dV + base * kBS : nullptr,
-                                                 dV ? int64_t(rows) * kBS * es : 0);
+                                                 dV ? int64_t(rows) * kBS * eo : 0);
 
     // Suffix state at the tile end: Z1^T[16 cb + 4 g + rr][16 w + lr], Y1[16 w + lr].
     const float* sr = suffix_records + (n * tiles + ti) * rec;
@@ -447,7 +473,15 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
             if (tensor >= 3) continue;
             const int blk = (tid + s * kThreads) % G::kBlk;
             const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
-            st[s].load(tensor == 0 ? kr : tensor == 1 ? vr : gr, r0, a, b);
+            // One call per tensor: choosing the buffer and the row stride
+            // with conditional expressions put the captured locals (and the
+            // staging registers) in scratch memory, 3x slower.
+            if (tensor == 0)
+                st[s].load(kr, r0, a, b, ldq);
+            else if (tensor == 1)
+                st[s].load(vr, r0, a, b, ldv);
+            else
+                st[s].load(gr, r0, a, b, ldv);
         }
     };
     auto stage_store = [&]() {
@@ -467,9 +501,9 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
         for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-                const int elem = (r0 + 16 * bi + 4 * gq + rr) * kBS + 16 * w + lr;
-                qreg[bi][rr] = load1<TIn>(qr, elem);
-                dreg[bi][rr] = load1<float>(d32r, elem);
+                const int row = r0 + 16 * bi + 4 * gq + rr;
+                qreg[bi][rr] = load1<TIn>(qr, row * ldq + 16 * w + lr);
+                dreg[bi][rr] = load1<float>(d32r, row * kBS + 16 * w + lr);
             }
     };
 
@@ -618,7 +652,7 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
         for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
-                store1<TIn>(dkr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dk[bj][rr]);
+                store1<TOut>(dkr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dk[bj][rr]);
         // 4: dV[j][c] for c-block w.
         {
             f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -649,7 +683,7 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
                 dv[bj] = mfma3<kSplit>(ph, pl, gh, gl, dv[bj]);
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
-                    store1<TIn>(dvr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dv[bj][rr]);
+                    store1<TOut>(dvr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dv[bj][rr]);
             }
         }
         // 5: the suffix state before this sub-chunk.
@@ -672,12 +706,25 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
 
 }  // namespace
 
-bool causal_bwd_mfma_supported(int S, int d) { return S == kBS && d == kBS; }
+bool causal_bwd_mfma_supported(int S, int d) {
+    return S % kBS == 0 && d % kBS == 0 && S >= kBS && d >= kBS && S <= 256 && d <= 128;
+}
+
+BwdBlock single_block(const Problem& p) {
+    BwdBlock b;
+    b.ldq = b.ldv = kBS;
+    b.fwd_d = kBS;
+    b.fwd_a = kBS * kBS;
+    b.fwd_rec = p.rec;
+    return b;
+}
 
 hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
-                                     float* bwd_records, const Problem& p, hipStream_t stream) {
-    if (!causal_bwd_mfma_supported(p.S, p.d) || p.tile % kBC != 0) return hipErrorInvalidValue;
+                                     float* bwd_records, const Problem& p, const BwdBlock& blk,
+                                     hipStream_t stream) {
+    // p describes one 64 x 64 block (p.S = p.d = 64, p.rec its record).
+    if (p.S != kBS || p.d != kBS || p.tile % kBC != 0) return hipErrorInvalidValue;
     // fp32: dQ is written only as the fp32 copy (pass the caller's dQ as dq32).
     if (p.dtype != RACE_BF16 && dQ) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
@@ -687,14 +734,14 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
         causal_bwd_dq_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
             static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
             static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ),
-            dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec);
+            dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec, blk);
     } else {
         using G = BwdGeo<float>;
         const size_t lds = G::kDqLds;
         causal_bwd_dq_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
             static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
             static_cast<const float*>(g), static_cast<float*>(dQ), dq32, apre, fwd_records,
-            bwd_records, p.T, p.tile, p.tiles, p.rec);
+            bwd_records, p.T, p.tile, p.tiles, p.rec, blk);
     }
     return hipGetLastError();
 }
@@ -702,25 +749,24 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
 hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
-                                      const Problem& p, hipStream_t stream) {
-    if (!causal_bwd_mfma_supported(p.S, p.d) || p.tile % kBC != 0) return hipErrorInvalidValue;
+                                      const Problem& p, const BwdBlock& blk, bool fp32_parts,
+                                      hipStream_t stream) {
+    if (p.S != kBS || p.d != kBS || p.tile % kBC != 0) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+#define RACE_DKV(TIN, TOUT)                                                                          \
+    causal_bwd_dkv_mfma_kernel<TIN, TOUT><<<grid, kThreads, BwdGeo<TIN>::kDkvLds, stream>>>(         \
+        static_cast<const TIN*>(q), static_cast<const TIN*>(k), static_cast<const TIN*>(v),         \
+        static_cast<const TIN*>(g), dq32, apre, suffix_records, static_cast<TOUT*>(dK),             \
+        static_cast<TOUT*>(dV), p.T, p.tile, p.tiles, p.rec, blk)
     if (p.dtype == RACE_BF16) {
-        using G = BwdGeo<bf16_t>;
-        const size_t lds = G::kDkvLds;
-        causal_bwd_dkv_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
-            static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-            static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), dq32, apre,
-            suffix_records, static_cast<bf16_t*>(dK), static_cast<bf16_t*>(dV), p.T, p.tile, p.tiles,
-            p.rec);
+        if (fp32_parts)
+            RACE_DKV(bf16_t, float);
+        else
+            RACE_DKV(bf16_t, bf16_t);
     } else {
-        using G = BwdGeo<float>;
-        const size_t lds = G::kDkvLds;
-        causal_bwd_dkv_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
-            static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
-            static_cast<const float*>(g), dq32, apre, suffix_records, static_cast<float*>(dK),
-            static_cast<float*>(dV), p.T, p.tile, p.tiles, p.rec);
+        RACE_DKV(float, float);
     }
+#undef RACE_DKV
     return hipGetLastError();
 }
 

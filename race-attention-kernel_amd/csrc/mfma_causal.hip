@@ -404,25 +404,28 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
 }
 
-template <typename TIn, int S, int D, int C, int kMinBlocks, int NW = 4>
-hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void* out, float* records,
-                              float* state, const Problem& p, hipStream_t stream, Marks* marks) {
+// K1 alone: the register-direct kernel where it applies, else the workgroup one.
+template <typename TIn, int S, int D, int C, int kMinBlocks>
+hipError_t launch_sums_family(const void* k, const void* v, float* records, const Problem& p,
+                              hipStream_t stream) {
     using G = Geo<TIn, S, D, C>;
-    using GO = Geo<TIn, S, D, C, NW>;
     // Tiles are whole sub-chunks, and a tile's bytes fit a 32-bit buffer range.
     if (p.tile % C != 0) return hipErrorInvalidValue;
     if (int64_t(p.tile) * (S > D ? S : D) * int64_t(sizeof(TIn)) >= (int64_t(1) << 31))
         return hipErrorInvalidValue;
+    if (direct_sums_supported(S, D)) return launch_tile_sums_direct(k, v, records, p, stream);
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
-    hipError_t err;
-    if (direct_sums_supported(S, D)) {
-        err = launch_tile_sums_direct(k, v, records, p, stream);
-    } else {
-        tile_sums_mfma_kernel<TIn, S, D, C, kMinBlocks><<<grid, kThreads, G::kSumsLds, stream>>>(
-            static_cast<const TIn*>(k), static_cast<const TIn*>(v), records, p.T, p.tile, p.tiles,
-            p.rec);
-        err = hipGetLastError();
-    }
+    tile_sums_mfma_kernel<TIn, S, D, C, kMinBlocks><<<grid, kThreads, G::kSumsLds, stream>>>(
+        static_cast<const TIn*>(k), static_cast<const TIn*>(v), records, p.T, p.tile, p.tiles, p.rec);
+    return hipGetLastError();
+}
+
+template <typename TIn, int S, int D, int C, int kMinBlocks, int NW = 4>
+hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void* out, float* records,
+                              float* state, const Problem& p, hipStream_t stream, Marks* marks) {
+    using GO = Geo<TIn, S, D, C, NW>;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    hipError_t err = launch_sums_family<TIn, S, D, C, kMinBlocks>(k, v, records, p, stream);
     if (err != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
     if ((err = launch_tile_scan(records, state, p, stream)) != hipSuccess) return err;
@@ -457,7 +460,26 @@ hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out,
     return hipErrorInvalidValue;
 }
 
+template <typename TIn>
+hipError_t dispatch_sums(const void* k, const void* v, float* records, const Problem& p,
+                         hipStream_t stream) {
+    // The K1 launches of dispatch_mfma, shape for shape.
+    if (p.S == 64 && p.d == 64) return launch_sums_family<TIn, 64, 64, 32, 4>(k, v, records, p, stream);
+    if (p.S == 64 && p.d == 128) return launch_sums_family<TIn, 64, 128, 64, 1>(k, v, records, p, stream);
+    if (p.S == 128 && p.d == 64) return launch_sums_family<TIn, 128, 64, 64, 1>(k, v, records, p, stream);
+    if (p.S == 128 && p.d == 128) return launch_sums_family<TIn, 128, 128, 64, 1>(k, v, records, p, stream);
+    if (p.S == 256 && p.d == 64) return launch_sums_family<TIn, 256, 64, 32, 1>(k, v, records, p, stream);
+    if (p.S == 256 && p.d == 128) return launch_sums_family<TIn, 256, 128, 32, 1>(k, v, records, p, stream);
+    return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+hipError_t launch_tile_sums_mfma(const void* k, const void* v, float* records, const Problem& p,
+                                 hipStream_t stream) {
+    if (p.dtype == RACE_BF16) return dispatch_sums<bf16_t>(k, v, records, p, stream);
+    return dispatch_sums<float>(k, v, records, p, stream);
+}
 
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel) {
     if (kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(S, d, dtype))

@@ -191,14 +191,14 @@ BwdLayout bwd_layout(const Problem& p) {
 // of dQ and, unless the caller hands in the forward's records, the forward
 // prefix records (last, so the two layouts share every other offset).
 struct CausalBwdLayout {
-    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0, acc = 0;
-    int64_t total() const { return bwd + apre + dq32 + fwd + acc; }
+    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0, parts = 0, acc = 0;
+    int64_t total() const { return bwd + apre + dq32 + fwd + parts + acc; }
 };
 
-// Column groups of the causal backward: 1 where the state of every value
-// column fits one workgroup's LDS, else the fewest groups of equal width that
-// fit (each walk then takes one group; causal_bwd.hip), 0 where none does.
-// *C gets the groups' sub-chunk length.
+// Column groups of the vector-ALU causal backward: 1 where the state of
+// every value column fits one workgroup's LDS, else the fewest groups of
+// equal width that fit (each walk then takes one group; causal_bwd.hip), 0
+// where none does.  *C gets the groups' sub-chunk length.
 int causal_bwd_groups(int S, int d, int lds_limit, int* C) {
     for (int G = 1; G <= d; ++G) {
         if (d % G != 0) continue;
@@ -212,21 +212,57 @@ int causal_bwd_groups(int S, int d, int lds_limit, int* C) {
     return 0;
 }
 
-// Workspace of the causal backward with `groups` column groups: the suffix
-// records (of one group's width; the groups take turns), the running mass,
-// dq32, the forward prefix records unless given, and with several groups of
-// bf16 tokens the fp32 running sums of dQ and dK.
-CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, int groups) {
+// How a causal backward runs: on the matrix cores in 64 x 64 blocks (bucket
+// group x value group; one block at S = d = 64), or on the vector ALU in
+// column groups (0 groups: refused).  Planned for gfx950's LDS per
+// workgroup, so the workspace query needs no device.
+struct CausalBwdPlan {
+    bool mfma = false;
+    int mblocks = 1, hblocks = 1;  // bucket groups, value groups (matrix cores)
+    int groups = 0, C = 0;         // column groups, sub-chunk (vector ALU)
+    bool blocked() const { return mfma && mblocks * hblocks > 1; }
+};
+
+CausalBwdPlan plan_causal_bwd(const Problem& p, int kernel) {
+    CausalBwdPlan pl;
+    pl.mfma = kernel != RACE_KERNEL_VALU && causal_bwd_mfma_supported(p.S, p.d) && p.tile % 32 == 0;
+    if (pl.mfma) {
+        pl.mblocks = p.S / 64;
+        pl.hblocks = p.d / 64;
+        pl.groups = 1;
+        pl.C = 32;
+    } else {
+        pl.groups = causal_bwd_groups(p.S, p.d, kGfx950LdsBytes, &pl.C);
+    }
+    return pl;
+}
+
+// Workspace of the causal backward: the forward prefix records unless given,
+// the suffix records (of one column group, or of one 64 x 64 block: the
+// groups and blocks take turns), the running mass every 16 tokens, dq32 (dQ,
+// or the current group's or block's part of it); with blocks the blocks' fp32
+// dK and dV parts and, for bf16 tokens, fp32 running sums of dQ, dK, dV; with
+// several column groups of bf16 tokens the running sums of dQ and dK.
+CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const CausalBwdPlan& pl) {
     CausalBwdLayout l;
+    const int64_t NT = p.N * p.T;
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
+    if (pl.blocked()) {
+        l.bwd = p.N * p.tiles * record_floats(64, 64);
+        l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
+        l.dq32 = round64(NT * 64);
+        l.parts = 2 * round64(NT * 64);
+        l.acc = p.dtype == RACE_BF16 ? 2 * round64(NT * p.S) + round64(NT * p.d) : 0;
+        return l;
+    }
+    const int groups = pl.groups > 1 ? pl.groups : 1;
     const int64_t rec_g = groups > 1 ? record_floats(p.S, p.d / groups) : p.rec;
     l.bwd = p.N * p.tiles * rec_g;
     l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(p.S));
-    l.dq32 = round64(p.N * p.T * int64_t(p.S));
-    l.acc = (groups > 1 && p.dtype == RACE_BF16) ? 2 * round64(p.N * p.T * int64_t(p.S)) : 0;
+    l.dq32 = round64(NT * p.S);
+    l.acc = (groups > 1 && p.dtype == RACE_BF16) ? 2 * round64(NT * p.S) : 0;
     return l;
 }
-
 
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -245,7 +281,50 @@ __global__ void copy_floats_kernel(const float* src, float* dst, int64_t n) {
     if (i < n) dst[i] = src[i];
 }
 
+// One 64 x 64 block's fp32 part into its place: rows of 64 values of part
+// added to (or, first, written over) rows of `ld` values of dst, or written
+// to out (as TOut) instead of dst.  Four values per thread.
+template <typename TOut>
+__global__ void accumulate_block_kernel(const float* __restrict__ part, float* __restrict__ dst,
+                                        TOut* __restrict__ out, int64_t rows, int ld, int first) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * 16) return;
+    const int64_t row = i >> 4;
+    const int c = 4 * int(i & 15);
+    float4 x = *reinterpret_cast<const float4*>(part + row * 64 + c);
+    const int64_t o = row * ld + c;
+    if (!first) {
+        const float4 y = *reinterpret_cast<const float4*>(dst + o);
+        x = make_float4(y.x + x.x, y.y + x.y, y.z + x.z, y.w + x.w);
+    }
+    if (!out) {
+        *reinterpret_cast<float4*>(dst + o) = x;
+    } else {
+        store_val(out + o, x.x);
+        store_val(out + o + 1, x.y);
+        store_val(out + o + 2, x.z);
+        store_val(out + o + 3, x.w);
+    }
+}
+
 // dst = src elementwise (a no-op when dst is null or is src).
+}  // namespace
+
+hipError_t launch_accumulate_block(const float* part, float* dst, void* out, int dtype, int64_t rows,
+                                   int ld, bool first, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    const unsigned blocks = unsigned((rows * 16 + kThreads - 1) / kThreads);
+    if (out && dtype == RACE_BF16)
+        accumulate_block_kernel<bf16_t><<<blocks, kThreads, 0, stream>>>(part, dst, static_cast<bf16_t*>(out),
+                                                                         rows, ld, first ? 1 : 0);
+    else
+        accumulate_block_kernel<float><<<blocks, kThreads, 0, stream>>>(part, dst, static_cast<float*>(out),
+                                                                        rows, ld, first ? 1 : 0);
+    return hipGetLastError();
+}
+
+namespace {
+
 hipError_t copy_floats(const float* src, float* dst, int64_t n, hipStream_t stream) {
     if (n <= 0 || !dst || dst == src) return hipSuccess;
     copy_floats_kernel<<<unsigned((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(src, dst, n);
@@ -256,13 +335,6 @@ hipError_t max_lds(int* bytes) {
     return cached_attribute(g_lds_bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, bytes);
 }
 
-// The column groups of a backward problem (0 where none fits: the backward
-// refuses the shape, its workspace query sizes one group), planned for
-// gfx950's LDS per workgroup so that the workspace query needs no device.
-hipError_t causal_bwd_plan(const Problem& p, int* groups, int* C) {
-    *groups = causal_bwd_groups(p.S, p.d, kGfx950LdsBytes, C);
-    return hipSuccess;
-}
 
 // The non-causal reduction and map: the 16-byte-vector kernels when both
 // widths are multiples of 4, the scalar ones otherwise.
@@ -717,8 +789,8 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     bool mfma = false;
     race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
-    const bool use_mfma = kernel != RACE_KERNEL_VALU && causal_bwd_mfma_supported(p.S, p.d) &&
-                          p.tile % 32 == 0;
+    const CausalBwdPlan pl = plan_causal_bwd(p, kernel);
+    const bool use_mfma = pl.mfma;
     if (kernel == RACE_KERNEL_MFMA && !use_mfma) return RACE_ERROR_INVALID_VALUE;
     // Saved forward records come with the forward's (explicit) tile length.
     if (fwd_records && (!opts || opts->tile_tokens <= 0 || !aligned16(fwd_records)))
@@ -729,22 +801,22 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         return RACE_ERROR_INVALID_VALUE;
     if ((dQ && !aligned16(dQ)) || (dK && !aligned16(dK)) || (dV && !aligned16(dV)))
         return RACE_ERROR_INVALID_VALUE;
-    int groups = 0, C = 0;
-    RACE_TRY(causal_bwd_plan(p, &groups, &C));
-    const CausalBwdLayout l = causal_bwd_layout(p, fwd_records != nullptr, groups > 1 ? groups : 1);
+    const int groups = pl.groups, C = pl.C;
+    const CausalBwdLayout l = causal_bwd_layout(p, fwd_records != nullptr, pl);
     if (!workspace || !aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
         return RACE_ERROR_INVALID_VALUE;
-    if (groups == 0 || (use_mfma && (groups != 1 || C != 32))) return RACE_ERROR_INVALID_VALUE;
+    if (groups == 0) return RACE_ERROR_INVALID_VALUE;
     float* bwd_rec = static_cast<float*>(workspace);
     float* apre = bwd_rec + l.bwd;
     float* dq32 = apre + l.apre;
     float* fwd_ws = dq32 + l.dq32;
-    float* acc = fwd_ws + l.fwd;
-    // B3 reads dQ back in fp32.  With one column group an fp32 dQ is that
-    // copy: B1 writes it once, into the caller's buffer, and B3 reads it from
-    // there.  With several, dq32 holds the current group's part.
+    float* parts = fwd_ws + l.fwd;
+    float* acc = parts + l.parts;
+    // B3 reads dQ back in fp32.  With one column group (or block) an fp32 dQ
+    // is that copy: B1 writes it once, into the caller's buffer, and B3 reads
+    // it from there.  With several, dq32 holds the current group's part.
     void* dq_out = dQ;
-    if (dQ && p.dtype == RACE_F32 && groups == 1) {
+    if (dQ && p.dtype == RACE_F32 && groups == 1 && !pl.blocked()) {
         dq32 = static_cast<float*>(dQ);
         dq_out = nullptr;
     }
@@ -756,6 +828,8 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     if (!fwd_rec) {
         if (direct_sums_supported(p.S, p.d) && p.tile % 64 == 0)
             RACE_TRY(launch_tile_sums_direct(probsK, V, fwd_ws, p, stream));
+        else if (mfma_causal_supported(p.S, p.d))
+            RACE_TRY(launch_tile_sums_mfma(probsK, V, fwd_ws, p, stream));
         else
             RACE_TRY(launch_tile_outer_sums(probsK, V, fwd_ws, p, p.S, p.d, stream));
         RACE_TRY(marks->mark(stream));
@@ -763,16 +837,79 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         RACE_TRY(marks->mark(stream));
         fwd_rec = fwd_ws;
     }
-    if (use_mfma) {
+    if (use_mfma && !pl.blocked()) {
+        const BwdBlock blk = single_block(p);
         RACE_TRY(launch_causal_bwd_dq_mfma(probsQ, probsK, V, dOut, dq_out, dq32, apre, fwd_rec,
-                                           bwd_rec, p, stream));
+                                           bwd_rec, p, blk, stream));
         RACE_TRY(marks->mark(stream));
         if (!dK && !dV) return RACE_SUCCESS;
         RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
         RACE_TRY(marks->mark(stream));
         RACE_TRY(launch_causal_bwd_dkv_mfma(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p,
-                                            stream));
+                                            blk, /*fp32_parts=*/false, stream));
         return marks->mark(stream);
+    }
+    if (use_mfma) {
+        // 64 x 64 blocks, bucket group m outer and value group h inner: dQ and
+        // dK of group m are summed over h, dV of group h over m, in that fixed
+        // order, in fp32 (the fp32 outputs themselves, or workspace for bf16
+        // outputs, whose last addend writes the caller's buffers).
+        Problem pb = p;
+        pb.S = pb.d = 64;
+        pb.rec = record_floats(64, 64);
+        const bool f32 = p.dtype == RACE_F32;
+        const int64_t es = f32 ? 4 : 2, NT = p.N * p.T;
+        float* dk_part = parts;
+        float* dv_part = parts + round64(NT * 64);
+        float* acc_q = f32 ? static_cast<float*>(dQ) : (dQ ? acc : nullptr);
+        float* acc_k = f32 ? static_cast<float*>(dK) : (dK ? acc + round64(NT * p.S) : nullptr);
+        float* acc_v = f32 ? static_cast<float*>(dV) : (dV ? acc + 2 * round64(NT * p.S) : nullptr);
+        for (int m = 0; m < pl.mblocks; ++m) {
+            for (int h = 0; h < pl.hblocks; ++h) {
+                BwdBlock blk;
+                blk.ldq = p.S;
+                blk.ldv = p.d;
+                blk.s0 = 64 * m;
+                blk.c0 = 64 * h;
+                blk.fwd_d = p.d;
+                blk.fwd_a = int64_t(p.S) * p.d;
+                blk.fwd_rec = p.rec;
+                const void* qb = static_cast<const char*>(probsQ) + 64 * m * es;
+                const void* kb = static_cast<const char*>(probsK) + 64 * m * es;
+                const void* vb = static_cast<const char*>(V) + 64 * h * es;
+                const void* gb = static_cast<const char*>(dOut) + 64 * h * es;
+                const bool last_h = h == pl.hblocks - 1, last_m = m == pl.mblocks - 1;
+                RACE_TRY(launch_causal_bwd_dq_mfma(qb, kb, vb, gb, nullptr, dq32, apre, fwd_rec, bwd_rec,
+                                                   pb, blk, stream));
+                RACE_TRY(marks->mark(stream));
+                if (acc_q) {
+                    void* out = (!f32 && last_h) ? static_cast<char*>(dQ) + 64 * m * es : nullptr;
+                    RACE_TRY(launch_accumulate_block(dq32, acc_q + 64 * m, out, p.dtype, NT, p.S, h == 0,
+                                                     stream));
+                    RACE_TRY(marks->mark(stream));
+                }
+                if (!dK && !dV) continue;
+                RACE_TRY(launch_tile_scan(bwd_rec, nullptr, pb, stream, /*reverse=*/true));
+                RACE_TRY(marks->mark(stream));
+                RACE_TRY(launch_causal_bwd_dkv_mfma(qb, kb, vb, gb, dq32, apre, bwd_rec,
+                                                    dK ? dk_part : nullptr, dV ? dv_part : nullptr, pb,
+                                                    blk, /*fp32_parts=*/true, stream));
+                RACE_TRY(marks->mark(stream));
+                if (acc_k) {
+                    void* out = (!f32 && last_h) ? static_cast<char*>(dK) + 64 * m * es : nullptr;
+                    RACE_TRY(launch_accumulate_block(dk_part, acc_k + 64 * m, out, p.dtype, NT, p.S,
+                                                     h == 0, stream));
+                    RACE_TRY(marks->mark(stream));
+                }
+                if (acc_v) {
+                    void* out = (!f32 && last_m) ? static_cast<char*>(dV) + 64 * h * es : nullptr;
+                    RACE_TRY(launch_accumulate_block(dv_part, acc_v + 64 * h, out, p.dtype, NT, p.d,
+                                                     m == 0, stream));
+                    RACE_TRY(marks->mark(stream));
+                }
+            }
+        }
+        return RACE_SUCCESS;
     }
     if (groups == 1) {
         const BwdCols cols = all_columns(p);
@@ -841,9 +978,8 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
     race_options topts = {opts ? opts->tile_tokens : 0, RACE_KERNEL_VALU};
     const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
-    int groups = 0, C = 0;
-    RACE_TRY(causal_bwd_plan(p, &groups, &C));
-    *bytes = size_t(causal_bwd_layout(p, false, groups > 1 ? groups : 1).total()) * sizeof(float);
+    *bytes = size_t(causal_bwd_layout(p, false, plan_causal_bwd(p, kernel_choice(opts))).total()) *
+             sizeof(float);
     return RACE_SUCCESS;
 }
 
@@ -855,9 +991,8 @@ race_status race_causal_bwd_from_records_workspace_bytes(const race_shape* shape
     race_options topts = {opts->tile_tokens, RACE_KERNEL_VALU};
     const race_status st = make_problem(shape, 0, &topts, &mfma, &p);
     if (st != RACE_SUCCESS) return st;
-    int groups = 0, C = 0;
-    RACE_TRY(causal_bwd_plan(p, &groups, &C));
-    *bytes = size_t(causal_bwd_layout(p, true, groups > 1 ? groups : 1).total()) * sizeof(float);
+    *bytes = size_t(causal_bwd_layout(p, true, plan_causal_bwd(p, kernel_choice(opts))).total()) *
+             sizeof(float);
     return RACE_SUCCESS;
 }
 

@@ -199,17 +199,45 @@ hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, co
                                  const float* suffix_records, void* dK, void* dV, const Problem& p,
                                  int C, const BwdCols& cols, hipStream_t stream);
 
-// Matrix-core kernels of the causal backward (mfma_bwd.hip): S = d = 64,
-// 32-token sub-chunks, the same buffers as the vector-ALU kernels.  With fp32
-// tokens the dQ kernel writes dQ only through dq32 (dQ must be null).
+// Matrix-core kernels of the causal backward (mfma_bwd.hip): 64 x 64 blocks
+// (S = d = 64, or one block of S and d multiples of 64: bucket group m, value
+// group h), 32-token sub-chunks, the same buffers as the vector-ALU kernels.
+// With fp32 tokens the dQ kernel writes dQ only through dq32 (dQ must be null).
+struct BwdBlock {
+    int ldq = 64;          // row stride of probsQ and probsK (the full S)
+    int ldv = 64;          // row stride of V and dOut (the full d)
+    int s0 = 0, c0 = 0;    // the block's first bucket and value column
+    int fwd_d = 64;        // row length of B in the forward records (the full d)
+    int64_t fwd_a = 4096;  // offset of A in a forward record (full S * full d)
+    int64_t fwd_rec = 0;   // stride of the forward records
+};
+// Shapes the blocks cover: S in {64, 128, 256}, d in {64, 128}.
 bool causal_bwd_mfma_supported(int S, int d);
+// The single block of an S = d = 64 problem.
+BwdBlock single_block(const Problem& p);
+// p is the block's problem (S = d = 64 and its record size); q, k, v, g point
+// at the block's first column; dq32, apre and bwd_records are the block's own
+// (rows of 64).
 hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
-                                     float* bwd_records, const Problem& p, hipStream_t stream);
+                                     float* bwd_records, const Problem& p, const BwdBlock& blk,
+                                     hipStream_t stream);
+// dK and dV (rows of 64): the caller's gradients, or with fp32_parts the
+// block's fp32 parts for bf16 tokens.
 hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
-                                      const Problem& p, hipStream_t stream);
+                                      const Problem& p, const BwdBlock& blk, bool fp32_parts,
+                                      hipStream_t stream);
+// dst (rows of ld values, from its first column) += part (rows of 64 fp32
+// values), over rows x 64: with `first` dst = part; the result goes to out
+// (dtype, rows of ld) instead of dst when out is given.  Elementwise.
+hipError_t launch_accumulate_block(const float* part, float* dst, void* out, int dtype, int64_t rows,
+                                   int ld, bool first, hipStream_t stream);
+// The forward's tile sums (K1) on the matrix cores for the shapes
+// mfma_causal_supported takes, into records of p.rec floats.
+hipError_t launch_tile_sums_mfma(const void* k, const void* v, float* records, const Problem& p,
+                                 hipStream_t stream);
 
 // ---- bucket-probability front end (hashing.hip) ----
 bool hash_shape_ok(int64_t rows, int dk, int L, int K);

@@ -187,6 +187,23 @@ def test_mfma_backward_needs_its_specialization(race, cuda):
         race.race_causal_backward(q, k, v, g, kernel="mfma")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("L, R, d", [(8, 32, 128), (4, 32, 128), (8, 32, 64), (2, 32, 128)])
+def test_matrix_core_blocks_agree_with_the_vector_alu(race, oracle, cuda, dtype, L, R, d):
+    # S, d multiples of 64 above 64 run the matrix-core kernels in 64 x 64
+    # blocks; the vector-ALU walks (forced) compute the same gradients.
+    say("c-bwd blocks", L, R, d, dtype)
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, 777, L, R, d, seed=50 + d, dtype=dtype,
+                                                       grad_out=True))
+    got = race.race_causal_backward(q, k, v, g, kernel="mfma")
+    ref = race.race_causal_backward(q, k, v, g, kernel="valu")
+    out = race.race_fused_fwd(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    check_grads(oracle, q, k, v, g, out, *got, tol_for(dtype))
+    for name, a, b in (("dQ", got[0], ref[0]), ("dV", got[2], ref[2])):
+        assert per_stream_rel_err(to_np(a), to_np(b).astype(np.float64)) <= 2 * tol_for(dtype), name
+
+
 def test_unsupported_shape_raises(race, cuda):
     # S = 512: past the library's 256 buckets.
     q, k, v, g = (x.to(cuda) for x in race.make_inputs(1, 64, 4, 128, 8, seed=27, grad_out=True))
