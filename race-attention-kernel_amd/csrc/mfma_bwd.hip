@@ -20,8 +20,8 @@
 // (m, h) gives dQ and dK of bucket group m summed over h, and dV of value
 // group h summed over m.  The kernels take one block through BwdBlock: row
 // strides of the full tensors and where the block's state sits in the full
-// forward records; race_api.hip runs the blocks in a fixed order and adds
-// their fp32 parts (accumulate_block_kernel).
+// forward records; race_api.hip runs the blocks in a fixed order and the
+// kernels add each block's part to fp32 running sums (BwdBlock).
 //
 // Layout.  Workgroups are 4 wave64s; wave w owns bucket block w
 // (s = 16 w .. 16 w + 15).  Products use v_mfma_f32_16x16x32_bf16 with the
@@ -172,6 +172,12 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(dQ ? dQ + base * kBS : nullptr,
                                                  dQ ? int64_t(rows) * kBS * es : 0);
     const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+    // Several blocks: dQ's running sum and, for the last addend of bf16
+    // tokens, the caller's dQ (rows of ldq).
+    const __amdgpu_buffer_rsrc_t aqr =
+        make_rsrc(blk.acc_q ? blk.acc_q + base * ldq : nullptr, blk.acc_q ? int64_t(rows) * ldq * 4 : 0);
+    const __amdgpu_buffer_rsrc_t fqr = make_rsrc(
+        blk.fin_q ? static_cast<TIn*>(blk.fin_q) + base * ldq : nullptr, blk.fin_q ? int64_t(rows) * ldq * es : 0);
 
     // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][16 w + lr]
     // (the block's rows and columns of the forward record).
@@ -256,6 +262,22 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
             }
         }
         T32::template write<kPolicyDefault, kThreads>(c32, d32r, r0);
+        if (blk.blocked && blk.acc_q) {
+            // The block's part into dQ's running sum (rows outside the tile,
+            // and all rows of the first flush, fall outside the views).
+#pragma unroll
+            for (int i = 0; i < T32::template Chunks<kThreads>::kPer; ++i) {
+                const int qi = tid + i * kThreads;
+                const int off = (r0 + (qi >> 4)) * ldq + 4 * (qi & 15);
+                f32x4 t = __builtin_bit_cast(f32x4, c32.x[i]);
+                if (!blk.q_first) t = t + __builtin_bit_cast(f32x4, buf_load16<kPolicyDefault>(aqr, off * 4));
+                if (blk.fin_q)
+                    store4<TIn, kPolicyDefault>(fqr, off * es, t);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), aqr, off * 4, 0,
+                                                           kPolicyDefault);
+            }
+        }
     };
     stage_load(0);
     load_q(0);
@@ -412,11 +434,11 @@ __device__ __forceinline__ bf16x8 triu_frag(int off, int g, int lr) {
 //   3. dK = V Z1^T + M^T W + triu(1) alpha + Y1        (Z1^T from registers)
 //   4. dV = K Z1 + P^T G                                (Z1 from an LDS plane)
 //   5. Z1^T += G^T W, Y1 += 1^T alpha
-template <typename TIn, typename TOut>
+template <typename TIn>
 __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, const float* __restrict__ dq32, const float* __restrict__ apre,
-    const float* __restrict__ suffix_records, TOut* __restrict__ dK, TOut* __restrict__ dV,
+    const float* __restrict__ suffix_records, TIn* __restrict__ dK, TIn* __restrict__ dV,
     int64_t T, int tile, int64_t tiles, int64_t rec, BwdBlock blk) {
     using G = BwdGeo<TIn>;
     using PR = typename G::PR;
@@ -437,19 +459,42 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const int64_t t_begin = ti * tile;
     const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
     const int64_t base = n * T + t_begin;
-    constexpr int es = int(sizeof(TIn)), eo = int(sizeof(TOut));
+    constexpr int es = int(sizeof(TIn));
     const int ldq = blk.ldq, ldv = blk.ldv;
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * es);
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * ldq, int64_t(rows) * ldq * es);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * ldv, int64_t(rows) * ldv * es);
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * ldv, int64_t(rows) * ldv * es);
     const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
-    // dK and dV: the caller's gradients (one block) or the block's fp32 parts,
-    // rows of kBS values either way.
     const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * kBS : nullptr,
-                                                 dK ? int64_t(rows) * kBS * eo : 0);
+                                                 dK ? int64_t(rows) * kBS * es : 0);
     const __amdgpu_buffer_rsrc_t dvr = make_rsrc(dV ? dV + base * kBS : nullptr,
-                                                 dV ? int64_t(rows) * kBS * eo : 0);
+                                                 dV ? int64_t(rows) * kBS * es : 0);
+    // Several blocks: the running sums of dK (rows of ldq) and dV (rows of
+    // ldv), and the caller's gradients for the last addend of bf16 tokens.
+    const __amdgpu_buffer_rsrc_t akr =
+        make_rsrc(blk.acc_k ? blk.acc_k + base * ldq : nullptr, blk.acc_k ? int64_t(rows) * ldq * 4 : 0);
+    const __amdgpu_buffer_rsrc_t avr =
+        make_rsrc(blk.acc_v ? blk.acc_v + base * ldv : nullptr, blk.acc_v ? int64_t(rows) * ldv * 4 : 0);
+    const __amdgpu_buffer_rsrc_t fkr = make_rsrc(
+        blk.fin_k ? static_cast<TIn*>(blk.fin_k) + base * ldq : nullptr, blk.fin_k ? int64_t(rows) * ldq * es : 0);
+    const __amdgpu_buffer_rsrc_t fvr = make_rsrc(
+        blk.fin_v ? static_cast<TIn*>(blk.fin_v) + base * ldv : nullptr, blk.fin_v ? int64_t(rows) * ldv * es : 0);
+    // One gradient value at (row, col): as it is (one block), or added to its
+    // running sum (blocks).
+    auto put_grad = [&](__amdgpu_buffer_rsrc_t own, __amdgpu_buffer_rsrc_t accr, __amdgpu_buffer_rsrc_t finr,
+                        bool has_acc, bool first, bool has_fin, int ld, int row, int col, float x) {
+        if (!blk.blocked) {
+            store1<TIn>(own, row * kBS + col, x);
+        } else if (has_acc) {
+            const int off = row * ld + col;
+            if (!first) x += load1<float>(accr, off);
+            if (has_fin)
+                store1<TIn>(finr, off, x);
+            else
+                store1<float>(accr, off, x);
+        }
+    };
 
     // Suffix state at the tile end: Z1^T[16 cb + 4 g + rr][16 w + lr], Y1[16 w + lr].
     const float* sr = suffix_records + (n * tiles + ti) * rec;
@@ -652,7 +697,8 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
         for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
-                store1<TOut>(dkr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dk[bj][rr]);
+                put_grad(dkr, akr, fkr, blk.acc_k != nullptr, blk.k_first, blk.fin_k != nullptr, ldq,
+                         r0 + 16 * bj + 4 * gq + rr, 16 * w + lr, dk[bj][rr]);
         // 4: dV[j][c] for c-block w.
         {
             f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -683,7 +729,8 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
                 dv[bj] = mfma3<kSplit>(ph, pl, gh, gl, dv[bj]);
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
-                    store1<TOut>(dvr, (r0 + 16 * bj + 4 * gq + rr) * kBS + 16 * w + lr, dv[bj][rr]);
+                    put_grad(dvr, avr, fvr, blk.acc_v != nullptr, blk.v_first, blk.fin_v != nullptr, ldv,
+                             r0 + 16 * bj + 4 * gq + rr, 16 * w + lr, dv[bj][rr]);
             }
         }
         // 5: the suffix state before this sub-chunk.
@@ -749,23 +796,18 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
 hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
-                                      const Problem& p, const BwdBlock& blk, bool fp32_parts,
-                                      hipStream_t stream) {
+                                      const Problem& p, const BwdBlock& blk, hipStream_t stream) {
     if (p.S != kBS || p.d != kBS || p.tile % kBC != 0) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
-#define RACE_DKV(TIN, TOUT)                                                                          \
-    causal_bwd_dkv_mfma_kernel<TIN, TOUT><<<grid, kThreads, BwdGeo<TIN>::kDkvLds, stream>>>(         \
+#define RACE_DKV(TIN)                                                                                \
+    causal_bwd_dkv_mfma_kernel<TIN><<<grid, kThreads, BwdGeo<TIN>::kDkvLds, stream>>>(               \
         static_cast<const TIN*>(q), static_cast<const TIN*>(k), static_cast<const TIN*>(v),         \
-        static_cast<const TIN*>(g), dq32, apre, suffix_records, static_cast<TOUT*>(dK),             \
-        static_cast<TOUT*>(dV), p.T, p.tile, p.tiles, p.rec, blk)
-    if (p.dtype == RACE_BF16) {
-        if (fp32_parts)
-            RACE_DKV(bf16_t, float);
-        else
-            RACE_DKV(bf16_t, bf16_t);
-    } else {
-        RACE_DKV(float, float);
-    }
+        static_cast<const TIN*>(g), dq32, apre, suffix_records, static_cast<TIN*>(dK),              \
+        static_cast<TIN*>(dV), p.T, p.tile, p.tiles, p.rec, blk)
+    if (p.dtype == RACE_BF16)
+        RACE_DKV(bf16_t);
+    else
+        RACE_DKV(float);
 #undef RACE_DKV
     return hipGetLastError();
 }

@@ -191,8 +191,8 @@ BwdLayout bwd_layout(const Problem& p) {
 // of dQ and, unless the caller hands in the forward's records, the forward
 // prefix records (last, so the two layouts share every other offset).
 struct CausalBwdLayout {
-    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0, parts = 0, acc = 0;
-    int64_t total() const { return bwd + apre + dq32 + fwd + parts + acc; }
+    int64_t bwd = 0, apre = 0, dq32 = 0, fwd = 0, acc = 0;
+    int64_t total() const { return bwd + apre + dq32 + fwd + acc; }
 };
 
 // Column groups of the vector-ALU causal backward: 1 where the state of
@@ -240,9 +240,9 @@ CausalBwdPlan plan_causal_bwd(const Problem& p, int kernel) {
 // Workspace of the causal backward: the forward prefix records unless given,
 // the suffix records (of one column group, or of one 64 x 64 block: the
 // groups and blocks take turns), the running mass every 16 tokens, dq32 (dQ,
-// or the current group's or block's part of it); with blocks the blocks' fp32
-// dK and dV parts and, for bf16 tokens, fp32 running sums of dQ, dK, dV; with
-// several column groups of bf16 tokens the running sums of dQ and dK.
+// or the current group's or block's part of it); with blocks of bf16 tokens
+// fp32 running sums of dQ, dK, dV; with several column groups of bf16 tokens
+// the running sums of dQ and dK.
 CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const CausalBwdPlan& pl) {
     CausalBwdLayout l;
     const int64_t NT = p.N * p.T;
@@ -251,7 +251,6 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
         l.bwd = p.N * p.tiles * record_floats(64, 64);
         l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
         l.dq32 = round64(NT * 64);
-        l.parts = 2 * round64(NT * 64);
         l.acc = p.dtype == RACE_BF16 ? 2 * round64(NT * p.S) + round64(NT * p.d) : 0;
         return l;
     }
@@ -281,50 +280,7 @@ __global__ void copy_floats_kernel(const float* src, float* dst, int64_t n) {
     if (i < n) dst[i] = src[i];
 }
 
-// One 64 x 64 block's fp32 part into its place: rows of 64 values of part
-// added to (or, first, written over) rows of `ld` values of dst, or written
-// to out (as TOut) instead of dst.  Four values per thread.
-template <typename TOut>
-__global__ void accumulate_block_kernel(const float* __restrict__ part, float* __restrict__ dst,
-                                        TOut* __restrict__ out, int64_t rows, int ld, int first) {
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= rows * 16) return;
-    const int64_t row = i >> 4;
-    const int c = 4 * int(i & 15);
-    float4 x = *reinterpret_cast<const float4*>(part + row * 64 + c);
-    const int64_t o = row * ld + c;
-    if (!first) {
-        const float4 y = *reinterpret_cast<const float4*>(dst + o);
-        x = make_float4(y.x + x.x, y.y + x.y, y.z + x.z, y.w + x.w);
-    }
-    if (!out) {
-        *reinterpret_cast<float4*>(dst + o) = x;
-    } else {
-        store_val(out + o, x.x);
-        store_val(out + o + 1, x.y);
-        store_val(out + o + 2, x.z);
-        store_val(out + o + 3, x.w);
-    }
-}
-
 // dst = src elementwise (a no-op when dst is null or is src).
-}  // namespace
-
-hipError_t launch_accumulate_block(const float* part, float* dst, void* out, int dtype, int64_t rows,
-                                   int ld, bool first, hipStream_t stream) {
-    if (rows <= 0) return hipSuccess;
-    const unsigned blocks = unsigned((rows * 16 + kThreads - 1) / kThreads);
-    if (out && dtype == RACE_BF16)
-        accumulate_block_kernel<bf16_t><<<blocks, kThreads, 0, stream>>>(part, dst, static_cast<bf16_t*>(out),
-                                                                         rows, ld, first ? 1 : 0);
-    else
-        accumulate_block_kernel<float><<<blocks, kThreads, 0, stream>>>(part, dst, static_cast<float*>(out),
-                                                                        rows, ld, first ? 1 : 0);
-    return hipGetLastError();
-}
-
-namespace {
-
 hipError_t copy_floats(const float* src, float* dst, int64_t n, hipStream_t stream) {
     if (n <= 0 || !dst || dst == src) return hipSuccess;
     copy_floats_kernel<<<unsigned((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(src, dst, n);
@@ -810,8 +766,7 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     float* apre = bwd_rec + l.bwd;
     float* dq32 = apre + l.apre;
     float* fwd_ws = dq32 + l.dq32;
-    float* parts = fwd_ws + l.fwd;
-    float* acc = parts + l.parts;
+    float* acc = fwd_ws + l.fwd;
     // B3 reads dQ back in fp32.  With one column group (or block) an fp32 dQ
     // is that copy: B1 writes it once, into the caller's buffer, and B3 reads
     // it from there.  With several, dq32 holds the current group's part.
@@ -846,26 +801,29 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p, stream, /*reverse=*/true));
         RACE_TRY(marks->mark(stream));
         RACE_TRY(launch_causal_bwd_dkv_mfma(probsQ, probsK, V, dOut, dq32, apre, bwd_rec, dK, dV, p,
-                                            blk, /*fp32_parts=*/false, stream));
+                                            blk, stream));
         return marks->mark(stream);
     }
     if (use_mfma) {
         // 64 x 64 blocks, bucket group m outer and value group h inner: dQ and
         // dK of group m are summed over h, dV of group h over m, in that fixed
         // order, in fp32 (the fp32 outputs themselves, or workspace for bf16
-        // outputs, whose last addend writes the caller's buffers).
+        // outputs, whose last addend writes the caller's buffers), inside the
+        // kernels.
         Problem pb = p;
         pb.S = pb.d = 64;
         pb.rec = record_floats(64, 64);
         const bool f32 = p.dtype == RACE_F32;
         const int64_t es = f32 ? 4 : 2, NT = p.N * p.T;
-        float* dk_part = parts;
-        float* dv_part = parts + round64(NT * 64);
         float* acc_q = f32 ? static_cast<float*>(dQ) : (dQ ? acc : nullptr);
         float* acc_k = f32 ? static_cast<float*>(dK) : (dK ? acc + round64(NT * p.S) : nullptr);
         float* acc_v = f32 ? static_cast<float*>(dV) : (dV ? acc + 2 * round64(NT * p.S) : nullptr);
+        auto col = [](void* base, int64_t c, int64_t es_) -> void* {
+            return base ? static_cast<void*>(static_cast<char*>(base) + c * es_) : nullptr;
+        };
         for (int m = 0; m < pl.mblocks; ++m) {
             for (int h = 0; h < pl.hblocks; ++h) {
+                const bool last_h = h == pl.hblocks - 1, last_m = m == pl.mblocks - 1;
                 BwdBlock blk;
                 blk.ldq = p.S;
                 blk.ldv = p.d;
@@ -874,39 +832,31 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
                 blk.fwd_d = p.d;
                 blk.fwd_a = int64_t(p.S) * p.d;
                 blk.fwd_rec = p.rec;
+                blk.blocked = 1;
+                blk.acc_q = acc_q ? acc_q + 64 * m : nullptr;
+                blk.acc_k = acc_k ? acc_k + 64 * m : nullptr;
+                blk.acc_v = acc_v ? acc_v + 64 * h : nullptr;
+                blk.q_first = h == 0;
+                blk.k_first = h == 0;
+                blk.v_first = m == 0;
+                if (!f32) {
+                    blk.fin_q = last_h ? col(dQ, 64 * m, es) : nullptr;
+                    blk.fin_k = last_h ? col(dK, 64 * m, es) : nullptr;
+                    blk.fin_v = last_m ? col(dV, 64 * h, es) : nullptr;
+                }
                 const void* qb = static_cast<const char*>(probsQ) + 64 * m * es;
                 const void* kb = static_cast<const char*>(probsK) + 64 * m * es;
                 const void* vb = static_cast<const char*>(V) + 64 * h * es;
                 const void* gb = static_cast<const char*>(dOut) + 64 * h * es;
-                const bool last_h = h == pl.hblocks - 1, last_m = m == pl.mblocks - 1;
                 RACE_TRY(launch_causal_bwd_dq_mfma(qb, kb, vb, gb, nullptr, dq32, apre, fwd_rec, bwd_rec,
                                                    pb, blk, stream));
                 RACE_TRY(marks->mark(stream));
-                if (acc_q) {
-                    void* out = (!f32 && last_h) ? static_cast<char*>(dQ) + 64 * m * es : nullptr;
-                    RACE_TRY(launch_accumulate_block(dq32, acc_q + 64 * m, out, p.dtype, NT, p.S, h == 0,
-                                                     stream));
-                    RACE_TRY(marks->mark(stream));
-                }
                 if (!dK && !dV) continue;
                 RACE_TRY(launch_tile_scan(bwd_rec, nullptr, pb, stream, /*reverse=*/true));
                 RACE_TRY(marks->mark(stream));
-                RACE_TRY(launch_causal_bwd_dkv_mfma(qb, kb, vb, gb, dq32, apre, bwd_rec,
-                                                    dK ? dk_part : nullptr, dV ? dv_part : nullptr, pb,
-                                                    blk, /*fp32_parts=*/true, stream));
+                RACE_TRY(launch_causal_bwd_dkv_mfma(qb, kb, vb, gb, dq32, apre, bwd_rec, nullptr, nullptr,
+                                                    pb, blk, stream));
                 RACE_TRY(marks->mark(stream));
-                if (acc_k) {
-                    void* out = (!f32 && last_h) ? static_cast<char*>(dK) + 64 * m * es : nullptr;
-                    RACE_TRY(launch_accumulate_block(dk_part, acc_k + 64 * m, out, p.dtype, NT, p.S,
-                                                     h == 0, stream));
-                    RACE_TRY(marks->mark(stream));
-                }
-                if (acc_v) {
-                    void* out = (!f32 && last_m) ? static_cast<char*>(dV) + 64 * h * es : nullptr;
-                    RACE_TRY(launch_accumulate_block(dv_part, acc_v + 64 * h, out, p.dtype, NT, p.d,
-                                                     m == 0, stream));
-                    RACE_TRY(marks->mark(stream));
-                }
             }
         }
         return RACE_SUCCESS;

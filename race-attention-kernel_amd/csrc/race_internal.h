@@ -204,12 +204,26 @@ hipError_t launch_causal_bwd_dkv(const void* q, const void* k, const void* v, co
 // group h), 32-token sub-chunks, the same buffers as the vector-ALU kernels.
 // With fp32 tokens the dQ kernel writes dQ only through dq32 (dQ must be null).
 struct BwdBlock {
-    int ldq = 64;          // row stride of probsQ and probsK (the full S)
-    int ldv = 64;          // row stride of V and dOut (the full d)
+    int ldq = 64;          // row stride of probsQ, probsK, dQ and dK (the full S)
+    int ldv = 64;          // row stride of V, dOut and dV (the full d)
     int s0 = 0, c0 = 0;    // the block's first bucket and value column
     int fwd_d = 64;        // row length of B in the forward records (the full d)
     int64_t fwd_a = 4096;  // offset of A in a forward record (full S * full d)
     int64_t fwd_rec = 0;   // stride of the forward records
+    // Several blocks (blocked = 1): fp32 running sums of dQ, dK (rows of ldq)
+    // and dV (rows of ldv), at the block's first column, to which the kernels
+    // add the block's part (the first addend writes them; a null sum is a
+    // gradient not asked for); with fin_* set, the last addend goes to the
+    // caller's gradient (dtype, same strides) instead.  One block (blocked =
+    // 0): the gradients are written as they are.
+    int blocked = 0;
+    float* acc_q = nullptr;
+    float* acc_k = nullptr;
+    float* acc_v = nullptr;
+    void* fin_q = nullptr;
+    void* fin_k = nullptr;
+    void* fin_v = nullptr;
+    int q_first = 1, k_first = 1, v_first = 1;
 };
 // Shapes the blocks cover: S in {64, 128, 256}, d in {64, 128}.
 bool causal_bwd_mfma_supported(int S, int d);
@@ -222,18 +236,12 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
                                      float* bwd_records, const Problem& p, const BwdBlock& blk,
                                      hipStream_t stream);
-// dK and dV (rows of 64): the caller's gradients, or with fp32_parts the
-// block's fp32 parts for bf16 tokens.
+// dK and dV: the caller's gradients (one block, rows of 64), or through the
+// block's running sums.
 hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
-                                      const Problem& p, const BwdBlock& blk, bool fp32_parts,
-                                      hipStream_t stream);
-// dst (rows of ld values, from its first column) += part (rows of 64 fp32
-// values), over rows x 64: with `first` dst = part; the result goes to out
-// (dtype, rows of ld) instead of dst when out is given.  Elementwise.
-hipError_t launch_accumulate_block(const float* part, float* dst, void* out, int dtype, int64_t rows,
-                                   int ld, bool first, hipStream_t stream);
+                                      const Problem& p, const BwdBlock& blk, hipStream_t stream);
 // The forward's tile sums (K1) on the matrix cores for the shapes
 // mfma_causal_supported takes, into records of p.rec floats.
 hipError_t launch_tile_sums_mfma(const void* k, const void* v, float* records, const Problem& p,
