@@ -577,9 +577,17 @@ hipError_t launch_hashed_shape(const HashedArgs& a, const Problem& p, hipStream_
     if constexpr (!kp_ok(S, KP)) {
         return hipErrorInvalidValue;
     } else if constexpr (S == 64 && D == 64) {
-        // Three workgroups per CU (a fourth would spill), rows double-buffered,
-        // 64-token sub-chunks for the tile sums.
-        return launch_hashed_family<TIn, 64, 64, 32, KP, 3, 4, 64, true>(a, p, stream, marks);
+        // bf16 rows, where the output pass's LDS allows four workgroups per CU
+        // (at most 40 KB each): four, rows single-buffered (double-buffered
+        // they would spill).  Otherwise three workgroups per CU (a fourth
+        // would spill), rows double-buffered.  64-token sub-chunks for the
+        // tile sums either way.
+        constexpr bool kFour = !std::is_same<TIn, float>::value &&
+                               hashed_output_lds<TIn, 64, 64, 32, KP, 4, true>() <= kMaxLds / 4;
+        if constexpr (kFour)
+            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false>(a, p, stream, marks);
+        else
+            return launch_hashed_family<TIn, 64, 64, 32, KP, 3, 4, 64, true>(a, p, stream, marks);
     } else if constexpr (S == 256 && D == 128) {
         return launch_hashed_family<TIn, 256, 128, 32, KP, 1, 8>(a, p, stream, marks);
     } else {
