@@ -95,6 +95,17 @@ BWD_PHASES = {
 }
 
 
+def noncausal_bwd_phases(S: int, d: int, tiles: int) -> list:
+    """The non-causal backward's launches as race_api.hip issues them: at
+    S = d = 64 the query side and the key side, with the finalize between
+    them past NONCAUSAL_FOLD_TILES tiles per stream; the five passes
+    otherwise."""
+    if S == 64 and d == 64:
+        mid = ["bwd_finalize"] if tiles > NONCAUSAL_FOLD_TILES else []
+        return ["query_grad"] + mid + ["key_grad"]
+    return BWD_PHASES[False]
+
+
 class HipEvents:
     """hipEvent_t handles from the HIP runtime torch already loaded."""
 
@@ -190,6 +201,8 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
         "bwd_finalize": state + small,             # dE tile records, state -> dB, dA
         "token_map_dk": es * (d + S) * NT,
         "token_map_dv": es * (S + d) * NT,
+        "query_grad": es * (2 * S + d) * NT,       # q, dOut -> dQ (and the dE records)
+        "key_grad": es * (2 * S + 2 * d) * NT,     # k, v -> dK, dV
         "hash_q": es * (d + S) * NT,               # rows of d_k = d -> probabilities
         "hash_k": es * (d + S) * NT,
         "hashed_sums": es * 2 * d * NT,            # K rows, V (hashing inside)
@@ -732,7 +745,7 @@ def measure(args, T: int) -> dict:
     if run_fwd:
         names += fwd_names
     if run_bwd:
-        names += BWD_PHASES[cfg.causal]
+        names += BWD_PHASES[True] if cfg.causal else noncausal_bwd_phases(cfg.S, cfg.d, tiles)
 
     if args.calibrate_copy:
         # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE counters give

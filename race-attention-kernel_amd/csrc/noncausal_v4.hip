@@ -318,6 +318,10 @@ __device__ __forceinline__ float sum_parts(const float* __restrict__ p, int part
     return v;
 }
 
+// Parts (tile records) a slice stages with every load in flight at once: the
+// non-causal forward folds at most this many per stream.
+constexpr int kSliceParts = 4;
+
 // Ms[a][c] = M[a][c0 + c] of the map operand for stream n (divided by its
 // divisor when it has one) for the slice's columns c < ncols, zero beyond,
 // a < Wa; the first token block's workgroups also save the undivided values
@@ -335,11 +339,39 @@ __device__ __forceinline__ void stage_slice(float* __restrict__ Ms, const MapOpe
     float* sv = op.save && blockIdx.x == 0 ? op.save + n * op.save_stream : nullptr;
     for (int ab = 0; ab < Wa; ab += 8 * kRows) {
         float v[8], q[8];
+        if (op.parts <= kSliceParts) {
+            // Every part of the 8 rows is requested before the sums (a loop
+            // over the parts waited for each part in turn); the sums run in
+            // part order, as sum_parts adds them.
+            float vp[kSliceParts][8], qp[kSliceParts][8];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const int a = min(ab + a0 + m * kRows, Wa - 1);  // clamped: no branch
-            v[m] = sum_parts(col + a * op.row, op.parts, op.part_stride);
-            q[m] = dv ? sum_parts(dv + (op.div_by_col ? cg : a), op.parts, op.part_stride) : 0.f;
+            for (int t = 0; t < kSliceParts; ++t) {
+                const int64_t po = int64_t(min(t, op.parts - 1)) * op.part_stride;
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {
+                    const int a = min(ab + a0 + m * kRows, Wa - 1);  // clamped: no branch
+                    vp[t][m] = col[a * op.row + po];
+                    qp[t][m] = dv ? dv[(op.div_by_col ? cg : a) + po] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                v[m] = vp[0][m];
+                q[m] = qp[0][m];
+#pragma unroll
+                for (int t = 1; t < kSliceParts; ++t)
+                    if (t < op.parts) {
+                        v[m] += vp[t][m];
+                        q[m] += qp[t][m];
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const int a = min(ab + a0 + m * kRows, Wa - 1);
+                v[m] = sum_parts(col + a * op.row, op.parts, op.part_stride);
+                q[m] = dv ? sum_parts(dv + (op.div_by_col ? cg : a), op.parts, op.part_stride) : 0.f;
+            }
         }
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
@@ -557,6 +589,361 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// The backward at S = d = 64 in two passes, split the way the reference
+// splits its non-causal backward (src/noncausal/kernels/race_bwd.cu:4-28:
+// query side, bucket gradients, key side):
+//   query side  dQ[t][s] = sum_c G[t][c] E[s][c]   (G = dOut)
+//               dE[s][c] = sum_t Q[t][s] G[t][c]   (one record per tile)
+//   key side    dB = dE / (A + eps), dA[s] = -sum_c dE[s][c] E[s][c] / (A[s] + eps)
+//               dK[t][s] = sum_c V[t][c] dB[s][c] + dA[s],  dV[t][c] = sum_s K[t][s] dB[s][c]
+// so dOut is read once, and the bucket gradients are formed by every key-side
+// workgroup as it stages them (no separate finalize launch for up to
+// kFoldParts tiles per stream).
+//
+// Both kernels walk their tokens in stages of kGradStage rows of two tensors,
+// staged row-major in LDS with the next stage's rows in registers.  Map
+// thread (tt, cc) = (tid / 16, tid % 16) computes tokens tt + 16 r (r < 4)
+// and the 4 output columns 4 cc .. + 3; in a wave the four tt are adjacent
+// rows, so the 16-byte slot j of row i is stored at slot j ^ (i & 3) and the
+// four rows' reads fall in different banks.
+constexpr int kGradStage = 64;
+constexpr int kFoldParts = kKeyGradFoldParts;
+constexpr int kGradBlocks = 3;  // workgroups per CU the two passes are built for (LDS allows 3)
+
+// The slot of a stage row (16-byte slots XORed by row & 3).
+__device__ __forceinline__ int row_slot(int i, int j) { return j ^ (i & 3); }
+
+template <typename TIn>
+struct GradStage {
+    static constexpr int W = 64;
+    static constexpr int NV = kGradStage * (W / 4) / kThreads;  // 16-byte vectors per tensor and thread
+    float4 pa[NV], pb[NV];
+    __device__ __forceinline__ void fetch(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int r0) {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = threadIdx.x + m * kThreads;
+            const int i = e >> 4, v = e & 15;
+            pa[m] = buf_load4<TIn>(ra, ((r0 + i) * W + 4 * v) * int(sizeof(TIn)));
+        }
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = threadIdx.x + m * kThreads;
+            const int i = e >> 4, v = e & 15;
+            pb[m] = buf_load4<TIn>(rb, ((r0 + i) * W + 4 * v) * int(sizeof(TIn)));
+        }
+    }
+    // a rows plain (swizzle_a false) or swizzled, b rows swizzled.
+    template <bool kSwizzleA>
+    __device__ __forceinline__ void stash(float* __restrict__ as, float* __restrict__ bs) const {
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            const int e = threadIdx.x + m * kThreads;
+            const int i = e >> 4, v = e & 15;
+            store4(as + i * W + 4 * (kSwizzleA ? row_slot(i, v) : v), pa[m]);
+            store4(bs + i * W + 4 * row_slot(i, v), pb[m]);
+        }
+    }
+};
+
+// Query side: one workgroup per (tile, stream).  LDS: E transposed (pitch
+// kEtPitch), the stage's Q rows (plain) and G rows (swizzled).  Reduction:
+// threads 0..127 take tokens 0..15 of every 32, 128..255 tokens 16..31, each
+// an 8 x 4 tile of dE (rows 8 (u / 16) .., columns 4 (u % 16) .., u = tid %
+// 128), the two halves added in a fixed order at the end: outer64_kernel's
+// order, so the records are the same whichever kernel forms them.  A ragged last tile reads
+// zero rows past T (buffer views), which add nothing, and drops their stores.
+constexpr int kEtPitch = 68;
+
+template <typename TIn>
+__global__ __launch_bounds__(kThreads, kGradBlocks) void query_grad64_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ g, TIn* __restrict__ dq,
+    const float* __restrict__ state, float* __restrict__ records, int64_t T, int chunk,
+    int64_t chunks, int64_t rec) {
+    constexpr int W = 64, ST = kGradStage;
+    extern __shared__ float smem[];
+    float* Et = smem;                // [64 c][kEtPitch]: Et[c][s] = E[s][c]
+    float* qs = Et + W * kEtPitch;   // [ST][64]
+    float* gs = qs + ST * W;         // [ST][64], swizzled
+    float* part = qs;                // [64][64] after the loop
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y, ci = blockIdx.x;
+    const int64_t t_begin = ci * chunk;
+    const int rows = int(min(T, t_begin + chunk) - t_begin);
+    const int64_t es = sizeof(TIn);
+    const auto qr = mfma::make_rsrc(q + (n * T + t_begin) * W, int64_t(rows) * W * es);
+    const auto gr = mfma::make_rsrc(g + (n * T + t_begin) * W, int64_t(rows) * W * es);
+    const auto dr = mfma::make_rsrc(dq + (n * T + t_begin) * W, int64_t(rows) * W * es);
+
+    GradStage<TIn> st;
+    st.fetch(qr, gr, 0);
+    // E[s][c] = B[s][c] / (A[s] + eps) from the state, transposed into LDS:
+    // lane c of wave w takes rows s = w + 4 m (coalesced loads, all issued
+    // before the first division).
+    {
+        const int c = tid & 63, s0 = tid >> 6;
+        const float* sn = state + n * (W * W + W);
+        float b[16], a[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            b[m] = sn[(s0 + 4 * m) * W + c];
+            a[m] = sn[W * W + s0 + 4 * m];
+        }
+#pragma unroll
+        for (int m = 0; m < 16; ++m) Et[c * kEtPitch + s0 + 4 * m] = b[m] / (a[m] + kEps);
+    }
+
+    const int half = tid >> 7, u = tid & 127;
+    const int a8 = u >> 4, b4 = u & 15;
+    const int tt = tid >> 4, cc = tid & 15;
+    float acc[8][4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
+
+    for (int r0 = 0; r0 < rows; r0 += ST) {
+        __syncthreads();
+        st.template stash<false>(qs, gs);
+        __syncthreads();
+        if (r0 + ST < rows) st.fetch(qr, gr, r0 + ST);
+        // dE partial over this thread's 32 tokens of the stage: of each 32
+        // tokens, half 0 takes the first 16 and half 1 the next 16, in order
+        // (outer64_kernel's split, so the records agree bit for bit).  The
+        // next token's operands are read while the current token's products
+        // run (two register sets).
+#pragma unroll 2
+        for (int i = 0; i < ST / 2; i += 2) {
+            // Two tokens' operands are read before their products run.
+            float4 x0[2], x1[2], yv[2];
+#pragma unroll
+            for (int u2 = 0; u2 < 2; ++u2) {
+                const int ii = i + u2;
+                const int t = 32 * (ii >> 4) + 16 * half + (ii & 15);
+                x0[u2] = *reinterpret_cast<const float4*>(qs + t * W + 8 * a8);
+                x1[u2] = *reinterpret_cast<const float4*>(qs + t * W + 8 * a8 + 4);
+                yv[u2] = *reinterpret_cast<const float4*>(gs + t * W + 4 * row_slot(t, b4));
+            }
+#pragma unroll
+            for (int u2 = 0; u2 < 2; ++u2) {
+                const float xr[8] = {x0[u2].x, x0[u2].y, x0[u2].z, x0[u2].w,
+                                     x1[u2].x, x1[u2].y, x1[u2].z, x1[u2].w};
+                const float yc[4] = {yv[u2].x, yv[u2].y, yv[u2].z, yv[u2].w};
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(xr[r], yc[c], acc[r][c]);
+            }
+        }
+        // dQ for tokens tt + 16 r, buckets 4 cc .. + 3 (contraction over c in
+        // order, as the map kernels do).
+        float mo[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) mo[r][c] = 0.f;
+#pragma unroll 2
+        for (int j = 0; j < W / 4; ++j) {
+            // The group's eight operand vectors are read before its products.
+            float4 gv[4], ev[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                gv[r] = *reinterpret_cast<const float4*>(gs + (tt + 16 * r) * W + 4 * row_slot(tt, j));
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                ev[k] = *reinterpret_cast<const float4*>(Et + (4 * j + k) * kEtPitch + 4 * cc);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float ec[4] = {ev[k].x, ev[k].y, ev[k].z, ev[k].w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float gk = k == 0 ? gv[r].x : k == 1 ? gv[r].y : k == 2 ? gv[r].z : gv[r].w;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) mo[r][c] = fmaf(gk, ec[c], mo[r][c]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            buf_store4<TIn>(dr, ((r0 + tt + 16 * r) * W + 4 * cc) * int(es),
+                            make_float4(mo[r][0], mo[r][1], mo[r][2], mo[r][3]));
+    }
+
+    // dE = half 0 + half 1 into the tile's record (B part; A part unused).
+    float* rp = records + (n * chunks + ci) * rec;
+    __syncthreads();
+    if (half == 1) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            store4(part + (8 * a8 + r) * W + 4 * b4, make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]));
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const float4 o = *reinterpret_cast<const float4*>(part + (8 * a8 + r) * W + 4 * b4);
+            store4(rp + (8 * a8 + r) * W + 4 * b4,
+                   make_float4(acc[r][0] + o.x, acc[r][1] + o.y, acc[r][2] + o.z, acc[r][3] + o.w));
+        }
+    }
+}
+
+// Key side: one workgroup per (tile, stream).  LDS: dB [s][c] with the
+// 16-byte slot j of row s at j ^ ((s / 4) & 15) (the dK reads take rows
+// 4 cc .. + 3 for 16 cc at once, the dV reads whole rows: both spread over
+// the banks), dA [64], the stage's K and V rows (swizzled).  dB and dA come
+// from `parts` dE records (summed in order) and the state with the
+// arithmetic of bwd_finalize_kernel, or, with `ready`, from dB ([N][64][64])
+// and dA ([N][64]) formed by it.
+template <typename TIn>
+__global__ __launch_bounds__(kThreads, kGradBlocks) void key_grad64_kernel(
+    const TIn* __restrict__ k, const TIn* __restrict__ v, TIn* __restrict__ dk,
+    TIn* __restrict__ dv, const float* __restrict__ dE_records, int parts, int64_t rec,
+    const float* __restrict__ state, const float* __restrict__ dB_ready,
+    const float* __restrict__ dA_ready, int64_t T, int chunk) {
+    constexpr int W = 64, ST = kGradStage;
+    extern __shared__ float smem[];
+    float* dBs = smem;           // [64][64], swizzled
+    float* dAs = dBs + W * W;    // [64]
+    float* ks = dAs + W;         // [ST][64], swizzled
+    float* vs = ks + ST * W;     // [ST][64], swizzled
+    const int tid = threadIdx.x;
+    const int64_t n = blockIdx.y;
+    const int64_t t_begin = int64_t(blockIdx.x) * chunk;
+    const int rows = int(min(T, t_begin + chunk) - t_begin);
+    const int64_t es = sizeof(TIn);
+    const auto kr = mfma::make_rsrc(k + (n * T + t_begin) * W, int64_t(rows) * W * es);
+    const auto vr = mfma::make_rsrc(v + (n * T + t_begin) * W, int64_t(rows) * W * es);
+    const auto dkr = mfma::make_rsrc(dk + (n * T + t_begin) * W, int64_t(rows) * W * es);
+    const auto dvr = mfma::make_rsrc(dv + (n * T + t_begin) * W, int64_t(rows) * W * es);
+    auto db_at = [](int s, int c) { return s * W + 4 * ((c >> 2) ^ ((s >> 2) & 15)) + (c & 3); };
+
+    GradStage<TIn> st;
+    st.fetch(kr, vr, 0);
+    {
+        // Lane c of wave w forms rows s = w + 4 m.
+        const int c = tid & 63, s0 = tid >> 6;
+        if (dB_ready) {
+            const float* bn = dB_ready + n * W * W;
+            float b[16], a[16];
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                b[m] = bn[(s0 + 4 * m) * W + c];
+                a[m] = dA_ready[n * W + s0 + 4 * m];
+            }
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                dBs[db_at(s0 + 4 * m, c)] = b[m];
+                if (c == 0) dAs[s0 + 4 * m] = a[m];
+            }
+        } else {
+            const float* sn = state + n * (W * W + W);
+            const float* rn = dE_records + n * int64_t(parts) * rec;
+            // Four rows at a time: every part, B and A value requested before
+            // the sums.
+#pragma unroll
+            for (int mb = 0; mb < 16; mb += 4) {
+                float gp[kFoldParts][4], b[4], a[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int s = s0 + 4 * (mb + m);
+#pragma unroll
+                    for (int p = 0; p < kFoldParts; ++p)
+                        gp[p][m] = rn[int64_t(min(p, parts - 1)) * rec + s * W + c];
+                    b[m] = sn[s * W + c];
+                    a[m] = sn[W * W + s];
+                }
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int s = s0 + 4 * (mb + m);
+                    float gs = 0.f;
+#pragma unroll
+                    for (int p = 0; p < kFoldParts; ++p)
+                        if (p < parts) gs += gp[p][m];
+                    const float den = a[m] + kEps;
+                    const float e = b[m] / den;
+                    dBs[db_at(s, c)] = gs / den;
+                    float dsum = fmaf(0.f, 0.f, gs * e);
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
+                    if (c == 0) dAs[s] = -dsum / den;
+                }
+            }
+        }
+    }
+
+    const int tt = tid >> 4, cc = tid & 15;
+    for (int r0 = 0; r0 < rows; r0 += ST) {
+        __syncthreads();
+        st.template stash<true>(ks, vs);
+        __syncthreads();
+        if (r0 + ST < rows) st.fetch(kr, vr, r0 + ST);
+        // dK[t][4 cc + i] = dA + sum_c V[t][c] dB[4 cc + i][c], c in order.
+        float ok[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float bias = dAs[4 * cc + i];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ok[r][i] = bias;
+        }
+#pragma unroll 2
+        for (int j = 0; j < W / 4; ++j) {
+            float4 xv[4], bv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xv[r] = *reinterpret_cast<const float4*>(vs + (tt + 16 * r) * W + 4 * row_slot(tt, j));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                bv[i] = *reinterpret_cast<const float4*>(dBs + (4 * cc + i) * W + 4 * (j ^ cc));
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = kk == 0 ? xv[r].x : kk == 1 ? xv[r].y : kk == 2 ? xv[r].z : xv[r].w;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float b = kk == 0 ? bv[i].x : kk == 1 ? bv[i].y : kk == 2 ? bv[i].z : bv[i].w;
+                        ok[r][i] = fmaf(x, b, ok[r][i]);
+                    }
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            buf_store4<TIn>(dkr, ((r0 + tt + 16 * r) * W + 4 * cc) * int(es),
+                            make_float4(ok[r][0], ok[r][1], ok[r][2], ok[r][3]));
+        // dV[t][4 cc + c] = sum_s K[t][s] dB[s][4 cc + c], s in order.
+        float ov[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ov[r][c] = 0.f;
+#pragma unroll 2
+        for (int j = 0; j < W / 4; ++j) {
+            float4 xv[4], bv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xv[r] = *reinterpret_cast<const float4*>(ks + (tt + 16 * r) * W + 4 * row_slot(tt, j));
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                bv[kk] = *reinterpret_cast<const float4*>(dBs + (4 * j + kk) * W + 4 * (cc ^ j));
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float bc[4] = {bv[kk].x, bv[kk].y, bv[kk].z, bv[kk].w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = kk == 0 ? xv[r].x : kk == 1 ? xv[r].y : kk == 2 ? xv[r].z : xv[r].w;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) ov[r][c] = fmaf(x, bc[c], ov[r][c]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            buf_store4<TIn>(dvr, ((r0 + tt + 16 * r) * W + 4 * cc) * int(es),
+                            make_float4(ov[r][0], ov[r][1], ov[r][2], ov[r][3]));
+    }
+}
+
 int pow2_at_least(int x) {
     int m = 1;
     while (m < x) m *= 2;
@@ -617,6 +1004,46 @@ hipError_t launch_outer_sums4(const void* x, const void* y, float* records, cons
 #undef RACE_OS4_NV
 #undef RACE_OS4_NT
 #undef RACE_OS4
+    return hipGetLastError();
+}
+
+size_t query_grad64_lds_bytes() {
+    return size_t(64 * kEtPitch + 2 * kGradStage * 64) * sizeof(float);
+}
+size_t key_grad64_lds_bytes() { return size_t(64 * 64 + 64 + 2 * kGradStage * 64) * sizeof(float); }
+
+hipError_t launch_query_grad64(const void* q, const void* g, void* dq, const float* state,
+                               float* records, const Problem& p, hipStream_t stream) {
+    if (p.S != 64 || p.d != 64) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    const size_t lds = query_grad64_lds_bytes();
+    if (p.dtype == RACE_BF16)
+        query_grad64_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+            static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dq),
+            state, records, p.T, p.tile, p.tiles, p.rec);
+    else
+        query_grad64_kernel<float><<<grid, kThreads, lds, stream>>>(
+            static_cast<const float*>(q), static_cast<const float*>(g), static_cast<float*>(dq),
+            state, records, p.T, p.tile, p.tiles, p.rec);
+    return hipGetLastError();
+}
+
+hipError_t launch_key_grad64(const void* k, const void* v, void* dk, void* dv,
+                             const float* dE_records, const float* state, const float* dB_ready,
+                             const float* dA_ready, const Problem& p, hipStream_t stream) {
+    if (p.S != 64 || p.d != 64) return hipErrorInvalidValue;
+    if (!dB_ready && (p.tiles > kKeyGradFoldParts || !dE_records || !state)) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    const size_t lds = key_grad64_lds_bytes();
+    const int parts = int(p.tiles);
+    if (p.dtype == RACE_BF16)
+        key_grad64_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+            static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v), static_cast<bf16_t*>(dk),
+            static_cast<bf16_t*>(dv), dE_records, parts, p.rec, state, dB_ready, dA_ready, p.T, p.tile);
+    else
+        key_grad64_kernel<float><<<grid, kThreads, lds, stream>>>(
+            static_cast<const float*>(k), static_cast<const float*>(v), static_cast<float*>(dk),
+            static_cast<float*>(dv), dE_records, parts, p.rec, state, dB_ready, dA_ready, p.T, p.tile);
     return hipGetLastError();
 }
 

@@ -529,9 +529,33 @@ race_status noncausal_bwd_impl(const void* probsQ, const void* probsK, const voi
     const int64_t state_stride = Sd + p.S;
 
     RACE_TRY(marks->mark(stream));
+    // S = d = 64: the query side (dQ and the dE records, dOut read once) and,
+    // with both dK and dV asked for, the key side each in one pass; the key
+    // side forms dB and dA itself from up to kKeyGradFoldParts records per
+    // stream, after the finalize otherwise.
+    const bool w64 = p.S == 64 && p.d == 64;
+    if (w64 && dQ && (dK || dV)) {
+        RACE_TRY(launch_query_grad64(probsQ, dOut, dQ, state, records, p, stream));
+        RACE_TRY(marks->mark(stream));
+    }
+    if (w64 && dK && dV) {
+        if (!dQ) {
+            RACE_TRY(outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
+            RACE_TRY(marks->mark(stream));
+        }
+        if (p.tiles <= kKeyGradFoldParts) {
+            RACE_TRY(launch_key_grad64(probsK, V, dK, dV, records, state, nullptr, nullptr, p, stream));
+        } else {
+            RACE_TRY(launch_bwd_finalize(records, state, dB, dA, p, stream));
+            RACE_TRY(marks->mark(stream));
+            RACE_TRY(launch_key_grad64(probsK, V, dK, dV, nullptr, nullptr, dB, dA, p, stream));
+        }
+        return marks->mark(stream);
+    }
+    const bool dE_done = w64 && dQ && (dK || dV);
     // dQ = dOut E^T: M[a = c][b = s] = E[s*d + c] = B[s*d + c] / (A[s] + eps),
     // read straight from the state.
-    if (dQ) {
+    if (dQ && !dE_done) {
         MapOperand op = map_operand(state, state_stride, 1, p.d);
         op.div = state + Sd;
         op.div_stream = state_stride;
@@ -542,8 +566,10 @@ race_status noncausal_bwd_impl(const void* probsQ, const void* probsK, const voi
     if (!dK && !dV) return RACE_SUCCESS;
     // dE = Q^T dOut as per-tile partials; the finalize adds them in a fixed
     // order.
-    RACE_TRY(outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
-    RACE_TRY(marks->mark(stream));
+    if (!dE_done) {
+        RACE_TRY(outer_sums(probsQ, dOut, records, p, p.S, p.d, stream));
+        RACE_TRY(marks->mark(stream));
+    }
     RACE_TRY(launch_bwd_finalize(records, state, dB, dA, p, stream));
     RACE_TRY(marks->mark(stream));
     // dK = V dB^T + dA: M[a = c][b = s] = dB[s*d + c].

@@ -154,6 +154,17 @@ hipError_t launch_outer_sums4(const void* x, const void* y, float* records, cons
 hipError_t launch_map4(const void* x, void* out, const MapOperand& op, const Problem& p, int Wa,
                        int Wb, hipStream_t stream);
 size_t map4_lds_bytes(int Wa);
+// The backward at S = d = 64 as a query-side pass (dQ, and the dE tile
+// records into `records`, one per tile of p.tile tokens) and a key-side pass
+// (dK, dV).  The key side forms dB and dA from the dE records and the state
+// itself for at most kKeyGradFoldParts tiles per stream (dB_ready null), or
+// reads them from dB_ready ([N][64][64]) and dA_ready ([N][64]).
+constexpr int kKeyGradFoldParts = 4;
+hipError_t launch_query_grad64(const void* q, const void* g, void* dq, const float* state,
+                               float* records, const Problem& p, hipStream_t stream);
+hipError_t launch_key_grad64(const void* k, const void* v, void* dk, void* dv,
+                             const float* dE_records, const float* state, const float* dB_ready,
+                             const float* dA_ready, const Problem& p, hipStream_t stream);
 
 // ---- causal backward (causal_bwd.hip): fp32 vector-ALU kernels ----
 

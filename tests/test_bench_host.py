@@ -43,3 +43,12 @@ def test_sweep_lengths_cover_cfg1_and_cfg2():
     b = load_bench()
     assert 4096 in b.CPU_SWEEP_T and b.CPU_SWEEP_T[-1] == 65536
     assert b.GPU_SWEEP_T == [512 << i for i in range(8)]
+
+
+def test_noncausal_backward_launch_names_follow_the_library():
+    # race_api.hip: at S = d = 64 the query side and the key side (with the
+    # finalize between them past 4 tiles per stream); five passes otherwise.
+    b = load_bench()
+    assert b.noncausal_bwd_phases(64, 64, 2) == ["query_grad", "key_grad"]
+    assert b.noncausal_bwd_phases(64, 64, 8) == ["query_grad", "bwd_finalize", "key_grad"]
+    assert b.noncausal_bwd_phases(256, 128, 2) == b.BWD_PHASES[False]

@@ -568,3 +568,110 @@ def test_sigma_writes_cover_each_token_plane_once(NPB):
         seen[lr * pitch + 16 * pb + 4 * g + r] += 1
     assert len(seen) == 16 * 16 * NPB and set(seen.values()) == {1}
     assert max(seen) < 16 * pitch
+
+
+# ---------------------------------------------------------------------------
+# noncausal_v4.hip: the S = d = 64 backward passes (query_grad64_kernel,
+# key_grad64_kernel).  Workgroup of 256 threads, stage of 64 rows of 64 fp32.
+
+def row_slot(i: int, j: int) -> int:
+    return j ^ (i & 3)
+
+
+def db_at(s: int, c: int) -> int:
+    """Float index of dB[s][c] in the key side's LDS tile."""
+    return s * 64 + 4 * ((c >> 2) ^ ((s >> 2) & 15)) + (c & 3)
+
+
+def groups16():
+    """The 16-lane groups of a workgroup (tid ranges served per LDS pass)."""
+    return [range(g, g + 16) for g in range(0, 256, 16)]
+
+
+def max_bank_load(addr_bytes) -> int:
+    """Worst bank load of one 16-lane group's 16-byte accesses (one address
+    read by several lanes is one access)."""
+    return max(bank_load((a, 16) for a in set(addr_bytes)).values())
+
+
+def test_stage_rows_are_staged_once_and_read_back():
+    # GradStage::stash: vector e = tid + 256 m holds row e / 16, slot e % 16.
+    seen = Counter()
+    for tid, m in itertools.product(range(256), range(4)):
+        e = tid + 256 * m
+        i, v = e >> 4, e & 15
+        seen[i * 64 + 4 * row_slot(i, v)] += 1
+    assert sorted(seen) == list(range(0, 64 * 64, 4)) and set(seen.values()) == {1}
+    # Reading slot row_slot(i, j) of row i returns columns 4 j .. 4 j + 3.
+    for i, j in itertools.product(range(64), range(16)):
+        v = [v for v in range(16) if row_slot(i, v) == row_slot(i, j)]
+        assert v == [j]
+
+
+def test_stage_stores_are_conflict_free():
+    for grp in groups16():
+        for m in range(4):
+            addrs = []
+            for tid in grp:
+                e = tid + 256 * m
+                i, v = e >> 4, e & 15
+                addrs.append(4 * (i * 64 + 4 * row_slot(i, v)))
+            assert max_bank_load(addrs) == 1
+
+
+def test_map_threads_cover_every_output_once():
+    # Thread (tt, cc) = (tid / 16, tid % 16): rows tt + 16 r, columns 4 cc ...
+    seen = Counter()
+    for tid, r, c in itertools.product(range(256), range(4), range(4)):
+        tt, cc = tid >> 4, tid & 15
+        seen[(tt + 16 * r, 4 * cc + c)] += 1
+    assert len(seen) == 64 * 64 and set(seen.values()) == {1}
+
+
+def test_reduction_tokens_follow_the_outer64_order():
+    # query_grad64_kernel: thread half h takes t = 32 (i / 16) + 16 h + i % 16;
+    # outer64_kernel stages 32-token blocks and half h takes tokens 16 h .. of
+    # each.  Same per-thread sequence, every token once per stage.
+    for h in range(2):
+        ours = [32 * (i >> 4) + 16 * h + (i & 15) for i in range(32)]
+        outer64 = [32 * b + 16 * h + i for b in range(2) for i in range(16)]
+        assert ours == outer64
+    both = sorted(32 * (i >> 4) + 16 * h + (i & 15) for h in range(2) for i in range(32))
+    assert both == list(range(64))
+
+
+@pytest.mark.parametrize("j", range(16))
+def test_operand_reads_are_conflict_free(j):
+    # Map operands: Et rows (pitch 68) and the key side's dB, both reads.
+    for grp in groups16():
+        for k in range(4):
+            et = [4 * ((4 * j + k) * 68 + 4 * (tid & 15)) for tid in grp]
+            assert max_bank_load(et) == 1
+            dv_b = [4 * (db_at(4 * j + k, 0) + 4 * ((tid & 15) ^ j)) for tid in grp]
+            assert max_bank_load(dv_b) == 1
+        for i in range(4):
+            dk_b = [4 * ((4 * (tid & 15) + i) * 64 + 4 * (j ^ (tid & 15))) for tid in grp]
+            assert max_bank_load(dk_b) == 1
+        # Stage rows for the maps (one row per group) and the reduction's G row.
+        for r in range(4):
+            assert max_bank_load([4 * (((tid >> 4) + 16 * r) * 64 + 4 * row_slot(tid >> 4, j)) for tid in grp]) == 1
+        t = 5
+        assert max_bank_load([4 * (t * 64 + 4 * row_slot(t, tid & 15)) for tid in grp]) == 1
+
+
+def test_db_tile_places_each_element_once_and_the_reads_find_it():
+    assert sorted(db_at(s, c) for s in range(64) for c in range(64)) == list(range(64 * 64))
+    for s, c in itertools.product(range(64), range(64)):
+        j, cc, i = c >> 2, s >> 2, s & 3
+        # dK read of row 4 cc + i at slot j ^ cc; dV read of row s at slot (c >> 2) ^ (s >> 2).
+        assert db_at(s, c) == (4 * cc + i) * 64 + 4 * (j ^ cc) + (c & 3)
+        assert db_at(s, c) == s * 64 + 4 * ((c >> 2) ^ (s >> 2)) + (c & 3)
+
+
+def test_operand_tiles_without_their_layout_conflict():
+    # Planted mistakes: an unswizzled dB (the dK read of 16 rows at one slot)
+    # and E transposed at pitch 64 (the prologue's column writes).
+    grp = range(16)
+    assert max_bank_load([4 * ((4 * tid + 0) * 64 + 4 * 3) for tid in grp]) == 16
+    assert max(bank_load((4 * (c * 64 + 7), 4) for c in grp).values()) == 16
+    assert max(bank_load((4 * (c * 68 + 7), 4) for c in grp).values()) == 1
