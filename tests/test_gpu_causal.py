@@ -65,6 +65,23 @@ def test_shapes_and_ragged_lengths(race, ext, oracle, cuda, kernel, dtype, L, R,
     assert per_stream_rel_err(to_np(out), ref) <= tol_for(dtype)
 
 
+@pytest.mark.parametrize("T, tile", [(1, 64), (31, 64), (33, 64), (95, 64), (96, 128), (1000, 64),
+                                     (1000, 128), (4097, 2048), (5000, 1024)])
+def test_s256_bf16_sub_chunks_and_tiles(race, ext, oracle, cuda, T, tile):
+    # S = 256, d = 128, bf16 (the cfg5 shape's eight-wave workgroup output
+    # pass, 32-token sub-chunks): ragged last sub-chunks, one-sub-chunk tiles
+    # and several tiles per stream, against the oracle and against the fp32
+    # path on the same values.
+    skip_unless_kernel(ext, "mfma_wg", 8, 32, 128)
+    say("s256 bf16", T, tile)
+    q, k, v = race.make_inputs(2, T, 8, 32, 128, seed=T + 3 * tile, dtype=torch.bfloat16)
+    out = run(race, q.to(cuda), k.to(cuda), v.to(cuda), "mfma_wg", tile)
+    ref = oracle.causal_recurrence(to_np(q), to_np(k), to_np(v))
+    assert per_stream_rel_err(to_np(out), ref) <= tol_for(torch.bfloat16)
+    f32 = run(race, q.float().to(cuda), k.float().to(cuda), v.float().to(cuda), "mfma_wg", tile)
+    assert per_stream_rel_err(to_np(out), to_np(f32).astype(np.float64)) <= tol_for(torch.bfloat16)
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 127, 129, 2047, 2049, 3 * 2048 + 17, 10000])
 def test_forced_tile_lengths_agree(race, ext, oracle, cuda, kernel, T):
