@@ -138,7 +138,7 @@ __device__ __forceinline__ void split8v(const f32x4& a, const f32x4& b, bf16x8& 
 // at every sub-chunk start, and the tile's suffix totals Z = sum W (x) g,
 // Y = sum alpha into its record.  For fp32 tokens the fp32 copy is the only
 // dQ output (the caller passes its dQ as dq32 and no dQ).
-template <typename TIn>
+template <typename TIn, bool kSums>
 __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
@@ -245,6 +245,24 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     // The fp32 tile's 16-byte chunks go to dq32 as they are and, for bf16
     // tokens, to dQ as 8-byte bf16 chunks (chunk q holds elements 4 q .. 4 q + 3
     // of the row-major tile).
+    // dQ's running sum over the rows of the sub-chunk being computed,
+    // requested with its tokens and added at the flush one sub-chunk later
+    // (read where it is added, every flush waited a full memory round trip).
+    constexpr int kAccPer = T32::template Chunks<kThreads>::kPer;
+    f32x4 aq_next[kAccPer], aq_cur[kAccPer];
+    // (The first addend reads nothing: an empty view returns zeros.)
+    const __amdgpu_buffer_rsrc_t aq_rd = make_rsrc(blk.acc_q && !blk.q_first ? blk.acc_q + base * ldq : nullptr,
+                                                   blk.acc_q && !blk.q_first ? int64_t(rows) * ldq * 4 : 0);
+    auto load_acc_q = [&](int r0) {
+#pragma unroll
+        for (int i = 0; i < kAccPer; ++i) {
+            const int qi = tid + i * kThreads;
+            const int off = (r0 + (qi >> 4)) * ldq + 4 * (qi & 15);
+            aq_next[i] = __builtin_bit_cast(f32x4, buf_load16<kPolicyDefault>(aq_rd, off * 4));
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < kAccPer; ++i) aq_next[i] = aq_cur[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto flush = [&](int r0) {
         typename T32::template Chunks<kThreads> c32;
         T32::template read<kThreads>(D32s, c32);
@@ -262,7 +280,7 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
             }
         }
         T32::template write<kPolicyDefault, kThreads>(c32, d32r, r0);
-        if (blk.blocked && blk.acc_q) {
+        if (kSums && blk.acc_q) {
             // The block's part into dQ's running sum (rows outside the tile,
             // and all rows of the first flush, fall outside the views).
 #pragma unroll
@@ -270,7 +288,7 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
                 const int qi = tid + i * kThreads;
                 const int off = (r0 + (qi >> 4)) * ldq + 4 * (qi & 15);
                 f32x4 t = __builtin_bit_cast(f32x4, c32.x[i]);
-                if (!blk.q_first) t = t + __builtin_bit_cast(f32x4, buf_load16<kPolicyDefault>(aqr, off * 4));
+                if (!blk.q_first) t = t + aq_cur[i];
                 if (blk.fin_q)
                     store4<TIn, kPolicyDefault>(fqr, off * es, t);
                 else
@@ -292,6 +310,11 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
             for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
         stage_load(r0 + kBC);  // past the tile: zeros, never used
         load_q(r0 + kBC);
+        if constexpr (kSums) {
+#pragma unroll
+            for (int i = 0; i < kAccPer; ++i) aq_cur[i] = aq_next[i];
+            load_acc_q(r0);
+        }
         // After the prefetch: a wait for those loads then leaves these stores
         // in flight (one counter covers both, in issue order).  Unconditional:
         // at r0 = 0 the offsets are negative, outside the buffer ranges, and
@@ -401,6 +424,10 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         }
     }
     __syncthreads();
+    if constexpr (kSums) {
+#pragma unroll
+        for (int i = 0; i < kAccPer; ++i) aq_cur[i] = aq_next[i];
+    }
     if (r0 > 0) flush(r0 - kBC);
 
     // Suffix totals of this tile: Z[s][c] (record layout B[s][c]) and Y[s].
@@ -434,7 +461,7 @@ __device__ __forceinline__ bf16x8 triu_frag(int off, int g, int lr) {
 //   3. dK = V Z1^T + M^T W + triu(1) alpha + Y1        (Z1^T from registers)
 //   4. dV = K Z1 + P^T G                                (Z1 from an LDS plane)
 //   5. Z1^T += G^T W, Y1 += 1^T alpha
-template <typename TIn>
+template <typename TIn, bool kSums>
 __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, const float* __restrict__ dq32, const float* __restrict__ apre,
@@ -482,18 +509,43 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
         blk.fin_v ? static_cast<TIn*>(blk.fin_v) + base * ldv : nullptr, blk.fin_v ? int64_t(rows) * ldv * es : 0);
     // One gradient value at (row, col): as it is (one block), or added to its
     // running sum (blocks).
+    // `sum` is the running sum at (row, col), prefetched with the sub-chunk's
+    // tokens (read where it is added, the loads waited a full memory round
+    // trip in every sub-chunk).
     auto put_grad = [&](__amdgpu_buffer_rsrc_t own, __amdgpu_buffer_rsrc_t accr, __amdgpu_buffer_rsrc_t finr,
-                        bool has_acc, bool first, bool has_fin, int ld, int row, int col, float x) {
-        if (!blk.blocked) {
+                        bool has_acc, bool first, bool has_fin, int ld, int row, int col, float x,
+                        float sum) {
+        if (!kSums) {
             store1<TIn>(own, row * kBS + col, x);
         } else if (has_acc) {
             const int off = row * ld + col;
-            if (!first) x += load1<float>(accr, off);
+            if (!first) x += sum;
             if (has_fin)
                 store1<TIn>(finr, off, x);
             else
                 store1<float>(accr, off, x);
         }
+    };
+    // Read views of the running sums (empty for a first addend: zeros).
+    const __amdgpu_buffer_rsrc_t ak_rd = make_rsrc(blk.acc_k && !blk.k_first ? blk.acc_k + base * ldq : nullptr,
+                                                   blk.acc_k && !blk.k_first ? int64_t(rows) * ldq * 4 : 0);
+    const __amdgpu_buffer_rsrc_t av_rd = make_rsrc(blk.acc_v && !blk.v_first ? blk.acc_v + base * ldv : nullptr,
+                                                   blk.acc_v && !blk.v_first ? int64_t(rows) * ldv * 4 : 0);
+    float ksum_n[2][4], vsum_n[2][4];
+    auto load_sums = [&](int r0) {
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = r0 + 16 * bj + 4 * gq + rr;
+                ksum_n[bj][rr] = load1<float>(ak_rd, row * ldq + 16 * w + lr);
+                // fp32 tokens: the dV sum is read where it is added (both
+                // prefetched, the fp32 kernel's registers spill).
+                if constexpr (!kSplit)
+                    vsum_n[bj][rr] = load1<float>(av_rd, row * ldv + 16 * w + lr);
+                else
+                    vsum_n[bj][rr] = 0.f;
+            }
     };
 
     // Suffix state at the tile end: Z1^T[16 cb + 4 g + rr][16 w + lr], Y1[16 w + lr].
@@ -561,22 +613,31 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     float a0n;
     stage_load(last);
     load_qd(last);
+    if constexpr (kSums) load_sums(last);
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+            if constexpr (!kSums) ksum_n[bj][rr] = vsum_n[bj][rr] = 0.f;
     a0n = ap[(last / kBC) * kBS];
     for (int r0 = last; r0 >= 0; r0 -= kBC) {
         __syncthreads();
         stage_store();
-        float qc[2][4], dc[2][4];
+        float qc[2][4], dc[2][4], ksum[2][4], vsum[2][4];
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 qc[bi][rr] = qreg[bi][rr];
                 dc[bi][rr] = dreg[bi][rr];
+                ksum[bi][rr] = ksum_n[bi][rr];
+                vsum[bi][rr] = vsum_n[bi][rr];
             }
         const float a0 = a0n;
         if (r0 > 0) {
             stage_load(r0 - kBC);
             load_qd(r0 - kBC);
+            if constexpr (kSums) load_sums(r0 - kBC);
             a0n = ap[(r0 / kBC - 1) * kBS];
         }
         // Z1 (the suffix state after this sub-chunk) as a plane for dV: row s,
@@ -698,7 +759,7 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
                 put_grad(dkr, akr, fkr, blk.acc_k != nullptr, blk.k_first, blk.fin_k != nullptr, ldq,
-                         r0 + 16 * bj + 4 * gq + rr, 16 * w + lr, dk[bj][rr]);
+                         r0 + 16 * bj + 4 * gq + rr, 16 * w + lr, dk[bj][rr], ksum[bj][rr]);
         // 4: dV[j][c] for c-block w.
         {
             f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -730,7 +791,9 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
                     put_grad(dvr, avr, fvr, blk.acc_v != nullptr, blk.v_first, blk.fin_v != nullptr, ldv,
-                             r0 + 16 * bj + 4 * gq + rr, 16 * w + lr, dv[bj][rr]);
+                             r0 + 16 * bj + 4 * gq + rr, 16 * w + lr, dv[bj][rr],
+                             kSplit ? load1<float>(av_rd, (r0 + 16 * bj + 4 * gq + rr) * ldv + 16 * w + lr)
+                                    : vsum[bj][rr]);
             }
         }
         // 5: the suffix state before this sub-chunk.
@@ -778,14 +841,16 @@ hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v
     if (p.dtype == RACE_BF16) {
         using G = BwdGeo<bf16_t>;
         const size_t lds = G::kDqLds;
-        causal_bwd_dq_mfma_kernel<bf16_t><<<grid, kThreads, lds, stream>>>(
+        auto kern = blk.blocked ? causal_bwd_dq_mfma_kernel<bf16_t, true> : causal_bwd_dq_mfma_kernel<bf16_t, false>;
+        kern<<<grid, kThreads, lds, stream>>>(
             static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
             static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ),
             dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec, blk);
     } else {
         using G = BwdGeo<float>;
         const size_t lds = G::kDqLds;
-        causal_bwd_dq_mfma_kernel<float><<<grid, kThreads, lds, stream>>>(
+        auto kern = blk.blocked ? causal_bwd_dq_mfma_kernel<float, true> : causal_bwd_dq_mfma_kernel<float, false>;
+        kern<<<grid, kThreads, lds, stream>>>(
             static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
             static_cast<const float*>(g), static_cast<float*>(dQ), dq32, apre, fwd_records,
             bwd_records, p.T, p.tile, p.tiles, p.rec, blk);
@@ -800,7 +865,8 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
     if (p.S != kBS || p.d != kBS || p.tile % kBC != 0) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
 #define RACE_DKV(TIN)                                                                                \
-    causal_bwd_dkv_mfma_kernel<TIN><<<grid, kThreads, BwdGeo<TIN>::kDkvLds, stream>>>(               \
+    (blk.blocked ? causal_bwd_dkv_mfma_kernel<TIN, true> : causal_bwd_dkv_mfma_kernel<TIN, false>)   \
+        <<<grid, kThreads, BwdGeo<TIN>::kDkvLds, stream>>>(                                          \
         static_cast<const TIN*>(q), static_cast<const TIN*>(k), static_cast<const TIN*>(v),         \
         static_cast<const TIN*>(g), dq32, apre, suffix_records, static_cast<TIN*>(dK),              \
         static_cast<TIN*>(dV), p.T, p.tile, p.tiles, p.rec, blk)
