@@ -43,7 +43,7 @@ line for that configuration; the CPU baseline belongs to the headline
 instead of the JSON line.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
-                       [--pass fwd|bwd|fwdbwd|module] [--T T] [--kernel auto|valu|mfma|mfma_wg]
+                       [--pass fwd|bwd|fwdbwd|module] [--T T] [--kernel auto|valu|mfma|mfma_wg|single]
                        [--tile N] [--no-cpu-baseline] [--no-max-t] [--sweep]
                        [--calibrate-copy MIB]
 """
@@ -84,6 +84,7 @@ PHASES = {
     (False, "valu"): ["tile_sums", "tile_reduce", "token_map"],
     (True, "mfma"): ["tile_sums_mfma", "tile_scan", "output_pass_mfma"],
     (True, "hashed"): ["hashed_sums", "tile_scan", "hashed_output"],
+    (True, "single"): ["single_arm", "single_pass"],
 }
 # Non-causal forwards with at most this many tiles per stream add the tile
 # records inside the map (no tile_reduce launch), as race_api.hip does.
@@ -165,7 +166,8 @@ def parse_args():
     ap.add_argument("--alg1-variant", choices=["fp32", "bf16"], default="bf16",
                     help="rounding variant of --pass alg1 (fp32-accurate or bf16 features)")
     ap.add_argument("--T", type=int, default=0)
-    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg", "decode"], default="auto")
+    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg", "decode", "single"],
+                    default="auto")
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-max-t", action="store_true",
@@ -190,6 +192,8 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
         "tile_reduce": state,
         "output_pass_valu": es * (2 * S + 2 * d) * NT,
         "output_pass_mfma": es * (2 * S + 2 * d) * NT,
+        "single_arm": 4.0 * cfg.N * tiles,         # zeroes one flag per tile
+        "single_pass": es * (2 * S + 2 * d) * NT,  # q, k, v read once -> out
         "token_map": es * (S + d) * NT,
         # backward: each launch's own operands (reads) and outputs (writes)
         "bwd_tile_sums": es * (S + d) * NT,
@@ -628,6 +632,8 @@ def measure(args, T: int) -> dict:
     if cfg.causal and (kernel_id in (2, 3) or (kernel_id == 0 and race.ops._lib.ext().shape_supported(
             cfg.L, cfg.R, cfg.d)[1])):
         family = "mfma"
+    if cfg.causal and kernel_id == race.ops.KERNELS["single"]:
+        family = "single"
     ws = torch.empty(max(ws_bytes // 4, 1), device=dev, dtype=torch.float32)
     out = torch.empty_like(v)
     stream = torch.cuda.current_stream().cuda_stream

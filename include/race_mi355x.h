@@ -75,7 +75,12 @@ typedef enum race_kernel {
     RACE_KERNEL_VALU = 1,
     RACE_KERNEL_MFMA = 2,
     RACE_KERNEL_MFMA_WG = 3,
-    RACE_KERNEL_DECODE = 4 /* race_fwd_carry only: the one-launch token-serial kernel */
+    RACE_KERNEL_DECODE = 4, /* race_fwd_carry only: the one-launch token-serial kernel */
+    /* Causal forward, S = d = 64, fp32 or bf16, N = 8 or 16, on an MI355X
+     * with all 256 CUs: one persistent launch that reads every operand once
+     * (tiles of 128 tokens; tile_tokens must be 0 or 128).  Anything else
+     * returns RACE_ERROR_INVALID_VALUE. */
+    RACE_KERNEL_SINGLE = 5
 } race_kernel;
 
 /* Shape of one call.  Mirrors CausalShape

@@ -54,10 +54,10 @@ int kernel_choice(const race_options* o) { return o ? o->kernel : RACE_KERNEL_AU
 race_status resolve_kernel(const race_shape* sh, int causal, const race_options* o, bool* mfma) {
     const int k = kernel_choice(o);
     if (k != RACE_KERNEL_AUTO && k != RACE_KERNEL_VALU && k != RACE_KERNEL_MFMA &&
-        k != RACE_KERNEL_MFMA_WG)
+        k != RACE_KERNEL_MFMA_WG && k != RACE_KERNEL_SINGLE)
         return RACE_ERROR_INVALID_VALUE;
     const bool has = causal && mfma_causal_supported(sub(sh), sh->head_dim);
-    const bool forced = k == RACE_KERNEL_MFMA || k == RACE_KERNEL_MFMA_WG;
+    const bool forced = k == RACE_KERNEL_MFMA || k == RACE_KERNEL_MFMA_WG || k == RACE_KERNEL_SINGLE;
     if (forced && !has) return RACE_ERROR_INVALID_VALUE;
     *mfma = forced || (k == RACE_KERNEL_AUTO && has);
     return RACE_SUCCESS;
@@ -101,6 +101,11 @@ int pow2_floor(int64_t x) {
 
 race_status resolve_tile(const race_shape* sh, int causal, const race_options* o, bool mfma,
                          int* tile) {
+    if (kernel_choice(o) == RACE_KERNEL_SINGLE) {
+        if (o->tile_tokens != 0 && o->tile_tokens != kSinglePassTile) return RACE_ERROR_INVALID_VALUE;
+        *tile = kSinglePassTile;
+        return RACE_SUCCESS;
+    }
     if (o && o->tile_tokens != 0) {
         if (o->tile_tokens < 0 || o->tile_tokens % RACE_SUB_CHUNK_TOKENS != 0)
             return RACE_ERROR_INVALID_VALUE;
@@ -151,6 +156,13 @@ race_status make_problem(const race_shape* sh, int causal, const race_options* o
     p->tile = tile;
     p->tiles = sh->seq_len == 0 ? 0 : (sh->seq_len + tile - 1) / tile;
     p->rec = record_floats(p->S, p->d);
+    if (p->kernel == RACE_KERNEL_SINGLE) {
+        int cus = 0;
+        const hipError_t err = cu_count(&cus);
+        if (err != hipSuccess) return err;
+        if (!causal || !single_pass_supported(*p, cus)) return RACE_ERROR_INVALID_VALUE;
+        p->single = true;
+    }
     return RACE_SUCCESS;
 }
 
@@ -158,13 +170,15 @@ race_status make_problem(const race_shape* sh, int causal, const race_options* o
 struct FwdLayout {
     int64_t records = 0;  // [N][tiles][rec]
     int64_t E = 0;        // non-causal: [N][S*d]
-    int64_t total() const { return records + E; }
+    int64_t words = 0;    // one-read causal forward: tile flags and control words (int32)
+    int64_t total() const { return records + E + words; }
 };
 
 FwdLayout fwd_layout(const Problem& p, int causal) {
     FwdLayout l;
     l.records = p.N * p.tiles * p.rec;
     if (!causal) l.E = round64(p.N * p.S * p.d);
+    if (p.single) l.words = single_pass_flag_words(p.N, p.tiles) + kSinglePassCtlWords;
     return l;
 }
 
@@ -410,6 +424,14 @@ race_status fwd_impl(const void* probsQ, const void* probsK, const void* V, void
     float* records = ws;
 
     if (causal) {
+        if (p.single) {
+            int cus = 0;
+            RACE_TRY(cu_count(&cus));
+            RACE_TRY(marks->mark(stream));
+            return launch_causal_single(probsQ, probsK, V, out, records,
+                                        reinterpret_cast<int*>(records + l.records), state, init, p,
+                                        cus, stream, marks);
+        }
         if (mfma) {
             RACE_TRY(marks->mark(stream));
             return launch_causal_mfma(probsQ, probsK, V, out, records, state, p, stream, marks);

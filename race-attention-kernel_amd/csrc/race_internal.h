@@ -52,6 +52,7 @@ struct Problem {
     int tile;        // tokens per tile (multiple of RACE_SUB_CHUNK_TOKENS)
     int64_t tiles;   // ceil(T / tile)
     int64_t rec;     // record_floats(S, d)
+    bool single = false;  // the one-read causal forward (single_pass.hip) runs
     // Causal forward continued from a carried state ([N][S*d+S], B then A):
     // the scan starts every stream from it instead of zero.  Null otherwise.
     const float* init = nullptr;
@@ -311,5 +312,21 @@ bool mfma_causal_supported(int S, int d);
 hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void* out,
                               float* records, float* state, const Problem& p, hipStream_t stream,
                               Marks* marks);
+
+// ---- One-read causal forward (single_pass.hip): S = d = 64 ----
+// Tiles of kSinglePassTile tokens; the workspace holds the records, then one
+// flag word per (stream, tile) (rounded up to 64 words), then the control
+// words (per-XCD ticket counters and an error word).
+constexpr int kSinglePassTile = 128;
+constexpr int64_t kSinglePassCtlWords = 64;
+inline int64_t single_pass_flag_words(int64_t N, int64_t tiles) { return ((N * tiles + 63) / 64) * 64; }
+// Shape and device conditions of the path (`cus`: the device's CU count).
+bool single_pass_supported(const Problem& p, int cus);
+// Zeroes the flag and control words, then one persistent launch of `cus`
+// workgroups.  `words` = records + N * tiles * rec.  The final state goes to
+// `state` when not null; `init` seeds the running sums when not null.
+hipError_t launch_causal_single(const void* q, const void* k, const void* v, void* out,
+                                float* records, int* words, float* state, const float* init,
+                                const Problem& p, int cus, hipStream_t stream, Marks* marks);
 
 }  // namespace race

@@ -30,7 +30,7 @@ from torch.autograd.function import once_differentiable
 
 from . import _lib
 
-KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3, "decode": 4}
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3, "decode": 4, "single": 5}
 
 
 def _kernel_id(kernel: str | int) -> int:
