@@ -69,6 +69,16 @@ struct BwdGeo {
     // staged the same way it measured slower (196 -> 260 us).
     static constexpr int kT32Bytes = kBC * kBS * 4;
     static constexpr int kDqLds = 3 * kRBytes + kMBytes + kT32Bytes;
+    // B1 over DV value columns (64, or all 128 of a d = 128 problem at once):
+    // V and G planes of DV columns, staged as (kBC / 4) (DV / E) blocks each.
+    template <int DV>
+    using PV = Plane<kSplit, DV>;
+    template <int DV>
+    static constexpr int kVBytes = kBC * PV<DV>::kPitch;
+    template <int DV>
+    static constexpr int kDqLdsV = kRBytes + 2 * kVBytes<DV> + kMBytes + kT32Bytes;
+    template <int DV>
+    static constexpr int kBlkV = (kBC / 4) * (DV / E);
     static constexpr int kDkvLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
     // Staging: blocks of 4 tokens x E features per tensor.
     static constexpr int kBlk = (kBC / 4) * (kBS / E);   // 128 (fp32) or 64 (bf16)
@@ -138,7 +148,7 @@ __device__ __forceinline__ void split8v(const f32x4& a, const f32x4& b, bf16x8& 
 // at every sub-chunk start, and the tile's suffix totals Z = sum W (x) g,
 // Y = sum alpha into its record.  For fp32 tokens the fp32 copy is the only
 // dQ output (the caller passes its dQ as dq32 and no dQ).
-template <typename TIn, bool kSums>
+template <typename TIn, bool kSums, int DV>
 __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     const TIn* __restrict__ g, TIn* __restrict__ dQ, float* __restrict__ dq32,
@@ -148,12 +158,16 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     using G = BwdGeo<TIn>;
     using PR = typename G::PR;
     using PM = typename G::PM;
+    using PV = typename G::template PV<DV>;  // V and G planes: DV value columns
     constexpr bool kSplit = G::kSplit;
+    constexpr int NCB = DV / 16;             // value column blocks
+    constexpr int NKV = DV / 32;             // contraction steps over the value columns
+    static_assert(DV == kBS || DV == 2 * kBS, "64 or 128 value columns");
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Ks = lds;
     unsigned char* Vs = Ks + G::kRBytes;
-    unsigned char* Gs = Vs + G::kRBytes;
-    unsigned char* Ms = Gs + G::kRBytes;
+    unsigned char* Gs = Vs + G::template kVBytes<DV>;
+    unsigned char* Ms = Gs + G::template kVBytes<DV>;
     unsigned char* D32s = Ms + G::kMBytes;
     using T32 = OutTile<float, kBS, kBC>;
 
@@ -182,9 +196,9 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][16 w + lr]
     // (the block's rows and columns of the forward record).
     const float* fr = fwd_records + (n * tiles + ti) * blk.fwd_rec;
-    f32x4 b0t[4], zt[4];
+    f32x4 b0t[NCB], zt[NCB];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             b0t[cb][rr] = fr[int64_t(blk.s0 + 16 * w + lr) * blk.fwd_d + blk.c0 + 16 * cb + 4 * gq + rr];
@@ -194,38 +208,48 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     float ypart = 0.f;
     const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
 
-    // Staging: this wave's tensor (K, V or G) and block.
-    const int nslots = (3 * G::kBlk + kThreads - 1) / kThreads;
-    auto slot_tensor = [&](int s) { return __builtin_amdgcn_readfirstlane((tid + s * kThreads) / G::kBlk); };
-    StageBlock<TIn> st[2];
+    // Staging: this wave's tensor (K, V or G) and block.  Slot e = tid +
+    // 256 s counts K's blocks, then V's, then G's (kBlkV each, DV wide);
+    // every boundary is a multiple of 64, so a wave stages one tensor.
+    constexpr int kBlkK = G::kBlk, kBlkV = G::template kBlkV<DV>;
+    constexpr int kSlots = (kBlkK + 2 * kBlkV + kThreads - 1) / kThreads;
+    static_assert(kBlkK % 64 == 0 && kBlkV % 64 == 0, "a wave stages one tensor");
+    auto slot_tensor = [&](int s) {
+        const int e = __builtin_amdgcn_readfirstlane(tid + s * kThreads - l);
+        return e < kBlkK ? 0 : e < kBlkK + kBlkV ? 1 : e < kBlkK + 2 * kBlkV ? 2 : 3;
+    };
+    auto slot_block = [&](int s, int tensor) {
+        const int e = tid + s * kThreads;
+        return tensor == 0 ? e : tensor == 1 ? e - kBlkK : e - kBlkK - kBlkV;
+    };
+    StageBlock<TIn> st[kSlots];
     auto stage_load = [&](int r0) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            if (s >= nslots) break;
+        for (int s = 0; s < kSlots; ++s) {
             const int tensor = slot_tensor(s);
             if (tensor >= 3) continue;
-            const int blk = (tid + s * kThreads) % G::kBlk;
-            const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
+            const int blk = slot_block(s, tensor);
             // One call per tensor: choosing the buffer and the row stride
             // with conditional expressions put the captured locals (and the
             // staging registers) in scratch memory, 3x slower.
             if (tensor == 0)
-                st[s].load(kr, r0, a, b, ldq);
+                st[s].load(kr, r0, blk / (kBS / G::E), blk % (kBS / G::E), ldq);
             else if (tensor == 1)
-                st[s].load(vr, r0, a, b, ldv);
+                st[s].load(vr, r0, blk / (DV / G::E), blk % (DV / G::E), ldv);
             else
-                st[s].load(gr, r0, a, b, ldv);
+                st[s].load(gr, r0, blk / (DV / G::E), blk % (DV / G::E), ldv);
         }
     };
     auto stage_store = [&]() {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            if (s >= nslots) break;
+        for (int s = 0; s < kSlots; ++s) {
             const int tensor = slot_tensor(s);
             if (tensor >= 3) continue;
-            const int blk = (tid + s * kThreads) % G::kBlk;
-            const int a = blk / (kBS / G::E), b = blk % (kBS / G::E);
-            st[s].template store_r<PR>(tensor == 0 ? Ks : tensor == 1 ? Vs : Gs, a, b);
+            const int blk = slot_block(s, tensor);
+            if (tensor == 0)
+                st[s].template store_r<PR>(Ks, blk / (kBS / G::E), blk % (kBS / G::E));
+            else
+                st[s].template store_r<PV>(tensor == 1 ? Vs : Gs, blk / (DV / G::E), blk % (DV / G::E));
         }
     };
     // Q at this lane's (i, s) positions.
@@ -351,10 +375,10 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         const int mbj = w == 2 ? 1 : 0, mbi = w >= 1 ? 1 : 0;
         if (w < 3) {
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
+            for (int kk = 0; kk < NKV; ++kk) {
                 bf16x8 ah, al, bh, bl;
-                PR::frag(Vs, 16 * mbj + lr, kk, gq, ah, al);
-                PR::frag(Gs, 16 * mbi + lr, kk, gq, bh, bl);
+                PV::frag(Vs, 16 * mbj + lr, kk, gq, ah, al);
+                PV::frag(Gs, 16 * mbi + lr, kk, gq, bh, bl);
                 mt = mfma3<kSplit>(ah, al, bh, bl, mt);
             }
             if (mbj == mbi) {
@@ -373,13 +397,13 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         // 3: U = G B0^T + M K;  dQ = r U;  alpha = -W dQ.
         f32x4 u[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < NKV; ++kk) {
             bf16x8 bh, bl;
             split8v<kSplit>(b0t[2 * kk], b0t[2 * kk + 1], bh, bl);
 #pragma unroll
             for (int bi = 0; bi < 2; ++bi) {
                 bf16x8 gh, gl;
-                PR::frag(Gs, 16 * bi + lr, kk, gq, gh, gl);
+                PV::frag(Gs, 16 * bi + lr, kk, gq, gh, gl);
                 u[bi] = mfma3<kSplit>(gh, gl, bh, bl, u[bi]);
             }
         }
@@ -410,16 +434,16 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         bf16x8 wh, wl;
         split8v<kSplit>(wv[0], wv[1], wh, wl);
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
+        for (int cb = 0; cb < NCB; ++cb) {
             bf16x8 gh, gl;
-            PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
+            PV::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
             zt[cb] = mfma3<kSplit>(gh, gl, wh, wl, zt[cb]);
         }
         // 5: B0^T += V^T K.
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
+        for (int cb = 0; cb < NCB; ++cb) {
             bf16x8 vh, vl;
-            PR::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
+            PV::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
             b0t[cb] = mfma3<kSplit>(vh, vl, kh, kl, b0t[cb]);
         }
     }
@@ -430,15 +454,22 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     }
     if (r0 > 0) flush(r0 - kBC);
 
-    // Suffix totals of this tile: Z[s][c] (record layout B[s][c]) and Y[s].
-    float* br = bwd_records + (n * tiles + ti) * rec;
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) br[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr] = zt[cb][rr];
+    // Suffix totals of this tile: Z[s][c] (record layout B[s][c]) and Y[s],
+    // one 64 x 64 record per value group h (records of group h start h N
+    // tiles records in); Y, the totals of alpha over all DV columns, goes to
+    // group 0's record and group 1's holds zero.
     float y = ypart + __shfl_xor(ypart, 16);
     y = y + __shfl_xor(y, 32);
-    if (gq == 0) br[kBS * kBS + 16 * w + lr] = y;
+#pragma unroll
+    for (int h = 0; h < DV / kBS; ++h) {
+        float* br = bwd_records + (int64_t(h) * gridDim.y * tiles + n * tiles + ti) * rec;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                br[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr] = zt[4 * h + cb][rr];
+        if (gq == 0) br[kBS * kBS + 16 * w + lr] = h == 0 ? y : 0.f;
+    }
 }
 
 // Upper-triangular ones as an A operand: element e of lane (g, lr) is
@@ -492,7 +523,9 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + base * ldq, int64_t(rows) * ldq * es);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + base * ldv, int64_t(rows) * ldv * es);
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(g + base * ldv, int64_t(rows) * ldv * es);
-    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+    // Without the alpha terms dQ is not read: an empty view returns zeros.
+    const __amdgpu_buffer_rsrc_t d32r =
+        make_rsrc(blk.alpha ? dq32 + base * kBS : nullptr, blk.alpha ? int64_t(rows) * kBS * 4 : 0);
     const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * kBS : nullptr,
                                                  dK ? int64_t(rows) * kBS * es : 0);
     const __amdgpu_buffer_rsrc_t dvr = make_rsrc(dV ? dV + base * kBS : nullptr,
@@ -555,7 +588,7 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) zt[cb][rr] = sr[(16 * w + lr) * kBS + 16 * cb + 4 * gq + rr];
-    float y1 = sr[kBS * kBS + 16 * w + lr];
+    float y1 = blk.alpha ? sr[kBS * kBS + 16 * w + lr] : 0.f;
     const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
     const bf16x8 up0 = triu_frag(0, gq, lr), up1 = triu_frag(16, gq, lr);
 
@@ -832,24 +865,36 @@ BwdBlock single_block(const Problem& p) {
 hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
                                      float* bwd_records, const Problem& p, const BwdBlock& blk,
-                                     hipStream_t stream) {
-    // p describes one 64 x 64 block (p.S = p.d = 64, p.rec its record).
+                                     hipStream_t stream, int dv) {
+    // p describes one 64 x 64 block (p.S = p.d = 64, p.rec its record); with
+    // dv = 128 the walk takes both value groups of a d = 128 problem (bf16,
+    // blocked) and writes one record array per group.
     if (p.S != kBS || p.d != kBS || p.tile % kBC != 0) return hipErrorInvalidValue;
+    if (dv != kBS && !(dv == 2 * kBS && p.dtype == RACE_BF16 && blk.blocked)) return hipErrorInvalidValue;
     // fp32: dQ is written only as the fp32 copy (pass the caller's dQ as dq32).
     if (p.dtype != RACE_BF16 && dQ) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     if (p.dtype == RACE_BF16) {
         using G = BwdGeo<bf16_t>;
-        const size_t lds = G::kDqLds;
-        auto kern = blk.blocked ? causal_bwd_dq_mfma_kernel<bf16_t, true> : causal_bwd_dq_mfma_kernel<bf16_t, false>;
+        if (dv == 2 * kBS) {
+            causal_bwd_dq_mfma_kernel<bf16_t, true, 2 * kBS><<<grid, kThreads, G::kDqLdsV<2 * kBS>, stream>>>(
+                static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ),
+                dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec, blk);
+            return hipGetLastError();
+        }
+        const size_t lds = G::kDqLdsV<kBS>;
+        auto kern = blk.blocked ? causal_bwd_dq_mfma_kernel<bf16_t, true, kBS>
+                                : causal_bwd_dq_mfma_kernel<bf16_t, false, kBS>;
         kern<<<grid, kThreads, lds, stream>>>(
             static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
             static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ),
             dq32, apre, fwd_records, bwd_records, p.T, p.tile, p.tiles, p.rec, blk);
     } else {
         using G = BwdGeo<float>;
-        const size_t lds = G::kDqLds;
-        auto kern = blk.blocked ? causal_bwd_dq_mfma_kernel<float, true> : causal_bwd_dq_mfma_kernel<float, false>;
+        const size_t lds = G::kDqLdsV<kBS>;
+        auto kern = blk.blocked ? causal_bwd_dq_mfma_kernel<float, true, kBS>
+                                : causal_bwd_dq_mfma_kernel<float, false, kBS>;
         kern<<<grid, kThreads, lds, stream>>>(
             static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
             static_cast<const float*>(g), static_cast<float*>(dQ), dq32, apre, fwd_records,

@@ -234,12 +234,17 @@ struct CausalBwdPlan {
     bool mfma = false;
     int mblocks = 1, hblocks = 1;  // bucket groups, value groups (matrix cores)
     int groups = 0, C = 0;         // column groups, sub-chunk (vector ALU)
+    bool bf16 = false;
     bool blocked() const { return mfma && mblocks * hblocks > 1; }
+    // bf16 with d = 128: one forward walk per bucket group over both value
+    // groups (its dQ whole; no dQ running sum).
+    bool wide() const { return blocked() && bf16 && hblocks == 2; }
 };
 
 CausalBwdPlan plan_causal_bwd(const Problem& p, int kernel) {
     CausalBwdPlan pl;
     pl.mfma = kernel != RACE_KERNEL_VALU && causal_bwd_mfma_supported(p.S, p.d) && p.tile % 32 == 0;
+    pl.bf16 = p.dtype == RACE_BF16;
     if (pl.mfma) {
         pl.mblocks = p.S / 64;
         pl.hblocks = p.d / 64;
@@ -262,7 +267,9 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
     const int64_t NT = p.N * p.T;
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
     if (pl.blocked()) {
-        l.bwd = p.N * p.tiles * record_floats(64, 64);
+        // One walk over both value groups (bf16, d = 128) keeps the suffix
+        // records of both groups.
+        l.bwd = (pl.wide() ? 2 : 1) * p.N * p.tiles * record_floats(64, 64);
         l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
         l.dq32 = round64(NT * 64);
         l.acc = p.dtype == RACE_BF16 ? 2 * round64(NT * p.S) + round64(NT * p.d) : 0;
@@ -869,6 +876,58 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         auto col = [](void* base, int64_t c, int64_t es_) -> void* {
             return base ? static_cast<void*>(static_cast<char*>(base) + c * es_) : nullptr;
         };
+        if (pl.wide()) {
+            // Per bucket group m: one forward walk over all 128 value columns
+            // (dQ of group m whole, straight to the caller's dQ; the suffix
+            // records of both value groups), one reverse scan of both record
+            // arrays, then the backward walk of each value group, the terms
+            // of alpha in group 0's.
+            Problem p2 = pb;
+            p2.N = 2 * p.N;  // both groups' records, scanned as 2N streams
+            float* rec_h[2] = {bwd_rec, bwd_rec + p.N * p.tiles * pb.rec};
+            for (int m = 0; m < pl.mblocks; ++m) {
+                const bool last_m = m == pl.mblocks - 1;
+                const void* qb = static_cast<const char*>(probsQ) + 64 * m * es;
+                const void* kb = static_cast<const char*>(probsK) + 64 * m * es;
+                BwdBlock b1;
+                b1.ldq = p.S;
+                b1.ldv = p.d;
+                b1.s0 = 64 * m;
+                b1.c0 = 0;
+                b1.fwd_d = p.d;
+                b1.fwd_a = int64_t(p.S) * p.d;
+                b1.fwd_rec = p.rec;
+                b1.blocked = 1;
+                b1.acc_q = acc_q ? acc_q + 64 * m : nullptr;
+                b1.q_first = 1;
+                b1.fin_q = col(dQ, 64 * m, es);
+                RACE_TRY(launch_causal_bwd_dq_mfma(qb, kb, V, dOut, nullptr, dq32, apre, fwd_rec, bwd_rec,
+                                                   pb, b1, stream, 128));
+                RACE_TRY(marks->mark(stream));
+                if (!dK && !dV) continue;
+                RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p2, stream, /*reverse=*/true));
+                RACE_TRY(marks->mark(stream));
+                for (int h = 0; h < 2; ++h) {
+                    BwdBlock blk = b1;
+                    blk.c0 = 64 * h;
+                    blk.acc_q = nullptr;
+                    blk.fin_q = nullptr;
+                    blk.acc_k = acc_k ? acc_k + 64 * m : nullptr;
+                    blk.acc_v = acc_v ? acc_v + 64 * h : nullptr;
+                    blk.k_first = h == 0;
+                    blk.v_first = m == 0;
+                    blk.fin_k = h == 1 ? col(dK, 64 * m, es) : nullptr;
+                    blk.fin_v = last_m ? col(dV, 64 * h, es) : nullptr;
+                    blk.alpha = h == 0;
+                    const void* vb = static_cast<const char*>(V) + 64 * h * es;
+                    const void* gb = static_cast<const char*>(dOut) + 64 * h * es;
+                    RACE_TRY(launch_causal_bwd_dkv_mfma(qb, kb, vb, gb, dq32, apre, rec_h[h], nullptr,
+                                                        nullptr, pb, blk, stream));
+                    RACE_TRY(marks->mark(stream));
+                }
+            }
+            return RACE_SUCCESS;
+        }
         for (int m = 0; m < pl.mblocks; ++m) {
             for (int h = 0; h < pl.hblocks; ++h) {
                 const bool last_h = h == pl.hblocks - 1, last_m = m == pl.mblocks - 1;

@@ -236,6 +236,7 @@ struct BwdBlock {
     void* fin_k = nullptr;
     void* fin_v = nullptr;
     int q_first = 1, k_first = 1, v_first = 1;
+    int alpha = 1;  // B3: the terms of alpha = -W dQ (and Y) belong to this block
 };
 // Shapes the blocks cover: S in {64, 128, 256}, d in {64, 128}.
 bool causal_bwd_mfma_supported(int S, int d);
@@ -243,13 +244,18 @@ bool causal_bwd_mfma_supported(int S, int d);
 BwdBlock single_block(const Problem& p);
 // p is the block's problem (S = d = 64 and its record size); q, k, v, g point
 // at the block's first column; dq32, apre and bwd_records are the block's own
-// (rows of 64).
+// (rows of 64).  dv = 128 (bf16 blocks only): one walk over both value groups
+// of a d = 128 problem, the bucket group's whole dQ at once, with the suffix
+// records of value group h at bwd_records + h * N * tiles * rec (Y, the
+// totals of alpha, in group 0's records and zero in group 1's).
 hipError_t launch_causal_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* g,
                                      void* dQ, float* dq32, float* apre, const float* fwd_records,
                                      float* bwd_records, const Problem& p, const BwdBlock& blk,
-                                     hipStream_t stream);
+                                     hipStream_t stream, int dv = 64);
 // dK and dV: the caller's gradients (one block, rows of 64), or through the
-// block's running sums.
+// block's running sums.  With blk.alpha = 0 the block leaves out the terms
+// of alpha = -W dQ (dQ is not read): a walk over both value groups put
+// them, for the whole dQ, into value group 0's block.
 hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* v, const void* g,
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
