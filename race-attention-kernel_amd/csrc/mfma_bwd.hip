@@ -304,9 +304,11 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
             }
         }
         T32::template write<kPolicyDefault, kThreads>(c32, d32r, r0);
-        if (kSums && blk.acc_q) {
+        if (kSums && (blk.acc_q || blk.fin_q)) {
             // The block's part into dQ's running sum (rows outside the tile,
-            // and all rows of the first flush, fall outside the views).
+            // and all rows of the first flush, fall outside the views); a
+            // first addend with fin_q (a walk over every value column) is
+            // dQ itself.
 #pragma unroll
             for (int i = 0; i < T32::template Chunks<kThreads>::kPer; ++i) {
                 const int qi = tid + i * kThreads;

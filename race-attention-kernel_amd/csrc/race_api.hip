@@ -272,7 +272,9 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
         l.bwd = (pl.wide() ? 2 : 1) * p.N * p.tiles * record_floats(64, 64);
         l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
         l.dq32 = round64(NT * 64);
-        l.acc = p.dtype == RACE_BF16 ? 2 * round64(NT * p.S) + round64(NT * p.d) : 0;
+        // bf16: fp32 running sums of dK and dV, and of dQ unless one walk
+        // takes every value column.
+        l.acc = p.dtype == RACE_BF16 ? (pl.wide() ? 1 : 2) * round64(NT * p.S) + round64(NT * p.d) : 0;
         return l;
     }
     const int groups = pl.groups > 1 ? pl.groups : 1;
@@ -870,9 +872,12 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         pb.rec = record_floats(64, 64);
         const bool f32 = p.dtype == RACE_F32;
         const int64_t es = f32 ? 4 : 2, NT = p.N * p.T;
-        float* acc_q = f32 ? static_cast<float*>(dQ) : (dQ ? acc : nullptr);
-        float* acc_k = f32 ? static_cast<float*>(dK) : (dK ? acc + round64(NT * p.S) : nullptr);
-        float* acc_v = f32 ? static_cast<float*>(dV) : (dV ? acc + 2 * round64(NT * p.S) : nullptr);
+        // bf16 running sums in the workspace: dQ (not for a walk over every
+        // value column, whose dQ is whole), then dK, then dV.
+        const int64_t q_sum = pl.wide() ? 0 : round64(NT * p.S);
+        float* acc_q = f32 ? static_cast<float*>(dQ) : (dQ && !pl.wide() ? acc : nullptr);
+        float* acc_k = f32 ? static_cast<float*>(dK) : (dK ? acc + q_sum : nullptr);
+        float* acc_v = f32 ? static_cast<float*>(dV) : (dV ? acc + q_sum + round64(NT * p.S) : nullptr);
         auto col = [](void* base, int64_t c, int64_t es_) -> void* {
             return base ? static_cast<void*>(static_cast<char*>(base) + c * es_) : nullptr;
         };
@@ -898,7 +903,7 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
                 b1.fwd_a = int64_t(p.S) * p.d;
                 b1.fwd_rec = p.rec;
                 b1.blocked = 1;
-                b1.acc_q = acc_q ? acc_q + 64 * m : nullptr;
+                b1.acc_q = nullptr;  // dQ of group m is whole: written straight to the caller's dQ
                 b1.q_first = 1;
                 b1.fin_q = col(dQ, 64 * m, es);
                 RACE_TRY(launch_causal_bwd_dq_mfma(qb, kb, V, dOut, nullptr, dq32, apre, fwd_rec, bwd_rec,

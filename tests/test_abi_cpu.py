@@ -92,8 +92,10 @@ def test_workspace_bytes_for_explicit_tiles(race):
 def test_causal_bwd_workspace_for_matrix_core_blocks(race):
     # S = 256, d = 128: 64 x 64 blocks on the matrix cores.  Forward records
     # of the full shape, suffix records of one block, the running mass every
-    # 16 tokens and dq32 for one block, and for bf16 tokens fp32 running sums
-    # of dQ, dK (N T S each) and dV (N T d).  Host arithmetic only.
+    # 16 tokens and dq32 for one block; fp32 tokens add nothing.  bf16 tokens
+    # take one forward walk over both value groups per bucket group: suffix
+    # records of two blocks, and fp32 running sums of dK (N T S) and dV (N T
+    # d) only (the walk writes dQ whole).  Host arithmetic only.
     from race_attention_kernel_amd import abi
 
     def r64(x):
@@ -104,7 +106,7 @@ def test_causal_bwd_workspace_for_matrix_core_blocks(race):
     rec_full, rec_blk = r64(S * d + S), r64(64 * 64 + 64)
     NT = N * T
     base = N * tiles * rec_full + N * tiles * rec_blk + r64(N * tiles * (tile // 16) * 64) + r64(NT * 64)
-    for dt, extra in ((abi.RACE_F32, 0), (abi.RACE_BF16, 2 * r64(NT * S) + r64(NT * d))):
+    for dt, extra in ((abi.RACE_F32, 0), (abi.RACE_BF16, N * tiles * rec_blk + r64(NT * S) + r64(NT * d))):
         st, nbytes = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 32, d, dt), abi.options(tile, 0))
         assert st == 0 and nbytes == (base + extra) * 4
     # Forced vector-ALU walks: two column groups of 64, no block parts.
