@@ -55,7 +55,7 @@ def main() -> int:
 
     t0 = time.time()
     # cfg2: every T x kernel family, all 8 streams, fp32.
-    for kernel in ("valu", "mfma", "mfma_wg"):
+    for kernel in ("valu", "mfma", "mfma_wg", "single"):
         for T in (512, 2048, 8192, 32768, 65536):
             q, k, v = race.make_inputs(8, T, 4, 16, 64, seed=T)
             out = race.race_fused_fwd(q.to(dev), k.to(dev), v.to(dev), causal=True, kernel=kernel)
@@ -75,17 +75,41 @@ def main() -> int:
         ref = oracle.causal_recurrence(qn, kn, vn, nthreads=16)
         fm, fr = f_units(o, ref)
         add("cfg3 causal fwd bf16", f"N=8 T={T}", "8/8", per_stream_rel_err(o, ref), fm, fr)
-    # cfg5: bf16, S = 256, d = 128; 16 of the 128 streams.
+    # cfg3 shape through the one-read forward (kernel "single"), bf16.
+    T = 1 << 18
+    q, k, v = race.make_inputs(8, T, 4, 16, 64, seed=T, dtype=torch.bfloat16, device=dev, gen_device="cuda")
+    out = race.race_fused_fwd(q, k, v, causal=True, kernel="single")
+    torch.cuda.synchronize()
+    o = to_np(out)
+    ref = oracle.causal_recurrence(to_np(q), to_np(k), to_np(v), nthreads=16)
+    fm, fr = f_units(o, ref)
+    add("cfg3 causal fwd bf16, single", f"N=8 T={T}", "8/8", per_stream_rel_err(o, ref), fm, fr)
+    del q, k, v, out
+    torch.cuda.empty_cache()
+    # cfg5: bf16, S = 256, d = 128; 16 of the 128 streams.  Then the
+    # backward through autograd (forward walks over both value groups),
+    # 4 streams against the oracle's VJP.
     q, k, v = race.make_inputs(128, 16384, 8, 32, 128, seed=5, dtype=torch.bfloat16, device=dev,
                                gen_device="cuda")
-    out = race.race_fused_fwd(q, k, v, causal=True)
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = race.race_fused_fwd(qg, kg, vg, causal=True)
     torch.cuda.synchronize()
     pick = list(range(0, 128, 8))
     o = to_np(out[pick])
     ref = oracle.causal_recurrence(to_np(q[pick]), to_np(k[pick]), to_np(v[pick]), nthreads=16)
     fm, fr = f_units(o, ref)
     add("cfg5 causal fwd bf16", "N=128 T=16384 S=256 d=128", "16/128", per_stream_rel_err(o, ref), fm, fr)
-    del q, k, v, out
+    g = torch.randn(v.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(6)).to(v.dtype)
+    out.backward(g)
+    torch.cuda.synchronize()
+    pick = [0, 41, 86, 127]
+    rq, rk, rv = oracle.causal_bwd(*(to_np(x[pick]) for x in (q, k, v, g)), nthreads=16)
+    for name, got, want in (("dQ", qg.grad, rq), ("dK", kg.grad, rk), ("dV", vg.grad, rv)):
+        gn = to_np(got[pick])
+        fm, fr = f_units(gn, want)
+        add(f"cfg5 causal bwd {name} bf16", "N=128 T=16384 S=256 d=128", "4/128",
+            per_stream_rel_err(gn, want), fm, fr)
+    del q, k, v, out, qg, kg, vg, g
     torch.cuda.empty_cache()
     # cfg4: non-causal forward and the three gradients, every stream.
     q, k, v, g = race.make_inputs(384, 1024, 4, 16, 64, seed=4, grad_out=True)

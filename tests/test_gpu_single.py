@@ -55,11 +55,16 @@ def test_single_matches_oracle(race, oracle, cuda, dtype, N, T):
     assert err <= tol_for(dtype)
 
 
-def test_single_cfg2_full_size(race, oracle, cuda):
-    # cfg2: N=8, L=4, R=16, d=64, T=65536, fp32 (512 tiles per stream).
+def test_single_cfg2_full_size(race, ext, oracle, cuda):
+    # cfg2: N=8, L=4, R=16, d=64, T=65536, fp32 (512 tiles per stream).  The
+    # torch binding runs the one-read path: its records come in 128-token
+    # tiles, the same output as the op.
     say("single cfg2")
     q, k, v = race.make_inputs(8, 65536, 4, 16, 64, seed=65536)
     out = run(race, q.to(cuda), k.to(cuda), v.to(cuda))
+    dbg = ext.forward_debug(q.to(cuda), k.to(cuda), v.to(cuda), True, 0, race.ops.KERNELS["single"])
+    torch.cuda.synchronize()
+    assert dbg[-1] == TILE and torch.equal(dbg[0], out)
     ref = oracle.causal_recurrence(to_np(q), to_np(k), to_np(v), nthreads=16)
     err = per_stream_rel_err(to_np(out), ref)
     say("single cfg2", f"max rel err {err:.3e}")
