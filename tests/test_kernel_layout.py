@@ -675,3 +675,80 @@ def test_operand_tiles_without_their_layout_conflict():
     assert max_bank_load([4 * ((4 * tid + 0) * 64 + 4 * 3) for tid in grp]) == 16
     assert max(bank_load((4 * (c * 64 + 7), 4) for c in grp).values()) == 16
     assert max(bank_load((4 * (c * 68 + 7), 4) for c in grp).values()) == 1
+
+
+# ---------------------------------------------------------------------------
+# mfma_bwd.hip causal_bwd_dq_mfma_kernel<TIn, kSums, DV>: the staging slots.
+# Slot e = tid + 256 s counts K's blocks (4 tokens x E features of the 64
+# bucket columns), then V's and G's (of DV value columns each); a wave's 64
+# slots must name one tensor, and every block of every tensor is staged once.
+
+def bwd_stage_slots(E: int, DV: int):
+    C, S = 32, 64
+    blk_k, blk_v = (C // 4) * (S // E), (C // 4) * (DV // E)
+    slots = -(-(blk_k + 2 * blk_v) // 256)
+    out = []
+    for s in range(slots):
+        for tid in range(256):
+            e = tid + 256 * s
+            e_wave = e - (tid & 63)
+            tensor = 0 if e_wave < blk_k else 1 if e_wave < blk_k + blk_v else 2 if e_wave < blk_k + 2 * blk_v else 3
+            if tensor == 3:
+                continue
+            blk = e if tensor == 0 else e - blk_k if tensor == 1 else e - blk_k - blk_v
+            width = S if tensor == 0 else DV
+            a, b = divmod(blk, width // E)
+            out.append((s, tid, tensor, a, b))
+    return out, blk_k, blk_v
+
+
+@pytest.mark.parametrize("E, DV", [(8, 64), (8, 128), (4, 64)])
+def test_bwd_staging_covers_every_block_once(E, DV):
+    slots, blk_k, blk_v = bwd_stage_slots(E, DV)
+    seen = Counter((tensor, a, b) for _, _, tensor, a, b in slots)
+    want = {(0, a, b) for a in range(8) for b in range(64 // E)}
+    want |= {(t, a, b) for t in (1, 2) for a in range(8) for b in range(DV // E)}
+    assert set(seen) == want and set(seen.values()) == {1}
+    # a wave stages one tensor (its buffer and stride are uniform)
+    per_wave = {}
+    for s, tid, tensor, _, _ in slots:
+        per_wave.setdefault((s, tid >> 6), set()).add(tensor)
+    assert all(len(t) == 1 for t in per_wave.values())
+    assert blk_k % 64 == 0 and blk_v % 64 == 0
+
+
+def test_bwd_staging_with_a_misplaced_boundary_fails():
+    # Planted mistake: V's blocks counted from the wrong boundary (blk_v
+    # instead of blk_k) would stage K's last blocks twice and miss some of G.
+    E, DV = 8, 128
+    slots, blk_k, blk_v = bwd_stage_slots(E, DV)
+    wrong = Counter()
+    for s, tid, tensor, _, _ in slots:
+        e = tid + 256 * s
+        blk = e if tensor == 0 else e - blk_v if tensor == 1 else e - 2 * blk_v
+        if blk < 0:
+            continue
+        width = 64 if tensor == 0 else DV
+        wrong[(tensor, *divmod(blk, width // E))] += 1
+    want = {(0, a, b) for a in range(8) for b in range(8)} | {(t, a, b) for t in (1, 2) for a in range(8) for b in range(16)}
+    assert set(wrong) != want
+
+
+@pytest.mark.parametrize("N, tiles", [(1, 1), (128, 32), (3, 7)])
+def test_wide_walk_record_arrays_do_not_overlap(N, tiles):
+    # Records of value group h start at h N tiles rec (rec = 4160 floats);
+    # the reverse scan takes both arrays as 2N streams of tiles records.
+    rec = 4160
+    spans = []
+    for h in range(2):
+        for n in range(N):
+            for ti in range(tiles):
+                start = (h * N * tiles + n * tiles + ti) * rec
+                spans.append((start, start + 64 * 64 + 64))
+    spans.sort()
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+    assert spans[-1][1] <= 2 * N * tiles * rec
+    # the scan's stream 2N-view: stream n' = h N + n holds exactly group h, stream n
+    for h in range(2):
+        for n in range(N):
+            assert (h * N + n) * tiles * rec == (h * N * tiles + n * tiles) * rec
