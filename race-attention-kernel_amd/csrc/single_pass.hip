@@ -23,10 +23,13 @@
 // their workgroups the scanners of the XCD's streams; later tickets name
 // tiles, interleaved over the XCD's streams in tile order.  A workgroup
 // holding a tile waits only for that tile's prefix, which needs the totals of
-// earlier tiles of the stream; those tiles were ticketed earlier, so they are
-// held by running workgroups that publish their totals before they wait for
-// anything.  No wait can close a cycle, whatever the number of resident
-// workgroups.  Every wait is still bounded: after kSpSpinLimit polls it sets
+// earlier tiles of the stream.  Those were ticketed earlier, by workgroups
+// that are running, and a workgroup waits only while each tile whose totals
+// it has not yet published was ticketed after the tile it waits for.  So
+// every wait points to an earlier ticket and none can close a cycle, whatever
+// the number of resident workgroups (tests/test_single_pass_protocol.py
+// emulates the protocol; dealing tiles out by launch index instead
+// deadlocks there).  Every wait is still bounded: after kSpSpinLimit polls it sets
 // the error word, and every later wait gives up at once, so the kernel always
 // ends (with the error word set and the output not valid).
 //
