@@ -152,3 +152,18 @@ def test_single_refuses_what_it_does_not_take(race, ext, cuda):
     assert abi.fwd_workspace_bytes(sh, True, abi.options(64, abi.RACE_KERNEL_SINGLE))[0] == abi.RACE_ERROR_INVALID_VALUE
     assert abi.fwd_workspace_bytes(sh, False, abi.options(0, abi.RACE_KERNEL_SINGLE))[0] == abi.RACE_ERROR_INVALID_VALUE
     assert abi.fwd_workspace_bytes(sh, True, abi.options(128, abi.RACE_KERNEL_SINGLE))[0] == 0
+
+
+def test_single_through_autograd(race, oracle, cuda):
+    # The one-read forward keeps its records (128-token tiles) for the
+    # backward, which starts from them: the gradients against the oracle VJP,
+    # dK relative to the scale of its cancelling terms as in the causal
+    # backward suite.
+    from test_gpu_causal_bwd import check_grads
+    say("single autograd")
+    q, k, v, g = race.make_inputs(8, 1000, 4, 16, 64, seed=12, grad_out=True)
+    qg, kg, vg = (x.to(cuda).requires_grad_(True) for x in (q, k, v))
+    out = race.race_fused_fwd(qg, kg, vg, causal=True, kernel="single")
+    out.backward(g.to(cuda))
+    torch.cuda.synchronize()
+    check_grads(oracle, q, k, v, g, out.detach(), qg.grad, kg.grad, vg.grad, FP32_TOL)
