@@ -40,16 +40,20 @@ constexpr int npb_of(int S, int KP) { return ((S >> KP) * KP + 15) / 16; }
 // L * KP <= 64.
 constexpr bool kp_ok(int S, int KP) { return KP >= 2 && (S >> KP) >= 1 && (S >> KP) * KP <= 64; }
 
-// Token rows [C][Wd] of one sub-chunk in registers (blocks of 4 rows x one
-// 16-byte vector), then stored as a plane tile.  The V part of KVStage for a
-// workgroup of NT threads.
+// Token rows [C][Wd] of one sub-chunk in registers (blocks of kRows rows x
+// one 16-byte vector, kRows = 4, 2 or 1: the most that still gives every one
+// of the NT threads a block), then stored as a plane tile.  The V part of
+// KVStage for a workgroup of NT threads.
 template <typename TIn, int Wd, int C, int P, int NT>
 struct RowStage {
     static constexpr int E = Elem<TIn>::kPerVec;
     static constexpr bool kSplit = std::is_same<TIn, float>::value;
-    static constexpr int kBlk = (C / 4) * (Wd / E);
+    static constexpr int kVecs = C * (Wd / E);
+    static constexpr int kRows = kVecs >= 4 * NT ? 4 : kVecs >= 2 * NT ? 2 : 1;
+    static constexpr int kBlk = (C / kRows) * (Wd / E);
     static constexpr int kPer = (kBlk + NT - 1) / NT;
-    uint4 x[kPer][4];
+    static_assert(C % kRows == 0, "whole blocks of rows");
+    uint4 x[kPer][kRows];
 
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int r0) {
         const int tid = threadIdx.x;
@@ -59,8 +63,8 @@ struct RowStage {
             const int a = blk / (Wd / E), b = blk % (Wd / E);
             if (kBlk % NT == 0 || blk < kBlk) {
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    x[p][rr] = buf_load16<P>(r, ((r0 + 4 * a + rr) * Wd + b * E) * int(sizeof(TIn)));
+                for (int rr = 0; rr < kRows; ++rr)
+                    x[p][rr] = buf_load16<P>(r, ((r0 + kRows * a + rr) * Wd + b * E) * int(sizeof(TIn)));
             }
         }
     }
@@ -76,7 +80,7 @@ struct RowStage {
 #pragma unroll
             for (int h = 0; h < E / 4; ++h)
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
+                for (int rr = 0; rr < kRows; ++rr) {
                     uint2 hi, lo;
                     if constexpr (kSplit) {
                         split4<true>(Elem<TIn>::get(x[p][rr], 4 * h), Elem<TIn>::get(x[p][rr], 4 * h + 1),
@@ -86,7 +90,7 @@ struct RowStage {
                         hi = make_uint2(h ? x[p][rr].z : x[p][rr].x, h ? x[p][rr].w : x[p][rr].y);
                         lo = hi;
                     }
-                    PL::put4(t, 4 * a + rr, b * E + 4 * h, hi, lo);
+                    PL::put4(t, kRows * a + rr, b * E + 4 * h, hi, lo);
                 }
         }
     }
@@ -99,12 +103,16 @@ struct RowStage {
 // workgroup barrier.  Each item decodes its table's sigma pairs once and
 // writes the R / 4 corner quads: keys into the token-row plane tile (rows at
 // or past `valid` zero: zero rows hash to 1/R, which would add mass), queries
-// into the float tile Qf (OutTile layout).
-template <typename TIn, int D, int S, int KP, int C, bool kQuery, typename PW>
+// into the float tile Qf (OutTile layout), or with kQInPlane into the plane
+// tile W will occupy: the four floats of a quad as the raw bits of its hi
+// (two) and lo (two) slots, which the thread that forms W there reads back
+// before it overwrites them.
+template <typename TIn, int D, int S, int KP, int C, bool kQuery, typename PW, bool kQInPlane = false>
 __device__ __forceinline__ void hash_block(const Projector<TIn, D, npb_of(S, KP)>& pj, const PW& wp, float* U,
                                            int t0, unsigned char* dst, int valid, float scale2, int g,
                                            int lr) {
     constexpr int NPB = npb_of(S, KP), L = tables_of(S, KP), R = 1 << KP;
+    static_assert(!kQInPlane || std::is_same<TIn, float>::value, "fp32 plane slots hold a float each");
     using PS = Plane<std::is_same<TIn, float>::value, S>;
     using QT = OutTile<float, S, C>;
     constexpr int kUP = 16 * NPB + 1;
@@ -123,7 +131,10 @@ __device__ __forceinline__ void hash_block(const Projector<TIn, D, npb_of(S, KP)
 #pragma unroll
         for (int m = 0; m < R / 4; ++m) {
             const f32x4 q = live * ct.quad(m);
-            if constexpr (kQuery) {
+            if constexpr (kQuery && kQInPlane) {
+                PS::put4(dst, t, l * R + 4 * m, make_uint2(__float_as_uint(q[0]), __float_as_uint(q[1])),
+                         make_uint2(__float_as_uint(q[2]), __float_as_uint(q[3])));
+            } else if constexpr (kQuery) {
                 QT::put(dst, t, l * R + 4 * m, q);
             } else {
                 uint2 hi, lo;
@@ -262,7 +273,11 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
 //   (2) running mass, W = Phi_Q / (Abar + eps)
 //   (3) P^T blocks = masked K W^T into the P tile
 //   then output and state update as in the probability-input kernel.
-template <typename TIn, int S, int D, int C, int KP, int kMinBlocks, int NW, bool kWl, bool kDB>
+// kLean (fp32 rows): Phi_Q goes into the W plane's own slots and each lane
+// stores its output quad straight from the accumulators, so neither the
+// query-feature tile nor the output tile takes LDS (37 KB at S = d = 64, C =
+// 32: four workgroups per CU where 53 KB allowed three).
+template <typename TIn, int S, int D, int C, int KP, int kMinBlocks, int NW, bool kWl, bool kDB, bool kLean>
 __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
     const TIn* __restrict__ qx, const TIn* __restrict__ kx, const TIn* __restrict__ v,
     const float* __restrict__ planes, TIn* __restrict__ out, const float* __restrict__ records,
@@ -274,6 +289,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
     using PC = typename G::PC;
     using PD = typename G::PD;
     constexpr bool kSplit = G::kSplit;
+    static_assert(!kLean || kSplit, "the lean layout keeps fp32 Phi_Q in the hi/lo plane slots");
     constexpr int NSB = S / 16, NBI = C / 16, NKS = S / 32, NKC = C / 32;
     constexpr int SBW = S / (16 * NW), CBW = D / (16 * NW);
     constexpr int NLB = NBI * (NBI + 1) / 2;
@@ -291,9 +307,9 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
     float* Uq = reinterpret_cast<float*>(Ps);
     float* Uk = Uq + C * kUP;
     unsigned char* Vs = Ps + kPU;
-    unsigned char* Os = Vs + G::kVBytes;
-    unsigned char* Qf = Os + C * D * int(sizeof(TIn));  // Phi_Q [C][S] fp32
-    unsigned char* Wl = Qf + C * S * 4;                   // the staged planes (kWl)
+    unsigned char* Os = Vs + G::kVBytes;                                  // out (not kLean)
+    unsigned char* Qf = Os + (kLean ? 0 : C * D * int(sizeof(TIn)));      // Phi_Q [C][S] fp32 (not kLean)
+    unsigned char* Wl = Qf + (kLean ? 0 : C * S * 4);                     // the staged planes (kWl)
     using OT = OutTile<TIn, D, C>;
     using QT = OutTile<float, S, C>;
 
@@ -372,7 +388,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
         __syncthreads();
         // Unconditional flush (at r0 = 0 the offsets fall outside the buffer
         // range and the stores are dropped), as in the probability kernel.
-        OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
+        if constexpr (!kLean) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
         vst.store(Vs);
         vst.load(vr, r0 + C);  // prefetch (past the tile: zeros, never used)
         if constexpr (kDB) load_rows(nxt, r0 + C);
@@ -380,7 +396,8 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
         for (int j = 0; j < kJobsW; ++j) {
             const int job = w + NW * j;
             if (job < NBI)
-                hash_block<TIn, D, S, KP, C, true>(cur.j[j], wp, Uq, 16 * job, Qf, rows - r0, scale2, g, lr);
+                hash_block<TIn, D, S, KP, C, true, PW, kLean>(cur.j[j], wp, Uq, 16 * job, kLean ? Ws : Qf,
+                                                              rows - r0, scale2, g, lr);
             else if (job < kJobs)
                 hash_block<TIn, D, S, KP, C, false>(cur.j[j], wp, Uk, 16 * (job - NBI), Ks, rows - r0,
                                                     scale2, g, lr);
@@ -407,7 +424,16 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
                     if constexpr (kSplit) acc = mfma16(kl[kk], lf, acc);
                     acc = mfma16(kh[kk], lf, acc);
                 }
-                const f32x4 qv = QT::get4(Qf, 16 * bi + lr, 16 * sb + 4 * g);
+                f32x4 qv;
+                if constexpr (kLean) {
+                    const int at = PS::off4(16 * bi + lr, 16 * sb + 4 * g);
+                    const uint2 h = *reinterpret_cast<const uint2*>(Ws + at);
+                    const uint2 lo = *reinterpret_cast<const uint2*>(Ws + at + PS::kLoOff);
+                    qv = f32x4{__uint_as_float(h.x), __uint_as_float(h.y), __uint_as_float(lo.x),
+                               __uint_as_float(lo.y)};
+                } else {
+                    qv = QT::get4(Qf, 16 * bi + lr, 16 * sb + 4 * g);
+                }
                 uint2 hi, lo;
                 split4<kSplit>(qv[0] * __builtin_amdgcn_rcpf(acc[0] + kEps),
                                qv[1] * __builtin_amdgcn_rcpf(acc[1] + kEps),
@@ -497,7 +523,10 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
                     }
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
-                OT::put(Os, 16 * bi + lr, 16 * cb + 4 * g, o[bi]);
+                if constexpr (kLean)  // rows past the tile fall outside or_ and are dropped
+                    store4<TIn, kStoreP>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * 4, o[bi]);
+                else
+                    OT::put(Os, 16 * bi + lr, 16 * cb + 4 * g, o[bi]);
             }
 #pragma unroll
             for (int sb = 0; sb < NSB; ++sb) {
@@ -520,18 +549,20 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
         if (r0 + C < rows) sub_chunk(r0 + C, pjB, pjA);
     }
     r0 = ((rows + C - 1) / C) * C;  // one past the last sub-chunk
-    __syncthreads();
-    if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
+    if constexpr (!kLean) {
+        __syncthreads();
+        if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
+    }
 }
 
 // LDS of the output pass, with (kWl) or without the staged planes.
-template <typename TIn, int S, int D, int C, int KP, int NW, bool kWl>
+template <typename TIn, int S, int D, int C, int KP, int NW, bool kWl, bool kLean = false>
 constexpr int hashed_output_lds() {
     using G = Geo<TIn, S, D, C, NW>;
     constexpr int NPB = npb_of(S, KP);
     constexpr int kUBytes = C * (16 * NPB + 1) * 4;
     constexpr int kPU = G::kPBytes > 2 * kUBytes ? G::kPBytes : 2 * kUBytes;
-    return G::kWBytes + G::kKBytes + kPU + G::kVBytes + C * D * int(sizeof(TIn)) + C * S * 4 +
+    return G::kWBytes + G::kKBytes + kPU + G::kVBytes + (kLean ? 0 : C * D * int(sizeof(TIn)) + C * S * 4) +
            (kWl ? planes_lds_bytes<TIn, D, NPB>() : 0);
 }
 constexpr int kMaxLds = 160 * 1024;  // gfx950: LDS per workgroup
@@ -544,15 +575,17 @@ constexpr int hashed_sums_lds() {
 }
 
 // C: the output pass's sub-chunk; CS: the tile sums' (a multiple of C); kDB:
-// double-buffered row registers (where they fit).
+// double-buffered row registers (where they fit); kLean: the output pass's
+// fp32 layout without the query-feature and output tiles.
 template <typename TIn, int S, int D, int C, int KP, int kMinBlocks, int NW = 4, int CS = C,
-          bool kDB = false>
+          bool kDB = false, bool kLean = false>
 hipError_t launch_hashed_family(const HashedArgs& a, const Problem& p, hipStream_t stream, Marks* marks) {
     if (p.tile % C != 0 || p.tile % CS != 0) return hipErrorInvalidValue;
     // The planes go to LDS when the output pass has room for them (not at
     // fp32, S = d = 128).  gfx950 gives a workgroup at most 160 KB.
-    constexpr bool kWl = hashed_output_lds<TIn, S, D, C, KP, NW, true>() <= kMaxLds;
-    static_assert(hashed_output_lds<TIn, S, D, C, KP, NW, false>() <= kMaxLds, "output pass LDS");
+    constexpr bool kWl = hashed_output_lds<TIn, S, D, C, KP, NW, true, kLean>() <= kMaxLds;
+    constexpr int kOutLds = hashed_output_lds<TIn, S, D, C, KP, NW, kWl, kLean>();
+    static_assert(kOutLds <= kMaxLds, "output pass LDS");
     static_assert(hashed_sums_lds<TIn, S, D, CS, KP>() <= kMaxLds, "tile sums LDS");
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     hipError_t err;
@@ -564,8 +597,8 @@ hipError_t launch_hashed_family(const HashedArgs& a, const Problem& p, hipStream
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
     if ((err = launch_tile_scan(a.records, a.state, p, stream)) != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
-    hashed_output_kernel<TIn, S, D, C, KP, kMinBlocks, NW, kWl, kDB>
-        <<<grid, 64 * NW, hashed_output_lds<TIn, S, D, C, KP, NW, kWl>(), stream>>>(
+    hashed_output_kernel<TIn, S, D, C, KP, kMinBlocks, NW, kWl, kDB, kLean>
+        <<<grid, 64 * NW, kOutLds, stream>>>(
             static_cast<const TIn*>(a.q), static_cast<const TIn*>(a.k), static_cast<const TIn*>(a.v),
             a.planes, static_cast<TIn*>(a.out), a.records, p.T, p.tile, p.tiles, p.rec);
     if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -577,15 +610,15 @@ hipError_t launch_hashed_shape(const HashedArgs& a, const Problem& p, hipStream_
     if constexpr (!kp_ok(S, KP)) {
         return hipErrorInvalidValue;
     } else if constexpr (S == 64 && D == 64) {
-        // bf16 rows, where the output pass's LDS allows four workgroups per CU
-        // (at most 40 KB each): four, rows single-buffered (double-buffered
-        // they would spill).  Otherwise three workgroups per CU (a fourth
-        // would spill), rows double-buffered.  64-token sub-chunks for the
-        // tile sums either way.
-        constexpr bool kFour = !std::is_same<TIn, float>::value &&
-                               hashed_output_lds<TIn, 64, 64, 32, KP, 4, true>() <= kMaxLds / 4;
+        // Four workgroups per CU where the output pass fits 40 KB of LDS (bf16
+        // rows in the ordinary layout, fp32 rows in the lean one), rows
+        // single-buffered (double-buffered they would spill).  Else (fewer
+        // planes per table: more tables, larger hash scratch and planes)
+        // three, rows double-buffered.  64-token sub-chunks for the tile sums.
+        constexpr bool kLean = std::is_same<TIn, float>::value;
+        constexpr bool kFour = hashed_output_lds<TIn, 64, 64, 32, KP, 4, true, kLean>() <= kMaxLds / 4;
         if constexpr (kFour)
-            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false>(a, p, stream, marks);
+            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false, kLean>(a, p, stream, marks);
         else
             return launch_hashed_family<TIn, 64, 64, 32, KP, 3, 4, 64, true>(a, p, stream, marks);
     } else if constexpr (S == 256 && D == 128) {
