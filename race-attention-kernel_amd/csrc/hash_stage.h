@@ -111,13 +111,25 @@ struct Projector {
 // or the cached planes buffer itself (PlanesGlobal, for kernels whose LDS is
 // full) hand the fp32 projection the four values of plane row `row` at
 // columns c .. c + 3; PlanesB3 hands the bf16 projection its three terms.
-struct PlanesLds {
+// fp32 rows: padded to D + 4 floats, or (kSwz) D floats with 16-byte chunk
+// c / 4 of row `row` at chunk (c / 4) ^ (row % 16).  Either way the 16 rows a
+// lane group reads at one column spread over every bank; the padded layout
+// reads at immediate offsets from one address, the swizzled one saves the
+// padding (256 bytes per 16 rows at D = 64) for an address per chunk.
+template <int D, bool kSwz>
+__device__ __forceinline__ int plane_at(int row, int c) {
+    static_assert(!kSwz || D % 64 == 0, "at least 16 chunks per row for the swizzle");
+    return kSwz ? row * D + 4 * ((c >> 2) ^ (row & 15)) : row * (D + 4) + c;
+}
+template <bool kSwz>
+struct PlanesLdsT {
     const float* w;
     template <int D>
     __device__ __forceinline__ f32x4 get4(int row, int c) const {
-        return *reinterpret_cast<const f32x4*>(w + row * (D + 4) + c);
+        return *reinterpret_cast<const f32x4*>(w + plane_at<D, kSwz>(row, c));
     }
 };
+using PlanesLds = PlanesLdsT<false>;
 // The planes as three bf16 terms (hi, mid, lo) in LDS, [3][16 NPB][D + 8]
 // (the padding spreads a 16-lane column of rows over the banks): the A
 // operand of the bf16 projection.
@@ -137,16 +149,16 @@ struct PlanesGlobal {
     }
 };
 
-// The planes [LK][D] fp32 into LDS rows of D + 4 floats (the padding spreads
-// a 16-lane column of rows over the banks), rows LK .. 16 NPB - 1 zero.
+// The planes [LK][D] fp32 into LDS rows as PlanesLdsT<kSwz> reads them, rows
+// LK .. 16 NPB - 1 zero.
 // Cooperative over the NT threads of the workgroup; the caller synchronizes.
-template <int D, int NPB, int NT>
+template <int D, int NPB, int NT, bool kSwz = false>
 __device__ __forceinline__ void stage_planes(float* Wl, const float* __restrict__ planes, int LK) {
     for (int e = threadIdx.x; e < 16 * NPB * (D / 4); e += NT) {
         const int row = e / (D / 4), c4 = 4 * (e % (D / 4));
         f32x4 w = {0.f, 0.f, 0.f, 0.f};
         if (row < LK) w = *reinterpret_cast<const f32x4*>(planes + row * D + c4);
-        *reinterpret_cast<f32x4*>(Wl + row * (D + 4) + c4) = w;
+        *reinterpret_cast<f32x4*>(Wl + plane_at<D, kSwz>(row, c4)) = w;
     }
 }
 
@@ -173,9 +185,9 @@ __device__ __forceinline__ void stage_planes_b3(unsigned char* Wb, const float* 
 }
 
 // LDS of the staged planes for rows of TIn.
-template <typename TIn, int D, int NPB>
+template <typename TIn, int D, int NPB, bool kSwz = false>
 constexpr int planes_lds_bytes() {
-    return std::is_same<TIn, float>::value ? 16 * NPB * (D + 4) * 4 : 3 * 16 * NPB * (D + 8) * 2;
+    return std::is_same<TIn, float>::value ? 16 * NPB * (kSwz ? D : D + 4) * 4 : 3 * 16 * NPB * (D + 8) * 2;
 }
 
 // z = scale2 tanh(p) of the projections in acc (scale2 = 2 / sqrt(D)),

@@ -150,6 +150,17 @@ __device__ __forceinline__ void hash_block(const Projector<TIn, D, npb_of(S, KP)
 // tile record (B [S][D] then A [S]).  Wave w hashes 16-token block w of
 // each sub-chunk (when C / 16 > w) and owns the V columns of c-blocks w,
 // w + 4, .. for B and the buckets of s-blocks w, w + 4, .. for A.
+//
+// Where a wave's plane values fit its own 16 rows of the K plane tile and
+// one pass over (token, table) items decodes them all (16 L <= 64), they are
+// kept there (sums_u_in_k): every lane of the wave reads its items' values
+// before the wave writes those rows, and only this wave writes them.
+template <typename TIn, int S, int KP>
+constexpr bool sums_u_in_k() {
+    return 16 * tables_of(S, KP) <= 64 &&
+           (16 * npb_of(S, KP) + 1) * 4 <= Plane<std::is_same<TIn, float>::value, S>::kPitch;
+}
+
 template <typename TIn, int S, int D, int C, int KP, int kMinBlocks, bool kDB>
 __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
     const TIn* __restrict__ kx, const TIn* __restrict__ v, const float* __restrict__ planes,
@@ -162,10 +173,11 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
     constexpr int NSB = S / 16, NKC = C / 32, CBW = D / 64, SBW = S / 64;
     constexpr int kUP = 16 * NPB + 1;
     extern __shared__ __align__(16) unsigned char lds[];
+    constexpr bool kUInK = sums_u_in_k<TIn, S, KP>();
     unsigned char* Ks = lds;
     unsigned char* Vs = Ks + G::kKBytes;
-    float* U = reinterpret_cast<float*>(Vs + G::kVBytes);  // [C][kUP]
-    unsigned char* Wl = reinterpret_cast<unsigned char*>(U + C * kUP);  // the staged planes
+    unsigned char* Ue = Vs + G::kVBytes;                     // [C][kUP] (not kUInK)
+    unsigned char* Wl = Ue + (kUInK ? 0 : C * kUP * 4);      // the staged planes
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -177,10 +189,14 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + (n * T + t_begin) * D, int64_t(rows) * D * sizeof(TIn));
     const float scale2 = 2.0f * __builtin_amdgcn_rsqf(float(D));
     const bool projects = w < C / 16;
-    using PW = std::conditional_t<std::is_same<TIn, float>::value, PlanesLds, PlanesB3>;
+    // This wave's plane values: token t at U + t kUP.
+    float* U = reinterpret_cast<float*>(kUInK ? Ks + 16 * w * (PS::kPitch - 4 * kUP) : Ue);
+    // fp32 planes swizzled: the padding would keep S = d = 64 from four
+    // workgroups per CU (40 KB of LDS each).
+    using PW = std::conditional_t<std::is_same<TIn, float>::value, PlanesLdsT<true>, PlanesB3>;
     PW wp;
     if constexpr (std::is_same<TIn, float>::value) {
-        stage_planes<D, NPB, kThreads>(reinterpret_cast<float*>(Wl), planes, LK);
+        stage_planes<D, NPB, kThreads, true>(reinterpret_cast<float*>(Wl), planes, LK);
         wp.w = reinterpret_cast<const float*>(Wl);
     } else {
         stage_planes_b3<D, NPB, kThreads>(Wl, planes, LK);
@@ -571,14 +587,16 @@ template <typename TIn, int S, int D, int C, int KP>
 constexpr int hashed_sums_lds() {
     using G = Geo<TIn, S, D, C>;
     constexpr int NPB = npb_of(S, KP);
-    return G::kKBytes + G::kVBytes + C * (16 * NPB + 1) * 4 + planes_lds_bytes<TIn, D, NPB>();
+    return G::kKBytes + G::kVBytes + (sums_u_in_k<TIn, S, KP>() ? 0 : C * (16 * NPB + 1) * 4) +
+           planes_lds_bytes<TIn, D, NPB, true>();
 }
 
 // C: the output pass's sub-chunk; CS: the tile sums' (a multiple of C); kDB:
 // double-buffered row registers (where they fit); kLean: the output pass's
-// fp32 layout without the query-feature and output tiles.
+// fp32 layout without the query-feature and output tiles; kSumsBlocks and
+// kSumsDB: the tile sums' workgroups per CU and row buffering.
 template <typename TIn, int S, int D, int C, int KP, int kMinBlocks, int NW = 4, int CS = C,
-          bool kDB = false, bool kLean = false>
+          bool kDB = false, bool kLean = false, int kSumsBlocks = kMinBlocks, bool kSumsDB = kDB>
 hipError_t launch_hashed_family(const HashedArgs& a, const Problem& p, hipStream_t stream, Marks* marks) {
     if (p.tile % C != 0 || p.tile % CS != 0) return hipErrorInvalidValue;
     // The planes go to LDS when the output pass has room for them (not at
@@ -589,7 +607,7 @@ hipError_t launch_hashed_family(const HashedArgs& a, const Problem& p, hipStream
     static_assert(hashed_sums_lds<TIn, S, D, CS, KP>() <= kMaxLds, "tile sums LDS");
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     hipError_t err;
-    hashed_sums_kernel<TIn, S, D, CS, KP, kMinBlocks, kDB>
+    hashed_sums_kernel<TIn, S, D, CS, KP, kSumsBlocks, kSumsDB>
         <<<grid, kThreads, hashed_sums_lds<TIn, S, D, CS, KP>(), stream>>>(
             static_cast<const TIn*>(a.k), static_cast<const TIn*>(a.v), a.planes, a.records, p.T, p.tile,
             p.tiles, p.rec);
@@ -618,7 +636,7 @@ hipError_t launch_hashed_shape(const HashedArgs& a, const Problem& p, hipStream_
         constexpr bool kLean = std::is_same<TIn, float>::value;
         constexpr bool kFour = hashed_output_lds<TIn, 64, 64, 32, KP, 4, true, kLean>() <= kMaxLds / 4;
         if constexpr (kFour)
-            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false, kLean>(a, p, stream, marks);
+            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false, kLean, 4, kLean>(a, p, stream, marks);
         else
             return launch_hashed_family<TIn, 64, 64, 32, KP, 3, 4, 64, true>(a, p, stream, marks);
     } else if constexpr (S == 256 && D == 128) {

@@ -489,6 +489,130 @@ def test_plane_stagings_spread_a_column_of_rows(D):
     assert max(load.values()) > 1
 
 
+def plane_at(D: int, swz: bool, row: int, c: int) -> int:
+    """hash_stage.h plane_at<D, kSwz>: float offset of plane row `row`,
+    columns c .. c + 3 (c % 4 == 0)."""
+    return row * D + 4 * ((c >> 2) ^ (row & 15)) if swz else row * (D + 4) + c
+
+
+@pytest.mark.parametrize("D, NPB", [(64, 1), (64, 2), (128, 1), (128, 4)])
+def test_swizzled_planes_place_each_chunk_once_and_spread(D, NPB):
+    # PlanesLdsT<true> (the tile sums): rows of D floats, no padding; every
+    # 16-byte chunk has one place inside its row, and get4 of the 16 rows of a
+    # block (lr) at one column touches each bank once.
+    places = Counter(plane_at(D, True, row, c) for row in range(16 * NPB) for c in range(0, D, 4))
+    assert sorted(places) == list(range(0, 16 * NPB * D, 4)) and set(places.values()) == {1}
+    for row in range(16 * NPB):
+        assert all(row * D <= plane_at(D, True, row, c) < (row + 1) * D for c in range(0, D, 4))
+    for pb, c in itertools.product(range(NPB), range(0, D, 4)):
+        load = bank_load((plane_at(D, True, 16 * pb + lr, c) * 4, 16) for lr in range(16))
+        assert len(load) == BANKS and max(load.values()) == 1
+    # Planted mistake: swizzling by row % 4 only leaves 4-way conflicts.
+    load = bank_load(((16 + lr) * D * 4 + 16 * (lr & 3), 16) for lr in range(16))
+    assert max(load.values()) > 1
+
+
+def sums_u_in_k(S: int, KP: int, split: bool) -> bool:
+    """hashed_kernels.h sums_u_in_k: a wave's plane values live in its own 16
+    rows of the K plane tile when one decode pass covers them (16 L <= 64)
+    and a token's kUP floats fit one row's pitch."""
+    L = S >> KP
+    npb = (L * KP + 15) // 16
+    return 16 * L <= 64 and (16 * npb + 1) * 4 <= Plane(split, S).pitch
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("S, KP", [(64, 2), (64, 3), (64, 4), (64, 5), (64, 6), (128, 4), (256, 4)])
+def test_sums_plane_values_stay_in_their_waves_rows(split, S, KP):
+    L = S >> KP
+    if L < 1 or L * KP > 64:
+        pytest.skip("not a hashed shape")
+    npb = (L * KP + 15) // 16
+    kup = 16 * npb + 1
+    P = Plane(split, S)
+    if not sums_u_in_k(S, KP, split):
+        assert 16 * L > 64 or 4 * kup > P.pitch
+        return
+    # One pass over the (token, table) items: every value is read before the
+    # wave writes any feature.
+    assert (16 * L + 63) // 64 == 1
+    spans = []
+    for w in range(4):
+        base = 16 * w * (P.pitch - 4 * kup)  # the kernel's U for wave w
+        lo = base + (16 * w) * kup * 4
+        hi = base + (16 * w + 15) * kup * 4 + 4 * kup
+        # inside rows 16 w .. 16 w + 15 of the K tile, which only wave w writes
+        assert 16 * w * P.pitch <= lo and hi <= (16 * w + 16) * P.pitch
+        spans.append((lo, hi))
+    assert all(spans[i][1] <= spans[i + 1][0] for i in range(3))
+
+
+def test_four_workgroups_fit_the_s64_lds():
+    # S = d = 64, fp32 rows: the tile sums (64-token sub-chunks: K and V plane
+    # tiles, the plane values inside K, swizzled planes) and the lean output
+    # pass (W, K, V plane tiles, P / plane values, padded planes) each fit
+    # 40 KB, a quarter of gfx950's 160 KB.
+    P = Plane(True, 64)
+    sums = 2 * 64 * P.pitch + 16 * 64 * 4
+    assert sums <= 40 * 1024
+    u = 32 * 17 * 4
+    p_tile = Plane(True, 32).pitch * 32
+    out = 3 * 32 * P.pitch + max(p_tile, 2 * u) + 16 * (64 + 4) * 4
+    assert out <= 40 * 1024
+    # With padded planes the sums would not: the planted layout.
+    assert 2 * 64 * P.pitch + 16 * 68 * 4 > 40 * 1024
+
+
+@pytest.mark.parametrize("C, Wd, es, NT", [(32, 64, 4, 256), (64, 64, 4, 256), (32, 64, 2, 256),
+                                           (32, 128, 4, 256), (64, 128, 2, 512), (32, 64, 4, 512)])
+def test_row_stage_blocks_cover_the_sub_chunk_once(C, Wd, es, NT):
+    # hashed_kernels.h RowStage: blocks of kRows rows x one 16-byte vector,
+    # kRows the most (4, 2, 1) that still gives every thread a block.
+    E = 16 // es
+    vecs = C * (Wd // E)
+    rows = 4 if vecs >= 4 * NT else 2 if vecs >= 2 * NT else 1
+    blocks = (C // rows) * (Wd // E)
+    per = -(-blocks // NT)
+    seen = Counter()
+    busy = set()
+    for tid, p_ in itertools.product(range(NT), range(per)):
+        blk = tid + p_ * NT
+        if blk >= blocks:
+            continue
+        busy.add(tid)
+        a, b = divmod(blk, Wd // E)
+        for rr in range(rows):
+            seen[(rows * a + rr, b)] += 1
+    assert sorted(seen) == [(r, b) for r in range(C) for b in range(Wd // E)]
+    assert set(seen.values()) == {1}
+    if vecs >= NT:
+        assert len(busy) == NT
+
+
+@pytest.mark.parametrize("S, C, NW", [(64, 32, 4), (128, 32, 4), (256, 32, 8)])
+def test_lean_query_features_are_converted_in_place_by_one_thread(S, C, NW):
+    # Lean output pass: the hash writes Phi_Q's quad (row t, columns l R + 4 m
+    # .. + 3) into the W plane's hi / lo slots; in the mass phase thread
+    # (w, g, lr) reads rows 16 bi + lr, columns 16 sb + 4 g .. + 3 (sb = w +
+    # NW sbw) and writes W there.  Every quad is handled by exactly one
+    # thread, so the in-place conversion races with nobody.
+    P = Plane(True, S)
+    owner = Counter()
+    for w, g, lr, bi in itertools.product(range(NW), range(4), range(16), range(C // 16)):
+        for sbw in range(S // (16 * NW)):
+            sb = w + NW * sbw
+            owner[P.off4(16 * bi + lr, 16 * sb + 4 * g)] += 1
+    written = {P.off4(t, k0) for t in range(C) for k0 in range(0, S, 4)}
+    assert set(owner) == written and set(owner.values()) == {1}
+    # The hi and lo 8-byte slots of a quad lie in its row, apart from every
+    # other quad's.
+    slots = Counter()
+    for off in written:
+        slots[off] += 1
+        slots[off + P.lo_off] += 1
+    assert set(slots.values()) == {1}
+
+
 def sigma(x):
     return 1.0 / (1.0 + math.exp(-x))
 
