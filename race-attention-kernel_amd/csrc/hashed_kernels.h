@@ -540,7 +540,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
                 if constexpr (kLean)  // rows past the tile fall outside or_ and are dropped
-                    store4<TIn, kStoreP>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * 4, o[bi]);
+                    store4<TIn, kOutStorePolicy>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * 4, o[bi]);
                 else
                     OT::put(Os, 16 * bi + lr, 16 * cb + 4 * g, o[bi]);
             }
