@@ -539,7 +539,11 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
                     }
                     o[bi] = mfma3<kSplit>(vh[kk], vl[kk], ph, pl, o[bi]);
                 }
-                if constexpr (kLean)  // rows past the tile fall outside or_ and are dropped
+                // Lean: rows past the tile fall outside or_ and are dropped.  The
+                // default (write-back) policy lets the two 64-byte halves of a
+                // 128-byte line, stored by two waves, meet in L2; streamed, lines
+                // left half written and reached HBM twice (1.23x the bytes).
+                if constexpr (kLean)
                     store4<TIn, kOutStorePolicy>(or_, ((r0 + 16 * bi + lr) * D + 16 * cb + 4 * g) * 4, o[bi]);
                 else
                     OT::put(Os, 16 * bi + lr, 16 * cb + 4 * g, o[bi]);
