@@ -107,6 +107,11 @@ def noncausal_bwd_phases(S: int, d: int, tiles: int) -> list:
     return BWD_PHASES[False]
 
 
+# Steps of the per-kernel (event-marked) region: each holds up to 66 HIP
+# events, so it does not grow with --steps.
+PROFILED_STEPS = 50
+
+
 class HipEvents:
     """hipEvent_t handles from the HIP runtime torch already loaded."""
 
@@ -151,8 +156,12 @@ class HipEvents:
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 2000 timed steps (about 0.3 s at cfg2): after a host-side pause the
+    # GPU's clock ramps up over several milliseconds, which a window of a few
+    # steps would mostly measure (cfg2 forward, 20 steps: 3190-3220 M tokens/s;
+    # 200 after 2000 warmup, or 2000 after 5: 3345).
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg2")
     ap.add_argument("--pass", dest="pass_",
                     choices=["fwd", "bwd", "fwdbwd", "module", "module_twostep", "alg1", "decode"],
@@ -417,7 +426,8 @@ def bench_alg1(args) -> int:
         del src, dst
 
     events = HipEvents()
-    per_step = [events.array(8) for _ in range(args.steps)]
+    n_prof = min(args.steps, PROFILED_STEPS)
+    per_step = [events.array(8) for _ in range(n_prof)]
     warm = events.array(8)
     for _ in range(args.warmup):
         plain()
@@ -434,7 +444,7 @@ def bench_alg1(args) -> int:
     wall = time.perf_counter() - t0
     ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
     n = 0
-    for i in range(args.steps):
+    for i in range(n_prof):
         st_, n = abi.alg1_fwd_profiled(*ptrs, None, sh, args.tile, variant, ws.data_ptr(), ws_bytes,
                                        stream, per_step[i])
         check(st_)
@@ -539,7 +549,8 @@ def bench_decode(args) -> int:
         check(abi.fwd_carry(*ptrs, sh, opts, ws.data_ptr(), ws_bytes, stream))
 
     events = HipEvents()
-    per_step = [events.array(8) for _ in range(args.steps)]
+    n_prof = min(args.steps, PROFILED_STEPS)
+    per_step = [events.array(8) for _ in range(n_prof)]
     for _ in range(args.warmup):
         plain()
     torch.cuda.synchronize()
@@ -553,7 +564,7 @@ def bench_decode(args) -> int:
     wall = time.perf_counter() - t0
     ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
     n = 0
-    for i in range(args.steps):
+    for i in range(n_prof):
         st_, n = abi.fwd_carry_profiled(*ptrs, sh, opts, ws.data_ptr(), ws_bytes, stream, per_step[i])
         check(st_)
     torch.cuda.synchronize()
@@ -764,7 +775,8 @@ def measure(args, T: int) -> dict:
 
     events = HipEvents()
     max_launches = 64
-    per_step = [events.array(max_launches + 2) for _ in range(args.steps)]
+    n_prof = min(args.steps, PROFILED_STEPS)
+    per_step = [events.array(max_launches + 2) for _ in range(n_prof)]
     warm = events.array(max_launches + 2)
 
     for _ in range(args.warmup):
@@ -784,14 +796,14 @@ def measure(args, T: int) -> dict:
     wall = time.perf_counter() - t0
     ms_per_step = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
 
-    # Timed region 2 (per-kernel durations): K profiled steps, which put an
-    # event before the first launch and after every launch.
+    # Timed region 2 (per-kernel durations): min(K, PROFILED_STEPS) profiled
+    # steps, which put an event before the first launch and after every launch.
     n_events = 0
-    for i in range(args.steps):
+    for i in range(n_prof):
         n_events = profiled(per_step[i])
     torch.cuda.synchronize()
 
-    profiled_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1]) / args.steps
+    profiled_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1]) / n_prof
     # Intervals between consecutive events; the forward's last event and the
     # backward's first one bracket nothing and are dropped below.
     n_gaps = n_events - 1
