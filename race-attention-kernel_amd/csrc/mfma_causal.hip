@@ -484,9 +484,14 @@ hipError_t launch_tile_sums_mfma(const void* k, const void* v, float* records, c
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel) {
     if (kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(S, d, dtype))
         return direct_output_tiles_per_cu();
-    // S = d = 64 keeps four workgroups resident per CU (one round); the others
-    // run one or two per CU over two or more rounds; S = 256 prefers longer
-    // tiles (fewer 132 KB records to scan).
+    // fp32 S = d = 64 (the workgroup output pass, four resident per CU):
+    // two tiles per CU.  Measured over 2000-step windows at cfg2 (T = 65536):
+    // 1024-token tiles 3536 M tokens/s against 3351 for 512 and 2337 for 2048;
+    // the hashed module 3051 against 3003.  The longer tiles halve the
+    // records and the scan and start half as many workgroups on the same
+    // loads.  The others run one or two per CU over two or more rounds; S =
+    // 256 prefers longer tiles (fewer 132 KB records to scan).
+    if (S == 64 && d == 64 && dtype == RACE_F32) return 2;
     return S >= 256 ? 2 : 4;
 }
 
