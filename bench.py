@@ -8,8 +8,10 @@ values) generated on the GPU and resident in HBM before the timed region.  A "st
 race_fused_fwd pass over that batch: every kernel of the op, through the C
 ABI (include/race_mi355x.h), with caller-owned output and workspace.
 
-Timing: W untimed warmup steps, then two timed regions, each of K steps
-bracketed by torch.cuda.synchronize() on both sides.  The first runs plain
+Timing: W untimed warmup steps, then an untimed clock-settling phase (plain
+steps until --settle-ms of GPU time has passed, 250 by default; reported as
+config.settle_ms and config.settle_steps), then two timed regions, each of K
+steps bracketed by torch.cuda.synchronize() on both sides.  The first runs plain
 race_fwd steps back to back on the stream between two HIP events: `value` =
 N*T / (mean step time) in M tokens/s.  The second runs race_fwd_profiled,
 which records a HIP event on the launch stream before the first kernel and
@@ -45,7 +47,7 @@ instead of the JSON line.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5]
                        [--pass fwd|bwd|fwdbwd|module] [--T T] [--kernel auto|valu|mfma|mfma_wg|single]
                        [--tile N] [--no-cpu-baseline] [--no-max-t] [--sweep]
-                       [--calibrate-copy MIB]
+                       [--calibrate-copy MIB] [--settle-ms MS]
 """
 from __future__ import annotations
 
@@ -110,6 +112,40 @@ def noncausal_bwd_phases(S: int, d: int, tiles: int) -> list:
 # Steps of the per-kernel (event-marked) region: each holds up to 66 HIP
 # events, so it does not grow with --steps.
 PROFILED_STEPS = 50
+
+# Untimed clock-settling phase run after the warmup steps and right before
+# the timed regions: plain steps until this much GPU time has passed.  The
+# GPU sits idle while the CPU baseline runs, and its clock then ramps over
+# several milliseconds of load; without this phase a window of 20 steps
+# (about 3.6 ms at cfg2) measured mostly that ramp.
+SETTLE_MS = 250.0
+SETTLE_MAX_STEPS = 200000
+
+
+def settle(plain, stream, events, target_ms: float) -> dict:
+    """Runs plain() steps back to back, in batches that double, until the
+    batches' GPU time (HIP events on `stream`) reaches target_ms; returns
+    {"settle_ms": GPU ms spent, "settle_steps": steps run}.  Untimed: nothing
+    here enters `value`."""
+    import torch
+
+    if target_ms <= 0:
+        return {"settle_ms": 0.0, "settle_steps": 0}
+    ev = events.array(2)
+    spent, steps, batch = 0.0, 0, 4
+    while spent < target_ms and steps < SETTLE_MAX_STEPS:
+        events.record(ev[0], stream)
+        for _ in range(batch):
+            plain()
+        events.record(ev[1], stream)
+        torch.cuda.synchronize()
+        dt = events.elapsed_ms(ev[0], ev[1])
+        spent += dt
+        steps += batch
+        # Aim the next batch at the time still missing, at most doubling.
+        per_step = max(dt / batch, 1e-4)
+        batch = int(min(2 * batch, max(4, (target_ms - spent) / per_step + 1)))
+    return {"settle_ms": round(spent, 2), "settle_steps": steps}
 
 
 class HipEvents:
@@ -185,6 +221,10 @@ def parse_args():
                     help="measure the pass at T = 512 ... 65536 and print a markdown table instead")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before timing (rocprofv3 counter scale)")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="GPU milliseconds of untimed plain steps between the warmup and the timed "
+                         "regions, so the clock has settled (0 turns the phase off); reported as "
+                         "config.settle_ms and config.settle_steps")
     return ap.parse_args()
 
 
@@ -434,6 +474,7 @@ def bench_alg1(args) -> int:
         check(abi.alg1_fwd_profiled(*ptrs, None, sh, args.tile, variant, ws.data_ptr(), ws_bytes,
                                     stream, warm)[0])
     torch.cuda.synchronize()
+    settled = settle(plain, stream, events, args.settle_ms)
     bracket = events.array(2)
     t0 = time.perf_counter()
     events.record(bracket[0], stream)
@@ -483,7 +524,7 @@ def bench_alg1(args) -> int:
             "workload": f"alg1: causal Algorithm 1 with hashing, BH={BH} T={T} d={D} P={P} L={L} "
                         f"beta=1/sqrt(d) bf16, {args.alg1_variant} variant",
             "BH": BH, "T": T, "D": D, "P": P, "L": L, "S": S, "variant": args.alg1_variant,
-            "tile_tokens": tile, "launches_per_step": len(gaps),
+            "tile_tokens": tile, "launches_per_step": len(gaps), **settled,
             "kernel_ms": {names[j]: round(gaps[j], 5) for j in range(len(gaps))},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
             "peak_hbm_bytes_per_token": round(peak_bytes / T, 1),
@@ -554,6 +595,7 @@ def bench_decode(args) -> int:
     for _ in range(args.warmup):
         plain()
     torch.cuda.synchronize()
+    settled = settle(plain, stream, events, args.settle_ms)
     bracket = events.array(2)
     t0 = time.perf_counter()
     events.record(bracket[0], stream)
@@ -595,7 +637,7 @@ def bench_decode(args) -> int:
             "workload": f"{args.workload} decode: race_fwd_carry of {T} token(s) per stream, N={N} "
                         f"S={S} d={d}, state carried in place from a 4096-token prompt",
             "N": N, "S": S, "d": d, "T": T, "kernel": args.kernel if args.kernel != "auto" else "decode",
-            "launches_per_step": len(gaps),
+            "launches_per_step": len(gaps), **settled,
             "kernel_ms": {names[j]: round(gaps[j], 6) for j in range(len(gaps))},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 6),
             "state_bytes": state_bytes,
@@ -783,6 +825,7 @@ def measure(args, T: int) -> dict:
         plain()
         profiled(warm)
     torch.cuda.synchronize()
+    settled = settle(plain, stream, events, args.settle_ms)
 
     # Timed region 1 (`value`): K plain steps, back to back on one stream,
     # between two events.
@@ -851,7 +894,7 @@ def measure(args, T: int) -> dict:
                         f"L={cfg.L} R={cfg.R} d={cfg.d} T={T} {'bf16' if es == 2 else 'fp32'}",
             "N": cfg.N, "T": T, "L": cfg.L, "R": cfg.R, "d": cfg.d, "causal": cfg.causal,
             "pass": args.pass_,
-            "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch,
+            "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch, **settled,
             "kernel_ms": {names[j]: round(phase_ms[j], 5) for j in range(n_launch)},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
             "profiled_ms_per_step": round(profiled_ms, 5),

@@ -52,3 +52,39 @@ def test_noncausal_backward_launch_names_follow_the_library():
     assert b.noncausal_bwd_phases(64, 64, 2) == ["query_grad", "key_grad"]
     assert b.noncausal_bwd_phases(64, 64, 8) == ["query_grad", "bwd_finalize", "key_grad"]
     assert b.noncausal_bwd_phases(256, 128, 2) == b.BWD_PHASES[False]
+
+
+
+class _FakeEvents:
+    """Stands in for HipEvents: each plain() step 'takes' 0.5 ms of GPU time."""
+
+    def __init__(self):
+        self.pending = 0
+
+    def array(self, n):
+        return [None] * n
+
+    def record(self, h, stream):
+        pass
+
+    def elapsed_ms(self, a, b):
+        dt, self.pending = 0.5 * self.pending, 0
+        return dt
+
+
+def test_settle_runs_until_the_gpu_time_is_reached(monkeypatch):
+    b = load_bench()
+    import torch
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    ev = _FakeEvents()
+    ran = []
+
+    def plain():
+        ran.append(1)
+        ev.pending += 1
+
+    got = b.settle(plain, 0, ev, 250.0)
+    assert got["settle_steps"] == len(ran)
+    # The last batch aims at the time still missing, so it overshoots by at most a step or two.
+    assert 250.0 <= got["settle_ms"] <= 251.0
+    assert b.settle(plain, 0, ev, 0.0) == {"settle_ms": 0.0, "settle_steps": 0}
