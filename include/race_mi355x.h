@@ -56,6 +56,9 @@ typedef int32_t race_status;
 #define RACE_SUCCESS 0
 #define RACE_ERROR_INVALID_VALUE 1 /* equals hipErrorInvalidValue */
 #define RACE_ERROR_SCRATCH_TOO_SMALL 2 /* race_fwd_noalloc only; equals hipErrorOutOfMemory */
+/* race_fwd_single_status only: a bounded wait of the one-read kernel gave up
+ * (outside the range of HIP's error codes, which other calls pass through). */
+#define RACE_ERROR_SINGLE_PASS_GAVE_UP 4096
 
 typedef enum race_dtype {
     RACE_F32 = 0,
@@ -152,6 +155,29 @@ race_status race_fwd_profiled(const void* probsQ, const void* probsK, const void
                               const race_options* opts, void* workspace, size_t workspace_bytes,
                               hipStream_t stream, hipEvent_t* events, int32_t max_events,
                               int32_t* n_events);
+
+/* Status of the last RACE_KERNEL_SINGLE forward whose workspace this is
+ * (workspace NULL: the current GPU's race_fwd_noalloc scratch).  Waits for
+ * `stream`, then reads the kernel's error word.  The one-read kernel's
+ * workgroups wait on flags other workgroups set, each wait bounded; a wait
+ * that gives up sets the word, the output rows of every tile whose prefix
+ * never arrived are NaN and `state` is NaN, and every other output is valid.
+ * Returns RACE_SUCCESS when no wait gave up, RACE_ERROR_SINGLE_PASS_GAVE_UP
+ * when one did, RACE_ERROR_INVALID_VALUE when the arguments do not name a
+ * RACE_KERNEL_SINGLE causal call or the workspace is too small.  The
+ * reference's causal forward has no cross-workgroup wait; like its
+ * launchers (src/causal_v2/kernels/race_causal_fwd.h:48-49) this reports the
+ * first error. */
+race_status race_fwd_single_status(const race_shape* shape, const race_options* opts,
+                                   const void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream);
+
+/* Test hook of the one-read kernel, no counterpart in the reference: while
+ * `on` is nonzero, every RACE_KERNEL_SINGLE launch in this process arms its
+ * error word as already set, so every bounded wait gives up at once and every
+ * workgroup exits normally (all outputs and `state` NaN, and
+ * race_fwd_single_status reports RACE_ERROR_SINGLE_PASS_GAVE_UP). */
+race_status race_single_pass_test_give_up(int32_t on);
 
 /* Bytes of the per-GPU scratch array race_fwd_noalloc takes its workspace
  * from.  32 MiB: at the automatic tile length on a 256-CU MI355X the cfg2

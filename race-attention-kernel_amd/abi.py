@@ -13,6 +13,7 @@ from . import _lib
 RACE_SUCCESS = 0
 RACE_ERROR_INVALID_VALUE = 1
 RACE_ERROR_SCRATCH_TOO_SMALL = 2
+RACE_ERROR_SINGLE_PASS_GAVE_UP = 4096
 RACE_NOALLOC_SCRATCH_BYTES = 32 << 20
 RACE_F32 = 0
 RACE_BF16 = 1
@@ -38,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "race_fwd",
     "race_fwd_profiled",
     "race_fwd_noalloc",
+    "race_fwd_single_status",
+    "race_single_pass_test_give_up",
     "race_fwd_carry_workspace_bytes",
     "race_fwd_carry",
     "race_fwd_carry_profiled",
@@ -110,6 +113,8 @@ def lib() -> ctypes.CDLL:
         L.race_fwd_profiled.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp, sz, vp,
                                         ctypes.POINTER(vp), i32, ctypes.POINTER(i32)]
         L.race_fwd_noalloc.argtypes = [vp, vp, vp, vp, vp, shp, i32, opp, vp]
+        L.race_fwd_single_status.argtypes = [shp, opp, vp, sz, vp]
+        L.race_single_pass_test_give_up.argtypes = [i32]
         L.race_fwd_carry_workspace_bytes.argtypes = [shp, opp, ctypes.POINTER(sz)]
         L.race_fwd_carry.argtypes = [vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp]
         L.race_fwd_carry_profiled.argtypes = [vp, vp, vp, vp, vp, vp, shp, opp, vp, sz, vp, vp, i32,
@@ -183,6 +188,20 @@ def fwd_noalloc(q: int, k: int, v: int, out: int, state: int | None, sh: RaceSha
     per-GPU scratch array); returns the status."""
     return lib().race_fwd_noalloc(q, k, v, out, state, ctypes.byref(sh), int(causal),
                                   ctypes.byref(opts) if opts is not None else None, stream)
+
+
+def fwd_single_status(sh: RaceShape, opts: RaceOptions, workspace: int | None, workspace_bytes: int,
+                      stream: int = 0) -> int:
+    """race_fwd_single_status: waits for `stream`, then reports whether a
+    bounded wait of the last one-read launch on this workspace gave up
+    (workspace None: the current GPU's no-alloc scratch)."""
+    return lib().race_fwd_single_status(ctypes.byref(sh), ctypes.byref(opts), workspace,
+                                        workspace_bytes, stream)
+
+
+def single_pass_test_give_up(on: bool) -> int:
+    """race_single_pass_test_give_up: preset the one-read kernel's error word."""
+    return lib().race_single_pass_test_give_up(int(bool(on)))
 
 
 def hashed_fwd_workspace_bytes(sh: RaceShape, planes_per_table: int, opts: RaceOptions | None = None):

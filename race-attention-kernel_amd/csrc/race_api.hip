@@ -359,6 +359,9 @@ const char* race_status_string(race_status status) {
         return "invalid value: unsupported shape or kernel, null or misaligned pointer, "
                "workspace too small, or tile length not a positive multiple of "
                "RACE_SUB_CHUNK_TOKENS";
+    if (status == RACE_ERROR_SINGLE_PASS_GAVE_UP)
+        return "one-read forward gave up: a bounded wait of RACE_KERNEL_SINGLE expired; the "
+               "output rows of the tiles whose prefix never arrived, and the state, are NaN";
     if (status == RACE_ERROR_SCRATCH_TOO_SMALL)
         return "scratch too small: the call needs more workspace than the "
                "RACE_NOALLOC_SCRATCH_BYTES race_fwd_noalloc holds per GPU; use race_fwd "
@@ -709,6 +712,37 @@ race_status race_fwd_noalloc(const void* probsQ, const void* probsK, const void*
     Marks none;
     return fwd_impl(probsQ, probsK, V, out, state, nullptr, shape, causal, opts, ws,
                     size_t(RACE_NOALLOC_SCRATCH_BYTES), stream, &none);
+}
+
+race_status race_fwd_single_status(const race_shape* shape, const race_options* opts,
+                                   const void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+    if (!opts || opts->kernel != RACE_KERNEL_SINGLE) return RACE_ERROR_INVALID_VALUE;
+    Problem p;
+    bool mfma = false;
+    race_status st = make_problem(shape, 1, opts, &mfma, &p);
+    if (st != RACE_SUCCESS) return st;
+    if (p.N == 0 || p.T == 0) return RACE_SUCCESS;  // nothing was launched
+    const FwdLayout l = fwd_layout(p, 1);
+    if (!workspace) {
+        void* ws = nullptr;
+        RACE_TRY(current_scratch(&ws));
+        workspace = ws;
+        workspace_bytes = size_t(RACE_NOALLOC_SCRATCH_BYTES);
+    }
+    if (!aligned16(workspace) || workspace_bytes < size_t(l.total()) * sizeof(float))
+        return RACE_ERROR_INVALID_VALUE;
+    const int* words = reinterpret_cast<const int*>(static_cast<const float*>(workspace) + l.records);
+    int word = 0;
+    RACE_TRY(hipMemcpyAsync(&word, words + single_pass_error_word(p.N, p.tiles), sizeof(int),
+                            hipMemcpyDeviceToHost, stream));
+    RACE_TRY(hipStreamSynchronize(stream));
+    return word != 0 ? RACE_ERROR_SINGLE_PASS_GAVE_UP : RACE_SUCCESS;
+}
+
+race_status race_single_pass_test_give_up(int32_t on) {
+    single_pass_preset_give_up(on != 0);
+    return RACE_SUCCESS;
 }
 
 race_status race_fwd_carry_workspace_bytes(const race_shape* shape, const race_options* opts,

@@ -334,5 +334,11 @@ bool single_pass_supported(const Problem& p, int cus);
 hipError_t launch_causal_single(const void* q, const void* k, const void* v, void* out,
                                 float* records, int* words, float* state, const float* init,
                                 const Problem& p, int cus, hipStream_t stream, Marks* marks);
+// Index in `words` of the error word: nonzero once a bounded wait gave up
+// (the affected output tiles and `state` then hold NaN).
+int64_t single_pass_error_word(int64_t N, int64_t tiles);
+// Test hook: while on, every launch arms the error word as already set, so
+// every bounded wait gives up at once and every workgroup exits normally.
+void single_pass_preset_give_up(bool on);
 
 }  // namespace race

@@ -31,13 +31,19 @@
 // emulates the protocol; dealing tiles out by launch index instead
 // deadlocks there).  Every wait is still bounded: after kSpSpinLimit polls it sets
 // the error word, and every later wait gives up at once, so the kernel always
-// ends (with the error word set and the output not valid).
+// ends.  A give-up is never silent: a tile whose prefix wait gave up computes
+// its output from a NaN prefix, so every output row of that tile is NaN, and a
+// scanner that gave up writes NaN into `state`; the host reads the error word
+// back with race_fwd_single_status.  The arming kernel can preset the error
+// word (a test hook), which makes every wait give up at once.
 //
 // Pipeline of a tile workgroup.  Tiles are NSUB sub-chunks of C = 32 tokens.
 // Step s stages sub-chunk s of the workgroup's tile sequence (phase 1) and
 // runs the output of sub-chunk s - L (phase 2), L = R - 1, from a ring of R
 // LDS slots, so a tile's totals are published L - NSUB steps before its
 // output starts and the scanner's latency hides behind that lag.
+#include <atomic>
+
 #include "causal_geo.h"
 
 namespace race {
@@ -82,16 +88,19 @@ __device__ __forceinline__ void drain_vm() { asm volatile("s_waitcnt vmcnt(0)" :
 __device__ __forceinline__ void settle(f32x4& x) { asm volatile("" : "+v"(x)); }
 
 // Polls *f until it reaches `want`; false once the spin limit is spent here or
-// the error word is set by any wave.
+// the error word is set by any wave (checked first, so a preset error word
+// fails every wait, ready or not).
 __device__ __forceinline__ bool wait_flag(const int* f, int want, int* ctl) {
     for (int i = 0; i < kSpSpinLimit; ++i) {
-        if (flag_load(f) >= want) return true;
         if (flag_load(ctl + kSpErr) != 0) return false;
+        if (flag_load(f) >= want) return true;
         __builtin_amdgcn_s_sleep(2);
     }
     flag_store(ctl + kSpErr, 1);
     return false;
 }
+
+__device__ __forceinline__ float quiet_nan() { return __builtin_bit_cast(float, 0x7fc00000u); }
 
 // A tile job: stream n and tile i of the job index v on an XCD with 2^mshift
 // streams (one or two).  Kept in scalar registers: buffer resources built
@@ -143,7 +152,11 @@ __device__ __forceinline__ void sp_scan(float* __restrict__ records, int* __rest
     int64_t pos = 0;
     int f = w0 ? poll(0) : 0;
     int idle = 0;
-    while (pos < tiles) {
+    // An error word set before the scan starts (a wait elsewhere gave up, or
+    // the test preset) stops it here: no prefix is published, so every tile
+    // wait of the stream gives up too.
+    const bool preset = __builtin_amdgcn_readfirstlane(flag_load(ctl + kSpErr)) != 0;
+    while (!preset && pos < tiles) {
         if (w0) {
             const bool ready = l < kSpWindow && pos + l < tiles && f >= kFlagTotals;
             const uint64_t not_ready = __ballot(!ready);
@@ -194,7 +207,13 @@ __device__ __forceinline__ void sp_scan(float* __restrict__ records, int* __rest
         if (w0 && l < r) __hip_atomic_fetch_add(fl + pos + l, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         pos += r;
     }
-    if (state && pos == tiles) {
+    if (state) {
+        // A scan that gave up leaves NaN, never a partial sum, in the state.
+        if (pos != tiles) {
+            const float nan = quiet_nan();
+            run0 = f32x4{nan, nan, nan, nan};
+            run1 = run0;
+        }
         float* sp = state + n * kStateFloats;
         *reinterpret_cast<f32x4*>(sp + 4 * c0) = run0;
         if (has_b) *reinterpret_cast<f32x4*>(sp + 4 * c1) = run1;
@@ -335,7 +354,7 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
         if (p2) {
             t2 = sp_tile(job_at(k2), x, mshift);
             if (j2 == 0) {
-                wait_flag(flags + t2.n * tiles + t2.i, kFlagPrefix, ctl);
+                const bool ready = wait_flag(flags + t2.n * tiles + t2.i, kFlagPrefix, ctl);
                 const __amdgpu_buffer_rsrc_t pr =
                     make_rsrc(records + (t2.n * tiles + t2.i) * rec, rec * int64_t(sizeof(float)));
 #pragma unroll
@@ -356,6 +375,15 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
                 for (int sb = 0; sb < NSB; ++sb) settle(b0[sb]);
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) a0[rr] = a[rr];
+                // A prefix that never arrived: NaN reaches every W and every
+                // product of the tile, so each of its output rows is NaN.
+                if (!ready) {
+                    const float nan = quiet_nan();
+#pragma unroll
+                    for (int sb = 0; sb < NSB; ++sb) b0[sb] = f32x4{nan, nan, nan, nan};
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) a0[rr] = nan;
+                }
             }
         }
         const int rows2 = p2 ? rows_of(t2) : 0;
@@ -553,11 +581,15 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
     }
 }
 
-// Zeroes the tile flags and the control words ahead of the main kernel.
-__global__ __launch_bounds__(kThreads) void single_arm_kernel(int* __restrict__ words, int64_t count) {
+// Zeroes the tile flags and the control words ahead of the main kernel; the
+// error word (index err_at) gets err_value, 0 unless the test hook presets it.
+__global__ __launch_bounds__(kThreads) void single_arm_kernel(int* __restrict__ words, int64_t count,
+                                                              int64_t err_at, int err_value) {
     for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += int64_t(gridDim.x) * kThreads)
-        words[i] = 0;
+        words[i] = i == err_at ? err_value : 0;
 }
+
+std::atomic<int> g_preset_give_up{0};
 
 template <typename TIn, int NSUB, int R>
 hipError_t launch_single(const void* q, const void* k, const void* v, void* out, float* records,
@@ -567,7 +599,8 @@ hipError_t launch_single(const void* q, const void* k, const void* v, void* out,
     if (p.tile != SG::kTile) return hipErrorInvalidValue;
     const int64_t nflags = single_pass_flag_words(p.N, p.tiles);
     const int64_t count = nflags + kSinglePassCtlWords;
-    single_arm_kernel<<<dim3(unsigned((count + kThreads - 1) / kThreads)), kThreads, 0, stream>>>(words, count);
+    single_arm_kernel<<<dim3(unsigned((count + kThreads - 1) / kThreads)), kThreads, 0, stream>>>(
+        words, count, nflags + kSpErr, g_preset_give_up.load() ? 1 : 0);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
@@ -594,6 +627,10 @@ bool single_pass_supported(const Problem& p, int cus) {
 }
 
 int single_pass_tile() { return kSinglePassTile; }
+
+int64_t single_pass_error_word(int64_t N, int64_t tiles) { return single_pass_flag_words(N, tiles) + kSpErr; }
+
+void single_pass_preset_give_up(bool on) { g_preset_give_up.store(on ? 1 : 0); }
 
 hipError_t launch_causal_single(const void* q, const void* k, const void* v, void* out,
                                 float* records, int* words, float* state, const float* init,

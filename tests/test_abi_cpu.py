@@ -36,6 +36,19 @@ def test_abi_version_and_status_strings(race):
     assert abi.lib().race_abi_version() == 1
     assert abi.status_string(0) == "success"
     assert "invalid value" in abi.status_string(1)
+    assert "gave up" in abi.status_string(abi.RACE_ERROR_SINGLE_PASS_GAVE_UP)
+
+
+def test_single_status_refuses_other_kernels_on_the_host(race):
+    # race_fwd_single_status names a RACE_KERNEL_SINGLE call; anything else is
+    # refused before any device is touched.
+    from race_attention_kernel_amd import abi
+
+    sh = abi.shape(8, 4096, 4, 16, 64)
+    for kernel in (abi.RACE_KERNEL_AUTO, abi.RACE_KERNEL_MFMA, abi.RACE_KERNEL_VALU):
+        assert abi.fwd_single_status(sh, abi.options(0, kernel), 16, 1 << 20, 0) == \
+            abi.RACE_ERROR_INVALID_VALUE
+    assert abi.single_pass_test_give_up(False) == 0
 
 
 @pytest.mark.parametrize("L, R, d, ok", [(4, 16, 64, True), (8, 32, 128, True), (1, 1, 1, True),

@@ -167,3 +167,54 @@ def test_single_through_autograd(race, oracle, cuda):
     out.backward(g.to(cuda))
     torch.cuda.synchronize()
     check_grads(oracle, q, k, v, g, out.detach(), qg.grad, kg.grad, vg.grad, FP32_TOL)
+
+
+def test_single_give_up_is_visible(race, oracle, cuda):
+    # With the test hook on, the arming kernel presets the error word, so every
+    # bounded wait gives up at its first poll and every workgroup exits
+    # normally.  No tile's prefix arrives: every output row is NaN, the state
+    # is NaN, and race_fwd_single_status reports the give-up; with the hook
+    # off the next call on the same workspace is correct and reports success.
+    import math
+
+    from race_attention_kernel_amd import abi
+
+    N, T = 8, 3000
+    q, k, v = race.make_inputs(N, T, 4, 16, 64, seed=21)
+    qg, kg, vg = q.to(cuda), k.to(cuda), v.to(cuda)
+    sh = abi.shape(N, T, 4, 16, 64, abi.RACE_F32)
+    opts = abi.options(0, abi.RACE_KERNEL_SINGLE)
+    st, nbytes, _, _ = abi.fwd_workspace_bytes(sh, True, opts)
+    assert st == 0
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    out = torch.zeros_like(vg)
+    state = torch.zeros(N, 64 * 64 + 64, device=cuda)
+
+    def call():
+        return abi.fwd(qg.data_ptr(), kg.data_ptr(), vg.data_ptr(), out.data_ptr(), state.data_ptr(), sh,
+                       True, opts, ws.data_ptr(), nbytes, stream)
+
+    say("single give-up preset", N, T)
+    assert abi.single_pass_test_give_up(True) == 0
+    try:
+        assert call() == 0  # the launch itself succeeds
+        got = abi.fwd_single_status(sh, opts, ws.data_ptr(), nbytes, stream)
+    finally:
+        abi.single_pass_test_give_up(False)
+    assert got == abi.RACE_ERROR_SINGLE_PASS_GAVE_UP
+    assert "gave up" in abi.status_string(got)
+    assert torch.isnan(out).all()
+    assert torch.isnan(state).all()
+
+    say("single after the preset", N, T)
+    assert call() == 0
+    assert abi.fwd_single_status(sh, opts, ws.data_ptr(), nbytes, stream) == 0
+    ref, fin = oracle.causal_recurrence(to_np(q), to_np(k), to_np(v), want_state=True, nthreads=16)
+    assert per_stream_rel_err(out.cpu().numpy(), ref) <= FP32_TOL
+    assert per_stream_rel_err(state.cpu().numpy(), fin) <= FP32_TOL
+    assert not math.isnan(float(out.abs().max()))
+    # The status call refuses arguments that do not name a one-read call.
+    assert abi.fwd_single_status(sh, abi.options(0, 0), ws.data_ptr(), nbytes, stream) == \
+        abi.RACE_ERROR_INVALID_VALUE
+    assert abi.fwd_single_status(sh, opts, ws.data_ptr(), nbytes - 4, stream) == abi.RACE_ERROR_INVALID_VALUE

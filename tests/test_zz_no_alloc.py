@@ -56,6 +56,31 @@ def test_noalloc_equals_race_fwd_on_two_calls_in_a_row(race, ext, cuda, causal):
         assert torch.equal(got2, want)
 
 
+def test_noalloc_one_read_forward_rearms_its_flags(race, ext, cuda):
+    # RACE_KERNEL_SINGLE keeps ticket counters and tile flags in the scratch
+    # array after its records; every call re-arms them (zeroes them ahead of
+    # the main kernel).  Two calls in a row, the second smaller, on the array
+    # the earlier tests left behind: both equal race_fwd bitwise and leave
+    # the error word clear.
+    from race_attention_kernel_amd import abi
+
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the one-read forward runs on a full MI355X (256 CUs)")
+    kernel = abi.RACE_KERNEL_SINGLE
+    stream = torch.cuda.current_stream().cuda_stream
+    for i, (N, T, dtype) in enumerate([(16, 4096, torch.float32), (8, 1500, torch.bfloat16)]):
+        say("noalloc single call", i, N, T, dtype)
+        q, k, v = race.make_inputs(N, T, 4, 16, 64, seed=90 + i, dtype=dtype, device=cuda,
+                                   gen_device="cuda")
+        got, got_state = _noalloc(abi, q, k, v, True, 0, kernel, True)
+        sh = abi.shape(N, T, 4, 16, 64, abi.RACE_BF16 if dtype == torch.bfloat16 else abi.RACE_F32)
+        assert abi.fwd_single_status(sh, abi.options(0, kernel), None, 0, stream) == 0
+        want, want_state = ext.forward(q, k, v, True, 0, kernel, True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        assert torch.equal(got_state, want_state)
+
+
 def test_noalloc_refuses_calls_past_its_scratch(race, cuda):
     from race_attention_kernel_amd import abi
 
