@@ -53,7 +53,8 @@ def test_cfg2_sweep_matches_oracle(race, ext, oracle, cuda, kernel, T):
 @pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("L, R, d", [(1, 1, 1), (1, 2, 16), (2, 8, 32), (4, 16, 64), (3, 5, 7),
-                                     (8, 32, 128), (16, 16, 128), (4, 16, 128), (8, 16, 64)])
+                                     (8, 32, 128), (16, 16, 128), (4, 16, 128), (8, 16, 64),
+                                     (16, 16, 64)])
 @pytest.mark.parametrize("T", [1, 63, 65, 300])
 def test_shapes_and_ragged_lengths(race, ext, oracle, cuda, kernel, dtype, L, R, d, T):
     skip_unless_kernel(ext, kernel, L, R, d)

@@ -36,8 +36,17 @@ def oracle_out(oracle, k, q, v, planes, L, K):
     return oracle.causal_recurrence(pq, pk, v.cpu().double().numpy())
 
 
+# (L, K, d): every (S, d) specialization the fused kernels take (S = L 2^K in
+# {64, 128, 256}, d in {64, 128}), one, two, three and four 16-plane blocks
+# (L K up to 16, 32, 48, 64), and plane counts K = 2 ... 8.
 SHAPES = [(4, 4, 64), (2, 5, 64), (8, 3, 64), (16, 2, 64), (8, 4, 128), (4, 5, 128), (8, 5, 128),
-          (1, 6, 64), (4, 6, 128)]
+          (1, 6, 64), (4, 6, 128),
+          (2, 5, 128),   # S = 64, d = 128
+          (8, 4, 64),    # S = 128, d = 64, L K = 32
+          (16, 4, 64),   # S = 256, d = 64, L K = 64: four plane blocks
+          (32, 2, 128),  # S = 128, d = 128, L K = 64
+          (1, 7, 64),    # S = 128, K = 7
+          (1, 8, 128)]   # S = 256, K = 8
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
