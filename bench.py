@@ -10,13 +10,18 @@ ABI (include/race_mi355x.h), with caller-owned output and workspace.
 
 Timing: W untimed warmup steps, then an untimed clock-settling phase (plain
 steps until --settle-ms of GPU time has passed, 250 by default; reported as
-config.settle_ms and config.settle_steps), then two timed regions, each of K
+config.settle_ms and config.settle_steps), then timed regions, each of K
 steps bracketed by torch.cuda.synchronize() on both sides.  The first runs plain
 race_fwd steps back to back on the stream between two HIP events: `value` =
-N*T / (mean step time) in M tokens/s.  The second runs race_fwd_profiled,
-which records a HIP event on the launch stream before the first kernel and
-after every kernel; the per-kernel durations behind `roofline` come from it
-(its step time, with the extra events, is `profiled_ms_per_step`).
+N*T / (mean step time) in M tokens/s.  Every step reads the same inputs
+(--input-sets R cycles through R sets instead), so part of them may still sit
+in the 256 MB memory-side cache from the step before.  The second runs
+race_fwd_profiled, which records a HIP event on the launch stream before the
+first kernel and after every kernel; the per-kernel durations behind
+`roofline` come from it (its step time, with the extra events, is
+`profiled_ms_per_step`).  For the forward pass a third region runs K plain
+steps alternating two input sets, which no step finds left over from the
+step before: config.fresh_inputs.
 
 roofline: the dominant kernel's algorithmic HBM bytes per launch (each
 operand it streams read once, its output written once: bytes per
@@ -119,6 +124,8 @@ PROFILED_STEPS = 50
 # several milliseconds of load; without this phase a window of 20 steps
 # (about 3.6 ms at cfg2) measured mostly that ramp.
 SETTLE_MS = 250.0
+# Input sets the forward steps cycle through by default (--input-sets).
+INPUT_SETS = 1
 SETTLE_MAX_STEPS = 200000
 
 
@@ -221,6 +228,10 @@ def parse_args():
                     help="measure the pass at T = 512 ... 65536 and print a markdown table instead")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before timing (rocprofv3 counter scale)")
+    ap.add_argument("--input-sets", type=int, default=INPUT_SETS, metavar="R",
+                    help="the forward's steps cycle through R input sets (probsQ, probsK, V, out); "
+                         "with R >= 2 no step finds the previous step's operands in the 256 MB "
+                         "memory-side cache; reported as config.input_sets")
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                     help="GPU milliseconds of untimed plain steps between the warmup and the timed "
                          "regions, so the clock has settled (0 turns the phase off); reported as "
@@ -691,6 +702,28 @@ def measure(args, T: int) -> dict:
     out = torch.empty_like(v)
     stream = torch.cuda.current_stream().cuda_stream
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+    # The forward's steps cycle through `input_sets` sets of operands (other
+    # seeds), so that with two or more a step never re-reads the previous
+    # step's bytes from the memory-side cache.  Their memory is left out of
+    # the peak-HBM figure, which describes one call.
+    # A third timed region (`config.fresh_inputs`) alternates two sets, so its
+    # figure never profits from the previous call's operands.
+    n_sets = max(1, args.input_sets) if args.pass_ == "fwd" else 1
+    n_alloc = max(n_sets, 2) if args.pass_ == "fwd" else 1
+    sets = [(q, k, v, out)]
+    extra_bytes = 0
+    for j in range(1, n_alloc):
+        qj, kj, vj = race.config_inputs(cfg, T, seed=j, device=dev, gen_device="cuda")
+        sets.append((qj, kj, vj, torch.empty_like(vj)))
+        extra_bytes += sum(x.numel() * x.element_size() for x in sets[-1])
+    ptr_sets = [tuple(x.data_ptr() for x in st_) for st_ in sets]
+    turn = [0]
+    active = [n_sets]
+
+    def fwd_ptrs():
+        p_ = ptr_sets[turn[0] % active[0]]
+        turn[0] += 1
+        return p_
 
     def check(st_):
         if st_ != 0:
@@ -753,7 +786,7 @@ def measure(args, T: int) -> dict:
         if run_hash:
             hash_both()
         if run_fwd:
-            check(abi.fwd(*ptrs, sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
+            check(abi.fwd(*fwd_ptrs(), sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes, stream))
         if run_bwd:
             if cfg.causal:
                 check(abi.causal_bwd(*bptrs, *gptrs, sh, bopts, bws.data_ptr(), bws_bytes, stream))
@@ -777,7 +810,7 @@ def measure(args, T: int) -> dict:
             n_used = 3
         if run_fwd:
             tail = (ctypes.c_void_p * (len(evs) - n_used)).from_buffer(evs, n_used * ctypes.sizeof(ctypes.c_void_p))
-            st_, n = abi.fwd_profiled(*ptrs, sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
+            st_, n = abi.fwd_profiled(*fwd_ptrs(), sptr, sh, cfg.causal, opts, ws.data_ptr(), ws_bytes,
                                       stream, tail)
             check(st_)
             n_used += n
@@ -847,6 +880,22 @@ def measure(args, T: int) -> dict:
     torch.cuda.synchronize()
 
     profiled_ms = events.elapsed_ms(per_step[0][0], per_step[-1][n_events - 1]) / n_prof
+
+    # Timed region 3 (forward only): K plain steps alternating two input sets.
+    fresh = None
+    if args.pass_ == "fwd":
+        active[0] = 2
+        events.record(bracket[0], stream)
+        for _ in range(args.steps):
+            plain()
+        events.record(bracket[1], stream)
+        torch.cuda.synchronize()
+        active[0] = n_sets
+        fresh_ms = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
+        fresh = {"input_sets": 2, "ms_per_step": round(fresh_ms, 5),
+                 "m_tokens_per_s": round(cfg.N * T / (fresh_ms * 1e-3) / 1e6, 3),
+                 "whole_op_frac": round(op_bytes(args.pass_, cfg, T, es) / (fresh_ms * 1e-3) / 1e9
+                                        / PEAK_HBM_GBPS, 4)}
     # Intervals between consecutive events; the forward's last event and the
     # backward's first one bracket nothing and are dropped below.
     n_gaps = n_events - 1
@@ -864,7 +913,8 @@ def measure(args, T: int) -> dict:
     dom = max(range(n_launch), key=lambda j: phase_ms[j])
     dom_bytes = phase_bytes(names[dom], cfg, T, es, tiles, rec)
     achieved = dom_bytes / (phase_ms[dom] * 1e-3) / 1e9
-    peak_bytes = torch.cuda.max_memory_allocated(dev)
+    # The extra input sets are left out of the peak: it describes one call.
+    peak_bytes = torch.cuda.max_memory_allocated(dev) - extra_bytes
     events.destroy()
 
     NT = cfg.N * T
@@ -895,6 +945,8 @@ def measure(args, T: int) -> dict:
             "N": cfg.N, "T": T, "L": cfg.L, "R": cfg.R, "d": cfg.d, "causal": cfg.causal,
             "pass": args.pass_,
             "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch, **settled,
+            "input_sets": n_sets,
+            "fresh_inputs": fresh,
             "kernel_ms": {names[j]: round(phase_ms[j], 5) for j in range(n_launch)},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
             "profiled_ms_per_step": round(profiled_ms, 5),
@@ -918,7 +970,7 @@ def measure(args, T: int) -> dict:
         },
         "cpu_baseline": None,
     }
-    del q, k, v, out, ws
+    del q, k, v, out, ws, sets, ptr_sets
     if run_bwd:
         del g, dq, dk, dv, bws
     if run_hash or run_hashed:

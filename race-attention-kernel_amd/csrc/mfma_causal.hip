@@ -42,6 +42,19 @@
 // ds_read_b64_tr_b16 (Plane::frag_tr), two reads per fragment and plane.
 #include "causal_geo.h"
 
+// fp32 S = d = 64 output pass: two sub-chunks of operands in flight in
+// registers ahead of the one in LDS, at two workgroups per CU (the launch
+// bound that leaves room for them).  With the automatic 1024-token tiles two
+// workgroups per CU is what the launch holds anyway; measured at cfg2
+// (20 steps after the settling phase, one box): 3755 -> 3794 M tokens/s with
+// the same inputs every step, 3469 -> 3510 with two input sets alternating.
+#ifndef RACE_OUT_F32_DEPTH
+#define RACE_OUT_F32_DEPTH 2
+#endif
+#ifndef RACE_OUT_F32_6464_MINBLOCKS
+#define RACE_OUT_F32_6464_MINBLOCKS 2
+#endif
+
 namespace race {
 namespace {
 
@@ -178,6 +191,9 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     constexpr int kQChunks = C * QT::kChunks;
     constexpr int kQPer = (kQChunks + G::kT - 1) / G::kT;
     constexpr int kStoreP = std::is_same<TIn, float>::value ? kOutWgStorePolicyF32 : kOutStorePolicy;
+    constexpr int kQP = std::is_same<TIn, float>::value ? kOutQPolicyF32 : kOutQPolicy;
+    // Sub-chunks of operands in flight in registers ahead of the one in LDS.
+    constexpr int kDepth = (std::is_same<TIn, float>::value && S == 64 && D == 64) ? RACE_OUT_F32_DEPTH : 1;
 
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -222,14 +238,14 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
             for (int i = 0; i < kQPer; ++i) {
                 const int qi = tid + i * G::kT;
                 if (kQChunks % G::kT == 0 || qi < kQChunks)
-                    qr[i] = buf_load16<kOutQPolicy>(qr_, r0 * S * int(sizeof(TIn)) + 16 * qi);
+                    qr[i] = buf_load16<kQP>(qr_, r0 * S * int(sizeof(TIn)) + 16 * qi);
             }
         } else {
 #pragma unroll
             for (int sbw = 0; sbw < SBW; ++sbw)
 #pragma unroll
                 for (int bi = 0; bi < NBI; ++bi)
-                    qr[sbw][bi] = load_q4<TIn, kOutQPolicy>(
+                    qr[sbw][bi] = load_q4<TIn, kQP>(
                         qr_, ((r0 + 16 * bi + lr) * S + 16 * (w + NW * sbw) + 4 * g) * int(sizeof(TIn)));
         }
     };
@@ -261,8 +277,8 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
                 for (int bi = 0; bi < NBI; ++bi) qc[sbw][bi] = qr[sbw][bi];
         }
         // Prefetch (past the tile: zeros, never used).
-        st.load(kr, vr, r0 + C);
-        load_q(qr, r0 + C);
+        st.load(kr, vr, r0 + kDepth * C);
+        load_q(qr, r0 + kDepth * C);
         __syncthreads();
 
         // 1 + 2: running mass and W.
@@ -394,12 +410,19 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
         }
     };
 
-    KVStage<TIn, S, D, C, kOutKVPolicy, NW> st;
-    QRegs qr;
-    st.load(kr, vr, 0);
-    load_q(qr, 0);
+    KVStage<TIn, S, D, C, kOutKVPolicy, NW> st[kDepth];
+    QRegs qr[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        st[d].load(kr, vr, d * C);
+        load_q(qr[d], d * C);
+    }
     int r0 = 0;
-    for (; r0 < rows; r0 += C) sub_chunk(st, qr, r0);
+    for (; r0 < rows; r0 += kDepth * C) {
+        sub_chunk(st[0], qr[0], r0);
+        // A sub-chunk past a ragged tile end reads zeros and stores nothing.
+        if constexpr (kDepth == 2) sub_chunk(st[1], qr[1], r0 + C);
+    }
     __syncthreads();
     if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);
 }
@@ -446,7 +469,8 @@ hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out,
     // workgroup) so four workgroups share a CU and keep four times the loads
     // in flight; the output pass there is bound by bytes in flight, not math.
     if (p.S == 64 && p.d == 64)
-        return launch_mfma_family<TIn, 64, 64, 32, 4>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, 64, 64, 32, std::is_same<TIn, float>::value ? RACE_OUT_F32_6464_MINBLOCKS : 4>(
+            q, k, v, out, records, state, p, stream, marks);
     if (p.S == 64 && p.d == 128)
         return launch_mfma_family<TIn, 64, 128, 64, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 128 && p.d == 64)
@@ -464,7 +488,9 @@ template <typename TIn>
 hipError_t dispatch_sums(const void* k, const void* v, float* records, const Problem& p,
                          hipStream_t stream) {
     // The K1 launches of dispatch_mfma, shape for shape.
-    if (p.S == 64 && p.d == 64) return launch_sums_family<TIn, 64, 64, 32, 4>(k, v, records, p, stream);
+    if (p.S == 64 && p.d == 64)
+        return launch_sums_family<TIn, 64, 64, 32, std::is_same<TIn, float>::value ? RACE_OUT_F32_6464_MINBLOCKS : 4>(
+            k, v, records, p, stream);
     if (p.S == 64 && p.d == 128) return launch_sums_family<TIn, 64, 128, 64, 1>(k, v, records, p, stream);
     if (p.S == 128 && p.d == 64) return launch_sums_family<TIn, 128, 64, 64, 1>(k, v, records, p, stream);
     if (p.S == 128 && p.d == 128) return launch_sums_family<TIn, 128, 128, 64, 1>(k, v, records, p, stream);

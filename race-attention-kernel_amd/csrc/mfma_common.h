@@ -121,7 +121,23 @@ constexpr int kPolicyStream = 2;
 #ifndef RACE_ALG1_STORE_POLICY
 #define RACE_ALG1_STORE_POLICY 0
 #endif
+#ifndef RACE_SUMS_F32_LOAD_POLICY
+#define RACE_SUMS_F32_LOAD_POLICY 0
+#endif
+#ifndef RACE_OUT_Q_F32_POLICY
+#define RACE_OUT_Q_F32_POLICY 2
+#endif
 constexpr int kSumsLoadPolicy = RACE_SUMS_LOAD_POLICY;  // K1 reads of K and V
+// fp32 tokens at S = d = 64: K1 (tile_sums_quad_kernel) walks each tile from
+// its end to its start with cache-allocating loads, so the 256 MB memory-side
+// cache holds the start of every tile when the output pass begins there; the
+// output pass streams Q past the cache (`nt`) so it does not evict them.
+// Measured at cfg2 (T = 65536, one box, 20 steps after the settling phase)
+// with one-wave-per-tile K1 walking backward: 3527 -> 3748 M tokens/s with
+// the same inputs every step, 3210 -> 3372 with two input sets alternating
+// (no step finds its inputs left over from the step before).
+constexpr int kSumsF32LoadPolicy = RACE_SUMS_F32_LOAD_POLICY;
+constexpr int kOutQPolicyF32 = RACE_OUT_Q_F32_POLICY;
 constexpr int kOutKVPolicy = RACE_OUT_KV_POLICY;        // K3 reads of K and V read once
 constexpr int kOutQPolicy = RACE_OUT_Q_POLICY;          // K3 reads of Q
 constexpr int kOutStorePolicy = RACE_OUT_STORE_POLICY;  // register-direct K3 writes of out

@@ -13,7 +13,8 @@
 //
 // tile_sums_direct_kernel: per-tile totals B_tile = K^T V and A_tile =
 // colsum(K) (the K1 of the causal decomposition, src/causal_v2/kernels/
-// race_causal_fwd.h:23-27), one wave per tile.
+// race_causal_fwd.h:23-27), one wave per tile; tile_sums_quad_kernel: the
+// same for fp32 S = d = 64 with four waves per tile.
 #include "mfma_common.h"
 
 namespace race {
@@ -22,6 +23,16 @@ namespace {
 using namespace mfma;
 
 constexpr int kDirC = 32;  // tokens per sub-chunk
+// tile_sums_quad_kernel reads the first RACE_SUMS_F32_ALLOC_EIGHTHS eighths
+// of each tile (the part the output pass reads first, and K1 last) with the
+// cache-allocating policy, the rest `nt`: what the output pass reaches last
+// would have left the memory-side cache by then.  Measured at cfg2 (20 steps
+// after the settling phase, one box): 6/8 3795 M tokens/s, 8/8 3688, 4/8 3745,
+// 2/8 3705 with the same inputs every step; 3476, 3465, 3478, 3442 with two
+// input sets alternating.
+#ifndef RACE_SUMS_F32_ALLOC_EIGHTHS
+#define RACE_SUMS_F32_ALLOC_EIGHTHS 6
+#endif
 
 // Eight floats (permuted-k order) to bf16 hi/lo fragments.
 template <bool kSplit>
@@ -39,6 +50,7 @@ struct DRows {
     static constexpr int NG = W / 64;
     f32x4 x[NG][2][4];  // [column group][h][r]: columns 64 gg + 4 lr .. + 3 of row 16 h + 4 g + r
 
+    template <int PP = P>
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int r0, int g, int lr) {
 #pragma unroll
         for (int gg = 0; gg < NG; ++gg)
@@ -46,7 +58,7 @@ struct DRows {
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    x[gg][h][r] = load_q4<TIn, P>(
+                    x[gg][h][r] = load_q4<TIn, PP>(
                         rs, ((r0 + 16 * h + 4 * g + r) * W + 64 * gg + 4 * lr) * int(sizeof(TIn)));
     }
     // The 8 rows of column 64 gg + 4 lr + c, in permuted-k order.
@@ -169,6 +181,130 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_direct_kernel(
             a[sb] = x;
         }
         if (g == 0) *reinterpret_cast<f32x4*>(rp + S * D + 64 * sg + 4 * lr) = a;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K1 for fp32 S = d = 64: one workgroup per tile, so the launch spreads over
+// every CU (one wave per tile left half of them idle at cfg2).  The tile's
+// sub-chunk pairs (64 tokens) are dealt to the four waves round-robin from
+// the last pair down: at each step the workgroup reads the 256 tokens below
+// the previous step's, so it walks the tile from its end to its start, with
+// cache-allocating loads (kSumsF32LoadPolicy).  The start of every tile is
+// then what the 256 MB memory-side cache holds most recently when the output
+// pass, which walks each tile from its start, begins.  The four partial sums
+// meet in LDS and are added in wave order, so the record is the same bit for
+// bit on every run.
+template <int S, int D>
+__global__ __launch_bounds__(kThreads, 2) void tile_sums_quad_kernel(
+    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ records, int64_t T,
+    int tile, int64_t tiles, int64_t rec) {
+    static_assert(S == 64 && D == 64, "one 64 x 64 block per wave");
+    constexpr int C = kDirC, LP = kSumsF32LoadPolicy;
+    constexpr int kPart = S * D + S;  // floats of one wave's partial record in LDS
+    extern __shared__ __align__(16) float part[];  // [4][kPart]
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, g = l >> 4, lr = l & 15;
+    const int64_t n = blockIdx.y, ti = blockIdx.x;
+    const int64_t t_begin = ti * tile;
+    const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + (n * T + t_begin) * S, int64_t(rows) * S * 4);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v + (n * T + t_begin) * D, int64_t(rows) * D * 4);
+
+    f32x4 acc[4][4];  // [sb][cb]: B[4 (4 g + r) + sb][4 lr + cb] at element r
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[sb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float asum[4] = {0.f, 0.f, 0.f, 0.f};
+
+    // Consume the sub-chunk held in (kx, vx), then refill them from row
+    // `next` (past the tile the loads read zeros, which are never consumed).
+    auto chunk = [&](auto pol, DRows<float, S, LP>& kx, DRows<float, D, LP>& vx, int next) {
+        constexpr int PP = decltype(pol)::value;
+        bf16x8 vh[4], vl[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            float e[8];
+            vx.col(0, cb, e);
+            split8<true>(e, vh[cb], vl[cb]);
+        }
+        vx.template load<PP>(vr, next, g, lr);
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+            float e[8];
+            kx.col(0, sb, e);
+            asum[sb] += (((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7])));
+            bf16x8 kh, kl;
+            split8<true>(e, kh, kl);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) acc[sb][cb] = mfma3<true>(kh, kl, vh[cb], vl[cb], acc[sb][cb]);
+        }
+        kx.template load<PP>(kr, next, g, lr);
+    };
+
+    // Pair p covers rows 2 C p .. 2 C p + 2 C - 1 (the second half may lie
+    // past the tile and read zeros).  Wave w takes pairs P-1-w, P-5-w, ...
+    const int pairs = (rows + 2 * C - 1) / (2 * C);
+    int p = pairs - 1 - w;
+    const int first = p >= 0 ? 2 * C * p : rows;
+    // Pairs from `pcut` up are read `nt`, the rest with the allocating policy.
+    const int pcut = int((int64_t(pairs) * RACE_SUMS_F32_ALLOC_EIGHTHS + 7) / 8);
+    const int cut = 2 * C * pcut;
+    DRows<float, S, LP> k0, k1;
+    DRows<float, D, LP> v0, v1;
+    if (first < cut) {
+        k0.load(kr, first, g, lr);
+        v0.load(vr, first, g, lr);
+        k1.load(kr, first + C, g, lr);
+        v1.load(vr, first + C, g, lr);
+    } else {
+        k0.template load<kPolicyStream>(kr, first, g, lr);
+        v0.template load<kPolicyStream>(vr, first, g, lr);
+        k1.template load<kPolicyStream>(kr, first + C, g, lr);
+        v1.template load<kPolicyStream>(vr, first + C, g, lr);
+    }
+    using Alloc = std::integral_constant<int, LP>;
+    using Stream = std::integral_constant<int, kPolicyStream>;
+    for (; p - 4 >= pcut; p -= 4) {
+        const int nx = 2 * C * (p - 4);
+        chunk(Stream{}, k0, v0, nx);
+        chunk(Stream{}, k1, v1, nx + C);
+    }
+    for (; p >= 0; p -= 4) {
+        const int nx = 2 * C * (p - 4);  // below row 0 (last round): outside the range, zeros
+        chunk(Alloc{}, k0, v0, nx);
+        chunk(Alloc{}, k1, v1, nx + C);
+    }
+
+    // Partial record of wave w: B row 16 g + 4 r + sb, columns 4 lr .. + 3,
+    // then A (the token groups g added in a fixed order).
+    float* mine = part + w * kPart;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<f32x4*>(mine + (16 * g + 4 * r + sb) * D + 4 * lr) =
+                f32x4{acc[sb][0][r], acc[sb][1][r], acc[sb][2][r], acc[sb][3][r]};
+    {
+        f32x4 a;
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+            float x = asum[sb];
+            x = x + __shfl_xor(x, 16);
+            x = x + __shfl_xor(x, 32);
+            a[sb] = x;
+        }
+        if (g == 0) *reinterpret_cast<f32x4*>(mine + S * D + 4 * lr) = a;
+    }
+    __syncthreads();
+    // record = ((part0 + part1) + part2) + part3, 16-byte pieces.
+    float* rp = records + (n * tiles + ti) * rec;
+    for (int i = threadIdx.x; i < kPart / 4; i += kThreads) {
+        f32x4 x = *reinterpret_cast<const f32x4*>(part + 4 * i);
+#pragma unroll
+        for (int j = 1; j < 4; ++j) x += *reinterpret_cast<const f32x4*>(part + j * kPart + 4 * i);
+        *reinterpret_cast<f32x4*>(rp + 4 * i) = x;
     }
 }
 
@@ -400,6 +536,12 @@ bool direct_sums_supported(int S, int d) {
 hipError_t launch_tile_sums_direct(const void* k, const void* v, float* records, const Problem& p,
                                    hipStream_t stream) {
     if (p.tile % (2 * kDirC) != 0) return hipErrorInvalidValue;
+    if (p.dtype == RACE_F32 && p.S == 64 && p.d == 64) {
+        constexpr size_t kLds = 4 * (64 * 64 + 64) * sizeof(float);
+        tile_sums_quad_kernel<64, 64><<<dim3(unsigned(p.tiles), unsigned(p.N)), kThreads, kLds, stream>>>(
+            static_cast<const float*>(k), static_cast<const float*>(v), records, p.T, p.tile, p.tiles, p.rec);
+        return hipGetLastError();
+    }
     const int64_t total = p.N * p.tiles;
     const dim3 grid(unsigned((total + 3) / 4));
 #define RACE_SUMS(TIN, S_, D_, MB)                                                                 \

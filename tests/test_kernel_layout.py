@@ -314,6 +314,79 @@ def test_direct_kernels_map_waves_to_tiles_once(N, tiles):
     assert len(seen) == total and set(seen.values()) == {1}
 
 
+def quad_walk(rows: int, eighths: int = 6, C: int = 32):
+    """mfma_direct.hip tile_sums_quad_kernel: per wave w, the rows of every
+    sub-chunk it consumes, in order, with the policy of the load that fetched
+    it ('alloc' or 'nt'), and the wave's refill offsets past the last round."""
+    pairs = -(-rows // (2 * C))
+    pcut = -(-(pairs * eighths) // 8)
+    cut = 2 * C * pcut
+    waves = []
+    for w in range(4):
+        p = pairs - 1 - w
+        first = 2 * C * p if p >= 0 else rows
+        pol = "alloc" if first < cut else "nt"
+        held = [(first, pol), (first + C, pol)]   # k0/v0, k1/v1
+        seq, tail = [], []
+        while p >= 0:
+            nx = 2 * C * (p - 4)
+            npol = "nt" if p - 4 >= pcut else "alloc"
+            for h in range(2):
+                seq.append(held[h])
+                held[h] = (nx + h * C, npol)
+            p -= 4
+        tail = [r for r, _ in held]
+        waves.append((seq, tail))
+    return pairs, pcut, waves
+
+
+@pytest.mark.parametrize("rows", [1, 31, 32, 63, 64, 65, 200, 256, 300, 1000, 1024, 4096])
+def test_quad_sums_consume_every_sub_chunk_once_end_first(rows):
+    C = 32
+    pairs, pcut, waves = quad_walk(rows)
+    seen = Counter()
+    for seq, _ in waves:
+        seen.update(r for r, _ in seq)
+    # Every sub-chunk start of the tile's pairs once (the second half of the
+    # last pair may lie past the tile: it reads zeros and adds nothing).
+    assert sorted(seen) == list(range(0, 2 * C * pairs, C)) and set(seen.values()) == {1}
+    # Round j of the four waves covers the four pairs below round j - 1's.
+    for j in range(max(len(seq) for seq, _ in waves) // 2):
+        got = sorted(seq[2 * j][0] // (2 * C) for seq, _ in waves if len(seq) > 2 * j)
+        want = [p for p in range(pairs - 1 - 4 * j - 3, pairs - 4 * j) if p >= 0]
+        assert got == want
+    # The pairs below the cut arrive through allocating loads, the rest `nt`.
+    for seq, _ in waves:
+        for r, pol in seq:
+            assert pol == ("alloc" if r // (2 * C) < pcut else "nt")
+
+
+@pytest.mark.parametrize("rows", [1, 64, 300, 1024])
+def test_quad_sums_refills_past_the_walk_read_zero(rows):
+    # The refill after a wave's last round starts below row 0: as a 32-bit
+    # buffer offset it is past the range, so the loads return zeros.
+    S, es = 64, 4
+    _, _, waves = quad_walk(rows)
+    for seq, tail in waves:
+        for r0 in tail:
+            if seq:
+                assert r0 < 0
+            for row in range(r0, r0 + 32):
+                for c in range(0, S * es, 16):
+                    off = (row * S * es + c) & 0xFFFFFFFF
+                    assert off >= rows * S * es
+
+
+def test_quad_sums_walk_with_a_wrong_round_stride_fails():
+    # Planted mistake: rounds of 2 pairs instead of 4 visit pairs twice.
+    rows, C = 1024, 32
+    pairs = rows // (2 * C)
+    seen = Counter()
+    for w in range(4):
+        seen.update(range(pairs - 1 - w, -1, -2))
+    assert set(seen.values()) != {1}
+
+
 @pytest.mark.parametrize("tiles, groups", [(1, 1), (7, 4), (128, 8), (1000, 16), (3, 8)])
 def test_scan_groups_partition_the_tiles(tiles, groups):
     # valu_kernels.hip tile_scan_kernel: group gi scans tiles
