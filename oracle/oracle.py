@@ -54,6 +54,7 @@ Layouts: probsQ/probsK [N, T, S] (S = L*R, table-major), V/out [N, T, d].
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 import subprocess
 
@@ -62,12 +63,17 @@ import numpy as np
 EPS = 1e-6  # src/race_baseline.py:47
 
 _HERE = pathlib.Path(__file__).resolve().parent
-_LIB_PATH = _HERE / "liboracle.so"
+# RACE_ORACLE_LIB names another build of race_oracle.c to load instead (the
+# sanitizer stage, tests/sanitize.py, sets it).
+_LIB_OVERRIDE = os.environ.get("RACE_ORACLE_LIB")
+_LIB_PATH = pathlib.Path(_LIB_OVERRIDE) if _LIB_OVERRIDE else _HERE / "liboracle.so"
 _lib = None
 
 
 def build(force: bool = False) -> pathlib.Path:
     """Compile liboracle.so with the Makefile beside this file."""
+    if _LIB_OVERRIDE:
+        return _LIB_PATH
     if force or not _LIB_PATH.exists() or (
         _LIB_PATH.stat().st_mtime < (_HERE / "race_oracle.c").stat().st_mtime
     ):

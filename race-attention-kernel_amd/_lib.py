@@ -7,12 +7,17 @@ from __future__ import annotations
 
 import ctypes
 import importlib.util
+import os
 import pathlib
 import sysconfig
 
 PKG = pathlib.Path(__file__).resolve().parent
-LIB_PATH = PKG / "librace_mi355x.so"
-EXT_PATH = PKG / ("_race_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+# RACE_MI355X_LIB_DIR names another directory holding both built libraries
+# (the sanitizer stage's host-instrumented build, tests/sanitize.py); by default
+# they are the in-tree ones next to this file.
+LIB_DIR = pathlib.Path(os.environ.get("RACE_MI355X_LIB_DIR", PKG))
+LIB_PATH = LIB_DIR / "librace_mi355x.so"
+EXT_PATH = LIB_DIR / ("_race_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 _ext = None
 _cdll = None
