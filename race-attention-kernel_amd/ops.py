@@ -18,9 +18,9 @@ dense and returns only the gradients autograd asks for.  The causal backward
 has no counterpart in the reference (its design outline is
 docs/causal_v2_design.md:689-742); here the forward keeps its scanned tile
 records (the prefix state at every tile start: (S*d + S)*4 bytes per tile,
-i.e. that over the tile length per token -- 260 bytes per token at the cfg2
-shape's 512-token tiles, 2 KB at S = 256, d = 128 with the shortest 64-token
-tiles) and the backward starts from them instead of recomputing them.  The
+i.e. that over the tile length per token -- 130 bytes per token at the cfg2
+shape's automatic 1024-token tiles, 2 KB at S = 256, d = 128 with the
+shortest 64-token tiles) and the backward starts from them instead of recomputing them.  The
 reference's [N, T, S, d] prefix tensor is never formed.
 """
 from __future__ import annotations
