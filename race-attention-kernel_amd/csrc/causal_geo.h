@@ -17,11 +17,17 @@ struct Geo {
     static constexpr int kT = 64 * NW;  // threads per workgroup (NW wave64s)
     static constexpr bool kSplit = std::is_same<TIn, float>::value;
     static constexpr int E = Elem<TIn>::kPerVec;
-    using PS = Plane<kSplit, S>;  // token rows over buckets: W, K
+    using PS = Plane<kSplit, S>;  // token rows over buckets: W
+    // The K tile (token rows over buckets, read transposed by the running mass
+    // and the state update): bf16 rows of 256 buckets hold odd rows' chunk
+    // halves swapped (Plane kHalfSwap), which leaves the transposed reads
+    // without bank conflicts.
+    static constexpr bool kKHalfSwap = !kSplit && S == 256;
+    using PK = Plane<kSplit, S, kKHalfSwap>;
     using PC = Plane<kSplit, C>;  // query rows over keys: P
     using PD = Plane<kSplit, D>;  // token rows over value columns: V
     static constexpr int kWBytes = C * PS::kPitch;
-    static constexpr int kKBytes = C * PS::kPitch;
+    static constexpr int kKBytes = C * PK::kPitch;
     static constexpr int kPBytes = C * PC::kPitch;
     static constexpr int kVBytes = C * PD::kPitch;
     // The output tile [C][D] in TIn, rows of 16-byte chunks swizzled by row
@@ -104,7 +110,7 @@ struct KVStage {
                         hi = make_uint2(h ? k[p][rr].z : k[p][rr].x, h ? k[p][rr].w : k[p][rr].y);
                         lo = hi;
                     }
-                    G::PS::put4(Ks, 4 * a + rr, b * E + 4 * h, hi, lo);
+                    G::PK::put4(Ks, 4 * a + rr, b * E + 4 * h, hi, lo);
                 }
                 if (asum) {
 #pragma unroll

@@ -71,6 +71,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
     int tile, int64_t tiles, int64_t rec) {
     using G = Geo<TIn, S, D, C>;
     using PS = typename G::PS;
+    using PK = typename G::PK;
     using PD = typename G::PD;
     constexpr bool kSplit = G::kSplit;
     constexpr int NSB = S / 16, NKC = C / 32, CBW = D / 64;
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 #pragma unroll
             for (int kk = 0; kk < NKC; ++kk) {
                 bf16x8 kh, kl;
-                PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh, kl);
+                PK::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh, kl);
 #pragma unroll
                 for (int cbw = 0; cbw < CBW; ++cbw)
                     acc[sb][cbw] = mfma3<kSplit>(kh, kl, vh[cbw][kk], vl[cbw][kk], acc[sb][cbw]);
@@ -171,6 +172,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     int64_t rec) {
     using G = Geo<TIn, S, D, C, NW>;
     using PS = typename G::PS;
+    using PK = typename G::PK;
     using PC = typename G::PC;
     using PD = typename G::PD;
     constexpr bool kSplit = G::kSplit;
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
             const int sb = w + NW * sbw;
             bf16x8 kh[NKC], kl[NKC];
 #pragma unroll
-            for (int kk = 0; kk < NKC; ++kk) PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh[kk], kl[kk]);
+            for (int kk = 0; kk < NKC; ++kk) PK::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh[kk], kl[kk]);
             f32x4 last;
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) {
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
                 bf16x8 ah, al, bh, bl;
-                PS::frag(Ks, 16 * rem + lr, kk, g, ah, al);
+                PK::frag(Ks, 16 * rem + lr, kk, g, ah, al);
                 PS::frag(Ws, 16 * bi + lr, kk, g, bh, bl);
                 pacc[pb] = mfma3<kSplit>(ah, al, bh, bl, pacc[pb]);
             }
@@ -400,7 +402,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
 #pragma unroll
                 for (int kk = 0; kk < NKC; ++kk) {
                     bf16x8 kh, kl;
-                    PS::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh, kl);
+                    PK::frag_tr(Ks, 32 * kk, 16 * sb, g, lr, kh, kl);
                     b0[sb][cbw] = mfma3<kSplit>(kh, kl, vh[kk], vl[kk], b0[sb][cbw]);
                 }
                 // Where the carried state fills the register file, keep the

@@ -184,17 +184,27 @@ __device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t r, int off, const 
 // fragment reads (16 consecutive rows, one chunk) touch every bank once, and
 // the transposed staging stores (rows 4 apart, one 8-byte half chunk) are
 // spread over all banks instead of piling into two.
-template <bool kSplit, int K>
+//
+// kHalfSwap: odd rows also hold the two 8-byte halves of every chunk swapped.
+// A transposed read (8 bytes per lane, served 32 lanes per pass) reads 8 rows
+// x 4 chunks all in the same half of their chunk, so without the swap its 32
+// pieces meet on the 16 half-chunk slots of one parity in a 256-byte span: a
+// 2-way conflict on every such read.  With it, the odd rows' pieces take the
+// other parity and (bf16 rows of 256 elements, the K tile at S = 256) every
+// pass touches each bank once.  The 16-byte fragment reads keep their
+// addresses and swap the halves back in registers for odd rows.
+template <bool kSplit, int K, bool kHalfSwap = false>
 struct Plane {
     static constexpr int kLoOff = 2 * K;                       // bytes to the lo plane
     static constexpr int kPitch = (kSplit ? 4 : 2) * K + 32;   // row pitch in bytes
     static constexpr int kMask = (K / 8 < 8 ? K / 8 : 8) - 1;
     __device__ __forceinline__ static int sw(int row) { return ((row >> 3) ^ ((row >> 2) & 1)) & kMask; }
+    // Which 8-byte half of a chunk holds a chunk's first four elements.
+    __device__ __forceinline__ static int hs(int row) { return kHalfSwap ? (row & 1) : 0; }
     // Store 4 consecutive elements k0..k0+3 (k0 % 4 == 0) of row `row`.
     __device__ __forceinline__ static void put4(unsigned char* t, int row, int k0, const uint2& hi,
                                                 const uint2& lo) {
-        const int pos = fpos(k0);
-        unsigned char* p = t + row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 8 * ((pos >> 2) & 1);
+        unsigned char* p = t + off4(row, k0);
         *reinterpret_cast<uint2*>(p) = hi;
         if constexpr (kSplit) *reinterpret_cast<uint2*>(p + kLoOff) = lo;
     }
@@ -202,7 +212,7 @@ struct Plane {
     __device__ __forceinline__ static void put1(unsigned char* t, int row, int k, uint16_t hi,
                                                 uint16_t lo) {
         const int pos = fpos(k);
-        unsigned char* p = t + row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 2 * (pos & 7);
+        unsigned char* p = t + row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 2 * ((pos & 7) ^ (hs(row) << 2));
         *reinterpret_cast<uint16_t*>(p) = hi;
         if constexpr (kSplit) *reinterpret_cast<uint16_t*>(p + kLoOff) = lo;
     }
@@ -212,12 +222,18 @@ struct Plane {
         const unsigned char* p = t + row * kPitch + 16 * ((4 * kk + g) ^ sw(row));
         hi = *reinterpret_cast<const bf16x8*>(p);
         if constexpr (kSplit) lo = *reinterpret_cast<const bf16x8*>(p + kLoOff);
+        if constexpr (kHalfSwap) {
+            if (row & 1) {
+                hi = __builtin_shufflevector(hi, hi, 4, 5, 6, 7, 0, 1, 2, 3);
+                if constexpr (kSplit) lo = __builtin_shufflevector(lo, lo, 4, 5, 6, 7, 0, 1, 2, 3);
+            }
+        }
     }
     // Byte offset of the 8-byte group holding elements k0 .. k0 + 3 (k0 % 4 == 0)
     // of row `row` in the hi plane.
     __device__ __forceinline__ static int off4(int row, int k0) {
         const int pos = fpos(k0);
-        return row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 8 * ((pos >> 2) & 1);
+        return row * kPitch + 16 * ((pos >> 3) ^ sw(row)) + 8 * (((pos >> 2) & 1) ^ hs(row));
     }
     // Fragment of the transposed tile, whose contraction index runs over this
     // plane's rows: lane (g, lr) gets elements (row0 + 4 g + e % 4 + 16 (e / 4),

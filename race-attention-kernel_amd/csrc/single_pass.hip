@@ -230,6 +230,7 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
     using SG = SpGeo<TIn, NSUB, R>;
     using G = typename SG::G;
     using PS = typename G::PS;
+    using PK = typename G::PK;
     using PC = typename G::PC;
     using PD = typename G::PD;
     using OT = OutTile<TIn, kSpD, kSpC>;
@@ -439,7 +440,7 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
 #pragma unroll
             for (int sb = 0; sb < NSB; ++sb) {
                 bf16x8 kh, kl;
-                PS::frag_tr(K1, 0, 16 * sb, g, lr, kh, kl);
+                PK::frag_tr(K1, 0, 16 * sb, g, lr, kh, kl);
                 gb[sb] = mfma3<kSplit>(kh, kl, vh, vl, gb[sb]);
                 if (sb == w) {
                     if constexpr (kSplit) ga = mfma16(kl, ones, ga);
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
         // Phase 2, steps 1 + 2: running mass and W = Q / (Abar + eps).
         if (p2) {
             bf16x8 kh, kl;
-            PS::frag_tr(K2, 0, 16 * w, g, lr, kh, kl);
+            PK::frag_tr(K2, 0, 16 * w, g, lr, kh, kl);
             f32x4 last;
 #pragma unroll
             for (int bi = 0; bi < NBI; ++bi) {
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
                 bf16x8 ah, al, bh, bl;
-                PS::frag(K2, 16 * rem + lr, kk, g, ah, al);
+                PK::frag(K2, 16 * rem + lr, kk, g, ah, al);
                 PS::frag(Ws, 16 * bi + lr, kk, g, bh, bl);
                 pacc = mfma3<kSplit>(ah, al, bh, bl, pacc);
             }
@@ -566,7 +567,7 @@ __global__ __launch_bounds__(kSpT, 1) void causal_single_kernel(
 #pragma unroll
             for (int sb = 0; sb < NSB; ++sb) {
                 bf16x8 kh, kl;
-                PS::frag_tr(K2, 0, 16 * sb, g, lr, kh, kl);
+                PK::frag_tr(K2, 0, 16 * sb, g, lr, kh, kl);
                 b0[sb] = mfma3<kSplit>(kh, kl, vh, vl, b0[sb]);
             }
             flush_o = make_rsrc(out + base2 * D, int64_t(rows2) * D * es);

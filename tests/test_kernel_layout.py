@@ -46,26 +46,41 @@ class Plane:
     the lo plane at +2K bytes when split), chunk u of row r stored at
     u ^ sw(r), rows 32 bytes longer than the planes."""
 
-    def __init__(self, split: bool, K: int, swizzle: bool = True):
+    def __init__(self, split: bool, K: int, swizzle: bool = True, half_swap: bool = False):
         self.split, self.K = split, K
         self.lo_off = 2 * K
         self.pitch = (4 if split else 2) * K + 32
         self.mask = min(K // 8, 8) - 1
         self.swizzle = swizzle
+        self.half_swap = half_swap
 
     def sw(self, row: int) -> int:
         return (((row >> 3) ^ ((row >> 2) & 1)) & self.mask) if self.swizzle else 0
 
+    def hs(self, row: int) -> int:
+        """Plane<..., kHalfSwap>::hs(): odd rows hold each chunk's halves swapped."""
+        return (row & 1) if self.half_swap else 0
+
     def elem(self, row: int, k: int) -> int:   # put1
         p = fpos(k)
-        return row * self.pitch + 16 * ((p >> 3) ^ self.sw(row)) + 2 * (p & 7)
+        return row * self.pitch + 16 * ((p >> 3) ^ self.sw(row)) + 2 * ((p & 7) ^ (self.hs(row) << 2))
 
     def off4(self, row: int, k0: int) -> int:  # put4 / off4
         p = fpos(k0)
-        return row * self.pitch + 16 * ((p >> 3) ^ self.sw(row)) + 8 * ((p >> 2) & 1)
+        return row * self.pitch + 16 * ((p >> 3) ^ self.sw(row)) + 8 * (((p >> 2) & 1) ^ self.hs(row))
 
-    def frag(self, row: int, kk: int, g: int) -> int:  # frag
+    def frag(self, row: int, kk: int, g: int) -> int:  # frag (the address; see frag_values)
         return row * self.pitch + 16 * ((4 * kk + g) ^ self.sw(row))
+
+    def frag_values(self, mem: dict, row: int, kk: int, g: int, fix: bool = True) -> list:
+        """The 8 values frag() hands lane (g, row): the 16 bytes at frag(), with
+        the halves swapped back in registers for odd rows of a half-swapped
+        plane (fix=False: a planted mistake that forgets the swap)."""
+        a = self.frag(row, kk, g)
+        vals = [mem[a + 2 * e] for e in range(8)]
+        if self.half_swap and fix and (row & 1):
+            vals = vals[4:] + vals[:4]
+        return vals
 
 
 class OutTile:
@@ -237,6 +252,73 @@ def test_frag_tr_reads_at_most_two_way(split, K):
     for row0, col0, g in itertools.product(range(0, 64, 32), range(0, K, 16), range(4)):
         load = bank_load((P.off4(row0 + 4 * g + (lr >> 2), col0 + 4 * (lr & 3)), 8) for lr in range(16))
         assert max(load.values()) <= 2
+
+
+def max_ways(accesses) -> int:
+    return max(bank_load(accesses).values())
+
+
+def frag_tr_pass(P: Plane, row0: int, col0: int, half: int, second: int):
+    """The 32 lanes of one pass of a transposed read (ds_read_b64_tr_b16: 8
+    bytes per lane, 32 lanes served per pass): lane groups g = 2 half, 2 half
+    + 1, rows row0 + second + 4 g + lr / 4."""
+    return [(P.off4(row0 + second + 4 * g + (lr >> 2), col0 + 4 * (lr & 3)), 8)
+            for g in (2 * half, 2 * half + 1) for lr in range(16)]
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("K", PLANE_KS)
+def test_half_swapped_plane_hands_out_the_same_fragments(split, K):
+    # put1/put4 store, frag (with the register swap) and frag_tr read back the
+    # values of the plain plane: the layout change is invisible to the math.
+    P = Plane(split, K, half_swap=True)
+    rows = 64
+    mem = {P.elem(r, k): (r, k) for r in range(rows) for k in range(K)}
+    assert len(mem) == rows * K
+    for r, k0 in itertools.product(range(rows), range(0, K, 4)):
+        assert [mem[P.off4(r, k0) + 2 * j] for j in range(4)] == [(r, k) for k in range(k0, k0 + 4)]
+    for r, kk, g in itertools.product(range(rows), range(K // 32), range(4)):
+        assert P.frag_values(mem, r, kk, g) == [(r, k_of(kk, g, e)) for e in range(8)]
+    for row0, col0, g in itertools.product(range(0, rows, 32), range(0, K, 16), range(4)):
+        got = frag_tr(P, mem, row0, col0, g)
+        for lr in range(16):
+            assert got[lr] == [(row0 + 4 * g + e % 4 + 16 * (e // 4), col0 + lr) for e in range(8)]
+
+
+def test_half_swapped_fragments_need_the_register_swap():
+    # Planted mistake: reading a half-swapped plane's fragment without
+    # swapping its halves back hands odd rows permuted contraction elements.
+    P = Plane(False, 256, half_swap=True)
+    mem = {P.elem(r, k): (r, k) for r in range(32) for k in range(256)}
+    assert P.frag_values(mem, 1, 0, 0, fix=False) != [(1, k_of(0, 0, e)) for e in range(8)]
+    assert P.frag_values(mem, 0, 0, 0, fix=False) == [(0, k_of(0, 0, e)) for e in range(8)]
+
+
+def test_k_tile_transposed_reads_are_conflict_free_with_the_half_swap():
+    # causal_geo.h Geo::PK for bf16 S = 256 (the cfg5 K tile): 32-lane passes
+    # of the transposed reads touch each bank once with the half swap; the
+    # plain plane puts every pass's 32 pieces on the 16 slots of one parity
+    # (2-way), which is what the cfg5 counters measured.
+    plain, swapped = Plane(False, 256), Plane(False, 256, half_swap=True)
+    for row0, col0, half, second in itertools.product(range(0, 64, 32), range(0, 256, 16), range(2), (0, 16)):
+        assert max_ways(frag_tr_pass(swapped, row0, col0, half, second)) == 1
+        assert max_ways(frag_tr_pass(plain, row0, col0, half, second)) == 2
+
+
+def test_k_tile_fragment_reads_stay_conflict_free_with_the_half_swap():
+    # The 16-byte fragment reads (16-lane passes) keep their addresses.
+    P = Plane(False, 256, half_swap=True)
+    for base, kk, g in itertools.product(range(0, 64, 16), range(8), range(4)):
+        assert max_ways((P.frag(base + lr, kk, g), 16) for lr in range(16)) == 1
+
+
+def test_k_tile_staging_stores_are_no_worse_with_the_half_swap():
+    # KVStage::store of bf16 rows (E = 8): a 32-lane pass writes one row, 32
+    # 8-byte pieces; a 512-byte row covers every bank twice either way.
+    plain, swapped = Plane(False, 256), Plane(False, 256, half_swap=True)
+    for a, rr, h in itertools.product(range(8), range(4), range(2)):
+        for P in (plain, swapped):
+            assert max_ways((P.off4(4 * a + rr, 8 * b + 4 * h), 8) for b in range(32)) <= 2
 
 
 @pytest.mark.parametrize("es, D, C", [(4, 64, 32), (4, 64, 64), (4, 128, 32), (4, 128, 64), (2, 64, 32),
