@@ -510,7 +510,7 @@ hipError_t launch_tile_sums_mfma(const void* k, const void* v, float* records, c
 }
 
 int mfma_tiles_per_cu(int S, int d, int dtype, int kernel) {
-    if (kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(S, d, dtype))
+    if (kernel == RACE_KERNEL_MFMA && direct_output_supported(S, d, dtype))
         return direct_output_tiles_per_cu();
     // fp32 S = d = 64 (the workgroup output pass, four resident per CU):
     // two tiles per CU.  Measured over 2000-step windows at cfg2 (T = 65536):
@@ -531,7 +531,11 @@ hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void*
                               float* records, float* state, const Problem& p, hipStream_t stream,
                               Marks* marks) {
     if (!mfma_causal_supported(p.S, p.d)) return hipErrorInvalidValue;
-    if (p.kernel != RACE_KERNEL_MFMA_WG && direct_output_supported(p.S, p.d, p.dtype) &&
+    // The register-direct output pass runs when asked for (RACE_KERNEL_MFMA);
+    // the automatic choice is the workgroup pass everywhere: at cfg3 (bf16, S
+    // = d = 64, T = 2^20, 8192-token tiles) it measured 844 against 864 us,
+    // 7286 against 7174 M tokens/s over the whole op.
+    if (p.kernel == RACE_KERNEL_MFMA && direct_output_supported(p.S, p.d, p.dtype) &&
         p.tile % 64 == 0) {
         hipError_t err = launch_tile_sums_direct(k, v, records, p, stream);
         if (err != hipSuccess) return err;
