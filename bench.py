@@ -218,7 +218,7 @@ def parse_args():
     ap.add_argument("--alg1-variant", choices=["fp32", "bf16"], default="bf16",
                     help="rounding variant of --pass alg1 (fp32-accurate or bf16 features)")
     ap.add_argument("--T", type=int, default=0)
-    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg", "decode", "single"],
+    ap.add_argument("--kernel", choices=["auto", "valu", "mfma", "mfma_wg", "decode", "single", "mfma_precise"],
                     default="auto")
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -693,7 +693,7 @@ def measure(args, T: int) -> dict:
     tile = race.select_tile_tokens(cfg.N, T, cfg.L, cfg.R, cfg.d, bf16=(es == 2), causal=cfg.causal,
                                    tile_tokens=args.tile, kernel=kernel_id)
     family = "valu"
-    if cfg.causal and (kernel_id in (2, 3) or (kernel_id == 0 and race.ops._lib.ext().shape_supported(
+    if cfg.causal and (kernel_id in (2, 3, 6) or (kernel_id == 0 and race.ops._lib.ext().shape_supported(
             cfg.L, cfg.R, cfg.d)[1])):
         family = "mfma"
     if cfg.causal and kernel_id == race.ops.KERNELS["single"]:

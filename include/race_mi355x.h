@@ -83,7 +83,19 @@ typedef enum race_kernel {
      * with all 256 CUs: one persistent launch that reads every operand once
      * (tiles of 128 tokens; tile_tokens must be 0 or 128).  Anything else
      * returns RACE_ERROR_INVALID_VALUE. */
-    RACE_KERNEL_SINGLE = 5
+    RACE_KERNEL_SINGLE = 5,
+    /* Causal forward (race_fwd, race_fwd_noalloc, the tile path of
+     * race_fwd_carry) on the workgroup matrix-core kernels with every
+     * product fp32-accurate for bf16 tokens too: W, the masked scores and the
+     * carried state enter the products as bf16 hi + lo pairs, as they do for
+     * fp32 tokens, so a bf16 result differs from the exact one by about its
+     * own rounding.  No counterpart in the reference's per-bucket path (its
+     * bf16 tensor-core kernel carries B as hi + lo, race_causal_fwd_tc.cu:36,
+     * and rounds W and the scores).  fp32 tokens: the same as MFMA_WG.
+     * Shapes without matrix-core kernels, the non-causal op, the backward,
+     * the hashed and the Algorithm-1 entry points return
+     * RACE_ERROR_INVALID_VALUE. */
+    RACE_KERNEL_MFMA_PRECISE = 6
 } race_kernel;
 
 /* Shape of one call.  Mirrors CausalShape

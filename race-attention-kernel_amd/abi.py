@@ -23,6 +23,7 @@ RACE_KERNEL_MFMA = 2
 RACE_KERNEL_MFMA_WG = 3
 RACE_KERNEL_DECODE = 4
 RACE_KERNEL_SINGLE = 5
+RACE_KERNEL_MFMA_PRECISE = 6
 RACE_DECODE_TOKENS = 16
 RACE_SUB_CHUNK_TOKENS = 64
 RACE_ALG1_FP32 = 0

@@ -12,10 +12,14 @@ namespace mfma {
 // Geometry of one (S, D, C, dtype) specialization.  Every tile is stored with
 // tokens as rows (W, K, V; P with queries as rows); products that contract
 // over tokens read their fragments transposed (Plane::frag_tr).
-template <typename TIn, int S, int D, int C, int NW = 4>
+// kPrecise (bf16 tokens): every product carries its fp32 operands as bf16
+// hi + lo pairs, as the fp32 path does (W, P and the carried state; the lo
+// parts of bf16 K and V are zero), so the result is fp32-accurate up to the
+// output's own rounding.
+template <typename TIn, int S, int D, int C, int NW = 4, bool kPrecise = false>
 struct Geo {
     static constexpr int kT = 64 * NW;  // threads per workgroup (NW wave64s)
-    static constexpr bool kSplit = std::is_same<TIn, float>::value;
+    static constexpr bool kSplit = std::is_same<TIn, float>::value || kPrecise;
     static constexpr int E = Elem<TIn>::kPerVec;
     using PS = Plane<kSplit, S>;  // token rows over buckets: W
     // The K tile (token rows over buckets, read transposed by the running mass
@@ -51,9 +55,9 @@ struct Geo {
 };
 
 // Raw K and V registers of one sub-chunk.
-template <typename TIn, int S, int D, int C, int P, int NW = 4>
+template <typename TIn, int S, int D, int C, int P, int NW = 4, bool kPrecise = false>
 struct KVStage {
-    using G = Geo<TIn, S, D, C, NW>;
+    using G = Geo<TIn, S, D, C, NW, kPrecise>;
     uint4 k[G::kKPer][4];
     uint4 v[G::kVPer][4];
 

@@ -165,12 +165,12 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void tile_sums_mfma_kernel(
 //   5. B0 += K^T V                             same c-blocks, all s-blocks
 // NW waves per workgroup (4, or 8 where the carried state would otherwise
 // fill the register file: two waves per SIMD then share the CU's work).
-template <typename TIn, int S, int D, int C, int kMinBlocks, int NW>
+template <typename TIn, int S, int D, int C, int kMinBlocks, int NW, bool kPrecise>
 __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v,
     TIn* __restrict__ out, const float* __restrict__ records, int64_t T, int tile, int64_t tiles,
     int64_t rec) {
-    using G = Geo<TIn, S, D, C, NW>;
+    using G = Geo<TIn, S, D, C, NW, kPrecise>;
     using PS = typename G::PS;
     using PK = typename G::PK;
     using PC = typename G::PC;
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     // refilled with the next sub-chunk (a deeper prefetch measured slower).
     // The previous sub-chunk's output tile is flushed after the first barrier
     // (measured: issuing it after the prefetch instead was slower at cfg5).
-    auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy, NW>& st, QRegs& qr, int r0) {
+    auto sub_chunk = [&](KVStage<TIn, S, D, C, kOutKVPolicy, NW, kPrecise>& st, QRegs& qr, int r0) {
         __syncthreads();
         // Unconditional: at r0 = 0 the offsets are negative, outside the
         // buffer range, so those stores are dropped.  (A conditional flush
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
         }
     };
 
-    KVStage<TIn, S, D, C, kOutKVPolicy, NW> st[kDepth];
+    KVStage<TIn, S, D, C, kOutKVPolicy, NW, kPrecise> st[kDepth];
     QRegs qr[kDepth];
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
@@ -445,17 +445,18 @@ hipError_t launch_sums_family(const void* k, const void* v, float* records, cons
     return hipGetLastError();
 }
 
-template <typename TIn, int S, int D, int C, int kMinBlocks, int NW = 4>
+template <typename TIn, bool kPrecise, int S, int D, int C, int kMinBlocks, int NW = 4>
 hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void* out, float* records,
                               float* state, const Problem& p, hipStream_t stream, Marks* marks) {
-    using GO = Geo<TIn, S, D, C, NW>;
+    using GO = Geo<TIn, S, D, C, NW, kPrecise>;
+    static_assert(GO::kOutputLds <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     hipError_t err = launch_sums_family<TIn, S, D, C, kMinBlocks>(k, v, records, p, stream);
     if (err != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
     if ((err = launch_tile_scan(records, state, p, stream)) != hipSuccess) return err;
     if (marks && (err = marks->mark(stream)) != hipSuccess) return err;
-    causal_output_mfma_kernel<TIn, S, D, C, kMinBlocks, NW><<<grid, GO::kT, GO::kOutputLds, stream>>>(
+    causal_output_mfma_kernel<TIn, S, D, C, kMinBlocks, NW, kPrecise><<<grid, GO::kT, GO::kOutputLds, stream>>>(
         static_cast<const TIn*>(q), static_cast<const TIn*>(k), static_cast<const TIn*>(v),
         static_cast<TIn*>(out), records, p.T, p.tile, p.tiles, p.rec);
     err = hipGetLastError();
@@ -464,25 +465,27 @@ hipError_t launch_mfma_family(const void* q, const void* k, const void* v, void*
     return hipSuccess;
 }
 
-template <typename TIn>
+template <typename TIn, bool kPrecise = false>
 hipError_t dispatch_mfma(const void* q, const void* k, const void* v, void* out, float* records,
                          float* state, const Problem& p, hipStream_t stream, Marks* marks) {
     // S = d = 64: 32-token sub-chunks halve every LDS plane (32 KB per
     // workgroup) so four workgroups share a CU and keep four times the loads
     // in flight; the output pass there is bound by bytes in flight, not math.
     if (p.S == 64 && p.d == 64)
-        return launch_mfma_family<TIn, 64, 64, 32, std::is_same<TIn, float>::value ? RACE_OUT_F32_6464_MINBLOCKS : 4>(
+        return launch_mfma_family<TIn, kPrecise, 64, 64, 32,
+                                  std::is_same<TIn, float>::value ? RACE_OUT_F32_6464_MINBLOCKS : 4>(
             q, k, v, out, records, state, p, stream, marks);
     if (p.S == 64 && p.d == 128)
-        return launch_mfma_family<TIn, 64, 128, 64, 1>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, kPrecise, 64, 128, 64, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 128 && p.d == 64)
-        return launch_mfma_family<TIn, 128, 64, 64, 1>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, kPrecise, 128, 64, 64, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 128 && p.d == 128)
-        return launch_mfma_family<TIn, 128, 128, 64, 1>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, kPrecise, 128, 128, 64, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 256 && p.d == 64)
-        return launch_mfma_family<TIn, 256, 64, 32, 1>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, kPrecise, 256, 64, 32, 1>(q, k, v, out, records, state, p, stream, marks);
     if (p.S == 256 && p.d == 128)
-        return launch_mfma_family<TIn, 256, 128, 32, 1, 8>(q, k, v, out, records, state, p, stream, marks);
+        return launch_mfma_family<TIn, kPrecise, 256, 128, 32, 1, 8>(q, k, v, out, records, state, p, stream,
+                                                                       marks);
     return hipErrorInvalidValue;
 }
 
@@ -546,6 +549,8 @@ hipError_t launch_causal_mfma(const void* q, const void* k, const void* v, void*
             return err;
         return marks ? marks->mark(stream) : hipSuccess;
     }
+    if (p.dtype == RACE_BF16 && p.kernel == RACE_KERNEL_MFMA_PRECISE)
+        return dispatch_mfma<bf16_t, true>(q, k, v, out, records, state, p, stream, marks);
     if (p.dtype == RACE_BF16)
         return dispatch_mfma<bf16_t>(q, k, v, out, records, state, p, stream, marks);
     return dispatch_mfma<float>(q, k, v, out, records, state, p, stream, marks);

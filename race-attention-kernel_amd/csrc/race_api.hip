@@ -54,10 +54,11 @@ int kernel_choice(const race_options* o) { return o ? o->kernel : RACE_KERNEL_AU
 race_status resolve_kernel(const race_shape* sh, int causal, const race_options* o, bool* mfma) {
     const int k = kernel_choice(o);
     if (k != RACE_KERNEL_AUTO && k != RACE_KERNEL_VALU && k != RACE_KERNEL_MFMA &&
-        k != RACE_KERNEL_MFMA_WG && k != RACE_KERNEL_SINGLE)
+        k != RACE_KERNEL_MFMA_WG && k != RACE_KERNEL_SINGLE && k != RACE_KERNEL_MFMA_PRECISE)
         return RACE_ERROR_INVALID_VALUE;
     const bool has = causal && mfma_causal_supported(sub(sh), sh->head_dim);
-    const bool forced = k == RACE_KERNEL_MFMA || k == RACE_KERNEL_MFMA_WG || k == RACE_KERNEL_SINGLE;
+    const bool forced = k == RACE_KERNEL_MFMA || k == RACE_KERNEL_MFMA_WG || k == RACE_KERNEL_SINGLE ||
+                        k == RACE_KERNEL_MFMA_PRECISE;
     if (forced && !has) return RACE_ERROR_INVALID_VALUE;
     *mfma = forced || (k == RACE_KERNEL_AUTO && has);
     return RACE_SUCCESS;
@@ -240,6 +241,11 @@ struct CausalBwdPlan {
     // groups (its dQ whole; no dQ running sum).
     bool wide() const { return blocked() && bf16 && hblocks == 2; }
 };
+
+// The causal backward's kernel choices: automatic, vector ALU or matrix cores.
+bool bwd_kernel_ok(int kernel) {
+    return kernel == RACE_KERNEL_AUTO || kernel == RACE_KERNEL_VALU || kernel == RACE_KERNEL_MFMA;
+}
 
 CausalBwdPlan plan_causal_bwd(const Problem& p, int kernel) {
     CausalBwdPlan pl;
@@ -829,8 +835,7 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
                             Marks* marks) {
     // The tile policy is the vector-ALU one; the kernel family is chosen here.
     const int kernel = kernel_choice(opts);
-    if (kernel != RACE_KERNEL_AUTO && kernel != RACE_KERNEL_VALU && kernel != RACE_KERNEL_MFMA)
-        return RACE_ERROR_INVALID_VALUE;
+    if (!bwd_kernel_ok(kernel)) return RACE_ERROR_INVALID_VALUE;
     race_options topts = {opts ? opts->tile_tokens : 0, RACE_KERNEL_VALU};
     Problem p;
     bool mfma = false;
@@ -1067,7 +1072,7 @@ extern "C" {
 
 race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
                                             size_t* bytes) {
-    if (!bytes) return RACE_ERROR_INVALID_VALUE;
+    if (!bytes || !bwd_kernel_ok(kernel_choice(opts))) return RACE_ERROR_INVALID_VALUE;
     Problem p;
     bool mfma = false;
     // The backward uses the vector-ALU tile policy for both kernel families.
@@ -1081,7 +1086,7 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
 
 race_status race_causal_bwd_from_records_workspace_bytes(const race_shape* shape,
                                                          const race_options* opts, size_t* bytes) {
-    if (!bytes || !opts || opts->tile_tokens <= 0) return RACE_ERROR_INVALID_VALUE;
+    if (!bytes || !opts || opts->tile_tokens <= 0 || !bwd_kernel_ok(opts->kernel)) return RACE_ERROR_INVALID_VALUE;
     Problem p;
     bool mfma = false;
     race_options topts = {opts->tile_tokens, RACE_KERNEL_VALU};

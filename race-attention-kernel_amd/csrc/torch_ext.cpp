@@ -154,11 +154,12 @@ race_options make_options(int64_t tile_tokens, int64_t kernel, bool allow_decode
                 "tile_tokens must be 0 (automatic) or a positive multiple of ",
                 RACE_SUB_CHUNK_TOKENS, ", got ", tile_tokens);
     if (allow_decode) {
-        TORCH_CHECK(kernel >= 0 && kernel <= RACE_KERNEL_SINGLE,
-                    "kernel must be 0 (auto), 1 (valu), 2 (mfma), 3 (mfma_wg), 4 (decode) or 5 (single)");
+        TORCH_CHECK(kernel >= 0 && kernel <= RACE_KERNEL_MFMA_PRECISE,
+                    "kernel must be 0 (auto), 1 (valu), 2 (mfma), 3 (mfma_wg), 4 (decode), 5 (single) "
+                    "or 6 (mfma_precise)");
     } else {
-        TORCH_CHECK(kernel >= 0 && kernel <= RACE_KERNEL_SINGLE && kernel != RACE_KERNEL_DECODE,
-                    "kernel must be 0 (auto), 1 (valu), 2 (mfma), 3 (mfma_wg) or 5 (single)");
+        TORCH_CHECK(kernel >= 0 && kernel <= RACE_KERNEL_MFMA_PRECISE && kernel != RACE_KERNEL_DECODE,
+                    "kernel must be 0 (auto), 1 (valu), 2 (mfma), 3 (mfma_wg), 5 (single) or 6 (mfma_precise)");
     }
     race_options o;
     o.tile_tokens = static_cast<int32_t>(tile_tokens);

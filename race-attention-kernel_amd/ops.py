@@ -30,7 +30,7 @@ from torch.autograd.function import once_differentiable
 
 from . import _lib
 
-KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3, "decode": 4, "single": 5}
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "mfma_wg": 3, "decode": 4, "single": 5, "mfma_precise": 6}
 
 
 def _kernel_id(kernel: str | int) -> int:
@@ -102,7 +102,10 @@ def race_fused_fwd(probsQ: torch.Tensor, probsK: torch.Tensor, V: torch.Tensor, 
         causal: inclusive running sums (True) or full-sequence sums (False).
         tile_tokens: 0 for automatic, else a positive multiple of 64 (the
             tokens each workgroup of the causal output pass owns).
-        kernel: "auto", "valu" (fp32 vector kernels) or "mfma" (matrix cores).
+        kernel: "auto", "valu" (fp32 vector kernels), "mfma" (matrix cores),
+            "mfma_wg" (the workgroup matrix-core kernels) or "mfma_precise"
+            (causal: the workgroup kernels with every product fp32-accurate
+            for bf16 inputs too; the backward keeps its own choice).
 
     Returns:
         out: [N, T, d] in V's dtype.

@@ -130,6 +130,30 @@ def test_causal_bwd_workspace_for_matrix_core_blocks(race):
                   + r64(NT * S)) * 4
 
 
+def test_precise_kernel_choice_on_the_host(race):
+    # RACE_KERNEL_MFMA_PRECISE: the causal forward's workgroup kernels with
+    # fp32-accurate products; same workspace as MFMA_WG, refused where there is
+    # no matrix-core kernel, for the non-causal op and for the backward.
+    from race_attention_kernel_amd import abi, ops
+
+    assert ops.KERNELS["mfma_precise"] == abi.RACE_KERNEL_MFMA_PRECISE == 6
+    for dt in (abi.RACE_BF16, abi.RACE_F32):
+        sh = abi.shape(8, 4096, 8, 32, 128, dt)
+        # An explicit tile: the automatic one reads the device's CU count.
+        st, nb, tiles, rec = abi.fwd_workspace_bytes(sh, True, abi.options(512, abi.RACE_KERNEL_MFMA_PRECISE))
+        assert st == 0 and tiles == 8
+        assert (st, nb, tiles, rec) == abi.fwd_workspace_bytes(sh, True, abi.options(512, abi.RACE_KERNEL_MFMA_WG))
+    bad = abi.options(512, abi.RACE_KERNEL_MFMA_PRECISE)
+    assert abi.fwd_workspace_bytes(abi.shape(8, 4096, 3, 5, 7, abi.RACE_BF16), True, bad)[0] == \
+        abi.RACE_ERROR_INVALID_VALUE
+    assert abi.fwd_workspace_bytes(abi.shape(8, 4096, 4, 16, 64, abi.RACE_BF16), False, bad)[0] == \
+        abi.RACE_ERROR_INVALID_VALUE
+    assert abi.causal_bwd_workspace_bytes(abi.shape(8, 4096, 4, 16, 64, abi.RACE_BF16), bad)[0] == \
+        abi.RACE_ERROR_INVALID_VALUE
+    assert abi.fwd_workspace_bytes(abi.shape(8, 4096, 4, 16, 64), True, abi.options(512, 7))[0] == \
+        abi.RACE_ERROR_INVALID_VALUE
+
+
 def test_scratch_per_token_is_constant(race):
     # The causal workspace is O(T / tile): per token it stays at 4 * rec / tile bytes.
     from race_attention_kernel_amd import abi
