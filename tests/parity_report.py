@@ -84,6 +84,12 @@ def main() -> int:
     ref = oracle.causal_recurrence(to_np(q), to_np(k), to_np(v), nthreads=16)
     fm, fr = f_units(o, ref)
     add("cfg3 causal fwd bf16, single", f"N=8 T={T}", "8/8", per_stream_rel_err(o, ref), fm, fr)
+    # The same inputs through the fp32-accurate bf16 forward (kernel "mfma_precise").
+    out = race.race_fused_fwd(q, k, v, causal=True, kernel="mfma_precise")
+    torch.cuda.synchronize()
+    o = to_np(out)
+    fm, fr = f_units(o, ref)
+    add("cfg3 causal fwd bf16, mfma_precise", f"N=8 T={T}", "8/8", per_stream_rel_err(o, ref), fm, fr)
     del q, k, v, out
     torch.cuda.empty_cache()
     # cfg5: bf16, S = 256, d = 128; 16 of the 128 streams.  Then the
@@ -99,6 +105,12 @@ def main() -> int:
     ref = oracle.causal_recurrence(to_np(q[pick]), to_np(k[pick]), to_np(v[pick]), nthreads=16)
     fm, fr = f_units(o, ref)
     add("cfg5 causal fwd bf16", "N=128 T=16384 S=256 d=128", "16/128", per_stream_rel_err(o, ref), fm, fr)
+    with torch.no_grad():
+        o = to_np(race.race_fused_fwd(q, k, v, causal=True, kernel="mfma_precise")[pick])
+    torch.cuda.synchronize()
+    fm, fr = f_units(o, ref)
+    add("cfg5 causal fwd bf16, mfma_precise", "N=128 T=16384 S=256 d=128", "16/128",
+        per_stream_rel_err(o, ref), fm, fr)
     g = torch.randn(v.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(6)).to(v.dtype)
     out.backward(g)
     torch.cuda.synchronize()
