@@ -849,6 +849,280 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// B3 over a 128 x 128 block (bf16 tokens, d = 128): two 64-bucket groups
+// (g2 = 0, 1: buckets 64 g2 .. of the block) and every value column in one
+// backward walk, eight waves.  Wave w owns buckets 16 w .. 16 w + 15 of the
+// block (dK, W, alpha, the carried Z1^T columns) and value columns 16 w ..
+// 16 w + 15 (dV).  The steps are those of causal_bwd_dkv_mfma_kernel with
+// the contractions over buckets and value columns four 32-wide steps long.
+// dK of the block is complete (every value column is in the walk) and goes
+// to the caller's dK; dV, a sum over the blocks of a problem, goes through
+// its fp32 running sum unless the block is the only one.
+constexpr int kWideS = 128, kWideD = 128, kWideWaves = 8, kWideThreads = 64 * kWideWaves;
+
+struct WideGeo {
+    using PR = Plane<false, 128>;  // rows = tokens (or buckets), k = buckets or value columns
+    using PM = Plane<false, kBC>;  // k = tokens
+    static constexpr int kRBytes = kBC * PR::kPitch;
+    static constexpr int kWTBytes = kWideS * PM::kPitch;  // W^T [s][i]
+    static constexpr int kMBytes = kBC * PM::kPitch;
+    static constexpr int kZBytes = kWideS * PR::kPitch;   // Z1 [s][c]
+    static constexpr int kLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
+    static constexpr int kBlk = (kBC / 4) * (128 / 8);    // staging blocks of one tensor
+    static_assert(3 * kBlk <= kWideThreads && kBlk % 64 == 0, "one staging block per thread, a tensor per wave");
+};
+
+__global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ g, bf16_t* __restrict__ dK, int64_t T, int tile, int64_t tiles, int64_t rec,
+    BwdWide wb) {
+    using G = WideGeo;
+    using PR = G::PR;
+    using PM = G::PM;
+    extern __shared__ __align__(16) unsigned char lds[];
+    unsigned char* Ks = lds;
+    unsigned char* Vs = Ks + G::kRBytes;
+    unsigned char* Gs = Vs + G::kRBytes;
+    unsigned char* WT = Gs + G::kRBytes;
+    unsigned char* MT = WT + G::kWTBytes;
+    unsigned char* PTp = MT + G::kMBytes;
+    unsigned char* Zr = PTp + G::kMBytes;
+
+    const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g2 = w >> 2;               // this wave's 64-bucket group
+    const int sl = 16 * (w & 3) + lr;    // the lane's bucket inside it
+    const int64_t n = blockIdx.y, ti = blockIdx.x;
+    const int64_t t_begin = ti * tile;
+    const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
+    const int64_t base = n * T + t_begin;
+    const int ldq = wb.ldq;
+    // The group's buffers, chosen without indexing the argument struct by a
+    // run-time value (which copies it to scratch memory).
+    const float* dq32 = g2 ? wb.dq32[1] : wb.dq32[0];
+    const float* apre = g2 ? wb.apre[1] : wb.apre[0];
+    const float* rec0 = g2 ? wb.rec[1][0] : wb.rec[0][0];
+    const float* rec1 = g2 ? wb.rec[1][1] : wb.rec[0][1];
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
+    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+    const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * ldq : nullptr, dK ? int64_t(rows) * ldq * 2 : 0);
+    // dV: the running sum (written; read unless this is the first addend)
+    // and the caller's dV for the last addend.  A gradient not asked for has
+    // empty views, which drop the stores.
+    const __amdgpu_buffer_rsrc_t avr =
+        make_rsrc(wb.acc_v ? wb.acc_v + base * kWideD : nullptr, wb.acc_v ? int64_t(rows) * kWideD * 4 : 0);
+    const __amdgpu_buffer_rsrc_t av_rd = make_rsrc(wb.acc_v && !wb.v_first ? wb.acc_v + base * kWideD : nullptr,
+                                                   wb.acc_v && !wb.v_first ? int64_t(rows) * kWideD * 4 : 0);
+    const __amdgpu_buffer_rsrc_t fvr = make_rsrc(wb.fin_v ? static_cast<bf16_t*>(wb.fin_v) + base * kWideD : nullptr,
+                                                 wb.fin_v ? int64_t(rows) * kWideD * 2 : 0);
+
+    // Suffix state at the tile end: Z1^T[16 cb + 4 g + rr][16 w + lr] from the
+    // records of (group g2, value half cb / 4); Y1 from value half 0's.
+    f32x4 zt[8];
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+        const float* sr = (cb < 4 ? rec0 : rec1) + (n * tiles + ti) * rec;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) zt[cb][rr] = sr[sl * kBS + 16 * (cb & 3) + 4 * gq + rr];
+    }
+    float y1 = rec0[(n * tiles + ti) * rec + kBS * kBS + sl];
+    const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
+    const bf16x8 up0 = triu_frag(0, gq, lr), up1 = triu_frag(16, gq, lr);
+
+    // Staging: threads 0..383 take one block of 4 tokens x 8 columns of K,
+    // V or G (two waves per tensor); waves 6 and 7 stage nothing.
+    // The wave's tensor is uniform, so its buffer, stride and plane are
+    // chosen once; waves 6 and 7 get an empty view (loads return zero).
+    const int tensor = __builtin_amdgcn_readfirstlane(tid / G::kBlk);
+    const int sa = (tid % G::kBlk) / 16, sb = tid % 16;
+    const int sld = tensor == 0 ? ldq : kWideD;
+    const bf16_t* ssrc = tensor == 0 ? k + base * ldq : tensor == 1 ? v + base * kWideD : g + base * kWideD;
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
+    unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
+    StageBlock<bf16_t> st;
+    float qreg[2][4], dreg[2][4], vsum_n[2][4];
+    auto load_rows = [&](int r0) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = r0 + 16 * bi + 4 * gq + rr;
+                qreg[bi][rr] = load1<bf16_t>(qr, row * ldq + 16 * w + lr);
+                dreg[bi][rr] = load1<float>(d32r, row * kBS + sl);
+                vsum_n[bi][rr] = load1<float>(av_rd, row * kWideD + 16 * w + lr);
+            }
+    };
+
+    const int subs = tile / kBC;
+    const float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS + sl;
+    const int last = ((rows - 1) / kBC) * kBC;
+    st.load(srs, last, sa, sb, sld);
+    load_rows(last);
+    float a0n = ap[(last / kBC) * kBS];
+    for (int r0 = last; r0 >= 0; r0 -= kBC) {
+        __syncthreads();
+        if (tensor < 3) st.store_r<PR>(splane, sa, sb);
+        float qc[2][4], dc[2][4], vsum[2][4];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                qc[bi][rr] = qreg[bi][rr];
+                dc[bi][rr] = dreg[bi][rr];
+                vsum[bi][rr] = vsum_n[bi][rr];
+            }
+        const float a0 = a0n;
+        if (r0 > 0) {
+            st.load(srs, r0 - kBC, sa, sb, sld);
+            load_rows(r0 - kBC);
+            a0n = ap[(r0 / kBC - 1) * kBS];
+        }
+        // Z1 as a plane for dV: row s, four consecutive c per lane.
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+            uint2 hi, lo;
+            split4<false>(zt[cb][0], zt[cb][1], zt[cb][2], zt[cb][3], hi, lo);
+            PR::put4(Zr, 16 * w + lr, 16 * cb + 4 * gq, hi, lo);
+        }
+        __syncthreads();
+
+        // 1: Abar, r, W, alpha; W^T into its plane (row s, four consecutive i).
+        bf16x8 kh, kl;
+        PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
+        f32x4 wv[2], al[2];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            f32x4 acc = {a0, a0, a0, a0};
+            acc = mfma16(bi == 0 ? tri0 : tri1, kh, acc);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                wv[bi][rr] = qc[bi][rr] * __builtin_amdgcn_rcpf(acc[rr] + kEps);
+                al[bi][rr] = -wv[bi][rr] * dc[bi][rr];
+            }
+            uint2 hi, lo;
+            split4<false>(wv[bi][0], wv[bi][1], wv[bi][2], wv[bi][3], hi, lo);
+            PM::put4(WT, 16 * w + lr, 16 * bi + 4 * gq, hi, lo);
+        }
+        __syncthreads();
+
+        // 2: M = tril(G V^T) blocks on waves 0..2, P = tril(W K^T) blocks on
+        //    waves 3..5; blocks (0,0), (1,0), (1,1), written with rows j.
+        if (w < 6) {
+            const int b = w < 3 ? w : w - 3;
+            const int bi = b >= 1 ? 1 : 0, bj = b == 2 ? 1 : 0;
+            f32x4 m = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                bf16x8 ah, alo, bh, bl;
+                if (w < 3) {
+                    PR::frag(Gs, 16 * bi + lr, kk, gq, ah, alo);
+                    PR::frag(Vs, 16 * bj + lr, kk, gq, bh, bl);
+                } else {
+                    PM::frag_tr(WT, 32 * kk, 16 * bi, gq, lr, ah, alo);
+                    PR::frag(Ks, 16 * bj + lr, kk, gq, bh, bl);
+                }
+                m = mfma16(ah, bh, m);
+            }
+            if (bi == bj) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    if (lr > 4 * gq + rr) m[rr] = 0.f;
+            }
+            uint2 hi, lo;
+            split4<false>(m[0], m[1], m[2], m[3], hi, lo);
+            PM::put4(w < 3 ? MT : PTp, 16 * bj + lr, 16 * bi + 4 * gq, hi, lo);
+        }
+        __syncthreads();
+
+        bf16x8 wh, wl, ah2, al2;
+        split8v<false>(wv[0], wv[1], wh, wl);
+        split8v<false>(al[0], al[1], ah2, al2);
+        // 3: dK[j][s] for this wave's buckets: V Z1^T + M^T W + triu(1) alpha + Y1.
+        f32x4 dk[2];
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) dk[bj] = f32x4{y1, y1, y1, y1};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            bf16x8 zh, zl;
+            split8v<false>(zt[2 * kk], zt[2 * kk + 1], zh, zl);
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) {
+                bf16x8 vh, vl;
+                PR::frag(Vs, 16 * bj + lr, kk, gq, vh, vl);
+                dk[bj] = mfma16(vh, zh, dk[bj]);
+            }
+        }
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+            bf16x8 mh, ml;
+            PM::frag(MT, 16 * bj + lr, 0, gq, mh, ml);
+            if (bj == 1) {
+                // Tokens i < 16 of the second j-block are above the diagonal.
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mh[e] = __bf16(0.0f);
+            }
+            dk[bj] = mfma16(mh, wh, dk[bj]);
+            dk[bj] = mfma16(bj == 0 ? up0 : up1, ah2, dk[bj]);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                store1<bf16_t>(dkr, (r0 + 16 * bj + 4 * gq + rr) * ldq + 16 * w + lr, dk[bj][rr]);
+        }
+        // 4: dV[j][c] for this wave's value columns: K Z1 + P^T G.
+        {
+            f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                bf16x8 zh, zl;
+                PR::frag_tr(Zr, 32 * kk, 16 * w, gq, lr, zh, zl);
+#pragma unroll
+                for (int bj = 0; bj < 2; ++bj) {
+                    bf16x8 kh2, kl2;
+                    PR::frag(Ks, 16 * bj + lr, kk, gq, kh2, kl2);
+                    dv[bj] = mfma16(kh2, zh, dv[bj]);
+                }
+            }
+            bf16x8 gh, gl;
+            PR::frag_tr(Gs, 0, 16 * w, gq, lr, gh, gl);
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) {
+                bf16x8 ph, pl;
+                PM::frag(PTp, 16 * bj + lr, 0, gq, ph, pl);
+                if (bj == 1) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ph[e] = __bf16(0.0f);
+                }
+                dv[bj] = mfma16(ph, gh, dv[bj]);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int off = (r0 + 16 * bj + 4 * gq + rr) * kWideD + 16 * w + lr;
+                    // The first addend's read view is empty: vsum is zero.
+                    const float x = dv[bj][rr] + vsum[bj][rr];
+                    if (wb.fin_v)
+                        store1<bf16_t>(fvr, off, x);
+                    else
+                        store1<float>(avr, off, x);
+                }
+            }
+        }
+        // 5: the suffix state before this sub-chunk.
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+            bf16x8 gh, gl;
+            PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
+            zt[cb] = mfma16(gh, wh, zt[cb]);
+        }
+        float ys = 0.f;
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) ys += al[bi][rr];
+        ys = ys + __shfl_xor(ys, 16);
+        ys = ys + __shfl_xor(ys, 32);
+        y1 += ys;
+    }
+}
+
 }  // namespace
 
 bool causal_bwd_mfma_supported(int S, int d) {
@@ -922,6 +1196,20 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
     else
         RACE_DKV(float);
 #undef RACE_DKV
+    return hipGetLastError();
+}
+
+hipError_t launch_causal_bwd_dkv_wide(const void* q, const void* k, const void* v, const void* g, void* dK,
+                                      const Problem& p, const BwdWide& wb, hipStream_t stream) {
+    if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || p.tile % kBC != 0 || wb.ldq != p.S)
+        return hipErrorInvalidValue;
+    for (int g2 = 0; g2 < 2; ++g2)
+        if (!wb.dq32[g2] || !wb.apre[g2] || !wb.rec[g2][0] || !wb.rec[g2][1]) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    causal_bwd_dkv_wide_kernel<<<grid, kWideThreads, WideGeo::kLds, stream>>>(
+        static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
+        static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dK), p.T, p.tile, p.tiles, record_floats(kBS, kBS),
+        wb);
     return hipGetLastError();
 }
 

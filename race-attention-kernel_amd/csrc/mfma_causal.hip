@@ -421,9 +421,9 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void causal_output_mfma_kernel
     }
     int r0 = 0;
     for (; r0 < rows; r0 += kDepth * C) {
-        sub_chunk(st[0], qr[0], r0);
         // A sub-chunk past a ragged tile end reads zeros and stores nothing.
-        if constexpr (kDepth == 2) sub_chunk(st[1], qr[1], r0 + C);
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) sub_chunk(st[d], qr[d], r0 + d * C);
     }
     __syncthreads();
     if (r0 > 0) OT::template flush<kStoreP, G::kT>(Os, or_, r0 - C);

@@ -19,6 +19,12 @@ constexpr int64_t kMaxStreams = 65535;  // grid.y
 // (fewer tile records; measured faster at cfg3), every other path 4096.
 constexpr int kMaxAutoTile = 16384;
 constexpr int kMaxAutoTileOther = 4096;
+// Causal backward of bf16 tokens with d = 128 and S = 128 or 256: backward
+// walks over 128-bucket x 128-column blocks (causal_bwd_dkv_wide_kernel).
+#ifndef RACE_BWD_WIDE_WALKS
+#define RACE_BWD_WIDE_WALKS 1
+#endif
+constexpr bool kBwdWideWalks = RACE_BWD_WIDE_WALKS != 0;
 
 int64_t round64(int64_t floats) { return ((floats + 63) / 64) * 64; }
 
@@ -240,6 +246,10 @@ struct CausalBwdPlan {
     // bf16 with d = 128: one forward walk per bucket group over both value
     // groups (its dQ whole; no dQ running sum).
     bool wide() const { return blocked() && bf16 && hblocks == 2; }
+    // ... and, with an even number of bucket groups (S = 128 or 256), one
+    // backward walk per pair of them over every value column (their dK
+    // whole; dV summed over the pairs).
+    bool wide2() const { return wide() && mblocks % 2 == 0 && kBwdWideWalks; }
 };
 
 // The causal backward's kernel choices: automatic, vector ALU or matrix cores.
@@ -272,6 +282,16 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
     CausalBwdLayout l;
     const int64_t NT = p.N * p.T;
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
+    if (pl.wide2()) {
+        // The two bucket groups of a pair: suffix records of both value
+        // groups each, running mass and dq32 each; a dV running sum when
+        // there are several pairs.
+        l.bwd = 4 * p.N * p.tiles * record_floats(64, 64);
+        l.apre = 2 * round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
+        l.dq32 = 2 * round64(NT * 64);
+        l.acc = pl.mblocks > 2 ? round64(NT * p.d) : 0;
+        return l;
+    }
     if (pl.blocked()) {
         // One walk over both value groups (bf16, d = 128) keeps the suffix
         // records of both groups.
@@ -920,6 +940,62 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
         auto col = [](void* base, int64_t c, int64_t es_) -> void* {
             return base ? static_cast<void*>(static_cast<char*>(base) + c * es_) : nullptr;
         };
+        if (pl.wide2()) {
+            // Per pair of bucket groups (2 mp, 2 mp + 1): a forward walk over
+            // all 128 value columns for each (its dQ whole, straight to the
+            // caller's dQ; the suffix records of both value groups), one
+            // reverse scan of the pair's four record arrays, then one
+            // backward walk over the pair's 128 buckets and every value
+            // column: dK of those buckets whole, dV added to its running sum
+            // over the pairs in pair order (the last pair writes the
+            // caller's dV).
+            Problem p4 = pb;
+            p4.N = 4 * p.N;
+            const int64_t rec_n = p.N * p.tiles * pb.rec;
+            const int64_t apre_g = round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
+            const int64_t dq_g = round64(NT * 64);
+            const int pairs = pl.mblocks / 2;
+            for (int mp = 0; mp < pairs; ++mp) {
+                for (int g2 = 0; g2 < 2; ++g2) {
+                    const int m = 2 * mp + g2;
+                    BwdBlock b1;
+                    b1.ldq = p.S;
+                    b1.ldv = p.d;
+                    b1.s0 = 64 * m;
+                    b1.c0 = 0;
+                    b1.fwd_d = p.d;
+                    b1.fwd_a = int64_t(p.S) * p.d;
+                    b1.fwd_rec = p.rec;
+                    b1.blocked = 1;
+                    b1.q_first = 1;
+                    b1.fin_q = col(dQ, 64 * m, es);
+                    RACE_TRY(launch_causal_bwd_dq_mfma(static_cast<const char*>(probsQ) + 64 * m * es,
+                                                       static_cast<const char*>(probsK) + 64 * m * es, V, dOut,
+                                                       nullptr, dq32 + g2 * dq_g, apre + g2 * apre_g, fwd_rec,
+                                                       bwd_rec + 2 * g2 * rec_n, pb, b1, stream, 128));
+                    RACE_TRY(marks->mark(stream));
+                }
+                if (!dK && !dV) continue;
+                RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p4, stream, /*reverse=*/true));
+                RACE_TRY(marks->mark(stream));
+                BwdWide wb;
+                wb.ldq = p.S;
+                for (int g2 = 0; g2 < 2; ++g2) {
+                    wb.dq32[g2] = dq32 + g2 * dq_g;
+                    wb.apre[g2] = apre + g2 * apre_g;
+                    wb.rec[g2][0] = bwd_rec + (2 * g2) * rec_n;
+                    wb.rec[g2][1] = bwd_rec + (2 * g2 + 1) * rec_n;
+                }
+                wb.acc_v = dV && pairs > 1 ? acc : nullptr;
+                wb.v_first = mp == 0;
+                wb.fin_v = mp == pairs - 1 ? dV : nullptr;
+                RACE_TRY(launch_causal_bwd_dkv_wide(static_cast<const char*>(probsQ) + 128 * mp * es,
+                                                    static_cast<const char*>(probsK) + 128 * mp * es, V, dOut,
+                                                    col(dK, 128 * mp, es), p, wb, stream));
+                RACE_TRY(marks->mark(stream));
+            }
+            return RACE_SUCCESS;
+        }
         if (pl.wide()) {
             // Per bucket group m: one forward walk over all 128 value columns
             // (dQ of group m whole, straight to the caller's dQ; the suffix

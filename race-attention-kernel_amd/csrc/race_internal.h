@@ -260,6 +260,22 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
                                       const Problem& p, const BwdBlock& blk, hipStream_t stream);
+// The backward walk over a 128-bucket x 128-column block (bf16 tokens, d =
+// 128): the buffers the two 64-bucket forward walks of the block wrote, per
+// group g2 (buckets 64 g2 .. of the block), and dV's accumulation.
+struct BwdWide {
+    int ldq = 0;                                  // row stride of probsQ, probsK, dK (the full S)
+    const float* dq32[2] = {nullptr, nullptr};    // fp32 dQ per group, rows of 64
+    const float* apre[2] = {nullptr, nullptr};    // running mass per sub-chunk, per group
+    const float* rec[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};  // scanned suffix records (g2, value half)
+    float* acc_v = nullptr;  // dV's fp32 running sum (rows of 128), or null
+    void* fin_v = nullptr;   // the caller's dV (bf16) for the last addend, or null
+    int v_first = 1;         // the first addend writes acc_v without reading it
+};
+// dK of the block's buckets whole (q, k and dK point at its first bucket) and
+// its part of dV; p is the whole problem.
+hipError_t launch_causal_bwd_dkv_wide(const void* q, const void* k, const void* v, const void* g, void* dK,
+                                      const Problem& p, const BwdWide& wb, hipStream_t stream);
 // The forward's tile sums (K1) on the matrix cores for the shapes
 // mfma_causal_supported takes, into records of p.rec floats.
 hipError_t launch_tile_sums_mfma(const void* k, const void* v, float* records, const Problem& p,
