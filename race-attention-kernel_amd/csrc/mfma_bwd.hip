@@ -869,9 +869,217 @@ struct WideGeo {
     static constexpr int kMBytes = kBC * PM::kPitch;
     static constexpr int kZBytes = kWideS * PR::kPitch;   // Z1 [s][c]
     static constexpr int kLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
+    static constexpr int kDqLds = 3 * kRBytes + kMBytes + kBC * kWideS * 4;  // B1: K, V, G, M, dQ tile
     static constexpr int kBlk = (kBC / 4) * (128 / 8);    // staging blocks of one tensor
     static_assert(3 * kBlk <= kWideThreads && kBlk % 64 == 0, "one staging block per thread, a tensor per wave");
 };
+
+// B1 over a 128 x 128 block (bf16 tokens, d = 128): the forward walk of
+// causal_bwd_dq_mfma_kernel over 128 buckets and every value column at once,
+// eight waves (wave w: buckets 16 w .. 16 w + 15 of the block).  It writes
+// the block's dQ whole (bf16, the caller's dQ), its fp32 copy [N T][128], the
+// running mass at every sub-chunk start [N][tiles][subs][128], and the
+// tile's suffix totals as four 64 x 64 records, (bucket group g2, value
+// half h) at bwd_records + (2 g2 + h) N tiles rec.
+__global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ g, bf16_t* __restrict__ dQ, float* __restrict__ dq32,
+    float* __restrict__ apre, const float* __restrict__ fwd_records, float* __restrict__ bwd_records,
+    int64_t T, int tile, int64_t tiles, int64_t rec, int ldq, int s0, int64_t fwd_rec) {
+    using G = WideGeo;
+    using PR = G::PR;
+    using PM = G::PM;
+    using T32 = OutTile<float, kWideS, kBC>;
+    extern __shared__ __align__(16) unsigned char lds[];
+    unsigned char* Ks = lds;
+    unsigned char* Vs = Ks + G::kRBytes;
+    unsigned char* Gs = Vs + G::kRBytes;
+    unsigned char* Ms = Gs + G::kRBytes;
+    unsigned char* D32s = Ms + G::kMBytes;
+
+    const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = 16 * w + lr;  // the lane's bucket in the block
+    const int64_t n = blockIdx.y, ti = blockIdx.x;
+    const int64_t t_begin = ti * tile;
+    const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
+    const int64_t base = n * T + t_begin;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
+    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kWideS, int64_t(rows) * kWideS * 4);
+    const __amdgpu_buffer_rsrc_t dqr = make_rsrc(dQ ? dQ + base * ldq : nullptr, dQ ? int64_t(rows) * ldq * 2 : 0);
+
+    // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][s].
+    const float* fr = fwd_records + (n * tiles + ti) * fwd_rec;
+    f32x4 b0t[8], zt[8];
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            b0t[cb][rr] = fr[int64_t(s0 + s) * kWideD + 16 * cb + 4 * gq + rr];
+            zt[cb][rr] = 0.f;
+        }
+    // The forward record holds B [S][128] then A [S]; S = ldq.
+    float a0 = fr[int64_t(ldq) * kWideD + s0 + s];
+    float ypart = 0.f;
+    const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
+
+    // Staging as in causal_bwd_dkv_wide_kernel.
+    const int tensor = __builtin_amdgcn_readfirstlane(tid / G::kBlk);
+    const int sa = (tid % G::kBlk) / 16, sb = tid % 16;
+    const int sld = tensor == 0 ? ldq : kWideD;
+    const bf16_t* ssrc = tensor == 0 ? k + base * ldq : tensor == 1 ? v + base * kWideD : g + base * kWideD;
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
+    unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
+    StageBlock<bf16_t> st;
+    float qreg[2][4];
+    auto load_q = [&](int r0) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                qreg[bi][rr] = load1<bf16_t>(qr, (r0 + 16 * bi + 4 * gq + rr) * ldq + s);
+    };
+
+    const int subs = tile / kBC;
+    float* ap = apre + (n * tiles + ti) * int64_t(subs) * kWideS;
+    // The previous sub-chunk's dQ tile: whole rows of its fp32 copy, and dQ
+    // as bf16 (16-byte chunk c of a row holds elements 4 c .. 4 c + 3).
+    constexpr int kChunksPerRow = T32::kChunks;
+    auto flush = [&](int r0) {
+        typename T32::template Chunks<kWideThreads> c32;
+        T32::template read<kWideThreads>(D32s, c32);
+#pragma unroll
+        for (int i = 0; i < T32::template Chunks<kWideThreads>::kPer; ++i) {
+            const int qi = tid + i * kWideThreads;
+            const uint4 x = c32.x[i];
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{pack2(__uint_as_float(x.x), __uint_as_float(x.y)),
+                      pack2(__uint_as_float(x.z), __uint_as_float(x.w))},
+                dqr, ((r0 + qi / kChunksPerRow) * ldq + 4 * (qi % kChunksPerRow)) * 2, 0, kPolicyDefault);
+        }
+        T32::template write<kPolicyDefault, kWideThreads>(c32, d32r, r0);
+    };
+    st.load(srs, 0, sa, sb, sld);
+    load_q(0);
+    int r0 = 0;
+    for (; r0 < rows; r0 += kBC) {
+        __syncthreads();
+        if (tensor < 3) st.store_r<PR>(splane, sa, sb);
+        float qc[2][4];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
+        st.load(srs, r0 + kBC, sa, sb, sld);  // past the tile: zeros, never used
+        load_q(r0 + kBC);
+        // Unconditional: at r0 = 0 the offsets are negative, outside the
+        // buffer ranges, and the stores are dropped.
+        flush(r0 - kBC);
+        if (gq == 0) ap[(r0 / kBC) * kWideS + s] = a0;
+        __syncthreads();
+
+        // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
+        bf16x8 kh, kl;
+        PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
+        f32x4 rv[2], wv[2];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            f32x4 acc = {a0, a0, a0, a0};
+            acc = mfma16(bi == 0 ? tri0 : tri1, kh, acc);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                rv[bi][rr] = __builtin_amdgcn_rcpf(acc[rr] + kEps);
+                wv[bi][rr] = qc[bi][rr] * rv[bi][rr];
+            }
+            if (bi == 1) a0 = __shfl(acc[3], 48 + lr);  // inclusive mass at the last token
+        }
+
+        // 2: M^T blocks (j-block, i-block) = V G^T, j <= i: (0,0), (0,1), (1,1) on waves 0..2.
+        if (w < 3) {
+            const int mbj = w == 2 ? 1 : 0, mbi = w >= 1 ? 1 : 0;
+            f32x4 mt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                bf16x8 ah, al, bh, bl;
+                PR::frag(Vs, 16 * mbj + lr, kk, gq, ah, al);
+                PR::frag(Gs, 16 * mbi + lr, kk, gq, bh, bl);
+                mt = mfma16(ah, bh, mt);
+            }
+            if (mbj == mbi) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    if (4 * gq + rr > lr) mt[rr] = 0.f;
+            }
+            uint2 hi, lo;
+            split4<false>(mt[0], mt[1], mt[2], mt[3], hi, lo);
+            PM::put4(Ms, 16 * mbi + lr, 16 * mbj + 4 * gq, hi, lo);
+        }
+        __syncthreads();
+
+        // 3: U = G B0^T + M K;  dQ = r U;  alpha = -W dQ.
+        f32x4 u[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            bf16x8 bh, bl;
+            split8v<false>(b0t[2 * kk], b0t[2 * kk + 1], bh, bl);
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi) {
+                bf16x8 gh, gl;
+                PR::frag(Gs, 16 * bi + lr, kk, gq, gh, gl);
+                u[bi] = mfma16(gh, bh, u[bi]);
+            }
+        }
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            bf16x8 mh, ml;
+            PM::frag(Ms, 16 * bi + lr, 0, gq, mh, ml);
+            if (bi == 0) {
+                // Tokens 16..31 of the first block's row are above the diagonal.
+#pragma unroll
+                for (int e = 4; e < 8; ++e) mh[e] = __bf16(0.0f);
+            }
+            u[bi] = mfma16(mh, kh, u[bi]);
+        }
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const float dqv = rv[bi][rr] * u[bi][rr];
+                T32::put1(D32s, 16 * bi + 4 * gq + rr, s, dqv);
+                ypart += -wv[bi][rr] * dqv;
+            }
+
+        // 4: Z^T += G^T W;  5: B0^T += V^T K.
+        bf16x8 wh, wl;
+        split8v<false>(wv[0], wv[1], wh, wl);
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+            bf16x8 gh, gl, vh, vl;
+            PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
+            zt[cb] = mfma16(gh, wh, zt[cb]);
+            PR::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
+            b0t[cb] = mfma16(vh, kh, b0t[cb]);
+        }
+    }
+    __syncthreads();
+    if (r0 > 0) flush(r0 - kBC);
+
+    // Suffix totals of this tile into the four 64 x 64 records: Z[s][c]
+    // (record layout B[s][c]) and Y[s], the totals of alpha, in value half
+    // 0's record (half 1's holds zero).
+    float y = ypart + __shfl_xor(ypart, 16);
+    y = y + __shfl_xor(y, 32);
+    const int g2 = w >> 2, sl = 16 * (w & 3) + lr;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float* br = bwd_records + (int64_t(2 * g2 + h) * gridDim.y * tiles + n * tiles + ti) * rec;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) br[sl * kBS + 16 * cb + 4 * gq + rr] = zt[4 * h + cb][rr];
+        if (gq == 0) br[kBS * kBS + sl] = h == 0 ? y : 0.f;
+    }
+}
 
 __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -900,12 +1108,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     const int ldq = wb.ldq;
     // The group's buffers, chosen without indexing the argument struct by a
     // run-time value (which copies it to scratch memory).
-    const float* dq32 = g2 ? wb.dq32[1] : wb.dq32[0];
-    const float* apre = g2 ? wb.apre[1] : wb.apre[0];
     const float* rec0 = g2 ? wb.rec[1][0] : wb.rec[0][0];
     const float* rec1 = g2 ? wb.rec[1][1] : wb.rec[0][1];
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
-    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kBS, int64_t(rows) * kBS * 4);
+    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(wb.dq32 + base * kWideS, int64_t(rows) * kWideS * 4);
     const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * ldq : nullptr, dK ? int64_t(rows) * ldq * 2 : 0);
     // dV: the running sum (written; read unless this is the first addend)
     // and the caller's dV for the last addend.  A gradient not asked for has
@@ -949,17 +1155,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
             for (int rr = 0; rr < 4; ++rr) {
                 const int row = r0 + 16 * bi + 4 * gq + rr;
                 qreg[bi][rr] = load1<bf16_t>(qr, row * ldq + 16 * w + lr);
-                dreg[bi][rr] = load1<float>(d32r, row * kBS + sl);
+                dreg[bi][rr] = load1<float>(d32r, row * kWideS + 16 * w + lr);
                 vsum_n[bi][rr] = load1<float>(av_rd, row * kWideD + 16 * w + lr);
             }
     };
 
     const int subs = tile / kBC;
-    const float* ap = apre + (n * tiles + ti) * int64_t(subs) * kBS + sl;
+    const float* ap = wb.apre + (n * tiles + ti) * int64_t(subs) * kWideS + 16 * w + lr;
     const int last = ((rows - 1) / kBC) * kBC;
     st.load(srs, last, sa, sb, sld);
     load_rows(last);
-    float a0n = ap[(last / kBC) * kBS];
+    float a0n = ap[(last / kBC) * kWideS];
     for (int r0 = last; r0 >= 0; r0 -= kBC) {
         __syncthreads();
         if (tensor < 3) st.store_r<PR>(splane, sa, sb);
@@ -976,7 +1182,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
         if (r0 > 0) {
             st.load(srs, r0 - kBC, sa, sb, sld);
             load_rows(r0 - kBC);
-            a0n = ap[(r0 / kBC - 1) * kBS];
+            a0n = ap[(r0 / kBC - 1) * kWideS];
         }
         // Z1 as a plane for dV: row s, four consecutive c per lane.
 #pragma unroll
@@ -1199,12 +1405,27 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
     return hipGetLastError();
 }
 
+hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dQ,
+                                     float* dq32, float* apre, const float* fwd_records, float* bwd_records,
+                                     const Problem& p, int s0, hipStream_t stream) {
+    if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || s0 % kWideS != 0 || s0 >= p.S ||
+        p.tile % kBC != 0)
+        return hipErrorInvalidValue;
+    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    causal_bwd_dq_wide_kernel<<<grid, kWideThreads, WideGeo::kDqLds, stream>>>(
+        static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
+        static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ), dq32, apre, fwd_records, bwd_records, p.T,
+        p.tile, p.tiles, record_floats(kBS, kBS), p.S, s0, p.rec);
+    return hipGetLastError();
+}
+
 hipError_t launch_causal_bwd_dkv_wide(const void* q, const void* k, const void* v, const void* g, void* dK,
                                       const Problem& p, const BwdWide& wb, hipStream_t stream) {
     if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || p.tile % kBC != 0 || wb.ldq != p.S)
         return hipErrorInvalidValue;
+    if (!wb.dq32 || !wb.apre) return hipErrorInvalidValue;
     for (int g2 = 0; g2 < 2; ++g2)
-        if (!wb.dq32[g2] || !wb.apre[g2] || !wb.rec[g2][0] || !wb.rec[g2][1]) return hipErrorInvalidValue;
+        if (!wb.rec[g2][0] || !wb.rec[g2][1]) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     causal_bwd_dkv_wide_kernel<<<grid, kWideThreads, WideGeo::kLds, stream>>>(
         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),

@@ -283,12 +283,12 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
     const int64_t NT = p.N * p.T;
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
     if (pl.wide2()) {
-        // The two bucket groups of a pair: suffix records of both value
-        // groups each, running mass and dq32 each; a dV running sum when
-        // there are several pairs.
+        // A pair of bucket groups: the suffix records of its four 64 x 64
+        // blocks, its running mass and dq32 (128 buckets); a dV running sum
+        // when there are several pairs.
         l.bwd = 4 * p.N * p.tiles * record_floats(64, 64);
-        l.apre = 2 * round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
-        l.dq32 = 2 * round64(NT * 64);
+        l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(128));
+        l.dq32 = round64(NT * 128);
         l.acc = pl.mblocks > 2 ? round64(NT * p.d) : 0;
         return l;
     }
@@ -941,48 +941,31 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
             return base ? static_cast<void*>(static_cast<char*>(base) + c * es_) : nullptr;
         };
         if (pl.wide2()) {
-            // Per pair of bucket groups (2 mp, 2 mp + 1): a forward walk over
-            // all 128 value columns for each (its dQ whole, straight to the
-            // caller's dQ; the suffix records of both value groups), one
-            // reverse scan of the pair's four record arrays, then one
-            // backward walk over the pair's 128 buckets and every value
-            // column: dK of those buckets whole, dV added to its running sum
-            // over the pairs in pair order (the last pair writes the
-            // caller's dV).
+            // Per pair of bucket groups (buckets 128 mp ..): one forward walk
+            // over its 128 buckets and every value column (its dQ whole,
+            // straight to the caller's dQ; the suffix records of its four
+            // 64 x 64 blocks), one reverse scan of those records, then one
+            // backward walk over the same block: dK of its buckets whole, dV
+            // added to its running sum over the pairs in pair order (the
+            // last pair writes the caller's dV).
             Problem p4 = pb;
             p4.N = 4 * p.N;
             const int64_t rec_n = p.N * p.tiles * pb.rec;
-            const int64_t apre_g = round64(p.N * p.tiles * (p.tile / 16) * int64_t(64));
-            const int64_t dq_g = round64(NT * 64);
             const int pairs = pl.mblocks / 2;
             for (int mp = 0; mp < pairs; ++mp) {
-                for (int g2 = 0; g2 < 2; ++g2) {
-                    const int m = 2 * mp + g2;
-                    BwdBlock b1;
-                    b1.ldq = p.S;
-                    b1.ldv = p.d;
-                    b1.s0 = 64 * m;
-                    b1.c0 = 0;
-                    b1.fwd_d = p.d;
-                    b1.fwd_a = int64_t(p.S) * p.d;
-                    b1.fwd_rec = p.rec;
-                    b1.blocked = 1;
-                    b1.q_first = 1;
-                    b1.fin_q = col(dQ, 64 * m, es);
-                    RACE_TRY(launch_causal_bwd_dq_mfma(static_cast<const char*>(probsQ) + 64 * m * es,
-                                                       static_cast<const char*>(probsK) + 64 * m * es, V, dOut,
-                                                       nullptr, dq32 + g2 * dq_g, apre + g2 * apre_g, fwd_rec,
-                                                       bwd_rec + 2 * g2 * rec_n, pb, b1, stream, 128));
-                    RACE_TRY(marks->mark(stream));
-                }
+                RACE_TRY(launch_causal_bwd_dq_wide(static_cast<const char*>(probsQ) + 128 * mp * es,
+                                                   static_cast<const char*>(probsK) + 128 * mp * es, V, dOut,
+                                                   col(dQ, 128 * mp, es), dq32, apre, fwd_rec, bwd_rec, p,
+                                                   128 * mp, stream));
+                RACE_TRY(marks->mark(stream));
                 if (!dK && !dV) continue;
                 RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p4, stream, /*reverse=*/true));
                 RACE_TRY(marks->mark(stream));
                 BwdWide wb;
                 wb.ldq = p.S;
+                wb.dq32 = dq32;
+                wb.apre = apre;
                 for (int g2 = 0; g2 < 2; ++g2) {
-                    wb.dq32[g2] = dq32 + g2 * dq_g;
-                    wb.apre[g2] = apre + g2 * apre_g;
                     wb.rec[g2][0] = bwd_rec + (2 * g2) * rec_n;
                     wb.rec[g2][1] = bwd_rec + (2 * g2 + 1) * rec_n;
                 }

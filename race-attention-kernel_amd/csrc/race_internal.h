@@ -260,13 +260,21 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
                                       const Problem& p, const BwdBlock& blk, hipStream_t stream);
-// The backward walk over a 128-bucket x 128-column block (bf16 tokens, d =
-// 128): the buffers the two 64-bucket forward walks of the block wrote, per
-// group g2 (buckets 64 g2 .. of the block), and dV's accumulation.
+// The forward walk (B1) over a 128-bucket x 128-column block (bf16 tokens,
+// d = 128; buckets s0 .. s0 + 127, with q, k and dQ pointing at bucket s0 of
+// the full tensors and fwd_records the full problem's): dQ of those buckets
+// whole, dq32 [N T][128], the running mass
+// [N][tiles][tile / 32][128] and the suffix records of the block's four 64 x
+// 64 blocks, (group g2, value half h) at bwd_records + (2 g2 + h) N tiles rec.
+hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dQ,
+                                     float* dq32, float* apre, const float* fwd_records, float* bwd_records,
+                                     const Problem& p, int s0, hipStream_t stream);
+// The backward walk over the same block: the buffers its forward walk wrote
+// and dV's accumulation.
 struct BwdWide {
-    int ldq = 0;                                  // row stride of probsQ, probsK, dK (the full S)
-    const float* dq32[2] = {nullptr, nullptr};    // fp32 dQ per group, rows of 64
-    const float* apre[2] = {nullptr, nullptr};    // running mass per sub-chunk, per group
+    int ldq = 0;                 // row stride of probsQ, probsK, dK (the full S)
+    const float* dq32 = nullptr; // fp32 dQ of the block, rows of 128
+    const float* apre = nullptr; // running mass per sub-chunk, rows of 128
     const float* rec[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};  // scanned suffix records (g2, value half)
     float* acc_v = nullptr;  // dV's fp32 running sum (rows of 128), or null
     void* fin_v = nullptr;   // the caller's dV (bf16) for the last addend, or null

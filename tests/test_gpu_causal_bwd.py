@@ -161,10 +161,12 @@ def test_matches_torch_autograd(race, oracle, cuda):
 
 @pytest.mark.parametrize("need", [(True, False, False), (False, True, False), (False, False, True),
                                   (False, True, True)])
-@pytest.mark.parametrize("L, R, d, dtype", [(4, 16, 64, torch.float32), (4, 32, 128, torch.bfloat16)])
+@pytest.mark.parametrize("L, R, d, dtype", [(4, 16, 64, torch.float32), (4, 32, 128, torch.bfloat16),
+                                            (8, 32, 128, torch.bfloat16)])
 def test_only_requested_gradients(race, cuda, need, L, R, d, dtype):
-    # (4, 32, 128) bf16: the blocked backward whose forward walk takes both
-    # value groups at once.
+    # bf16 with d = 128: walks over 128-bucket x 128-column blocks, one block
+    # at S = 128 (4, 32) and two at S = 256 (8, 32), whose dV goes through a
+    # running sum over the blocks.
     say("c-bwd needs-grad", need, L, R, d, dtype)
     q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, 500, L, R, d, seed=24, dtype=dtype, grad_out=True))
     leaves = [x.clone().requires_grad_(n) for x, n in zip((q, k, v), need)]
