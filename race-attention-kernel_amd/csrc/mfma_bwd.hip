@@ -869,7 +869,14 @@ struct WideGeo {
     static constexpr int kMBytes = kBC * PM::kPitch;
     static constexpr int kZBytes = kWideS * PR::kPitch;   // Z1 [s][c]
     static constexpr int kLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
-    static constexpr int kDqLds = 3 * kRBytes + kMBytes + kBC * kWideS * 4;  // B1: K, V, G, M, dQ tile
+    using QT = OutTile<bf16_t, kWideS, kBC>;  // rows of 128 bf16
+    using FT = OutTile<float, kWideS, kBC>;   // rows of 128 fp32
+    static constexpr int kQTBytes = kBC * QT::kRowBytes;
+    static constexpr int kFTBytes = kBC * FT::kRowBytes;
+    static constexpr int kDqLds = 3 * kRBytes + kMBytes + kFTBytes + kQTBytes;  // B1: K, V, G, M, dQ tile, Q rows
+    // B3 with its row tiles: Q, dq32, dV's sum in; dK, dV out.
+    static constexpr int kDkvLds = kLds + 2 * kQTBytes + 3 * kFTBytes;
+    static_assert(kDkvLds <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
     static constexpr int kBlk = (kBC / 4) * (128 / 8);    // staging blocks of one tensor
     static_assert(3 * kBlk <= kWideThreads && kBlk % 64 == 0, "one staging block per thread, a tensor per wave");
 };
@@ -896,6 +903,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     unsigned char* Gs = Vs + G::kRBytes;
     unsigned char* Ms = Gs + G::kRBytes;
     unsigned char* D32s = Ms + G::kMBytes;
+    unsigned char* Qt = D32s + kBC * kWideS * 4;  // Q rows of the sub-chunk
+    using QT = G::QT;
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -931,13 +940,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
     unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
     StageBlock<bf16_t> st;
-    float qreg[2][4];
+    // Q's rows: chunk tid of the sub-chunk (row tid / 16, 8 buckets) in
+    // from global memory, then read in the accumulator layout.
+    static_assert(QT::kChunks * kBC == kWideThreads, "one Q chunk per thread");
+    uint4 qx;
     auto load_q = [&](int r0) {
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                qreg[bi][rr] = load1<bf16_t>(qr, (r0 + 16 * bi + 4 * gq + rr) * ldq + s);
+        qx = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
     };
 
     const int subs = tile / kBC;
@@ -965,11 +973,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     for (; r0 < rows; r0 += kBC) {
         __syncthreads();
         if (tensor < 3) st.store_r<PR>(splane, sa, sb);
-        float qc[2][4];
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
+        *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qx;
         st.load(srs, r0 + kBC, sa, sb, sld);  // past the tile: zeros, never used
         load_q(r0 + kBC);
         // Unconditional: at r0 = 0 the offsets are negative, outside the
@@ -979,6 +983,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
         __syncthreads();
 
         // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
+        float qc[2][4];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                qc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Qt + QT::at(16 * bi + 4 * gq + rr, 2 * s)));
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         f32x4 rv[2], wv[2];
@@ -1096,6 +1106,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     unsigned char* MT = WT + G::kWTBytes;
     unsigned char* PTp = MT + G::kMBytes;
     unsigned char* Zr = PTp + G::kMBytes;
+    // Row tiles: Q, dq32 and dV's running sum of the sub-chunk in (whole rows
+    // in from global memory, read in the accumulator layout), dK and dV of
+    // the previous one out (written in the accumulator layout, stored as
+    // whole rows).
+    unsigned char* Qt = Zr + G::kZBytes;
+    unsigned char* Dt = Qt + G::kQTBytes;
+    unsigned char* Vt = Dt + G::kFTBytes;
+    unsigned char* dKt = Vt + G::kFTBytes;
+    unsigned char* dVt = dKt + G::kQTBytes;
+    using QT = G::QT;
+    using FT = G::FT;
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1147,17 +1168,47 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
     unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
     StageBlock<bf16_t> st;
-    float qreg[2][4], dreg[2][4], vsum_n[2][4];
+    // Row chunks of 16 bytes: Q's chunk tid (row tid / 16 of the sub-chunk,
+    // 8 buckets), dq32's and the dV sum's chunks tid and tid + 512 (rows of
+    // 32 chunks).
+    static_assert(QT::kChunks * kBC == kWideThreads && FT::kChunks * kBC == 2 * kWideThreads, "chunk split");
+    uint4 qx, dx[2], vx[2];
     auto load_rows = [&](int r0) {
+        qx = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
+        for (int i = 0; i < 2; ++i) {
+            dx[i] = buf_load16<kPolicyDefault>(d32r, r0 * FT::kRowBytes + 16 * (tid + i * kWideThreads));
+            vx[i] = buf_load16<kPolicyDefault>(av_rd, r0 * FT::kRowBytes + 16 * (tid + i * kWideThreads));
+        }
+    };
+    auto store_rows = [&]() {
+        *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qx;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = r0 + 16 * bi + 4 * gq + rr;
-                qreg[bi][rr] = load1<bf16_t>(qr, row * ldq + 16 * w + lr);
-                dreg[bi][rr] = load1<float>(d32r, row * kWideS + 16 * w + lr);
-                vsum_n[bi][rr] = load1<float>(av_rd, row * kWideD + 16 * w + lr);
-            }
+        for (int i = 0; i < 2; ++i) {
+            *reinterpret_cast<uint4*>(Dt + FT::chunk_at(tid + i * kWideThreads)) = dx[i];
+            *reinterpret_cast<uint4*>(Vt + FT::chunk_at(tid + i * kWideThreads)) = vx[i];
+        }
+    };
+    // dK and dV rows of the sub-chunk at r0 (rows past the tile, and all of
+    // them before the first sub-chunk, fall outside the views).
+    auto flush = [&](int r0) {
+        const uint4 kx = *reinterpret_cast<const uint4*>(dKt + QT::chunk_at(tid));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, kx), dkr,
+                                               ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2, 0,
+                                               kPolicyDefault);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kWideThreads;
+            const uint4 x = *reinterpret_cast<const uint4*>(dVt + FT::chunk_at(c));
+            if (wb.fin_v)
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    u32x2{pack2(__uint_as_float(x.x), __uint_as_float(x.y)),
+                          pack2(__uint_as_float(x.z), __uint_as_float(x.w))},
+                    fvr, (r0 * kWideD + 4 * c) * 2, 0, kPolicyDefault);
+            else
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), avr, (r0 * kWideD + 4 * c) * 4,
+                                                       0, kPolicyDefault);
+        }
     };
 
     const int subs = tile / kBC;
@@ -1168,16 +1219,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     float a0n = ap[(last / kBC) * kWideS];
     for (int r0 = last; r0 >= 0; r0 -= kBC) {
         __syncthreads();
+        flush(r0 + kBC);
         if (tensor < 3) st.store_r<PR>(splane, sa, sb);
-        float qc[2][4], dc[2][4], vsum[2][4];
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                qc[bi][rr] = qreg[bi][rr];
-                dc[bi][rr] = dreg[bi][rr];
-                vsum[bi][rr] = vsum_n[bi][rr];
-            }
+        store_rows();
         const float a0 = a0n;
         if (r0 > 0) {
             st.load(srs, r0 - kBC, sa, sb, sld);
@@ -1194,6 +1238,15 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
         __syncthreads();
 
         // 1: Abar, r, W, alpha; W^T into its plane (row s, four consecutive i).
+        float qc[2][4], dc[2][4];
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = 16 * bi + 4 * gq + rr;
+                qc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Qt + QT::at(row, 2 * (16 * w + lr))));
+                dc[bi][rr] = *reinterpret_cast<const float*>(Dt + FT::at(row, 4 * (16 * w + lr)));
+            }
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         f32x4 wv[2], al[2];
@@ -1271,8 +1324,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
             dk[bj] = mfma16(mh, wh, dk[bj]);
             dk[bj] = mfma16(bj == 0 ? up0 : up1, ah2, dk[bj]);
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                store1<bf16_t>(dkr, (r0 + 16 * bj + 4 * gq + rr) * ldq + 16 * w + lr, dk[bj][rr]);
+            for (int rr = 0; rr < 4; ++rr) QT::put1(dKt, 16 * bj + 4 * gq + rr, 16 * w + lr, dk[bj][rr]);
         }
         // 4: dV[j][c] for this wave's value columns: K Z1 + P^T G.
         {
@@ -1301,13 +1353,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
                 dv[bj] = mfma16(ph, gh, dv[bj]);
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    const int off = (r0 + 16 * bj + 4 * gq + rr) * kWideD + 16 * w + lr;
-                    // The first addend's read view is empty: vsum is zero.
-                    const float x = dv[bj][rr] + vsum[bj][rr];
-                    if (wb.fin_v)
-                        store1<bf16_t>(fvr, off, x);
-                    else
-                        store1<float>(avr, off, x);
+                    const int row = 16 * bj + 4 * gq + rr;
+                    // The first addend's read view is empty: the sum is zero.
+                    const float sum = *reinterpret_cast<const float*>(Vt + FT::at(row, 4 * (16 * w + lr)));
+                    FT::put1(dVt, row, 16 * w + lr, dv[bj][rr] + sum);
                 }
             }
         }
@@ -1327,6 +1376,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
         ys = ys + __shfl_xor(ys, 32);
         y1 += ys;
     }
+    __syncthreads();
+    flush(0);
 }
 
 }  // namespace
@@ -1427,7 +1478,7 @@ hipError_t launch_causal_bwd_dkv_wide(const void* q, const void* k, const void* 
     for (int g2 = 0; g2 < 2; ++g2)
         if (!wb.rec[g2][0] || !wb.rec[g2][1]) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
-    causal_bwd_dkv_wide_kernel<<<grid, kWideThreads, WideGeo::kLds, stream>>>(
+    causal_bwd_dkv_wide_kernel<<<grid, kWideThreads, WideGeo::kDkvLds, stream>>>(
         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
         static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dK), p.T, p.tile, p.tiles, record_floats(kBS, kBS),
         wb);
