@@ -874,8 +874,8 @@ struct WideGeo {
     static constexpr int kQTBytes = kBC * QT::kRowBytes;
     static constexpr int kFTBytes = kBC * FT::kRowBytes;
     static constexpr int kDqLds = 3 * kRBytes + kMBytes + kFTBytes + kQTBytes;  // B1: K, V, G, M, dQ tile, Q rows
-    // B3 with its row tiles: Q, dq32, dV's sum in; dK, dV out.
-    static constexpr int kDkvLds = kLds + 2 * kQTBytes + 3 * kFTBytes;
+    // B3 with its row tiles: Q, dQ hi and lo, dV's sum in; dK, dV out.
+    static constexpr int kDkvLds = kLds + 4 * kQTBytes + 2 * kFTBytes;
     static_assert(kDkvLds <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
     static constexpr int kBlk = (kBC / 4) * (128 / 8);    // staging blocks of one tensor
     static_assert(3 * kBlk <= kWideThreads && kBlk % 64 == 0, "one staging block per thread, a tensor per wave");
@@ -890,9 +890,9 @@ struct WideGeo {
 // half h) at bwd_records + (2 g2 + h) N tiles rec.
 __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const bf16_t* __restrict__ g, bf16_t* __restrict__ dQ, float* __restrict__ dq32,
+    const bf16_t* __restrict__ g, bf16_t* __restrict__ dq_hi, bf16_t* __restrict__ dq_lo,
     float* __restrict__ apre, const float* __restrict__ fwd_records, float* __restrict__ bwd_records,
-    int64_t T, int tile, int64_t tiles, int64_t rec, int ldq, int s0, int64_t fwd_rec) {
+    int64_t T, int tile, int64_t tiles, int64_t rec, int ldq, int ld_hi, int s0, int64_t fwd_rec) {
     using G = WideGeo;
     using PR = G::PR;
     using PM = G::PM;
@@ -914,8 +914,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
     const int64_t base = n * T + t_begin;
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
-    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(dq32 + base * kWideS, int64_t(rows) * kWideS * 4);
-    const __amdgpu_buffer_rsrc_t dqr = make_rsrc(dQ ? dQ + base * ldq : nullptr, dQ ? int64_t(rows) * ldq * 2 : 0);
+    // dQ as bf16 (hi, the caller's dQ or workspace rows of ld_hi) and the
+    // bf16 rounding of its remainder (lo, rows of 128): hi + lo is dQ to
+    // about 2^-17, which the backward walk reads back.
+    const __amdgpu_buffer_rsrc_t hir = make_rsrc(dq_hi + base * ld_hi, int64_t(rows) * ld_hi * 2);
+    const __amdgpu_buffer_rsrc_t lor = make_rsrc(dq_lo + base * kWideS, int64_t(rows) * kWideS * 2);
 
     // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][s].
     const float* fr = fwd_records + (n * tiles + ti) * fwd_rec;
@@ -959,13 +962,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
 #pragma unroll
         for (int i = 0; i < T32::template Chunks<kWideThreads>::kPer; ++i) {
             const int qi = tid + i * kWideThreads;
-            const uint4 x = c32.x[i];
-            __builtin_amdgcn_raw_buffer_store_b64(
-                u32x2{pack2(__uint_as_float(x.x), __uint_as_float(x.y)),
-                      pack2(__uint_as_float(x.z), __uint_as_float(x.w))},
-                dqr, ((r0 + qi / kChunksPerRow) * ldq + 4 * (qi % kChunksPerRow)) * 2, 0, kPolicyDefault);
+            const f32x4 x = __builtin_bit_cast(f32x4, c32.x[i]);
+            const u32x2 hi = {pack2(x[0], x[1]), pack2(x[2], x[3])};
+            const u32x2 lo = {pack2(x[0] - lo_half(hi[0]), x[1] - hi_half(hi[0])),
+                              pack2(x[2] - lo_half(hi[1]), x[3] - hi_half(hi[1]))};
+            const int row = r0 + qi / kChunksPerRow, c4 = 4 * (qi % kChunksPerRow);
+            __builtin_amdgcn_raw_buffer_store_b64(hi, hir, (row * ld_hi + c4) * 2, 0, kPolicyDefault);
+            __builtin_amdgcn_raw_buffer_store_b64(lo, lor, (row * kWideS + c4) * 2, 0, kPolicyDefault);
         }
-        T32::template write<kPolicyDefault, kWideThreads>(c32, d32r, r0);
     };
     st.load(srs, 0, sa, sb, sld);
     load_q(0);
@@ -1106,13 +1110,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     unsigned char* MT = WT + G::kWTBytes;
     unsigned char* PTp = MT + G::kMBytes;
     unsigned char* Zr = PTp + G::kMBytes;
-    // Row tiles: Q, dq32 and dV's running sum of the sub-chunk in (whole rows
+    // Row tiles: Q, dQ (hi and lo) and dV's running sum of the sub-chunk in (whole rows
     // in from global memory, read in the accumulator layout), dK and dV of
     // the previous one out (written in the accumulator layout, stored as
     // whole rows).
     unsigned char* Qt = Zr + G::kZBytes;
-    unsigned char* Dt = Qt + G::kQTBytes;
-    unsigned char* Vt = Dt + G::kFTBytes;
+    unsigned char* Dh = Qt + G::kQTBytes;
+    unsigned char* Dl = Dh + G::kQTBytes;
+    unsigned char* Vt = Dl + G::kQTBytes;
     unsigned char* dKt = Vt + G::kFTBytes;
     unsigned char* dVt = dKt + G::kQTBytes;
     using QT = G::QT;
@@ -1132,7 +1137,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     const float* rec0 = g2 ? wb.rec[1][0] : wb.rec[0][0];
     const float* rec1 = g2 ? wb.rec[1][1] : wb.rec[0][1];
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
-    const __amdgpu_buffer_rsrc_t d32r = make_rsrc(wb.dq32 + base * kWideS, int64_t(rows) * kWideS * 4);
+    const __amdgpu_buffer_rsrc_t hir =
+        make_rsrc(static_cast<const bf16_t*>(wb.dq_hi) + base * wb.ld_hi, int64_t(rows) * wb.ld_hi * 2);
+    const __amdgpu_buffer_rsrc_t lor =
+        make_rsrc(static_cast<const bf16_t*>(wb.dq_lo) + base * kWideS, int64_t(rows) * kWideS * 2);
     const __amdgpu_buffer_rsrc_t dkr = make_rsrc(dK ? dK + base * ldq : nullptr, dK ? int64_t(rows) * ldq * 2 : 0);
     // dV: the running sum (written; read unless this is the first addend)
     // and the caller's dV for the last addend.  A gradient not asked for has
@@ -1168,26 +1176,26 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
     unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
     StageBlock<bf16_t> st;
-    // Row chunks of 16 bytes: Q's chunk tid (row tid / 16 of the sub-chunk,
-    // 8 buckets), dq32's and the dV sum's chunks tid and tid + 512 (rows of
-    // 32 chunks).
+    // Row chunks of 16 bytes: Q's, dQ's hi and lo chunk tid (row tid / 16 of
+    // the sub-chunk, 8 buckets), the dV sum's chunks tid and tid + 512 (rows
+    // of 32 chunks).
     static_assert(QT::kChunks * kBC == kWideThreads && FT::kChunks * kBC == 2 * kWideThreads, "chunk split");
-    uint4 qx, dx[2], vx[2];
+    uint4 qx, hx, lx, vx[2];
     auto load_rows = [&](int r0) {
-        qx = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
+        const int row = r0 + tid / QT::kChunks, c8 = 8 * (tid % QT::kChunks);
+        qx = buf_load16<kPolicyDefault>(qr, (row * ldq + c8) * 2);
+        hx = buf_load16<kPolicyDefault>(hir, (row * wb.ld_hi + c8) * 2);
+        lx = buf_load16<kPolicyDefault>(lor, (row * kWideS + c8) * 2);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            dx[i] = buf_load16<kPolicyDefault>(d32r, r0 * FT::kRowBytes + 16 * (tid + i * kWideThreads));
+        for (int i = 0; i < 2; ++i)
             vx[i] = buf_load16<kPolicyDefault>(av_rd, r0 * FT::kRowBytes + 16 * (tid + i * kWideThreads));
-        }
     };
     auto store_rows = [&]() {
         *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qx;
+        *reinterpret_cast<uint4*>(Dh + QT::chunk_at(tid)) = hx;
+        *reinterpret_cast<uint4*>(Dl + QT::chunk_at(tid)) = lx;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            *reinterpret_cast<uint4*>(Dt + FT::chunk_at(tid + i * kWideThreads)) = dx[i];
-            *reinterpret_cast<uint4*>(Vt + FT::chunk_at(tid + i * kWideThreads)) = vx[i];
-        }
+        for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(Vt + FT::chunk_at(tid + i * kWideThreads)) = vx[i];
     };
     // dK and dV rows of the sub-chunk at r0 (rows past the tile, and all of
     // them before the first sub-chunk, fall outside the views).
@@ -1245,7 +1253,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
             for (int rr = 0; rr < 4; ++rr) {
                 const int row = 16 * bi + 4 * gq + rr;
                 qc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Qt + QT::at(row, 2 * (16 * w + lr))));
-                dc[bi][rr] = *reinterpret_cast<const float*>(Dt + FT::at(row, 4 * (16 * w + lr)));
+                dc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Dh + QT::at(row, 2 * (16 * w + lr)))) +
+                             to_f32(*reinterpret_cast<const bf16_t*>(Dl + QT::at(row, 2 * (16 * w + lr))));
             }
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
@@ -1456,17 +1465,17 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
     return hipGetLastError();
 }
 
-hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dQ,
-                                     float* dq32, float* apre, const float* fwd_records, float* bwd_records,
-                                     const Problem& p, int s0, hipStream_t stream) {
+hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dq_hi,
+                                     int ld_hi, void* dq_lo, float* apre, const float* fwd_records,
+                                     float* bwd_records, const Problem& p, int s0, hipStream_t stream) {
     if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || s0 % kWideS != 0 || s0 >= p.S ||
-        p.tile % kBC != 0)
+        p.tile % kBC != 0 || !dq_hi || !dq_lo || ld_hi < kWideS)
         return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     causal_bwd_dq_wide_kernel<<<grid, kWideThreads, WideGeo::kDqLds, stream>>>(
         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
-        static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dQ), dq32, apre, fwd_records, bwd_records, p.T,
-        p.tile, p.tiles, record_floats(kBS, kBS), p.S, s0, p.rec);
+        static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dq_hi), static_cast<bf16_t*>(dq_lo), apre, fwd_records,
+        bwd_records, p.T, p.tile, p.tiles, record_floats(kBS, kBS), p.S, ld_hi, s0, p.rec);
     return hipGetLastError();
 }
 
@@ -1474,7 +1483,7 @@ hipError_t launch_causal_bwd_dkv_wide(const void* q, const void* k, const void* 
                                       const Problem& p, const BwdWide& wb, hipStream_t stream) {
     if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || p.tile % kBC != 0 || wb.ldq != p.S)
         return hipErrorInvalidValue;
-    if (!wb.dq32 || !wb.apre) return hipErrorInvalidValue;
+    if (!wb.dq_hi || !wb.dq_lo || wb.ld_hi < kWideS || !wb.apre) return hipErrorInvalidValue;
     for (int g2 = 0; g2 < 2; ++g2)
         if (!wb.rec[g2][0] || !wb.rec[g2][1]) return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));

@@ -284,8 +284,9 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
     if (pl.wide2()) {
         // A pair of bucket groups: the suffix records of its four 64 x 64
-        // blocks, its running mass and dq32 (128 buckets); a dV running sum
-        // when there are several pairs.
+        // blocks, its running mass and dQ's bf16 remainders and bf16 part
+        // (128 buckets, 2 + 2 bytes); a dV running sum when there are several
+        // pairs.
         l.bwd = 4 * p.N * p.tiles * record_floats(64, 64);
         l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(128));
         l.dq32 = round64(NT * 128);
@@ -952,18 +953,27 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
             p4.N = 4 * p.N;
             const int64_t rec_n = p.N * p.tiles * pb.rec;
             const int pairs = pl.mblocks / 2;
+            // The dq32 region holds dQ's bf16 remainders [N T][128] and, when
+            // dQ is not asked for, its bf16 part after them.
+            bf16_t* dq_lo_ws = reinterpret_cast<bf16_t*>(dq32);
             for (int mp = 0; mp < pairs; ++mp) {
+                // dQ's bf16 part goes to the caller's dQ (or, not asked for,
+                // to the workspace after the remainders).
+                void* dq_hi = dQ ? col(dQ, 128 * mp, es) : static_cast<void*>(dq_lo_ws + NT * 128);
+                const int ld_hi = dQ ? p.S : 128;
                 RACE_TRY(launch_causal_bwd_dq_wide(static_cast<const char*>(probsQ) + 128 * mp * es,
                                                    static_cast<const char*>(probsK) + 128 * mp * es, V, dOut,
-                                                   col(dQ, 128 * mp, es), dq32, apre, fwd_rec, bwd_rec, p,
-                                                   128 * mp, stream));
+                                                   dq_hi, ld_hi, dq_lo_ws, apre, fwd_rec, bwd_rec, p, 128 * mp,
+                                                   stream));
                 RACE_TRY(marks->mark(stream));
                 if (!dK && !dV) continue;
                 RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p4, stream, /*reverse=*/true));
                 RACE_TRY(marks->mark(stream));
                 BwdWide wb;
                 wb.ldq = p.S;
-                wb.dq32 = dq32;
+                wb.dq_hi = dq_hi;
+                wb.ld_hi = ld_hi;
+                wb.dq_lo = dq_lo_ws;
                 wb.apre = apre;
                 for (int g2 = 0; g2 < 2; ++g2) {
                     wb.rec[g2][0] = bwd_rec + (2 * g2) * rec_n;

@@ -261,19 +261,23 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
                                       const float* suffix_records, void* dK, void* dV,
                                       const Problem& p, const BwdBlock& blk, hipStream_t stream);
 // The forward walk (B1) over a 128-bucket x 128-column block (bf16 tokens,
-// d = 128; buckets s0 .. s0 + 127, with q, k and dQ pointing at bucket s0 of
-// the full tensors and fwd_records the full problem's): dQ of those buckets
-// whole, dq32 [N T][128], the running mass
-// [N][tiles][tile / 32][128] and the suffix records of the block's four 64 x
-// 64 blocks, (group g2, value half h) at bwd_records + (2 g2 + h) N tiles rec.
-hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dQ,
-                                     float* dq32, float* apre, const float* fwd_records, float* bwd_records,
-                                     const Problem& p, int s0, hipStream_t stream);
+// d = 128; buckets s0 .. s0 + 127, with q and k pointing at bucket s0 of the
+// full tensors and fwd_records the full problem's): dQ of those buckets whole
+// as bf16 (dq_hi, rows of ld_hi: the caller's dQ at bucket s0, or workspace)
+// with the bf16 rounding of each remainder (dq_lo, rows of 128), which the
+// backward walk reads back as hi + lo; the running mass
+// [N][tiles][tile / 32][128]; the suffix records of the block's four 64 x 64
+// parts, (group g2, value half h) at bwd_records + (2 g2 + h) N tiles rec.
+hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dq_hi,
+                                     int ld_hi, void* dq_lo, float* apre, const float* fwd_records,
+                                     float* bwd_records, const Problem& p, int s0, hipStream_t stream);
 // The backward walk over the same block: the buffers its forward walk wrote
 // and dV's accumulation.
 struct BwdWide {
     int ldq = 0;                 // row stride of probsQ, probsK, dK (the full S)
-    const float* dq32 = nullptr; // fp32 dQ of the block, rows of 128
+    const void* dq_hi = nullptr; // dQ of the block as bf16, rows of ld_hi
+    int ld_hi = 0;
+    const void* dq_lo = nullptr; // the bf16 remainders, rows of 128
     const float* apre = nullptr; // running mass per sub-chunk, rows of 128
     const float* rec[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};  // scanned suffix records (g2, value half)
     float* acc_v = nullptr;  // dV's fp32 running sum (rows of 128), or null
