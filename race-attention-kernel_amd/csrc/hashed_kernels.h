@@ -27,6 +27,16 @@
 #include "causal_geo.h"
 #include "hash_stage.h"
 
+#ifndef RACE_HASHED_SUMS_ALLOC_EIGHTHS
+#define RACE_HASHED_SUMS_ALLOC_EIGHTHS 6
+#endif
+// Resident fp32 tile-sum workgroups per CU (S = d = 64, the lean layout):
+// the automatic 1024-token tiles start two per CU at cfg2, and the
+// end-to-start walk spills at the four-per-CU register bound.
+#ifndef RACE_HASHED_SUMS_F32_BLOCKS
+#define RACE_HASHED_SUMS_F32_BLOCKS 2
+#endif
+
 namespace race {
 namespace hashed {
 
@@ -55,6 +65,7 @@ struct RowStage {
     static_assert(C % kRows == 0, "whole blocks of rows");
     uint4 x[kPer][kRows];
 
+    template <int PP = P>
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int r0) {
         const int tid = threadIdx.x;
 #pragma unroll
@@ -64,7 +75,7 @@ struct RowStage {
             if (kBlk % NT == 0 || blk < kBlk) {
 #pragma unroll
                 for (int rr = 0; rr < kRows; ++rr)
-                    x[p][rr] = buf_load16<P>(r, ((r0 + kRows * a + rr) * Wd + b * E) * int(sizeof(TIn)));
+                    x[p][rr] = buf_load16<PP>(r, ((r0 + kRows * a + rr) * Wd + b * E) * int(sizeof(TIn)));
             }
         }
     }
@@ -174,6 +185,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
     constexpr int kUP = 16 * NPB + 1;
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr bool kUInK = sums_u_in_k<TIn, S, KP>();
+    // fp32 rows at S = d = 64 (the cfg2 module): the memory-side cache
+    // ordering of the probability-fed tile sums (mfma_direct.hip).
+    constexpr bool kEndFirst = std::is_same<TIn, float>::value && S == 64 && D == 64 && kDB;
     unsigned char* Ks = lds;
     unsigned char* Vs = Ks + G::kKBytes;
     unsigned char* Ue = Vs + G::kVBytes;                     // [C][kUP] (not kUInK)
@@ -221,16 +235,19 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
     RowStage<TIn, D, C, kSumsLoadPolicy, kThreads> vst;
     Projector<TIn, D, NPB> pjA;
     std::conditional_t<kDB, Projector<TIn, D, NPB>, Projector<TIn, D, NPB>&> pjB = pjA;
-    vst.load(vr, 0);
-    if (projects) pjA.template load<kSumsLoadPolicy>(kr, 16 * w, g, lr);
-    auto step = [&](int r0, const Projector<TIn, D, NPB>& cur, Projector<TIn, D, NPB>& nxt) {
+    using Stream = std::integral_constant<int, kSumsLoadPolicy>;
+    using Alloc = std::integral_constant<int, kPolicyDefault>;
+    // One sub-chunk at r0; the next one the walk takes (at rn, past either
+    // end of the tile: zeros, never used) is loaded with policy `pol`.
+    auto step = [&](auto pol, int r0, int rn, const Projector<TIn, D, NPB>& cur, Projector<TIn, D, NPB>& nxt) {
+        constexpr int PP = decltype(pol)::value;
         __syncthreads();  // the previous sub-chunk's tiles have been read
         vst.store(Vs);
-        vst.load(vr, r0 + C);  // prefetch (past the tile: zeros, never used)
+        vst.template load<PP>(vr, rn);
         if (projects) {
-            if constexpr (kDB) nxt.template load<kSumsLoadPolicy>(kr, r0 + C + 16 * w, g, lr);
+            if constexpr (kDB) nxt.template load<PP>(kr, rn + 16 * w, g, lr);
             hash_block<TIn, D, S, KP, C, false>(cur, wp, U, 16 * w, Ks, rows - r0, scale2, g, lr);
-            if constexpr (!kDB) nxt.template load<kSumsLoadPolicy>(kr, r0 + C + 16 * w, g, lr);
+            if constexpr (!kDB) nxt.template load<PP>(kr, rn + 16 * w, g, lr);
         }
         __syncthreads();
 #pragma unroll
@@ -258,9 +275,36 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void hashed_sums_kernel(
             }
         }
     };
-    for (int r0 = 0; r0 < rows; r0 += 2 * C) {
-        step(r0, pjA, pjB);
-        if (r0 + C < rows) step(r0 + C, pjB, pjA);
+    if constexpr (kEndFirst) {
+        // End to start, the streamed part first; the first
+        // RACE_HASHED_SUMS_ALLOC_EIGHTHS eighths of the tile (what the output
+        // pass reads first) with the cache-allocating policy, last.
+        const int last = ((rows - 1) / C) * C;
+        const int cut = C * int((int64_t(tile / C) * RACE_HASHED_SUMS_ALLOC_EIGHTHS + 7) / 8);
+        if (last < cut) {
+            vst.template load<Alloc::value>(vr, last);
+            if (projects) pjA.template load<Alloc::value>(kr, last + 16 * w, g, lr);
+        } else {
+            vst.template load<Stream::value>(vr, last);
+            if (projects) pjA.template load<Stream::value>(kr, last + 16 * w, g, lr);
+        }
+        int r0 = last;
+        for (; r0 - 2 * C >= cut; r0 -= 2 * C) {
+            step(Stream{}, r0, r0 - C, pjA, pjB);
+            step(Stream{}, r0 - C, r0 - 2 * C, pjB, pjA);
+        }
+        for (; r0 >= C; r0 -= 2 * C) {
+            step(Alloc{}, r0, r0 - C, pjA, pjB);
+            step(Alloc{}, r0 - C, r0 - 2 * C, pjB, pjA);
+        }
+        if (r0 >= 0) step(Alloc{}, r0, r0 - C, pjA, pjB);
+    } else {
+        vst.load(vr, 0);
+        if (projects) pjA.template load<kSumsLoadPolicy>(kr, 16 * w, g, lr);
+        for (int r0 = 0; r0 < rows; r0 += 2 * C) {
+            step(Stream{}, r0, r0 + C, pjA, pjB);
+            if (r0 + C < rows) step(Stream{}, r0 + C, r0 + 2 * C, pjB, pjA);
+        }
     }
 
     float* r = records + (n * tiles + ti) * rec;
@@ -316,6 +360,9 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
     constexpr int kJobs = 2 * NBI;  // (Q or K, 16-token block)
     constexpr int kJobsW = (kJobs + NW - 1) / NW;
     constexpr int kStoreP = std::is_same<TIn, float>::value ? kOutWgStorePolicyF32 : kOutStorePolicy;
+    // fp32 rows at S = d = 64: Q streams past the memory-side cache, which
+    // holds the K and V rows the tile sums left there.
+    constexpr int kQP = (std::is_same<TIn, float>::value && S == 64 && D == 64) ? kOutQPolicyF32 : kOutQPolicy;
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char* Ws = lds;
     unsigned char* Ks = Ws + G::kWBytes;
@@ -393,7 +440,7 @@ __global__ __launch_bounds__(64 * NW, kMinBlocks) void hashed_output_kernel(
             const int job = w + NW * j;
             if (job < kJobs) {
                 if (job < NBI)
-                    dst.j[j].template load<kOutQPolicy>(qr, r0 + 16 * job, g, lr);
+                    dst.j[j].template load<kQP>(qr, r0 + 16 * job, g, lr);
                 else
                     dst.j[j].template load<kOutKVPolicy>(kr, r0 + 16 * (job - NBI), g, lr);
             }
@@ -640,7 +687,8 @@ hipError_t launch_hashed_shape(const HashedArgs& a, const Problem& p, hipStream_
         constexpr bool kLean = std::is_same<TIn, float>::value;
         constexpr bool kFour = hashed_output_lds<TIn, 64, 64, 32, KP, 4, true, kLean>() <= kMaxLds / 4;
         if constexpr (kFour)
-            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false, kLean, 4, kLean>(a, p, stream, marks);
+            return launch_hashed_family<TIn, 64, 64, 32, KP, 4, 4, 64, false, kLean,
+                                        kLean ? RACE_HASHED_SUMS_F32_BLOCKS : 4, kLean>(a, p, stream, marks);
         else
             return launch_hashed_family<TIn, 64, 64, 32, KP, 3, 4, 64, true>(a, p, stream, marks);
     } else if constexpr (S == 256 && D == 128) {
