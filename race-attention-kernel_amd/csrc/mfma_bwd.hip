@@ -860,6 +860,13 @@ __global__ __launch_bounds__(kThreads, 2) void causal_bwd_dkv_mfma_kernel(
 // to the caller's dK; dV, a sum over the blocks of a problem, goes through
 // its fp32 running sum unless the block is the only one.
 constexpr int kWideS = 128, kWideD = 128, kWideWaves = 8, kWideThreads = 64 * kWideWaves;
+// Sub-chunks of operands the block forward walk keeps in flight in
+// registers.  Two measured slower at cfg5 (661-674 against 642-653 us per
+// walk, two alternating runs on one box, 256 VGPRs): the walk is not waiting
+// on its loads.
+#ifndef RACE_BWD_WIDE_DQ_DEPTH
+#define RACE_BWD_WIDE_DQ_DEPTH 1
+#endif
 
 struct WideGeo {
     using PR = Plane<false, 128>;  // rows = tokens (or buckets), k = buckets or value columns
@@ -942,19 +949,22 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const bf16_t* ssrc = tensor == 0 ? k + base * ldq : tensor == 1 ? v + base * kWideD : g + base * kWideD;
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
     unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
-    StageBlock<bf16_t> st;
+    // Sub-chunks of operands in flight in registers ahead of the one in LDS.
+    constexpr int kDepth = RACE_BWD_WIDE_DQ_DEPTH;
+    StageBlock<bf16_t> st[kDepth];
     // Q's rows: chunk tid of the sub-chunk (row tid / 16, 8 buckets) in
     // from global memory, then read in the accumulator layout.
     static_assert(QT::kChunks * kBC == kWideThreads, "one Q chunk per thread");
-    uint4 qx;
-    auto load_q = [&](int r0) {
-        qx = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
+    uint4 qx[kDepth];
+    auto load_q = [&](uint4& x, int r0) {
+        x = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
     };
 
     const int subs = tile / kBC;
     float* ap = apre + (n * tiles + ti) * int64_t(subs) * kWideS;
-    // The previous sub-chunk's dQ tile: whole rows of its fp32 copy, and dQ
-    // as bf16 (16-byte chunk c of a row holds elements 4 c .. 4 c + 3).
+    // The previous sub-chunk's dQ tile as whole rows: dQ as bf16 and the
+    // bf16 remainders (16-byte chunk c of a tile row holds elements 4 c ..
+    // 4 c + 3).
     constexpr int kChunksPerRow = T32::kChunks;
     auto flush = [&](int r0) {
         typename T32::template Chunks<kWideThreads> c32;
@@ -971,19 +981,22 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
             __builtin_amdgcn_raw_buffer_store_b64(lo, lor, (row * kWideS + c4) * 2, 0, kPolicyDefault);
         }
     };
-    st.load(srs, 0, sa, sb, sld);
-    load_q(0);
-    int r0 = 0;
-    for (; r0 < rows; r0 += kBC) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        st[d].load(srs, d * kBC, sa, sb, sld);
+        load_q(qx[d], d * kBC);
+    }
+    auto sub_chunk = [&](StageBlock<bf16_t>& stg, uint4& qv, int r0) {
         __syncthreads();
-        if (tensor < 3) st.store_r<PR>(splane, sa, sb);
-        *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qx;
-        st.load(srs, r0 + kBC, sa, sb, sld);  // past the tile: zeros, never used
-        load_q(r0 + kBC);
+        if (tensor < 3) stg.store_r<PR>(splane, sa, sb);
+        *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qv;
+        stg.load(srs, r0 + kDepth * kBC, sa, sb, sld);  // past the tile: zeros, never used
+        load_q(qv, r0 + kDepth * kBC);
         // Unconditional: at r0 = 0 the offsets are negative, outside the
-        // buffer ranges, and the stores are dropped.
+        // buffer ranges, and the stores are dropped; a sub-chunk past a
+        // ragged tile end reads zeros and stores nothing.
         flush(r0 - kBC);
-        if (gq == 0) ap[(r0 / kBC) * kWideS + s] = a0;
+        if (gq == 0 && r0 < rows) ap[(r0 / kBC) * kWideS + s] = a0;
         __syncthreads();
 
         // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
@@ -1074,6 +1087,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
             PR::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
             b0t[cb] = mfma16(vh, kh, b0t[cb]);
         }
+    };
+    int r0 = 0;
+    for (; r0 < rows; r0 += kDepth * kBC) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) sub_chunk(st[d], qx[d], r0 + d * kBC);
     }
     __syncthreads();
     if (r0 > 0) flush(r0 - kBC);
