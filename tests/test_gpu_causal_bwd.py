@@ -124,6 +124,31 @@ def test_tile_lengths(race, oracle, cuda, tile):
     check_grads(oracle, q, k, v, g, out, dq, dk, dv, FP32_TOL)
 
 
+@pytest.mark.parametrize("L, R", [(4, 32), (8, 32)])
+@pytest.mark.parametrize("tile", [64, 256, 1024])
+def test_block_walks_at_explicit_tiles(race, oracle, cuda, L, R, tile):
+    # bf16, d = 128, S = 128 and 256: the walks over 128 x 128 blocks with
+    # many tiles per stream (the reverse scan of the block's four record
+    # arrays crosses them) and a ragged last tile and sub-chunk.
+    say("c-bwd block tile", L, R, tile)
+    q, k, v, g = (x.to(cuda) for x in race.make_inputs(2, 1500, L, R, 128, seed=26, dtype=torch.bfloat16,
+                                                         grad_out=True))
+    dq, dk, dv = race.race_causal_backward(q, k, v, g, tile_tokens=tile)
+    out = race.race_fused_fwd(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol_for(torch.bfloat16))
+
+
+def test_block_walks_bitwise_reproducible(race, cuda):
+    say("c-bwd block bitwise")
+    q, k, v, g = race.make_inputs(3, 2100, 8, 32, 128, seed=27, dtype=torch.bfloat16, grad_out=True)
+    first = forward_backward(race, q, k, v, g, cuda)
+    for _ in range(2):
+        again = forward_backward(race, q, k, v, g, cuda)
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])
 @pytest.mark.parametrize("T", [1, 31, 33, 100, 2000])
