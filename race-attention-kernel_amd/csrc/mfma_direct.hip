@@ -29,7 +29,8 @@ constexpr int kDirC = 32;  // tokens per sub-chunk
 // would have left the memory-side cache by then.  Measured at cfg2 (20 steps
 // after the settling phase, one box): 6/8 3795 M tokens/s, 8/8 3688, 4/8 3745,
 // 2/8 3705 with the same inputs every step; 3476, 3465, 3478, 3442 with two
-// input sets alternating.
+// input sets alternating.  On another box, three alternating runs each: 6/8
+// 3810-3843, 5/8 3763-3791, 7/8 3742-3770.
 #ifndef RACE_SUMS_F32_ALLOC_EIGHTHS
 #define RACE_SUMS_F32_ALLOC_EIGHTHS 6
 #endif
