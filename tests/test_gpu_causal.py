@@ -267,6 +267,30 @@ def test_cfg5_bf16_large_buckets(race, oracle, cuda):
     assert_bf16_floor(o, ref, float(np.abs(vn).max()), "cfg5")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [150, 200, 1000])
+def test_s256_many_streams_ragged_tiles(race, oracle, cuda, dtype, T):
+    # S = 256, d = 128 with 256 streams and 64-token tiles: odd and even tile
+    # counts per stream, ragged last tiles, a grid of one to four rounds.
+    # Eight streams spread over the batch against the oracle, and the final
+    # state.
+    say("s256 many streams", T, dtype)
+    q, k, v = race.make_inputs(256, T, 8, 32, 128, seed=31 + T, dtype=dtype, device=cuda, gen_device="cuda")
+    out, state = race.race_fused_fwd_with_state(q, k, v, causal=True, tile_tokens=64)
+    torch.cuda.synchronize()
+    pick = [0, 37, 74, 111, 148, 185, 222, 255]
+    qn, kn, vn = (to_np(x[pick]) for x in (q, k, v))
+    ref = oracle.causal_recurrence(qn, kn, vn, nthreads=16)
+    assert per_stream_rel_err(to_np(out[pick]), ref) <= tol_for(dtype)
+    # The state after the last token: B = K^T V, A = colsum K over the stream.
+    kd, vd = kn.astype(np.float64), vn.astype(np.float64)
+    b = np.einsum("nts,ntc->nsc", kd, vd)
+    a = kd.sum(1)
+    st = to_np(state[pick]).astype(np.float64)
+    assert np.abs(st[:, :256 * 128] - b.reshape(len(pick), -1)).max() <= 1e-4 * np.abs(b).max()
+    assert np.abs(st[:, 256 * 128:] - a).max() <= 1e-4 * np.abs(a).max()
+
+
 def test_final_state_is_the_decode_handoff(race, oracle, cuda):
     say("final-state")
     q, k, v = race.make_inputs(2, 3333, 4, 16, 64, seed=21)
