@@ -925,7 +925,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     // bf16 rounding of its remainder (lo, rows of 128): hi + lo is dQ to
     // about 2^-17, which the backward walk reads back.
     const __amdgpu_buffer_rsrc_t hir = make_rsrc(dq_hi + base * ld_hi, int64_t(rows) * ld_hi * 2);
-    const __amdgpu_buffer_rsrc_t lor = make_rsrc(dq_lo + base * kWideS, int64_t(rows) * kWideS * 2);
+    // No remainders when no backward walk reads them (dq_lo null: an empty
+    // view drops the stores).
+    const __amdgpu_buffer_rsrc_t lor =
+        make_rsrc(dq_lo ? dq_lo + base * kWideS : nullptr, dq_lo ? int64_t(rows) * kWideS * 2 : 0);
 
     // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][s].
     const float* fr = fwd_records + (n * tiles + ti) * fwd_rec;
@@ -1487,7 +1490,7 @@ hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v
                                      int ld_hi, void* dq_lo, float* apre, const float* fwd_records,
                                      float* bwd_records, const Problem& p, int s0, hipStream_t stream) {
     if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || s0 % kWideS != 0 || s0 >= p.S ||
-        p.tile % kBC != 0 || !dq_hi || !dq_lo || ld_hi < kWideS)
+        p.tile % kBC != 0 || !dq_hi || ld_hi < kWideS)
         return hipErrorInvalidValue;
     const dim3 grid(unsigned(p.tiles), unsigned(p.N));
     causal_bwd_dq_wide_kernel<<<grid, kWideThreads, WideGeo::kDqLds, stream>>>(

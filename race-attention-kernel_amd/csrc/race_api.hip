@@ -963,7 +963,8 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
                 const int ld_hi = dQ ? p.S : 128;
                 RACE_TRY(launch_causal_bwd_dq_wide(static_cast<const char*>(probsQ) + 128 * mp * es,
                                                    static_cast<const char*>(probsK) + 128 * mp * es, V, dOut,
-                                                   dq_hi, ld_hi, dq_lo_ws, apre, fwd_rec, bwd_rec, p, 128 * mp,
+                                                   dq_hi, ld_hi, dK || dV ? dq_lo_ws : nullptr, apre, fwd_rec,
+                                                   bwd_rec, p, 128 * mp,
                                                    stream));
                 RACE_TRY(marks->mark(stream));
                 if (!dK && !dV) continue;

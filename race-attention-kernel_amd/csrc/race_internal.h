@@ -264,8 +264,8 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
 // d = 128; buckets s0 .. s0 + 127, with q and k pointing at bucket s0 of the
 // full tensors and fwd_records the full problem's): dQ of those buckets whole
 // as bf16 (dq_hi, rows of ld_hi: the caller's dQ at bucket s0, or workspace)
-// with the bf16 rounding of each remainder (dq_lo, rows of 128), which the
-// backward walk reads back as hi + lo; the running mass
+// with the bf16 rounding of each remainder (dq_lo, rows of 128; null when no
+// backward walk follows), which the backward walk reads back as hi + lo; the running mass
 // [N][tiles][tile / 32][128]; the suffix records of the block's four 64 x 64
 // parts, (group g2, value half h) at bwd_records + (2 g2 + h) N tiles rec.
 hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dq_hi,
