@@ -52,6 +52,16 @@ constexpr int kBS = 64;  // buckets (S) and value columns (d)
 // Resident B1 workgroups per CU: two since dQ is staged through LDS (three
 // spill registers there; measured 139 against 170 us at cfg2).
 constexpr int kDqBlocks = RACE_BWD_DQ_BLOCKS;
+// B1 takes Q's rows of a sub-chunk as whole 16-byte rows into an LDS tile
+// (read in the accumulator layout there) rather than 4 (fp32) or 2 (bf16)
+// bytes per lane and row straight from global memory: 132 -> 130 us at cfg2,
+// 1535 -> 1520 us at the cfg3 shape.  The same in B3 measured no faster at
+// cfg2 and 1.5% slower at the cfg3 shape (the Q tile on top of 66 KB of LDS).
+
+#ifndef RACE_BWD_STAGE_Q
+#define RACE_BWD_STAGE_Q 1
+#endif
+constexpr bool kStageQ = RACE_BWD_STAGE_Q != 0;
 
 template <typename TIn>
 struct BwdGeo {
@@ -75,8 +85,12 @@ struct BwdGeo {
     using PV = Plane<kSplit, DV>;
     template <int DV>
     static constexpr int kVBytes = kBC * PV<DV>::kPitch;
+    // ... and, staged, Q's rows of the sub-chunk (whole 16-byte rows in,
+    // read in the accumulator layout).
+    using QT = OutTile<TIn, kBS, kBC>;
+    static constexpr int kQTBytes = kBC * QT::kRowBytes;
     template <int DV>
-    static constexpr int kDqLdsV = kRBytes + 2 * kVBytes<DV> + kMBytes + kT32Bytes;
+    static constexpr int kDqLdsV = kRBytes + 2 * kVBytes<DV> + kMBytes + kT32Bytes + (kStageQ ? kQTBytes : 0);
     template <int DV>
     static constexpr int kBlkV = (kBC / 4) * (DV / E);
     static constexpr int kDkvLds = 3 * kRBytes + kWTBytes + 2 * kMBytes + kZBytes;
@@ -169,7 +183,9 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
     unsigned char* Gs = Vs + G::template kVBytes<DV>;
     unsigned char* Ms = Gs + G::template kVBytes<DV>;
     unsigned char* D32s = Ms + G::kMBytes;
+    unsigned char* Qt = D32s + G::kT32Bytes;  // Q rows (kStageQ)
     using T32 = OutTile<float, kBS, kBC>;
+    using QT = typename G::QT;
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -252,14 +268,28 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
                 st[s].template store_r<PV>(tensor == 1 ? Vs : Gs, blk / (DV / G::E), blk % (DV / G::E));
         }
     };
-    // Q at this lane's (i, s) positions.
+    // Q at this lane's (i, s) positions, or (kStageQ) the sub-chunk's rows
+    // as 16-byte chunks: chunk c = tid + i kThreads is row c / QT::kChunks.
+    constexpr int kQC = kBC * QT::kChunks;
+    constexpr int kQPer = (kQC + kThreads - 1) / kThreads;
+    static_assert(kQC % kThreads == 0, "whole chunks per thread");
     float qreg[2][4];
+    uint4 qx[kQPer];
     auto load_q = [&](int r0) {
+        if constexpr (kStageQ) {
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
+            for (int i = 0; i < kQPer; ++i) {
+                const int c = tid + i * kThreads;
+                qx[i] = buf_load16<kPolicyDefault>(
+                    qr, ((r0 + c / QT::kChunks) * ldq + (c % QT::kChunks) * G::E) * int(sizeof(TIn)));
+            }
+        } else {
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                qreg[bi][rr] = load1<TIn>(qr, (r0 + 16 * bi + 4 * gq + rr) * ldq + 16 * w + lr);
+            for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    qreg[bi][rr] = load1<TIn>(qr, (r0 + 16 * bi + 4 * gq + rr) * ldq + 16 * w + lr);
+        }
     };
 
     const int subs = tile / kBC;
@@ -330,10 +360,15 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         __syncthreads();
         stage_store();
         float qc[2][4];
+        if constexpr (kStageQ) {
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
+            for (int i = 0; i < kQPer; ++i) *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid + i * kThreads)) = qx[i];
+        } else {
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
+            for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = qreg[bi][rr];
+        }
         stage_load(r0 + kBC);  // past the tile: zeros, never used
         load_q(r0 + kBC);
         if constexpr (kSums) {
@@ -352,6 +387,18 @@ __global__ __launch_bounds__(kThreads, kDqBlocks) void causal_bwd_dq_mfma_kernel
         __syncthreads();
 
         // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
+        if constexpr (kStageQ) {
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const unsigned char* qp = Qt + QT::at(16 * bi + 4 * gq + rr, (16 * w + lr) * int(sizeof(TIn)));
+                    if constexpr (std::is_same<TIn, float>::value)
+                        qc[bi][rr] = *reinterpret_cast<const float*>(qp);
+                    else
+                        qc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(qp));
+                }
+        }
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         f32x4 ab[2];
