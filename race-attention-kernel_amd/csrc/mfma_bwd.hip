@@ -57,7 +57,6 @@ constexpr int kDqBlocks = RACE_BWD_DQ_BLOCKS;
 // bytes per lane and row straight from global memory: 132 -> 130 us at cfg2,
 // 1535 -> 1520 us at the cfg3 shape.  The same in B3 measured no faster at
 // cfg2 and 1.5% slower at the cfg3 shape (the Q tile on top of 66 KB of LDS).
-
 #ifndef RACE_BWD_STAGE_Q
 #define RACE_BWD_STAGE_Q 1
 #endif
