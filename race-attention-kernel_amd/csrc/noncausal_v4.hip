@@ -610,6 +610,12 @@ __global__ __launch_bounds__(kThreads) void map64_kernel(
 constexpr int kGradStage = 64;
 constexpr int kFoldParts = kKeyGradFoldParts;
 constexpr int kGradBlocks = 3;  // workgroups per CU the two passes are built for (LDS allows 3)
+// Rows of dB a key-side thread forms per round of record loads (16 in all;
+// 8 per round measured the same as 4 at cfg4, 16 spills).
+#ifndef RACE_KEY_GRAD_ROWS
+#define RACE_KEY_GRAD_ROWS 4
+#endif
+constexpr int kKeyGradRows = RACE_KEY_GRAD_ROWS;
 
 // The slot of a stage row (16-byte slots XORed by row & 3).
 __device__ __forceinline__ int row_slot(int i, int j) { return j ^ (i & 3); }
@@ -839,13 +845,13 @@ __global__ __launch_bounds__(kThreads, kGradBlocks) void key_grad64_kernel(
         } else {
             const float* sn = state + n * (W * W + W);
             const float* rn = dE_records + n * int64_t(parts) * rec;
-            // Four rows at a time: every part, B and A value requested before
-            // the sums.
+            // RACE_KEY_GRAD_ROWS rows at a time: every part, B and A value
+            // requested before the sums.
 #pragma unroll
-            for (int mb = 0; mb < 16; mb += 4) {
-                float gp[kFoldParts][4], b[4], a[4];
+            for (int mb = 0; mb < 16; mb += kKeyGradRows) {
+                float gp[kFoldParts][kKeyGradRows], b[kKeyGradRows], a[kKeyGradRows];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
+                for (int m = 0; m < kKeyGradRows; ++m) {
                     const int s = s0 + 4 * (mb + m);
 #pragma unroll
                     for (int p = 0; p < kFoldParts; ++p)
@@ -854,7 +860,7 @@ __global__ __launch_bounds__(kThreads, kGradBlocks) void key_grad64_kernel(
                     a[m] = sn[W * W + s];
                 }
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
+                for (int m = 0; m < kKeyGradRows; ++m) {
                     const int s = s0 + 4 * (mb + m);
                     float gs = 0.f;
 #pragma unroll
@@ -872,75 +878,84 @@ __global__ __launch_bounds__(kThreads, kGradBlocks) void key_grad64_kernel(
         }
     }
 
-    const int tt = tid >> 4, cc = tid & 15;
+    // Waves 0-1 form dK and waves 2-3 dV, each thread an 8 x 4 register tile:
+    // tokens tt + 8 r (r < 8) and columns 4 cc .. 4 cc + 3, the contraction in
+    // order (so the gradients are those of one thread per 4 x 4 tile doing
+    // both maps).  Per 128 FMAs a thread reads 4 dB vectors (one per lane
+    // and instruction) and 8 token vectors (4 rows per wave: broadcast), half
+    // the dB traffic of 4 x 4 tiles, which held the passes at the LDS rate.
+    const int half = __builtin_amdgcn_readfirstlane(tid >> 7);
+    const int tt = (tid & 127) >> 4, cc = tid & 15;
     for (int r0 = 0; r0 < rows; r0 += ST) {
         __syncthreads();
         st.template stash<true>(ks, vs);
         __syncthreads();
         if (r0 + ST < rows) st.fetch(kr, vr, r0 + ST);
-        // dK[t][4 cc + i] = dA + sum_c V[t][c] dB[4 cc + i][c], c in order.
-        float ok[4][4];
+        float o[8][4];
+        if (half == 0) {
+            // dK[t][4 cc + i] = dA + sum_c V[t][c] dB[4 cc + i][c].
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float bias = dAs[4 * cc + i];
+            for (int i = 0; i < 4; ++i) {
+                const float bias = dAs[4 * cc + i];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ok[r][i] = bias;
-        }
+                for (int r = 0; r < 8; ++r) o[r][i] = bias;
+            }
 #pragma unroll 2
-        for (int j = 0; j < W / 4; ++j) {
-            float4 xv[4], bv[4];
+            for (int j = 0; j < W / 4; ++j) {
+                float4 xv[8], bv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                xv[r] = *reinterpret_cast<const float4*>(vs + (tt + 16 * r) * W + 4 * row_slot(tt, j));
+                for (int r = 0; r < 8; ++r)
+                    xv[r] = *reinterpret_cast<const float4*>(vs + (tt + 8 * r) * W + 4 * row_slot(tt, j));
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                bv[i] = *reinterpret_cast<const float4*>(dBs + (4 * cc + i) * W + 4 * (j ^ cc));
+                for (int i = 0; i < 4; ++i)
+                    bv[i] = *reinterpret_cast<const float4*>(dBs + (4 * cc + i) * W + 4 * (j ^ cc));
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
+                for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float x = kk == 0 ? xv[r].x : kk == 1 ? xv[r].y : kk == 2 ? xv[r].z : xv[r].w;
+                    for (int r = 0; r < 8; ++r) {
+                        const float x = kk == 0 ? xv[r].x : kk == 1 ? xv[r].y : kk == 2 ? xv[r].z : xv[r].w;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float b = kk == 0 ? bv[i].x : kk == 1 ? bv[i].y : kk == 2 ? bv[i].z : bv[i].w;
-                        ok[r][i] = fmaf(x, b, ok[r][i]);
+                        for (int i = 0; i < 4; ++i) {
+                            const float b = kk == 0 ? bv[i].x : kk == 1 ? bv[i].y : kk == 2 ? bv[i].z : bv[i].w;
+                            o[r][i] = fmaf(x, b, o[r][i]);
+                        }
+                    }
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                buf_store4<TIn>(dkr, ((r0 + tt + 8 * r) * W + 4 * cc) * int(es),
+                                make_float4(o[r][0], o[r][1], o[r][2], o[r][3]));
+        } else {
+            // dV[t][4 cc + c] = sum_s K[t][s] dB[s][4 cc + c].
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) o[r][c] = 0.f;
+#pragma unroll 2
+            for (int j = 0; j < W / 4; ++j) {
+                float4 xv[8], bv[4];
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    xv[r] = *reinterpret_cast<const float4*>(ks + (tt + 8 * r) * W + 4 * row_slot(tt, j));
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    bv[kk] = *reinterpret_cast<const float4*>(dBs + (4 * j + kk) * W + 4 * (cc ^ j));
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const float bc[4] = {bv[kk].x, bv[kk].y, bv[kk].z, bv[kk].w};
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        const float x = kk == 0 ? xv[r].x : kk == 1 ? xv[r].y : kk == 2 ? xv[r].z : xv[r].w;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) o[r][c] = fmaf(x, bc[c], o[r][c]);
                     }
                 }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            buf_store4<TIn>(dkr, ((r0 + tt + 16 * r) * W + 4 * cc) * int(es),
-                            make_float4(ok[r][0], ok[r][1], ok[r][2], ok[r][3]));
-        // dV[t][4 cc + c] = sum_s K[t][s] dB[s][4 cc + c], s in order.
-        float ov[4][4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) ov[r][c] = 0.f;
-#pragma unroll 2
-        for (int j = 0; j < W / 4; ++j) {
-            float4 xv[4], bv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                xv[r] = *reinterpret_cast<const float4*>(ks + (tt + 16 * r) * W + 4 * row_slot(tt, j));
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                bv[kk] = *reinterpret_cast<const float4*>(dBs + (4 * j + kk) * W + 4 * (cc ^ j));
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const float bc[4] = {bv[kk].x, bv[kk].y, bv[kk].z, bv[kk].w};
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float x = kk == 0 ? xv[r].x : kk == 1 ? xv[r].y : kk == 2 ? xv[r].z : xv[r].w;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) ov[r][c] = fmaf(x, bc[c], ov[r][c]);
-                }
             }
-        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            buf_store4<TIn>(dvr, ((r0 + tt + 16 * r) * W + 4 * cc) * int(es),
-                            make_float4(ov[r][0], ov[r][1], ov[r][2], ov[r][3]));
+            for (int r = 0; r < 8; ++r)
+                buf_store4<TIn>(dvr, ((r0 + tt + 8 * r) * W + 4 * cc) * int(es),
+                                make_float4(o[r][0], o[r][1], o[r][2], o[r][3]));
+        }
     }
 }
 
