@@ -21,7 +21,11 @@
 // group h summed over m.  The kernels take one block through BwdBlock: row
 // strides of the full tensors and where the block's state sits in the full
 // forward records; race_api.hip runs the blocks in a fixed order and the
-// kernels add each block's part to fp32 running sums (BwdBlock).
+// kernels add each block's part to fp32 running sums (BwdBlock).  For bf16
+// tokens with d = 128 and S = 128 or 256 the walks instead take 128-bucket x
+// 128-column blocks with eight waves (causal_bwd_dq_wide_kernel,
+// causal_bwd_dkv_wide_kernel): dQ and dK of a block whole, dV summed over the
+// blocks.
 //
 // Layout.  Workgroups are 4 wave64s; wave w owns bucket block w
 // (s = 16 w .. 16 w + 15).  Products use v_mfma_f32_16x16x32_bf16 with the

@@ -234,7 +234,8 @@ int causal_bwd_groups(int S, int d, int lds_limit, int* C) {
 }
 
 // How a causal backward runs: on the matrix cores in 64 x 64 blocks (bucket
-// group x value group; one block at S = d = 64), or on the vector ALU in
+// group x value group; one block at S = d = 64; with bf16 tokens, d = 128 and
+// S = 128 or 256, walks over 128 x 128 blocks), or on the vector ALU in
 // column groups (0 groups: refused).  Planned for gfx950's LDS per
 // workgroup, so the workspace query needs no device.
 struct CausalBwdPlan {
