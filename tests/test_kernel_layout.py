@@ -1031,3 +1031,133 @@ def test_wide_walk_record_arrays_do_not_overlap(N, tiles):
     for h in range(2):
         for n in range(N):
             assert (h * N + n) * tiles * rec == (h * N * tiles + n * tiles) * rec
+
+
+# ---------------------------------------------------------------------------
+# mfma_bwd.hip: the block walks over 128 buckets x 128 value columns (bf16
+# tokens, eight waves, 512 threads): causal_bwd_dq_wide_kernel and
+# causal_bwd_dkv_wide_kernel.
+
+WIDE_THREADS, WIDE_S, WIDE_D, WIDE_C = 512, 128, 128, 32
+
+
+def wide_stage_blocks():
+    """Staging of K, V, G: thread tid takes tensor tid / kBlk (kBlk = (32 / 4)
+    (128 / 8) = 128 blocks per tensor) and block (sa, sb) = ((tid % 128) /
+    16, tid % 16): rows 4 sa .. 4 sa + 3, columns 8 sb .. 8 sb + 7 (one
+    16-byte bf16 load per row); threads 384..511 (tensor 3) stage nothing."""
+    kblk = (WIDE_C // 4) * (128 // 8)
+    cover = {t: Counter() for t in range(3)}
+    for tid in range(WIDE_THREADS):
+        tensor = tid // kblk
+        if tensor >= 3:
+            continue
+        sa, sb = (tid % kblk) // 16, tid % 16
+        for rr in range(4):
+            for e in range(8):
+                cover[tensor][(4 * sa + rr, 8 * sb + e)] += 1
+    return kblk, cover
+
+
+def test_wide_staging_covers_each_tile_once_one_tensor_per_wave():
+    kblk, cover = wide_stage_blocks()
+    assert kblk % 64 == 0  # a wave's 64 threads share one tensor
+    for t in range(3):
+        assert set(cover[t].values()) == {1}
+        assert set(cover[t]) == {(r, c) for r in range(WIDE_C) for c in range(128)}
+
+
+def test_wide_row_chunks_cover_the_sub_chunk_once():
+    # Q, dQ's bf16 part and remainders (bf16 rows of 128: 16 chunks) take
+    # chunk tid; the dV sum and the dV tile (fp32 rows of 128: 32 chunks)
+    # chunks tid and tid + 512.  Chunk c is row c / chunks, elements
+    # (c % chunks) * (16 / es) ...
+    for es, per in ((2, 1), (4, 2)):
+        chunks = WIDE_S * es // 16
+        seen = Counter()
+        for tid in range(WIDE_THREADS):
+            for i in range(per):
+                c = tid + i * WIDE_THREADS
+                row, first = c // chunks, (c % chunks) * (16 // es)
+                for e in range(16 // es):
+                    seen[(row, first + e)] += 1
+        assert set(seen.values()) == {1}
+        assert set(seen) == {(r, k) for r in range(WIDE_C) for k in range(WIDE_S)}
+
+
+def test_wide_records_map_every_block_entry_once():
+    # causal_bwd_dkv_wide_kernel: wave w (group g2 = w >> 2, bucket sl = 16
+    # (w & 3) + lr inside the group) loads zt[cb][rr] from record (g2, cb >> 2)
+    # at sl * 64 + 16 (cb & 3) + 4 gq + rr; causal_bwd_dq_wide_kernel stores
+    # its suffix totals to the same places.  Every entry of the four 64 x 64
+    # records once; the lane's (bucket, column) in the block is (16 w + lr,
+    # 16 cb + 4 gq + rr).
+    seen = Counter()
+    block = Counter()
+    for w in range(8):
+        g2 = w >> 2
+        for lane in range(64):
+            gq, lr = lane >> 4, lane & 15
+            sl = 16 * (w & 3) + lr
+            for cb in range(8):
+                for rr in range(4):
+                    seen[(g2, cb >> 2, sl * 64 + 16 * (cb & 3) + 4 * gq + rr)] += 1
+                    block[(16 * w + lr, 16 * cb + 4 * gq + rr)] += 1
+                    # The record entry is bucket 64 g2 + sl, column 64 (cb >> 2) + ..
+                    assert 64 * g2 + sl == 16 * w + lr
+    assert set(seen.values()) == {1} and len(seen) == 4 * 64 * 64
+    assert set(block.values()) == {1} and len(block) == WIDE_S * WIDE_D
+
+
+def wide_backward_flushes(rows: int):
+    """causal_bwd_dkv_wide_kernel: the walk runs r0 = last, last - 32, ..., 0
+    (last = ((rows - 1) / 32) 32); each sub-chunk first flushes the dK / dV
+    tile of r0 + 32 (the one before in walk order) and a final flush writes
+    r0 = 0.  Tile rows of 128 values: dK bf16 chunk c at ((r0 + c / 16) ld
+    + 8 (c % 16)) 2 with ld = 256 (the full S), dV fp32 chunk c at (r0 128 +
+    4 c) 4; the views cover the tile's rows."""
+    ld = 256
+    rng_k, rng_v = rows * ld * 2, rows * WIDE_D * 4
+    wk, wv = Counter(), Counter()
+
+    def flush(r0):
+        for c in range(WIDE_C * 16):
+            off = ((r0 + c // 16) * ld + 8 * (c % 16)) * 2
+            if buffer_store_kept(off, 16, rng_k):
+                wk[(off // 2) // ld] += 1
+        for c in range(WIDE_C * 32):
+            off = (r0 * WIDE_D + 4 * c) * 4
+            if buffer_store_kept(off, 16, rng_v):
+                wv[(off // 4) // WIDE_D] += 1
+
+    last = ((rows - 1) // WIDE_C) * WIDE_C
+    r0 = last
+    while r0 >= 0:
+        flush(r0 + WIDE_C)
+        r0 -= WIDE_C
+    flush(0)
+    return wk, wv
+
+
+@pytest.mark.parametrize("rows", [1, 31, 32, 33, 100, 4096])
+def test_wide_backward_walk_flushes_each_row_once(rows):
+    wk, wv = wide_backward_flushes(rows)
+    assert sorted(wk) == list(range(rows)) and set(wk.values()) == {16}
+    assert sorted(wv) == list(range(rows)) and set(wv.values()) == {32}
+
+
+def test_wide_backward_walk_without_the_final_flush_loses_the_first_rows():
+    # Planted mistake: the flush after the loop writes the walk's last
+    # sub-chunk (rows 0..31); leaving it out loses them.
+    rows = 100
+    ld = 256
+    rng = rows * ld * 2
+    written = set()
+    r0 = ((rows - 1) // WIDE_C) * WIDE_C
+    while r0 >= 0:
+        for c in range(WIDE_C * 16):
+            off = ((r0 + WIDE_C + c // 16) * ld + 8 * (c % 16)) * 2
+            if buffer_store_kept(off, 16, rng):
+                written.add((off // 2) // ld)
+        r0 -= WIDE_C
+    assert not written & set(range(WIDE_C))
