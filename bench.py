@@ -106,16 +106,15 @@ BWD_PHASES = {
 def causal_bwd_phases(S: int, d: int, es: int) -> list:
     """The causal backward's launches as race_api.hip issues them (starting
     from the inputs): one 64 x 64 block at S = d = 64; with bf16 tokens, d =
-    128 and S = 128 or 256, a forward walk, a reverse scan and a backward walk
-    per 128-bucket block (pair of 64-bucket groups); other shapes get generic
+    128 and S = 128 or 256, the forward walks of every 128-bucket block
+    (pair of 64-bucket groups) in one launch, one reverse scan of all their
+    records, then a backward walk per block; other shapes get generic
     names."""
     if S == 64 and d == 64:
         return BWD_PHASES[True]
     if es == 2 and d == 128 and S in (128, 256):
-        names = ["bwd_tile_sums", "tile_scan"]
-        for mp in range(S // 128):
-            names += [f"bwd_dq_pair{mp}", f"suffix_scan_pair{mp}", f"bwd_dkv_pair{mp}"]
-        return names
+        names = ["bwd_tile_sums", "tile_scan", "bwd_dq_walks", "suffix_scan_blocks"]
+        return names + [f"bwd_dkv_pair{mp}" for mp in range(S // 128)]
     return []
 
 
@@ -261,15 +260,16 @@ def phase_bytes(name: str, cfg, T: int, es: int, tiles: int, rec: int) -> float:
     S, d = cfg.S, cfg.d
     state = 4.0 * cfg.N * tiles * rec
     small = 4.0 * cfg.N * (S * d + S) * 3
-    # Backward walks over a 128-bucket block: that block's Q, K (and dQ, dK)
-    # columns, every value column; the reverse scan of its four 64 x 64
-    # record arrays.
-    if name.startswith("bwd_dq_pair"):
-        return es * (3 * 128 + 2 * d) * NT
+    # Walks over 128-bucket blocks: the forward walks of every block (each
+    # block's Q, K and dQ columns, every value column once), a backward walk
+    # per block (its Q, K, dK columns, every value column, dV); the reverse
+    # scan of four 64 x 64 record arrays per block.
+    if name == "bwd_dq_walks":
+        return es * (3 * S + 2 * d) * NT
     if name.startswith("bwd_dkv_pair"):
         return es * (3 * 128 + 3 * d) * NT
-    if name.startswith("suffix_scan_pair"):
-        return 2 * 4.0 * 4 * cfg.N * tiles * (64 * 64 + 64)
+    if name == "suffix_scan_blocks":
+        return 2 * 4.0 * 4 * (S // 128) * cfg.N * tiles * (64 * 64 + 64)
     return {
         "tile_sums": es * (S + d) * NT,
         "tile_sums_mfma": es * (S + d) * NT,

@@ -25,7 +25,8 @@
 // tokens with d = 128 and S = 128 or 256 the walks instead take 128-bucket x
 // 128-column blocks with eight waves (causal_bwd_dq_wide_kernel,
 // causal_bwd_dkv_wide_kernel): dQ and dK of a block whole, dV summed over the
-// blocks.
+// blocks; one launch takes the forward walks of every block, with the
+// workgroups that read the same V and dOut rows on the same XCD.
 //
 // Layout.  Workgroups are 4 wave64s; wave w owns bucket block w
 // (s = 16 w .. 16 w + 15).  Products use v_mfma_f32_16x16x32_bf16 with the
@@ -938,18 +939,24 @@ struct WideGeo {
     static_assert(3 * kBlk <= kWideThreads && kBlk % 64 == 0, "one staging block per thread, a tensor per wave");
 };
 
-// B1 over a 128 x 128 block (bf16 tokens, d = 128): the forward walk of
+// B1 over 128 x 128 blocks (bf16 tokens, d = 128): the forward walk of
 // causal_bwd_dq_mfma_kernel over 128 buckets and every value column at once,
-// eight waves (wave w: buckets 16 w .. 16 w + 15 of the block).  It writes
-// the block's dQ whole (bf16, the caller's dQ), its fp32 copy [N T][128], the
-// running mass at every sub-chunk start [N][tiles][subs][128], and the
-// tile's suffix totals as four 64 x 64 records, (bucket group g2, value
-// half h) at bwd_records + (2 g2 + h) N tiles rec.
+// eight waves (wave w: buckets 16 w .. 16 w + 15 of the block).  For its
+// block it writes dQ whole (bf16, the caller's dQ) and dQ's bf16 remainders
+// [N T][128], the running mass at every sub-chunk start
+// [N][tiles][subs][128], and the tile's suffix totals as four 64 x 64
+// records, (bucket group g2, value half h) at bwd_records + (2 g2 + h) N tiles
+// rec.  One launch walks the blocks of `pairs` consecutive 128-bucket groups
+// (block b: buckets s0 + 128 b ..; its outputs at b times the *_ps strides):
+// the workgroups of one tile and stream, which read the same V and dOut rows,
+// are 8 apart in launch order, so they land on the same XCD and the second
+// reads of those rows come from its L2.
 __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const bf16_t* __restrict__ g, bf16_t* __restrict__ dq_hi, bf16_t* __restrict__ dq_lo,
-    float* __restrict__ apre, const float* __restrict__ fwd_records, float* __restrict__ bwd_records,
-    int64_t T, int tile, int64_t tiles, int64_t rec, int ldq, int ld_hi, int s0, int64_t fwd_rec) {
+    const bf16_t* __restrict__ q_in, const bf16_t* __restrict__ k_in, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ g, bf16_t* __restrict__ dq_hi_in, bf16_t* __restrict__ dq_lo_in,
+    float* __restrict__ apre_in, const float* __restrict__ fwd_records, float* __restrict__ bwd_records_in,
+    int64_t N, int64_t T, int tile, int64_t tiles, int64_t rec, int ldq, int ld_hi, int s0_in, int64_t fwd_rec,
+    DqWidePairs pp) {
     using G = WideGeo;
     using PR = G::PR;
     using PM = G::PM;
@@ -966,7 +973,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int s = 16 * w + lr;  // the lane's bucket in the block
-    const int64_t n = blockIdx.y, ti = blockIdx.x;
+    const WideItem it = wide_item(blockIdx.x, pp.pairs, N * tiles);
+    if (it.item < 0) return;  // the last group's padding
+    const int64_t n = it.item / tiles, ti = it.item % tiles;
+    const int b = it.block;
+    const bf16_t* q = q_in + kWideS * b;
+    const bf16_t* k = k_in + kWideS * b;
+    bf16_t* dq_hi = dq_hi_in + b * pp.hi_ps;
+    bf16_t* dq_lo = dq_lo_in ? dq_lo_in + b * pp.lo_ps : nullptr;
+    float* apre = apre_in + b * pp.ap_ps;
+    float* bwd_records = bwd_records_in + b * pp.rec_ps;
+    const int s0 = s0_in + kWideS * b;
     const int64_t t_begin = ti * tile;
     const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
     const int64_t base = n * T + t_begin;
@@ -1157,7 +1174,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const int g2 = w >> 2, sl = 16 * (w & 3) + lr;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        float* br = bwd_records + (int64_t(2 * g2 + h) * gridDim.y * tiles + n * tiles + ti) * rec;
+        float* br = bwd_records + (int64_t(2 * g2 + h) * N * tiles + n * tiles + ti) * rec;
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
@@ -1538,15 +1555,19 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
 
 hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dq_hi,
                                      int ld_hi, void* dq_lo, float* apre, const float* fwd_records,
-                                     float* bwd_records, const Problem& p, int s0, hipStream_t stream) {
-    if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || s0 % kWideS != 0 || s0 >= p.S ||
-        p.tile % kBC != 0 || !dq_hi || ld_hi < kWideS)
+                                     float* bwd_records, const Problem& p, int s0, const DqWidePairs& pp,
+                                     hipStream_t stream) {
+    if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || s0 % kWideS != 0 || pp.pairs < 1 ||
+        s0 + kWideS * pp.pairs > p.S || p.tile % kBC != 0 || !dq_hi || ld_hi < kWideS)
         return hipErrorInvalidValue;
-    const dim3 grid(unsigned(p.tiles), unsigned(p.N));
+    const int64_t groups = (p.N * p.tiles + kWideXcds - 1) / kWideXcds;
+    // gfx950 takes at most 2^32 - 1 work-items along a grid dimension.
+    if (groups * kWideXcds * pp.pairs * kWideThreads > int64_t(UINT32_MAX)) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(groups * kWideXcds * pp.pairs));
     causal_bwd_dq_wide_kernel<<<grid, kWideThreads, WideGeo::kDqLds, stream>>>(
         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
         static_cast<const bf16_t*>(g), static_cast<bf16_t*>(dq_hi), static_cast<bf16_t*>(dq_lo), apre, fwd_records,
-        bwd_records, p.T, p.tile, p.tiles, record_floats(kBS, kBS), p.S, ld_hi, s0, p.rec);
+        bwd_records, p.N, p.T, p.tile, p.tiles, record_floats(kBS, kBS), p.S, ld_hi, s0, p.rec, pp);
     return hipGetLastError();
 }
 

@@ -273,6 +273,10 @@ CausalBwdPlan plan_causal_bwd(const Problem& p, int kernel) {
     return pl;
 }
 
+// The running mass of one 128-bucket block walk: 128 floats per 16 tokens
+// of each tile.
+int64_t wide_apre_floats(const Problem& p) { return round64(p.N * p.tiles * (p.tile / 16) * int64_t(128)); }
+
 // Workspace of the causal backward: the forward prefix records unless given,
 // the suffix records (of one column group, or of one 64 x 64 block: the
 // groups and blocks take turns), the running mass every 16 tokens, dq32 (dQ,
@@ -284,14 +288,15 @@ CausalBwdLayout causal_bwd_layout(const Problem& p, bool records_given, const Ca
     const int64_t NT = p.N * p.T;
     l.fwd = records_given ? 0 : p.N * p.tiles * p.rec;
     if (pl.wide2()) {
-        // A pair of bucket groups: the suffix records of its four 64 x 64
-        // blocks, its running mass and dQ's bf16 remainders and bf16 part
-        // (128 buckets, 2 + 2 bytes); a dV running sum when there are several
-        // pairs.
-        l.bwd = 4 * p.N * p.tiles * record_floats(64, 64);
-        l.apre = round64(p.N * p.tiles * (p.tile / 16) * int64_t(128));
-        l.dq32 = round64(NT * 128);
-        l.acc = pl.mblocks > 2 ? round64(NT * p.d) : 0;
+        // Per pair of bucket groups (one forward-walk launch covers them
+        // all): the suffix records of its four 64 x 64 blocks, its running
+        // mass, and dQ's bf16 remainders and bf16 part (128 buckets, 2 + 2
+        // bytes); a dV running sum when there are several pairs.
+        const int64_t pairs = pl.mblocks / 2;
+        l.bwd = pairs * 4 * p.N * p.tiles * record_floats(64, 64);
+        l.apre = pairs * wide_apre_floats(p);
+        l.dq32 = round64(pairs * NT * 128);
+        l.acc = pairs > 1 ? round64(NT * p.d) : 0;
         return l;
     }
     if (pl.blocked()) {
@@ -324,6 +329,19 @@ hipError_t zero_fill(float* p, int64_t n, hipStream_t stream) {
     if (n <= 0 || !p) return hipSuccess;
     fill_zero_kernel<<<unsigned((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(p, n);
     return hipGetLastError();
+}
+
+// The reverse scan of suffix records kept as pr.N record streams (several
+// arrays of N streams each, back to back), in launches of at most
+// kMaxStreams streams (the scan's grid.y).
+hipError_t scan_suffix_records(float* records, const Problem& pr, hipStream_t stream) {
+    for (int64_t n0 = 0; n0 < pr.N; n0 += kMaxStreams) {
+        Problem part = pr;
+        part.N = pr.N - n0 < kMaxStreams ? pr.N - n0 : kMaxStreams;
+        const hipError_t e = launch_tile_scan(records + n0 * pr.tiles * pr.rec, nullptr, part, stream, /*reverse=*/true);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 __global__ void copy_floats_kernel(const float* src, float* dst, int64_t n) {
@@ -943,43 +961,46 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
             return base ? static_cast<void*>(static_cast<char*>(base) + c * es_) : nullptr;
         };
         if (pl.wide2()) {
-            // Per pair of bucket groups (buckets 128 mp ..): one forward walk
+            // Per pair of bucket groups (buckets 128 mp ..): a forward walk
             // over its 128 buckets and every value column (its dQ whole,
             // straight to the caller's dQ; the suffix records of its four
-            // 64 x 64 blocks), one reverse scan of those records, then one
-            // backward walk over the same block: dK of its buckets whole, dV
-            // added to its running sum over the pairs in pair order (the
-            // last pair writes the caller's dV).
-            Problem p4 = pb;
-            p4.N = 4 * p.N;
-            const int64_t rec_n = p.N * p.tiles * pb.rec;
+            // 64 x 64 blocks), all pairs in one launch; one reverse scan of
+            // every pair's records; then per pair a backward walk over the
+            // same block: dK of its buckets whole, dV added to its running
+            // sum over the pairs in pair order (the last pair writes the
+            // caller's dV).
             const int pairs = pl.mblocks / 2;
-            // The dq32 region holds dQ's bf16 remainders [N T][128] and, when
-            // dQ is not asked for, its bf16 part after them.
+            const int64_t rec_n = p.N * p.tiles * pb.rec;
+            // The dq32 region holds dQ's bf16 remainders [pairs][N T][128]
+            // and, when dQ is not asked for, its bf16 part after them.
             bf16_t* dq_lo_ws = reinterpret_cast<bf16_t*>(dq32);
+            bf16_t* dq_hi_ws = dq_lo_ws + pairs * NT * 128;
+            DqWidePairs pp;
+            pp.pairs = pairs;
+            pp.hi_ps = dQ ? 128 : NT * 128;  // the caller's dQ: the pair's first column
+            pp.lo_ps = NT * 128;
+            pp.ap_ps = wide_apre_floats(p);
+            pp.rec_ps = 4 * rec_n;
+            void* dq_hi0 = dQ ? dQ : static_cast<void*>(dq_hi_ws);
+            const int ld_hi = dQ ? p.S : 128;
+            RACE_TRY(launch_causal_bwd_dq_wide(probsQ, probsK, V, dOut, dq_hi0, ld_hi, dK || dV ? dq_lo_ws : nullptr,
+                                               apre, fwd_rec, bwd_rec, p, 0, pp, stream));
+            RACE_TRY(marks->mark(stream));
+            if (!dK && !dV) return RACE_SUCCESS;
+            Problem p4 = pb;
+            p4.N = pairs * 4 * p.N;
+            RACE_TRY(scan_suffix_records(bwd_rec, p4, stream));
+            RACE_TRY(marks->mark(stream));
             for (int mp = 0; mp < pairs; ++mp) {
-                // dQ's bf16 part goes to the caller's dQ (or, not asked for,
-                // to the workspace after the remainders).
-                void* dq_hi = dQ ? col(dQ, 128 * mp, es) : static_cast<void*>(dq_lo_ws + NT * 128);
-                const int ld_hi = dQ ? p.S : 128;
-                RACE_TRY(launch_causal_bwd_dq_wide(static_cast<const char*>(probsQ) + 128 * mp * es,
-                                                   static_cast<const char*>(probsK) + 128 * mp * es, V, dOut,
-                                                   dq_hi, ld_hi, dK || dV ? dq_lo_ws : nullptr, apre, fwd_rec,
-                                                   bwd_rec, p, 128 * mp,
-                                                   stream));
-                RACE_TRY(marks->mark(stream));
-                if (!dK && !dV) continue;
-                RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p4, stream, /*reverse=*/true));
-                RACE_TRY(marks->mark(stream));
                 BwdWide wb;
                 wb.ldq = p.S;
-                wb.dq_hi = dq_hi;
+                wb.dq_hi = static_cast<const bf16_t*>(dq_hi0) + mp * pp.hi_ps;
                 wb.ld_hi = ld_hi;
-                wb.dq_lo = dq_lo_ws;
-                wb.apre = apre;
+                wb.dq_lo = dq_lo_ws + mp * pp.lo_ps;
+                wb.apre = apre + mp * pp.ap_ps;
                 for (int g2 = 0; g2 < 2; ++g2) {
-                    wb.rec[g2][0] = bwd_rec + (2 * g2) * rec_n;
-                    wb.rec[g2][1] = bwd_rec + (2 * g2 + 1) * rec_n;
+                    wb.rec[g2][0] = bwd_rec + mp * pp.rec_ps + (2 * g2) * rec_n;
+                    wb.rec[g2][1] = bwd_rec + mp * pp.rec_ps + (2 * g2 + 1) * rec_n;
                 }
                 wb.acc_v = dV && pairs > 1 ? acc : nullptr;
                 wb.v_first = mp == 0;
@@ -1020,7 +1041,7 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
                                                    pb, b1, stream, 128));
                 RACE_TRY(marks->mark(stream));
                 if (!dK && !dV) continue;
-                RACE_TRY(launch_tile_scan(bwd_rec, nullptr, p2, stream, /*reverse=*/true));
+                RACE_TRY(scan_suffix_records(bwd_rec, p2, stream));
                 RACE_TRY(marks->mark(stream));
                 for (int h = 0; h < 2; ++h) {
                     BwdBlock blk = b1;

@@ -260,17 +260,49 @@ hipError_t launch_causal_bwd_dkv_mfma(const void* q, const void* k, const void* 
                                       const float* dq32, const float* apre,
                                       const float* suffix_records, void* dK, void* dV,
                                       const Problem& p, const BwdBlock& blk, hipStream_t stream);
-// The forward walk (B1) over a 128-bucket x 128-column block (bf16 tokens,
-// d = 128; buckets s0 .. s0 + 127, with q and k pointing at bucket s0 of the
-// full tensors and fwd_records the full problem's): dQ of those buckets whole
-// as bf16 (dq_hi, rows of ld_hi: the caller's dQ at bucket s0, or workspace)
-// with the bf16 rounding of each remainder (dq_lo, rows of 128; null when no
-// backward walk follows), which the backward walk reads back as hi + lo; the running mass
+// How one forward-walk launch covers `pairs` consecutive 128-bucket blocks:
+// block b's outputs lie b times these strides (in elements of each buffer)
+// past the pointers the launch is given.
+struct DqWidePairs {
+    int pairs = 1;
+    int64_t hi_ps = 0;   // dq_hi (bf16)
+    int64_t lo_ps = 0;   // dq_lo (bf16)
+    int64_t ap_ps = 0;   // apre (floats)
+    int64_t rec_ps = 0;  // bwd_records (floats)
+};
+// Workgroups per launch-order group of the block walks: gfx950 hands
+// consecutive workgroups of a launch to its eight XCDs in turn, so
+// workgroups kWideXcds apart run on the same XCD.
+constexpr int kWideXcds = 8;
+// Workgroup x of a forward-walk launch over `pairs` blocks walks item
+// (stream n, tile ti: item = n tiles + ti) of block `block`: groups of
+// kWideXcds items, each listed once per block, so the workgroups of one
+// item (the same V and dOut rows) are kWideXcds apart.  item is -1 for the
+// padding past the last item.
+struct WideItem {
+    int64_t item;
+    int block;
+};
+__host__ __device__ inline WideItem wide_item(int64_t x, int pairs, int64_t items) {
+    const int64_t per = int64_t(kWideXcds) * pairs;
+    const int64_t grp = x / per, in = x % per;
+    const int64_t item = grp * kWideXcds + in % kWideXcds;
+    return {item < items ? item : -1, int(in / kWideXcds)};
+}
+// The forward walk (B1) over 128-bucket x 128-column blocks (bf16 tokens,
+// d = 128; block b holds buckets s0 + 128 b .. s0 + 128 b + 127, with q and k
+// pointing at bucket s0 of the full tensors and fwd_records the full
+// problem's): dQ of those buckets whole as bf16 (dq_hi, rows of ld_hi: the
+// caller's dQ at bucket s0, or workspace) with the bf16 rounding of each
+// remainder (dq_lo, rows of 128; null when no backward walk follows), which
+// the backward walk reads back as hi + lo; the running mass
 // [N][tiles][tile / 32][128]; the suffix records of the block's four 64 x 64
 // parts, (group g2, value half h) at bwd_records + (2 g2 + h) N tiles rec.
+// Block b's outputs are offset by b times pp's strides.
 hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v, const void* g, void* dq_hi,
                                      int ld_hi, void* dq_lo, float* apre, const float* fwd_records,
-                                     float* bwd_records, const Problem& p, int s0, hipStream_t stream);
+                                     float* bwd_records, const Problem& p, int s0, const DqWidePairs& pp,
+                                     hipStream_t stream);
 // The backward walk over the same block: the buffers its forward walk wrote
 // and dV's accumulation.
 struct BwdWide {

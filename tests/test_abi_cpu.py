@@ -106,11 +106,13 @@ def test_causal_bwd_workspace_for_matrix_core_blocks(race):
     # S = 256, d = 128: 64 x 64 blocks on the matrix cores.  Forward records
     # of the full shape, suffix records of one block, the running mass every
     # 16 tokens and dq32 for one block; fp32 tokens add nothing.  bf16 tokens
-    # take one forward walk over both value groups per bucket group and one
-    # backward walk per pair of bucket groups: the suffix records of a pair's
-    # four blocks, the running mass and dq32 of both groups, and an fp32
-    # running sum of dV (N T d) over the two pairs (the walks write dQ and dK
-    # whole).  S = 128 is a single pair: no running sum.  Host arithmetic only.
+    # take a forward and a backward walk per pair of bucket groups (128
+    # buckets), the forward walks of every pair in one launch: per pair the
+    # suffix records of its four blocks, its running mass (128 buckets every
+    # 16 tokens) and dQ's bf16 remainders and bf16 part (N T x 128 x 4
+    # bytes), and an fp32 running sum of dV (N T d) over the two pairs (the
+    # walks write dQ and dK whole).  S = 128 is a single pair: no running sum.
+    # Host arithmetic only.
     from race_attention_kernel_amd import abi
 
     def r64(x):
@@ -124,12 +126,14 @@ def test_causal_bwd_workspace_for_matrix_core_blocks(race):
     base = N * tiles * rec_full + N * tiles * rec_blk + apre + dq32
     st, nbytes = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 32, d, abi.RACE_F32), abi.options(tile, 0))
     assert st == 0 and nbytes == base * 4
-    pair = N * tiles * rec_full + 4 * N * tiles * rec_blk + 2 * apre + 2 * dq32
+    apre_pair = r64(N * tiles * (tile // 16) * 128)
+    pairs2 = N * tiles * rec_full + 8 * N * tiles * rec_blk + 2 * apre_pair + r64(2 * NT * 128)
     st, nbytes = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 32, d, abi.RACE_BF16), abi.options(tile, 0))
-    assert st == 0 and nbytes == (pair + r64(NT * d)) * 4
+    assert st == 0 and nbytes == (pairs2 + r64(NT * d)) * 4
     rec_128 = r64(128 * d + 128)
+    pair1 = N * tiles * rec_128 + 4 * N * tiles * rec_blk + apre_pair + r64(NT * 128)
     st, nbytes = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 16, d, abi.RACE_BF16), abi.options(tile, 0))
-    assert st == 0 and nbytes == (pair - N * tiles * (rec_full - rec_128)) * 4
+    assert st == 0 and nbytes == pair1 * 4
     # Forced vector-ALU walks: two column groups of 64, no block parts.
     st, vb = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 32, d, abi.RACE_F32),
                                             abi.options(tile, abi.RACE_KERNEL_VALU))

@@ -56,14 +56,14 @@ def test_noncausal_backward_launch_names_follow_the_library():
 
 def test_causal_backward_launch_names_follow_the_library():
     # race_api.hip: one 64 x 64 block at S = d = 64; bf16 with d = 128 and S
-    # = 128 or 256, a forward walk, a reverse scan and a backward walk per
-    # 128-bucket block after the forward's tile sums and scan; other shapes
-    # get generic names.
+    # = 128 or 256, after the forward's tile sums and scan the forward walks
+    # of every 128-bucket block in one launch, one reverse scan, then a
+    # backward walk per block; other shapes get generic names.
     b = load_bench()
     assert b.causal_bwd_phases(64, 64, 4) == b.BWD_PHASES[True]
     assert b.causal_bwd_phases(256, 128, 2) == [
-        "bwd_tile_sums", "tile_scan", "bwd_dq_pair0", "suffix_scan_pair0", "bwd_dkv_pair0",
-        "bwd_dq_pair1", "suffix_scan_pair1", "bwd_dkv_pair1"]
+        "bwd_tile_sums", "tile_scan", "bwd_dq_walks", "suffix_scan_blocks", "bwd_dkv_pair0",
+        "bwd_dkv_pair1"]
     assert len(b.causal_bwd_phases(128, 128, 2)) == 5
     assert b.causal_bwd_phases(256, 128, 4) == []
 

@@ -139,6 +139,26 @@ def test_block_walks_at_explicit_tiles(race, oracle, cuda, L, R, tile):
     check_grads(oracle, q, k, v, g, out, dq, dk, dv, tol_for(torch.bfloat16))
 
 
+def test_block_walks_many_streams(race, oracle, cuda):
+    # S = 256: the reverse scan takes the suffix records of both 128-bucket
+    # blocks as 8 N record streams, past the 65535 streams of one scan launch
+    # for N > 8191; it runs in launches of at most 65535.  Record stream
+    # (4 b + a) N + n (block b, array a) of the streams checked here falls on
+    # both sides of the launch boundaries (65535 and 131070 at N = 16400).
+    N, T = 16400, 40
+    say("c-bwd block many streams", N, T)
+    q, k, v = race.make_inputs(N, T, 8, 32, 128, seed=28, dtype=torch.bfloat16, device=cuda, gen_device="cuda")
+    g = torch.randn(v.shape, device=cuda, generator=torch.Generator(device=cuda).manual_seed(29)).to(v.dtype)
+    dq, dk, dv = race.race_causal_backward(q, k, v, g)
+    torch.cuda.synchronize()
+    pick = [0, 8000, 16269, 16270, 16334, 16335, 16399]
+    qn, kn, vn, gn = (to_np(x[pick]) for x in (q, k, v, g))
+    rq, rk, rv = oracle.causal_bwd(qn, kn, vn, gn, nthreads=16)
+    errs = [per_stream_rel_err(to_np(x[pick]), r) for x, r in ((dq, rq), (dk, rk), (dv, rv))]
+    say("c-bwd many streams errors", *(f"{e:.2e}" for e in errs))
+    assert max(errs) <= tol_for(torch.bfloat16)
+
+
 def test_block_walks_bitwise_reproducible(race, cuda):
     say("c-bwd block bitwise")
     q, k, v, g = race.make_inputs(3, 2100, 8, 32, 128, seed=27, dtype=torch.bfloat16, grad_out=True)
@@ -259,7 +279,8 @@ def test_unsupported_shape_raises(race, cuda):
 
 def test_cfg5_shape_backward(race, oracle, cuda):
     # cfg5 (N = 128, L = 8, R = 32, d = 128, T = 16384, bf16) through
-    # autograd: two column groups of 64; 4 streams against the oracle VJP.
+    # autograd: the walks over two 128 x 128 blocks; 16 streams against the
+    # oracle VJP.
     say("c-bwd cfg5")
     q, k, v = race.make_inputs(128, 16384, 8, 32, 128, seed=5, dtype=torch.bfloat16, device=cuda,
                                gen_device="cuda")

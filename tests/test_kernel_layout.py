@@ -1161,3 +1161,64 @@ def test_wide_backward_walk_without_the_final_flush_loses_the_first_rows():
                 written.add((off // 2) // ld)
         r0 -= WIDE_C
     assert not written & set(range(WIDE_C))
+
+
+# ---------------------------------------------------------------------------
+# race_internal.h wide_item(): one forward-walk launch over `pairs` 128-bucket
+# blocks.  Workgroup x walks item (stream n, tile ti) of block b; the
+# workgroups of one item read the same V and dOut rows and must sit
+# kWideXcds = 8 apart (workgroup x runs on XCD x mod 8).
+
+XCDS = 8
+
+
+def wide_item(x: int, pairs: int, items: int):
+    per = XCDS * pairs
+    grp, inside = divmod(x, per)
+    item = grp * XCDS + inside % XCDS
+    return (item if item < items else -1), inside // XCDS
+
+
+def wide_grid(pairs: int, items: int) -> int:
+    """launch_causal_bwd_dq_wide: ceil(items / 8) groups of 8 pairs workgroups."""
+    return -(-items // XCDS) * XCDS * pairs
+
+
+@pytest.mark.parametrize("pairs", [1, 2])
+@pytest.mark.parametrize("items", [1, 7, 8, 9, 512, 1000])
+def test_wide_forward_walks_cover_every_item_and_block_once(pairs, items):
+    seen = Counter()
+    xcd = {}
+    pad = 0
+    for x in range(wide_grid(pairs, items)):
+        item, b = wide_item(x, pairs, items)
+        assert 0 <= b < pairs
+        if item < 0:
+            pad += 1
+            continue
+        seen[(item, b)] += 1
+        xcd.setdefault(item, set()).add(x % XCDS)
+    assert set(seen.values()) == {1} and len(seen) == items * pairs
+    assert pad < XCDS * pairs
+    # The workgroups of one item share an XCD, and within a block the items
+    # keep launch order (item i before item i + 1).
+    assert all(len(v) == 1 for v in xcd.values())
+    for b in range(pairs):
+        order = [wide_item(x, pairs, items)[0] for x in range(wide_grid(pairs, items))
+                 if wide_item(x, pairs, items)[1] == b and wide_item(x, pairs, items)[0] >= 0]
+        assert order == list(range(items))
+    # One block: the identity mapping of the grid before the blocks shared a launch.
+    if pairs == 1:
+        assert all(wide_item(x, 1, items)[0] == x for x in range(items))
+
+
+def test_wide_forward_walks_interleaved_blocks_split_an_item_over_xcds():
+    # Planted mistake: block = x mod pairs (the blocks of an item adjacent in
+    # launch order) covers every item and block once but puts the two
+    # workgroups of an item on different XCDs.
+    pairs, items = 2, 64
+    xcd = {}
+    for x in range(items * pairs):
+        item, b = divmod(x, pairs)
+        xcd.setdefault(item, set()).add(x % XCDS)
+    assert any(len(v) > 1 for v in xcd.values())
