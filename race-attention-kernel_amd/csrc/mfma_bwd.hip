@@ -931,7 +931,8 @@ struct WideGeo {
     using FT = OutTile<float, kWideS, kBC>;   // rows of 128 fp32
     static constexpr int kQTBytes = kBC * QT::kRowBytes;
     static constexpr int kFTBytes = kBC * FT::kRowBytes;
-    static constexpr int kDqLds = 3 * kRBytes + kMBytes + kFTBytes + kQTBytes;  // B1: K, V, G, M, dQ tile, Q rows
+    static constexpr int kPlanesBytes = 3 * kRBytes;  // K, V, G of one sub-chunk
+    static constexpr int kDqLds = 2 * kPlanesBytes + kMBytes + kFTBytes + kQTBytes;  // B1: two plane slots, M, dQ tile, Q rows
     // B3 with its row tiles: Q, dQ hi and lo, dV's sum in; dK, dV out.
     static constexpr int kDkvLds = kLds + 4 * kQTBytes + 2 * kFTBytes;
     static_assert(kDkvLds <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
@@ -962,10 +963,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     using PM = G::PM;
     using T32 = OutTile<float, kWideS, kBC>;
     extern __shared__ __align__(16) unsigned char lds[];
-    unsigned char* Ks = lds;
-    unsigned char* Vs = Ks + G::kRBytes;
-    unsigned char* Gs = Vs + G::kRBytes;
-    unsigned char* Ms = Gs + G::kRBytes;
+    // Two slots of the K, V, G planes (sub-chunks alternate), then M, the
+    // dQ tile and the Q rows.
+    unsigned char* Ms = lds + 2 * G::kPlanesBytes;
     unsigned char* D32s = Ms + G::kMBytes;
     unsigned char* Qt = D32s + kBC * kWideS * 4;  // Q rows of the sub-chunk
     using QT = G::QT;
@@ -1018,7 +1018,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const int sld = tensor == 0 ? ldq : kWideD;
     const bf16_t* ssrc = tensor == 0 ? k + base * ldq : tensor == 1 ? v + base * kWideD : g + base * kWideD;
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
-    unsigned char* splane = tensor == 0 ? Ks : tensor == 1 ? Vs : Gs;
+    const int splane = tensor * G::kRBytes;  // the staged tensor's plane inside a slot
     // Sub-chunks of operands in flight in registers ahead of the one in LDS.
     constexpr int kDepth = RACE_BWD_WIDE_DQ_DEPTH;
     StageBlock<bf16_t> st[kDepth];
@@ -1056,18 +1056,27 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
         st[d].load(srs, d * kBC, sa, sb, sld);
         load_q(qx[d], d * kBC);
     }
+    // Sub-chunk r0 uses plane slot (r0 / kBC) & 1, so two barriers per
+    // sub-chunk suffice: its staging and Q-row stores need none before them
+    // (the slot was last read two sub-chunks back, with two barriers since;
+    // the Q rows were last read before the previous sub-chunk's second
+    // barrier), and the previous dQ tile is read after the first barrier and
+    // rewritten only after the second.
     auto sub_chunk = [&](StageBlock<bf16_t>& stg, uint4& qv, int r0) {
-        __syncthreads();
-        if (tensor < 3) stg.store_r<PR>(splane, sa, sb);
+        unsigned char* Ks = lds + ((r0 / kBC) & 1) * G::kPlanesBytes;
+        unsigned char* Vs = Ks + G::kRBytes;
+        unsigned char* Gs = Vs + G::kRBytes;
+        if (tensor < 3) stg.store_r<PR>(Ks + splane, sa, sb);
         *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qv;
         stg.load(srs, r0 + kDepth * kBC, sa, sb, sld);  // past the tile: zeros, never used
         load_q(qv, r0 + kDepth * kBC);
+        __syncthreads();
+        // The previous sub-chunk's dQ tile, complete since this barrier.
         // Unconditional: at r0 = 0 the offsets are negative, outside the
         // buffer ranges, and the stores are dropped; a sub-chunk past a
         // ragged tile end reads zeros and stores nothing.
         flush(r0 - kBC);
         if (gq == 0 && r0 < rows) ap[(r0 / kBC) * kWideS + s] = a0;
-        __syncthreads();
 
         // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
         float qc[2][4];

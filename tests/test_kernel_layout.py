@@ -1222,3 +1222,62 @@ def test_wide_forward_walks_interleaved_blocks_split_an_item_over_xcds():
         item, b = divmod(x, pairs)
         xcd.setdefault(item, set()).add(x % XCDS)
     assert any(len(v) > 1 for v in xcd.values())
+
+
+# ---------------------------------------------------------------------------
+# mfma_bwd.hip causal_bwd_dq_wide_kernel: the LDS regions each sub-chunk
+# touches between its two barriers.  A barrier ends an epoch for every wave
+# at once, so two waves may touch one region in the same epoch only if
+# neither writes it (the writes of one epoch by different waves are disjoint
+# chunks, which the staging tests above cover).
+
+
+def dq_walk_epochs(subs: int, slots: int):
+    """Per epoch: {(region, 'r'|'w', wave)} of the walk over `subs`
+    sub-chunks with `slots` plane slots (regions: plane slot p, Qt, M,
+    D32 = the dQ tile)."""
+    epochs = [set()]
+
+    def acc(region, kind, waves=range(8)):
+        for w in waves:
+            epochs[-1].add((region, kind, w))
+
+    for t in range(subs):
+        plane = f"plane{t % slots}"
+        acc(plane, "w", range(6))   # staging: waves 0..5 (three tensors)
+        acc("Qt", "w")
+        epochs.append(set())         # first barrier
+        acc("D32", "r")              # flush of sub-chunk t - 1
+        acc("Qt", "r")               # step 1
+        acc(plane, "r")              # step 1 (K), step 2 (V, G)
+        acc("M", "w", range(3))      # step 2 on waves 0..2
+        epochs.append(set())         # second barrier
+        acc("M", "r")                # step 3
+        acc(plane, "r")              # steps 3..5 (G, V)
+        acc("D32", "w")              # step 3
+    epochs.append(set())             # barrier before the last flush
+    acc("D32", "r")
+    return epochs
+
+
+def epoch_conflicts(epochs):
+    bad = []
+    for e, ev in enumerate(epochs):
+        for region in {r for r, _, _ in ev}:
+            writers = {w for r, k, w in ev if r == region and k == "w"}
+            users = {w for r, k, w in ev if r == region}
+            if writers and len(users) > 1 and not all(k == "w" for r, k, _ in ev if r == region):
+                bad.append((e, region))
+    return bad
+
+
+@pytest.mark.parametrize("subs", [1, 2, 3, 128])
+def test_wide_forward_walk_two_slots_need_two_barriers(subs):
+    assert epoch_conflicts(dq_walk_epochs(subs, 2)) == []
+
+
+def test_wide_forward_walk_one_slot_without_the_top_barrier_races():
+    # Planted mistake: one plane slot and no barrier before the staging
+    # stores: sub-chunk t + 1's staging writes the slot while slower waves
+    # still read it in steps 3..5 of sub-chunk t.
+    assert ("plane0" in {r for _, r in epoch_conflicts(dq_walk_epochs(2, 1))})
