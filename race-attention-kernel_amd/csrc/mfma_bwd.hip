@@ -1376,19 +1376,28 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
         if (w < 6) {
             const int b = w < 3 ? w : w - 3;
             const int bi = b >= 1 ? 1 : 0, bj = b == 2 ? 1 : 0;
+            // All four steps' fragments are read before the products, one
+            // branch per wave (a branch per step made each product wait for
+            // its own reads).
+            bf16x8 ah[4], bh[4];
+            if (w < 3) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    bf16x8 alo, bl;
+                    PR::frag(Gs, 16 * bi + lr, kk, gq, ah[kk], alo);
+                    PR::frag(Vs, 16 * bj + lr, kk, gq, bh[kk], bl);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    bf16x8 alo, bl;
+                    PM::frag_tr(WT, 32 * kk, 16 * bi, gq, lr, ah[kk], alo);
+                    PR::frag(Ks, 16 * bj + lr, kk, gq, bh[kk], bl);
+                }
+            }
             f32x4 m = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                bf16x8 ah, alo, bh, bl;
-                if (w < 3) {
-                    PR::frag(Gs, 16 * bi + lr, kk, gq, ah, alo);
-                    PR::frag(Vs, 16 * bj + lr, kk, gq, bh, bl);
-                } else {
-                    PM::frag_tr(WT, 32 * kk, 16 * bi, gq, lr, ah, alo);
-                    PR::frag(Ks, 16 * bj + lr, kk, gq, bh, bl);
-                }
-                m = mfma16(ah, bh, m);
-            }
+            for (int kk = 0; kk < 4; ++kk) m = mfma16(ah[kk], bh[kk], m);
             if (bi == bj) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
