@@ -273,9 +273,9 @@ CausalBwdPlan plan_causal_bwd(const Problem& p, int kernel) {
     return pl;
 }
 
-// The running mass of one 128-bucket block walk: 128 floats per 16 tokens
-// of each tile.
-int64_t wide_apre_floats(const Problem& p) { return round64(p.N * p.tiles * (p.tile / 16) * int64_t(128)); }
+// The running mass of one 128-bucket block walk: 128 floats per 32-token
+// sub-chunk of each tile (the walks take tiles of whole sub-chunks).
+int64_t wide_apre_floats(const Problem& p) { return round64(p.N * p.tiles * (p.tile / 32) * int64_t(128)); }
 
 // Workspace of the causal backward: the forward prefix records unless given,
 // the suffix records (of one column group, or of one 64 x 64 block: the

@@ -109,7 +109,7 @@ def test_causal_bwd_workspace_for_matrix_core_blocks(race):
     # take a forward and a backward walk per pair of bucket groups (128
     # buckets), the forward walks of every pair in one launch: per pair the
     # suffix records of its four blocks, its running mass (128 buckets every
-    # 16 tokens) and dQ's bf16 remainders and bf16 part (N T x 128 x 4
+    # 32 tokens) and dQ's bf16 remainders and bf16 part (N T x 128 x 4
     # bytes), and an fp32 running sum of dV (N T d) over the two pairs (the
     # walks write dQ and dK whole).  S = 128 is a single pair: no running sum.
     # Host arithmetic only.
@@ -126,7 +126,7 @@ def test_causal_bwd_workspace_for_matrix_core_blocks(race):
     base = N * tiles * rec_full + N * tiles * rec_blk + apre + dq32
     st, nbytes = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 32, d, abi.RACE_F32), abi.options(tile, 0))
     assert st == 0 and nbytes == base * 4
-    apre_pair = r64(N * tiles * (tile // 16) * 128)
+    apre_pair = r64(N * tiles * (tile // 32) * 128)
     pairs2 = N * tiles * rec_full + 8 * N * tiles * rec_blk + 2 * apre_pair + r64(2 * NT * 128)
     st, nbytes = abi.causal_bwd_workspace_bytes(abi.shape(N, T, 8, 32, d, abi.RACE_BF16), abi.options(tile, 0))
     assert st == 0 and nbytes == (pairs2 + r64(NT * d)) * 4
