@@ -932,9 +932,9 @@ struct WideGeo {
     static constexpr int kQTBytes = kBC * QT::kRowBytes;
     static constexpr int kFTBytes = kBC * FT::kRowBytes;
     static constexpr int kPlanesBytes = 3 * kRBytes;  // K, V, G of one sub-chunk
-    static constexpr int kDqLds = 2 * kPlanesBytes + kMBytes + kFTBytes + kQTBytes;  // B1: two plane slots, M, dQ tile, Q rows
+    static constexpr int kDqLds = 2 * kPlanesBytes + kMBytes + kFTBytes + kRBytes;  // B1: two plane slots, M, dQ tile, Q plane
     // B3 with its row tiles: Q, dQ hi and lo, dV's sum in; dK, dV out.
-    static constexpr int kDkvLds = kLds + 4 * kQTBytes + 2 * kFTBytes;
+    static constexpr int kDkvLds = kLds + 3 * kRBytes + kQTBytes + 2 * kFTBytes;
     static_assert(kDkvLds <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
     static constexpr int kBlk = (kBC / 4) * (128 / 8);    // staging blocks of one tensor
     static_assert(3 * kBlk <= kWideThreads && kBlk % 64 == 0, "one staging block per thread, a tensor per wave");
@@ -967,7 +967,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     // dQ tile and the Q rows.
     unsigned char* Ms = lds + 2 * G::kPlanesBytes;
     unsigned char* D32s = Ms + G::kMBytes;
-    unsigned char* Qt = D32s + kBC * kWideS * 4;  // Q rows of the sub-chunk
+    unsigned char* Qt = D32s + kBC * kWideS * 4;  // Q of the sub-chunk as a plane (rows = tokens)
     using QT = G::QT;
 
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
@@ -1023,9 +1023,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     constexpr int kDepth = RACE_BWD_WIDE_DQ_DEPTH;
     StageBlock<bf16_t> st[kDepth];
     // Q's rows: chunk tid of the sub-chunk (row tid / 16, 8 buckets) in
-    // from global memory, then read in the accumulator layout.
+    // from global memory, into a plane read transposed.
     static_assert(QT::kChunks * kBC == kWideThreads, "one Q chunk per thread");
     uint4 qx[kDepth];
+    // Row chunk tid of the sub-chunk (row tid / 16, buckets 8 (tid % 16) ..
+    // + 7) into a plane whose transposed reads give each lane its bucket's
+    // values at the accumulator layout's rows.
+    auto put_row_chunk = [&](unsigned char* plane, const uint4& x) {
+        const int row = tid / QT::kChunks, k0 = 8 * (tid % QT::kChunks);
+        PR::put4(plane, row, k0, uint2{x.x, x.y}, uint2{});
+        PR::put4(plane, row, k0 + 4, uint2{x.z, x.w}, uint2{});
+    };
     auto load_q = [&](uint4& x, int r0) {
         x = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
     };
@@ -1067,7 +1075,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
         unsigned char* Vs = Ks + G::kRBytes;
         unsigned char* Gs = Vs + G::kRBytes;
         if (tensor < 3) stg.store_r<PR>(Ks + splane, sa, sb);
-        *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qv;
+        put_row_chunk(Qt, qv);
         stg.load(srs, r0 + kDepth * kBC, sa, sb, sld);  // past the tile: zeros, never used
         load_q(qv, r0 + kDepth * kBC);
         __syncthreads();
@@ -1080,11 +1088,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
 
         // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
         float qc[2][4];
+        {
+            bf16x8 qf, unused;
+            PR::frag_tr(Qt, 0, 16 * w, gq, lr, qf, unused);
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
+            for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                qc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Qt + QT::at(16 * bi + 4 * gq + rr, 2 * s)));
+                for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = float(qf[4 * bi + rr]);
+        }
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         f32x4 rv[2], wv[2];
@@ -1207,14 +1218,15 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     unsigned char* MT = WT + G::kWTBytes;
     unsigned char* PTp = MT + G::kMBytes;
     unsigned char* Zr = PTp + G::kMBytes;
-    // Row tiles: Q, dQ (hi and lo) and dV's running sum of the sub-chunk in (whole rows
-    // in from global memory, read in the accumulator layout), dK and dV of
-    // the previous one out (written in the accumulator layout, stored as
+    // Q and dQ (hi and lo) of the sub-chunk come in as whole rows into
+    // planes read transposed, dV's running sum as whole rows into a row tile
+    // read in the accumulator layout; dK and dV of the previous sub-chunk go
+    // out through row tiles (written in the accumulator layout, stored as
     // whole rows).
     unsigned char* Qt = Zr + G::kZBytes;
-    unsigned char* Dh = Qt + G::kQTBytes;
-    unsigned char* Dl = Dh + G::kQTBytes;
-    unsigned char* Vt = Dl + G::kQTBytes;
+    unsigned char* Dh = Qt + G::kRBytes;
+    unsigned char* Dl = Dh + G::kRBytes;
+    unsigned char* Vt = Dl + G::kRBytes;
     unsigned char* dKt = Vt + G::kFTBytes;
     unsigned char* dVt = dKt + G::kQTBytes;
     using QT = G::QT;
@@ -1278,6 +1290,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
     // of 32 chunks).
     static_assert(QT::kChunks * kBC == kWideThreads && FT::kChunks * kBC == 2 * kWideThreads, "chunk split");
     uint4 qx, hx, lx, vx[2];
+    // Row chunk tid (row tid / 16, buckets 8 (tid % 16) .. + 7) of Q and dQ's
+    // two parts into planes whose transposed reads give each lane its
+    // bucket's values at the accumulator layout's rows.
+    auto put_row_chunk = [&](unsigned char* plane, const uint4& x) {
+        const int row = tid / QT::kChunks, k0 = 8 * (tid % QT::kChunks);
+        PR::put4(plane, row, k0, uint2{x.x, x.y}, uint2{});
+        PR::put4(plane, row, k0 + 4, uint2{x.z, x.w}, uint2{});
+    };
     auto load_rows = [&](int r0) {
         const int row = r0 + tid / QT::kChunks, c8 = 8 * (tid % QT::kChunks);
         qx = buf_load16<kPolicyDefault>(qr, (row * ldq + c8) * 2);
@@ -1288,9 +1308,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
             vx[i] = buf_load16<kPolicyDefault>(av_rd, r0 * FT::kRowBytes + 16 * (tid + i * kWideThreads));
     };
     auto store_rows = [&]() {
-        *reinterpret_cast<uint4*>(Qt + QT::chunk_at(tid)) = qx;
-        *reinterpret_cast<uint4*>(Dh + QT::chunk_at(tid)) = hx;
-        *reinterpret_cast<uint4*>(Dl + QT::chunk_at(tid)) = lx;
+        put_row_chunk(Qt, qx);
+        put_row_chunk(Dh, hx);
+        put_row_chunk(Dl, lx);
 #pragma unroll
         for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(Vt + FT::chunk_at(tid + i * kWideThreads)) = vx[i];
     };
@@ -1344,15 +1364,19 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
 
         // 1: Abar, r, W, alpha; W^T into its plane (row s, four consecutive i).
         float qc[2][4], dc[2][4];
+        {
+            bf16x8 qf, hf, lf, unused;
+            PR::frag_tr(Qt, 0, 16 * w, gq, lr, qf, unused);
+            PR::frag_tr(Dh, 0, 16 * w, gq, lr, hf, unused);
+            PR::frag_tr(Dl, 0, 16 * w, gq, lr, lf, unused);
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
+            for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = 16 * bi + 4 * gq + rr;
-                qc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Qt + QT::at(row, 2 * (16 * w + lr))));
-                dc[bi][rr] = to_f32(*reinterpret_cast<const bf16_t*>(Dh + QT::at(row, 2 * (16 * w + lr)))) +
-                             to_f32(*reinterpret_cast<const bf16_t*>(Dl + QT::at(row, 2 * (16 * w + lr))));
-            }
+                for (int rr = 0; rr < 4; ++rr) {
+                    qc[bi][rr] = float(qf[4 * bi + rr]);
+                    dc[bi][rr] = float(hf[4 * bi + rr]) + float(lf[4 * bi + rr]);
+                }
+        }
         bf16x8 kh, kl;
         PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
         f32x4 wv[2], al[2];

@@ -1281,3 +1281,49 @@ def test_wide_forward_walk_one_slot_without_the_top_barrier_races():
     # stores: sub-chunk t + 1's staging writes the slot while slower waves
     # still read it in steps 3..5 of sub-chunk t.
     assert ("plane0" in {r for _, r in epoch_conflicts(dq_walk_epochs(2, 1))})
+
+
+# ---------------------------------------------------------------------------
+# mfma_bwd.hip block walks: Q (and dQ's two bf16 parts) go from whole 16-byte
+# row chunks into Plane<false, 128> (put_row_chunk: chunk tid is row tid / 16,
+# buckets 8 (tid % 16) .. + 7, stored as two put4 of four), and step 1 reads
+# them with frag_tr(row0 = 0, col0 = 16 w): lane (g, lr) of wave w needs the
+# bucket 16 w + lr at rows 4 g + rr + 16 bi, element 4 bi + rr.
+
+
+def put_row_chunks(P: Plane, two_halves: bool = True) -> dict:
+    mem = {}
+    for tid in range(512):
+        row, k0 = divmod(tid, 16)
+        k0 *= 8
+        vals = [(row, k0 + j) for j in range(8)]
+        if two_halves:
+            for h in range(2):
+                a = P.off4(row, k0 + 4 * h)
+                for j in range(4):
+                    assert a + 2 * j not in mem
+                    mem[a + 2 * j] = vals[4 * h + j]
+        else:  # planted: the chunk stored whole at its first four's place
+            a = P.off4(row, k0)
+            for j in range(8):
+                mem[a + 2 * j] = vals[j]
+    return mem
+
+
+def test_row_chunks_in_a_plane_give_each_lane_its_bucket_at_accumulator_rows():
+    P = Plane(False, 128)
+    mem = put_row_chunks(P)
+    assert len(mem) == 32 * 128
+    for w, g in itertools.product(range(8), range(4)):
+        got = frag_tr(P, mem, 0, 16 * w, g)
+        for lr in range(16):
+            assert got[lr] == [(4 * g + e % 4 + 16 * (e // 4), 16 * w + lr) for e in range(8)]
+
+
+def test_row_chunks_stored_whole_give_the_wrong_buckets():
+    # Planted mistake: a 16-byte chunk written at once in natural order; the
+    # plane's fpos order puts elements 4..7 of the chunk elsewhere.
+    P = Plane(False, 128)
+    mem = put_row_chunks(P, two_halves=False)
+    got = frag_tr(P, mem, 0, 0, 0)
+    assert any(got[lr] != [(e % 4 + 16 * (e // 4), lr) for e in range(8)] for lr in range(16))
