@@ -21,7 +21,10 @@ first kernel and after every kernel; the per-kernel durations behind
 `roofline` come from it (its step time, with the extra events, is
 `profiled_ms_per_step`).  For the forward pass a third region runs K plain
 steps alternating two input sets, which no step finds left over from the
-step before: config.fresh_inputs.
+step before: config.fresh_inputs.  For the causal backward on the matrix
+cores a fourth region times K backward steps started, as autograd starts
+them, from a forward call's scanned tile records (the backward's own tile
+sums and scan skipped): config.bwd_from_saved_records.
 
 roofline: the dominant kernel's algorithmic HBM bytes per launch (each
 operand it streams read once, its output written once: bytes per
@@ -922,6 +925,35 @@ def measure(args, T: int) -> dict:
                  "m_tokens_per_s": round(cfg.N * T / (fresh_ms * 1e-3) / 1e6, 3),
                  "whole_op_frac": round(op_bytes(args.pass_, cfg, T, es) / (fresh_ms * 1e-3) / 1e9
                                         / PEAK_HBM_GBPS, 4)}
+    # Timed region 4 (causal backward on the matrix cores): the backward as
+    # autograd runs it, from a forward call's scanned tile records (the
+    # backward's own tile sums and scan skipped), K steps after W warmup
+    # steps.  Its workspace is left out of the peak-HBM figure.
+    peak_bytes = torch.cuda.max_memory_allocated(dev) - extra_bytes
+    from_records = None
+    if args.pass_ == "bwd" and cfg.causal and family == "mfma":
+        check(abi.fwd(*ptrs, None, sh, True, opts, ws.data_ptr(), ws_bytes, stream))
+        ropts = abi.options(tile, 0)
+        st_, rws_bytes = abi.causal_bwd_from_records_workspace_bytes(sh, ropts)
+        check(st_)
+        rws = torch.empty(max(rws_bytes // 4, 1), device=dev, dtype=torch.float32)
+
+        def from_rec():
+            check(abi.causal_bwd_from_records(*bptrs, ws.data_ptr(), *gptrs, sh, ropts, rws.data_ptr(),
+                                              rws_bytes, stream))
+
+        for _ in range(args.warmup):
+            from_rec()
+        events.record(bracket[0], stream)
+        for _ in range(args.steps):
+            from_rec()
+        events.record(bracket[1], stream)
+        torch.cuda.synchronize()
+        rec_ms = events.elapsed_ms(bracket[0], bracket[1]) / args.steps
+        from_records = {"ms_per_step": round(rec_ms, 5),
+                        "m_tokens_per_s": round(cfg.N * T / (rec_ms * 1e-3) / 1e6, 3),
+                        "tile_tokens": tile}
+        del rws
     # Intervals between consecutive events; the forward's last event and the
     # backward's first one bracket nothing and are dropped below.
     n_gaps = n_events - 1
@@ -939,8 +971,8 @@ def measure(args, T: int) -> dict:
     dom = max(range(n_launch), key=lambda j: phase_ms[j])
     dom_bytes = phase_bytes(names[dom], cfg, T, es, tiles, rec)
     achieved = dom_bytes / (phase_ms[dom] * 1e-3) / 1e9
-    # The extra input sets are left out of the peak: it describes one call.
-    peak_bytes = torch.cuda.max_memory_allocated(dev) - extra_bytes
+    # The extra input sets are left out of the peak (taken above): it
+    # describes one call.
     events.destroy()
 
     NT = cfg.N * T
@@ -973,6 +1005,7 @@ def measure(args, T: int) -> dict:
             "kernel": family, "tile_tokens": tile, "launches_per_step": n_launch, **settled,
             "input_sets": n_sets,
             "fresh_inputs": fresh,
+            "bwd_from_saved_records": from_records,
             "kernel_ms": {names[j]: round(phase_ms[j], 5) for j in range(n_launch)},
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
             "profiled_ms_per_step": round(profiled_ms, 5),
