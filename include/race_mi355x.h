@@ -267,9 +267,13 @@ race_status race_noncausal_bwd(const void* probsQ, const void* probsK, const voi
                                const race_shape* shape, const race_options* opts, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace of race_causal_bwd in bytes: two record arrays [N][tiles][rec],
- * the running mass at every 16-token step ([N][tiles][tile/16][S]) and an
- * fp32 copy of dQ ([N][T][S]) -- O(1) per token. */
+/* Workspace of race_causal_bwd in bytes, O(1) per token: the forward prefix
+ * records and the suffix records (of the walk's column group or block), the
+ * running mass at every sub-chunk start and dQ as the walks hand it over
+ * (an fp32 copy, or bf16 remainders); with bf16 tokens on the matrix cores
+ * also fp32 running sums of the gradients summed over blocks.  The size
+ * depends on the shape, dtype, tile length and kernel option (a host
+ * computation, no device needed). */
 race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_options* opts,
                                             size_t* bytes);
 
@@ -285,9 +289,13 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
  *   dk_j[s] = <Z_j[s][:], v_j> + Y_j[s],  dv_j[c] = sum_s k_j[s] Z_j[s][c].
  * The forward prefix states are recomputed (tile totals and their scan), so
  * only the forward's inputs are needed.  Any of dQ, dK, dV may be NULL to
- * skip it.  Runs the fp32 vector-ALU kernels; shapes whose state S*(d+1)
- * plus a 16-token sub-chunk do not fit one workgroup's LDS (e.g. S = 256,
- * d = 128) return RACE_ERROR_INVALID_VALUE, as does RACE_KERNEL_MFMA. */
+ * skip it.  Kernels: with S and d multiples of 64 (S <= 256, d <= 128) and
+ * tiles of whole 32-token sub-chunks, the matrix cores (64 x 64 bucket x
+ * value blocks; bf16 tokens with d = 128 and S = 128 or 256 in walks over
+ * 128 x 128 blocks); otherwise the vector ALU, in column groups where the
+ * state does not fit one workgroup's LDS (RACE_KERNEL_VALU forces it).
+ * RACE_KERNEL_MFMA on a shape without matrix-core kernels, a shape no kernel
+ * takes, and the other kernel options return RACE_ERROR_INVALID_VALUE. */
 race_status race_causal_bwd(const void* probsQ, const void* probsK, const void* V,
                             const void* dOut, void* dQ, void* dK, void* dV,
                             const race_shape* shape, const race_options* opts, void* workspace,
