@@ -89,9 +89,10 @@ typedef enum race_kernel {
      * product fp32-accurate for bf16 tokens too: W, the masked scores and the
      * carried state enter the products as bf16 hi + lo pairs, as they do for
      * fp32 tokens, so a bf16 result differs from the exact one by about its
-     * own rounding.  No counterpart in the reference's per-bucket path (its
-     * bf16 tensor-core kernel carries B as hi + lo, race_causal_fwd_tc.cu:36,
-     * and rounds W and the scores).  fp32 tokens: the same as MFMA_WG.
+     * own rounding.  No counterpart in the reference's per-bucket path; its
+     * bf16 tensor-core Algorithm-1 kernel likewise carries B and its scores
+     * as hi + lo pairs (race_causal_fwd_tc.cu:23-40).  fp32 tokens: the same
+     * as MFMA_WG.
      * Shapes without matrix-core kernels, the non-causal op, the backward,
      * the hashed and the Algorithm-1 entry points return
      * RACE_ERROR_INVALID_VALUE. */
