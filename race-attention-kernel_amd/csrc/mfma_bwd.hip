@@ -1436,10 +1436,18 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
         bf16x8 wh, wl, ah2, al2;
         split8v<false>(wv[0], wv[1], wh, wl);
         split8v<false>(al[0], al[1], ah2, al2);
-        // 3: dK[j][s] for this wave's buckets: V Z1^T + M^T W + triu(1) alpha + Y1.
+        // 3: dK for this wave's buckets: V Z1^T + M^T W + triu(1) alpha + Y1,
+        //    formed transposed (each product with its operands swapped), so
+        //    a lane holds buckets 16 w + 4 g .. + 3 of token 16 bj + lr: four
+        //    consecutive values of a dK row.
         f32x4 dk[2];
+        {
+            f32x4 y4;
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj) dk[bj] = f32x4{y1, y1, y1, y1};
+            for (int rr = 0; rr < 4; ++rr) y4[rr] = __shfl(y1, 4 * gq + rr);
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) dk[bj] = y4;
+        }
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             bf16x8 zh, zl;
@@ -1448,7 +1456,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
             for (int bj = 0; bj < 2; ++bj) {
                 bf16x8 vh, vl;
                 PR::frag(Vs, 16 * bj + lr, kk, gq, vh, vl);
-                dk[bj] = mfma16(vh, zh, dk[bj]);
+                dk[bj] = mfma16(zh, vh, dk[bj]);
             }
         }
 #pragma unroll
@@ -1460,12 +1468,13 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) mh[e] = __bf16(0.0f);
             }
-            dk[bj] = mfma16(mh, wh, dk[bj]);
-            dk[bj] = mfma16(bj == 0 ? up0 : up1, ah2, dk[bj]);
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) QT::put1(dKt, 16 * bj + 4 * gq + rr, 16 * w + lr, dk[bj][rr]);
+            dk[bj] = mfma16(wh, mh, dk[bj]);
+            dk[bj] = mfma16(ah2, bj == 0 ? up0 : up1, dk[bj]);
+            QT::put(dKt, 16 * bj + lr, 16 * w + 4 * gq, dk[bj]);
         }
-        // 4: dV[j][c] for this wave's value columns: K Z1 + P^T G.
+        // 4: dV for this wave's value columns: K Z1 + P^T G, transposed the
+        //    same way (columns 16 w + 4 g .. + 3 of token 16 bj + lr), added
+        //    to the running sum's four values of that row.
         {
             f32x4 dv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -1476,7 +1485,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
                 for (int bj = 0; bj < 2; ++bj) {
                     bf16x8 kh2, kl2;
                     PR::frag(Ks, 16 * bj + lr, kk, gq, kh2, kl2);
-                    dv[bj] = mfma16(kh2, zh, dv[bj]);
+                    dv[bj] = mfma16(zh, kh2, dv[bj]);
                 }
             }
             bf16x8 gh, gl;
@@ -1489,14 +1498,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dkv_wide_kernel(
 #pragma unroll
                     for (int e = 0; e < 4; ++e) ph[e] = __bf16(0.0f);
                 }
-                dv[bj] = mfma16(ph, gh, dv[bj]);
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int row = 16 * bj + 4 * gq + rr;
-                    // The first addend's read view is empty: the sum is zero.
-                    const float sum = *reinterpret_cast<const float*>(Vt + FT::at(row, 4 * (16 * w + lr)));
-                    FT::put1(dVt, row, 16 * w + lr, dv[bj][rr] + sum);
-                }
+                dv[bj] = mfma16(gh, ph, dv[bj]);
+                // The first addend's read view is empty: the sum is zero.
+                const f32x4 sum = FT::get4(Vt, 16 * bj + lr, 16 * w + 4 * gq);
+                FT::put(dVt, 16 * bj + lr, 16 * w + 4 * gq, dv[bj] + sum);
             }
         }
         // 5: the suffix state before this sub-chunk.

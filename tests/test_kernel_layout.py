@@ -1327,3 +1327,56 @@ def test_row_chunks_stored_whole_give_the_wrong_buckets():
     mem = put_row_chunks(P, two_halves=False)
     got = frag_tr(P, mem, 0, 0, 0)
     assert any(got[lr] != [(e % 4 + 16 * (e // 4), lr) for e in range(8)] for lr in range(16))
+
+
+# ---------------------------------------------------------------------------
+# mfma_common.h mfma16 (v_mfma_f32_16x16x32_bf16) as the kernels use it: lane
+# (g, lr) supplies A[lr][k] and B[k][lr] for the 8 contraction indices
+# k = k_of(0, g, e) (any order of the 32 indices, the same for both
+# operands), and receives C[4 g + r][lr], r < 4.  The backward walk forms dK
+# and dV transposed by swapping the operands of every product: then a lane
+# holds four consecutive columns of one row.
+
+
+def mfma16_emul(a_frag, b_frag):
+    """a_frag[lane][e], b_frag[lane][e] (lane = 16 g + lr) -> c_frag[lane][r]."""
+    A = np.zeros((16, 32))
+    B = np.zeros((32, 16))
+    for lane in range(64):
+        g, lr = divmod(lane, 16)
+        for e in range(8):
+            k = k_of(0, g, e)
+            A[lr, k] = a_frag[lane][e]
+            B[k, lr] = b_frag[lane][e]
+    C = A @ B
+    return [[C[4 * (lane // 16) + r, lane % 16] for r in range(4)] for lane in range(64)]
+
+
+def test_swapped_operands_give_the_transposed_product_four_columns_per_lane():
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((64, 8))
+    b = rng.standard_normal((64, 8))
+    c = mfma16_emul(a, b)
+    ct = mfma16_emul(b, a)
+    M = np.zeros((16, 16))
+    Mt = np.zeros((16, 16))
+    for lane in range(64):
+        g, lr = divmod(lane, 16)
+        for r in range(4):
+            M[4 * g + r, lr] = c[lane][r]
+            Mt[4 * g + r, lr] = ct[lane][r]
+    assert np.allclose(Mt, M.T)
+    # Lane (g, lr) of the swapped product holds row lr, columns 4 g .. 4 g + 3.
+    for lane in range(64):
+        g, lr = divmod(lane, 16)
+        assert np.allclose(ct[lane], [M[lr, 4 * g + r] for r in range(4)])
+
+
+def test_swapping_only_one_product_of_a_sum_mixes_layouts():
+    # Planted mistake: a sum of two products with only one swapped is neither
+    # the product nor its transpose.
+    rng = np.random.default_rng(6)
+    a, b, x, y = (rng.standard_normal((64, 8)) for _ in range(4))
+    mixed = np.array(mfma16_emul(b, a)) + np.array(mfma16_emul(x, y))
+    right = np.array(mfma16_emul(b, a)) + np.array(mfma16_emul(y, x))
+    assert not np.allclose(mixed, right)
