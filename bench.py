@@ -106,17 +106,20 @@ BWD_PHASES = {
 }
 
 
-def causal_bwd_phases(S: int, d: int, es: int) -> list:
+def causal_bwd_phases(S: int, d: int, es: int, whole_streams: bool = False) -> list:
     """The causal backward's launches as race_api.hip issues them (starting
     from the inputs): one 64 x 64 block at S = d = 64; with bf16 tokens, d =
     128 and S = 128 or 256, the forward walks of every 128-bucket block
     (pair of 64-bucket groups) in one launch, one reverse scan of all their
     records, then a backward walk per block; other shapes get generic
-    names."""
+    names.  With `whole_streams` (the streams times the blocks fill the
+    device's CUs, or one tile per stream) the forward walks go through whole
+    streams and the forward's tile sums and scan are not run."""
     if S == 64 and d == 64:
         return BWD_PHASES[True]
     if es == 2 and d == 128 and S in (128, 256):
-        names = ["bwd_tile_sums", "tile_scan", "bwd_dq_walks", "suffix_scan_blocks"]
+        names = [] if whole_streams else ["bwd_tile_sums", "tile_scan"]
+        names += ["bwd_dq_walks", "suffix_scan_blocks"]
         return names + [f"bwd_dkv_pair{mp}" for mp in range(S // 128)]
     return []
 
@@ -865,7 +868,8 @@ def measure(args, T: int) -> dict:
     if run_fwd:
         names += fwd_names
     if run_bwd:
-        names += (causal_bwd_phases(cfg.S, cfg.d, es) if cfg.causal
+        whole = tiles == 1 or cfg.N * (cfg.S // 128) >= torch.cuda.get_device_properties(dev).multi_processor_count
+        names += (causal_bwd_phases(cfg.S, cfg.d, es, whole) if cfg.causal
                   else noncausal_bwd_phases(cfg.S, cfg.d, tiles))
 
     if args.calibrate_copy:

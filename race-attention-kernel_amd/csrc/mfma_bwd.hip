@@ -951,7 +951,10 @@ struct WideGeo {
 // (block b: buckets s0 + 128 b ..; its outputs at b times the *_ps strides):
 // the workgroups of one tile and stream, which read the same V and dOut rows,
 // are 8 apart in launch order, so they land on the same XCD and the second
-// reads of those rows come from its L2.
+// reads of those rows come from its L2.  With pp.whole a workgroup walks its
+// stream's tiles one after another, its prefix state carried on from zero,
+// so no forward records are needed (tile t's walk starts after a barrier
+// that follows every LDS read of tile t - 1, so the slots may restart).
 __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const bf16_t* __restrict__ q_in, const bf16_t* __restrict__ k_in, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ g, bf16_t* __restrict__ dq_hi_in, bf16_t* __restrict__ dq_lo_in,
@@ -973,9 +976,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     const int tid = threadIdx.x, l = tid & 63, gq = l >> 4, lr = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int s = 16 * w + lr;  // the lane's bucket in the block
-    const WideItem it = wide_item(blockIdx.x, pp.pairs, N * tiles);
+    // An item is a tile of a stream, or with pp.whole a stream, walked tile
+    // after tile from a zero prefix.
+    const WideItem it = wide_item(blockIdx.x, pp.pairs, pp.whole ? N : N * tiles);
     if (it.item < 0) return;  // the last group's padding
-    const int64_t n = it.item / tiles, ti = it.item % tiles;
+    const int64_t n = pp.whole ? it.item : it.item / tiles;
+    const int64_t ti0 = pp.whole ? 0 : it.item % tiles, ti1 = pp.whole ? tiles : ti0 + 1;
     const int b = it.block;
     const bf16_t* q = q_in + kWideS * b;
     const bf16_t* k = k_in + kWideS * b;
@@ -984,222 +990,228 @@ __global__ __launch_bounds__(kWideThreads, 1) void causal_bwd_dq_wide_kernel(
     float* apre = apre_in + b * pp.ap_ps;
     float* bwd_records = bwd_records_in + b * pp.rec_ps;
     const int s0 = s0_in + kWideS * b;
-    const int64_t t_begin = ti * tile;
-    const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
-    const int64_t base = n * T + t_begin;
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
-    // dQ as bf16 (hi, the caller's dQ or workspace rows of ld_hi) and the
-    // bf16 rounding of its remainder (lo, rows of 128): hi + lo is dQ to
-    // about 2^-17, which the backward walk reads back.
-    const __amdgpu_buffer_rsrc_t hir = make_rsrc(dq_hi + base * ld_hi, int64_t(rows) * ld_hi * 2);
-    // No remainders when no backward walk reads them (dq_lo null: an empty
-    // view drops the stores).
-    const __amdgpu_buffer_rsrc_t lor =
-        make_rsrc(dq_lo ? dq_lo + base * kWideS : nullptr, dq_lo ? int64_t(rows) * kWideS * 2 : 0);
-
-    // Prefix state at the tile start, transposed: B0^T[16 cb + 4 g + rr][s].
-    const float* fr = fwd_records + (n * tiles + ti) * fwd_rec;
-    f32x4 b0t[8], zt[8];
+    // Prefix state at the walk's start, transposed: B0^T[16 cb + 4 g + rr][s],
+    // from the forward record of its first tile (a whole stream starts at
+    // zero).  It runs on through the tiles of a whole-stream walk.
+    const float* fr = pp.whole ? nullptr : fwd_records + (n * tiles + ti0) * fwd_rec;
+    f32x4 b0t[8];
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            b0t[cb][rr] = fr[int64_t(s0 + s) * kWideD + 16 * cb + 4 * gq + rr];
-            zt[cb][rr] = 0.f;
-        }
+        for (int rr = 0; rr < 4; ++rr) b0t[cb][rr] = fr ? fr[int64_t(s0 + s) * kWideD + 16 * cb + 4 * gq + rr] : 0.f;
     // The forward record holds B [S][128] then A [S]; S = ldq.
-    float a0 = fr[int64_t(ldq) * kWideD + s0 + s];
-    float ypart = 0.f;
+    float a0 = fr ? fr[int64_t(ldq) * kWideD + s0 + s] : 0.f;
     const bf16x8 tri0 = tril_frag(0, gq, lr), tri1 = tril_frag(16, gq, lr);
 
-    // Staging as in causal_bwd_dkv_wide_kernel.
-    const int tensor = __builtin_amdgcn_readfirstlane(tid / G::kBlk);
-    const int sa = (tid % G::kBlk) / 16, sb = tid % 16;
-    const int sld = tensor == 0 ? ldq : kWideD;
-    const bf16_t* ssrc = tensor == 0 ? k + base * ldq : tensor == 1 ? v + base * kWideD : g + base * kWideD;
-    const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
-    const int splane = tensor * G::kRBytes;  // the staged tensor's plane inside a slot
-    // Sub-chunks of operands in flight in registers ahead of the one in LDS.
-    constexpr int kDepth = RACE_BWD_WIDE_DQ_DEPTH;
-    StageBlock<bf16_t> st[kDepth];
-    // Q's rows: chunk tid of the sub-chunk (row tid / 16, 8 buckets) in
-    // from global memory, into a plane read transposed.
-    static_assert(QT::kChunks * kBC == kWideThreads, "one Q chunk per thread");
-    uint4 qx[kDepth];
-    // Row chunk tid of the sub-chunk (row tid / 16, buckets 8 (tid % 16) ..
-    // + 7) into a plane whose transposed reads give each lane its bucket's
-    // values at the accumulator layout's rows.
-    auto put_row_chunk = [&](unsigned char* plane, const uint4& x) {
-        const int row = tid / QT::kChunks, k0 = 8 * (tid % QT::kChunks);
-        PR::put4(plane, row, k0, uint2{x.x, x.y}, uint2{});
-        PR::put4(plane, row, k0 + 4, uint2{x.z, x.w}, uint2{});
-    };
-    auto load_q = [&](uint4& x, int r0) {
-        x = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
-    };
+    for (int64_t ti = ti0; ti < ti1; ++ti) {
+        const int64_t t_begin = ti * tile;
+        const int rows = int(min<int64_t>(T, t_begin + tile) - t_begin);
+        const int64_t base = n * T + t_begin;
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + base * ldq, int64_t(rows) * ldq * 2);
+        // dQ as bf16 (hi, the caller's dQ or workspace rows of ld_hi) and the
+        // bf16 rounding of its remainder (lo, rows of 128): hi + lo is dQ to
+        // about 2^-17, which the backward walk reads back.
+        const __amdgpu_buffer_rsrc_t hir = make_rsrc(dq_hi + base * ld_hi, int64_t(rows) * ld_hi * 2);
+        // No remainders when no backward walk reads them (dq_lo null: an empty
+        // view drops the stores).
+        const __amdgpu_buffer_rsrc_t lor =
+            make_rsrc(dq_lo ? dq_lo + base * kWideS : nullptr, dq_lo ? int64_t(rows) * kWideS * 2 : 0);
 
-    const int subs = tile / kBC;
-    float* ap = apre + (n * tiles + ti) * int64_t(subs) * kWideS;
-    // The previous sub-chunk's dQ tile as whole rows: dQ as bf16 and the
-    // bf16 remainders (16-byte chunk c of a tile row holds elements 4 c ..
-    // 4 c + 3).
-    constexpr int kChunksPerRow = T32::kChunks;
-    auto flush = [&](int r0) {
-        typename T32::template Chunks<kWideThreads> c32;
-        T32::template read<kWideThreads>(D32s, c32);
+        // The tile's suffix totals start at zero.
+        f32x4 zt[8];
 #pragma unroll
-        for (int i = 0; i < T32::template Chunks<kWideThreads>::kPer; ++i) {
-            const int qi = tid + i * kWideThreads;
-            const f32x4 x = __builtin_bit_cast(f32x4, c32.x[i]);
-            const u32x2 hi = {pack2(x[0], x[1]), pack2(x[2], x[3])};
-            const u32x2 lo = {pack2(x[0] - lo_half(hi[0]), x[1] - hi_half(hi[0])),
-                              pack2(x[2] - lo_half(hi[1]), x[3] - hi_half(hi[1]))};
-            const int row = r0 + qi / kChunksPerRow, c4 = 4 * (qi % kChunksPerRow);
-            __builtin_amdgcn_raw_buffer_store_b64(hi, hir, (row * ld_hi + c4) * 2, 0, kPolicyDefault);
-            __builtin_amdgcn_raw_buffer_store_b64(lo, lor, (row * kWideS + c4) * 2, 0, kPolicyDefault);
+        for (int cb = 0; cb < 8; ++cb) zt[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float ypart = 0.f;
+
+        // Staging as in causal_bwd_dkv_wide_kernel.
+        const int tensor = __builtin_amdgcn_readfirstlane(tid / G::kBlk);
+        const int sa = (tid % G::kBlk) / 16, sb = tid % 16;
+        const int sld = tensor == 0 ? ldq : kWideD;
+        const bf16_t* ssrc = tensor == 0 ? k + base * ldq : tensor == 1 ? v + base * kWideD : g + base * kWideD;
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(tensor < 3 ? ssrc : nullptr, tensor < 3 ? int64_t(rows) * sld * 2 : 0);
+        const int splane = tensor * G::kRBytes;  // the staged tensor's plane inside a slot
+        // Sub-chunks of operands in flight in registers ahead of the one in LDS.
+        constexpr int kDepth = RACE_BWD_WIDE_DQ_DEPTH;
+        StageBlock<bf16_t> st[kDepth];
+        // Q's rows: chunk tid of the sub-chunk (row tid / 16, 8 buckets) in
+        // from global memory, into a plane read transposed.
+        static_assert(QT::kChunks * kBC == kWideThreads, "one Q chunk per thread");
+        uint4 qx[kDepth];
+        // Row chunk tid of the sub-chunk (row tid / 16, buckets 8 (tid % 16) ..
+        // + 7) into a plane whose transposed reads give each lane its bucket's
+        // values at the accumulator layout's rows.
+        auto put_row_chunk = [&](unsigned char* plane, const uint4& x) {
+            const int row = tid / QT::kChunks, k0 = 8 * (tid % QT::kChunks);
+            PR::put4(plane, row, k0, uint2{x.x, x.y}, uint2{});
+            PR::put4(plane, row, k0 + 4, uint2{x.z, x.w}, uint2{});
+        };
+        auto load_q = [&](uint4& x, int r0) {
+            x = buf_load16<kPolicyDefault>(qr, ((r0 + tid / QT::kChunks) * ldq + 8 * (tid % QT::kChunks)) * 2);
+        };
+
+        const int subs = tile / kBC;
+        float* ap = apre + (n * tiles + ti) * int64_t(subs) * kWideS;
+        // The previous sub-chunk's dQ tile as whole rows: dQ as bf16 and the
+        // bf16 remainders (16-byte chunk c of a tile row holds elements 4 c ..
+        // 4 c + 3).
+        constexpr int kChunksPerRow = T32::kChunks;
+        auto flush = [&](int r0) {
+            typename T32::template Chunks<kWideThreads> c32;
+            T32::template read<kWideThreads>(D32s, c32);
+#pragma unroll
+            for (int i = 0; i < T32::template Chunks<kWideThreads>::kPer; ++i) {
+                const int qi = tid + i * kWideThreads;
+                const f32x4 x = __builtin_bit_cast(f32x4, c32.x[i]);
+                const u32x2 hi = {pack2(x[0], x[1]), pack2(x[2], x[3])};
+                const u32x2 lo = {pack2(x[0] - lo_half(hi[0]), x[1] - hi_half(hi[0])),
+                                  pack2(x[2] - lo_half(hi[1]), x[3] - hi_half(hi[1]))};
+                const int row = r0 + qi / kChunksPerRow, c4 = 4 * (qi % kChunksPerRow);
+                __builtin_amdgcn_raw_buffer_store_b64(hi, hir, (row * ld_hi + c4) * 2, 0, kPolicyDefault);
+                __builtin_amdgcn_raw_buffer_store_b64(lo, lor, (row * kWideS + c4) * 2, 0, kPolicyDefault);
+            }
+        };
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            st[d].load(srs, d * kBC, sa, sb, sld);
+            load_q(qx[d], d * kBC);
         }
-    };
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        st[d].load(srs, d * kBC, sa, sb, sld);
-        load_q(qx[d], d * kBC);
-    }
-    // Sub-chunk r0 uses plane slot (r0 / kBC) & 1, so two barriers per
-    // sub-chunk suffice: its staging and Q-row stores need none before them
-    // (the slot was last read two sub-chunks back, with two barriers since;
-    // the Q rows were last read before the previous sub-chunk's second
-    // barrier), and the previous dQ tile is read after the first barrier and
-    // rewritten only after the second.
-    auto sub_chunk = [&](StageBlock<bf16_t>& stg, uint4& qv, int r0) {
-        unsigned char* Ks = lds + ((r0 / kBC) & 1) * G::kPlanesBytes;
-        unsigned char* Vs = Ks + G::kRBytes;
-        unsigned char* Gs = Vs + G::kRBytes;
-        if (tensor < 3) stg.store_r<PR>(Ks + splane, sa, sb);
-        put_row_chunk(Qt, qv);
-        stg.load(srs, r0 + kDepth * kBC, sa, sb, sld);  // past the tile: zeros, never used
-        load_q(qv, r0 + kDepth * kBC);
-        __syncthreads();
-        // The previous sub-chunk's dQ tile, complete since this barrier.
-        // Unconditional: at r0 = 0 the offsets are negative, outside the
-        // buffer ranges, and the stores are dropped; a sub-chunk past a
-        // ragged tile end reads zeros and stores nothing.
-        flush(r0 - kBC);
-        if (gq == 0 && r0 < rows) ap[(r0 / kBC) * kWideS + s] = a0;
+        // Sub-chunk r0 uses plane slot (r0 / kBC) & 1, so two barriers per
+        // sub-chunk suffice: its staging and Q-row stores need none before them
+        // (the slot was last read two sub-chunks back, with two barriers since;
+        // the Q rows were last read before the previous sub-chunk's second
+        // barrier), and the previous dQ tile is read after the first barrier and
+        // rewritten only after the second.
+        auto sub_chunk = [&](StageBlock<bf16_t>& stg, uint4& qv, int r0) {
+            unsigned char* Ks = lds + ((r0 / kBC) & 1) * G::kPlanesBytes;
+            unsigned char* Vs = Ks + G::kRBytes;
+            unsigned char* Gs = Vs + G::kRBytes;
+            if (tensor < 3) stg.store_r<PR>(Ks + splane, sa, sb);
+            put_row_chunk(Qt, qv);
+            stg.load(srs, r0 + kDepth * kBC, sa, sb, sld);  // past the tile: zeros, never used
+            load_q(qv, r0 + kDepth * kBC);
+            __syncthreads();
+            // The previous sub-chunk's dQ tile, complete since this barrier.
+            // Unconditional: at r0 = 0 the offsets are negative, outside the
+            // buffer ranges, and the stores are dropped; a sub-chunk past a
+            // ragged tile end reads zeros and stores nothing.
+            flush(r0 - kBC);
+            if (gq == 0 && r0 < rows) ap[(r0 / kBC) * kWideS + s] = a0;
 
-        // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
-        float qc[2][4];
-        {
-            bf16x8 qf, unused;
-            PR::frag_tr(Qt, 0, 16 * w, gq, lr, qf, unused);
+            // 1: Abar[i][s] = A0[s] + sum_{j <= i} K[j][s], r and W.
+            float qc[2][4];
+            {
+                bf16x8 qf, unused;
+                PR::frag_tr(Qt, 0, 16 * w, gq, lr, qf, unused);
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = float(qf[4 * bi + rr]);
+            }
+            bf16x8 kh, kl;
+            PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
+            f32x4 rv[2], wv[2];
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi) {
+                f32x4 acc = {a0, a0, a0, a0};
+                acc = mfma16(bi == 0 ? tri0 : tri1, kh, acc);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    rv[bi][rr] = __builtin_amdgcn_rcpf(acc[rr] + kEps);
+                    wv[bi][rr] = qc[bi][rr] * rv[bi][rr];
+                }
+                if (bi == 1) a0 = __shfl(acc[3], 48 + lr);  // inclusive mass at the last token
+            }
+
+            // 2: M^T blocks (j-block, i-block) = V G^T, j <= i: (0,0), (0,1), (1,1) on waves 0..2.
+            if (w < 3) {
+                const int mbj = w == 2 ? 1 : 0, mbi = w >= 1 ? 1 : 0;
+                f32x4 mt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    bf16x8 ah, al, bh, bl;
+                    PR::frag(Vs, 16 * mbj + lr, kk, gq, ah, al);
+                    PR::frag(Gs, 16 * mbi + lr, kk, gq, bh, bl);
+                    mt = mfma16(ah, bh, mt);
+                }
+                if (mbj == mbi) {
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        if (4 * gq + rr > lr) mt[rr] = 0.f;
+                }
+                uint2 hi, lo;
+                split4<false>(mt[0], mt[1], mt[2], mt[3], hi, lo);
+                PM::put4(Ms, 16 * mbi + lr, 16 * mbj + 4 * gq, hi, lo);
+            }
+            __syncthreads();
+
+            // 3: U = G B0^T + M K;  dQ = r U;  alpha = -W dQ.
+            f32x4 u[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                bf16x8 bh, bl;
+                split8v<false>(b0t[2 * kk], b0t[2 * kk + 1], bh, bl);
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi) {
+                    bf16x8 gh, gl;
+                    PR::frag(Gs, 16 * bi + lr, kk, gq, gh, gl);
+                    u[bi] = mfma16(gh, bh, u[bi]);
+                }
+            }
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi) {
+                bf16x8 mh, ml;
+                PM::frag(Ms, 16 * bi + lr, 0, gq, mh, ml);
+                if (bi == 0) {
+                    // Tokens 16..31 of the first block's row are above the diagonal.
+#pragma unroll
+                    for (int e = 4; e < 8; ++e) mh[e] = __bf16(0.0f);
+                }
+                u[bi] = mfma16(mh, kh, u[bi]);
+            }
 #pragma unroll
             for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) qc[bi][rr] = float(qf[4 * bi + rr]);
-        }
-        bf16x8 kh, kl;
-        PR::frag_tr(Ks, 0, 16 * w, gq, lr, kh, kl);
-        f32x4 rv[2], wv[2];
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
-            f32x4 acc = {a0, a0, a0, a0};
-            acc = mfma16(bi == 0 ? tri0 : tri1, kh, acc);
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                rv[bi][rr] = __builtin_amdgcn_rcpf(acc[rr] + kEps);
-                wv[bi][rr] = qc[bi][rr] * rv[bi][rr];
-            }
-            if (bi == 1) a0 = __shfl(acc[3], 48 + lr);  // inclusive mass at the last token
-        }
+                for (int rr = 0; rr < 4; ++rr) {
+                    const float dqv = rv[bi][rr] * u[bi][rr];
+                    T32::put1(D32s, 16 * bi + 4 * gq + rr, s, dqv);
+                    ypart += -wv[bi][rr] * dqv;
+                }
 
-        // 2: M^T blocks (j-block, i-block) = V G^T, j <= i: (0,0), (0,1), (1,1) on waves 0..2.
-        if (w < 3) {
-            const int mbj = w == 2 ? 1 : 0, mbi = w >= 1 ? 1 : 0;
-            f32x4 mt = {0.f, 0.f, 0.f, 0.f};
+            // 4: Z^T += G^T W;  5: B0^T += V^T K.
+            bf16x8 wh, wl;
+            split8v<false>(wv[0], wv[1], wh, wl);
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                bf16x8 ah, al, bh, bl;
-                PR::frag(Vs, 16 * mbj + lr, kk, gq, ah, al);
-                PR::frag(Gs, 16 * mbi + lr, kk, gq, bh, bl);
-                mt = mfma16(ah, bh, mt);
+            for (int cb = 0; cb < 8; ++cb) {
+                bf16x8 gh, gl, vh, vl;
+                PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
+                zt[cb] = mfma16(gh, wh, zt[cb]);
+                PR::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
+                b0t[cb] = mfma16(vh, kh, b0t[cb]);
             }
-            if (mbj == mbi) {
+        };
+        int r0 = 0;
+        for (; r0 < rows; r0 += kDepth * kBC) {
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    if (4 * gq + rr > lr) mt[rr] = 0.f;
-            }
-            uint2 hi, lo;
-            split4<false>(mt[0], mt[1], mt[2], mt[3], hi, lo);
-            PM::put4(Ms, 16 * mbi + lr, 16 * mbj + 4 * gq, hi, lo);
+            for (int d = 0; d < kDepth; ++d) sub_chunk(st[d], qx[d], r0 + d * kBC);
         }
         __syncthreads();
+        if (r0 > 0) flush(r0 - kBC);
 
-        // 3: U = G B0^T + M K;  dQ = r U;  alpha = -W dQ.
-        f32x4 u[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        // Suffix totals of this tile into the four 64 x 64 records: Z[s][c]
+        // (record layout B[s][c]) and Y[s], the totals of alpha, in value half
+        // 0's record (half 1's holds zero).
+        float y = ypart + __shfl_xor(ypart, 16);
+        y = y + __shfl_xor(y, 32);
+        const int g2 = w >> 2, sl = 16 * (w & 3) + lr;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            bf16x8 bh, bl;
-            split8v<false>(b0t[2 * kk], b0t[2 * kk + 1], bh, bl);
+        for (int h = 0; h < 2; ++h) {
+            float* br = bwd_records + (int64_t(2 * g2 + h) * N * tiles + n * tiles + ti) * rec;
 #pragma unroll
-            for (int bi = 0; bi < 2; ++bi) {
-                bf16x8 gh, gl;
-                PR::frag(Gs, 16 * bi + lr, kk, gq, gh, gl);
-                u[bi] = mfma16(gh, bh, u[bi]);
-            }
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) br[sl * kBS + 16 * cb + 4 * gq + rr] = zt[4 * h + cb][rr];
+            if (gq == 0) br[kBS * kBS + sl] = h == 0 ? y : 0.f;
         }
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
-            bf16x8 mh, ml;
-            PM::frag(Ms, 16 * bi + lr, 0, gq, mh, ml);
-            if (bi == 0) {
-                // Tokens 16..31 of the first block's row are above the diagonal.
-#pragma unroll
-                for (int e = 4; e < 8; ++e) mh[e] = __bf16(0.0f);
-            }
-            u[bi] = mfma16(mh, kh, u[bi]);
-        }
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const float dqv = rv[bi][rr] * u[bi][rr];
-                T32::put1(D32s, 16 * bi + 4 * gq + rr, s, dqv);
-                ypart += -wv[bi][rr] * dqv;
-            }
-
-        // 4: Z^T += G^T W;  5: B0^T += V^T K.
-        bf16x8 wh, wl;
-        split8v<false>(wv[0], wv[1], wh, wl);
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb) {
-            bf16x8 gh, gl, vh, vl;
-            PR::frag_tr(Gs, 0, 16 * cb, gq, lr, gh, gl);
-            zt[cb] = mfma16(gh, wh, zt[cb]);
-            PR::frag_tr(Vs, 0, 16 * cb, gq, lr, vh, vl);
-            b0t[cb] = mfma16(vh, kh, b0t[cb]);
-        }
-    };
-    int r0 = 0;
-    for (; r0 < rows; r0 += kDepth * kBC) {
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d) sub_chunk(st[d], qx[d], r0 + d * kBC);
-    }
-    __syncthreads();
-    if (r0 > 0) flush(r0 - kBC);
-
-    // Suffix totals of this tile into the four 64 x 64 records: Z[s][c]
-    // (record layout B[s][c]) and Y[s], the totals of alpha, in value half
-    // 0's record (half 1's holds zero).
-    float y = ypart + __shfl_xor(ypart, 16);
-    y = y + __shfl_xor(y, 32);
-    const int g2 = w >> 2, sl = 16 * (w & 3) + lr;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        float* br = bwd_records + (int64_t(2 * g2 + h) * N * tiles + n * tiles + ti) * rec;
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) br[sl * kBS + 16 * cb + 4 * gq + rr] = zt[4 * h + cb][rr];
-        if (gq == 0) br[kBS * kBS + sl] = h == 0 ? y : 0.f;
     }
 }
 
@@ -1607,7 +1619,8 @@ hipError_t launch_causal_bwd_dq_wide(const void* q, const void* k, const void* v
     if (p.dtype != RACE_BF16 || p.d != kWideD || p.S % kWideS != 0 || s0 % kWideS != 0 || pp.pairs < 1 ||
         s0 + kWideS * pp.pairs > p.S || p.tile % kBC != 0 || !dq_hi || ld_hi < kWideS)
         return hipErrorInvalidValue;
-    const int64_t groups = (p.N * p.tiles + kWideXcds - 1) / kWideXcds;
+    if (!pp.whole && !fwd_records) return hipErrorInvalidValue;
+    const int64_t groups = ((pp.whole ? p.N : p.N * p.tiles) + kWideXcds - 1) / kWideXcds;
     // gfx950 takes at most 2^32 - 1 work-items along a grid dimension.
     if (groups * kWideXcds * pp.pairs * kWideThreads > int64_t(UINT32_MAX)) return hipErrorInvalidValue;
     const dim3 grid(unsigned(groups * kWideXcds * pp.pairs));

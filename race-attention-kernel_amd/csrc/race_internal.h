@@ -269,13 +269,17 @@ struct DqWidePairs {
     int64_t lo_ps = 0;   // dq_lo (bf16)
     int64_t ap_ps = 0;   // apre (floats)
     int64_t rec_ps = 0;  // bwd_records (floats)
+    // 1: a workgroup walks every tile of its stream in order from a zero
+    // prefix (items are streams; fwd_records is not read); 0: one tile,
+    // from its forward record.
+    int whole = 0;
 };
 // Workgroups per launch-order group of the block walks: gfx950 hands
 // consecutive workgroups of a launch to its eight XCDs in turn, so
 // workgroups kWideXcds apart run on the same XCD.
 constexpr int kWideXcds = 8;
 // Workgroup x of a forward-walk launch over `pairs` blocks walks item
-// (stream n, tile ti: item = n tiles + ti) of block `block`: groups of
+// (stream n, tile ti: item = n tiles + ti; or stream n) of block `block`: groups of
 // kWideXcds items, each listed once per block, so the workgroups of one
 // item (the same V and dOut rows) are kWideXcds apart.  item is -1 for the
 // padding past the last item.

@@ -66,6 +66,9 @@ def test_causal_backward_launch_names_follow_the_library():
         "bwd_dkv_pair1"]
     assert len(b.causal_bwd_phases(128, 128, 2)) == 5
     assert b.causal_bwd_phases(256, 128, 4) == []
+    # Streams that fill the device: whole-stream forward walks, no tile sums or scan.
+    assert b.causal_bwd_phases(256, 128, 2, True) == [
+        "bwd_dq_walks", "suffix_scan_blocks", "bwd_dkv_pair0", "bwd_dkv_pair1"]
 
 
 

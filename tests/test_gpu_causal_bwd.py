@@ -159,6 +159,34 @@ def test_block_walks_many_streams(race, oracle, cuda):
     assert max(errs) <= tol_for(torch.bfloat16)
 
 
+@pytest.mark.parametrize("R", [16, 32])
+def test_block_walks_whole_streams_and_tiled(race, oracle, cuda, R):
+    # From the inputs, with the streams times the 128-bucket blocks filling
+    # the device's CUs, each forward walk goes through its whole stream from
+    # a zero prefix (the forward's tile sums and scan are skipped); through
+    # autograd the same shape walks tile by tile from the saved records.
+    # Four 256-token tiles, the last one ragged; both against the oracle VJP
+    # on a sample of streams.
+    S = 8 * R
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    N, T, tile = -(-cus // (S // 128)), 1000, 256
+    say("c-bwd whole streams", N, T, S, tile)
+    q, k, v = race.make_inputs(N, T, 8, R, 128, seed=31 + R, dtype=torch.bfloat16, device=cuda, gen_device="cuda")
+    g = torch.randn(v.shape, device=cuda, generator=torch.Generator(device=cuda).manual_seed(32 + R)).to(v.dtype)
+    whole = race.race_causal_backward(q, k, v, g, tile_tokens=tile)
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    race.race_fused_fwd(qg, kg, vg, causal=True, tile_tokens=tile).backward(g)
+    torch.cuda.synchronize()
+    tiled = (qg.grad, kg.grad, vg.grad)
+    pick = [0, 1, N // 2, N - 1]
+    qn, kn, vn, gn = (to_np(x[pick]) for x in (q, k, v, g))
+    refs = oracle.causal_bwd(qn, kn, vn, gn, nthreads=16)
+    for name, grads in (("whole", whole), ("tiled", tiled)):
+        errs = [per_stream_rel_err(to_np(x[pick]), r) for x, r in zip(grads, refs)]
+        say("c-bwd", name, *(f"{e:.2e}" for e in errs))
+        assert max(errs) <= tol_for(torch.bfloat16)
+
+
 def test_block_walks_bitwise_reproducible(race, cuda):
     say("c-bwd block bitwise")
     q, k, v, g = race.make_inputs(3, 2100, 8, 32, 128, seed=27, dtype=torch.bfloat16, grad_out=True)

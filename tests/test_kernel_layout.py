@@ -1232,31 +1232,35 @@ def test_wide_forward_walks_interleaved_blocks_split_an_item_over_xcds():
 # chunks, which the staging tests above cover).
 
 
-def dq_walk_epochs(subs: int, slots: int):
+def dq_walk_epochs(subs: int, slots: int, tiles: int = 1, end_barrier: bool = True):
     """Per epoch: {(region, 'r'|'w', wave)} of the walk over `subs`
     sub-chunks with `slots` plane slots (regions: plane slot p, Qt, M,
-    D32 = the dQ tile)."""
+    D32 = the dQ tile), for each of `tiles` tiles in turn (a whole-stream
+    walk): the slot index restarts at each tile, whose walk ends with a
+    barrier and the last flush."""
     epochs = [set()]
 
     def acc(region, kind, waves=range(8)):
         for w in waves:
             epochs[-1].add((region, kind, w))
 
-    for t in range(subs):
-        plane = f"plane{t % slots}"
-        acc(plane, "w", range(6))   # staging: waves 0..5 (three tensors)
-        acc("Qt", "w")
-        epochs.append(set())         # first barrier
-        acc("D32", "r")              # flush of sub-chunk t - 1
-        acc("Qt", "r")               # step 1
-        acc(plane, "r")              # step 1 (K), step 2 (V, G)
-        acc("M", "w", range(3))      # step 2 on waves 0..2
-        epochs.append(set())         # second barrier
-        acc("M", "r")                # step 3
-        acc(plane, "r")              # steps 3..5 (G, V)
-        acc("D32", "w")              # step 3
-    epochs.append(set())             # barrier before the last flush
-    acc("D32", "r")
+    for _ in range(tiles):
+        for t in range(subs):
+            plane = f"plane{t % slots}"
+            acc(plane, "w", range(6))   # staging: waves 0..5 (three tensors)
+            acc("Qt", "w")
+            epochs.append(set())         # first barrier
+            acc("D32", "r")              # flush of sub-chunk t - 1
+            acc("Qt", "r")               # step 1
+            acc(plane, "r")              # step 1 (K), step 2 (V, G)
+            acc("M", "w", range(3))      # step 2 on waves 0..2
+            epochs.append(set())         # second barrier
+            acc("M", "r")                # step 3
+            acc(plane, "r")              # steps 3..5 (G, V)
+            acc("D32", "w")              # step 3
+        if end_barrier:
+            epochs.append(set())         # barrier before the tile's last flush
+        acc("D32", "r")
     return epochs
 
 
@@ -1274,6 +1278,21 @@ def epoch_conflicts(epochs):
 @pytest.mark.parametrize("subs", [1, 2, 3, 128])
 def test_wide_forward_walk_two_slots_need_two_barriers(subs):
     assert epoch_conflicts(dq_walk_epochs(subs, 2)) == []
+
+
+@pytest.mark.parametrize("subs", [1, 3, 128])
+def test_whole_stream_walk_restarts_the_slots_at_each_tile(subs):
+    # With pp.whole a workgroup walks tile after tile; each tile's sub-chunks
+    # start again at slot 0, which an odd number of sub-chunks left last.
+    assert epoch_conflicts(dq_walk_epochs(subs, 2, tiles=3)) == []
+
+
+def test_whole_stream_walk_without_the_tile_end_barrier_races():
+    # Planted mistake: no barrier at the tile end; with an odd number of
+    # sub-chunks the next tile's staging writes slot 0 while slower waves
+    # still read it, and its Q rows overwrite Qt.
+    bad = {r for _, r in epoch_conflicts(dq_walk_epochs(3, 2, tiles=2, end_barrier=False))}
+    assert "plane0" in bad
 
 
 def test_wide_forward_walk_one_slot_without_the_top_barrier_races():
