@@ -307,28 +307,32 @@ def test_unsupported_shape_raises(race, cuda):
 
 def test_cfg5_shape_backward(race, oracle, cuda):
     # cfg5 (N = 128, L = 8, R = 32, d = 128, T = 16384, bf16) through
-    # autograd: the walks over two 128 x 128 blocks; 16 streams against the
-    # oracle VJP.
+    # autograd (the walks over two 128 x 128 blocks, tile by tile from the
+    # saved records) and from the inputs (N x 2 blocks covers the CUs of an
+    # MI355X, so the forward walks go through whole streams); 16 streams
+    # against the oracle VJP.
     say("c-bwd cfg5")
     q, k, v = race.make_inputs(128, 16384, 8, 32, 128, seed=5, dtype=torch.bfloat16, device=cuda,
                                gen_device="cuda")
     g = torch.randn(v.shape, device=cuda, generator=torch.Generator(device=cuda).manual_seed(6)).to(v.dtype)
     qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
     race.race_fused_fwd(qg, kg, vg, causal=True).backward(g)
+    inputs = race.race_causal_backward(q, k, v, g)
     torch.cuda.synchronize()
     # 16 streams spread over the batch, heads and both ends of the stream range.
     pick = [0, 9, 17, 26, 34, 41, 50, 58, 67, 75, 86, 93, 101, 110, 119, 127]
     qn, kn, vn, gn = (to_np(x[pick]) for x in (q, k, v, g))
     rq, rk, rv = oracle.causal_bwd(qn, kn, vn, gn, nthreads=16)
-    errs = [per_stream_rel_err(to_np(x.grad[pick]), r) for x, r in ((qg, rq), (kg, rk), (vg, rv))]
-    say("c-bwd cfg5 errors", *(f"{e:.2e}" for e in errs))
-    assert max(errs) <= tol_for(torch.bfloat16)
-    # Against the rounding floor of the bf16 gradients, stream by stream.
-    for name, x, r in (("dQ", qg, rq), ("dV", vg, rv)):
-        got = to_np(x.grad[pick])
-        for j in range(len(pick)):
-            assert_bf16_floor(got[j], r[j], float(np.abs(r[j]).max()), f"cfg5 {name} stream {pick[j]}",
-                              factors=CFG5_BWD_FLOOR_FACTORS)
+    for how, (dq, dk, dv) in (("autograd", (qg.grad, kg.grad, vg.grad)), ("inputs", inputs)):
+        errs = [per_stream_rel_err(to_np(x[pick]), r) for x, r in ((dq, rq), (dk, rk), (dv, rv))]
+        say("c-bwd cfg5 errors", how, *(f"{e:.2e}" for e in errs))
+        assert max(errs) <= tol_for(torch.bfloat16)
+        # Against the rounding floor of the bf16 gradients, stream by stream.
+        for name, x, r in (("dQ", dq, rq), ("dV", dv, rv)):
+            got = to_np(x[pick])
+            for j in range(len(pick)):
+                assert_bf16_floor(got[j], r[j], float(np.abs(r[j]).max()), f"cfg5 {how} {name} stream {pick[j]}",
+                                  factors=CFG5_BWD_FLOOR_FACTORS)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
