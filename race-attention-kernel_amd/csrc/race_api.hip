@@ -913,11 +913,13 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     }
 
     // The bf16 128 x 128 block walks can start every stream at its first
-    // token instead: when its streams alone fill the machine (or a stream is
-    // one tile), each forward walk goes through its whole stream, its prefix
-    // carried from zero, and the forward's tile sums and scan are skipped.
-    // At the cfg5 shape (N = 128, S = 256, 4 tiles) that saves 0.27 ms of
-    // 3.55 per step; with saved records the tiled walks keep reading them.
+    // token instead: when the streams times the blocks cover the CUs (one
+    // forward-walk workgroup per CU fits) or a stream is one tile, each
+    // forward walk goes through its whole stream, its prefix carried from
+    // zero, and the forward's tile sums and scan are skipped.  At the cfg5
+    // shape (N = 128, S = 256, 4 tiles) the step went from 3.49-3.50 to
+    // 3.21-3.23 ms (one box), the walks taking the same time; with saved
+    // records the tiled walks keep reading them.
     bool whole_streams = false;
     if (!fwd_records && use_mfma && pl.wide2()) {
         int cus = 0;
