@@ -917,11 +917,11 @@ race_status causal_bwd_impl(const void* probsQ, const void* probsK, const void* 
     // forward-walk workgroup per CU fits) or a stream is one tile, each
     // forward walk goes through its whole stream, its prefix carried from
     // zero, and the forward's tile sums and scan are skipped.  At the cfg5
-    // shape (N = 128, S = 256, 4 tiles) the step went from 3.49-3.50 to
-    // 3.21-3.23 ms (one box), the walks taking the same time; with saved
-    // records the tiled walks keep reading them.
+    // shape (N = 128, S = 256, 4 tiles) the step from the inputs went from
+    // 3.49-3.50 to 3.21-3.23 ms (one box), the walks taking the same time as
+    // tile by tile.  Saved records are then not read either.
     bool whole_streams = false;
-    if (!fwd_records && use_mfma && pl.wide2()) {
+    if (use_mfma && pl.wide2()) {
         int cus = 0;
         RACE_TRY(cu_count(&cus));
         whole_streams = p.tiles == 1 || p.N * (pl.mblocks / 2) >= cus;

@@ -161,11 +161,11 @@ def test_block_walks_many_streams(race, oracle, cuda):
 
 @pytest.mark.parametrize("R", [16, 32])
 def test_block_walks_whole_streams_and_tiled(race, oracle, cuda, R):
-    # From the inputs, with the streams times the 128-bucket blocks filling
-    # the device's CUs, each forward walk goes through its whole stream from
-    # a zero prefix (the forward's tile sums and scan are skipped); through
-    # autograd the same shape walks tile by tile from the saved records.
-    # Four 256-token tiles, the last one ragged; both against the oracle VJP
+    # With the streams times the 128-bucket blocks covering the device's CUs,
+    # each forward walk goes through its whole stream from a zero prefix (the
+    # forward's tile sums and scan, or the saved records, are not used), from
+    # the inputs and through autograd; one stream fewer walks tile by tile.
+    # Four 256-token tiles, the last one ragged; all against the oracle VJP
     # on a sample of streams.
     S = 8 * R
     cus = torch.cuda.get_device_properties(cuda).multi_processor_count
@@ -176,12 +176,13 @@ def test_block_walks_whole_streams_and_tiled(race, oracle, cuda, R):
     whole = race.race_causal_backward(q, k, v, g, tile_tokens=tile)
     qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
     race.race_fused_fwd(qg, kg, vg, causal=True, tile_tokens=tile).backward(g)
+    # One stream fewer than the CUs need: the tiled walks after the tile sums and scan.
+    tiled = race.race_causal_backward(*(x[: N - 1] for x in (q, k, v, g)), tile_tokens=tile)
     torch.cuda.synchronize()
-    tiled = (qg.grad, kg.grad, vg.grad)
-    pick = [0, 1, N // 2, N - 1]
+    pick = [0, 1, N // 2, N - 2]
     qn, kn, vn, gn = (to_np(x[pick]) for x in (q, k, v, g))
     refs = oracle.causal_bwd(qn, kn, vn, gn, nthreads=16)
-    for name, grads in (("whole", whole), ("tiled", tiled)):
+    for name, grads in (("whole", whole), ("autograd", (qg.grad, kg.grad, vg.grad)), ("tiled", tiled)):
         errs = [per_stream_rel_err(to_np(x[pick]), r) for x, r in zip(grads, refs)]
         say("c-bwd", name, *(f"{e:.2e}" for e in errs))
         assert max(errs) <= tol_for(torch.bfloat16)
@@ -307,10 +308,9 @@ def test_unsupported_shape_raises(race, cuda):
 
 def test_cfg5_shape_backward(race, oracle, cuda):
     # cfg5 (N = 128, L = 8, R = 32, d = 128, T = 16384, bf16) through
-    # autograd (the walks over two 128 x 128 blocks, tile by tile from the
-    # saved records) and from the inputs (N x 2 blocks covers the CUs of an
-    # MI355X, so the forward walks go through whole streams); 16 streams
-    # against the oracle VJP.
+    # autograd and from the inputs: the walks over two 128 x 128 blocks (N x 2
+    # blocks covers the CUs of an MI355X, so the forward walks go through
+    # whole streams); 16 streams against the oracle VJP.
     say("c-bwd cfg5")
     q, k, v = race.make_inputs(128, 16384, 8, 32, 128, seed=5, dtype=torch.bfloat16, device=cuda,
                                gen_device="cuda")
