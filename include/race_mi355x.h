@@ -291,8 +291,9 @@ race_status race_causal_bwd_workspace_bytes(const race_shape* shape, const race_
  * The forward prefix states are recomputed (tile totals and their scan), so
  * only the forward's inputs are needed; the 128 x 128 block walks below skip
  * that and walk each stream whole from its first token when N times the
- * 128-bucket blocks covers the device's CUs or a stream is one tile.  Any of dQ, dK, dV may be NULL to
- * skip it.  Kernels: with S and d multiples of 64 (S <= 256, d <= 128) and
+ * 128-bucket blocks covers the device's CUs or a stream is one tile (as does
+ * race_causal_bwd_from_records, which then reads no records).  Any of dQ,
+ * dK, dV may be NULL to skip it.  Kernels: with S and d multiples of 64 (S <= 256, d <= 128) and
  * tiles of whole 32-token sub-chunks, the matrix cores (64 x 64 bucket x
  * value blocks; bf16 tokens with d = 128 and S = 128 or 256 in walks over
  * 128 x 128 blocks); otherwise the vector ALU, in column groups where the
